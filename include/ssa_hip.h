@@ -1,0 +1,192 @@
+/*
+ * ssa_hip.h — C ABI of libssa_hip.so, the MI355X (gfx950) implementation of SSA's routed
+ * block-sparse attention hot path: block summaries, the cumulant router, the block-sparse
+ * flash-attention prefill and the routed decode step.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are device pointers. The last dimension (head_dim d) is contiguous;
+ *     the other dimensions are described by int64 element strides, so transposed views such as
+ *     HF's (b, n, h, d) -> (b, h, n, d) need no copy.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and never synchronises
+ *     with the host. Nothing is allocated: outputs and workspaces are provided by the caller, with
+ *     *_workspace_size() queries giving the byte counts.
+ *   - Every function returns SSA_OK (0) or a negative status; ssa_last_error() then returns a
+ *     thread-local message describing the failure.
+ *   - Block lists follow the compact router→attention contract of the reference
+ *     (ssa/ivf_kernel.py:72-99): kv_num (rows) int32 and kv_idx (rows, W) int32, the first kv_num
+ *     entries of a row being the selected key-block ids in ascending order and the rest padding (0).
+ *
+ * The reference is pure Python over torch/FlexAttention/Triton; each entry point names the
+ * reference function (file:line under ssa/) whose behaviour it reproduces.
+ */
+#ifndef SSA_HIP_H
+#define SSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSA_ABI_VERSION 1
+
+typedef void* ssa_stream_t; /* hipStream_t */
+
+enum ssa_status {
+  SSA_OK = 0,
+  SSA_ERR_INVALID = -1,     /* bad argument (shape, stride, null pointer, range)             */
+  SSA_ERR_UNSUPPORTED = -2, /* valid request this build does not implement (dtype, d, block) */
+  SSA_ERR_HIP = -3,         /* a HIP runtime call or kernel launch failed                    */
+  SSA_ERR_WORKSPACE = -4    /* workspace pointer/size too small                              */
+};
+
+enum ssa_dtype { SSA_F32 = 0, SSA_F16 = 1, SSA_BF16 = 2 };
+
+/* Block-summary modes. */
+enum ssa_stats_mode {
+  SSA_STATS_POP = 0,      /* mu, population var (/cnt), optional m3, over rows < n_real          */
+  SSA_STATS_UNBIASED = 1, /* mu, unbiased var (/(cnt-1)); every row must be real                 */
+  SSA_STATS_QMEAN = 2     /* query-block mean: sum of the rows present / block (pad rows = 0)    */
+};
+
+/* Router semantics. */
+enum ssa_route_mode {
+  SSA_ROUTE_BUDGET = 0, /* block_route_budget: candidates strictly before the query block      */
+  SSA_ROUTE_FLAT = 1,   /* block_route: candidates up to and including the query block          */
+  SSA_ROUTE_QUERY = 2   /* _selection_mask per query: candidates = blocks complete at the query */
+};
+
+int ssa_abi_version(void);
+const char* ssa_last_error(void);
+/* 1 if `device` is a gfx950 device this library has code for, 0 if not, <0 on error. */
+int ssa_device_supported(int device);
+
+/*
+ * Per-block summaries of x (B, H, n, d): out (B, H, nb, d) fp32 contiguous, nb = ceil(n/block).
+ * Sums are accumulated in fp64 and rounded once to fp32; the variance is two-pass about the
+ * fp64 mean.
+ *   POP:      rows r < min(n, n_real) of a block are counted; cnt = max(1, #counted);
+ *             mu = sum/cnt, var = sum((x-mu)^2)/cnt, m3 = sum((x-mu)^3)/cnt (m3 may be NULL).
+ *             Replaces ssa/ssa_kernel.py:78-91 (block_route_budget, incl. the n_real branch
+ *             :80-87) and ssa/gemma_ssa.py:65-82 (_block_stats).
+ *   UNBIASED: var = sum((x-mu)^2)/(cnt-1). Replaces ssa/ssa_kernel.py:42-43,47 (kb.var(3)).
+ *   QMEAN:    mu = sum over rows < n / block (var, m3 must be NULL). Replaces the query-block
+ *             summary q.view(...).float().mean(3) of ssa/ssa_kernel.py:44,79, which averages
+ *             the caller's zero pad rows in.
+ * Also serves ssa/ivf_kernel.py:50-60 (block_means) and ssa/ivf_decode.py:104-108.
+ */
+int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n, int64_t d,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_n, int64_t block,
+                      int64_t n_real, int mode, float* mu, float* var, float* m3,
+                      ssa_stream_t stream);
+
+/*
+ * Cumulant router. rows: (B, Hq, nbq, d) fp32 (query-block means, or query vectors in
+ * SSA_ROUTE_QUERY mode); mu, var (and m3): (B, Hkv, nbk, d) fp32; q-head h reads key head
+ * h / (Hq/Hkv). Score of row i against key block c, in the reference's evaluation order:
+ *   r = fl32( fl32(<q,mu_c>) + fl32(coef2 * fl32(<q*q, var_c>)) )
+ *       [ + fl32(coef3 * fl32(<q*q*q, m3_c>)) when m3 != NULL ]
+ * with each inner product accumulated in fp64 (q*q and q*q*q rounded to fp32 first, as the
+ * reference's elementwise products are). coef2 = 0.5*beta (0.5 for block_route, 0 for centroid
+ * routing, in which case var may be NULL); coef3 = beta^2/6.
+ * Selection per row (ties broken by the lowest block index):
+ *   BUDGET: candidates c < i; keep = top_c if top_c >= 0 else max(1, ceil(fl32(budget_frac)*i))
+ *           (ssa/ssa_kernel.py:101-116);
+ *   FLAT:   candidates c <= i; keep = top_c (ssa/ssa_kernel.py:48-55);
+ *   QUERY:  row r is the query at absolute position pos = query_pos + r; candidates are the key
+ *           blocks complete at pos, c < (pos+1)/block; keep = top_c or
+ *           max(1, ceil(fl32(budget_frac)*#candidates)); the "own" block is pos/block
+ *           (ssa/gemma_ssa.py:104-131).
+ *   The top min(keep, #candidates) candidates are unioned with the own block and its `local`
+ *   predecessors, clipped to [0, own], and written ascending: kv_num (B,Hq,nbq) and
+ *   kv_idx (B,Hq,nbq,W) (ssa/ssa_kernel.py:113-118 without the dense argsort).
+ * W must be >= the largest row count (ssa_route_width() computes it). The workspace holds the
+ * score keys of a chunk of rows; ssa_route_workspace_size() gives the size that routes every
+ * row in one pass, and any size >= ssa_route_workspace_size(B, Hq, 1, nbk, ...) works.
+ */
+int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c, float budget_frac,
+                        int64_t local, int64_t query_pos, int64_t block);
+size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk);
+int ssa_route(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
+              int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
+              int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
+              int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+              void* workspace, size_t workspace_bytes, ssa_stream_t stream);
+
+/*
+ * Expands compact lists to the reference's dense forms (ssa/ssa_kernel.py:117-118):
+ * sel (rows, nbk) uint8 (0/1) and/or kv_full (rows, nbk) int32 = the selected ids ascending
+ * followed by the unselected ids ascending (= argsort(sel, descending, stable)). Either output
+ * may be NULL.
+ */
+int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t rows, int64_t W,
+                         int64_t nbk, uint8_t* sel, int32_t* kv_full, ssa_stream_t stream);
+
+/*
+ * Block-sparse causal attention forward (replaces FlexAttention with
+ * BlockMask.from_kv_blocks(kv_num, kv_idx, block, mask_mod = kv<=q & kv<n):
+ * ssa/ssa_kernel.py:30-34,125-126, ssa/gemma_ssa.py:159-162,179, ssa/ivf_kernel.py:122-127).
+ * q, out: (B, Hq, n, d); k, v: (B, Hkv, n, d); query row t (in query block i = t/block) attends
+ * the keys j <= t, j < n, of the blocks kv_idx[b,h,i,:kv_num[b,h,i]] with
+ * softmax(scale * q.k) in fp32; out has q's dtype. strides[12] = q(b,h,n), k(b,h,n), v(b,h,n),
+ * out(b,h,n) in elements. lse (B, Hq, n) fp32 natural-log sum-exp, may be NULL.
+ * dtype: SSA_BF16 / SSA_F16 (MFMA, d = 64) or SSA_F32 (d = 64). block: 64 or a multiple of 128.
+ * The 16-bit paths read V transposed, (B, Hkv, d, n_pad) with n_pad = ceil(n/block)*block, from
+ * the workspace (ssa_sparse_attn_workspace_size() bytes). flags = 0: the call first writes V^T
+ * there itself; flags = SSA_ATTN_VT_READY: the workspace already holds V^T of this v (from
+ * ssa_transpose_v), e.g. kept resident across calls. The fp32 path needs no workspace.
+ */
+enum { SSA_ATTN_VT_READY = 1 };
+size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,
+                                      int64_t block);
+int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,
+                    int64_t block, int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                    void* vt, size_t vt_bytes, ssa_stream_t stream);
+int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out, int dtype,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t d, int64_t block,
+                        const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
+                        int64_t W, float scale, float* lse, int flags, void* workspace,
+                        size_t workspace_bytes, ssa_stream_t stream);
+
+/*
+ * Per-query attention over selected blocks (replaces ssa/ivf_decode.py:49-62, decode_attend, and
+ * the analytic masked softmax of ssa/gemma_ssa.py:232-240). q: (B, Hq, nq, d); caches k, v:
+ * (B, Hkv, cap, d); out (B, Hq, nq, d). Query row r of head (b,h) sits at absolute position
+ * pos + r and attends the keys j <= pos + r (j < cap) of blocks kv_idx[b,h,r,:kv_num[b,h,r]]
+ * (kv_num (B,Hq,nq), kv_idx (B,Hq,nq,W)) with softmax(scale * q.k) in fp32.
+ * strides[12] = q(b,h,n), k(b,h,n), v(b,h,n), out(b,h,n) in elements. A block id repeated in a
+ * row is attended once (the reference takes sorted(set(blocks))).
+ */
+size_t ssa_decode_attend_workspace_size(int64_t B, int64_t Hq, int64_t nq, int64_t W, int64_t d);
+int ssa_decode_attend(const void* q, const void* k, const void* v, void* out, int dtype,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t nq, int64_t cap, int64_t d,
+                      int64_t block, int64_t pos, const int64_t* strides, const int32_t* kv_num,
+                      const int32_t* kv_idx, int64_t W, float scale, void* workspace,
+                      size_t workspace_bytes, ssa_stream_t stream);
+
+/*
+ * One routed decode step on a KV cache (replaces the per-step body of ssa/ivf_decode.py:128-136
+ * with the exact cumulant router of ssa/gemma_ssa.py:85-137 at q_len = 1):
+ *   1. append k_new, v_new (B, Hkv, d) at position pos of the caches;
+ *   2. if pos+1 completes block c = pos/block, write its POP summary into mu/var[:, :, c];
+ *   3. route the queries q (B, Hq, d) over the complete blocks (SSA_ROUTE_QUERY, query_pos=pos);
+ *   4. attend (as ssa_decode_attend) into out.
+ * mu, var: (B, Hkv, cap/block, d) fp32 contiguous, holding the summaries of every block that
+ * was complete before this step. strides[14] = q(b,h), k_new(b,h), v_new(b,h), kcache(b,h,n),
+ * vcache(b,h,n), out(b,h). kv_num (B,Hq), kv_idx (B,Hq,W) receive the selection.
+ */
+size_t ssa_decode_step_workspace_size(int64_t B, int64_t Hq, int64_t cap, int64_t d,
+                                      int64_t block, int64_t W);
+int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* kcache,
+                    void* vcache, float* mu, float* var, void* out, int dtype, int64_t B,
+                    int64_t Hq, int64_t Hkv, int64_t cap, int64_t d, int64_t block, int64_t pos,
+                    const int64_t* strides, int64_t top_c, float budget_frac, int64_t local,
+                    float coef2, float scale, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+                    void* workspace, size_t workspace_bytes, ssa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSA_HIP_H */

@@ -1,0 +1,344 @@
+"""CPU oracle for SSA's routed block-sparse attention -- TEST INFRASTRUCTURE ONLY.
+
+A NumPy restatement of the reference algorithm, used as the checker by tests/, by
+__graft_entry__.smoke() and as the CPU baseline leg of bench.py. Nothing in the product path
+(ssa_amd/) imports it, and it is never a fallback for the HIP kernels.
+
+Numerics. Block statistics, query-block means and the router's inner products are accumulated
+in float64 from the float32 operands and rounded once to float32, with elementwise products
+(q*q, q*q*q) and the final combination r = E1 + c2*E2 (+ c3*E3) rounded to float32 exactly where
+the reference's float32 torch code rounds. These are the correctly rounded values of the
+reference formula; the reference's own float32 reductions differ from them by a few ulps, which
+can only change a selection where two candidate scores are within that noise (see
+`selection_gap`). Attention is exact masked softmax in float64.
+
+Pinning (what checks each function; details in tests/test_oracle.py):
+  block_stats / qmean    closed form on hand-built blocks; pad exclusion; golden fixtures via
+                         the selections they induce.
+  scores / select_rows   reference golden fixtures (tests/golden/, produced by the reference
+                         itself in float32) -- equal except on rows `selection_gap` flags as
+                         within float32 noise; brute-force enumeration on tiny rows; budget=1 ->
+                         all causal blocks; beta=0 -> centroid routing.
+  sparse_attention       reference golden outputs (FlexAttention / analytic path); full budget
+                         == dense causal softmax; needle known-answer test.
+  decode_attend          equals the prefill row for the same blocks; golden analytic q_len=1 rows.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# ---------------------------------------------------------------------------------------------
+# a1 / a2: block summaries
+# ---------------------------------------------------------------------------------------------
+
+
+def block_stats(x: np.ndarray, block: int, mode: str = "pop", n_real: int | None = None):
+    """x (B, H, n, d) -> mu, var, m3 (B, H, nb, d) float32, nb = ceil(n/block).
+
+    mode "pop": rows < n_real counted, cnt = max(1, #counted), var and m3 divide by cnt
+      -- ssa/ssa_kernel.py:80-91 (block_route_budget), ssa/gemma_ssa.py:65-82 (_block_stats).
+    mode "unbiased": var divides by cnt - 1 -- ssa/ssa_kernel.py:43,47 (kb.var(3)).
+    """
+    B, H, n, d = x.shape
+    nb = -(-n // block)
+    nr = n if n_real is None else min(n, int(n_real))
+    xp = np.zeros((B, H, nb * block, d), dtype=np.float64)
+    xp[:, :, :n] = x
+    valid = np.zeros((nb * block,), dtype=bool)
+    valid[:nr] = True
+    xb = xp.reshape(B, H, nb, block, d)
+    vb = valid.reshape(nb, block)[None, None, :, :, None]
+    cnt_rows = vb.sum(3)                                      # (1,1,nb,1)
+    cnt = np.maximum(cnt_rows, 1).astype(np.float64)
+    s1 = np.where(vb, xb, 0.0).sum(3)
+    mean = s1 / cnt
+    cen = np.where(vb, xb - mean[:, :, :, None, :], 0.0)
+    s2 = (cen * cen).sum(3)
+    s3 = (cen * cen * cen).sum(3)
+    vden = cnt - 1.0 if mode == "unbiased" else cnt
+    with np.errstate(divide="ignore", invalid="ignore"):
+        var = s2 / vden
+    return mean.astype(np.float32), var.astype(np.float32), (s3 / cnt).astype(np.float32)
+
+
+def qmean(q: np.ndarray, block: int) -> np.ndarray:
+    """Query-block summary q.view(B,H,nb,block,d).float().mean(3), pad rows counted as zeros
+    (ssa/ssa_kernel.py:44,79; the caller pads with zeros at ssa/gemma_ssa.py:149)."""
+    B, H, n, d = q.shape
+    nb = -(-n // block)
+    qp = np.zeros((B, H, nb * block, d), dtype=np.float64)
+    qp[:, :, :n] = q
+    return (qp.reshape(B, H, nb, block, d).sum(3) / block).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------
+# a3: cumulant score
+# ---------------------------------------------------------------------------------------------
+
+
+def scores(rows: np.ndarray, mu: np.ndarray, var: np.ndarray | None, coef2: float,
+           m3: np.ndarray | None = None, coef3: float = 0.0) -> np.ndarray:
+    """r[b,h,i,c] = fl32(fl32(<q,mu_c>) + fl32(c2 * fl32(<q*q, var_c>))) [+ fl32(c3*fl32(<q^3,m3_c>))]
+    for rows (B, Hq, R, d) and summaries (B, Hkv, nbk, d); query head h uses key head
+    h // (Hq/Hkv). Reference: ssa/ssa_kernel.py:96-99 (block_route_budget), :45-47 (block_route),
+    ssa/gemma_ssa.py:99-102 (_selection_mask)."""
+    B, Hq, R, d = rows.shape
+    Hkv = mu.shape[1]
+    G = Hq // Hkv
+    q = rows.astype(np.float32)
+    q2 = (q * q).astype(np.float32)                    # elementwise fp32 products, as torch
+    out = np.empty((B, Hq, R, mu.shape[2]), dtype=np.float32)
+    c2 = np.float32(coef2)
+    c3 = np.float32(coef3)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // G
+            e1 = (q[b, h].astype(np.float64) @ mu[b, kh].astype(np.float64).T).astype(np.float32)
+            r = e1
+            if var is not None and coef2 != 0.0:
+                e2 = (q2[b, h].astype(np.float64) @ var[b, kh].astype(np.float64).T).astype(np.float32)
+                r = (e1 + (c2 * e2).astype(np.float32)).astype(np.float32)
+            if m3 is not None:
+                q3 = (q2[b, h] * q[b, h]).astype(np.float32)
+                e3 = (q3.astype(np.float64) @ m3[b, kh].astype(np.float64).T).astype(np.float32)
+                r = (r + (c3 * e3).astype(np.float32)).astype(np.float32)
+            out[b, h] = r
+    return out
+
+
+def score_keys(r: np.ndarray) -> np.ndarray:
+    """Order-preserving uint32 keys of fp32 scores: -0 folded onto +0 (torch.topk treats them as
+    equal), NaN above +inf (torch.topk's NaN-is-largest)."""
+    r = np.where(r == 0.0, np.float32(0.0), r).astype(np.float32)
+    u = r.view(np.uint32)
+    k = np.where(u & np.uint32(0x80000000), ~u, u | np.uint32(0x80000000)).astype(np.uint32)
+    return np.where(np.isnan(r), np.uint32(0xFFFFFFFF), k).astype(np.uint32)
+
+
+# ---------------------------------------------------------------------------------------------
+# a4 / a5: selection and compaction
+# ---------------------------------------------------------------------------------------------
+
+
+def _keep_budget(frac: float, nvis: int) -> int:
+    """max(1, ceil(fl32(frac) * fl32(nvis))) computed in float32 (ssa/ssa_kernel.py:105-106,
+    ssa/gemma_ssa.py:117-118)."""
+    return max(1, int(math.ceil(float(np.float32(frac) * np.float32(nvis)))))
+
+
+def row_geometry(mode: str, i: int, nbk: int, top_c, budget_frac, query_pos=0, block=1):
+    """(cmax, keep, own) of row i: candidates are blocks [0, cmax), `keep` of them are kept (ties
+    to the lowest index), and the own block with its `local` predecessors is always added.
+    budget: c < i (ssa/ssa_kernel.py:101-106); flat: c <= i (ssa/ssa_kernel.py:48-52);
+    query: blocks complete at pos = query_pos + i (ssa/gemma_ssa.py:104-118)."""
+    if mode == "budget":
+        cmax, own = min(i, nbk), i
+    elif mode == "flat":
+        cmax, own = min(i + 1, nbk), i
+    elif mode == "query":
+        pos = query_pos + i
+        cmax, own = min((pos + 1) // block, nbk), pos // block
+    else:
+        raise ValueError(mode)
+    if mode == "flat" or top_c is not None:
+        keep = int(top_c)
+    else:
+        keep = _keep_budget(budget_frac, cmax)
+    return cmax, keep, own
+
+
+def select_rows(r: np.ndarray, mode: str, top_c, budget_frac: float, local: int,
+                query_pos: int = 0, block: int = 1):
+    """r (B, Hq, R, nbk) fp32 scores -> list-of-lists of selected block ids per row (ascending):
+    top-min(keep, cmax) candidates by (score desc, index asc) | own-local..own, clipped to
+    [0, min(own, nbk-1)]. Reference: ssa/ssa_kernel.py:101-116, :48-55; ssa/gemma_ssa.py:119-131."""
+    B, Hq, R, nbk = r.shape
+    keys = score_keys(r)
+    out = np.empty((B, Hq, R), dtype=object)
+    for i in range(R):
+        cmax, keep, own = row_geometry(mode, i, nbk, top_c, budget_frac, query_pos, block)
+        k = min(keep, cmax)
+        lo, hi = max(0, own - local), min(own, nbk - 1)
+        loc = set(range(lo, hi + 1))
+        for b in range(B):
+            for h in range(Hq):
+                if k >= cmax:
+                    pick = set(range(cmax))
+                elif k > 0:
+                    order = np.argsort(-keys[b, h, i, :cmax].astype(np.int64), kind="stable")
+                    pick = set(order[:k].tolist())
+                else:
+                    pick = set()
+                out[b, h, i] = sorted(pick | loc)
+    return out
+
+
+def compact(sel_lists, W: int | None = None):
+    """List-of-lists -> (kv_num (B,Hq,R) int32, kv_idx (B,Hq,R,W) int32, ascending, pad 0)."""
+    B, Hq, R = sel_lists.shape
+    if W is None:
+        W = max(1, max(len(x) for x in sel_lists.ravel()))
+    kv_num = np.zeros((B, Hq, R), dtype=np.int32)
+    kv_idx = np.zeros((B, Hq, R, W), dtype=np.int32)
+    for idx in np.ndindex(B, Hq, R):
+        ids = sel_lists[idx]
+        kv_num[idx] = len(ids)
+        kv_idx[idx][:len(ids)] = ids
+    return kv_num, kv_idx
+
+
+def route_budget(q, k, block, budget_frac=0.25, top_c=None, local=1, beta=2.0, edgeworth=False,
+                 n_real=None):
+    """block_route_budget (ssa/ssa_kernel.py:61-119) -> (kv_num, kv_idx compact). q (B,Hq,n,d),
+    k (B,Hkv,n,d), query head h reads key head h // (Hq/Hkv)."""
+    qb = qmean(q, block)
+    mu, var, m3 = block_stats(k, block, "pop", n_real)
+    r = scores(qb, mu, var, 0.5 * beta, m3 if edgeworth else None, beta ** 2 / 6.0)
+    return compact(select_rows(r, "budget", top_c, budget_frac, local))
+
+
+def route_flat(q, k, block, top_c=8, local=1, routing="cumulant"):
+    """block_route (ssa/ssa_kernel.py:37-58) -> (kv_num, kv_idx compact)."""
+    qb = qmean(q, block)
+    mu, var, _ = block_stats(k, block, "unbiased")
+    cum = routing == "cumulant"
+    r = scores(qb, mu, var if cum else None, 0.5 if cum else 0.0)
+    return compact(select_rows(r, "flat", top_c, 0.0, local))
+
+
+def route_query(qrows, k, block, pos0, top_c=None, budget_frac=0.25, local=1, beta=2.0,
+                kv_len=None):
+    """Per-query router of ssa/gemma_ssa.py:85-131: rows qrows (B,Hq,nq,d) at positions
+    pos0 + r over the complete blocks of k[:, :, :kv_len] -> (kv_num, kv_idx compact)."""
+    kv_len = k.shape[2] if kv_len is None else kv_len
+    mu, var, _ = block_stats(k[:, :, :kv_len], block, "pop")
+    r = scores(qrows, mu, var, 0.5 * beta)
+    return compact(select_rows(r, "query", top_c, budget_frac, local, pos0, block))
+
+
+def selection_gap(r64: np.ndarray, mode: str, top_c, budget_frac, query_pos=0, block=1):
+    """Per row, (gap, scale): gap = (K-th best) - ((K+1)-th best) exact score among the
+    candidates (inf when the row keeps all or none), scale = the row's magnitude sum used to
+    bound float32 evaluation noise. A row whose gap is below a few ulps of scale may legitimately
+    select differently under another float32 evaluation order (e.g. the reference's)."""
+    B, Hq, R, nbk = r64.shape
+    gap = np.full((B, Hq, R), np.inf)
+    for i in range(R):
+        cmax, keep, _ = row_geometry(mode, i, nbk, top_c, budget_frac, query_pos, block)
+        k = min(keep, cmax)
+        if k <= 0 or k >= cmax:
+            continue
+        srt = -np.sort(-r64[:, :, i, :cmax], axis=-1)
+        gap[:, :, i] = srt[..., k - 1] - srt[..., k]
+    return gap
+
+
+def exact_scores64(rows, mu, var, coef2, m3=None, coef3=0.0):
+    """fp64 scores from the same float32 operands (for gap certificates)."""
+    q = rows.astype(np.float32)
+    q2 = (q * q).astype(np.float32).astype(np.float64)
+    Hq, Hkv = rows.shape[1], mu.shape[1]
+    G = Hq // Hkv
+    kh = np.arange(Hq) // G
+    mu64 = mu.astype(np.float64)[:, kh]
+    r = np.einsum("bhid,bhcd->bhic", q.astype(np.float64), mu64)
+    mag = np.einsum("bhid,bhcd->bhic", np.abs(q.astype(np.float64)), np.abs(mu64))
+    if var is not None and coef2 != 0.0:
+        v64 = var.astype(np.float64)[:, kh]
+        r = r + coef2 * np.einsum("bhid,bhcd->bhic", q2, v64)
+        mag = mag + abs(coef2) * np.einsum("bhid,bhcd->bhic", q2, np.abs(v64))
+    if m3 is not None:
+        q3 = (q.astype(np.float32) ** 2 * q).astype(np.float64)
+        t64 = m3.astype(np.float64)[:, kh]
+        r = r + coef3 * np.einsum("bhid,bhcd->bhic", q3, t64)
+        mag = mag + abs(coef3) * np.einsum("bhid,bhcd->bhic", np.abs(q3), np.abs(t64))
+    return r, mag
+
+
+# ---------------------------------------------------------------------------------------------
+# a6 / a7: block-sparse attention (exact masked softmax)
+# ---------------------------------------------------------------------------------------------
+
+
+def sparse_attention(q, k, v, kv_num, kv_idx, block, scale=None, n=None, qblocks=None,
+                     heads=None):
+    """o_t = softmax_j(scale * q_t.k_j) v_j over keys j <= t, j < n of the selected blocks of
+    t's query block -- FlexAttention with BlockMask.from_kv_blocks + mask_mod kv<=q & kv<n
+    (ssa/ssa_kernel.py:33-34,125-126; ssa/gemma_ssa.py:159-162,179), in float64.
+    Returns float64 (B, Hq, n, d); rows of query blocks not in `qblocks` (if given) are NaN."""
+    B, Hq, N, d = q.shape
+    n = N if n is None else n
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    nb = -(-n // block)
+    out = np.full((B, Hq, n, d), np.nan)
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    for b in range(B):
+        for h in (range(Hq) if heads is None else heads):
+            kh = h // G
+            for i in (range(nb) if qblocks is None else qblocks):
+                t0, t1 = i * block, min((i + 1) * block, n)
+                ids = [int(c) for c in kv_idx[b, h, i, :kv_num[b, h, i]]]
+                keys = np.concatenate([np.arange(c * block, min((c + 1) * block, n)) for c in ids]) \
+                    if ids else np.zeros(0, dtype=np.int64)
+                s = scale * (q64[b, h, t0:t1] @ k64[b, kh, keys].T)
+                allow = keys[None, :] <= np.arange(t0, t1)[:, None]
+                s = np.where(allow, s, -np.inf)
+                m = s.max(-1, keepdims=True)
+                m = np.where(np.isfinite(m), m, 0.0)
+                p = np.exp(s - m)
+                l = p.sum(-1, keepdims=True)
+                out[b, h, t0:t1] = np.where(l > 0, (p @ v64[b, kh, keys]) / np.where(l > 0, l, 1), 0.0)
+    return out
+
+
+def dense_causal(q, k, v, scale=None):
+    """Exact causal softmax attention in float64 (the full-budget special case)."""
+    B, Hq, n, d = q.shape
+    G = Hq // k.shape[1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    kh = np.arange(Hq) // G
+    q64, k64, v64 = q.astype(np.float64), k.astype(np.float64)[:, kh], v.astype(np.float64)[:, kh]
+    s = scale * np.einsum("bhtd,bhjd->bhtj", q64, k64)
+    s = np.where(np.tril(np.ones((n, n), dtype=bool)), s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    return np.einsum("bhtj,bhjd->bhtd", p / p.sum(-1, keepdims=True), v64)
+
+
+# ---------------------------------------------------------------------------------------------
+# a10 / a11: decode
+# ---------------------------------------------------------------------------------------------
+
+
+def decode_attend(qvec, k, v, blocks, pos, block, scale=None):
+    """One attention row over the tokens <= pos of sorted(set(blocks)), float64
+    (ssa/ivf_decode.py:49-62; scale 1/sqrt(d) by default)."""
+    d = qvec.shape[-1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    ids = sorted(set(int(x) for x in blocks))
+    idx = np.concatenate([np.arange(c * block, min((c + 1) * block, pos + 1)) for c in ids]) \
+        if ids else np.zeros(0, dtype=np.int64)
+    idx = idx[idx <= pos]
+    if idx.size == 0:
+        return np.zeros(d)
+    s = scale * (k[idx].astype(np.float64) @ qvec.astype(np.float64))
+    p = np.exp(s - s.max())
+    return (p / p.sum()) @ v[idx].astype(np.float64)
+
+
+def attend_rows(q, k, v, kv_num, kv_idx, pos0, block, scale=None):
+    """Per-query rows: q (B,Hq,nq,d) at positions pos0 + r over caches k, v (B,Hkv,cap,d)."""
+    B, Hq, nq, d = q.shape
+    G = Hq // k.shape[1]
+    out = np.zeros((B, Hq, nq, d))
+    for b in range(B):
+        for h in range(Hq):
+            for r in range(nq):
+                ids = kv_idx[b, h, r, :kv_num[b, h, r]]
+                out[b, h, r] = decode_attend(q[b, h, r], k[b, h // G], v[b, h // G], ids, pos0 + r,
+                                             block, scale)
+    return out

@@ -1,0 +1,586 @@
+// Block-sparse causal flash attention (prefill) for gfx950.
+//
+// bf16/fp16 path (d = 64): a workgroup owns QT = 32*NW query rows of one query block of one
+// query head and walks that block's selected key blocks in KT-key sub-tiles. Each wave owns 32
+// query rows. Per sub-tile:
+//   S^T = K Q^T   on v_mfma_f32_32x32x16_{bf16,f16}: A = K rows (from LDS), B = the wave's Q
+//                 fragment (registers, loaded once). The K rows fed to MFMA row m are permuted
+//                 (bits 2 and 3 of m swapped) so that each lane's 16 accumulators of a 32-key
+//                 tile hold two runs of 8 consecutive keys -- exactly the B-operand layout of
+//                 the next product, so P never leaves registers.
+//   online softmax in fp32 (exp2 with scale*log2e folded into one FMA; O is rescaled only when
+//                 some row's running max grows, a wave-uniform branch),
+//   O^T += V^T P^T on MFMA: A = V^T rows (LDS), B = P^T (registers, bf16/fp16).
+// K and V^T sub-tiles are double-buffered in LDS with XOR-swizzled 16-byte chunks (conflict-free
+// ds_read_b128 for both 32- and 64-bank LDS); the next sub-tile's global loads are issued before
+// the current one is computed. V is transposed once per call into the workspace so V^T sub-tiles
+// are contiguous 16-byte runs of keys.
+// Workgroups are dispatched heaviest query blocks first, and the query heads sharing a key head
+// for the same query block are placed on the same XCD (shared local-window tiles hit its L2).
+//
+// fp32 path: a single-wave VALU kernel (one query row per lane), K/V sub-tiles of 64 keys in LDS.
+//
+// Semantics: FlexAttention with BlockMask.from_kv_blocks(kv_num, kv_idx, block) and
+// mask_mod = (kv <= q) & (kv < n) -- ssa/ssa_kernel.py:33-34,125-126; ssa/gemma_ssa.py:159-162,179.
+#include <math.h>
+
+#include "common.h"
+
+namespace ssa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnParams {
+  const char* q;
+  const char* k;
+  const char* v;   // natural V (fp32 path)
+  const char* vt;  // V^T workspace (B, Hkv, 64, n_pad) (16-bit path)
+  char* o;
+  int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
+  int64_t B, Hq, Hkv, G, n, n_pad, block, nbq;
+  const int32_t* kv_num;
+  const int32_t* kv_idx;
+  int64_t W;
+  float scale_log2;
+  float* lse;
+  int64_t qsub;   // query sub-tiles per query block
+  int64_t total;  // logical workgroups
+  int64_t group;  // logical workgroups placed together on one XCD
+};
+
+// Logical work item of a physical workgroup: XCD x = pid % 8 receives consecutive runs of
+// `group` logical items, runs interleaved across the 8 XCDs.
+__device__ inline int64_t logical_id(int64_t pid, int64_t group) {
+  const int64_t x = pid & 7, s = pid >> 3;
+  return ((s / group) * 8 + x) * group + (s % group);
+}
+
+// Permutation of a 32-key group: MFMA row m loads key sigma(m) (bits 2 and 3 swapped).
+__device__ inline int sigma32(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// XOR swizzles of 16-byte chunk indices (see the file comment).
+__device__ inline int swz_k(int row) {
+  return (((row ^ (row >> 2)) & 1) << 2) | (((row >> 3) & 1) << 1) | ((row >> 1) & 1);
+}
+template <int KT>
+__device__ inline int swz_v(int row) {
+  if constexpr (KT == 128) return row & 15;
+  else return ((row >> 1) & 7) ^ ((row & 1) << 2);
+}
+
+template <int DT>
+struct Mfma;
+template <>
+struct Mfma<SSA_BF16> {
+  typedef bf16x8 vec;
+  static __device__ inline f32x16 mma(const vec& a, const vec& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline vec from_bits(const u32x4& w) { return __builtin_bit_cast(vec, w); }
+  static __device__ inline vec pack(const float* p) {
+    vec r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (__bf16)p[j];
+    return r;
+  }
+  static __device__ inline unsigned int pack2(float a, float b) {
+    unsigned short lo = __builtin_bit_cast(unsigned short, (__bf16)a);
+    unsigned short hi = __builtin_bit_cast(unsigned short, (__bf16)b);
+    return (unsigned int)lo | ((unsigned int)hi << 16);
+  }
+};
+template <>
+struct Mfma<SSA_F16> {
+  typedef f16x8 vec;
+  static __device__ inline f32x16 mma(const vec& a, const vec& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline vec from_bits(const u32x4& w) { return __builtin_bit_cast(vec, w); }
+  static __device__ inline vec pack(const float* p) {
+    vec r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (_Float16)p[j];
+    return r;
+  }
+  static __device__ inline unsigned int pack2(float a, float b) {
+    unsigned short lo = __builtin_bit_cast(unsigned short, (_Float16)a);
+    unsigned short hi = __builtin_bit_cast(unsigned short, (_Float16)b);
+    return (unsigned int)lo | ((unsigned int)hi << 16);
+  }
+};
+
+// V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n. grid (n_pad/64, B*Hkv).
+__global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict__ v,
+                                                          char* __restrict__ vt, int64_t Hkv,
+                                                          int64_t n, int64_t n_pad, int64_t vsb,
+                                                          int64_t vsh, int64_t vsn) {
+  __shared__ unsigned short t[64][64 + 2];
+  const int64_t bk = blockIdx.y;
+  const int64_t b = bk / Hkv, kvh = bk % Hkv;
+  const int64_t k0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x;
+  const unsigned short* src = reinterpret_cast<const unsigned short*>(v) + b * vsb + kvh * vsh;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = tid + 256 * j;
+    const int row = q >> 3, ch = q & 7;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (k0 + row < n) w = *reinterpret_cast<const u32x4*>(src + (k0 + row) * vsn + ch * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[row][ch * 8 + 2 * e] = (unsigned short)(w[e] & 0xffffu);
+      t[row][ch * 8 + 2 * e + 1] = (unsigned short)(w[e] >> 16);
+    }
+  }
+  __syncthreads();
+  unsigned short* dst = reinterpret_cast<unsigned short*>(vt) + bk * 64 * n_pad;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = tid + 256 * j;
+    const int drow = q >> 3, kch = q & 7;
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (unsigned int)t[kch * 8 + 2 * e][drow] |
+             ((unsigned int)t[kch * 8 + 2 * e + 1][drow] << 16);
+    *reinterpret_cast<u32x4*>(dst + drow * n_pad + k0 + kch * 8) = w;
+  }
+}
+
+template <int DT, int NW, int KT>
+__global__ __launch_bounds__(NW * 64) void sparse_attn_mfma_kernel(AttnParams p) {
+  using M = Mfma<DT>;
+  typedef typename M::vec vec;
+  constexpr int QT = 32 * NW;
+  constexpr int NT = NW * 64;
+  constexpr int KBYTES = KT * 128;  // K sub-tile: KT rows x 64 halves
+  constexpr int VBYTES = KT * 128;  // V^T sub-tile: 64 rows x KT halves
+  constexpr int CHUNKS = KT * 8 / NT;  // 16-byte chunks per thread per operand
+  constexpr int NST = KT / 32;         // 32-key groups per sub-tile
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * (KBYTES + VBYTES)];
+
+  const int64_t L0 = logical_id(blockIdx.x, p.group);
+  if (L0 >= p.total) return;
+  int64_t L = L0;
+  const int64_t qs = L % p.qsub;
+  L /= p.qsub;
+  const int64_t hg = L % p.G;
+  L /= p.G;
+  const int64_t kvh = L % p.Hkv;
+  L /= p.Hkv;
+  const int64_t b = L % p.B;
+  L /= p.B;
+  const int64_t i = p.nbq - 1 - L;
+  const int64_t h = kvh * p.G + hg;
+
+  const int64_t q0 = i * p.block + qs * QT;
+  if (q0 >= p.n) return;
+  const int64_t qmax = q0 + QT - 1 < p.n - 1 ? q0 + QT - 1 : p.n - 1;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int64_t qw0 = q0 + w * 32;
+  const int64_t qpos = qw0 + col;
+
+  const int64_t row = (b * p.Hq + h) * p.nbq + i;
+  int cnt = p.kv_num[row];
+  if (cnt > p.W) cnt = (int)p.W;
+  if (cnt < 0) cnt = 0;
+  const int32_t* list = p.kv_idx + row * p.W;
+  const int S = (int)(p.block / KT);
+  const int T = cnt * S;
+
+  // Q fragment (B operand of S^T = K Q^T): lane holds query `col`, head dims 16*kd + 8*half + [0,8)
+  vec qf[4];
+  {
+    const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
+                               h * p.qsh + qpos * p.qsn + half * 8;
+#pragma unroll
+    for (int kd = 0; kd < 4; ++kd) {
+      u32x4 wv = {0u, 0u, 0u, 0u};
+      if (qpos < p.n) wv = *reinterpret_cast<const u32x4*>(qp + kd * 16);
+      qf[kd] = M::from_bits(wv);
+    }
+  }
+
+  const unsigned short* kbase =
+      reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
+  const unsigned short* vtbase =
+      reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
+
+  auto tile_key0 = [&](int t) -> int64_t {
+    const int32_t c = list[t / S];
+    if (c < 0 || (int64_t)c >= p.nbq) return -1;
+    return (int64_t)c * p.block + (int64_t)(t % S) * KT;
+  };
+  auto next_valid = [&](int t) -> int {
+    for (; t < T; ++t) {
+      const int64_t k0 = tile_key0(t);
+      if (k0 >= 0 && k0 <= qmax && k0 < p.n) break;
+    }
+    return t;
+  };
+
+  u32x4 kreg[CHUNKS], vreg[CHUNKS];
+  auto load_tile = [&](int64_t key0) {
+#pragma unroll
+    for (int j = 0; j < CHUNKS; ++j) {
+      const int qq = tid + j * NT;
+      const int kr = qq >> 3, kc = qq & 7;
+      u32x4 z = {0u, 0u, 0u, 0u};
+      kreg[j] = (key0 + kr < p.n) ? *reinterpret_cast<const u32x4*>(kbase + (key0 + kr) * p.ksn + kc * 8) : z;
+      const int vr = qq / (KT / 8), vc = qq % (KT / 8);
+      vreg[j] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)vr * p.n_pad + key0 + vc * 8);
+    }
+  };
+  auto store_tile = [&](int buf) {
+    unsigned char* kb = smem + buf * (KBYTES + VBYTES);
+    unsigned char* vb = kb + KBYTES;
+#pragma unroll
+    for (int j = 0; j < CHUNKS; ++j) {
+      const int qq = tid + j * NT;
+      const int kr = qq >> 3, kc = qq & 7;
+      *reinterpret_cast<u32x4*>(kb + kr * 128 + ((kc ^ swz_k(kr)) << 4)) = kreg[j];
+      const int vr = qq / (KT / 8), vc = qq % (KT / 8);
+      *reinterpret_cast<u32x4*>(vb + vr * (KT * 2) + ((vc ^ swz_v<KT>(vr)) << 4)) = vreg[j];
+    }
+  };
+
+  f32x16 oacc[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.0f;
+  float m_run = -INFINITY, l_part = 0.0f;
+  const float c2 = p.scale_log2;
+
+  int t = next_valid(0);
+  int64_t key0 = t < T ? tile_key0(t) : 0;
+  if (t < T) load_tile(key0);
+  int buf = 0;
+  while (t < T) {
+    store_tile(buf);
+    __syncthreads();
+    const int tn = next_valid(t + 1);
+    const int64_t key0n = tn < T ? tile_key0(tn) : 0;
+    if (tn < T) load_tile(key0n);
+
+    const unsigned char* kb = smem + buf * (KBYTES + VBYTES);
+    const unsigned char* vb = kb + KBYTES;
+    // ---- S^T = K Q^T ----
+    f32x16 sacc[NST];
+#pragma unroll
+    for (int tt = 0; tt < NST; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[tt][r] = 0.0f;
+      const int kr = tt * 32 + sigma32(col);
+      const int sw = swz_k(kr);
+#pragma unroll
+      for (int kd = 0; kd < 4; ++kd) {
+        const int ch = 2 * kd + half;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kb + kr * 128 + ((ch ^ sw) << 4));
+        sacc[tt] = M::mma(M::from_bits(a), qf[kd], sacc[tt]);
+      }
+    }
+    // ---- mask (diagonal / ragged tail sub-tiles only) ----
+    if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
+#pragma unroll
+      for (int tt = 0; tt < NST; ++tt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t key = key0 + tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
+          if (key > qpos || key >= p.n) sacc[tt][r] = -INFINITY;
+        }
+    }
+    // ---- online softmax ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < NST; ++tt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx * c2);
+    const bool grew = m_new > m_run;
+    if (__any(grew)) {
+      const float alpha = grew ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      l_part *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // ---- P^T (registers) and O^T += V^T P^T ----
+#pragma unroll
+    for (int tt = 0; tt < NST; ++tt) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float pv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[tt][8 * s + j], c2, -m_use));
+          l_part += pv[j];
+        }
+        const vec pb = M::pack(pv);
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const int vr = dt * 32 + col;
+          const int ch = 4 * tt + 2 * s + half;
+          const u32x4 a =
+              *reinterpret_cast<const u32x4*>(vb + vr * (KT * 2) + ((ch ^ swz_v<KT>(vr)) << 4));
+          oacc[dt] = M::mma(M::from_bits(a), pb, oacc[dt]);
+        }
+      }
+    }
+    buf ^= 1;
+    t = tn;
+    key0 = key0n;
+  }
+
+  // ---- epilogue: O = O^T / l ----
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (qpos < p.n) {
+    unsigned short* op =
+        reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos * p.osn;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int d0 = dt * 32 + rg * 8 + half * 4;
+        uint2 wv;
+        wv.x = M::pack2(oacc[dt][4 * rg] * inv, oacc[dt][4 * rg + 1] * inv);
+        wv.y = M::pack2(oacc[dt][4 * rg + 2] * inv, oacc[dt][4 * rg + 3] * inv);
+        *reinterpret_cast<uint2*>(op + d0) = wv;
+      }
+    if (p.lse != nullptr && half == 0)
+      p.lse[(b * p.Hq + h) * p.n + qpos] =
+          l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+  }
+}
+
+// fp32 path: one wave per 64 query rows, one row per lane. grid = logical items (no remap).
+__global__ __launch_bounds__(64) void sparse_attn_f32_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) float Ks[64][64];
+  __shared__ __attribute__((aligned(16))) float Vs[64][64];
+  int64_t L = blockIdx.x;
+  const int64_t qs = L % p.qsub;
+  L /= p.qsub;
+  const int64_t h = L % p.Hq;
+  L /= p.Hq;
+  const int64_t b = L % p.B;
+  L /= p.B;
+  const int64_t i = p.nbq - 1 - L;
+  const int64_t kvh = h / p.G;
+  const int lane = threadIdx.x;
+  const int64_t q0 = i * p.block + qs * 64;
+  if (q0 >= p.n) return;
+  const int64_t qmax = q0 + 63 < p.n - 1 ? q0 + 63 : p.n - 1;
+  const int64_t qpos = q0 + lane;
+
+  const float* qp = reinterpret_cast<const float*>(p.q) + b * p.qsb + h * p.qsh + qpos * p.qsn;
+  float qv[64], ov[64];
+#pragma unroll
+  for (int e = 0; e < 64; ++e) {
+    qv[e] = qpos < p.n ? qp[e] : 0.0f;
+    ov[e] = 0.0f;
+  }
+  const float* kbase = reinterpret_cast<const float*>(p.k) + b * p.ksb + kvh * p.ksh;
+  const float* vbase = reinterpret_cast<const float*>(p.v) + b * p.vsb + kvh * p.vsh;
+  const int64_t row = (b * p.Hq + h) * p.nbq + i;
+  int cnt = p.kv_num[row];
+  if (cnt > p.W) cnt = (int)p.W;
+  if (cnt < 0) cnt = 0;
+  const int32_t* list = p.kv_idx + row * p.W;
+  const int S = (int)(p.block / 64);
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float c2 = p.scale_log2;
+  for (int t = 0; t < cnt * S; ++t) {
+    const int32_t c = list[t / S];
+    if (c < 0 || (int64_t)c >= p.nbq) continue;
+    const int64_t key0 = (int64_t)c * p.block + (int64_t)(t % S) * 64;
+    if (key0 > qmax || key0 >= p.n) continue;
+    __syncthreads();
+    for (int e = lane; e < 64 * 64; e += 64) {
+      const int kr = e >> 6, kc = e & 63;
+      const bool in = key0 + kr < p.n;
+      Ks[kr][kc] = in ? kbase[(key0 + kr) * p.ksn + kc] : 0.0f;
+      Vs[kr][kc] = in ? vbase[(key0 + kr) * p.vsn + kc] : 0.0f;
+    }
+    __syncthreads();
+    float sv[64];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      float s = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 64; e += 4) {
+        const f32x4 kk = *reinterpret_cast<const f32x4*>(&Ks[j][e]);
+        s = fmaf(qv[e], kk[0], s);
+        s = fmaf(qv[e + 1], kk[1], s);
+        s = fmaf(qv[e + 2], kk[2], s);
+        s = fmaf(qv[e + 3], kk[3], s);
+      }
+      const int64_t key = key0 + j;
+      if (key > qpos || key >= p.n) s = -INFINITY;
+      sv[j] = s;
+      mx = fmaxf(mx, s);
+    }
+    const float m_new = fmaxf(m_run, mx * c2);
+    if (m_new > m_run) {
+      const float alpha = exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int e = 0; e < 64; ++e) ov[e] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const float pj = exp2f(fmaf(sv[j], c2, -m_use));
+      l_run += pj;
+#pragma unroll
+      for (int e = 0; e < 64; e += 4) {
+        const f32x4 vv = *reinterpret_cast<const f32x4*>(&Vs[j][e]);
+        ov[e] = fmaf(pj, vv[0], ov[e]);
+        ov[e + 1] = fmaf(pj, vv[1], ov[e + 1]);
+        ov[e + 2] = fmaf(pj, vv[2], ov[e + 2]);
+        ov[e + 3] = fmaf(pj, vv[3], ov[e + 3]);
+      }
+    }
+  }
+  if (qpos < p.n) {
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float* op = reinterpret_cast<float*>(p.o) + b * p.osb + h * p.osh + qpos * p.osn;
+#pragma unroll
+    for (int e = 0; e < 64; ++e) op[e] = ov[e] * inv;
+    if (p.lse != nullptr)
+      p.lse[(b * p.Hq + h) * p.n + qpos] =
+          l_run > 0.0f ? (m_run + log2f(l_run)) * kLn2 : -INFINITY;
+  }
+}
+
+template <int DT>
+int launch_mfma(AttnParams& p, hipStream_t stream) {
+  const int64_t G = p.G;
+  if (p.block == 64) {
+    p.qsub = 1;
+    p.group = G;
+    p.total = p.nbq * p.B * p.Hkv * G;
+    const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+    SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+    sparse_attn_mfma_kernel<DT, 2, 64><<<(unsigned)grid, 128, 0, stream>>>(p);
+  } else {
+    p.qsub = p.block / 128;
+    p.group = G * p.qsub;
+    p.total = p.nbq * p.B * p.Hkv * G * p.qsub;
+    const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+    SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+    sparse_attn_mfma_kernel<DT, 4, 128><<<(unsigned)grid, 256, 0, stream>>>(p);
+  }
+  return launch_status("sparse_attn_mfma_kernel");
+}
+
+}  // namespace
+}  // namespace ssa
+
+extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n,
+                                                 int64_t d, int64_t block) {
+  if (dtype == SSA_F32 || block <= 0) return 0;
+  const int64_t n_pad = (n + block - 1) / block * block;
+  return (size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u;
+}
+
+extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
+                               int64_t d, int64_t block, int64_t stride_b, int64_t stride_h,
+                               int64_t stride_n, void* vt, size_t vt_bytes, ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(v && vt, SSA_ERR_INVALID, "transpose_v: NULL pointer argument");
+  SSA_REQUIRE(dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
+              "transpose_v: 16-bit dtypes only");
+  SSA_REQUIRE(B > 0 && Hkv > 0 && n > 0 && block > 0, SSA_ERR_INVALID, "transpose_v: bad sizes");
+  SSA_REQUIRE(d == 64, SSA_ERR_UNSUPPORTED, "transpose_v: head_dim must be 64");
+  SSA_REQUIRE(block % 64 == 0, SSA_ERR_UNSUPPORTED, "transpose_v: block must be a multiple of 64");
+  SSA_REQUIRE(aligned16(v) && aligned16(vt) && stride_b % 8 == 0 && stride_h % 8 == 0 &&
+                  stride_n % 8 == 0,
+              SSA_ERR_UNSUPPORTED, "transpose_v: 16-byte alignment required");
+  const size_t need = ssa_sparse_attn_workspace_size(dtype, B, Hkv, n, d, block);
+  SSA_REQUIRE(vt_bytes >= need, SSA_ERR_WORKSPACE, "transpose_v: needs %zu bytes", need);
+  const int64_t n_pad = (n + block - 1) / block * block;
+  SSA_REQUIRE(B * Hkv < 65536 && n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
+              "transpose_v: grid too large");
+  dim3 tg((unsigned)(n_pad / 64), (unsigned)(B * Hkv));
+  transpose_v_kernel<<<tg, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const char*>(v), static_cast<char*>(vt), Hkv, n, n_pad, stride_b, stride_h,
+      stride_n);
+  return launch_status("transpose_v_kernel");
+}
+
+extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                   int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
+                                   int64_t d, int64_t block, const int64_t* strides,
+                                   const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
+                                   float scale, float* lse, int flags, void* workspace,
+                                   size_t workspace_bytes, ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(q && k && v && out && strides && kv_num && kv_idx, SSA_ERR_INVALID,
+              "sparse_attn: NULL pointer argument");
+  SSA_REQUIRE(dtype == SSA_F32 || dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
+              "sparse_attn: unknown dtype %d", dtype);
+  SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && n > 0 && W > 0, SSA_ERR_INVALID,
+              "sparse_attn: sizes must be positive");
+  SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "sparse_attn: Hq not a multiple of Hkv");
+  SSA_REQUIRE(d == 64, SSA_ERR_UNSUPPORTED, "sparse_attn: head_dim %lld unsupported (64)",
+              (long long)d);
+  SSA_REQUIRE(block == 64 || (block > 0 && block % 128 == 0), SSA_ERR_UNSUPPORTED,
+              "sparse_attn: block %lld unsupported (64 or a multiple of 128)", (long long)block);
+  SSA_REQUIRE(B * Hq < (1ll << 24), SSA_ERR_UNSUPPORTED, "sparse_attn: too many heads");
+  SSA_REQUIRE((flags & ~SSA_ATTN_VT_READY) == 0, SSA_ERR_INVALID, "sparse_attn: unknown flags");
+  const int64_t vec = dtype == SSA_F32 ? 4 : 8;
+  for (int s = 0; s < 12; ++s)
+    SSA_REQUIRE(strides[s] % vec == 0, SSA_ERR_UNSUPPORTED,
+                "sparse_attn: stride %d (%lld) not a multiple of 16 bytes", s,
+                (long long)strides[s]);
+  SSA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), SSA_ERR_UNSUPPORTED,
+              "sparse_attn: tensors must be 16-byte aligned");
+  SSA_REQUIRE(scale > 0.0f && isfinite(scale), SSA_ERR_INVALID, "sparse_attn: scale must be > 0");
+
+  AttnParams p;
+  p.q = static_cast<const char*>(q);
+  p.k = static_cast<const char*>(k);
+  p.v = static_cast<const char*>(v);
+  p.o = static_cast<char*>(out);
+  p.qsb = strides[0]; p.qsh = strides[1]; p.qsn = strides[2];
+  p.ksb = strides[3]; p.ksh = strides[4]; p.ksn = strides[5];
+  p.vsb = strides[6]; p.vsh = strides[7]; p.vsn = strides[8];
+  p.osb = strides[9]; p.osh = strides[10]; p.osn = strides[11];
+  p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.G = Hq / Hkv; p.n = n; p.block = block;
+  p.nbq = (n + block - 1) / block;
+  p.n_pad = p.nbq * block;
+  p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
+  p.scale_log2 = scale * kLog2e;
+  p.lse = lse;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  if (dtype == SSA_F32) {
+    p.vt = nullptr;
+    p.qsub = block / 64;
+    p.group = 1;
+    p.total = p.nbq * B * Hq * p.qsub;
+    SSA_REQUIRE(p.total < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+    sparse_attn_f32_kernel<<<(unsigned)p.total, 64, 0, st>>>(p);
+    return launch_status("sparse_attn_f32_kernel");
+  }
+  const size_t need = ssa_sparse_attn_workspace_size(dtype, B, Hkv, n, d, block);
+  SSA_REQUIRE(workspace != nullptr && workspace_bytes >= need && aligned16(workspace),
+              SSA_ERR_WORKSPACE, "sparse_attn: workspace needs %zu bytes (16-byte aligned)", need);
+  p.vt = static_cast<const char*>(workspace);
+  if (!(flags & SSA_ATTN_VT_READY))
+    SSA_TRY(ssa_transpose_v(v, dtype, B, Hkv, n, d, block, p.vsb, p.vsh, p.vsn, workspace,
+                            workspace_bytes, stream));
+  if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, st);
+  return launch_mfma<SSA_F16>(p, st);
+}

@@ -1,0 +1,82 @@
+// Shared helpers for the gfx950 kernels of libssa_hip.so: status/error plumbing, dtype traits,
+// and the order-preserving float key used by the router.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ssa_hip.h"
+
+namespace ssa {
+
+// Records a printf-style message as this thread's last error (read via ssa_last_error()).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Maps a hipError_t to SSA_ERR_HIP with a message naming `what`; SSA_OK on success.
+int hip_status(hipError_t e, const char* what);
+
+// Checks for a failed launch of the kernel named `what`.
+inline int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
+
+#define SSA_REQUIRE(cond, code, ...)   \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::ssa::set_error(__VA_ARGS__);   \
+      return (code);                   \
+    }                                  \
+  } while (0)
+
+#define SSA_TRY(expr)            \
+  do {                           \
+    int ssa_rc_ = (expr);        \
+    if (ssa_rc_ != SSA_OK)       \
+      return ssa_rc_;            \
+  } while (0)
+
+inline int dtype_size(int dtype) {
+  switch (dtype) {
+    case SSA_F32: return 4;
+    case SSA_F16: return 2;
+    case SSA_BF16: return 2;
+    default: return 0;
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- device-side helpers -----------------------------------------------------------------------
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Converts 8 packed 16-bit values (one 16-byte load) to fp32.
+__device__ inline void unpack8(const u32x4& w, float* out, bool is_bf16) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    unsigned int x = w[i];
+    if (is_bf16) {
+      out[2 * i] = __uint_as_float(x << 16);
+      out[2 * i + 1] = __uint_as_float(x & 0xffff0000u);
+    } else {
+      _Float16 lo = __builtin_bit_cast(_Float16, (unsigned short)(x & 0xffffu));
+      _Float16 hi = __builtin_bit_cast(_Float16, (unsigned short)(x >> 16));
+      out[2 * i] = (float)lo;
+      out[2 * i + 1] = (float)hi;
+    }
+  }
+}
+
+// Order-preserving map of an fp32 score to uint32 (larger score -> larger key). -0 is folded
+// onto +0 so the two compare equal, as they do for torch.topk; NaN maps above +inf (torch.topk
+// treats NaN as the largest value).
+__device__ inline unsigned int score_key(float r) {
+  if (r != r) return 0xffffffffu;
+  if (r == 0.0f) r = 0.0f;
+  unsigned int u = __float_as_uint(r);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+}  // namespace ssa

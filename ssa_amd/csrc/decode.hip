@@ -1,0 +1,407 @@
+// Routed decode: one query token per head attends the keys <= pos of its selected blocks.
+//
+// decode_partial_kernel: one wave per (query row, selected block) -- the gather is split over
+//   every selected block of every head, so a step's ~30 MB of K/V are read by ~1000 waves in
+//   parallel. Each wave computes its block's scores (one key per lane per pass, 16-byte row
+//   loads), the block's running max / sum in fp32 and its unnormalised output row (lane = head
+//   dim, coalesced V row reads), and writes (m, l, o) to the workspace.
+// decode_combine_kernel: merges a row's partials with the usual max-rescaling.
+// decode_step: append the new token -> summarise a just-completed block -> route the query over
+//   the complete blocks (route_impl, SSA_ROUTE_QUERY) -> partial -> combine.
+//
+// Reference: ssa/ivf_decode.py:49-62 (decode_attend), :128-136 (per-step body);
+// ssa/gemma_ssa.py:85-137,225-240 (exact per-query router and softmax at q_len = 1).
+#include <math.h>
+
+#include "common.h"
+
+namespace ssa {
+
+int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n, int64_t d,
+                         int64_t sb, int64_t sh, int64_t sn, int64_t block, int64_t n_real,
+                         int mode, float* mu, float* var, float* m3, int64_t nb_out,
+                         int64_t block_offset, hipStream_t stream);
+int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
+               int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
+               int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
+               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxDecodeBlock = 1024;
+constexpr int kMaxDecodeD = 256;
+
+struct DecodeParams {
+  const char* q;
+  const char* k;
+  const char* v;
+  char* o;
+  int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
+  int64_t B, Hq, G, nq, cap, d, block, pos;
+  const int32_t* kv_num;
+  const int32_t* kv_idx;
+  int64_t W;
+  float scale_log2;
+  float* part;  // (B*Hq*nq, W, d + 2): m, l, o[d]
+};
+
+template <int DT>
+__device__ inline float load_elem(const char* base, int64_t idx) {
+  if constexpr (DT == SSA_F32) return reinterpret_cast<const float*>(base)[idx];
+  else {
+    unsigned short u = reinterpret_cast<const unsigned short*>(base)[idx];
+    if constexpr (DT == SSA_BF16) return __uint_as_float((unsigned int)u << 16);
+    else return (float)__builtin_bit_cast(_Float16, u);
+  }
+}
+
+template <int DT>
+__device__ inline void store_elem(char* base, int64_t idx, float x) {
+  if constexpr (DT == SSA_F32) reinterpret_cast<float*>(base)[idx] = x;
+  else if constexpr (DT == SSA_BF16)
+    reinterpret_cast<unsigned short*>(base)[idx] = __builtin_bit_cast(unsigned short, (__bf16)x);
+  else
+    reinterpret_cast<unsigned short*>(base)[idx] = __builtin_bit_cast(unsigned short, (_Float16)x);
+}
+
+__device__ inline float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// grid (rows * W): block x handles selected block j = x % W of query row x / W, one wave each.
+template <int DT>
+__global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
+  __shared__ float qs[kMaxDecodeD];
+  __shared__ float ps[kMaxDecodeBlock];
+  const int lane = threadIdx.x;
+  const int64_t j = blockIdx.x % p.W;
+  const int64_t rowid = blockIdx.x / p.W;  // (b*Hq + h)*nq + r
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.G;
+  const int64_t pos = p.pos + r;
+  const int d = (int)p.d;
+  float* part = p.part + (rowid * p.W + j) * (p.d + 2);
+
+  int cnt = p.kv_num[rowid];
+  if (cnt > p.W) cnt = (int)p.W;
+  const int32_t* list = p.kv_idx + rowid * p.W;
+  bool empty = j >= cnt;
+  int64_t c = 0;
+  if (!empty) {
+    c = list[j];
+    const int64_t nblk = (p.cap + p.block - 1) / p.block;
+    if (c < 0 || c >= nblk || c * p.block > pos) empty = true;
+    for (int64_t jj = 0; jj < j && !empty; ++jj)  // a repeated id is attended once
+      if (list[jj] == c) empty = true;
+  }
+  if (empty) {
+    if (lane == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    for (int e = lane; e < d; e += 64) part[2 + e] = 0.0f;
+    return;
+  }
+  const int64_t key0 = c * p.block;
+  int64_t key1 = key0 + p.block;
+  if (key1 > pos + 1) key1 = pos + 1;
+  if (key1 > p.cap) key1 = p.cap;
+  const int nk = (int)(key1 - key0);
+
+  const char* qb = p.q;
+  const int64_t qoff = b * p.qsb + h * p.qsh + r * p.qsn;
+  for (int e = lane; e < d; e += 64) qs[e] = load_elem<DT>(qb, qoff + e);
+  __syncthreads();
+
+  const int64_t koff = b * p.ksb + kvh * p.ksh;
+  float mloc = -INFINITY;
+  for (int kk = lane; kk < nk; kk += 64) {
+    const int64_t roff = koff + (key0 + kk) * p.ksn;
+    float s = 0.0f;
+    if constexpr (DT == SSA_F32) {
+      for (int e = 0; e < d; e += 4) {
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.k) + roff + e);
+        s = fmaf(qs[e], kv[0], s);
+        s = fmaf(qs[e + 1], kv[1], s);
+        s = fmaf(qs[e + 2], kv[2], s);
+        s = fmaf(qs[e + 3], kv[3], s);
+      }
+    } else {
+      for (int e = 0; e < d; e += 8) {
+        const u32x4 w =
+            *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned short*>(p.k) + roff + e);
+        float kv[8];
+        unpack8(w, kv, DT == SSA_BF16);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s = fmaf(qs[e + t], kv[t], s);
+      }
+    }
+    const float sl = s * p.scale_log2;
+    ps[kk] = sl;
+    mloc = fmaxf(mloc, sl);
+  }
+  const float m = wave_max(mloc);
+  __syncthreads();
+  float lloc = 0.0f;
+  for (int kk = lane; kk < nk; kk += 64) {
+    const float pk = exp2f(ps[kk] - m);
+    ps[kk] = pk;
+    lloc += pk;
+  }
+  const float l = wave_sum(lloc);
+  __syncthreads();
+  const int64_t voff = b * p.vsb + kvh * p.vsh;
+  for (int e = lane; e < d; e += 64) {
+    float acc = 0.0f;
+    for (int kk = 0; kk < nk; ++kk)
+      acc = fmaf(ps[kk], load_elem<DT>(p.v, voff + (key0 + kk) * p.vsn + e), acc);
+    part[2 + e] = acc;
+  }
+  if (lane == 0) {
+    part[0] = m;
+    part[1] = l;
+  }
+}
+
+// grid (B*Hq*nq), one wave each.
+template <int DT>
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
+  const int lane = threadIdx.x;
+  const int64_t rowid = blockIdx.x;
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq;
+  int cnt = p.kv_num[rowid];
+  if (cnt > p.W) cnt = (int)p.W;
+  const float* part = p.part + rowid * p.W * (p.d + 2);
+  float M = -INFINITY;
+  for (int j = 0; j < cnt; ++j) M = fmaxf(M, part[j * (p.d + 2)]);
+  float L = 0.0f;
+  for (int j = 0; j < cnt; ++j) {
+    const float mj = part[j * (p.d + 2)];
+    if (mj != -INFINITY) L += part[j * (p.d + 2) + 1] * exp2f(mj - M);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  for (int e = lane; e < p.d; e += 64) {
+    float acc = 0.0f;
+    for (int j = 0; j < cnt; ++j) {
+      const float mj = part[j * (p.d + 2)];
+      if (mj != -INFINITY) acc = fmaf(part[j * (p.d + 2) + 2 + e], exp2f(mj - M), acc);
+    }
+    store_elem<DT>(p.o, b * p.osb + h * p.osh + r * p.osn + e, acc * inv);
+  }
+}
+
+// Element strides of the append: new token rows (b,h) and caches (b,h,n).
+struct AppendStrides {
+  int64_t knb, knh, vnb, vnh, kcb, kch, kcn, vcb, vch, vcn;
+};
+
+// k_new/v_new (B, Hkv, d) -> caches at row pos. grid (B*Hkv).
+template <int DT>
+__global__ __launch_bounds__(64) void decode_append_kernel(const char* kn, const char* vn,
+                                                           char* kc, char* vc, int64_t Hkv,
+                                                           int64_t d, int64_t pos,
+                                                           AppendStrides st) {
+  const int64_t bk = blockIdx.x;
+  const int64_t b = bk / Hkv, h = bk % Hkv;
+  for (int e = threadIdx.x; e < d; e += 64) {
+    store_elem<DT>(kc, b * st.kcb + h * st.kch + pos * st.kcn + e,
+                   load_elem<DT>(kn, b * st.knb + h * st.knh + e));
+    store_elem<DT>(vc, b * st.vcb + h * st.vch + pos * st.vcn + e,
+                   load_elem<DT>(vn, b * st.vnb + h * st.vnh + e));
+  }
+}
+
+// q (B, Hq, d) strided -> fp32 (B, Hq, d) contiguous. grid (B*Hq).
+template <int DT>
+__global__ __launch_bounds__(64) void rows_to_f32_kernel(const char* q, float* out, int64_t Hq,
+                                                         int64_t d, int64_t qsb, int64_t qsh) {
+  const int64_t r = blockIdx.x;
+  const int64_t b = r / Hq, h = r % Hq;
+  for (int e = threadIdx.x; e < d; e += 64) out[r * d + e] = load_elem<DT>(q, b * qsb + h * qsh + e);
+}
+
+int run_attend(int dtype, DecodeParams& p, hipStream_t stream) {
+  const int64_t rows = p.B * p.Hq * p.nq;
+  SSA_REQUIRE(rows * p.W < (1ll << 31), SSA_ERR_UNSUPPORTED, "decode: grid too large");
+  const unsigned g1 = (unsigned)(rows * p.W);
+  switch (dtype) {
+    case SSA_F32: decode_partial_kernel<SSA_F32><<<g1, 64, 0, stream>>>(p); break;
+    case SSA_F16: decode_partial_kernel<SSA_F16><<<g1, 64, 0, stream>>>(p); break;
+    default: decode_partial_kernel<SSA_BF16><<<g1, 64, 0, stream>>>(p); break;
+  }
+  SSA_TRY(launch_status("decode_partial_kernel"));
+  const unsigned g2 = (unsigned)rows;
+  switch (dtype) {
+    case SSA_F32: decode_combine_kernel<SSA_F32><<<g2, 64, 0, stream>>>(p); break;
+    case SSA_F16: decode_combine_kernel<SSA_F16><<<g2, 64, 0, stream>>>(p); break;
+    default: decode_combine_kernel<SSA_BF16><<<g2, 64, 0, stream>>>(p); break;
+  }
+  return launch_status("decode_combine_kernel");
+}
+
+int check_decode(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t nq, int64_t cap,
+                 int64_t d, int64_t block, int64_t pos, int64_t W, const int64_t* strides,
+                 int nstrides) {
+  SSA_REQUIRE(dtype == SSA_F32 || dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
+              "decode: unknown dtype %d", dtype);
+  SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && nq > 0 && cap > 0 && W > 0 && block > 0,
+              SSA_ERR_INVALID, "decode: sizes must be positive");
+  SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "decode: Hq not a multiple of Hkv");
+  SSA_REQUIRE(pos >= 0 && pos + nq <= cap, SSA_ERR_INVALID,
+              "decode: query positions [%lld,%lld) outside the cache [0,%lld)", (long long)pos,
+              (long long)(pos + nq), (long long)cap);
+  SSA_REQUIRE(d % 8 == 0 && d >= 8 && d <= kMaxDecodeD, SSA_ERR_UNSUPPORTED,
+              "decode: head_dim %lld unsupported (multiple of 8, <= 256)", (long long)d);
+  SSA_REQUIRE(block <= kMaxDecodeBlock, SSA_ERR_UNSUPPORTED, "decode: block > %d", kMaxDecodeBlock);
+  SSA_REQUIRE(W < 65536, SSA_ERR_UNSUPPORTED, "decode: W too large");
+  const int64_t vec = dtype == SSA_F32 ? 4 : 8;
+  for (int s = 0; s < nstrides; ++s)
+    SSA_REQUIRE(strides[s] % vec == 0, SSA_ERR_UNSUPPORTED,
+                "decode: stride %d not a multiple of 16 bytes", s);
+  return SSA_OK;
+}
+
+}  // namespace
+}  // namespace ssa
+
+extern "C" size_t ssa_decode_attend_workspace_size(int64_t B, int64_t Hq, int64_t nq, int64_t W,
+                                                   int64_t d) {
+  return (size_t)B * (size_t)Hq * (size_t)nq * (size_t)W * (size_t)(d + 2) * 4u;
+}
+
+extern "C" int ssa_decode_attend(const void* q, const void* k, const void* v, void* out, int dtype,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t nq, int64_t cap,
+                                 int64_t d, int64_t block, int64_t pos, const int64_t* strides,
+                                 const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
+                                 float scale, void* workspace, size_t workspace_bytes,
+                                 ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(q && k && v && out && strides && kv_num && kv_idx, SSA_ERR_INVALID,
+              "decode_attend: NULL pointer argument");
+  SSA_TRY(check_decode(dtype, B, Hq, Hkv, nq, cap, d, block, pos, W, strides, 12));
+  SSA_REQUIRE(aligned16(k) && aligned16(v), SSA_ERR_UNSUPPORTED,
+              "decode_attend: caches must be 16-byte aligned");
+  const size_t need = ssa_decode_attend_workspace_size(B, Hq, nq, W, d);
+  SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
+              "decode_attend: workspace needs %zu bytes", need);
+  SSA_REQUIRE(scale > 0.0f, SSA_ERR_INVALID, "decode_attend: scale must be > 0");
+  DecodeParams p;
+  p.q = static_cast<const char*>(q);
+  p.k = static_cast<const char*>(k);
+  p.v = static_cast<const char*>(v);
+  p.o = static_cast<char*>(out);
+  p.qsb = strides[0]; p.qsh = strides[1]; p.qsn = strides[2];
+  p.ksb = strides[3]; p.ksh = strides[4]; p.ksn = strides[5];
+  p.vsb = strides[6]; p.vsh = strides[7]; p.vsn = strides[8];
+  p.osb = strides[9]; p.osh = strides[10]; p.osn = strides[11];
+  p.B = B; p.Hq = Hq; p.G = Hq / Hkv; p.nq = nq; p.cap = cap; p.d = d; p.block = block;
+  p.pos = pos;
+  p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
+  p.scale_log2 = scale * kLog2e;
+  p.part = static_cast<float*>(workspace);
+  return run_attend(dtype, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t ssa_decode_step_workspace_size(int64_t B, int64_t Hq, int64_t cap, int64_t d,
+                                                 int64_t block, int64_t W) {
+  const int64_t nbk = block > 0 ? (cap + block - 1) / block : 0;
+  size_t qf = (size_t)B * Hq * d * 4u;
+  qf = (qf + 255) / 256 * 256;
+  size_t keys = (size_t)B * Hq * nbk * 4u;
+  keys = (keys + 255) / 256 * 256;
+  return qf + keys + ssa_decode_attend_workspace_size(B, Hq, 1, W, d);
+}
+
+extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* kcache,
+                               void* vcache, float* mu, float* var, void* out, int dtype,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t d,
+                               int64_t block, int64_t pos, const int64_t* strides, int64_t top_c,
+                               float budget_frac, int64_t local, float coef2, float scale,
+                               int32_t* kv_num, int32_t* kv_idx, int64_t W, void* workspace,
+                               size_t workspace_bytes, ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(q && k_new && v_new && kcache && vcache && mu && var && out && strides && kv_num &&
+                  kv_idx,
+              SSA_ERR_INVALID, "decode_step: NULL pointer argument");
+  SSA_TRY(check_decode(dtype, B, Hq, Hkv, 1, cap, d, block, pos, W, strides, 14));
+  SSA_REQUIRE(aligned16(kcache) && aligned16(vcache), SSA_ERR_UNSUPPORTED,
+              "decode_step: caches must be 16-byte aligned");
+  SSA_REQUIRE(scale > 0.0f, SSA_ERR_INVALID, "decode_step: scale must be > 0");
+  const size_t need = ssa_decode_step_workspace_size(B, Hq, cap, d, block, W);
+  SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
+              "decode_step: workspace needs %zu bytes", need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nbk = (cap + block - 1) / block;
+  const int es = dtype_size(dtype);
+  char* ws = static_cast<char*>(workspace);
+  const size_t qf_bytes = ((size_t)B * Hq * d * 4u + 255) / 256 * 256;
+  const size_t key_bytes = ((size_t)B * Hq * nbk * 4u + 255) / 256 * 256;
+  float* qf = reinterpret_cast<float*>(ws);
+  void* keys = ws + qf_bytes;
+  float* part = reinterpret_cast<float*>(ws + qf_bytes + key_bytes);
+
+  // 1. append the new token
+  AppendStrides as;
+  as.knb = strides[2]; as.knh = strides[3]; as.vnb = strides[4]; as.vnh = strides[5];
+  as.kcb = strides[6]; as.kch = strides[7]; as.kcn = strides[8];
+  as.vcb = strides[9]; as.vch = strides[10]; as.vcn = strides[11];
+  const char* kn = static_cast<const char*>(k_new);
+  const char* vn = static_cast<const char*>(v_new);
+  char* kc = static_cast<char*>(kcache);
+  char* vc = static_cast<char*>(vcache);
+  const unsigned gb = (unsigned)(B * Hkv);
+  switch (dtype) {
+    case SSA_F32: decode_append_kernel<SSA_F32><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
+    case SSA_F16: decode_append_kernel<SSA_F16><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
+    default: decode_append_kernel<SSA_BF16><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
+  }
+  SSA_TRY(launch_status("decode_append_kernel"));
+
+  // 2. a block completed at pos: its population summary becomes routable
+  if ((pos + 1) % block == 0) {
+    const int64_t c = pos / block;
+    const char* blk = kc + c * block * as.kcn * es;
+    SSA_TRY(launch_block_summary(blk, dtype, B, Hkv, block, d, as.kcb, as.kch, as.kcn, block, block,
+                                 SSA_STATS_POP, mu, var, nullptr, nbk, c, st));
+  }
+
+  // 3. route the queries over the complete blocks
+  const unsigned gr = (unsigned)(B * Hq);
+  const char* qc = static_cast<const char*>(q);
+  switch (dtype) {
+    case SSA_F32: rows_to_f32_kernel<SSA_F32><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
+    case SSA_F16: rows_to_f32_kernel<SSA_F16><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
+    default: rows_to_f32_kernel<SSA_BF16><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
+  }
+  SSA_TRY(launch_status("rows_to_f32_kernel"));
+  SSA_TRY(route_impl(qf, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
+                     budget_frac, local, coef2, 0.0f, pos, block, kv_num, kv_idx, W, keys,
+                     key_bytes, st));
+
+  // 4. attend
+  DecodeParams p;
+  p.q = qc;
+  p.k = kc;
+  p.v = vc;
+  p.o = static_cast<char*>(out);
+  p.qsb = strides[0]; p.qsh = strides[1]; p.qsn = 0;
+  p.ksb = as.kcb; p.ksh = as.kch; p.ksn = as.kcn;
+  p.vsb = as.vcb; p.vsh = as.vch; p.vsn = as.vcn;
+  p.osb = strides[12]; p.osh = strides[13]; p.osn = 0;
+  p.B = B; p.Hq = Hq; p.G = Hq / Hkv; p.nq = 1; p.cap = cap; p.d = d; p.block = block;
+  p.pos = pos;
+  p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
+  p.scale_log2 = scale * kLog2e;
+  p.part = part;
+  return run_attend(dtype, p, st);
+}

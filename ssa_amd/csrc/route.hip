@@ -1,0 +1,509 @@
+// Cumulant router: scores every (row, candidate key block) pair, then selects the top-keep
+// candidates per row, merges the local window and emits compact ascending block lists.
+//
+// Stage 1 (route_score_kernel): a 64-row x 64-candidate tile per workgroup. Rows of one key head
+//   (its Hq/Hkv query heads x the query blocks of the current chunk) share the candidates'
+//   mu / var / m3, which are staged once per tile in LDS. Inner products accumulate in fp64 from
+//   the fp32 operands (so each score is the correctly rounded value of the reference's formula up
+//   to fp64 noise) and the fp32 score is assembled in the reference's evaluation order. Scores
+//   are stored as order-preserving uint32 keys in the workspace.
+// Stage 2 (route_select_kernel): one 256-thread workgroup per row. An 8-bit-digit radix select
+//   finds the keep-th largest key T; keys > T are taken, and keys == T in increasing block order
+//   until keep is reached (ties -> lowest block index). The selection, the own block and its
+//   `local` predecessors are OR-ed into an LDS bitmap that is compacted in ascending order.
+//
+// Reference: ssa/ssa_kernel.py:45-57 (block_route), :92-118 (block_route_budget),
+// ssa/gemma_ssa.py:99-131 (_selection_mask).
+#include <math.h>
+
+#include "common.h"
+
+namespace ssa {
+namespace {
+
+constexpr int kTile = 64;       // rows and candidates per score tile
+constexpr int kDK = 32;         // head-dim chunk staged in LDS
+constexpr int kSelThreads = 256;
+constexpr int kMaxNbk = 65536;  // bitmap capacity of the select kernel
+constexpr int kCacheKeys = 8192;
+
+struct RouteGeom {
+  int mode;
+  int64_t Hq, Hkv, G;
+  int64_t nbq;       // query rows per head (whole problem)
+  int64_t nbk;       // key blocks
+  int64_t i0, ni;    // current chunk of query rows [i0, i0+ni)
+  int64_t query_pos;
+  int64_t block;
+  int64_t top_c;
+  float budget_frac;
+  int64_t local;
+};
+
+// Number of candidates of query row i: budget -> c < i, flat -> c <= i, query -> complete blocks.
+__host__ __device__ inline int64_t row_cmax(const RouteGeom& g, int64_t i) {
+  int64_t c;
+  if (g.mode == SSA_ROUTE_BUDGET) c = i;
+  else if (g.mode == SSA_ROUTE_FLAT) c = i + 1;
+  else c = (g.query_pos + i + 1) / g.block;
+  if (c > g.nbk) c = g.nbk;
+  return c < 0 ? 0 : c;
+}
+
+__host__ __device__ inline int64_t row_own(const RouteGeom& g, int64_t i) {
+  return g.mode == SSA_ROUTE_QUERY ? (g.query_pos + i) / g.block : i;
+}
+
+// keep count before clipping to the candidate count. Budget: ceil(fp32(frac) * nvis) in fp32,
+// clamped to >= 1 (ssa/ssa_kernel.py:105-106, ssa/gemma_ssa.py:115-118).
+__host__ __device__ inline int64_t row_keep(const RouteGeom& g, int64_t cmax) {
+  if (g.mode == SSA_ROUTE_FLAT || g.top_c >= 0) return g.top_c;
+  float prod = g.budget_frac * (float)cmax;
+  int64_t k = (int64_t)ceilf(prod);
+  return k < 1 ? 1 : k;
+}
+
+template <bool EDGE>
+__global__ __launch_bounds__(256) void route_score_kernel(
+    const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
+    unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
+  __shared__ float Qs[kDK][kTile + 1];
+  __shared__ float Q2s[kDK][kTile + 1];
+  __shared__ float Ms[kDK][kTile + 1];
+  __shared__ float Vs[kDK][kTile + 1];
+  __shared__ float Q3s[EDGE ? kDK : 1][kTile + 1];
+  __shared__ float M3s[EDGE ? kDK : 1][kTile + 1];
+
+  const int64_t bk = blockIdx.y;  // b * Hkv + kvh
+  const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
+  const int64_t rt = blockIdx.x / cand_tiles, ct = blockIdx.x % cand_tiles;
+  const int64_t R = g.G * g.ni;  // rows of this key head in the chunk
+  const int64_t r0 = rt * kTile;
+  const int64_t c0 = ct * kTile;
+  if (r0 >= R) return;
+  int64_t r_last = r0 + kTile - 1 < R ? r0 + kTile - 1 : R - 1;
+  const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
+  if (c0 >= row_cmax(g, imax)) return;  // uniform: no row of the tile has these candidates
+
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;
+  double e1[4][4], e2[4][4], e3[EDGE ? 4 : 1][EDGE ? 4 : 1];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e1[a][c] = 0.0;
+      e2[a][c] = 0.0;
+      if constexpr (EDGE) e3[a][c] = 0.0;
+    }
+
+  const float* kv_mu = mu + (bk * g.nbk) * d;
+  const float* kv_var = var ? var + (bk * g.nbk) * d : nullptr;
+  const float* kv_m3 = EDGE ? m3 + (bk * g.nbk) * d : nullptr;
+
+  for (int k0 = 0; k0 < d; k0 += kDK) {
+    __syncthreads();
+    for (int idx = tid; idx < kTile * kDK; idx += 256) {
+      const int rr = idx / kDK, kk = idx % kDK;
+      const int64_t r = r0 + rr;
+      const bool kin = k0 + kk < d;
+      float q = 0.0f;
+      if (r < R && kin) {
+        const int64_t h = kvh * g.G + r / g.ni;
+        const int64_t i = g.i0 + r % g.ni;
+        q = rows[((b * g.Hq + h) * g.nbq + i) * d + k0 + kk];
+      }
+      const float q2 = q * q;
+      Qs[kk][rr] = q;
+      Q2s[kk][rr] = q2;
+      if constexpr (EDGE) Q3s[kk][rr] = q2 * q;
+      const int64_t c = c0 + rr;
+      float m = 0.0f, v = 0.0f, t = 0.0f;
+      if (c < g.nbk && kin) {
+        m = kv_mu[c * d + k0 + kk];
+        if (kv_var) v = kv_var[c * d + k0 + kk];
+        if constexpr (EDGE) t = kv_m3[c * d + k0 + kk];
+      }
+      Ms[kk][rr] = m;
+      Vs[kk][rr] = v;
+      if constexpr (EDGE) M3s[kk][rr] = t;
+    }
+    __syncthreads();
+    const int kend = d - k0 < kDK ? d - k0 : kDK;
+    for (int kk = 0; kk < kend; ++kk) {
+      double qd[4], q2d[4], md[4], vd[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        qd[a] = (double)Qs[kk][tr + 16 * a];
+        q2d[a] = (double)Q2s[kk][tr + 16 * a];
+        md[a] = (double)Ms[kk][tc + 16 * a];
+        vd[a] = (double)Vs[kk][tc + 16 * a];
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          e1[a][c] = fma(qd[a], md[c], e1[a][c]);
+          e2[a][c] = fma(q2d[a], vd[c], e2[a][c]);
+        }
+      if constexpr (EDGE) {
+        double q3d[4], td[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          q3d[a] = (double)Q3s[kk][tr + 16 * a];
+          td[a] = (double)M3s[kk][tc + 16 * a];
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) e3[a][c] = fma(q3d[a], td[c], e3[a][c]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int64_t r = r0 + tr + 16 * a;
+    if (r >= R) continue;
+    const int64_t h = kvh * g.G + r / g.ni;
+    const int64_t il = r % g.ni;
+    const int64_t cmax = row_cmax(g, g.i0 + il);
+    unsigned int* krow = keys + ((b * g.Hq + h) * g.ni + il) * g.nbk;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t cand = c0 + tc + 16 * c;
+      if (cand >= cmax) continue;
+      // r = E1 + coef2*E2 (+ coef3*E3), each product term rounded to fp32 as torch does
+      // explicit _rn ops: no FMA contraction, so the rounding matches torch's mul then add
+      float s = __fadd_rn((float)e1[a][c], __fmul_rn(coef2, (float)e2[a][c]));
+      if constexpr (EDGE) s = __fadd_rn(s, __fmul_rn(coef3, (float)e3[a][c]));
+      krow[cand] = score_key(s);
+    }
+  }
+}
+
+// Block-wide exclusive scan of one int per thread (256 threads); returns the exclusive prefix
+// and writes the total to *total.
+__device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wave_sums[wave] = incl;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelThreads / 64; ++w) {
+    if (w < wave) base += wave_sums[w];
+    tot += wave_sums[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + incl - v;
+}
+
+__global__ __launch_bounds__(kSelThreads) void route_select_kernel(
+    const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
+    int32_t* __restrict__ kv_idx, int64_t W) {
+  __shared__ unsigned int bits[kMaxNbk / 32];
+  __shared__ unsigned int cache[kCacheKeys];
+  __shared__ unsigned int hist[256];
+  __shared__ int wave_sums[kSelThreads / 64];
+  __shared__ unsigned int sh_digit, sh_above;
+
+  const int tid = threadIdx.x;
+  const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
+  const int64_t bh = lrow / g.ni, il = lrow % g.ni;
+  const int64_t i = g.i0 + il;
+  const int64_t cmax = row_cmax(g, i);
+  int64_t keep = row_keep(g, cmax);
+  const int64_t K = keep < cmax ? keep : cmax;
+  const unsigned int* krow = keys + lrow * g.nbk;
+  const int nwords = (int)((g.nbk + 31) / 32);
+
+  for (int w = tid; w < nwords; w += kSelThreads) bits[w] = 0u;
+  const bool cached = cmax <= kCacheKeys;
+  if (cached && K > 0 && K < cmax)
+    for (int64_t c = tid; c < cmax; c += kSelThreads) cache[c] = krow[c];
+  __syncthreads();
+
+  if (K >= cmax) {
+    for (int64_t c = tid; c < cmax; c += kSelThreads) atomicOr(&bits[c >> 5], 1u << (c & 31));
+  } else if (K > 0) {
+    unsigned int prefix = 0u, pmask = 0u;
+    unsigned int kk = (unsigned int)K;  // rank of T among keys matching the prefix
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[tid] = 0u;
+      __syncthreads();
+      for (int64_t c = tid; c < cmax; c += kSelThreads) {
+        unsigned int key = cached ? cache[c] : krow[c];
+        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        unsigned int v[4], t = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = hist[4 * tid + j];
+          t += v[j];
+        }
+        unsigned int suf = t;  // inclusive suffix over lanes >= tid
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          unsigned int o = __shfl_down(suf, off, 64);
+          if (tid + off < 64) suf += o;
+        }
+        unsigned int above = suf - t;  // keys in bins of higher lanes
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+          if (above < kk && kk <= above + v[j]) {
+            sh_digit = (unsigned int)(4 * tid + j);
+            sh_above = above;
+          }
+          above += v[j];
+        }
+      }
+      __syncthreads();
+      prefix |= sh_digit << shift;
+      pmask |= 0xffu << shift;
+      kk -= sh_above;
+      __syncthreads();
+    }
+    const unsigned int T = prefix;
+    const unsigned int need_eq = kk;        // keys equal to T still to take
+    const unsigned int n_eq = hist[T & 255u];  // keys equal to T (last pass histogram)
+    __syncthreads();
+    if (need_eq == n_eq) {
+      for (int64_t c = tid; c < cmax; c += kSelThreads) {
+        unsigned int key = cached ? cache[c] : krow[c];
+        if (key >= T) atomicOr(&bits[c >> 5], 1u << (c & 31));
+      }
+    } else {
+      for (int64_t c = tid; c < cmax; c += kSelThreads) {
+        unsigned int key = cached ? cache[c] : krow[c];
+        if (key > T) atomicOr(&bits[c >> 5], 1u << (c & 31));
+      }
+      // ties at T: take the lowest block indices first
+      unsigned int taken = 0;
+      for (int64_t base = 0; base < cmax && taken < need_eq; base += kSelThreads) {
+        const int64_t c = base + tid;
+        int flag = 0;
+        if (c < cmax) {
+          unsigned int key = cached ? cache[c] : krow[c];
+          flag = key == T;
+        }
+        int tot;
+        int pre = block_exclusive_scan(flag, wave_sums, &tot);
+        if (flag && taken + (unsigned int)pre < need_eq) atomicOr(&bits[c >> 5], 1u << (c & 31));
+        taken += (unsigned int)tot;
+      }
+    }
+  }
+  __syncthreads();
+  // own block and its `local` predecessors, clipped to [0, own] and to existing blocks
+  const int64_t own = row_own(g, i);
+  int64_t lo = own - g.local;
+  if (lo < 0) lo = 0;
+  int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
+  for (int64_t c = lo + tid; c <= hi; c += kSelThreads) atomicOr(&bits[c >> 5], 1u << (c & 31));
+  __syncthreads();
+
+  // ascending compaction of the bitmap
+  const int wpt = (nwords + kSelThreads - 1) / kSelThreads;
+  const int w0 = tid * wpt;
+  int cnt = 0;
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
+  int total;
+  int pos = block_exclusive_scan(cnt, wave_sums, &total);
+  int32_t* out = kv_idx + (bh * g.nbq + i) * W;
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+    unsigned int m = bits[w];
+    while (m) {
+      int bit = __ffs(m) - 1;
+      m &= m - 1;
+      if (pos < W) out[pos] = (int32_t)(w * 32 + bit);
+      ++pos;
+    }
+  }
+  const int64_t num = total < W ? total : W;
+  for (int64_t p = num + tid; p < W; p += kSelThreads) out[p] = 0;
+  if (tid == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
+}
+
+__global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
+    const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int64_t W,
+    int64_t nbk, uint8_t* __restrict__ sel, int32_t* __restrict__ kv_full) {
+  __shared__ unsigned int bits[kMaxNbk / 32];
+  __shared__ unsigned int wpre[kMaxNbk / 32];
+  __shared__ int wave_sums[kSelThreads / 64];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int nwords = (int)((nbk + 31) / 32);
+  for (int w = tid; w < nwords; w += kSelThreads) bits[w] = 0u;
+  __syncthreads();
+  int num = kv_num[row];
+  if (num > W) num = (int)W;
+  if (num < 0) num = 0;
+  for (int j = tid; j < num; j += kSelThreads) {
+    int c = kv_idx[row * W + j];
+    if (c >= 0 && c < nbk) atomicOr(&bits[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  const int wpt = (nwords + kSelThreads - 1) / kSelThreads;
+  const int w0 = tid * wpt;
+  int cnt = 0;
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
+  int total;
+  int pre = block_exclusive_scan(cnt, wave_sums, &total);
+  for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+    wpre[w] = (unsigned int)pre;
+    pre += __popc(bits[w]);
+  }
+  __syncthreads();
+  for (int64_t c = tid; c < nbk; c += kSelThreads) {
+    const unsigned int word = bits[c >> 5];
+    const bool s = (word >> (c & 31)) & 1u;
+    const int64_t below = wpre[c >> 5] + __popc(word & ((1u << (c & 31)) - 1u));
+    if (sel) sel[row * nbk + c] = s ? 1 : 0;
+    if (kv_full) {
+      const int64_t p = s ? below : total + (c - below);
+      kv_full[row * nbk + p] = (int32_t)c;
+    }
+  }
+}
+
+}  // namespace
+
+// Routes every row; exposed to the decode step, which calls it with a single query row.
+int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
+               int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
+               int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
+               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+               void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  SSA_REQUIRE(rows && mu && kv_num && kv_idx, SSA_ERR_INVALID, "route: NULL pointer argument");
+  SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && nbq > 0 && nbk > 0 && d > 0, SSA_ERR_INVALID,
+              "route: sizes must be positive");
+  SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "route: Hq=%lld not a multiple of Hkv=%lld",
+              (long long)Hq, (long long)Hkv);
+  SSA_REQUIRE(mode == SSA_ROUTE_BUDGET || mode == SSA_ROUTE_FLAT || mode == SSA_ROUTE_QUERY,
+              SSA_ERR_INVALID, "route: unknown mode %d", mode);
+  SSA_REQUIRE(local >= 0, SSA_ERR_INVALID, "route: local must be >= 0");
+  SSA_REQUIRE(mode != SSA_ROUTE_FLAT || top_c >= 0, SSA_ERR_INVALID, "route: flat mode needs top_c");
+  SSA_REQUIRE(top_c >= 0 || budget_frac >= 0.0f, SSA_ERR_INVALID, "route: budget_frac < 0");
+  SSA_REQUIRE(mode != SSA_ROUTE_QUERY || (query_pos >= 0 && block > 0), SSA_ERR_INVALID,
+              "route: query mode needs query_pos >= 0 and block > 0");
+  SSA_REQUIRE(var != nullptr || coef2 == 0.0f, SSA_ERR_INVALID, "route: var is NULL, coef2 != 0");
+  SSA_REQUIRE(nbk <= kMaxNbk, SSA_ERR_UNSUPPORTED, "route: %lld key blocks exceed %d",
+              (long long)nbk, kMaxNbk);
+  SSA_REQUIRE(W >= 1, SSA_ERR_INVALID, "route: W must be >= 1");
+  const int64_t needW = ssa_route_width(mode, nbq, nbk, top_c, budget_frac, local, query_pos, block);
+  SSA_REQUIRE(W >= needW, SSA_ERR_INVALID, "route: W=%lld below the required width %lld",
+              (long long)W, (long long)needW);
+  const size_t row_bytes = (size_t)nbk * 4;
+  const size_t rows_per_i = (size_t)(B * Hq);
+  SSA_REQUIRE(workspace != nullptr && workspace_bytes >= row_bytes * rows_per_i,
+              SSA_ERR_WORKSPACE, "route: workspace of %zu bytes below the minimum %zu",
+              workspace_bytes, row_bytes * rows_per_i);
+  int64_t chunk = (int64_t)(workspace_bytes / (row_bytes * rows_per_i));
+  if (chunk > nbq) chunk = nbq;
+
+  RouteGeom g;
+  g.mode = mode;
+  g.Hq = Hq;
+  g.Hkv = Hkv;
+  g.G = Hq / Hkv;
+  g.nbq = nbq;
+  g.nbk = nbk;
+  g.query_pos = query_pos;
+  g.block = block;
+  g.top_c = top_c;
+  g.budget_frac = budget_frac;
+  g.local = local;
+  unsigned int* keys = static_cast<unsigned int*>(workspace);
+  for (int64_t i0 = 0; i0 < nbq; i0 += chunk) {
+    g.i0 = i0;
+    g.ni = nbq - i0 < chunk ? nbq - i0 : chunk;
+    const int64_t R = g.G * g.ni;
+    const int64_t row_tiles = (R + kTile - 1) / kTile;
+    const int64_t imax = i0 + g.ni - 1;
+    int64_t cmax_all = row_cmax(g, imax);
+    const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
+    if (cand_tiles > 0) {
+      SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
+                  "route: score grid too large");
+      dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
+      if (m3 != nullptr)
+        route_score_kernel<true><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,
+                                                           coef3, keys, row_tiles, cand_tiles);
+      else
+        route_score_kernel<false><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,
+                                                            coef3, keys, row_tiles, cand_tiles);
+      SSA_TRY(launch_status("route_score_kernel"));
+    }
+    const int64_t nrows = B * Hq * g.ni;
+    SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
+    route_select_kernel<<<(unsigned)nrows, kSelThreads, 0, stream>>>(keys, g, kv_num, kv_idx, W);
+    SSA_TRY(launch_status("route_select_kernel"));
+  }
+  return SSA_OK;
+}
+
+}  // namespace ssa
+
+extern "C" int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c,
+                                   float budget_frac, int64_t local, int64_t query_pos,
+                                   int64_t block) {
+  ssa::RouteGeom g;
+  g.mode = mode;
+  g.nbq = nbq;
+  g.nbk = nbk;
+  g.top_c = top_c;
+  g.budget_frac = budget_frac;
+  g.local = local < 0 ? 0 : local;
+  g.query_pos = query_pos;
+  g.block = block > 0 ? block : 1;
+  int64_t w = 1;
+  // keep is monotone in cmax, and cmax is monotone in the row index: the last row is the widest
+  // unless clipping by nbk makes several rows equal (still bounded by the last row).
+  for (int64_t i = nbq - 1; i >= 0 && i >= nbq - 2; --i) {
+    const int64_t cmax = ssa::row_cmax(g, i);
+    const int64_t keep = ssa::row_keep(g, cmax);
+    int64_t k = keep < cmax ? keep : cmax;
+    int64_t cnt = k + g.local + 1;
+    if (cnt > w) w = cnt;
+  }
+  return w < nbk ? w : nbk;
+}
+
+extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk) {
+  return (size_t)B * (size_t)Hq * (size_t)nbq * (size_t)nbk * 4u;
+}
+
+extern "C" int ssa_route(const float* rows, const float* mu, const float* var, const float* m3,
+                         int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d,
+                         int mode, int64_t top_c, float budget_frac, int64_t local, float coef2,
+                         float coef3, int64_t query_pos, int64_t block, int32_t* kv_num,
+                         int32_t* kv_idx, int64_t W, void* workspace, size_t workspace_bytes,
+                         ssa_stream_t stream) {
+  return ssa::route_impl(rows, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c, budget_frac,
+                         local, coef2, coef3, query_pos, block, kv_num, kv_idx, W, workspace,
+                         workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t rows,
+                                    int64_t W, int64_t nbk, uint8_t* sel, int32_t* kv_full,
+                                    ssa_stream_t stream) {
+  SSA_REQUIRE(kv_num && kv_idx, SSA_ERR_INVALID, "expand_selection: NULL list argument");
+  SSA_REQUIRE(rows > 0 && W > 0 && nbk > 0, SSA_ERR_INVALID, "expand_selection: bad sizes");
+  SSA_REQUIRE(nbk <= ssa::kMaxNbk, SSA_ERR_UNSUPPORTED, "expand_selection: nbk too large");
+  SSA_REQUIRE(rows < (1ll << 31), SSA_ERR_UNSUPPORTED, "expand_selection: too many rows");
+  if (sel == nullptr && kv_full == nullptr) return SSA_OK;
+  ssa::expand_selection_kernel<<<(unsigned)rows, ssa::kSelThreads, 0,
+                                 static_cast<hipStream_t>(stream)>>>(kv_num, kv_idx, W, nbk, sel,
+                                                                     kv_full);
+  return ssa::launch_status("expand_selection_kernel");
+}

@@ -1,0 +1,184 @@
+"""Drop-in for the reference's transformers attention-interface boundary (ssa/gemma_ssa.py).
+
+    SSAConfig, CFG, install_ssa(model, **cfg)            ssa/gemma_ssa.py:31-55,244-279
+    ssa_attention_forward(module, query, key, value,
+                          attention_mask, scaling, dropout, **kw)   ssa/gemma_ssa.py:183-241
+    repeat_kv(x, n)                                      ssa/gemma_ssa.py:58-63
+
+Dispatch mirrors the reference:
+  * sliding layers (route_full_only) defer to the model's prior attention function;
+  * prefill-shaped calls (q_len == kv_len > block) with impl "flex" (or "hip") take the fused
+    path: query-block routing with block_route_budget semantics and n_real padding
+    (ssa/gemma_ssa.py:140-180), then the block-sparse kernel, with donor/consumer sharing of the
+    selection across layers (ssa/gemma_ssa.py:210-223);
+  * everything else (decode q_len = 1, chunked prefill, impl "analytic") takes the per-query
+    path of ssa/gemma_ssa.py:225-241: each query is routed over the key blocks complete at its
+    position and attends its selected blocks, causally.
+Both paths run on HIP kernels with GQA by index (no repeat_kv copies) and write the
+(b, n, hq, d) output directly. Routing statistics are computed in fp32 (the reference's analytic
+path computes them in the input dtype; parity is defined against its fp32 run).
+Unlike the reference there is no CPU path: CPU tensors raise.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, fields
+
+import torch
+
+from . import _lib
+from .ivf_decode import attend_rows
+from .ssa_kernel import block_summary, route, sparse_attention
+
+
+@dataclass
+class SSAConfig:
+    block: int = 256
+    budget_frac: float = 0.25
+    top_c: int | None = None
+    local_w: int = 1
+    beta: float = 2.0
+    route_full_only: bool = True
+    edgeworth: bool = False
+    dense_layers: tuple = ()
+    impl: str = "analytic"
+    share_route_from: int | None = None
+    share_below: str = "per_layer"
+    proj_path: str | None = None
+
+
+CFG = SSAConfig()
+_FALLBACK = None
+_PROJ = None
+_SHARE = {"sig": None, "bm": None}
+ROUTE_MS = 0.0
+# When True, route time is accumulated into ROUTE_MS (costs two device synchronisations per
+# routed call, like the reference's timing at ssa/gemma_ssa.py:151-165).
+TIME_ROUTE = False
+
+
+def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
+    """(b, h, s, d) -> (b, h*n, s, d), each head repeated n times (ssa/gemma_ssa.py:58-63)."""
+    if n == 1:
+        return x
+    b, h, s, d = x.shape
+    return x[:, :, None, :, :].expand(b, h, n, s, d).reshape(b, h * n, s, d)
+
+
+def _block_lists(query, key, cfg, dense, n):
+    """Query-block routing of a prefill (block_route_budget semantics with n_real = n)."""
+    global ROUTE_MS
+    blk = cfg.block
+    if TIME_ROUTE:
+        torch.cuda.synchronize()
+        t0 = time.time()
+    qbar = block_summary(query, blk, "qmean")
+    mu, var, m3 = block_summary(key, blk, "pop", n_real=n, with_m3=cfg.edgeworth and not dense)
+    if dense:
+        kv = route(qbar, mu, var, None, "budget", None, 1.0, cfg.local_w, 0.5 * cfg.beta)
+    else:
+        kv = route(qbar, mu, var, m3, "budget", cfg.top_c, cfg.budget_frac, cfg.local_w,
+                   0.5 * cfg.beta, cfg.beta ** 2 / 6.0)
+    if TIME_ROUTE:
+        torch.cuda.synchronize()
+        ROUTE_MS += (time.time() - t0) * 1000
+    return kv
+
+
+def ssa_attention_forward(module, query, key, value, attention_mask=None, scaling=None,
+                          dropout=0.0, **kwargs):
+    """transformers attention-interface function. query (b, hq, n, d); key/value (b, hkv, n, d).
+    Returns (attn_output (b, n, hq, d), None). `attention_mask` is ignored (causality comes from
+    positions), as in the reference."""
+    cfg = CFG
+    is_sliding = bool(getattr(module, "is_sliding", False))
+    if (cfg.route_full_only and is_sliding) and _FALLBACK is not None:
+        return _FALLBACK(module, query, key, value, attention_mask,
+                         scaling=scaling, dropout=dropout, **kwargs)
+    _lib.require_device(query, key, value)
+    if scaling is None:
+        scaling = getattr(module, "scaling", 1.0)
+    b, hq, q_len, d = query.shape
+    kv_len = key.shape[2]
+    nb_layer = (kv_len + cfg.block - 1) // cfg.block
+    force_dense = getattr(module, "layer_idx", None) in cfg.dense_layers
+    is_dense = force_dense or (cfg.top_c is not None and cfg.top_c >= nb_layer) \
+        or (cfg.top_c is None and cfg.budget_frac >= 1.0)
+    out = torch.empty(b, q_len, hq, d, device=query.device, dtype=query.dtype)
+
+    if cfg.impl in ("flex", "hip") and q_len == kv_len and q_len > cfg.block:
+        li = getattr(module, "layer_idx", None)
+        donor = cfg.share_route_from
+        lists = None
+        if donor is not None and li is not None:
+            if li < donor:
+                is_dense = is_dense or cfg.share_below == "dense"
+            elif li > donor:
+                sig = (tuple(query.shape), kv_len, str(query.device))
+                if _SHARE["sig"] == sig:
+                    lists = _SHARE["bm"]
+        if lists is None:
+            lists = _block_lists(query, key, cfg, is_dense, q_len)
+        if donor is not None and li == donor:
+            _SHARE["sig"] = (tuple(query.shape), kv_len, str(query.device))
+            _SHARE["bm"] = lists
+        sparse_attention(query, key, value, lists[0], lists[1], cfg.block, scale=scaling,
+                         out=out.transpose(1, 2))
+        return out, None
+
+    # per-query (analytic) path: query row r sits at absolute position pos0 + r
+    cpos = kwargs.get("cache_position")
+    if cpos is not None:
+        cp = cpos.detach().to("cpu", torch.int64).view(-1)
+        pos0 = int(cp[0])
+        if cp.numel() != q_len or not torch.equal(cp, torch.arange(pos0, pos0 + q_len)):
+            raise NotImplementedError("ssa_amd needs contiguous cache_position values")
+    else:
+        pos0 = kv_len - q_len
+    if pos0 + q_len > kv_len or pos0 < 0:
+        raise ValueError("query positions exceed the key length")
+    mu, var, _ = block_summary(key, cfg.block, "pop", n_real=kv_len)
+    rows = query.float()
+    if is_dense:
+        top_c, frac = nb_layer, 0.0
+    else:
+        top_c, frac = cfg.top_c, cfg.budget_frac
+    kv_num, kv_idx = route(rows, mu, var, None, "query", top_c, frac, cfg.local_w,
+                           0.5 * cfg.beta, 0.0, query_pos=pos0, block=cfg.block)
+    attend_rows(query, key, value, kv_num, kv_idx, pos0, cfg.block, scale=scaling,
+                out=out.transpose(1, 2))
+    return out, None
+
+
+def install_ssa(model, **cfg_kwargs):
+    """Registers ssa_attention_forward as the model's attention implementation, resetting every
+    SSAConfig field not passed here to its default (ssa/gemma_ssa.py:244-279)."""
+    global _FALLBACK, _PROJ
+    defaults = SSAConfig()
+    for f in fields(SSAConfig):
+        setattr(CFG, f.name, getattr(defaults, f.name))
+    for k, val in cfg_kwargs.items():
+        setattr(CFG, k, val)
+    _SHARE["sig"] = None
+    _SHARE["bm"] = None
+    _PROJ = None
+    if CFG.proj_path:
+        raise NotImplementedError("trained routing projections (proj_path) are not implemented "
+                                  "by ssa_amd")
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    prior = getattr(model.config, "_attn_implementation", None) or "sdpa"
+    if prior == "ssa":
+        prior = None if _FALLBACK is not None else "sdpa"
+    if prior is not None:
+        try:
+            _FALLBACK = ALL_ATTENTION_FUNCTIONS.get_interface(prior)
+        except Exception:
+            _FALLBACK = ALL_ATTENTION_FUNCTIONS.get("sdpa")
+    ALL_ATTENTION_FUNCTIONS["ssa"] = ssa_attention_forward
+    model.config._attn_implementation = "ssa"
+    if hasattr(model.config, "get_text_config"):
+        try:
+            model.config.get_text_config()._attn_implementation = "ssa"
+        except Exception:
+            pass
+    return model

@@ -1,0 +1,257 @@
+"""Drop-in for the reference's routed block-sparse prefill (ssa/ssa_kernel.py), on gfx950 HIP kernels.
+
+Same names, arguments and return values as the reference:
+
+    block_route(q, k, block, top_c, local, routing)              ssa/ssa_kernel.py:37-58
+    block_route_budget(q, k, block, budget_frac, top_c, local,
+                       beta, edgeworth, n_real, sub, proj)       ssa/ssa_kernel.py:61-119
+    ssa_flex(q, k, v, block, top_c, local, routing)              ssa/ssa_kernel.py:122-126
+    dense(q, k, v)                                               ssa/ssa_kernel.py:129-130
+
+plus the primitives they are built from (block_summary, route, sparse_attention). Every call is
+asynchronous on the current stream (no host synchronisation, unlike the reference's `.item()` at
+ssa/ssa_kernel.py:107). Differences by design:
+  * K/V may have fewer heads than Q (GQA: query head h reads key head h // (Hq/Hkv)); the
+    reference needs repeat_kv copies (ssa/gemma_ssa.py:58-63).
+  * Routers return the dense `sel` and argsort-order `kv_idx` of the reference by default;
+    `compact=True` returns (kv_num, kv_idx[..., :W], None), the form the attention consumes.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+BLOCK = 128
+
+
+# ---------------------------------------------------------------------------------------------
+# primitives
+# ---------------------------------------------------------------------------------------------
+
+def _bhn_strides(t: torch.Tensor) -> tuple[int, int, int]:
+    if t.dim() != 4:
+        raise ValueError(f"expected a (B, H, n, d) tensor, got shape {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError("the head dimension must be contiguous")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Returns t, or a contiguous copy when its layout violates the kernels' 16-byte rules."""
+    vec = 4 if t.dtype == torch.float32 else 8
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % vec == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def block_summary(x: torch.Tensor, block: int, mode: str = "pop", n_real: int | None = None,
+                  with_m3: bool = False):
+    """Per-block summaries of x (B, H, n, d) -> fp32 (B, H, ceil(n/block), d) tensors.
+
+    mode "pop": (mu, var, m3|None) over rows < n_real (ssa/ssa_kernel.py:80-91,
+    ssa/gemma_ssa.py:65-82); "unbiased": (mu, var) with var/(cnt-1) (ssa/ssa_kernel.py:43,47);
+    "qmean": the query-block mean sum(rows)/block (ssa/ssa_kernel.py:44,79).
+    """
+    _lib.require_device(x)
+    x = _aligned(x)
+    B, H, n, d = x.shape
+    nb = -(-n // block)
+    code = {"pop": _lib.STATS_POP, "unbiased": _lib.STATS_UNBIASED, "qmean": _lib.STATS_QMEAN}[mode]
+    mu = torch.empty(B, H, nb, d, device=x.device, dtype=torch.float32)
+    var = None if mode == "qmean" else torch.empty_like(mu)
+    m3 = torch.empty_like(mu) if (with_m3 and mode != "qmean") else None
+    sb, sh, sn = _bhn_strides(x)
+    _lib.call("ssa_block_summary", x.data_ptr(), _lib.dtype_code(x.dtype), B, H, n, d, sb, sh, sn,
+              block, n if n_real is None else int(n_real), code, _lib.ptr(mu), _lib.ptr(var),
+              _lib.ptr(m3), _lib.stream_of(x))
+    if mode == "qmean":
+        return mu
+    return mu, var, m3
+
+
+_ROUTE_MODES = {"budget": _lib.ROUTE_BUDGET, "flat": _lib.ROUTE_FLAT, "query": _lib.ROUTE_QUERY}
+
+
+def route_width(mode: str, nbq: int, nbk: int, top_c: int | None, budget_frac: float,
+                local: int, query_pos: int = 0, block: int = 1) -> int:
+    return int(_lib.query("ssa_route_width", _ROUTE_MODES[mode], nbq, nbk,
+                          -1 if top_c is None else int(top_c), float(budget_frac), int(local),
+                          int(query_pos), int(block)))
+
+
+def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: torch.Tensor | None,
+          mode: str, top_c: int | None, budget_frac: float, local: int, coef2: float,
+          coef3: float = 0.0, query_pos: int = 0, block: int = 1,
+          workspace_limit: int = 1 << 30):
+    """Cumulant router over precomputed summaries -> compact (kv_num, kv_idx).
+
+    rows (B, Hq, nbq, d) fp32: query-block means (mode "budget"/"flat") or query vectors
+    ("query", row r at absolute position query_pos + r). mu/var/m3 (B, Hkv, nbk, d) fp32.
+    Returns kv_num (B, Hq, nbq) int32 and kv_idx (B, Hq, nbq, W) int32 (ascending, padded 0).
+    """
+    _lib.require_device(rows, mu, var, m3)
+    B, Hq, nbq, d = rows.shape
+    Hkv, nbk = mu.shape[1], mu.shape[2]
+    rows, mu = rows.contiguous(), mu.contiguous()
+    var = None if var is None else var.contiguous()
+    m3 = None if m3 is None else m3.contiguous()
+    W = route_width(mode, nbq, nbk, top_c, budget_frac, local, query_pos, block)
+    dev = rows.device
+    kv_num = torch.empty(B, Hq, nbq, device=dev, dtype=torch.int32)
+    kv_idx = torch.empty(B, Hq, nbq, W, device=dev, dtype=torch.int32)
+    full = int(_lib.query("ssa_route_workspace_size", B, Hq, nbq, nbk))
+    per_i = int(_lib.query("ssa_route_workspace_size", B, Hq, 1, nbk))
+    ws_bytes = max(per_i, min(full, workspace_limit // per_i * per_i))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    _lib.call("ssa_route", rows.data_ptr(), mu.data_ptr(), _lib.ptr(var), _lib.ptr(m3), B, Hq, Hkv,
+              nbq, nbk, d, _ROUTE_MODES[mode], -1 if top_c is None else int(top_c),
+              float(budget_frac), int(local), float(coef2), float(coef3), int(query_pos),
+              int(block), kv_num.data_ptr(), kv_idx.data_ptr(), W, ws.data_ptr(), ws_bytes,
+              _lib.stream_of(rows))
+    return kv_num, kv_idx
+
+
+def expand_selection(kv_num: torch.Tensor, kv_idx: torch.Tensor, nbk: int):
+    """Compact lists -> the reference's dense (kv_idx (…, nbk) in argsort order, sel bool)."""
+    _lib.require_device(kv_num, kv_idx)
+    lead = kv_num.shape
+    W = kv_idx.shape[-1]
+    rows = kv_num.numel()
+    sel = torch.empty(*lead, nbk, device=kv_num.device, dtype=torch.uint8)
+    full = torch.empty(*lead, nbk, device=kv_num.device, dtype=torch.int32)
+    _lib.call("ssa_expand_selection", kv_num.contiguous().data_ptr(),
+              kv_idx.contiguous().data_ptr(), rows, W, nbk, sel.data_ptr(), full.data_ptr(),
+              _lib.stream_of(kv_num))
+    return full, sel.view(torch.bool)
+
+
+def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
+    """V (B, Hkv, n, 64) 16-bit -> the V^T workspace (B, Hkv, 64, ceil(n/block)*block) that the
+    16-bit attention kernels read (keys >= n zero-filled). Pass it to sparse_attention(vt=...)
+    to skip the per-call transpose."""
+    _lib.require_device(v)
+    v = _aligned(v)
+    B, Hkv, n, d = v.shape
+    dt = _lib.dtype_code(v.dtype)
+    nbytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
+    n_pad = -(-n // block) * block
+    vt = torch.empty(B, Hkv, d, n_pad, device=v.device, dtype=v.dtype)
+    _lib.call("ssa_transpose_v", v.data_ptr(), dt, B, Hkv, n, d, block, *_bhn_strides(v),
+              vt.data_ptr(), nbytes, _lib.stream_of(v))
+    return vt
+
+
+def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: torch.Tensor,
+                     kv_idx: torch.Tensor, block: int, scale: float | None = None,
+                     out: torch.Tensor | None = None, return_lse: bool = False,
+                     vt: torch.Tensor | None = None):
+    """Block-sparse causal attention on the compact contract (replaces FlexAttention with
+    BlockMask.from_kv_blocks + mask_mod kv<=q & kv<n; ssa/ssa_kernel.py:125-126,
+    ssa/gemma_ssa.py:159-162,179).
+
+    q (B, Hq, n, d); k, v (B, Hkv, n, d); kv_num (B, Hq, nb); kv_idx (B, Hq, nb, W).
+    `out` may be any (B, Hq, n, d) view with a contiguous last dim (e.g. a transpose of a
+    (B, n, Hq, d) buffer). `vt` is an optional V^T from transpose_v(v, block).
+    Returns out (and lse (B, Hq, n) fp32 if requested).
+    """
+    _lib.require_device(q, k, v, kv_num, kv_idx)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    B, Hq, n, d = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, n, d) or v.shape != k.shape:
+        raise ValueError(f"k/v shape {tuple(k.shape)} incompatible with q {tuple(q.shape)}")
+    nb = -(-n // block)
+    if kv_num.shape != (B, Hq, nb) or kv_idx.dim() != 4 or kv_idx.shape[:3] != (B, Hq, nb):
+        raise ValueError("kv_num/kv_idx shapes do not match (B, Hq, ceil(n/block)[, W])")
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    kv_num = kv_num.to(torch.int32).contiguous()
+    kv_idx = kv_idx.to(torch.int32).contiguous()
+    lse = torch.empty(B, Hq, n, device=q.device, dtype=torch.float32) if return_lse else None
+    dt = _lib.dtype_code(q.dtype)
+    ws_bytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
+    flags = 0
+    if vt is not None and dt != _lib.F32:
+        if vt.numel() * vt.element_size() < ws_bytes or not vt.is_contiguous():
+            raise ValueError("vt is not a V^T workspace for this v (use transpose_v(v, block))")
+        ws, flags = vt, _lib.ATTN_VT_READY
+    else:
+        ws = torch.empty(max(ws_bytes, 16), device=q.device, dtype=torch.uint8)
+    strides = _lib.i64_array([*_bhn_strides(q), *_bhn_strides(k), *_bhn_strides(v),
+                              *_bhn_strides(out)])
+    _lib.call("ssa_sparse_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt,
+              B, Hq, Hkv, n, d, block, strides, kv_num.data_ptr(), kv_idx.data_ptr(),
+              kv_idx.shape[-1], float(scale), _lib.ptr(lse), flags, ws.data_ptr(), ws_bytes,
+              _lib.stream_of(q))
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------------------------
+# the reference's operator API
+# ---------------------------------------------------------------------------------------------
+
+def _finish(kv_num, kv_idx, nb, compact):
+    if compact:
+        return kv_num, kv_idx, None
+    full, sel = expand_selection(kv_num, kv_idx, nb)
+    return kv_num, full, sel
+
+
+def block_route(q, k, block=BLOCK, top_c=8, local=1, routing="cumulant", compact=False):
+    """Per query-block, the top-`top_c` causal key blocks (own block included in the competition)
+    by <q̄,μ> + ½<q̄²,σ²_unbiased> (or <q̄,μ> unless routing == "cumulant"), OR the own block and
+    `local` predecessors. Returns (kv_num (B,H,nb) int32, kv_idx (B,H,nb,nb) int32, sel bool).
+    Reference: ssa/ssa_kernel.py:37-58."""
+    B, H, n, d = q.shape
+    if n % block:
+        raise RuntimeError(f"block_route: n={n} is not a multiple of block={block}")
+    nb = n // block
+    qbar = block_summary(q, block, "qmean")
+    cumulant = routing == "cumulant"
+    mu, var, _ = block_summary(k, block, "unbiased" if cumulant else "pop")
+    kv_num, kv_idx = route(qbar, mu, var if cumulant else None, None, "flat", int(top_c), 0.0,
+                           int(local), 0.5 if cumulant else 0.0)
+    return _finish(kv_num, kv_idx, nb, compact)
+
+
+def block_route_budget(q, k, block=BLOCK, budget_frac=0.25, top_c=None, local=1, beta=2.0,
+                       edgeworth=False, n_real=None, sub=None, proj=None, compact=False):
+    """Budget router with gemma_ssa's semantics: per query block i keep the top
+    ceil(budget_frac·i) (or `top_c`) strictly-past key blocks by <q̄,μ> + ½β<q̄²,σ²>
+    (+ β²/6<q̄³,m3> if edgeworth), always OR the own block + `local` predecessors.
+    `n_real` excludes pad keys from the block statistics. Returns (kv_num, kv_idx, sel).
+    Reference: ssa/ssa_kernel.py:61-119."""
+    if proj is not None:
+        raise NotImplementedError("block_route_budget(proj=...) low-dimensional routing is not "
+                                  "implemented by ssa_amd")
+    if sub is not None and sub != block:
+        raise NotImplementedError("block_route_budget(sub=...) sub-block max-pooling is not "
+                                  "implemented by ssa_amd")
+    B, H, n, d = q.shape
+    if n % block:
+        raise RuntimeError(f"block_route_budget: n={n} is not a multiple of block={block}")
+    nb = n // block
+    qbar = block_summary(q, block, "qmean")
+    mu, var, m3 = block_summary(k, block, "pop", n_real=n_real, with_m3=edgeworth)
+    kv_num, kv_idx = route(qbar, mu, var, m3, "budget", top_c, float(budget_frac), int(local),
+                           0.5 * beta, beta ** 2 / 6.0)
+    return _finish(kv_num, kv_idx, nb, compact)
+
+
+def ssa_flex(q, k, v, block=BLOCK, top_c=8, local=1, routing="cumulant"):
+    """Full SSA prefill: route (block_route) -> block-sparse causal attention, scale 1/√d.
+    Reference: ssa/ssa_kernel.py:122-126."""
+    kv_num, kv_idx, _ = block_route(q, k, block, top_c, local, routing, compact=True)
+    return sparse_attention(q, k, v, kv_num, kv_idx, block)
+
+
+def dense(q, k, v):
+    """Dense causal attention baseline (torch SDPA), as ssa/ssa_kernel.py:129-130."""
+    return F.scaled_dot_product_attention(q, k, v, is_causal=True)

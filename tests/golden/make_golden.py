@@ -1,0 +1,182 @@
+"""Writes the golden fixtures under tests/golden/ by running the REFERENCE implementation
+(jonsmirl/ssa, read-only at /root/reference) on CPU in float32/float64.
+
+Run once in the build container (the reference is not present on GPU boxes):
+
+    python tests/golden/make_golden.py            # all cases
+    python tests/golden/make_golden.py c1_budget  # selected cases
+
+Each fixture is a small .npz of outputs only (selections as int16 compact lists, attention rows
+as float32/float64) plus the sha256 of the inputs, which the tests regenerate from the same
+seeded generators (ssa_amd.workloads / the seeds recorded here) and check against the hash.
+Reference functions used (ssa/ssa_kernel.py, ssa/gemma_ssa.py):
+  block_route_budget :61-119, block_route :37-58, ssa_flex :122-126,
+  _selection_mask :85-137, ssa_attention_forward :183-241 (impl="analytic").
+"""
+from __future__ import annotations
+
+import hashlib
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path.insert(0, str(ROOT))
+REFERENCE = Path("/root/reference")
+
+from ssa_amd import workloads as WL  # noqa: E402
+
+
+def sha(*arrays) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def reference():
+    sys.path.insert(0, str(REFERENCE))
+    from ssa import gemma_ssa, ssa_kernel  # noqa: E402
+    return ssa_kernel, gemma_ssa
+
+
+def compact_from_full(kv_num, kv_idx_full):
+    """Reference (kv_num, argsort-order kv_idx) -> compact int16 (kv_num, kv_idx[..., :W])."""
+    kv_num = kv_num.numpy().astype(np.int16)
+    W = int(kv_num.max())
+    ki = kv_idx_full[..., :W].numpy().astype(np.int16)
+    # the compact contract pads with 0 beyond kv_num
+    mask = np.arange(W)[None, None, None, :] < kv_num[..., None]
+    return kv_num, np.where(mask, ki, 0).astype(np.int16)
+
+
+def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
+    b, h, s, d = x.shape
+    return x[:, :, None].expand(b, h, n, s, d).reshape(b, h * n, s, d)
+
+
+def route_case(name, cfg_name, variant="segmented", **kw):
+    RK, _ = reference()
+    p = WL.make(cfg_name, variant)
+    cfg = p["cfg"]
+    q = torch.from_numpy(p["q"])
+    k = torch.from_numpy(p["k"])
+    G = cfg.Hq // cfg.Hkv
+    kk = repeat_kv(k, G) if G > 1 else k
+    fn = kw.pop("fn", "budget")
+    t0 = time.time()
+    with torch.no_grad():
+        if fn == "budget":
+            kv_num, kv_idx, _ = RK.block_route_budget(q, kk, cfg.block, **kw)
+        else:
+            kv_num, kv_idx, _ = RK.block_route(q, kk, cfg.block, **kw)
+    kn, ki = compact_from_full(kv_num, kv_idx)
+    np.savez_compressed(HERE / f"{name}.npz", kv_num=kn, kv_idx=ki,
+                        inputs_sha256=np.array(sha(p["q"], p["k"])),
+                        meta=np.array(repr({"cfg": cfg_name, "variant": variant, "fn": fn, **kw})))
+    print(f"{name}: rows={kn.size} W={ki.shape[-1]} ({time.time() - t0:.1f}s)")
+
+
+def flex_case(name):
+    """ssa_flex on C1 (fp32, CPU FlexAttention) -- the reference's own block-sparse output."""
+    RK, _ = reference()
+    p = WL.make("C1")
+    q, k, v = (torch.from_numpy(p[x]) for x in ("q", "k", "v"))
+    t0 = time.time()
+    with torch.no_grad():
+        out = RK.ssa_flex(q, k, v, block=64, top_c=8, local=1)
+    np.savez_compressed(HERE / f"{name}.npz", out=out.numpy().astype(np.float32),
+                        inputs_sha256=np.array(sha(p["q"], p["k"], p["v"])),
+                        meta=np.array(repr({"cfg": "C1", "fn": "ssa_flex", "block": 64,
+                                            "top_c": 8, "local": 1})))
+    print(f"{name}: out {tuple(out.shape)} ({time.time() - t0:.1f}s)")
+
+
+def query_case(name, n_cache=65536, positions=(65535, 65600, 65663)):
+    """_selection_mask at q_len=1 (the exact per-query decode router) in float32 on a C4-shaped
+    prefix: block set of each q-head for several decode positions."""
+    _, RG = reference()
+    p = WL.make("C4", n=n_cache + 128)
+    cfg = p["cfg"]
+    G = cfg.Hq // cfg.Hkv
+    q = torch.from_numpy(p["q"])
+    k = repeat_kv(torch.from_numpy(p["k"]), G)
+    scfg = RG.SSAConfig(block=cfg.block, top_c=cfg.top_c, local_w=cfg.local, beta=cfg.beta)
+    lists = []
+    t0 = time.time()
+    with torch.no_grad():
+        for pos in positions:
+            m = RG._selection_mask(q[:, :, pos:pos + 1], k[:, :, :pos + 1], scfg)  # (1,hq,1,pos+1)
+            nb = -(-(pos + 1) // cfg.block)
+            first = m[0, :, 0, ::cfg.block][:, :nb]                 # first key of each block
+            lists.append([np.flatnonzero((first[h] == 0).numpy()).astype(np.int16)
+                          for h in range(cfg.Hq)])
+    W = max(len(x) for row in lists for x in row)
+    kv_num = np.array([[len(x) for x in row] for row in lists], dtype=np.int16)
+    kv_idx = np.zeros((len(positions), cfg.Hq, W), dtype=np.int16)
+    for a, row in enumerate(lists):
+        for h, x in enumerate(row):
+            kv_idx[a, h, :len(x)] = x
+    np.savez_compressed(HERE / f"{name}.npz", kv_num=kv_num, kv_idx=kv_idx,
+                        positions=np.array(positions, dtype=np.int64),
+                        inputs_sha256=np.array(sha(p["q"], p["k"])),
+                        meta=np.array(repr({"cfg": "C4", "n_cache": n_cache,
+                                            "fn": "_selection_mask", "top_c": cfg.top_c,
+                                            "local_w": cfg.local})))
+    print(f"{name}: positions={positions} W={W} ({time.time() - t0:.1f}s)")
+
+
+def analytic_inputs(seed=11, b=1, hq=4, hkv=2, n=300, d=64):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((b, hq, n, d))
+    k = rng.standard_normal((b, hkv, n, d))
+    v = rng.standard_normal((b, hkv, n, d))
+    return q, k, v
+
+
+def analytic_case(name, budget_frac=0.5, block=64):
+    """ssa_attention_forward(impl='analytic') in float64: per-query routing + masked softmax,
+    GQA 2:1, n not a multiple of the block; prefill and a q_len=1 decode row."""
+    _, RG = reference()
+    from types import SimpleNamespace
+    q, k, v = analytic_inputs()
+    mod = SimpleNamespace(num_key_value_groups=q.shape[1] // k.shape[1], is_sliding=False,
+                          scaling=0.125, layer_idx=0)
+    RG.CFG = RG.SSAConfig(block=block, budget_frac=budget_frac, local_w=1, beta=2.0,
+                          impl="analytic")
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    with torch.no_grad():
+        full, _ = RG.ssa_attention_forward(mod, tq, tk, tv, scaling=0.125)
+        inc, _ = RG.ssa_attention_forward(mod, tq[:, :, -1:], tk, tv, scaling=0.125)
+    np.savez_compressed(HERE / f"{name}.npz", out=full.numpy(), out_last=inc.numpy(),
+                        inputs_sha256=np.array(sha(q, k, v)),
+                        meta=np.array(repr({"seed": 11, "block": block, "budget_frac": budget_frac,
+                                            "local_w": 1, "beta": 2.0, "scaling": 0.125})))
+    print(f"{name}: out {tuple(full.shape)}")
+
+
+CASES = {
+    "c1_budget": lambda: route_case("c1_budget", "C1", top_c=8, local=1, beta=2.0),
+    "c1_frac": lambda: route_case("c1_frac", "C1", budget_frac=0.25, local=1, beta=2.0),
+    "c1_flat": lambda: route_case("c1_flat", "C1", fn="flat", top_c=8, local=1),
+    "c2_budget": lambda: route_case("c2_budget", "C2", top_c=32, local=2, beta=2.0),
+    "c2_edgeworth": lambda: route_case("c2_edgeworth", "C2", top_c=32, local=2, beta=2.0,
+                                       edgeworth=True),
+    "c3_budget_seg": lambda: route_case("c3_budget_seg", "C3", "segmented", top_c=64, local=2,
+                                        beta=2.0),
+    "c3_budget_lit": lambda: route_case("c3_budget_lit", "C3", "literal", top_c=64, local=2,
+                                        beta=2.0),
+    "c4_query": lambda: query_case("c4_query"),
+    "c1_flex_out": lambda: flex_case("c1_flex_out"),
+    "analytic_gqa": lambda: analytic_case("analytic_gqa"),
+}
+
+if __name__ == "__main__":
+    torch.set_num_threads(8)
+    names = sys.argv[1:] or list(CASES)
+    for nm in names:
+        CASES[nm]()

@@ -1,0 +1,103 @@
+"""CPU tests of the C-ABI boundary: the library loads, exports every entry point the header
+declares, and rejects invalid arguments with a status and a message (no GPU work is issued on
+these paths)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ssa_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ssa_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ssa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_are_exported_and_bound():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 14, names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in ssa_hip.h but not exported"
+    assert sorted(_lib.exported_symbols()) == names
+
+
+def test_abi_version_and_error_text():
+    assert _lib.lib().ssa_abi_version() == _lib.ABI_VERSION
+    with pytest.raises(_lib.SSAError, match="NULL"):
+        _lib.call("ssa_sparse_attn_fwd", None, None, None, None, _lib.BF16, 1, 1, 1, 128, 64, 128,
+                  _lib.i64_array([0] * 12), None, None, 1, 1.0, None, 0, None, 0, None)
+
+
+def _status(name, *args):
+    return getattr(_lib.lib(), name)(*args)
+
+
+def test_invalid_arguments_are_rejected():
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    st12 = _lib.i64_array([128 * 64, 128 * 64, 64] * 4)
+    # head_dim 96 is not supported by the attention kernel
+    rc = _status("ssa_sparse_attn_fwd", fake, fake, fake, fake, _lib.BF16, 1, 1, 1, 128, 96, 128,
+                 st12, fake, fake, 1, 1.0, None, 0, None, 0, None)
+    assert rc == _lib.SSA_ERR_UNSUPPORTED
+    # block 96 is neither 64 nor a multiple of 128
+    rc = _status("ssa_sparse_attn_fwd", fake, fake, fake, fake, _lib.BF16, 1, 1, 1, 128, 64, 96,
+                 st12, fake, fake, 1, 1.0, None, 0, None, 0, None)
+    assert rc == _lib.SSA_ERR_UNSUPPORTED
+    # Hq not a multiple of Hkv
+    rc = _status("ssa_sparse_attn_fwd", fake, fake, fake, fake, _lib.BF16, 1, 3, 2, 128, 64, 128,
+                 st12, fake, fake, 1, 1.0, None, 0, None, 0, None)
+    assert rc == _lib.SSA_ERR_INVALID
+    # unknown dtype
+    rc = _status("ssa_block_summary", fake, 7, 1, 1, 64, 64, 4096, 4096, 64, 64, 64, 0, fake, fake,
+                 None, None)
+    assert rc == _lib.SSA_ERR_UNSUPPORTED
+    # QMEAN with a var output
+    rc = _status("ssa_block_summary", fake, _lib.F32, 1, 1, 64, 64, 4096, 4096, 64, 64, 64,
+                 _lib.STATS_QMEAN, fake, fake, None, None)
+    assert rc == _lib.SSA_ERR_INVALID
+    # route: W below the required width, then a too-small workspace
+    rc = _status("ssa_route", fake, fake, fake, None, 1, 1, 1, 16, 16, 64, _lib.ROUTE_BUDGET, 4,
+                 0.0, 1, 1.0, 0.0, 0, 1, fake, fake, 2, fake, 1 << 20, None)
+    assert rc == _lib.SSA_ERR_INVALID
+    rc = _status("ssa_route", fake, fake, fake, None, 1, 1, 1, 16, 16, 64, _lib.ROUTE_BUDGET, 4,
+                 0.0, 1, 1.0, 0.0, 0, 1, fake, fake, 6, fake, 8, None)
+    assert rc == _lib.SSA_ERR_WORKSPACE
+    # decode: position outside the cache
+    st12d = _lib.i64_array([64] * 12)
+    rc = _status("ssa_decode_attend", fake, fake, fake, fake, _lib.BF16, 1, 1, 1, 1, 256, 64, 128,
+                 256, st12d, fake, fake, 4, 1.0, fake, 1 << 20, None)
+    assert rc == _lib.SSA_ERR_INVALID
+    assert b"outside the cache" in _lib.lib().ssa_last_error()
+
+
+def test_route_width():
+    w = lambda *a: _lib.query("ssa_route_width", *a)  # noqa: E731
+    # budget, top_c=64, local=2, 1024 blocks -> 64 + 3
+    assert w(_lib.ROUTE_BUDGET, 1024, 1024, 64, 0.0, 2, 0, 1) == 67
+    # budget_frac=1.0 over 16 blocks: last row keeps 15 + own
+    assert w(_lib.ROUTE_BUDGET, 16, 16, -1, 1.0, 1, 0, 1) == 16
+    # flat, tiny problem: capped at the block count
+    assert w(_lib.ROUTE_FLAT, 4, 4, 8, 0.0, 1, 0, 1) == 4
+    # query mode at position 1M-1, block 128: 64 routed + 2 local
+    assert w(_lib.ROUTE_QUERY, 1, 8192, 64, 0.0, 1, 1048575, 128) == 66
+
+
+def test_workspace_queries():
+    assert _lib.query("ssa_sparse_attn_workspace_size", _lib.BF16, 1, 2, 300, 64, 128) == 2 * 64 * 384 * 2
+    assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F32, 1, 2, 300, 64, 128) == 0
+    assert _lib.query("ssa_route_workspace_size", 1, 14, 1024, 1024) == 14 * 1024 * 1024 * 4
+    assert _lib.query("ssa_decode_attend_workspace_size", 1, 14, 1, 66, 64) == 14 * 66 * 66 * 4
+
+
+def test_cpu_tensors_raise():
+    import torch
+    from ssa_amd import ssa_kernel as K
+    q = torch.randn(1, 1, 256, 64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        K.ssa_flex(q, q, q)

@@ -1,0 +1,369 @@
+"""GPU parity tests: the HIP kernels (through the C ABI, via the ssa_amd drop-in API) against the
+CPU oracle and the reference's golden outputs, on the seeded configurations and edge cases.
+
+Bars: selections bit-exact against the oracle and equal to the reference's float32 selections
+except on certified float32 near-ties; summaries within 1 ulp of the oracle; attention outputs
+within 2e-2 (bf16/fp16) or 1e-5 (fp32) max-abs of the oracle's float64 masked softmax."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import ssa_oracle as O
+from ssa_amd import gemma_ssa as G
+from ssa_amd import ivf_decode as D
+from ssa_amd import ssa_kernel as K
+from ssa_amd import workloads as WL
+from tests import golden_util as GU
+from tests.test_oracle import ROUTE_CASES, certificate_inputs, oracle_route
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def dev(x, dtype, cuda):
+    return WL.to_device(x, dtype, cuda)
+
+
+def np_of(t):
+    return t.detach().float().cpu().numpy()
+
+
+def ulp_diff(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, dtype=np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+# ---- a1 / a2 summaries -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_block_summary_matches_oracle(cuda, dtype):
+    rng = np.random.default_rng(7)
+    x = WL.round_to(rng.standard_normal((2, 3, 1000, 64)).astype(np.float32) * 3 + 1, dtype)
+    xt = dev(x, dtype, cuda)
+    mu, var, m3 = K.block_summary(xt, 128, "pop", n_real=990, with_m3=True)
+    omu, ovar, om3 = O.block_stats(x, 128, "pop", n_real=990)
+    assert ulp_diff(np_of(mu), omu).max() <= 1
+    assert ulp_diff(np_of(var), ovar).max() <= 1
+    assert np.abs(np_of(m3) - om3).max() <= 1e-6 * np.abs(om3).max()
+    mu_u, var_u, _ = K.block_summary(xt[:, :, :896], 128, "unbiased")
+    _, ovar_u, _ = O.block_stats(x[:, :, :896], 128, "unbiased")
+    assert ulp_diff(np_of(var_u), ovar_u).max() <= 1
+    qb = K.block_summary(xt, 128, "qmean")
+    assert ulp_diff(np_of(qb), O.qmean(x, 128)).max() <= 1
+
+
+def test_block_summary_strided_input(cuda):
+    """A (b, n, h, d) buffer viewed as (b, h, n, d) needs no copy and gives the same stats."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((1, 512, 4, 64)).astype(np.float32)
+    xt = dev(x, torch.float32, cuda).transpose(1, 2)
+    mu, var, _ = K.block_summary(xt, 64, "pop")
+    omu, ovar, _ = O.block_stats(x.transpose(0, 2, 1, 3), 64, "pop")
+    assert ulp_diff(np_of(mu), omu).max() <= 1 and ulp_diff(np_of(var), ovar).max() <= 1
+
+
+# ---- a3-a5 router ------------------------------------------------------------------------------
+
+def gpu_route(p, mode, kw, cuda):
+    cfg = p["cfg"]
+    q = dev(p["q"], cfg.dtype, cuda)
+    k = dev(p["k"], cfg.dtype, cuda)
+    if mode == "flat":
+        kv_num, kv_idx, _ = K.block_route(q, k, cfg.block, compact=True, **kw)
+    else:
+        kv_num, kv_idx, _ = K.block_route_budget(q, k, cfg.block, compact=True, **kw)
+    return kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+
+
+@pytest.mark.parametrize("case", list(ROUTE_CASES))
+def test_route_bit_exact_vs_oracle_and_reference(cuda, case):
+    cfg_name, variant, mode, kw = ROUTE_CASES[case]
+    p = WL.make(cfg_name, variant)
+    kv_num, kv_idx = gpu_route(p, mode, dict(kw), cuda)
+    onum, oidx = oracle_route(p, mode, dict(kw))
+    n, n_eq, _, bad = GU.compare_selections(kv_num, kv_idx, onum, oidx)
+    assert n_eq == n, f"{n - n_eq} rows differ from the oracle: {bad[:3]}"
+    assert (kv_num == onum).all()
+    g = GU.load(case)
+    r64, mag = certificate_inputs(p, mode, kw)
+    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag)
+    print(f"{case}: {n} rows, {n_eq} identical to the reference, {n_cert} certified near-ties")
+    assert not bad, bad[:3]
+
+
+def test_route_budget_frac_and_edge_rows(cuda):
+    """budget_frac keep in float32, top_c >= #blocks (dense), top_c = 0 (local window only),
+    a single block, and beta = 0 == centroid routing (test_share_route.py:27-37)."""
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((1, 2, 40 * 32, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 40 * 32, 64)).astype(np.float32)
+    qt, kt = dev(q, torch.float32, cuda), dev(k, torch.float32, cuda)
+    for kw in (dict(budget_frac=0.1, local=1), dict(budget_frac=0.3, local=0),
+               dict(budget_frac=1.0, local=1), dict(top_c=999, local=1), dict(top_c=0, local=2),
+               dict(top_c=3, local=1, beta=0.0)):
+        a, b, _ = K.block_route_budget(qt, kt, 32, compact=True, **kw)
+        on, oi = O.route_budget(q, k, 32, **{"top_c": None, **kw})
+        n, n_eq, _, bad = GU.compare_selections(a.cpu().numpy(), b.cpu().numpy(), on, oi)
+        assert n_eq == n, (kw, bad[:3])
+    one, onei, _ = K.block_route_budget(qt[:, :, :32], kt[:, :, :32], 32, compact=True, top_c=4)
+    assert one.cpu().tolist() == [[[1], [1]]] and onei.cpu().tolist() == [[[[0]], [[0]]]]
+    a0 = K.block_route_budget(qt, kt, 32, top_c=3, local=1, beta=0.0, compact=True)
+    ac = K.route(K.block_summary(qt, 32, "qmean"), K.block_summary(kt, 32, "pop")[0], None, None,
+                 "budget", 3, 0.0, 1, 0.0)
+    assert torch.equal(a0[0], ac[0]) and torch.equal(a0[1], ac[1])
+
+
+def test_route_ties_take_lowest_index(cuda):
+    """Identical key blocks tie exactly: the lowest block indices win."""
+    x = np.ones((1, 1, 16 * 32, 8), dtype=np.float32)
+    xt = dev(x, torch.float32, cuda)
+    kv_num, kv_idx, _ = K.block_route_budget(xt, xt, 32, top_c=3, local=0, compact=True)
+    rows = GU.row_sets(kv_num.cpu().numpy(), kv_idx.cpu().numpy())
+    for i, s in enumerate(rows):
+        assert s == frozenset(list(range(min(3, i))) + [i]), (i, s)
+
+
+def test_route_reference_dense_outputs(cuda):
+    """Default (non-compact) returns the reference's (kv_num, argsort-order kv_idx, sel)."""
+    rng = np.random.default_rng(10)
+    q = rng.standard_normal((1, 2, 8 * 64, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 8 * 64, 64)).astype(np.float32)
+    kv_num, kv_full, sel = K.block_route_budget(dev(q, torch.float32, cuda),
+                                                dev(k, torch.float32, cuda), 64, top_c=2, local=1)
+    assert sel.dtype == torch.bool and sel.shape == (1, 2, 8, 8)
+    ref = torch.argsort(sel.cpu().int(), dim=-1, descending=True, stable=True).int()
+    assert torch.equal(kv_full.cpu(), ref)
+    assert torch.equal(kv_num.cpu(), sel.cpu().sum(-1).int())
+    qi = torch.arange(8)
+    assert not (sel.cpu() & (qi[:, None] < qi[None, :])).any()
+
+
+# ---- a6-a8 attention ---------------------------------------------------------------------------
+
+def test_ssa_flex_c1_fp32_matches_reference_flexattention(cuda):
+    g = GU.load("c1_flex_out")
+    p = WL.make("C1")
+    q, k, v = (dev(p[x], torch.float32, cuda) for x in ("q", "k", "v"))
+    out = K.ssa_flex(q, k, v, block=64, top_c=8, local=1)
+    err = np.abs(np_of(out) - g["out"]).max()
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("cfg_name,n,qblocks", [("C2", 8192, [0, 1, 5, 63, 127]),
+                                                ("C3", 131072, [0, 3, 64, 511, 1023])])
+def test_sparse_attention_matches_oracle(cuda, cfg_name, n, qblocks):
+    p = WL.make(cfg_name, n=n)
+    cfg = p["cfg"]
+    q, k, v = (dev(p[x], cfg.dtype, cuda) for x in ("q", "k", "v"))
+    kv_num, kv_idx, _ = K.block_route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                             beta=cfg.beta, compact=True)
+    out = K.sparse_attention(q, k, v, kv_num, kv_idx, cfg.block)
+    heads = [0, 6, 13]
+    ref = O.sparse_attention(p["q"], p["k"], p["v"], kv_num.cpu().numpy(), kv_idx.cpu().numpy(),
+                             cfg.block, qblocks=qblocks, heads=heads)
+    o = np_of(out)
+    for h in heads:
+        for i in qblocks:
+            sl = slice(i * cfg.block, (i + 1) * cfg.block)
+            err = np.abs(o[0, h, sl] - ref[0, h, sl]).max()
+            assert err < TOL[cfg.dtype], (h, i, err)
+    assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("block", [64, 128, 256])
+def test_full_budget_matches_dense_sdpa(cuda, dtype, block):
+    """Every causal block selected -> dense causal attention (test_ssa_kernel.py:8-18)."""
+    torch.manual_seed(0)
+    n = 4 * 256
+    q = torch.randn(1, 2, n, 64, device=cuda, dtype=dtype)
+    k, v = torch.randn_like(q), torch.randn_like(q)
+    out = K.ssa_flex(q, k, v, block=block, top_c=n // block, local=n // block)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
+    assert (out.float() - ref).abs().max().item() < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype,block,n", [(torch.float16, 256, 1000), (torch.bfloat16, 128, 300),
+                                           (torch.bfloat16, 64, 333), (torch.float32, 64, 200)])
+def test_ragged_length_gqa_matches_oracle(cuda, dtype, block, n):
+    """n not a block multiple (pad keys masked, pad queries not written), GQA 3:1, lse."""
+    rng = np.random.default_rng(12)
+    q = WL.round_to(rng.standard_normal((1, 6, n, 64)).astype(np.float32), dtype)
+    k = WL.round_to(rng.standard_normal((1, 2, n, 64)).astype(np.float32), dtype)
+    v = WL.round_to(rng.standard_normal((1, 2, n, 64)).astype(np.float32), dtype)
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    kv_num, kv_idx = K.route(K.block_summary(qt, block, "qmean"),
+                             *K.block_summary(kt, block, "pop", n_real=n)[:2], None, "budget", 2,
+                             0.0, 1, 1.0)
+    out, lse = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, scale=0.2, return_lse=True)
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), block, scale=0.2)
+    assert np.abs(np_of(out) - ref).max() < TOL[dtype]
+    assert torch.isfinite(lse).all()
+
+
+def test_hf_layout_output_without_copies(cuda):
+    """(b, n, h, d) buffers viewed as (b, h, n, d): strided q/k/v and output."""
+    torch.manual_seed(1)
+    b, n, hq, hkv = 1, 512, 4, 2
+    qb = torch.randn(b, n, hq, 64, device=cuda, dtype=torch.bfloat16)
+    kb = torch.randn(b, n, hkv, 64, device=cuda, dtype=torch.bfloat16)
+    vb = torch.randn(b, n, hkv, 64, device=cuda, dtype=torch.bfloat16)
+    q, k, v = qb.transpose(1, 2), kb.transpose(1, 2), vb.transpose(1, 2)
+    kv_num, kv_idx, _ = K.block_route_budget(q, k, 128, top_c=2, local=0, compact=True)
+    outb = torch.empty(b, n, hq, 64, device=cuda, dtype=torch.bfloat16)
+    K.sparse_attention(q, k, v, kv_num, kv_idx, 128, out=outb.transpose(1, 2))
+    ref = K.sparse_attention(q.contiguous(), k.contiguous(), v.contiguous(), kv_num, kv_idx, 128)
+    assert torch.equal(outb.transpose(1, 2), ref)
+
+
+def test_no_future_leak(cuda):
+    """Perturbing keys/values after position `cut` leaves outputs <= cut unchanged."""
+    torch.manual_seed(0)
+    n, cut = 1024, 300
+    q = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.bfloat16)
+    k, v = torch.randn_like(q), torch.randn_like(q)
+    o1 = K.ssa_flex(q, k, v, block=128, top_c=2, local=1)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, cut + 1:] += 5
+    v2[:, :, cut + 1:] += 5
+    o2 = K.ssa_flex(q, k2, v2, block=128, top_c=2, local=1)
+    assert torch.equal(o1[:, :, :cut + 1], o2[:, :, :cut + 1])
+
+
+# ---- a10-a12 decode ----------------------------------------------------------------------------
+
+def test_decode_attend_matches_oracle_and_prefill_row(cuda):
+    rng = np.random.default_rng(13)
+    n, block = 12 * 128, 128
+    q = WL.round_to(rng.standard_normal((1, 1, n, 64)).astype(np.float32), torch.bfloat16)
+    k = WL.round_to(rng.standard_normal((1, 1, n, 64)).astype(np.float32), torch.bfloat16)
+    v = WL.round_to(rng.standard_normal((1, 1, n, 64)).astype(np.float32), torch.bfloat16)
+    qt, kt, vt = (dev(x, torch.bfloat16, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=4, local=1, compact=True)
+    pre = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block)
+    blocks = kv_idx[0, 0, 11, :int(kv_num[0, 0, 11])].tolist() + [3, 3]   # duplicates attend once
+    row = D.decode_attend(qt[0, 0, n - 1], kt[0, 0], vt[0, 0], blocks, n - 1, block)
+    ref = O.decode_attend(q[0, 0, n - 1], k[0, 0], v[0, 0], blocks, n - 1, block)
+    assert np.abs(np_of(row) - ref).max() < 2e-2
+    assert (row.float() - pre[0, 0, n - 1].float()).abs().max().item() < 2e-2
+    # a block past pos contributes nothing; pos inside a block clips it
+    row2 = D.decode_attend(qt[0, 0, 700], kt[0, 0], vt[0, 0], [0, 5, 9], 700, block)
+    ref2 = O.decode_attend(q[0, 0, 700], k[0, 0], v[0, 0], [0, 5, 9], 700, block)
+    assert np.abs(np_of(row2) - ref2).max() < 2e-2
+
+
+def test_routed_decoder_matches_reference_router_and_oracle(cuda):
+    """RoutedDecoder on a C4-shaped cache: the selection at each fixture position equals the
+    reference _selection_mask (float32) and the oracle; the output matches the oracle row."""
+    g = GU.load("c4_query")
+    p = WL.make("C4", n=65536 + 128)
+    cfg = p["cfg"]
+    positions = g["positions"].tolist()
+    dec = D.RoutedDecoder(1, cfg.Hq, cfg.Hkv, cfg.d, 65536 + 128, block=cfg.block,
+                          top_c=cfg.top_c, local=cfg.local, beta=cfg.beta, dtype=cfg.dtype,
+                          device=cuda)
+    start = positions[0]
+    dec.prefill(dev(p["k"][:, :, :start], cfg.dtype, cuda), dev(p["v"][:, :, :start], cfg.dtype, cuda))
+    G_ = cfg.Hq // cfg.Hkv
+    for pos in range(start, positions[-1] + 1):
+        q = dev(p["q"][:, :, pos], cfg.dtype, cuda)
+        out = dec.step(q, dev(p["k"][:, :, pos], cfg.dtype, cuda), dev(p["v"][:, :, pos], cfg.dtype, cuda))
+        if pos not in positions:
+            continue
+        a = positions.index(pos)
+        kn, ki = dec.kv_num.cpu().numpy(), dec.kv_idx.cpu().numpy()
+        onum, oidx = O.route_query(p["q"][:, :, pos:pos + 1], p["k"], cfg.block, pos,
+                                   top_c=cfg.top_c, local=cfg.local, beta=cfg.beta, kv_len=pos + 1)
+        n_, n_eq, _, bad = GU.compare_selections(kn, ki, onum[:, :, 0], oidx[:, :, 0])
+        assert n_eq == n_, (pos, bad)
+        mu, var, _ = O.block_stats(p["k"][:, :, :pos + 1], cfg.block, "pop")
+        r64, mag = O.exact_scores64(p["q"][:, :, pos:pos + 1], mu, var, 0.5 * cfg.beta)
+        n_, n_eq, n_cert, bad = GU.compare_selections(kn, ki, g["kv_num"][a][None],
+                                                      g["kv_idx"][a][None], r64[:, :, 0], mag[:, :, 0])
+        assert not bad, (pos, bad)
+        for h in (0, 7, 13):
+            ids = ki[0, h, :kn[0, h]]
+            ref = O.decode_attend(p["q"][0, h, pos], p["k"][0, h // G_], p["v"][0, h // G_], ids,
+                                  pos, cfg.block)
+            assert np.abs(np_of(out[0, h]) - ref).max() < 2e-2
+
+
+# ---- a9 real-model boundary --------------------------------------------------------------------
+
+def _mod(groups=1, scaling=0.125, layer_idx=0):
+    from types import SimpleNamespace
+    return SimpleNamespace(num_key_value_groups=groups, is_sliding=False, scaling=scaling,
+                           layer_idx=layer_idx)
+
+
+@pytest.mark.parametrize("impl", ["flex", "analytic"])
+def test_gemma_full_budget_matches_sdpa(cuda, impl):
+    """test_flex_swap.py:82-93 / test_gemma_ssa.py:45-52 restated, GQA 2:1, n=300 ragged."""
+    torch.manual_seed(0)
+    for n in (512, 300):
+        q = torch.randn(1, 4, n, 64, device=cuda, dtype=torch.float16)
+        k = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.float16)
+        v = torch.randn_like(k)
+        G.CFG = G.SSAConfig(block=128, budget_frac=1.0, impl=impl)
+        out, _ = G.ssa_attention_forward(_mod(groups=2), q, k, v, scaling=1 / 8)
+        ref = F.scaled_dot_product_attention(q.float(), G.repeat_kv(k, 2).float(),
+                                             G.repeat_kv(v, 2).float(), is_causal=True,
+                                             scale=1 / 8).transpose(1, 2)
+        assert out.shape == (1, n, 4, 64)
+        assert (out.float() - ref).abs().max().item() < 2e-2
+
+
+def test_gemma_analytic_matches_reference_fixture(cuda):
+    g = GU.load("analytic_gqa")
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, 4, 300, 64))
+    k = rng.standard_normal((1, 2, 300, 64))
+    v = rng.standard_normal((1, 2, 300, 64))
+    G.CFG = G.SSAConfig(block=64, budget_frac=0.5, local_w=1, beta=2.0, impl="analytic")
+    qt, kt, vt = (torch.from_numpy(x).float().to(cuda) for x in (q, k, v))
+    out, _ = G.ssa_attention_forward(_mod(groups=2), qt, kt, vt, scaling=0.125)
+    assert np.abs(np_of(out) - g["out"]).max() < 1e-5
+    inc, _ = G.ssa_attention_forward(_mod(groups=2), qt[:, :, -1:], kt, vt, scaling=0.125)
+    assert np.abs(np_of(inc) - g["out_last"]).max() < 1e-5
+
+
+def test_gemma_decode_equals_prefill_last_row(cuda):
+    """test_gemma_ssa.py:86-98 restated on the HIP per-query path."""
+    torch.manual_seed(2)
+    q = torch.randn(1, 4, 640, 64, device=cuda, dtype=torch.float32)
+    k = torch.randn(1, 2, 640, 64, device=cuda, dtype=torch.float32)
+    v = torch.randn_like(k)
+    for frac in (0.5, 0.25):
+        G.CFG = G.SSAConfig(block=64, budget_frac=frac, impl="analytic")
+        full, _ = G.ssa_attention_forward(_mod(groups=2), q, k, v, scaling=1.0)
+        inc, _ = G.ssa_attention_forward(_mod(groups=2), q[:, :, -1:], k, v, scaling=1.0)
+        assert (inc[:, 0] - full[:, -1]).abs().max().item() < 1e-5
+
+
+def test_gemma_flex_no_future_leak_and_sharing(cuda):
+    torch.manual_seed(0)
+    n, cut = 512, 256
+    q = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.float16)
+    k = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.float16)
+    v = torch.randn_like(k)
+    G.CFG = G.SSAConfig(block=128, budget_frac=0.5, impl="flex")
+    o1, _ = G.ssa_attention_forward(_mod(), q, k.clone(), v.clone(), scaling=1 / 8)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, cut + 1:] += 5.0 * torch.randn_like(k2[:, :, cut + 1:])
+    v2[:, :, cut + 1:] += 5.0 * torch.randn_like(v2[:, :, cut + 1:])
+    o2, _ = G.ssa_attention_forward(_mod(), q, k2, v2, scaling=1 / 8)
+    assert torch.equal(o1[:, :cut + 1], o2[:, :cut + 1])
+    # donor layer 0 stashes its selection; consumer layer 1 reuses the same object
+    G.CFG = G.SSAConfig(block=128, budget_frac=0.25, impl="flex", share_route_from=0)
+    G._SHARE["sig"] = None
+    G._SHARE["bm"] = None
+    G.ssa_attention_forward(_mod(layer_idx=0), q, k, v, scaling=1 / 8)
+    bm0 = G._SHARE["bm"]
+    assert bm0 is not None
+    G.ssa_attention_forward(_mod(layer_idx=1), q, k, v, scaling=1 / 8)
+    assert G._SHARE["bm"] is bm0

@@ -1,0 +1,243 @@
+"""CPU tests pinning the oracle (oracle/ssa_oracle.py) before it is trusted as the checker.
+
+* against the reference's own outputs (tests/golden/, written by tests/golden/make_golden.py
+  from the reference run in float32/float64): selections of block_route_budget / block_route /
+  _selection_mask, the FlexAttention output of ssa_flex, the analytic attention path;
+* against mathematics: closed-form block statistics, brute-force ranking on tiny rows, full
+  budget == dense causal softmax, the needle known-answer test, the reference's invariants.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ssa_oracle as O
+from ssa_amd import workloads as WL
+from tests import golden_util as GU
+
+ROUTE_CASES = {
+    # fixture: (config, variant, mode, kwargs)
+    "c1_budget": ("C1", "segmented", "budget", dict(top_c=8, local=1, beta=2.0)),
+    "c1_frac": ("C1", "segmented", "budget", dict(budget_frac=0.25, local=1, beta=2.0)),
+    "c1_flat": ("C1", "segmented", "flat", dict(top_c=8, local=1)),
+    "c2_budget": ("C2", "segmented", "budget", dict(top_c=32, local=2, beta=2.0)),
+    "c2_edgeworth": ("C2", "segmented", "budget", dict(top_c=32, local=2, beta=2.0, edgeworth=True)),
+    "c3_budget_seg": ("C3", "segmented", "budget", dict(top_c=64, local=2, beta=2.0)),
+    "c3_budget_lit": ("C3", "literal", "budget", dict(top_c=64, local=2, beta=2.0)),
+}
+
+
+def oracle_route(p, mode, kw):
+    cfg = p["cfg"]
+    if mode == "flat":
+        return O.route_flat(p["q"], p["k"], cfg.block, **kw)
+    return O.route_budget(p["q"], p["k"], cfg.block, **kw)
+
+
+def certificate_inputs(p, mode, kw):
+    cfg = p["cfg"]
+    qb = O.qmean(p["q"], cfg.block)
+    if mode == "flat":
+        mu, var, _ = O.block_stats(p["k"], cfg.block, "unbiased")
+        return O.exact_scores64(qb, mu, var, 0.5)
+    mu, var, m3 = O.block_stats(p["k"], cfg.block, "pop")
+    beta = kw.get("beta", 2.0)
+    return O.exact_scores64(qb, mu, var, 0.5 * beta, m3 if kw.get("edgeworth") else None,
+                            beta ** 2 / 6.0)
+
+
+@pytest.mark.parametrize("case", list(ROUTE_CASES))
+def test_oracle_selection_matches_reference(case):
+    cfg_name, variant, mode, kw = ROUTE_CASES[case]
+    g = GU.load(case)
+    p = WL.make(cfg_name, variant)
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"]), "generator drifted from the fixture"
+    kv_num, kv_idx = oracle_route(p, mode, dict(kw))
+    r64, mag = certificate_inputs(p, mode, kw)
+    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag)
+    print(f"{case}: {n} rows, {n_eq} identical, {n_cert} certified float32 near-ties")
+    assert not bad, bad[:5]
+    # the certificate must be rare: these inputs are not adversarial
+    assert n_cert <= max(2, n // 1000), (n_cert, n)
+
+
+def test_oracle_decode_selection_matches_reference():
+    g = GU.load("c4_query")
+    p = WL.make("C4", n=65536 + 128)
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"])
+    cfg = p["cfg"]
+    for a, pos in enumerate(g["positions"].tolist()):
+        rows = p["q"][:, :, pos:pos + 1]
+        kv_num, kv_idx = O.route_query(rows, p["k"], cfg.block, pos, top_c=cfg.top_c,
+                                       local=cfg.local, beta=cfg.beta, kv_len=pos + 1)
+        mu, var, _ = O.block_stats(p["k"][:, :, :pos + 1], cfg.block, "pop")
+        r64, mag = O.exact_scores64(rows, mu, var, 0.5 * cfg.beta)
+        n, n_eq, n_cert, bad = GU.compare_selections(kv_num[:, :, 0], kv_idx[:, :, 0],
+                                                     g["kv_num"][a][None], g["kv_idx"][a][None],
+                                                     r64[:, :, 0], mag[:, :, 0])
+        assert not bad and n_eq + n_cert == n, (pos, bad)
+
+
+def test_oracle_attention_matches_reference_flex_output():
+    """ssa_flex (FlexAttention, float32, CPU) on C1 vs the oracle's exact masked softmax over
+    the oracle's block_route selection: within the float32 tolerance 1e-5."""
+    g = GU.load("c1_flex_out")
+    p = WL.make("C1")
+    assert GU.sha(p["q"], p["k"], p["v"]) == str(g["inputs_sha256"])
+    kv_num, kv_idx = O.route_flat(p["q"], p["k"], 64, top_c=8, local=1)
+    out = O.sparse_attention(p["q"], p["k"], p["v"], kv_num, kv_idx, 64)
+    err = np.abs(out - g["out"]).max()
+    assert err < 1e-5, err
+
+
+def test_oracle_analytic_path_matches_reference():
+    """Per-query routing + masked softmax (ssa_attention_forward impl='analytic', float64,
+    GQA 2:1, n=300 not a block multiple) and the q_len=1 decode row."""
+    g = GU.load("analytic_gqa")
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, 4, 300, 64))
+    k = rng.standard_normal((1, 2, 300, 64))
+    v = rng.standard_normal((1, 2, 300, 64))
+    assert GU.sha(q, k, v) == str(g["inputs_sha256"])
+    kv_num, kv_idx = O.route_query(q, k, 64, 0, top_c=None, budget_frac=0.5, local=1, beta=2.0)
+    out = O.attend_rows(q, k, v, kv_num, kv_idx, 0, 64, scale=0.125)
+    ref = g["out"].transpose(0, 2, 1, 3)
+    # the reference takes its softmax in float32 even for float64 inputs (gemma_ssa.py:239),
+    # so it carries float32 rounding of the weights (~1e-7); a selection difference would be O(0.1)
+    assert np.abs(out - ref).max() < 2e-6
+    assert np.abs(out[:, :, -1] - g["out_last"][:, 0]).max() < 2e-6
+
+
+# ---- mathematics -------------------------------------------------------------------------------
+
+def test_block_stats_closed_form():
+    x = np.zeros((1, 1, 10, 8), dtype=np.float32)
+    x[0, 0, :, 0] = np.arange(10)             # block of 4: 0..3 -> mean 1.5, pop var 1.25
+    x[0, 0, :, 1] = 2.0                       # constant column -> var 0
+    mu, var, m3 = O.block_stats(x, 4, "pop")
+    assert mu.shape == (1, 1, 3, 8)
+    assert mu[0, 0, 0, 0] == 1.5 and var[0, 0, 0, 0] == 1.25 and m3[0, 0, 0, 0] == 0.0
+    assert var[0, 0, 0, 1] == 0.0 and mu[0, 0, 1, 1] == 2.0
+    # last block holds rows 8, 9 only (n=10): mean 8.5, pop var 0.25
+    assert mu[0, 0, 2, 0] == 8.5 and var[0, 0, 2, 0] == 0.25
+    _, uvar, _ = O.block_stats(x, 4, "unbiased")
+    assert uvar[0, 0, 0, 0] == np.float32(5.0 / 3.0)
+    # n_real excludes pad rows: rows >= 9 dropped -> block 2 = {8}
+    mu2, var2, _ = O.block_stats(x, 4, "pop", n_real=9)
+    assert mu2[0, 0, 2, 0] == 8.0 and var2[0, 0, 2, 0] == 0.0
+    # skew of {0, 0, 0, 4}: mean 1, m3 = (3*(-1)^3 + 27)/4 = 6
+    y = np.zeros((1, 1, 4, 8), dtype=np.float32)
+    y[0, 0, 3, 0] = 4.0
+    assert O.block_stats(y, 4, "pop")[2][0, 0, 0, 0] == 6.0
+    # query mean counts pad rows as zeros
+    assert O.qmean(x, 4)[0, 0, 2, 0] == np.float32((8 + 9) / 4)
+
+
+def test_scores_closed_form():
+    rows = np.array([[[[1.0, 2.0]]]], dtype=np.float32)           # (1,1,1,2)
+    mu = np.array([[[[3.0, -1.0], [0.5, 0.5]]]], dtype=np.float32)
+    var = np.array([[[[2.0, 1.0], [0.0, 4.0]]]], dtype=np.float32)
+    r = O.scores(rows, mu, var, coef2=1.0)
+    # <q,mu> + 1.0*<q^2,var>: (3-2) + (2+4) = 7 ; (0.5+1) + (0+16) = 17.5
+    assert r[0, 0, 0].tolist() == [7.0, 17.5]
+    m3 = np.array([[[[1.0, 0.0], [0.0, -1.0]]]], dtype=np.float32)
+    r3 = O.scores(rows, mu, var, 1.0, m3, coef3=2.0 / 3.0)
+    assert np.allclose(r3[0, 0, 0], [7.0 + 2.0 / 3.0, 17.5 - 16.0 / 3.0], atol=1e-5)
+
+
+def test_select_matches_bruteforce_ranking():
+    """select_rows against an independent O(n^2) rank count, with forced exact ties."""
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        nbk = int(rng.integers(2, 24))
+        r = rng.integers(-3, 4, size=(1, 1, nbk, nbk)).astype(np.float32)   # many exact ties
+        top_c = int(rng.integers(0, 6))
+        local = int(rng.integers(0, 3))
+        mode = ["budget", "flat"][trial % 2]
+        got = O.select_rows(r, mode, top_c, 0.0, local)
+        for i in range(nbk):
+            cmax = i if mode == "budget" else i + 1
+            k = min(top_c, cmax)
+            row = r[0, 0, i, :cmax]
+            rank = [sum(1 for y in range(cmax) if row[y] > row[x] or (row[y] == row[x] and y < x))
+                    for x in range(cmax)]
+            pick = {x for x in range(cmax) if rank[x] < k}
+            pick |= set(range(max(0, i - local), i + 1))
+            assert got[0, 0, i] == sorted(pick), (trial, i)
+
+
+def test_budget_keep_is_float32_ceil():
+    # ceil(fl32(0.1) * 10) = ceil(1.0000000149 rounded to fp32 = 1.0) = 1, not 2
+    assert O._keep_budget(0.1, 10) == 1
+    assert O._keep_budget(0.25, 0) == 1
+    assert O._keep_budget(0.3, 7) == 3      # fl32(0.3)*7 = 2.1000001 -> 3
+    assert O._keep_budget(1.0, 37) == 37
+
+
+def test_full_budget_equals_dense():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 4, 200, 16))
+    k = rng.standard_normal((1, 2, 200, 16))
+    v = rng.standard_normal((1, 2, 200, 16))
+    kv_num, kv_idx = O.route_budget(q, k, 32, budget_frac=1.0, local=1, n_real=200)
+    assert (kv_num[0, 0] == np.arange(1, 8)).all()
+    out = O.sparse_attention(q, k, v, kv_num, kv_idx, 32, n=200)
+    assert np.abs(out - O.dense_causal(q, k, v)).max() < 1e-12
+
+
+def test_needle_known_answer():
+    """test_gemma_ssa.py:100-121 restated: top_c=1, no local window, a key 12*u aligned with the
+    probe query in block 1 -> per-query routing selects it and the probe output is its value."""
+    rng = np.random.default_rng(0)
+    d, n, block = 64, 128, 32
+    q = rng.standard_normal((1, 1, n, d))
+    k = rng.standard_normal((1, 1, n, d))
+    v = rng.standard_normal((1, 1, n, d))
+    u = rng.standard_normal(d)
+    u /= np.linalg.norm(u)
+    q[0, 0, n - 1] = u
+    k[0, 0, 40] = 12.0 * u
+    v[0, 0, 40] = np.arange(d) / d
+    kv_num, kv_idx = O.route_query(q[:, :, -1:], k, block, n - 1, top_c=1, local=0, beta=2.0)
+    assert 1 in kv_idx[0, 0, 0, :kv_num[0, 0, 0]].tolist()
+    out = O.decode_attend(q[0, 0, -1], k[0, 0], v[0, 0], kv_idx[0, 0, 0, :kv_num[0, 0, 0]], n - 1,
+                          block, scale=1.0)
+    assert np.abs(out - v[0, 0, 40]).max() < 3e-3
+
+
+def test_budget_router_invariants():
+    """test_flex_swap.py:49-73 restated: causal, own block kept, counts monotone in budget."""
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 1, 32 * 128, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 32 * 128, 64)).astype(np.float32)
+    kv_num, kv_idx = O.route_budget(q, k, 128, budget_frac=0.25, local=1)
+    for i in range(32):
+        ids = kv_idx[0, 0, i, :kv_num[0, 0, i]].tolist()
+        assert all(c <= i for c in ids) and i in ids
+    counts = [int(O.route_budget(q, k, 128, budget_frac=f, local=0)[0].sum())
+              for f in (1.0, 0.5, 0.25, 0.1)]
+    assert counts[0] > counts[1] > counts[2] >= counts[3], counts
+
+
+def test_decode_row_equals_prefill_row():
+    """decode_attend over a query block's selection reproduces that block's last prefill row
+    (test_ivf_decode.py:14-29 restated)."""
+    rng = np.random.default_rng(3)
+    n, block = 12 * 64, 64
+    q = rng.standard_normal((1, 1, n, 64))
+    k = rng.standard_normal((1, 1, n, 64))
+    v = rng.standard_normal((1, 1, n, 64))
+    kv_num, kv_idx = O.route_budget(q, k, block, top_c=4, local=1)
+    pre = O.sparse_attention(q, k, v, kv_num, kv_idx, block, qblocks=[11])
+    row = O.decode_attend(q[0, 0, n - 1], k[0, 0], v[0, 0], kv_idx[0, 0, 11, :kv_num[0, 0, 11]],
+                          n - 1, block)
+    assert np.abs(row - pre[0, 0, n - 1]).max() < 1e-12
+
+
+def test_keys_order_and_special_values():
+    r = np.array([-np.inf, -2.0, -0.0, 0.0, 1e-30, 3.0, np.inf, np.nan], dtype=np.float32)
+    k = O.score_keys(r)
+    assert (np.diff(k[:2].astype(np.int64)) > 0).all()
+    assert k[2] == k[3]                                     # -0 == +0
+    assert list(np.argsort(k[[0, 1, 3, 4, 5, 6, 7]], kind="stable")) == list(range(7))
+    assert math.isnan(float(r[7])) and k[7] == np.uint32(0xFFFFFFFF)
