@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed block-sparse attention hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--variant segmented|literal]
+
+Headline workload ("C3"): one causal routed-prefill attention layer
+at the Qwen2.5-0.5B attention shape -- 14 query / 2 key heads, d = 64, n = 131072, bf16,
+block 128, top_c 64 + 2-block local window, beta 2. A step is the whole hot path over the
+resident inputs: query-block means + key-block mean/variance -> cumulant router -> V transpose
+-> block-sparse flash attention. value = n * K / (time of K steps) tokens/s.
+
+Also reported on the same line: per-kernel times (HIP events on the stream the kernels run on),
+the roofline of the dominant kernel (selected-block FLOPs = 4*b^2*d*sum(kv_num) per launch
+against the 2.5 PFLOP/s bf16 dense MFMA peak; HBM traffic from the committed rocprofv3 PMC
+summary when present), the dense causal baseline (torch SDPA) and this kernel at full budget,
+the routed decode step at a 1M-token cache ("C4", ms/step), and the CPU baseline: the NumPy
+oracle (oracle/ssa_oracle.py) timed on this host's cores on a bounded sample.
+
+Only one GPU is used: --gpus N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "routed prefill tokens/s @128K (Qwen-0.5B shape); decode ms/step @1M ctx"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--variant", default="segmented", choices=["segmented", "literal"])
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
+    ap.add_argument("--no-decode", action="store_true", help="skip the C4 decode step")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (PMC byte-count calibration)")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP-event timer on the current stream (where every ssa_amd kernel is launched)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.acc = {}
+
+    def run(self, name, fn, *a, **kw):
+        t = self.torch
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        s.record()
+        r = fn(*a, **kw)
+        e.record()
+        self.acc.setdefault(name, []).append((s, e))
+        return r
+
+    def mean_ms(self, name):
+        ev = self.acc[name]
+        return sum(s.elapsed_time(e) for s, e in ev) / len(ev)
+
+    def reset(self):
+        self.acc = {}
+
+
+def read_traffic():
+    if not TRAFFIC_FILE.exists():
+        return None
+    kv = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if ":" in line and not line.lstrip().startswith("#"):
+            key, val = line.split(":", 1)
+            kv[key.strip()] = val.strip()
+    try:
+        return float(kv["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(p, kv_num_all, threads):
+    """The oracle on the host: the C3 router in full plus attention for a stratified sample of
+    query blocks, extrapolated by sum(kv_num)."""
+    import numpy as np
+
+    from oracle import ssa_oracle as O
+    cfg = p["cfg"]
+    t0 = time.perf_counter()
+    onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                beta=cfg.beta)
+    t_route = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    nb = cfg.nb
+    blocks = sorted(set(np.linspace(0, nb - 1, 24).astype(int).tolist()))
+    heads = [int(h) for h in rng.integers(0, cfg.Hq, size=len(blocks))]
+    t0 = time.perf_counter()
+    sample_kv = 0
+    for i, h in zip(blocks, heads):
+        O.sparse_attention(p["q"], p["k"], p["v"], onum, oidx, cfg.block, qblocks=[i], heads=[h])
+        sample_kv += int(onum[0, h, i])
+    t_sample = time.perf_counter() - t0
+    total_kv = int(kv_num_all)
+    t_attn = t_sample * total_kv / sample_kv
+    t_total = t_route + t_attn
+    return {
+        "value": cfg.n / t_total, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle (NumPy float64) C3 router over all {cfg.Hq * nb} query-block rows "
+                   f"({t_route:.2f} s) + exact attention for {len(blocks)} (head, query-block) "
+                   f"pairs ({sample_kv} of {total_kv} selected tiles, {t_sample:.2f} s), "
+                   f"extrapolated by sum(kv_num) to {t_total:.1f} s per layer"),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "bench.py runs on exactly one GPU: this build has no "
+                          "multi-GPU path (one MI355X box has one GPU); run with --gpus 1"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from ssa_amd import ivf_decode as D
+    from ssa_amd import ssa_kernel as K
+    from ssa_amd import workloads as WL
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("bench: generating C3 inputs")
+    p = WL.make("C3", args.variant)
+    cfg = p["cfg"]
+    q, k, v = (WL.to_device(p[x], cfg.dtype, dev) for x in ("q", "k", "v"))
+    n, blk = cfg.n, cfg.block
+    tm = Timer(torch)
+
+    def step(timer):
+        qbar = timer.run("qmean", K.block_summary, q, blk, "qmean")
+        mu, var, _ = timer.run("kstats", K.block_summary, k, blk, "pop")
+        kv_num, kv_idx = timer.run("route", K.route, qbar, mu, var, None, "budget", cfg.top_c,
+                                   0.0, cfg.local, 0.5 * cfg.beta)
+        vt = timer.run("transpose_v", K.transpose_v, v, blk)
+        out = timer.run("attention", K.sparse_attention, q, k, v, kv_num, kv_idx, blk, vt=vt)
+        return out, kv_num
+
+    log(f"bench: warmup {args.warmup}")
+    for _ in range(args.warmup):
+        out, kv_num = step(tm)
+    torch.cuda.synchronize()
+    tm.reset()
+    log(f"bench: timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out, kv_num = step(tm)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall / args.steps * 1000.0
+    parts = {nm: tm.mean_ms(nm) for nm in ("qmean", "kstats", "route", "transpose_v", "attention")}
+    sum_kv = int(kv_num.sum().item())
+    flops = 4.0 * blk * blk * cfg.d * sum_kv
+    t_attn = parts["attention"] / 1e3
+    achieved = flops / t_attn / 1e12
+    traffic = read_traffic()
+    diag = cfg.Hq * cfg.nb
+    flops_causal = 4.0 * cfg.d * (blk * blk * (sum_kv - diag) + diag * blk * (blk + 1) / 2)
+    summary_bytes = (cfg.Hkv + cfg.Hq) * n * cfg.d * 2 + (2 * cfg.Hkv + cfg.Hq) * cfg.nb * cfg.d * 4
+    log(f"bench: {ms_step:.3f} ms/step; parts {parts}; sum kv_num {sum_kv}")
+
+    result = {
+        "metric": METRIC, "value": n / (ms_step / 1e3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": f"synthetic: seeded NumPy PCG64 (seed {cfg.seed}), keys from a 256-component "
+                f"Gaussian mixture ({args.variant}), Q/V ~ N(0,1), resident in HBM",
+        "config": {"workload": "C3: one causal routed-prefill attention layer, Qwen2.5-0.5B "
+                               "attention shape (14q/2kv heads, d=64), n=131072, block 128, "
+                               "top_c 64 + local 2, beta 2, summaries+router+attention per step",
+                   "n": n, "Hq": cfg.Hq, "Hkv": cfg.Hkv, "d": cfg.d, "block": blk,
+                   "top_c": cfg.top_c, "local": cfg.local, "beta": cfg.beta,
+                   "variant": args.variant},
+        "roofline": {"bound": "mfma", "kernel": "sparse_attn_mfma_kernel",
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "flops_per_launch": flops, "flops_causal_exact": flops_causal,
+                     "sum_kv_num": sum_kv},
+        "breakdown_ms": parts,
+        "summaries_gbs": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3) / 1e9,
+    }
+
+    if not args.no_dense:
+        log("bench: dense baselines")
+        kr, vr = k.repeat_interleave(cfg.Hq // cfg.Hkv, dim=1), v.repeat_interleave(cfg.Hq // cfg.Hkv, dim=1)
+        sd = Timer(torch)
+        for i in range(4):
+            sd.run("sdpa" if i else "warm", torch.nn.functional.scaled_dot_product_attention,
+                   q, kr, vr, is_causal=True)
+        qbar = K.block_summary(q, blk, "qmean")
+        mu, var, _ = K.block_summary(k, blk, "pop")
+        fnum, fidx = K.route(qbar, mu, var, None, "budget", None, 1.0, cfg.local, 0.5 * cfg.beta)
+        vt = K.transpose_v(v, blk)
+        for i in range(3):
+            sd.run("own_full" if i else "warm", K.sparse_attention, q, k, v, fnum, fidx, blk, vt=vt)
+        torch.cuda.synchronize()
+        dense_ms = sd.mean_ms("sdpa")
+        own_full = sd.mean_ms("own_full")
+        dense_flops = 4.0 * cfg.d * cfg.Hq * n * (n + 1) / 2
+        result["dense"] = {
+            "sdpa_causal_ms": dense_ms, "own_kernel_full_budget_ms": own_full,
+            "speedup_vs_sdpa": dense_ms / ms_step, "attention_speedup_vs_sdpa": dense_ms / parts["attention"],
+            "sdpa_tflops": dense_flops / (dense_ms / 1e3) / 1e12,
+            "own_full_tflops": 4.0 * blk * blk * cfg.d * int(fnum.sum().item()) / (own_full / 1e3) / 1e12,
+        }
+        del kr, vr
+
+    if not args.no_decode:
+        log("bench: C4 decode")
+        ds = WL.make_decode(steps=args.decode_steps + 8)
+        c4 = ds["cfg"]
+        ncache = ds["n_cache"]
+        dec = D.RoutedDecoder(1, c4.Hq, c4.Hkv, c4.d, ncache + args.decode_steps + 8,
+                              block=c4.block, top_c=c4.top_c, local=c4.local, beta=c4.beta,
+                              dtype=c4.dtype, device=dev)
+        kd, vd = WL.to_device(ds["k"], c4.dtype, dev), WL.to_device(ds["v"], c4.dtype, dev)
+        qd = WL.to_device(ds["q"], c4.dtype, dev)
+        dec.prefill(kd[:, :, :ncache], vd[:, :, :ncache])
+        out_d = torch.empty(1, c4.Hq, c4.d, device=dev, dtype=c4.dtype)
+        for t in range(8):
+            dec.step(qd[:, :, t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(8, 8 + args.decode_steps):
+            dec.step(qd[:, :, t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+        torch.cuda.synchronize()
+        dms = (time.perf_counter() - t0) / args.decode_steps * 1000.0
+        kvn = int(dec.kv_num.sum().item())
+        nbk = dec.pos // c4.block
+        dbytes = c4.Hkv * nbk * 2 * c4.d * 4 + kvn * c4.block * c4.d * 2 * 2
+        result["decode"] = {
+            "workload": "C4: routed decode step, bf16, 14q/2kv, d=64, KV cache 1,048,576 tokens "
+                        "(+ appended steps), block 128, top_c 64 + last 2 blocks, beta 2",
+            "ms_per_step": dms, "steps": args.decode_steps,
+            "bytes_per_step": dbytes, "achieved_gbs": dbytes / (dms / 1e3) / 1e9,
+            "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
+        }
+        del kd, vd, qd, dec
+
+    if args.calibrate_copy:
+        x = torch.empty(128 * 1024 * 1024, device=dev, dtype=torch.bfloat16)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = x.numel() * 2
+
+    if not args.no_cpu:
+        threads = len(os.sched_getaffinity(0))
+        try:
+            from threadpoolctl import threadpool_info
+            nt = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+            if nt:
+                threads = int(max(nt))
+        except Exception:
+            pass
+        log(f"bench: CPU baseline on {threads} threads")
+        result["cpu_baseline"] = cpu_baseline(p, sum_kv, threads)
+        try:
+            model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                         if l.startswith("model name"))
+            result["cpu_baseline"]["cpu_model"] = model
+        except Exception:
+            pass
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

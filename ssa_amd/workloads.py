@@ -105,8 +105,9 @@ def _gmm_keys(rng, Hkv, n, d, ncomp=256, std=0.3, run=32, literal=False):
 
 def make(name: str, variant: str = "segmented", n: int | None = None):
     """Host inputs of configuration `name` (C1-C4): dict with q, k, v float32 arrays already
-    rounded to the config dtype, the Config, and the planted needles. `n` truncates the sequence
-    (the generator draws the full-length tensors' prefix; used for reduced parity cases)."""
+    rounded to the config dtype, the Config, and the planted needles. `n` overrides the sequence
+    length: a smaller instance drawn the same way (not a prefix of the full-length draw), used for
+    reduced parity cases."""
     cfg = CONFIGS[name]
     rng = np.random.default_rng(cfg.seed)
     N = cfg.n if n is None else n
@@ -164,3 +165,32 @@ def make_c5_device(device="cuda", n: int | None = None):
         v[0, 0, p, j % cfg.d] = 1.0
         rec.append((0, 0, t, p))
     return {"cfg": cfg, "q": q, "k": k, "v": v, "needles": np.array(rec, dtype=np.int64)}
+
+
+def make_decode(n_cache: int | None = None, steps: int = 64):
+    """C4 decode inputs: a KV prefix of n_cache tokens (K from the segmented Gaussian mixture,
+    V ~ N(0,1), 8 needles per key head planted for the decode queries) plus `steps` tokens to
+    append, and one query per step per query head. Drawn from default_rng(seed 3) in its own
+    order (only the decoded queries are generated), so it is a different draw than make("C4")."""
+    cfg = C4
+    n = cfg.n if n_cache is None else n_cache
+    total = n + steps
+    rng = np.random.default_rng(cfg.seed)
+    k = _gmm_keys(rng, cfg.Hkv, total, cfg.d)
+    v = _normal(rng, (1, cfg.Hkv, total, cfg.d))
+    q = _normal(rng, (1, cfg.Hq, steps, cfg.d))
+    G = cfg.Hq // cfg.Hkv
+    rec = []
+    for kvh in range(cfg.Hkv):
+        for j in range(8):
+            qh = kvh * G + int(rng.integers(G))
+            t = int(rng.integers(steps))
+            p = int(rng.integers(0, n - 2 * cfg.block))
+            qt = q[0, qh, t]
+            k[0, kvh, p] = 4.0 * qt / np.linalg.norm(qt)
+            v[0, kvh, p] = 0.0
+            v[0, kvh, p, j] = 1.0
+            rec.append((kvh, qh, n + t, p))
+    q, k, v = (round_to(x, cfg.dtype) for x in (q, k, v))
+    return {"cfg": cfg, "n_cache": n, "steps": steps, "q": q, "k": k, "v": v,
+            "needles": np.array(rec, dtype=np.int64)}
