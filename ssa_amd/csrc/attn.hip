@@ -31,6 +31,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleSlack = 8.0f;
 
 struct AttnParams {
   const char* q;
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict
 }
 
 template <int DT, int NW, int KT>
-__global__ __launch_bounds__(NW * 64) void sparse_attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
   constexpr int QT = 32 * NW;
@@ -301,16 +302,19 @@ __global__ __launch_bounds__(NW * 64) void sparse_attn_mfma_kernel(AttnParams p)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx * c2);
-    const bool grew = m_new > m_run;
+    // Lazy rescale: the running max is only raised when a row's max exceeds it by more than
+    // kRescaleSlack (log2 units); otherwise the stale max is kept, so p <= 2^kRescaleSlack.
+    // Numerator and denominator share the same max, so the result is unchanged.
+    const float m_cand = mx * c2;
+    const bool grew = m_cand > m_run + kRescaleSlack;
     if (__any(grew)) {
-      const float alpha = grew ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      const float alpha = grew ? __builtin_amdgcn_exp2f(m_run - m_cand) : 1.0f;
       l_part *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = m_new;
+      m_run = grew ? m_cand : m_run;
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     // ---- P^T (registers) and O^T += V^T P^T ----
