@@ -11,10 +11,12 @@
 //   online softmax in fp32 (exp2 with scale*log2e folded into one FMA; O is rescaled only when
 //                 some row's running max grows, a wave-uniform branch),
 //   O^T += V^T P^T on MFMA: A = V^T rows (LDS), B = P^T (registers, bf16/fp16).
-// K and V^T sub-tiles are double-buffered in LDS with XOR-swizzled 16-byte chunks (conflict-free
-// ds_read_b128 for both 32- and 64-bank LDS); the next sub-tile's global loads are issued before
-// the current one is computed. V is transposed once per call into the workspace so V^T sub-tiles
-// are contiguous 16-byte runs of keys.
+// K and V^T sub-tiles are double-buffered in LDS with rows padded by 16 bytes (so the 16-byte
+// operand reads of 16 consecutive lanes hit distinct banks and every LDS address is a per-lane
+// base plus an immediate); the next sub-tile's global loads are issued before the current one is
+// computed, from a uniform sub-tile base plus one 32-bit per-thread offset. V is transposed once
+// per call into the workspace so V^T sub-tiles are contiguous 16-byte runs of keys. Row sums of
+// the rounded P use v_dot2 against ones (4 instructions per 8 values).
 // Workgroups are dispatched heaviest query blocks first, and the query heads sharing a key head
 // for the same query block are placed on the same XCD (shared local-window tiles hit its L2).
 //
@@ -61,16 +63,6 @@ __device__ inline int64_t logical_id(int64_t pid, int64_t group) {
 // Permutation of a 32-key group: MFMA row m loads key sigma(m) (bits 2 and 3 swapped).
 __device__ inline int sigma32(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-// XOR swizzles of 16-byte chunk indices (see the file comment).
-__device__ inline int swz_k(int row) {
-  return (((row ^ (row >> 2)) & 1) << 2) | (((row >> 3) & 1) << 1) | ((row >> 1) & 1);
-}
-template <int KT>
-__device__ inline int swz_v(int row) {
-  if constexpr (KT == 128) return row & 15;
-  else return ((row >> 1) & 7) ^ ((row & 1) << 2);
-}
-
 template <int DT>
 struct Mfma;
 template <>
@@ -91,6 +83,18 @@ struct Mfma<SSA_BF16> {
     unsigned short hi = __builtin_bit_cast(unsigned short, (__bf16)b);
     return (unsigned int)lo | ((unsigned int)hi << 16);
   }
+  // acc + sum of the 8 packed values, on v_dot2_f32_bf16 against ones
+  static __device__ inline float rowsum(const vec& v, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    const u32x4 w = __builtin_bit_cast(u32x4, v);
+    const v2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned int wi = w[i];  // (bit_cast of a vector-element subscript mis-lowers)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, wi), one, acc, false);
+    }
+    return acc;
+  }
 };
 template <>
 struct Mfma<SSA_F16> {
@@ -109,6 +113,18 @@ struct Mfma<SSA_F16> {
     unsigned short lo = __builtin_bit_cast(unsigned short, (_Float16)a);
     unsigned short hi = __builtin_bit_cast(unsigned short, (_Float16)b);
     return (unsigned int)lo | ((unsigned int)hi << 16);
+  }
+  // acc + sum of the 8 packed values, on v_dot2_f32_f16 against ones
+  static __device__ inline float rowsum(const vec& v, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    const u32x4 w = __builtin_bit_cast(u32x4, v);
+    const v2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned int wi = w[i];
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, wi), one, acc, false);
+    }
+    return acc;
   }
 };
 
@@ -154,13 +170,18 @@ template <int DT, int NW, int KT>
 __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
-  constexpr int QT = 32 * NW;
-  constexpr int NT = NW * 64;
-  constexpr int KBYTES = KT * 128;  // K sub-tile: KT rows x 64 halves
-  constexpr int VBYTES = KT * 128;  // V^T sub-tile: 64 rows x KT halves
-  constexpr int CHUNKS = KT * 8 / NT;  // 16-byte chunks per thread per operand
-  constexpr int NST = KT / 32;         // 32-key groups per sub-tile
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * (KBYTES + VBYTES)];
+  constexpr int QT = 32 * NW;           // query rows per workgroup
+  constexpr int NT = NW * 64;           // threads
+  constexpr int KROW = 64 * 2 + 16;     // LDS pitch of a K row (64 halves + 16 B pad)
+  constexpr int VROW = KT * 2 + 16;     // LDS pitch of a V^T row (KT halves + 16 B pad)
+  constexpr int KBYTES = KT * KROW;
+  constexpr int VBYTES = 64 * VROW;
+  constexpr int BUF = KBYTES + VBYTES;
+  constexpr int CHUNKS = KT * 8 / NT;   // 16-byte chunks per thread per operand per sub-tile
+  constexpr int NST = KT / 32;          // 32-key groups per sub-tile
+  constexpr int KSTEP = NT / 8;         // K rows covered by one chunk round
+  constexpr int VSTEP = NT / (KT / 8);  // V^T rows covered by one chunk round
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF];
 
   const int64_t L0 = logical_id(blockIdx.x, p.group);
   if (L0 >= p.total) return;
@@ -211,6 +232,19 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
   const unsigned short* vtbase =
       reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
 
+  // Per-thread load plan: chunk j of a sub-tile is K row (tid>>3) + j*KSTEP, 16-byte chunk tid&7,
+  // and V^T row tid/(KT/8) + j*VSTEP, chunk tid%(KT/8). Only the sub-tile base changes per tile
+  // (a uniform pointer), so the loop carries one 32-bit offset per operand.
+  const int kr0 = tid >> 3, kc0 = tid & 7;
+  const int vr0 = tid / (KT / 8), vc0 = tid % (KT / 8);
+  const uint32_t kgo = (uint32_t)(kr0 * p.ksn + kc0 * 8);
+  const uint32_t vgo = (uint32_t)(vr0 * p.n_pad + vc0 * 8);
+  const uint32_t klo = (uint32_t)(kr0 * KROW + kc0 * 16);
+  const uint32_t vlo = (uint32_t)(KBYTES + vr0 * VROW + vc0 * 16);
+  // Per-lane LDS read bases (MFMA A operands); every other offset is an immediate.
+  const uint32_t krd = (uint32_t)(sigma32(col) * KROW + half * 16);
+  const uint32_t vrd = (uint32_t)(KBYTES + col * VROW + half * 16);
+
   auto tile_key0 = [&](int t) -> int64_t {
     const int32_t c = list[t / S];
     if (c < 0 || (int64_t)c >= p.nbq) return -1;
@@ -226,26 +260,32 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
 
   u32x4 kreg[CHUNKS], vreg[CHUNKS];
   auto load_tile = [&](int64_t key0) {
+    const unsigned short* kt = kbase + key0 * p.ksn;
+    const unsigned short* vt = vtbase + key0;
+    if (key0 + KT <= p.n) {
 #pragma unroll
-    for (int j = 0; j < CHUNKS; ++j) {
-      const int qq = tid + j * NT;
-      const int kr = qq >> 3, kc = qq & 7;
-      u32x4 z = {0u, 0u, 0u, 0u};
-      kreg[j] = (key0 + kr < p.n) ? *reinterpret_cast<const u32x4*>(kbase + (key0 + kr) * p.ksn + kc * 8) : z;
-      const int vr = qq / (KT / 8), vc = qq % (KT / 8);
-      vreg[j] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)vr * p.n_pad + key0 + vc * 8);
+      for (int j = 0; j < CHUNKS; ++j)
+        kreg[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)j * KSTEP * p.ksn + kgo);
+    } else {  // ragged last sub-tile: rows >= n are zero
+      const int64_t nvalid = p.n - key0;
+#pragma unroll
+      for (int j = 0; j < CHUNKS; ++j) {
+        u32x4 z = {0u, 0u, 0u, 0u};
+        kreg[j] = kr0 + j * KSTEP < nvalid
+                      ? *reinterpret_cast<const u32x4*>(kt + (int64_t)j * KSTEP * p.ksn + kgo)
+                      : z;
+      }
     }
+#pragma unroll
+    for (int j = 0; j < CHUNKS; ++j)
+      vreg[j] = *reinterpret_cast<const u32x4*>(vt + (int64_t)j * VSTEP * p.n_pad + vgo);
   };
   auto store_tile = [&](int buf) {
-    unsigned char* kb = smem + buf * (KBYTES + VBYTES);
-    unsigned char* vb = kb + KBYTES;
+    unsigned char* base = smem + buf * BUF;
 #pragma unroll
     for (int j = 0; j < CHUNKS; ++j) {
-      const int qq = tid + j * NT;
-      const int kr = qq >> 3, kc = qq & 7;
-      *reinterpret_cast<u32x4*>(kb + kr * 128 + ((kc ^ swz_k(kr)) << 4)) = kreg[j];
-      const int vr = qq / (KT / 8), vc = qq % (KT / 8);
-      *reinterpret_cast<u32x4*>(vb + vr * (KT * 2) + ((vc ^ swz_v<KT>(vr)) << 4)) = vreg[j];
+      *reinterpret_cast<u32x4*>(base + klo + j * KSTEP * KROW) = kreg[j];
+      *reinterpret_cast<u32x4*>(base + vlo + j * VSTEP * VROW) = vreg[j];
     }
   };
 
@@ -268,31 +308,31 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
     const int64_t key0n = tn < T ? tile_key0(tn) : 0;
     if (tn < T) load_tile(key0n);
 
-    const unsigned char* kb = smem + buf * (KBYTES + VBYTES);
-    const unsigned char* vb = kb + KBYTES;
+    const unsigned char* kb = smem + buf * BUF + krd;
+    const unsigned char* vb = smem + buf * BUF + vrd;
     // ---- S^T = K Q^T ----
     f32x16 sacc[NST];
 #pragma unroll
     for (int tt = 0; tt < NST; ++tt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[tt][r] = 0.0f;
-      const int kr = tt * 32 + sigma32(col);
-      const int sw = swz_k(kr);
 #pragma unroll
       for (int kd = 0; kd < 4; ++kd) {
-        const int ch = 2 * kd + half;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(kb + kr * 128 + ((ch ^ sw) << 4));
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kb + tt * 32 * KROW + kd * 32);
         sacc[tt] = M::mma(M::from_bits(a), qf[kd], sacc[tt]);
       }
     }
     // ---- mask (diagonal / ragged tail sub-tiles only) ----
     if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
+      const int lim_q = (int)(qpos - key0);    // keys j <= qpos  <=>  local key <= lim_q
+      const int lim_n = (int)(p.n - 1 - key0);  // keys j < n
+      const int lim = lim_q < lim_n ? lim_q : lim_n;
 #pragma unroll
       for (int tt = 0; tt < NST; ++tt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t key = key0 + tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
-          if (key > qpos || key >= p.n) sacc[tt][r] = -INFINITY;
+          const int key = tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
+          if (key > lim) sacc[tt][r] = -INFINITY;
         }
     }
     // ---- online softmax ----
@@ -317,24 +357,20 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
       m_run = grew ? m_cand : m_run;
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    // ---- P^T (registers) and O^T += V^T P^T ----
+    // ---- P^T (registers) and O^T += V^T P^T; row sums of the rounded P on v_dot2 ----
 #pragma unroll
     for (int tt = 0; tt < NST; ++tt) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float pv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; ++j)
           pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[tt][8 * s + j], c2, -m_use));
-          l_part += pv[j];
-        }
         const vec pb = M::pack(pv);
+        l_part = M::rowsum(pb, l_part);
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt) {
-          const int vr = dt * 32 + col;
-          const int ch = 4 * tt + 2 * s + half;
-          const u32x4 a =
-              *reinterpret_cast<const u32x4*>(vb + vr * (KT * 2) + ((ch ^ swz_v<KT>(vr)) << 4));
+          const u32x4 a = *reinterpret_cast<const u32x4*>(vb + dt * 32 * VROW + (4 * tt + 2 * s) * 16);
           oacc[dt] = M::mma(M::from_bits(a), pb, oacc[dt]);
         }
       }
