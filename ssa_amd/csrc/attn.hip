@@ -166,6 +166,17 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict
   }
 }
 
+// Max / sum of a value with its partner lane (lane ^ 32) without an LDS round trip:
+// permlane32_swap(x, x) returns {x of lanes 0-31 (both halves), x of lanes 32-63 (both halves)}.
+__device__ inline float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int DT, int NW, int KT>
 __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams p) {
   using M = Mfma<DT>;
@@ -310,7 +321,9 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
 
     const unsigned char* kb = smem + buf * BUF + krd;
     const unsigned char* vb = smem + buf * BUF + vrd;
-    // ---- S^T = K Q^T ----
+    // ---- S^T = K Q^T (raised wave priority over the MFMA phases, so the matrix stream of one
+    // wave is not starved while the other wave on the SIMD runs softmax VALU work) ----
+    __builtin_amdgcn_s_setprio(1);
     f32x16 sacc[NST];
 #pragma unroll
     for (int tt = 0; tt < NST; ++tt) {
@@ -322,6 +335,7 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
         sacc[tt] = M::mma(M::from_bits(a), qf[kd], sacc[tt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---- mask (diagonal / ragged tail sub-tiles only) ----
     if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
       const int lim_q = (int)(qpos - key0);    // keys j <= qpos  <=>  local key <= lim_q
@@ -341,7 +355,7 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
     for (int tt = 0; tt < NST; ++tt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = pair_max(mx);
     // Lazy rescale: the running max is only raised when a row's max exceeds it by more than
     // kRescaleSlack (log2 units); otherwise the stale max is kept, so p <= 2^kRescaleSlack.
     // Numerator and denominator share the same max, so the result is unchanged.
@@ -358,6 +372,7 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     // ---- P^T (registers) and O^T += V^T P^T; row sums of the rounded P on v_dot2 ----
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int tt = 0; tt < NST; ++tt) {
 #pragma unroll
@@ -375,13 +390,14 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     buf ^= 1;
     t = tn;
     key0 = key0n;
   }
 
   // ---- epilogue: O = O^T / l ----
-  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float l_tot = pair_sum(l_part);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (qpos < p.n) {
     unsigned short* op =
