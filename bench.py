@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
     ap.add_argument("--no-decode", action="store_true", help="skip the C4 decode step")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 12M-token prefill")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC byte-count calibration)")
     return ap.parse_args()
@@ -261,6 +262,39 @@ def main():
             "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
         }
         del kd, vd, qd, dec
+
+    if not args.no_c5:
+        log("bench: C5 12M-token prefill")
+        del q, k, v
+        torch.cuda.empty_cache()
+        d5 = WL.make_c5_device(dev)
+        c5 = d5["cfg"]
+        q5, k5, v5 = d5["q"], d5["k"], d5["v"]
+        t5 = Timer(torch)
+        for rep in range(4):
+            tmr = t5 if rep else Timer(torch)
+            qb5 = tmr.run("summaries", K.block_summary, q5, c5.block, "qmean")
+            mu5, var5, _ = tmr.run("summaries_k", K.block_summary, k5, c5.block, "pop")
+            kn5, ki5 = tmr.run("route", K.route, qb5, mu5, var5, None, "budget", c5.top_c, 0.0,
+                               c5.local, 0.5 * c5.beta)
+            vt5 = tmr.run("transpose_v", K.transpose_v, v5, c5.block)
+            tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block, vt=vt5)
+        torch.cuda.synchronize()
+        router = t5.mean_ms("summaries") + t5.mean_ms("summaries_k") + t5.mean_ms("route")
+        attn = t5.mean_ms("transpose_v") + t5.mean_ms("attention")
+        kv5 = int(kn5.sum().item())
+        result["c5"] = {
+            "workload": "C5: single-head causal routed prefill, fp16, d=64, n=12,582,912, block 256 "
+                        "(49152 blocks), top_c 64 + local 1, beta 2; inputs seeded on the device",
+            "router_ms": router, "attention_ms": attn, "total_ms": router + attn,
+            "tokens_per_s": c5.n / ((router + attn) / 1e3),
+            "summaries_ms": t5.mean_ms("summaries") + t5.mean_ms("summaries_k"),
+            "route_ms": t5.mean_ms("route"), "attention_kernel_ms": t5.mean_ms("attention"),
+            "attention_tflops": 4.0 * c5.block * c5.block * c5.d * kv5 / (t5.mean_ms("attention") / 1e3) / 1e12,
+            "sum_kv_num": kv5,
+        }
+        del q5, k5, v5, d5, vt5
+        torch.cuda.empty_cache()
 
     if args.calibrate_copy:
         x = torch.empty(128 * 1024 * 1024, device=dev, dtype=torch.bfloat16)

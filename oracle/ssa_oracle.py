@@ -158,21 +158,29 @@ def select_rows(r: np.ndarray, mode: str, top_c, budget_frac: float, local: int,
     keys = score_keys(r)
     out = np.empty((B, Hq, R), dtype=object)
     for i in range(R):
-        cmax, keep, own = row_geometry(mode, i, nbk, top_c, budget_frac, query_pos, block)
-        k = min(keep, cmax)
-        lo, hi = max(0, own - local), min(own, nbk - 1)
-        loc = set(range(lo, hi + 1))
         for b in range(B):
             for h in range(Hq):
-                if k >= cmax:
-                    pick = set(range(cmax))
-                elif k > 0:
-                    order = np.argsort(-keys[b, h, i, :cmax].astype(np.int64), kind="stable")
-                    pick = set(order[:k].tolist())
-                else:
-                    pick = set()
-                out[b, h, i] = sorted(pick | loc)
+                out[b, h, i] = select_row(keys[b, h, i], i, mode, top_c, budget_frac, local,
+                                          query_pos, block)
     return out
+
+
+def select_row(keys: np.ndarray, i: int, mode: str, top_c, budget_frac: float, local: int,
+               query_pos: int = 0, block: int = 1) -> list:
+    """Selection of the single row i from its score keys (nbk,) (score_keys of the fp32 scores),
+    with the geometry of row_geometry; the per-row body of select_rows."""
+    nbk = keys.shape[0]
+    cmax, keep, own = row_geometry(mode, i, nbk, top_c, budget_frac, query_pos, block)
+    k = min(keep, cmax)
+    lo, hi = max(0, own - local), min(own, nbk - 1)
+    if k >= cmax:
+        pick = set(range(cmax))
+    elif k > 0:
+        order = np.argsort(-keys[:cmax].astype(np.int64), kind="stable")
+        pick = set(order[:k].tolist())
+    else:
+        pick = set()
+    return sorted(pick | set(range(lo, hi + 1)))
 
 
 def compact(sel_lists, W: int | None = None):

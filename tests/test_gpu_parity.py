@@ -235,6 +235,69 @@ def test_no_future_leak(cuda):
     assert torch.equal(o1[:, :, :cut + 1], o2[:, :, :cut + 1])
 
 
+def test_c5_full_length_properties_and_sampled_rows(cuda):
+    """C5 at its full 12.6M-token length (49152 blocks of 256, fp16): list structure for every
+    row, summaries of sampled blocks, the selections of sampled rows recomputed by the oracle from
+    the device summaries, and the attention of sampled query blocks against the oracle on the
+    gathered blocks (only the diagonal block is masked, so the gathered blocks keep the
+    geometry)."""
+    d5 = WL.make_c5_device(cuda)
+    c5 = d5["cfg"]
+    q, k, v = d5["q"], d5["k"], d5["v"]
+    blk, nb, T = c5.block, c5.nb, c5.top_c
+    qbar = K.block_summary(q, blk, "qmean")
+    mu, var, _ = K.block_summary(k, blk, "pop")
+    kv_num, kv_idx = K.route(qbar, mu, var, None, "budget", T, 0.0, c5.local, 0.5 * c5.beta)
+    out = K.sparse_attention(q, k, v, kv_num, kv_idx, blk)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+
+    num = kv_num[0, 0].long()
+    idx = kv_idx[0, 0].long()
+    i = torch.arange(nb, device=cuda)
+    # rows i <= top_c keep every earlier block; later rows keep top_c of them plus i-1 and i
+    assert torch.equal(num[:T + 1], i[:T + 1] + 1)
+    assert bool(((num[T + 1:] >= T + 1) & (num[T + 1:] <= T + 2)).all())
+    j = torch.arange(idx.shape[1], device=cuda)
+    valid = j[None, :] < num[:, None]
+    assert bool((idx.gather(1, (num - 1)[:, None])[:, 0] == i).all())
+    assert bool((idx.gather(1, (num - 2).clamp(min=0)[:, None])[1:, 0] == i[1:] - 1).all())
+    inc = (idx[:, 1:] > idx[:, :-1]) | ~valid[:, 1:]
+    assert bool(inc.all())
+    assert bool(((idx >= 0) & ((idx <= i[:, None]) | ~valid)).all())
+
+    rows = sorted({0, 1, 63, 64, 65, 66, 1000, 9999, 30000, nb - 2, nb - 1}
+                  | set(np.random.default_rng(5).integers(0, nb, 16).tolist()))
+    # summaries of the sampled blocks against the oracle (within 1 ulp)
+    for c in rows[:6] + rows[-3:]:
+        sl = slice(c * blk, (c + 1) * blk)
+        kb, qb = np_of(k[:, :, sl]), np_of(q[:, :, sl])
+        m_o, v_o, _ = O.block_stats(kb, blk, "pop")
+        assert ulp_diff(np_of(mu[:, :, c:c + 1]), m_o).max() <= 1
+        assert ulp_diff(np_of(var[:, :, c:c + 1]), v_o).max() <= 1
+        assert ulp_diff(np_of(qbar[:, :, c:c + 1]), O.qmean(qb, blk)).max() <= 1
+
+    mu_h, var_h, qbar_h = np_of(mu), np_of(var), np_of(qbar)
+    num_h, idx_h = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    for r in rows:
+        sc = O.scores(qbar_h[:, :, r:r + 1], mu_h, var_h, 0.5 * c5.beta)
+        sel = O.select_row(O.score_keys(sc)[0, 0, 0], r, "budget", T, 0.0, c5.local)
+        assert idx_h[0, 0, r, :num_h[0, 0, r]].tolist() == sel, r
+
+    for r in (0, 65, nb // 2, nb - 1):
+        ids = idx_h[0, 0, r, :num_h[0, 0, r]].tolist()
+        gk = np.concatenate([np_of(k[:, :, c * blk:(c + 1) * blk]) for c in ids], axis=2)
+        gv = np.concatenate([np_of(v[:, :, c * blk:(c + 1) * blk]) for c in ids], axis=2)
+        gq = np.zeros_like(gk)
+        gq[:, :, -blk:] = np_of(q[:, :, r * blk:(r + 1) * blk])
+        m = len(ids)
+        gnum = np.array([[[m] * m]], dtype=np.int32)
+        gidx = np.broadcast_to(np.arange(m, dtype=np.int32), (1, 1, m, m)).copy()
+        ref = O.sparse_attention(gq, gk, gv, gnum, gidx, blk, qblocks=[m - 1])
+        err = np.abs(np_of(out[:, :, r * blk:(r + 1) * blk]) - ref[:, :, -blk:]).max()
+        assert err < TOL[c5.dtype], (r, err)
+
+
 # ---- a10-a12 decode ----------------------------------------------------------------------------
 
 def test_decode_attend_matches_oracle_and_prefill_row(cuda):
