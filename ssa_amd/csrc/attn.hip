@@ -1,24 +1,28 @@
 // Block-sparse causal flash attention (prefill) for gfx950.
 //
-// bf16/fp16 path (d = 64): a workgroup owns QT = 32*NW query rows of one query block of one
-// query head and walks that block's selected key blocks in KT-key sub-tiles. Each wave owns 32
-// query rows. Per sub-tile:
-//   S^T = K Q^T   on v_mfma_f32_32x32x16_{bf16,f16}: A = K rows (from LDS), B = the wave's Q
+// bf16/fp16 path (d = 64), two kernels sharing one MFMA scheme:
+//   S^T = K Q^T   on v_mfma_f32_32x32x16_{bf16,f16}: A = K rows (from LDS), B = a wave's Q
 //                 fragment (registers, loaded once). The K rows fed to MFMA row m are permuted
 //                 (bits 2 and 3 of m swapped) so that each lane's 16 accumulators of a 32-key
 //                 tile hold two runs of 8 consecutive keys -- exactly the B-operand layout of
 //                 the next product, so P never leaves registers.
-//   online softmax in fp32 (exp2 with scale*log2e folded into one FMA; O is rescaled only when
-//                 some row's running max grows, a wave-uniform branch),
+//   online softmax in fp32 (exp2 with scale*log2e folded into one FMA; lazy rescale: the running
+//                 max only moves when a row's max exceeds it by more than 2^8),
 //   O^T += V^T P^T on MFMA: A = V^T rows (LDS), B = P^T (registers, bf16/fp16).
-// K and V^T sub-tiles are double-buffered in LDS with rows padded by 16 bytes (so the 16-byte
-// operand reads of 16 consecutive lanes hit distinct banks and every LDS address is a per-lane
-// base plus an immediate); the next sub-tile's global loads are issued before the current one is
-// computed, from a uniform sub-tile base plus one 32-bit per-thread offset. V is transposed once
-// per call into the workspace so V^T sub-tiles are contiguous 16-byte runs of keys. Row sums of
-// the rounded P use v_dot2 against ones (4 instructions per 8 values).
-// Workgroups are dispatched heaviest query blocks first, and the query heads sharing a key head
-// for the same query block are placed on the same XCD (shared local-window tiles hit its L2).
+// * sparse_attn_w64_kernel (block a multiple of 128): a wave owns 64 query rows (two 32-column
+//   MFMA groups, so every LDS operand fragment feeds two MFMAs); a workgroup = 2 waves = 128
+//   rows of one query block, walking its selected key blocks in 64-key sub-tiles. K and V^T
+//   sub-tiles go HBM -> LDS directly (global_load_lds_dwordx4, no staging registers) into a
+//   2-stage ring with an XOR swizzle (chunk c of row r at c ^ ((r >> 1) & 7)): the 16 lanes of
+//   one ds_read_b128 phase hit all 64 banks once.
+// * sparse_attn_mfma_kernel (block 64): a wave owns 32 query rows, a workgroup 2 waves = one
+//   query block; sub-tiles staged through registers into LDS rows padded by 16 bytes.
+// V is transposed once per call into the workspace so V^T sub-tiles are contiguous 16-byte runs
+// of keys. Row sums of the rounded P use v_dot2 against ones. Row max / sum across the two
+// 32-lane halves use v_permlane32_swap. Each wave's block list is held in a register window
+// read with v_readlane. Workgroups are dispatched heaviest query blocks first, and the query
+// heads sharing a key head for the same query block are placed on the same XCD (their shared
+// tiles hit its L2).
 //
 // fp32 path: a single-wave VALU kernel (one query row per lane), K/V sub-tiles of 64 keys in LDS.
 //
@@ -256,8 +260,17 @@ __global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams
   const uint32_t krd = (uint32_t)(sigma32(col) * KROW + half * 16);
   const uint32_t vrd = (uint32_t)(KBYTES + col * VROW + half * 16);
 
+  // The row's block list, 64 entries at a time in one VGPR (entry lbase + e in lane e), read
+  // with v_readlane: no memory wait per sub-tile.
+  int lbase = 0;
+  int32_t lreg = lane < cnt ? list[lane] : -1;
   auto tile_key0 = [&](int t) -> int64_t {
-    const int32_t c = list[t / S];
+    const int e = t / S;
+    if (e - lbase >= 64) {  // wave-uniform; once per 64 list entries
+      lbase = e;
+      lreg = e + lane < cnt ? list[e + lane] : -1;
+    }
+    const int32_t c = __builtin_amdgcn_readlane(lreg, e - lbase);
     if (c < 0 || (int64_t)c >= p.nbq) return -1;
     return (int64_t)c * p.block + (int64_t)(t % S) * KT;
   };
@@ -519,6 +532,296 @@ __global__ __launch_bounds__(64) void sparse_attn_f32_kernel(AttnParams p) {
   }
 }
 
+// 16-byte chunk c of LDS tile row r is stored at chunk c ^ swz(r): the 16 lanes served together
+// by one ds_read_b128 of an MFMA operand (16 distinct rows) then hit all 64 banks once.
+__device__ inline int swz(int r) { return (r >> 1) & 7; }
+
+// Wave tile of 64 query rows (two 32-column MFMA groups) against 64-key sub-tiles: every LDS
+// operand fragment feeds two MFMAs. A workgroup = 2 waves = 128 query rows of one query block.
+// K and V^T sub-tiles (64 rows x 128 B each, swizzled) go HBM -> LDS directly
+// (global_load_lds_dwordx4, no staging registers) into a 2-stage ring, one barrier per sub-tile.
+template <int DT>
+__global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
+  using M = Mfma<DT>;
+  typedef typename M::vec vec;
+  constexpr int KT = 64;
+  constexpr int TILE = KT * 128;  // bytes of one K or V^T sub-tile
+  __shared__ __attribute__((aligned(1024))) unsigned char kst0[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char vst0[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char kst1[TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char vst1[TILE];
+
+  const int64_t L0 = logical_id(blockIdx.x, p.group);
+  if (L0 >= p.total) return;
+  int64_t L = L0;
+  const int64_t qs = L % p.qsub;
+  L /= p.qsub;
+  const int64_t hg = L % p.G;
+  L /= p.G;
+  const int64_t kvh = L % p.Hkv;
+  L /= p.Hkv;
+  const int64_t b = L % p.B;
+  L /= p.B;
+  const int64_t i = p.nbq - 1 - L;
+  const int64_t h = kvh * p.G + hg;
+
+  const int64_t q0 = i * p.block + qs * 128;
+  if (q0 >= p.n) return;
+  const int64_t qmax = q0 + 127 < p.n - 1 ? q0 + 127 : p.n - 1;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, col = lane & 31;
+  const int64_t qw0 = q0 + w * 64;
+  const int64_t qpos0 = qw0 + col, qpos1 = qw0 + 32 + col;
+
+  const int64_t row = (b * p.Hq + h) * p.nbq + i;
+  int cnt = p.kv_num[row];
+  if (cnt > p.W) cnt = (int)p.W;
+  if (cnt < 0) cnt = 0;
+  const int32_t* list = p.kv_idx + row * p.W;
+  const int S = (int)(p.block / KT);
+  const int T = cnt * S;
+
+  // Q fragments (B operands of S^T = K Q^T) of the two column groups
+  vec qf[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int64_t qp = c ? qpos1 : qpos0;
+    const unsigned short* src = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
+                                h * p.qsh + qp * p.qsn + half * 8;
+#pragma unroll
+    for (int kd = 0; kd < 4; ++kd) {
+      u32x4 wv = {0u, 0u, 0u, 0u};
+      if (qp < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
+      qf[c][kd] = M::from_bits(wv);
+    }
+  }
+
+  const unsigned short* kbase =
+      reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
+  const unsigned short* vtbase =
+      reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
+
+  // Load plan: instruction j of wave w fills tile rows j*16 + w*8 + [0,8); lane -> row
+  // lr = w*8 + lane/8 (+ j*16), physical chunk lane%8 = logical chunk lc ^ swz(row).
+  const int lr = w * 8 + (lane >> 3);
+  const int lc = (lane & 7) ^ swz(lr);
+  const uint32_t kgo = (uint32_t)(lr * p.ksn + lc * 8);
+  const uint32_t vgo = (uint32_t)(lr * p.n_pad + lc * 8);
+  const int64_t kstep = 16 * p.ksn, vstep = 16 * p.n_pad;
+
+  // The row's block list, 64 entries at a time in one VGPR (entry lbase + e in lane e), read
+  // with v_readlane: no memory wait per sub-tile.
+  int lbase = 0;
+  int32_t lreg = lane < cnt ? list[lane] : -1;
+  auto tile_key0 = [&](int t) -> int64_t {
+    const int e = t / S;
+    if (e - lbase >= 64) {  // wave-uniform; once per 64 list entries
+      lbase = e;
+      lreg = e + lane < cnt ? list[e + lane] : -1;
+    }
+    const int32_t c = __builtin_amdgcn_readlane(lreg, e - lbase);
+    if (c < 0 || (int64_t)c >= p.nbq) return -1;
+    return (int64_t)c * p.block + (int64_t)(t % S) * KT;
+  };
+  auto next_valid = [&](int t) -> int {
+    for (; t < T; ++t) {
+      const int64_t k0 = tile_key0(t);
+      if (k0 >= 0 && k0 <= qmax && k0 < p.n) break;
+    }
+    return t;
+  };
+  auto issue = [&](unsigned char* kdst, unsigned char* vdst, int64_t key0) {
+    const unsigned short* kt = kbase + key0 * p.ksn;
+    const unsigned short* vt = vtbase + key0;
+    if (key0 + KT <= p.n) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(kt + j * kstep + kgo, kdst + j * 2048 + w * 1024, 16, 0, 0);
+    } else {  // ragged tail: rows >= n re-read row n-1 (their scores are masked)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int64_t r = key0 + j * 16 + lr;
+        if (r > p.n - 1) r = p.n - 1;
+        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lc * 8, kdst + j * 2048 + w * 1024,
+                                         16, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(vt + j * vstep + vgo, vdst + j * 2048 + w * 1024, 16, 0, 0);
+  };
+
+  // per-lane LDS read offsets: K row tt*32 + sigma32(col), V^T row dt*32 + col; chunk
+  // (2*step + half) ^ swz(row); tt / dt add 4096 (an immediate).
+  const int krow = sigma32(col);
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    koff[s] = (uint32_t)(krow * 128 + (((2 * s + half) ^ swz(krow)) * 16));
+    voff[s] = (uint32_t)(col * 128 + (((2 * s + half) ^ swz(col)) * 16));
+  }
+
+  f32x16 oacc[2][2];  // [dt][c]
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[dt][c][r] = 0.0f;
+  float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.0f, 0.0f};
+  const float c2 = p.scale_log2;
+
+  auto compute = [&](const unsigned char* ks, const unsigned char* vs, int64_t key0) {
+    // ---- S^T = K Q^T ----
+    u32x4 ka[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int kd = 0; kd < 4; ++kd)
+        ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * 4096);
+    f32x16 sacc[2][2];  // [tt][c]
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[tt][c][r] = 0.0f;
+#pragma unroll
+        for (int kd = 0; kd < 4; ++kd)
+          sacc[tt][c] = M::mma(M::from_bits(ka[tt][kd]), qf[c][kd], sacc[tt][c]);
+      }
+    __builtin_amdgcn_s_setprio(0);
+    // V^T fragments of the first two key steps, in flight during the softmax
+    u32x4 va[4][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+        va[s][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s] + dt * 4096);
+    // ---- mask (diagonal / ragged tail sub-tiles only) ----
+    if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int lim_q = (int)((c ? qpos1 : qpos0) - key0);
+        const int lim_n = (int)(p.n - 1 - key0);
+        const int lim = lim_q < lim_n ? lim_q : lim_n;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
+            if (key > lim) sacc[tt][c][r] = -INFINITY;
+          }
+      }
+    }
+    // ---- online softmax (lazy rescale) ----
+    float m_use[2];
+    bool grew[2];
+    float m_cand[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][c][r]);
+      mx = pair_max(mx);
+      m_cand[c] = mx * c2;
+      grew[c] = m_cand[c] > m_run[c] + kRescaleSlack;
+    }
+    if (__any(grew[0] || grew[1])) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float alpha = grew[c] ? __builtin_amdgcn_exp2f(m_run[c] - m_cand[c]) : 1.0f;
+        l_part[c] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][c][r] *= alpha;
+        m_run[c] = grew[c] ? m_cand[c] : m_run[c];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) m_use[c] = m_run[c] == -INFINITY ? 0.0f : m_run[c];
+    // ---- P^T (registers) and O^T += V^T P^T ----
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < 2) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+          va[s + 2][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s + 2] + dt * 4096);
+      }
+      vec pb[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float pv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[s >> 1][c][8 * (s & 1) + j], c2, -m_use[c]));
+        pb[c] = M::pack(pv);
+        l_part[c] = M::rowsum(pb[c], l_part[c]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // 2-stage ring, statically unrolled by two so each LDS access names its stage's array.
+  int t = next_valid(0);
+  int64_t key0 = t < T ? tile_key0(t) : 0;
+  if (t < T) issue(kst0, vst0, key0);
+  while (t < T) {
+    __syncthreads();  // stage 0 landed for all waves; stage 1 no longer read
+    int tn = next_valid(t + 1);
+    int64_t key0n = tn < T ? tile_key0(tn) : 0;
+    if (tn < T) issue(kst1, vst1, key0n);
+    if (key0 <= qw0 + 63) compute(kst0, vst0, key0);
+    t = tn;
+    key0 = key0n;
+    if (t >= T) break;
+    __syncthreads();  // stage 1 landed; stage 0 no longer read
+    tn = next_valid(t + 1);
+    key0n = tn < T ? tile_key0(tn) : 0;
+    if (tn < T) issue(kst0, vst0, key0n);
+    if (key0 <= qw0 + 63) compute(kst1, vst1, key0);
+    t = tn;
+    key0 = key0n;
+  }
+
+  // ---- epilogue: O = O^T / l ----
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int64_t qpos = c ? qpos1 : qpos0;
+    const float l_tot = pair_sum(l_part[c]);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (qpos < p.n) {
+      unsigned short* op =
+          reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos * p.osn;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int d0 = dt * 32 + rg * 8 + half * 4;
+          uint2 wv;
+          wv.x = M::pack2(oacc[dt][c][4 * rg] * inv, oacc[dt][c][4 * rg + 1] * inv);
+          wv.y = M::pack2(oacc[dt][c][4 * rg + 2] * inv, oacc[dt][c][4 * rg + 3] * inv);
+          *reinterpret_cast<uint2*>(op + d0) = wv;
+        }
+      if (p.lse != nullptr && half == 0)
+        p.lse[(b * p.Hq + h) * p.n + qpos] =
+            l_tot > 0.0f ? (m_run[c] + log2f(l_tot)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
 template <int DT>
 int launch_mfma(AttnParams& p, hipStream_t stream) {
   const int64_t G = p.G;
@@ -535,7 +838,7 @@ int launch_mfma(AttnParams& p, hipStream_t stream) {
     p.total = p.nbq * p.B * p.Hkv * G * p.qsub;
     const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
     SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-    sparse_attn_mfma_kernel<DT, 4, 128><<<(unsigned)grid, 256, 0, stream>>>(p);
+    sparse_attn_w64_kernel<DT><<<(unsigned)grid, 128, 0, stream>>>(p);
   }
   return launch_status("sparse_attn_mfma_kernel");
 }
