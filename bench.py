@@ -197,7 +197,7 @@ def main():
                    "n": n, "Hq": cfg.Hq, "Hkv": cfg.Hkv, "d": cfg.d, "block": blk,
                    "top_c": cfg.top_c, "local": cfg.local, "beta": cfg.beta,
                    "variant": args.variant},
-        "roofline": {"bound": "mfma", "kernel": "sparse_attn_w64_kernel",
+        "roofline": {"bound": "mfma", "kernel": "sparse_attn_dma_kernel",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "flops_per_launch": flops, "flops_causal_exact": flops_causal,

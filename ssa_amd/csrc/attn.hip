@@ -1,28 +1,26 @@
 // Block-sparse causal flash attention (prefill) for gfx950.
 //
-// bf16/fp16 path (d = 64), two kernels sharing one MFMA scheme:
+// bf16/fp16 path (d = 64), sparse_attn_dma_kernel<DT, NW, CG, WPE>:
+//   a wave owns CG groups of 32 query rows, a workgroup NW waves = one query block (block 64:
+//   2 waves x 32 rows) or 128 rows of it (block a multiple of 128: 2 waves x 64 rows, so every
+//   LDS operand fragment feeds two MFMAs), walking the block's selected key blocks in 64-key
+//   sub-tiles:
 //   S^T = K Q^T   on v_mfma_f32_32x32x16_{bf16,f16}: A = K rows (from LDS), B = a wave's Q
-//                 fragment (registers, loaded once). The K rows fed to MFMA row m are permuted
+//                 fragments (registers, loaded once). The K rows fed to MFMA row m are permuted
 //                 (bits 2 and 3 of m swapped) so that each lane's 16 accumulators of a 32-key
 //                 tile hold two runs of 8 consecutive keys -- exactly the B-operand layout of
 //                 the next product, so P never leaves registers.
 //   online softmax in fp32 (exp2 with scale*log2e folded into one FMA; lazy rescale: the running
 //                 max only moves when a row's max exceeds it by more than 2^8),
 //   O^T += V^T P^T on MFMA: A = V^T rows (LDS), B = P^T (registers, bf16/fp16).
-// * sparse_attn_w64_kernel (block a multiple of 128): a wave owns 64 query rows (two 32-column
-//   MFMA groups, so every LDS operand fragment feeds two MFMAs); a workgroup = 2 waves = 128
-//   rows of one query block, walking its selected key blocks in 64-key sub-tiles. K and V^T
-//   sub-tiles go HBM -> LDS directly (global_load_lds_dwordx4, no staging registers) into a
-//   2-stage ring with an XOR swizzle (chunk c of row r at c ^ ((r >> 1) & 7)): the 16 lanes of
-//   one ds_read_b128 phase hit all 64 banks once.
-// * sparse_attn_mfma_kernel (block 64): a wave owns 32 query rows, a workgroup 2 waves = one
-//   query block; sub-tiles staged through registers into LDS rows padded by 16 bytes.
-// V is transposed once per call into the workspace so V^T sub-tiles are contiguous 16-byte runs
-// of keys. Row sums of the rounded P use v_dot2 against ones. Row max / sum across the two
-// 32-lane halves use v_permlane32_swap. Each wave's block list is held in a register window
-// read with v_readlane. Workgroups are dispatched heaviest query blocks first, and the query
-// heads sharing a key head for the same query block are placed on the same XCD (their shared
-// tiles hit its L2).
+// K and V^T sub-tiles go HBM -> LDS directly (global_load_lds_dwordx4, no staging registers)
+// into a 2-stage ring with an XOR swizzle (16-byte chunk c of row r at c ^ ((r >> 1) & 7)): the
+// 16 lanes of one ds_read_b128 phase hit all 64 banks once. V is transposed once per call into
+// the workspace so V^T sub-tiles are contiguous 16-byte runs of keys. Row sums of the rounded P
+// use v_dot2 against ones; row max / sum across the two 32-lane halves use v_permlane32_swap.
+// Each wave's block list is held in a register window read with v_readlane. Workgroups are
+// dispatched heaviest query blocks first, and the query heads sharing a key head for the same
+// query block are placed on the same XCD (their shared tiles hit its L2).
 //
 // fp32 path: a single-wave VALU kernel (one query row per lane), K/V sub-tiles of 64 keys in LDS.
 //
@@ -181,256 +179,6 @@ __device__ inline float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int DT, int NW, int KT>
-__global__ __launch_bounds__(NW * 64, 2) void sparse_attn_mfma_kernel(AttnParams p) {
-  using M = Mfma<DT>;
-  typedef typename M::vec vec;
-  constexpr int QT = 32 * NW;           // query rows per workgroup
-  constexpr int NT = NW * 64;           // threads
-  constexpr int KROW = 64 * 2 + 16;     // LDS pitch of a K row (64 halves + 16 B pad)
-  constexpr int VROW = KT * 2 + 16;     // LDS pitch of a V^T row (KT halves + 16 B pad)
-  constexpr int KBYTES = KT * KROW;
-  constexpr int VBYTES = 64 * VROW;
-  constexpr int BUF = KBYTES + VBYTES;
-  constexpr int CHUNKS = KT * 8 / NT;   // 16-byte chunks per thread per operand per sub-tile
-  constexpr int NST = KT / 32;          // 32-key groups per sub-tile
-  constexpr int KSTEP = NT / 8;         // K rows covered by one chunk round
-  constexpr int VSTEP = NT / (KT / 8);  // V^T rows covered by one chunk round
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF];
-
-  const int64_t L0 = logical_id(blockIdx.x, p.group);
-  if (L0 >= p.total) return;
-  int64_t L = L0;
-  const int64_t qs = L % p.qsub;
-  L /= p.qsub;
-  const int64_t hg = L % p.G;
-  L /= p.G;
-  const int64_t kvh = L % p.Hkv;
-  L /= p.Hkv;
-  const int64_t b = L % p.B;
-  L /= p.B;
-  const int64_t i = p.nbq - 1 - L;
-  const int64_t h = kvh * p.G + hg;
-
-  const int64_t q0 = i * p.block + qs * QT;
-  if (q0 >= p.n) return;
-  const int64_t qmax = q0 + QT - 1 < p.n - 1 ? q0 + QT - 1 : p.n - 1;
-
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int half = lane >> 5, col = lane & 31;
-  const int64_t qw0 = q0 + w * 32;
-  const int64_t qpos = qw0 + col;
-
-  const int64_t row = (b * p.Hq + h) * p.nbq + i;
-  int cnt = p.kv_num[row];
-  if (cnt > p.W) cnt = (int)p.W;
-  if (cnt < 0) cnt = 0;
-  const int32_t* list = p.kv_idx + row * p.W;
-  const int S = (int)(p.block / KT);
-  const int T = cnt * S;
-
-  // Q fragment (B operand of S^T = K Q^T): lane holds query `col`, head dims 16*kd + 8*half + [0,8)
-  vec qf[4];
-  {
-    const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
-                               h * p.qsh + qpos * p.qsn + half * 8;
-#pragma unroll
-    for (int kd = 0; kd < 4; ++kd) {
-      u32x4 wv = {0u, 0u, 0u, 0u};
-      if (qpos < p.n) wv = *reinterpret_cast<const u32x4*>(qp + kd * 16);
-      qf[kd] = M::from_bits(wv);
-    }
-  }
-
-  const unsigned short* kbase =
-      reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
-  const unsigned short* vtbase =
-      reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
-
-  // Per-thread load plan: chunk j of a sub-tile is K row (tid>>3) + j*KSTEP, 16-byte chunk tid&7,
-  // and V^T row tid/(KT/8) + j*VSTEP, chunk tid%(KT/8). Only the sub-tile base changes per tile
-  // (a uniform pointer), so the loop carries one 32-bit offset per operand.
-  const int kr0 = tid >> 3, kc0 = tid & 7;
-  const int vr0 = tid / (KT / 8), vc0 = tid % (KT / 8);
-  const uint32_t kgo = (uint32_t)(kr0 * p.ksn + kc0 * 8);
-  const uint32_t vgo = (uint32_t)(vr0 * p.n_pad + vc0 * 8);
-  const uint32_t klo = (uint32_t)(kr0 * KROW + kc0 * 16);
-  const uint32_t vlo = (uint32_t)(KBYTES + vr0 * VROW + vc0 * 16);
-  // Per-lane LDS read bases (MFMA A operands); every other offset is an immediate.
-  const uint32_t krd = (uint32_t)(sigma32(col) * KROW + half * 16);
-  const uint32_t vrd = (uint32_t)(KBYTES + col * VROW + half * 16);
-
-  // The row's block list, 64 entries at a time in one VGPR (entry lbase + e in lane e), read
-  // with v_readlane: no memory wait per sub-tile.
-  int lbase = 0;
-  int32_t lreg = lane < cnt ? list[lane] : -1;
-  auto tile_key0 = [&](int t) -> int64_t {
-    const int e = t / S;
-    if (e - lbase >= 64) {  // wave-uniform; once per 64 list entries
-      lbase = e;
-      lreg = e + lane < cnt ? list[e + lane] : -1;
-    }
-    const int32_t c = __builtin_amdgcn_readlane(lreg, e - lbase);
-    if (c < 0 || (int64_t)c >= p.nbq) return -1;
-    return (int64_t)c * p.block + (int64_t)(t % S) * KT;
-  };
-  auto next_valid = [&](int t) -> int {
-    for (; t < T; ++t) {
-      const int64_t k0 = tile_key0(t);
-      if (k0 >= 0 && k0 <= qmax && k0 < p.n) break;
-    }
-    return t;
-  };
-
-  u32x4 kreg[CHUNKS], vreg[CHUNKS];
-  auto load_tile = [&](int64_t key0) {
-    const unsigned short* kt = kbase + key0 * p.ksn;
-    const unsigned short* vt = vtbase + key0;
-    if (key0 + KT <= p.n) {
-#pragma unroll
-      for (int j = 0; j < CHUNKS; ++j)
-        kreg[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)j * KSTEP * p.ksn + kgo);
-    } else {  // ragged last sub-tile: rows >= n are zero
-      const int64_t nvalid = p.n - key0;
-#pragma unroll
-      for (int j = 0; j < CHUNKS; ++j) {
-        u32x4 z = {0u, 0u, 0u, 0u};
-        kreg[j] = kr0 + j * KSTEP < nvalid
-                      ? *reinterpret_cast<const u32x4*>(kt + (int64_t)j * KSTEP * p.ksn + kgo)
-                      : z;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < CHUNKS; ++j)
-      vreg[j] = *reinterpret_cast<const u32x4*>(vt + (int64_t)j * VSTEP * p.n_pad + vgo);
-  };
-  auto store_tile = [&](int buf) {
-    unsigned char* base = smem + buf * BUF;
-#pragma unroll
-    for (int j = 0; j < CHUNKS; ++j) {
-      *reinterpret_cast<u32x4*>(base + klo + j * KSTEP * KROW) = kreg[j];
-      *reinterpret_cast<u32x4*>(base + vlo + j * VSTEP * VROW) = vreg[j];
-    }
-  };
-
-  f32x16 oacc[2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.0f;
-  float m_run = -INFINITY, l_part = 0.0f;
-  const float c2 = p.scale_log2;
-
-  int t = next_valid(0);
-  int64_t key0 = t < T ? tile_key0(t) : 0;
-  if (t < T) load_tile(key0);
-  int buf = 0;
-  while (t < T) {
-    store_tile(buf);
-    __syncthreads();
-    const int tn = next_valid(t + 1);
-    const int64_t key0n = tn < T ? tile_key0(tn) : 0;
-    if (tn < T) load_tile(key0n);
-
-    const unsigned char* kb = smem + buf * BUF + krd;
-    const unsigned char* vb = smem + buf * BUF + vrd;
-    // ---- S^T = K Q^T (raised wave priority over the MFMA phases, so the matrix stream of one
-    // wave is not starved while the other wave on the SIMD runs softmax VALU work) ----
-    __builtin_amdgcn_s_setprio(1);
-    f32x16 sacc[NST];
-#pragma unroll
-    for (int tt = 0; tt < NST; ++tt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[tt][r] = 0.0f;
-#pragma unroll
-      for (int kd = 0; kd < 4; ++kd) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(kb + tt * 32 * KROW + kd * 32);
-        sacc[tt] = M::mma(M::from_bits(a), qf[kd], sacc[tt]);
-      }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    // ---- mask (diagonal / ragged tail sub-tiles only) ----
-    if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
-      const int lim_q = (int)(qpos - key0);    // keys j <= qpos  <=>  local key <= lim_q
-      const int lim_n = (int)(p.n - 1 - key0);  // keys j < n
-      const int lim = lim_q < lim_n ? lim_q : lim_n;
-#pragma unroll
-      for (int tt = 0; tt < NST; ++tt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
-          if (key > lim) sacc[tt][r] = -INFINITY;
-        }
-    }
-    // ---- online softmax ----
-    float mx = -INFINITY;
-#pragma unroll
-    for (int tt = 0; tt < NST; ++tt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][r]);
-    mx = pair_max(mx);
-    // Lazy rescale: the running max is only raised when a row's max exceeds it by more than
-    // kRescaleSlack (log2 units); otherwise the stale max is kept, so p <= 2^kRescaleSlack.
-    // Numerator and denominator share the same max, so the result is unchanged.
-    const float m_cand = mx * c2;
-    const bool grew = m_cand > m_run + kRescaleSlack;
-    if (__any(grew)) {
-      const float alpha = grew ? __builtin_amdgcn_exp2f(m_run - m_cand) : 1.0f;
-      l_part *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      m_run = grew ? m_cand : m_run;
-    }
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    // ---- P^T (registers) and O^T += V^T P^T; row sums of the rounded P on v_dot2 ----
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int tt = 0; tt < NST; ++tt) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float pv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[tt][8 * s + j], c2, -m_use));
-        const vec pb = M::pack(pv);
-        l_part = M::rowsum(pb, l_part);
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(vb + dt * 32 * VROW + (4 * tt + 2 * s) * 16);
-          oacc[dt] = M::mma(M::from_bits(a), pb, oacc[dt]);
-        }
-      }
-    }
-    __builtin_amdgcn_s_setprio(0);
-    buf ^= 1;
-    t = tn;
-    key0 = key0n;
-  }
-
-  // ---- epilogue: O = O^T / l ----
-  const float l_tot = pair_sum(l_part);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qpos < p.n) {
-    unsigned short* op =
-        reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos * p.osn;
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int d0 = dt * 32 + rg * 8 + half * 4;
-        uint2 wv;
-        wv.x = M::pack2(oacc[dt][4 * rg] * inv, oacc[dt][4 * rg + 1] * inv);
-        wv.y = M::pack2(oacc[dt][4 * rg + 2] * inv, oacc[dt][4 * rg + 3] * inv);
-        *reinterpret_cast<uint2*>(op + d0) = wv;
-      }
-    if (p.lse != nullptr && half == 0)
-      p.lse[(b * p.Hq + h) * p.n + qpos] =
-          l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
-  }
-}
-
 // fp32 path: one wave per 64 query rows, one row per lane. grid = logical items (no remap).
 __global__ __launch_bounds__(64) void sparse_attn_f32_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) float Ks[64][64];
@@ -536,16 +284,18 @@ __global__ __launch_bounds__(64) void sparse_attn_f32_kernel(AttnParams p) {
 // by one ds_read_b128 of an MFMA operand (16 distinct rows) then hit all 64 banks once.
 __device__ inline int swz(int r) { return (r >> 1) & 7; }
 
-// Wave tile of 64 query rows (two 32-column MFMA groups) against 64-key sub-tiles: every LDS
-// operand fragment feeds two MFMAs. A workgroup = 2 waves = 128 query rows of one query block.
-// K and V^T sub-tiles (64 rows x 128 B each, swizzled) go HBM -> LDS directly
+// A wave owns CG groups of 32 query rows (every LDS operand fragment feeds CG MFMAs); a workgroup
+// of NW waves owns ROWS = 32*CG*NW rows of one query block and walks its selected key blocks in
+// 64-key sub-tiles. K and V^T sub-tiles (64 rows x 128 B each, swizzled) go HBM -> LDS directly
 // (global_load_lds_dwordx4, no staging registers) into a 2-stage ring, one barrier per sub-tile.
-template <int DT>
-__global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
+template <int DT, int NW, int CG, int WPE>
+__global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
   constexpr int KT = 64;
-  constexpr int TILE = KT * 128;  // bytes of one K or V^T sub-tile
+  constexpr int TILE = KT * 128;      // bytes of one K or V^T sub-tile
+  constexpr int ROWS = 32 * CG * NW;  // query rows per workgroup
+  constexpr int LPW = 8 / NW;         // 1 KB load instructions per wave per operand per sub-tile
   __shared__ __attribute__((aligned(1024))) unsigned char kst0[TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char vst0[TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char kst1[TILE];
@@ -565,15 +315,17 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
   const int64_t i = p.nbq - 1 - L;
   const int64_t h = kvh * p.G + hg;
 
-  const int64_t q0 = i * p.block + qs * 128;
+  const int64_t q0 = i * p.block + qs * ROWS;
   if (q0 >= p.n) return;
-  const int64_t qmax = q0 + 127 < p.n - 1 ? q0 + 127 : p.n - 1;
+  const int64_t qmax = q0 + ROWS - 1 < p.n - 1 ? q0 + ROWS - 1 : p.n - 1;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, col = lane & 31;
-  const int64_t qw0 = q0 + w * 64;
-  const int64_t qpos0 = qw0 + col, qpos1 = qw0 + 32 + col;
+  const int64_t qw0 = q0 + w * 32 * CG;  // first query row of this wave
+  int64_t qpos[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) qpos[c] = qw0 + 32 * c + col;
 
   const int64_t row = (b * p.Hq + h) * p.nbq + i;
   int cnt = p.kv_num[row];
@@ -583,17 +335,16 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
   const int S = (int)(p.block / KT);
   const int T = cnt * S;
 
-  // Q fragments (B operands of S^T = K Q^T) of the two column groups
-  vec qf[2][4];
+  // Q fragments (B operands of S^T = K Q^T) of the column groups
+  vec qf[CG][4];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int64_t qp = c ? qpos1 : qpos0;
+  for (int c = 0; c < CG; ++c) {
     const unsigned short* src = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
-                                h * p.qsh + qp * p.qsn + half * 8;
+                                h * p.qsh + qpos[c] * p.qsn + half * 8;
 #pragma unroll
     for (int kd = 0; kd < 4; ++kd) {
       u32x4 wv = {0u, 0u, 0u, 0u};
-      if (qp < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
+      if (qpos[c] < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
       qf[c][kd] = M::from_bits(wv);
     }
   }
@@ -603,13 +354,13 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
   const unsigned short* vtbase =
       reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
 
-  // Load plan: instruction j of wave w fills tile rows j*16 + w*8 + [0,8); lane -> row
-  // lr = w*8 + lane/8 (+ j*16), physical chunk lane%8 = logical chunk lc ^ swz(row).
+  // Load plan: instruction j of wave w fills tile rows j*8*NW + w*8 + [0,8) (1 KB, LDS offset
+  // j*1024*NW + w*1024); lane -> row lr (+ j*8*NW), physical chunk lane%8 = logical lc ^ swz(row).
   const int lr = w * 8 + (lane >> 3);
   const int lc = (lane & 7) ^ swz(lr);
   const uint32_t kgo = (uint32_t)(lr * p.ksn + lc * 8);
   const uint32_t vgo = (uint32_t)(lr * p.n_pad + lc * 8);
-  const int64_t kstep = 16 * p.ksn, vstep = 16 * p.n_pad;
+  const int64_t kstep = 8 * NW * p.ksn, vstep = 8 * NW * p.n_pad;
 
   // The row's block list, 64 entries at a time in one VGPR (entry lbase + e in lane e), read
   // with v_readlane: no memory wait per sub-tile.
@@ -637,20 +388,22 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
     const unsigned short* vt = vtbase + key0;
     if (key0 + KT <= p.n) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(kt + j * kstep + kgo, kdst + j * 2048 + w * 1024, 16, 0, 0);
+      for (int j = 0; j < LPW; ++j)
+        __builtin_amdgcn_global_load_lds(kt + j * kstep + kgo, kdst + j * 1024 * NW + w * 1024,
+                                         16, 0, 0);
     } else {  // ragged tail: rows >= n re-read row n-1 (their scores are masked)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int64_t r = key0 + j * 16 + lr;
+      for (int j = 0; j < LPW; ++j) {
+        int64_t r = key0 + j * 8 * NW + lr;
         if (r > p.n - 1) r = p.n - 1;
-        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lc * 8, kdst + j * 2048 + w * 1024,
-                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lc * 8,
+                                         kdst + j * 1024 * NW + w * 1024, 16, 0, 0);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds(vt + j * vstep + vgo, vdst + j * 2048 + w * 1024, 16, 0, 0);
+    for (int j = 0; j < LPW; ++j)
+      __builtin_amdgcn_global_load_lds(vt + j * vstep + vgo, vdst + j * 1024 * NW + w * 1024,
+                                       16, 0, 0);
   };
 
   // per-lane LDS read offsets: K row tt*32 + sigma32(col), V^T row dt*32 + col; chunk
@@ -663,14 +416,19 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
     voff[s] = (uint32_t)(col * 128 + (((2 * s + half) ^ swz(col)) * 16));
   }
 
-  f32x16 oacc[2][2];  // [dt][c]
+  f32x16 oacc[2][CG];  // [dt][c]
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < CG; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[dt][c][r] = 0.0f;
-  float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.0f, 0.0f};
+  float m_run[CG], l_part[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    m_run[c] = -INFINITY;
+    l_part[c] = 0.0f;
+  }
   const float c2 = p.scale_log2;
 
   auto compute = [&](const unsigned char* ks, const unsigned char* vs, int64_t key0) {
@@ -681,12 +439,12 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
 #pragma unroll
       for (int kd = 0; kd < 4; ++kd)
         ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * 4096);
-    f32x16 sacc[2][2];  // [tt][c]
+    f32x16 sacc[2][CG];  // [tt][c]
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < CG; ++c) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[tt][c][r] = 0.0f;
 #pragma unroll
@@ -704,8 +462,8 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
     // ---- mask (diagonal / ragged tail sub-tiles only) ----
     if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int lim_q = (int)((c ? qpos1 : qpos0) - key0);
+      for (int c = 0; c < CG; ++c) {
+        const int lim_q = (int)(qpos[c] - key0);
         const int lim_n = (int)(p.n - 1 - key0);
         const int lim = lim_q < lim_n ? lim_q : lim_n;
 #pragma unroll
@@ -718,11 +476,11 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
       }
     }
     // ---- online softmax (lazy rescale) ----
-    float m_use[2];
-    bool grew[2];
-    float m_cand[2];
+    float m_use[CG], m_cand[CG];
+    bool grew[CG];
+    bool any_grew = false;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < CG; ++c) {
       float mx = -INFINITY;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
@@ -731,10 +489,11 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
       mx = pair_max(mx);
       m_cand[c] = mx * c2;
       grew[c] = m_cand[c] > m_run[c] + kRescaleSlack;
+      any_grew = any_grew || grew[c];
     }
-    if (__any(grew[0] || grew[1])) {
+    if (__any(any_grew)) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < CG; ++c) {
         const float alpha = grew[c] ? __builtin_amdgcn_exp2f(m_run[c] - m_cand[c]) : 1.0f;
         l_part[c] *= alpha;
 #pragma unroll
@@ -745,7 +504,7 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
       }
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) m_use[c] = m_run[c] == -INFINITY ? 0.0f : m_run[c];
+    for (int c = 0; c < CG; ++c) m_use[c] = m_run[c] == -INFINITY ? 0.0f : m_run[c];
     // ---- P^T (registers) and O^T += V^T P^T ----
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -755,9 +514,9 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
         for (int dt = 0; dt < 2; ++dt)
           va[s + 2][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s + 2] + dt * 4096);
       }
-      vec pb[2];
+      vec pb[CG];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < CG; ++c) {
         float pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -768,7 +527,7 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < CG; ++c)
           oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -783,7 +542,7 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
     int tn = next_valid(t + 1);
     int64_t key0n = tn < T ? tile_key0(tn) : 0;
     if (tn < T) issue(kst1, vst1, key0n);
-    if (key0 <= qw0 + 63) compute(kst0, vst0, key0);
+    if (key0 <= qw0 + 32 * CG - 1) compute(kst0, vst0, key0);
     t = tn;
     key0 = key0n;
     if (t >= T) break;
@@ -791,20 +550,19 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
     tn = next_valid(t + 1);
     key0n = tn < T ? tile_key0(tn) : 0;
     if (tn < T) issue(kst0, vst0, key0n);
-    if (key0 <= qw0 + 63) compute(kst1, vst1, key0);
+    if (key0 <= qw0 + 32 * CG - 1) compute(kst1, vst1, key0);
     t = tn;
     key0 = key0n;
   }
 
   // ---- epilogue: O = O^T / l ----
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int64_t qpos = c ? qpos1 : qpos0;
+  for (int c = 0; c < CG; ++c) {
     const float l_tot = pair_sum(l_part[c]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (qpos < p.n) {
+    if (qpos[c] < p.n) {
       unsigned short* op =
-          reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos * p.osn;
+          reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos[c] * p.osn;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -816,7 +574,7 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
           *reinterpret_cast<uint2*>(op + d0) = wv;
         }
       if (p.lse != nullptr && half == 0)
-        p.lse[(b * p.Hq + h) * p.n + qpos] =
+        p.lse[(b * p.Hq + h) * p.n + qpos[c]] =
             l_tot > 0.0f ? (m_run[c] + log2f(l_tot)) * kLn2 : -INFINITY;
     }
   }
@@ -824,23 +582,18 @@ __global__ __launch_bounds__(128, 2) void sparse_attn_w64_kernel(AttnParams p) {
 
 template <int DT>
 int launch_mfma(AttnParams& p, hipStream_t stream) {
-  const int64_t G = p.G;
-  if (p.block == 64) {
-    p.qsub = 1;
-    p.group = G;
-    p.total = p.nbq * p.B * p.Hkv * G;
-    const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
-    SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-    sparse_attn_mfma_kernel<DT, 2, 64><<<(unsigned)grid, 128, 0, stream>>>(p);
-  } else {
-    p.qsub = p.block / 128;
-    p.group = G * p.qsub;
-    p.total = p.nbq * p.B * p.Hkv * G * p.qsub;
-    const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
-    SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-    sparse_attn_w64_kernel<DT><<<(unsigned)grid, 128, 0, stream>>>(p);
-  }
-  return launch_status("sparse_attn_mfma_kernel");
+  // block 64: 2 waves x 32 rows = one query block; otherwise 2 waves x 64 rows per workgroup
+  const bool b64 = p.block == 64;
+  p.qsub = b64 ? 1 : p.block / 128;
+  p.group = p.G * p.qsub;
+  p.total = p.nbq * p.B * p.Hkv * p.G * p.qsub;
+  const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+  SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+  if (b64)
+    sparse_attn_dma_kernel<DT, 2, 1, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+  else
+    sparse_attn_dma_kernel<DT, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+  return launch_status("sparse_attn_dma_kernel");
 }
 
 }  // namespace
