@@ -5,9 +5,10 @@
 //   parallel. Each wave computes its block's scores (one key per lane per pass, 16-byte row
 //   loads), the block's running max / sum in fp32 and its unnormalised output row (lane = head
 //   dim, coalesced V row reads), and writes (m, l, o) to the workspace.
-// decode_combine_kernel: merges a row's partials with the usual max-rescaling.
-// decode_step: append the new token -> summarise a just-completed block -> route the query over
-//   the complete blocks (route_impl, SSA_ROUTE_QUERY) -> partial -> combine.
+// decode_combine_kernel: merges a row's partials with the usual max-rescaling (4 waves per row).
+// decode_step: append the new token and convert the query rows (one launch) -> summarise a
+//   just-completed block -> route the query over the complete blocks (route_impl,
+//   SSA_ROUTE_QUERY) -> partial -> combine.
 //
 // Reference: ssa/ivf_decode.py:49-62 (decode_attend), :128-136 (per-step body);
 // ssa/gemma_ssa.py:85-137,225-240 (exact per-query router and softmax at q_len = 1).
@@ -160,11 +161,46 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
   const float l = wave_sum(lloc);
   __syncthreads();
   const int64_t voff = b * p.vsb + kvh * p.vsh;
-  for (int e = lane; e < d; e += 64) {
-    float acc = 0.0f;
-    for (int kk = 0; kk < nk; ++kk)
-      acc = fmaf(ps[kk], load_elem<DT>(p.v, voff + (key0 + kk) * p.vsn + e), acc);
-    part[2 + e] = acc;
+  if constexpr (DT == SSA_F32) {
+    for (int e = lane; e < d; e += 64) {
+      float acc = 0.0f;
+      for (int kk = 0; kk < nk; ++kk)
+        acc = fmaf(ps[kk], load_elem<DT>(p.v, voff + (key0 + kk) * p.vsn + e), acc);
+      part[2 + e] = acc;
+    }
+  } else {
+    // lane = (key group kg = lane / 8, 16-byte chunk ch = lane % 8): 8 keys per pass, 16-byte V
+    // row loads; the 8 key groups are summed with cross-lane shuffles.
+    const int kg = lane >> 3, ch = lane & 7;
+    const unsigned short* vb = reinterpret_cast<const unsigned short*>(p.v) + voff;
+    for (int e0 = 0; e0 < d; e0 += 64) {
+      const bool on = e0 + ch * 8 < d;
+      float acc[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+      if (on) {
+#pragma unroll 4
+        for (int kk = kg; kk < nk; kk += 8) {
+          const u32x4 wv = *reinterpret_cast<const u32x4*>(vb + (key0 + kk) * p.vsn + e0 + ch * 8);
+          float vv[8];
+          unpack8(wv, vv, DT == SSA_BF16);
+          const float pk = ps[kk];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) acc[t] = fmaf(pk, vv[t], acc[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        float x = acc[t];
+        x += __shfl_xor(x, 8, 64);
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        acc[t] = x;
+      }
+      if (kg == 0 && on)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) part[2 + e0 + ch * 8 + t] = acc[t];
+    }
   }
   if (lane == 0) {
     part[0] = m;
@@ -172,32 +208,66 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
   }
 }
 
-// grid (B*Hq*nq), one wave each.
+// grid (B*Hq*nq), 4 waves per row: weights of 256 partials at a time in LDS, each wave sums a
+// quarter of the partials for every head dim (coalesced rows), then the waves are added.
 template <int DT>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+  __shared__ float wts[256];
+  __shared__ float red[4][kMaxDecodeD];
+  __shared__ float sm[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t rowid = blockIdx.x;
   const int64_t bh = rowid / p.nq, r = rowid % p.nq;
   const int64_t b = bh / p.Hq, h = bh % p.Hq;
   int cnt = p.kv_num[rowid];
   if (cnt > p.W) cnt = (int)p.W;
-  const float* part = p.part + rowid * p.W * (p.d + 2);
+  const int64_t stride = p.d + 2;
+  const float* part = p.part + rowid * p.W * stride;
   float M = -INFINITY;
-  for (int j = 0; j < cnt; ++j) M = fmaxf(M, part[j * (p.d + 2)]);
+  for (int j = tid; j < cnt; j += 256) M = fmaxf(M, part[j * stride]);
+  M = wave_max(M);
+  if (lane == 0) sm[wv] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  __syncthreads();
   float L = 0.0f;
-  for (int j = 0; j < cnt; ++j) {
-    const float mj = part[j * (p.d + 2)];
-    if (mj != -INFINITY) L += part[j * (p.d + 2) + 1] * exp2f(mj - M);
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  for (int e = lane; e < p.d; e += 64) {
-    float acc = 0.0f;
-    for (int j = 0; j < cnt; ++j) {
-      const float mj = part[j * (p.d + 2)];
-      if (mj != -INFINITY) acc = fmaf(part[j * (p.d + 2) + 2 + e], exp2f(mj - M), acc);
+  float acc[kMaxDecodeD / 64];
+#pragma unroll
+  for (int k = 0; k < kMaxDecodeD / 64; ++k) acc[k] = 0.0f;
+  for (int j0 = 0; j0 < cnt; j0 += 256) {
+    const int j = j0 + tid;
+    float wj = 0.0f;
+    if (j < cnt) {
+      const float mj = part[j * stride];
+      if (mj != -INFINITY) {
+        wj = exp2f(mj - M);
+        L += part[j * stride + 1] * wj;
+      }
     }
-    store_elem<DT>(p.o, b * p.osb + h * p.osh + r * p.osn + e, acc * inv);
+    wts[tid] = wj;
+    __syncthreads();
+    const int jn = cnt - j0 < 256 ? cnt - j0 : 256;
+    for (int jj = wv; jj < jn; jj += 4) {
+      const float w = wts[jj];
+      if (w == 0.0f) continue;  // wave-uniform
+      const float* pr = part + (j0 + jj) * stride + 2;
+#pragma unroll
+      for (int k = 0; k < kMaxDecodeD / 64; ++k)
+        if (lane + 64 * k < p.d) acc[k] = fmaf(pr[lane + 64 * k], w, acc[k]);
+    }
+    __syncthreads();
   }
+  L = wave_sum(L);
+  if (lane == 0) sm[wv] = L;
+#pragma unroll
+  for (int k = 0; k < kMaxDecodeD / 64; ++k)
+    if (lane + 64 * k < p.d) red[wv][lane + 64 * k] = acc[k];
+  __syncthreads();
+  L = sm[0] + sm[1] + sm[2] + sm[3];
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  for (int e = tid; e < p.d; e += 256)
+    store_elem<DT>(p.o, b * p.osb + h * p.osh + r * p.osn + e,
+                   (red[0][e] + red[1][e] + red[2][e] + red[3][e]) * inv);
 }
 
 // Element strides of the append: new token rows (b,h) and caches (b,h,n).
@@ -205,29 +275,26 @@ struct AppendStrides {
   int64_t knb, knh, vnb, vnh, kcb, kch, kcn, vcb, vch, vcn;
 };
 
-// k_new/v_new (B, Hkv, d) -> caches at row pos. grid (B*Hkv).
+// One launch for the per-step preparation. grid (B*Hq): block (b, h) converts query row (b, h)
+// to contiguous fp32 (the router's rows), and the first query head of each key head also writes
+// k_new/v_new (B, Hkv, d) into the caches at row pos.
 template <int DT>
-__global__ __launch_bounds__(64) void decode_append_kernel(const char* kn, const char* vn,
-                                                           char* kc, char* vc, int64_t Hkv,
-                                                           int64_t d, int64_t pos,
-                                                           AppendStrides st) {
-  const int64_t bk = blockIdx.x;
-  const int64_t b = bk / Hkv, h = bk % Hkv;
-  for (int e = threadIdx.x; e < d; e += 64) {
-    store_elem<DT>(kc, b * st.kcb + h * st.kch + pos * st.kcn + e,
-                   load_elem<DT>(kn, b * st.knb + h * st.knh + e));
-    store_elem<DT>(vc, b * st.vcb + h * st.vch + pos * st.vcn + e,
-                   load_elem<DT>(vn, b * st.vnb + h * st.vnh + e));
-  }
-}
-
-// q (B, Hq, d) strided -> fp32 (B, Hq, d) contiguous. grid (B*Hq).
-template <int DT>
-__global__ __launch_bounds__(64) void rows_to_f32_kernel(const char* q, float* out, int64_t Hq,
-                                                         int64_t d, int64_t qsb, int64_t qsh) {
+__global__ __launch_bounds__(64) void decode_prep_kernel(const char* q, float* qf, const char* kn,
+                                                         const char* vn, char* kc, char* vc,
+                                                         int64_t Hq, int64_t G, int64_t d,
+                                                         int64_t qsb, int64_t qsh, int64_t pos,
+                                                         AppendStrides st) {
   const int64_t r = blockIdx.x;
   const int64_t b = r / Hq, h = r % Hq;
-  for (int e = threadIdx.x; e < d; e += 64) out[r * d + e] = load_elem<DT>(q, b * qsb + h * qsh + e);
+  for (int e = threadIdx.x; e < d; e += 64) qf[r * d + e] = load_elem<DT>(q, b * qsb + h * qsh + e);
+  if (h % G != 0) return;
+  const int64_t kvh = h / G;
+  for (int e = threadIdx.x; e < d; e += 64) {
+    store_elem<DT>(kc, b * st.kcb + kvh * st.kch + pos * st.kcn + e,
+                   load_elem<DT>(kn, b * st.knb + kvh * st.knh + e));
+    store_elem<DT>(vc, b * st.vcb + kvh * st.vch + pos * st.vcn + e,
+                   load_elem<DT>(vn, b * st.vnb + kvh * st.vnh + e));
+  }
 }
 
 int run_attend(int dtype, DecodeParams& p, hipStream_t stream) {
@@ -242,9 +309,9 @@ int run_attend(int dtype, DecodeParams& p, hipStream_t stream) {
   SSA_TRY(launch_status("decode_partial_kernel"));
   const unsigned g2 = (unsigned)rows;
   switch (dtype) {
-    case SSA_F32: decode_combine_kernel<SSA_F32><<<g2, 64, 0, stream>>>(p); break;
-    case SSA_F16: decode_combine_kernel<SSA_F16><<<g2, 64, 0, stream>>>(p); break;
-    default: decode_combine_kernel<SSA_BF16><<<g2, 64, 0, stream>>>(p); break;
+    case SSA_F32: decode_combine_kernel<SSA_F32><<<g2, 256, 0, stream>>>(p); break;
+    case SSA_F16: decode_combine_kernel<SSA_F16><<<g2, 256, 0, stream>>>(p); break;
+    default: decode_combine_kernel<SSA_BF16><<<g2, 256, 0, stream>>>(p); break;
   }
   return launch_status("decode_combine_kernel");
 }
@@ -350,7 +417,7 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   void* keys = ws + qf_bytes;
   float* part = reinterpret_cast<float*>(ws + qf_bytes + key_bytes);
 
-  // 1. append the new token
+  // 1. append the new token and convert the query rows (one launch)
   AppendStrides as;
   as.knb = strides[2]; as.knh = strides[3]; as.vnb = strides[4]; as.vnh = strides[5];
   as.kcb = strides[6]; as.kch = strides[7]; as.kcn = strides[8];
@@ -359,13 +426,24 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   const char* vn = static_cast<const char*>(v_new);
   char* kc = static_cast<char*>(kcache);
   char* vc = static_cast<char*>(vcache);
-  const unsigned gb = (unsigned)(B * Hkv);
+  const unsigned gr = (unsigned)(B * Hq);
+  const char* qc = static_cast<const char*>(q);
+  const int64_t G = Hq / Hkv;
   switch (dtype) {
-    case SSA_F32: decode_append_kernel<SSA_F32><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
-    case SSA_F16: decode_append_kernel<SSA_F16><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
-    default: decode_append_kernel<SSA_BF16><<<gb, 64, 0, st>>>(kn, vn, kc, vc, Hkv, d, pos, as); break;
+    case SSA_F32:
+      decode_prep_kernel<SSA_F32><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                      strides[1], pos, as);
+      break;
+    case SSA_F16:
+      decode_prep_kernel<SSA_F16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                      strides[1], pos, as);
+      break;
+    default:
+      decode_prep_kernel<SSA_BF16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                       strides[1], pos, as);
+      break;
   }
-  SSA_TRY(launch_status("decode_append_kernel"));
+  SSA_TRY(launch_status("decode_prep_kernel"));
 
   // 2. a block completed at pos: its population summary becomes routable
   if ((pos + 1) % block == 0) {
@@ -376,14 +454,6 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   }
 
   // 3. route the queries over the complete blocks
-  const unsigned gr = (unsigned)(B * Hq);
-  const char* qc = static_cast<const char*>(q);
-  switch (dtype) {
-    case SSA_F32: rows_to_f32_kernel<SSA_F32><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
-    case SSA_F16: rows_to_f32_kernel<SSA_F16><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
-    default: rows_to_f32_kernel<SSA_BF16><<<gr, 64, 0, st>>>(qc, qf, Hq, d, strides[0], strides[1]); break;
-  }
-  SSA_TRY(launch_status("rows_to_f32_kernel"));
   SSA_TRY(route_impl(qf, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
                      budget_frac, local, coef2, 0.0f, pos, block, kv_num, kv_idx, W, keys,
                      key_bytes, st));

@@ -26,6 +26,8 @@ constexpr int kDK = 32;         // head-dim chunk staged in LDS
 constexpr int kSelThreads = 256;
 constexpr int kMaxNbk = 65536;  // bitmap capacity of the select kernel
 constexpr int kCacheKeys = 8192;
+constexpr int kCand = 2048;        // candidate capacity of the filtered select
+constexpr int kFilterMin = 2048;   // rows with more candidates than this are filtered first
 
 struct RouteGeom {
   int mode;
@@ -183,8 +185,87 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   }
 }
 
-// Block-wide exclusive scan of one int per thread (256 threads); returns the exclusive prefix
+// Few-row variant (R <= 16 rows per key head, e.g. a decode step): thread t scores candidate
+// c0 + t / RP for row t % RP (RP = R rounded up to a power of two), so no work is spent on the
+// empty rows of a 64-row tile. Same fp64 accumulation order over the head dim and the same
+// fp32 assembly as route_score_kernel.
+template <bool EDGE>
+__global__ __launch_bounds__(256) void route_score_rows_kernel(
+    const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
+    unsigned int* __restrict__ keys, int rp_log2) {
+  constexpr int kMaxR = 16;
+  const int RP = 1 << rp_log2;
+  const int CPB = 256 >> rp_log2;  // candidates per workgroup
+  __shared__ float Qs[kMaxR][kDK + 1];
+  __shared__ float Q2s[kMaxR][kDK + 1];
+  __shared__ float Q3s[EDGE ? kMaxR : 1][kDK + 1];
+  __shared__ float Ms[256][kDK + 1];
+  __shared__ float Vs[256][kDK + 1];
+  __shared__ float M3s[EDGE ? 256 : 1][kDK + 1];
+
+  const int64_t bk = blockIdx.y;  // b * Hkv + kvh
+  const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
+  const int64_t R = g.G * g.ni;
+  const int64_t c0 = (int64_t)blockIdx.x * CPB;
+  if (c0 >= row_cmax(g, g.i0 + g.ni - 1)) return;  // uniform: beyond every row's candidates
+  const int tid = threadIdx.x;
+  const int r = tid & (RP - 1);
+  const int cl = tid >> rp_log2;
+  const int64_t c = c0 + cl;
+
+  const float* kv_mu = mu + (bk * g.nbk) * d;
+  const float* kv_var = var ? var + (bk * g.nbk) * d : nullptr;
+  const float* kv_m3 = EDGE ? m3 + (bk * g.nbk) * d : nullptr;
+  double e1 = 0.0, e2 = 0.0, e3 = 0.0;
+  for (int k0 = 0; k0 < d; k0 += kDK) {
+    __syncthreads();
+    for (int idx = tid; idx < kMaxR * kDK; idx += 256) {
+      const int rr = idx / kDK, kk = idx % kDK;
+      float q = 0.0f;
+      if (rr < R && k0 + kk < d) {
+        const int64_t h = kvh * g.G + rr / g.ni;
+        const int64_t i = g.i0 + rr % g.ni;
+        q = rows[((b * g.Hq + h) * g.nbq + i) * d + k0 + kk];
+      }
+      const float q2 = q * q;
+      Qs[rr][kk] = q;
+      Q2s[rr][kk] = q2;
+      if constexpr (EDGE) Q3s[rr][kk] = q2 * q;
+    }
+    for (int idx = tid; idx < CPB * kDK; idx += 256) {
+      const int cc = idx / kDK, kk = idx % kDK;
+      const int64_t cand = c0 + cc;
+      float m = 0.0f, v = 0.0f, t = 0.0f;
+      if (cand < g.nbk && k0 + kk < d) {
+        m = kv_mu[cand * d + k0 + kk];
+        if (kv_var) v = kv_var[cand * d + k0 + kk];
+        if constexpr (EDGE) t = kv_m3[cand * d + k0 + kk];
+      }
+      Ms[cc][kk] = m;
+      Vs[cc][kk] = v;
+      if constexpr (EDGE) M3s[cc][kk] = t;
+    }
+    __syncthreads();
+    const int kend = d - k0 < kDK ? d - k0 : kDK;
+    for (int kk = 0; kk < kend; ++kk) {
+      e1 = fma((double)Qs[r][kk], (double)Ms[cl][kk], e1);
+      e2 = fma((double)Q2s[r][kk], (double)Vs[cl][kk], e2);
+      if constexpr (EDGE) e3 = fma((double)Q3s[r][kk], (double)M3s[cl][kk], e3);
+    }
+  }
+  if (r >= R) return;
+  const int64_t h = kvh * g.G + r / g.ni;
+  const int64_t il = r % g.ni;
+  if (c >= row_cmax(g, g.i0 + il)) return;
+  float s = __fadd_rn((float)e1, __fmul_rn(coef2, (float)e2));
+  if constexpr (EDGE) s = __fadd_rn(s, __fmul_rn(coef3, (float)e3));
+  keys[((b * g.Hq + h) * g.ni + il) * g.nbk + c] = score_key(s);
+}
+
+// Block-wide exclusive scan of one int per thread (NT threads); returns the exclusive prefix
 // and writes the total to *total.
+template <int NT>
 __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int incl = v;
@@ -197,7 +278,7 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   __syncthreads();
   int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < kSelThreads / 64; ++w) {
+  for (int w = 0; w < NT / 64; ++w) {
     if (w < wave) base += wave_sums[w];
     tot += wave_sums[w];
   }
@@ -206,16 +287,24 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return base + incl - v;
 }
 
-__global__ __launch_bounds__(kSelThreads) void route_select_kernel(
+// Top-K of one row of score keys (K = min(keep, cmax)), ties to the lowest block index, then the
+// row's local window, compacted ascending into kv_idx (pad 0) with kv_num.
+// Rows of at most kCacheKeys candidates are staged in LDS; longer rows (more than kFilterMin) are
+// first filtered: the keys are split into P >= K disjoint groups, so the smallest group maximum
+// T0 is <= the K-th largest key; the keys >= T0 (with their indices) go to LDS and the radix
+// select runs on them (rows whose filter keeps more than kCand keys use the full row).
+template <int NT>
+__global__ __launch_bounds__(NT) void route_select_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
     int32_t* __restrict__ kv_idx, int64_t W) {
   __shared__ unsigned int bits[kMaxNbk / 32];
-  __shared__ unsigned int cache[kCacheKeys];
+  __shared__ unsigned int cache[kCacheKeys];  // the row's keys, or the filtered candidates
+  __shared__ unsigned int cidx[kCand];        // candidate block indices (filtered rows)
   __shared__ unsigned int hist[256];
-  __shared__ int wave_sums[kSelThreads / 64];
-  __shared__ unsigned int sh_digit, sh_above;
+  __shared__ int wave_sums[NT / 64];
+  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand;
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
   const int64_t bh = lrow / g.ni, il = lrow % g.ni;
   const int64_t i = g.i0 + il;
@@ -225,22 +314,73 @@ __global__ __launch_bounds__(kSelThreads) void route_select_kernel(
   const unsigned int* krow = keys + lrow * g.nbk;
   const int nwords = (int)((g.nbk + 31) / 32);
 
-  for (int w = tid; w < nwords; w += kSelThreads) bits[w] = 0u;
-  const bool cached = cmax <= kCacheKeys;
+  for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
+  const bool cached = cmax <= kCacheKeys;  // whole row in LDS, index order
   if (cached && K > 0 && K < cmax)
-    for (int64_t c = tid; c < cmax; c += kSelThreads) cache[c] = krow[c];
+    for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow[c];
+  if (tid == 0) {
+    sh_min = 0xffffffffu;
+    sh_ncand = 0u;
+  }
   __syncthreads();
 
+  // keys the radix select runs over: src[0, nsel), block index of entry c: filt ? cidx[c] : c
+  bool filt = false;
+  int64_t nsel = cmax;
+  if (!cached && K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
+    int pk = 1;
+    while (pk < K) pk <<= 1;
+    const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
+    unsigned int mx = 0u;
+    for (int64_t c = tid; c < cmax; c += NT) {
+      const unsigned int key = krow[c];
+      mx = key > mx ? key : mx;
+    }
+    for (int off = 1; off < gs; off <<= 1) {
+      const unsigned int o = __shfl_xor(mx, off, 64);
+      mx = o > mx ? o : mx;
+    }
+    // every lane now holds its group's maximum: T0 = the minimum over all lanes
+    for (int off = 1; off < 64; off <<= 1) {
+      const unsigned int o = __shfl_xor(mx, off, 64);
+      mx = o < mx ? o : mx;
+    }
+    if (lane == 0) atomicMin(&sh_min, mx);
+    __syncthreads();
+    const unsigned int t0 = sh_min;
+    for (int64_t c = tid; c < cmax; c += NT) {
+      const unsigned int key = krow[c];
+      if (key >= t0) {
+        const unsigned int slot = atomicAdd(&sh_ncand, 1u);
+        if (slot < (unsigned int)kCand) {
+          cache[slot] = key;
+          cidx[slot] = (unsigned int)c;
+        }
+      }
+    }
+    __syncthreads();
+    if (sh_ncand <= (unsigned int)kCand) {
+      filt = true;
+      nsel = sh_ncand;
+    }
+  }
+  const bool src_lds = cached || filt;
+  auto src = [&](int64_t c) -> unsigned int { return src_lds ? cache[c] : krow[c]; };
+  auto mark = [&](int64_t c) {
+    const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
+    atomicOr(&bits[blk >> 5], 1u << (blk & 31));
+  };
+
   if (K >= cmax) {
-    for (int64_t c = tid; c < cmax; c += kSelThreads) atomicOr(&bits[c >> 5], 1u << (c & 31));
+    for (int64_t c = tid; c < cmax; c += NT) atomicOr(&bits[c >> 5], 1u << (c & 31));
   } else if (K > 0) {
     unsigned int prefix = 0u, pmask = 0u;
     unsigned int kk = (unsigned int)K;  // rank of T among keys matching the prefix
     for (int shift = 24; shift >= 0; shift -= 8) {
-      hist[tid] = 0u;
+      for (int t = tid; t < 256; t += NT) hist[t] = 0u;
       __syncthreads();
-      for (int64_t c = tid; c < cmax; c += kSelThreads) {
-        unsigned int key = cached ? cache[c] : krow[c];
+      for (int64_t c = tid; c < nsel; c += NT) {
+        const unsigned int key = src(c);
         if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
       __syncthreads();
@@ -274,30 +414,26 @@ __global__ __launch_bounds__(kSelThreads) void route_select_kernel(
       __syncthreads();
     }
     const unsigned int T = prefix;
-    const unsigned int need_eq = kk;        // keys equal to T still to take
-    const unsigned int n_eq = hist[T & 255u];  // keys equal to T (last pass histogram)
+    const unsigned int need_eq = kk;           // keys equal to T still to take
+    const unsigned int n_eq = hist[T & 255u];  // keys equal to T (all of them are >= T0)
     __syncthreads();
     if (need_eq == n_eq) {
-      for (int64_t c = tid; c < cmax; c += kSelThreads) {
-        unsigned int key = cached ? cache[c] : krow[c];
-        if (key >= T) atomicOr(&bits[c >> 5], 1u << (c & 31));
-      }
+      for (int64_t c = tid; c < nsel; c += NT)
+        if (src(c) >= T) mark(c);
     } else {
-      for (int64_t c = tid; c < cmax; c += kSelThreads) {
-        unsigned int key = cached ? cache[c] : krow[c];
-        if (key > T) atomicOr(&bits[c >> 5], 1u << (c & 31));
-      }
-      // ties at T: take the lowest block indices first
+      for (int64_t c = tid; c < nsel; c += NT)
+        if (src(c) > T) mark(c);
+      // ties at T: the lowest block indices first (scan in index order)
       unsigned int taken = 0;
-      for (int64_t base = 0; base < cmax && taken < need_eq; base += kSelThreads) {
+      for (int64_t base = 0; base < cmax && taken < need_eq; base += NT) {
         const int64_t c = base + tid;
         int flag = 0;
         if (c < cmax) {
-          unsigned int key = cached ? cache[c] : krow[c];
+          const unsigned int key = cached ? cache[c] : krow[c];
           flag = key == T;
         }
         int tot;
-        int pre = block_exclusive_scan(flag, wave_sums, &tot);
+        int pre = block_exclusive_scan<NT>(flag, wave_sums, &tot);
         if (flag && taken + (unsigned int)pre < need_eq) atomicOr(&bits[c >> 5], 1u << (c & 31));
         taken += (unsigned int)tot;
       }
@@ -309,16 +445,16 @@ __global__ __launch_bounds__(kSelThreads) void route_select_kernel(
   int64_t lo = own - g.local;
   if (lo < 0) lo = 0;
   int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
-  for (int64_t c = lo + tid; c <= hi; c += kSelThreads) atomicOr(&bits[c >> 5], 1u << (c & 31));
+  for (int64_t c = lo + tid; c <= hi; c += NT) atomicOr(&bits[c >> 5], 1u << (c & 31));
   __syncthreads();
 
   // ascending compaction of the bitmap
-  const int wpt = (nwords + kSelThreads - 1) / kSelThreads;
+  const int wpt = (nwords + NT - 1) / NT;
   const int w0 = tid * wpt;
   int cnt = 0;
   for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
   int total;
-  int pos = block_exclusive_scan(cnt, wave_sums, &total);
+  int pos = block_exclusive_scan<NT>(cnt, wave_sums, &total);
   int32_t* out = kv_idx + (bh * g.nbq + i) * W;
   for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
     unsigned int m = bits[w];
@@ -330,7 +466,7 @@ __global__ __launch_bounds__(kSelThreads) void route_select_kernel(
     }
   }
   const int64_t num = total < W ? total : W;
-  for (int64_t p = num + tid; p < W; p += kSelThreads) out[p] = 0;
+  for (int64_t p = num + tid; p < W; p += NT) out[p] = 0;
   if (tid == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
@@ -358,7 +494,7 @@ __global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
   int cnt = 0;
   for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(bits[w]);
   int total;
-  int pre = block_exclusive_scan(cnt, wave_sums, &total);
+  int pre = block_exclusive_scan<kSelThreads>(cnt, wave_sums, &total);
   for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
     wpre[w] = (unsigned int)pre;
     pre += __popc(bits[w]);
@@ -432,7 +568,22 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     const int64_t imax = i0 + g.ni - 1;
     int64_t cmax_all = row_cmax(g, imax);
     const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
-    if (cand_tiles > 0) {
+    if (cand_tiles > 0 && R <= 16) {
+      int rp_log2 = 0;
+      while ((1 << rp_log2) < R) ++rp_log2;
+      const int64_t cpb = 256 >> rp_log2;
+      const int64_t nblk = (cmax_all + cpb - 1) / cpb;
+      SSA_REQUIRE(nblk < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
+                  "route: score grid too large");
+      dim3 grid((unsigned)nblk, (unsigned)(B * Hkv));
+      if (m3 != nullptr)
+        route_score_rows_kernel<true><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d,
+                                                                coef2, coef3, keys, rp_log2);
+      else
+        route_score_rows_kernel<false><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d,
+                                                                 coef2, coef3, keys, rp_log2);
+      SSA_TRY(launch_status("route_score_rows_kernel"));
+    } else if (cand_tiles > 0) {
       SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
                   "route: score grid too large");
       dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
@@ -446,7 +597,11 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     }
     const int64_t nrows = B * Hq * g.ni;
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
-    route_select_kernel<<<(unsigned)nrows, kSelThreads, 0, stream>>>(keys, g, kv_num, kv_idx, W);
+    if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
+      route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W);
+    else
+      route_select_kernel<kSelThreads><<<(unsigned)nrows, kSelThreads, 0, stream>>>(keys, g, kv_num,
+                                                                                  kv_idx, W);
     SSA_TRY(launch_status("route_select_kernel"));
   }
   return SSA_OK;

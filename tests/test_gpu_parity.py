@@ -128,6 +128,35 @@ def test_route_ties_take_lowest_index(cuda):
         assert s == frozenset(list(range(min(3, i))) + [i]), (i, s)
 
 
+@pytest.mark.parametrize("case", ["random", "top_ties", "all_equal"])
+def test_route_long_rows_match_oracle(cuda, case):
+    """Rows with more candidates than fit in LDS (12000 key blocks): the filtered select (random
+    scores), its tie handling (100 identical best blocks, 64 kept: lowest indices) and the
+    fallback when the filter keeps too much (all scores equal)."""
+    rng = np.random.default_rng(21)
+    nbk, d, block = 12000, 64, 64
+    mu = rng.standard_normal((1, 1, nbk, d)).astype(np.float32)
+    var = rng.uniform(0.5, 1.5, (1, 1, nbk, d)).astype(np.float32)
+    rows = rng.standard_normal((1, 2, 3, d)).astype(np.float32)
+    if case == "top_ties":
+        best = rng.choice(nbk, 100, replace=False)
+        mu[0, 0, best] = 3.0 * rows[0, 0, 0] / np.linalg.norm(rows[0, 0, 0])
+        var[0, 0, best] = 1.0
+    elif case == "all_equal":
+        mu[:] = mu[0, 0, 0]
+        var[:] = var[0, 0, 0]
+    pos0 = nbk * block - 3
+    kv_num, kv_idx = K.route(dev(rows, torch.float32, cuda), dev(mu, torch.float32, cuda),
+                             dev(var, torch.float32, cuda), None, "query", 64, 0.0, 1, 1.0,
+                             query_pos=pos0, block=block)
+    gn, gi = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    keys = O.score_keys(O.scores(rows, mu, var, 1.0))
+    for h in range(2):
+        for r in range(3):
+            sel = O.select_row(keys[0, h, r], r, "query", 64, 0.0, 1, pos0, block)
+            assert gi[0, h, r, :gn[0, h, r]].tolist() == sel, (case, h, r)
+
+
 def test_route_reference_dense_outputs(cuda):
     """Default (non-compact) returns the reference's (kv_num, argsort-order kv_idx, sel)."""
     rng = np.random.default_rng(10)
