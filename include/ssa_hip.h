@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 1
+#define SSA_ABI_VERSION 2
 
 typedef void* ssa_stream_t; /* hipStream_t */
 
@@ -113,6 +113,28 @@ int ssa_route(const float* rows, const float* mu, const float* var, const float*
               int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
               void* workspace, size_t workspace_bytes, ssa_stream_t stream);
+
+/*
+ * Sub-block routing (block_route_budget(sub=...), ssa/ssa_kernel.py:74-78,100): mu/var/m3 hold
+ * nbk*pool sub-block summaries (B, Hkv, nbk*pool, d); each candidate key block scores as the max
+ * of its pool sub-block scores, then selection proceeds as in ssa_route over nbk blocks.
+ * The workspace needs ssa_route_workspace_size(B, Hq, nbq, nbk * pool) bytes for one pass
+ * (any multiple of ssa_route_workspace_size(B, Hq, 1, nbk * pool) works). pool = 1 is ssa_route.
+ */
+int ssa_route_pooled(const float* rows, const float* mu, const float* var, const float* m3,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t pool,
+                     int64_t d, int mode, int64_t top_c, float budget_frac, int64_t local,
+                     float coef2, float coef3, int64_t query_pos, int64_t block, int32_t* kv_num,
+                     int32_t* kv_idx, int64_t W, void* workspace, size_t workspace_bytes,
+                     ssa_stream_t stream);
+
+/*
+ * Low-dimensional routing (block_route_budget(proj=...), ssa/ssa_kernel.py:92-94): out (rows,
+ * dout) = x (rows, din) @ w (din, dout), fp32 in and out, accumulated in fp64 and rounded once.
+ * Used for q_mean @ W_q and mu @ W_k before a centroid-only route (coef2 = 0).
+ */
+int ssa_project_rows(const float* x, const float* w, int64_t rows, int64_t din, int64_t dout,
+                     float* out, ssa_stream_t stream);
 
 /*
  * Expands compact lists to the reference's dense forms (ssa/ssa_kernel.py:117-118):

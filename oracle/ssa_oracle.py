@@ -197,13 +197,35 @@ def compact(sel_lists, W: int | None = None):
     return kv_num, kv_idx
 
 
+def project(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """fl32(x @ w) with the products summed in float64 (x (..., din), w (din, dout)): the
+    projections qb @ W_q and mu @ W_k of ssa/ssa_kernel.py:92-94, rounded once."""
+    return (x.astype(np.float64) @ np.asarray(w, dtype=np.float64)).astype(np.float32)
+
+
+def pool_max(r: np.ndarray, pool: int) -> np.ndarray:
+    """Max over each run of `pool` consecutive sub-block scores (last axis): the max-pool
+    rs.view(..., nb, spb).amax(-1) of ssa/ssa_kernel.py:100 (NaN propagates like torch.amax)."""
+    if pool == 1:
+        return r
+    return r.reshape(*r.shape[:-1], r.shape[-1] // pool, pool).max(-1)
+
+
 def route_budget(q, k, block, budget_frac=0.25, top_c=None, local=1, beta=2.0, edgeworth=False,
-                 n_real=None):
+                 n_real=None, sub=None, proj=None):
     """block_route_budget (ssa/ssa_kernel.py:61-119) -> (kv_num, kv_idx compact). q (B,Hq,n,d),
-    k (B,Hkv,n,d), query head h reads key head h // (Hq/Hkv)."""
+    k (B,Hkv,n,d), query head h reads key head h // (Hq/Hkv). `sub`: key summaries over
+    sub-blocks of that size, scores max-pooled to the block (:74-78,100). `proj`: a (d, d')
+    matrix or a pair (W_q, W_k); the score is then <qb W_q, mu W_k> only (:92-94)."""
     qb = qmean(q, block)
-    mu, var, m3 = block_stats(k, block, "pop", n_real)
-    r = scores(qb, mu, var, 0.5 * beta, m3 if edgeworth else None, beta ** 2 / 6.0)
+    sub_sz = block if sub is None else int(sub)
+    mu, var, m3 = block_stats(k, sub_sz, "pop", n_real)
+    if proj is not None:
+        wq, wk = proj if isinstance(proj, tuple) else (proj, proj)
+        r = scores(project(qb, wq), project(mu, wk), None, 0.0)
+    else:
+        r = scores(qb, mu, var, 0.5 * beta, m3 if edgeworth else None, beta ** 2 / 6.0)
+    r = pool_max(r, block // sub_sz)
     return compact(select_rows(r, "budget", top_c, budget_frac, local))
 
 

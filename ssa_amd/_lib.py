@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
@@ -41,6 +41,10 @@ _SIGNATURES = {
     "ssa_route": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                            _c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64, _c_i64, _c_p, _c_p,
                            _c_i64, _c_p, _c_sz, _c_p]),
+    "ssa_route_pooled": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                  _c_i64, _c_i64, _c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64,
+                                  _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_sz, _c_p]),
+    "ssa_project_rows": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "ssa_expand_selection": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "ssa_sparse_attn_workspace_size": (_c_sz, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ssa_transpose_v": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -25,8 +25,8 @@ int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t
 int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
                int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
                int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
-               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
-               void* workspace, size_t workspace_bytes, hipStream_t stream);
+               int64_t query_pos, int64_t block, int64_t pool, int32_t* kv_num, int32_t* kv_idx,
+               int64_t W, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 namespace {
 
@@ -455,7 +455,7 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
 
   // 3. route the queries over the complete blocks
   SSA_TRY(route_impl(qf, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
-                     budget_frac, local, coef2, 0.0f, pos, block, kv_num, kv_idx, W, keys,
+                     budget_frac, local, coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys,
                      key_bytes, st));
 
   // 4. attend

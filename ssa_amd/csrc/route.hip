@@ -40,6 +40,7 @@ struct RouteGeom {
   int64_t top_c;
   float budget_frac;
   int64_t local;
+  int64_t pool;  // scored candidates per key block (sub-blocks max-pooled to the block; 1 = none)
 };
 
 // Number of candidates of query row i: budget -> c < i, flat -> c <= i, query -> complete blocks.
@@ -50,6 +51,11 @@ __host__ __device__ inline int64_t row_cmax(const RouteGeom& g, int64_t i) {
   else c = (g.query_pos + i + 1) / g.block;
   if (c > g.nbk) c = g.nbk;
   return c < 0 ? 0 : c;
+}
+
+// scored candidates of row i (sub-block units)
+__host__ __device__ inline int64_t row_cmax_s(const RouteGeom& g, int64_t i) {
+  return row_cmax(g, i) * g.pool;
 }
 
 __host__ __device__ inline int64_t row_own(const RouteGeom& g, int64_t i) {
@@ -86,7 +92,8 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   if (r0 >= R) return;
   int64_t r_last = r0 + kTile - 1 < R ? r0 + kTile - 1 : R - 1;
   const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
-  if (c0 >= row_cmax(g, imax)) return;  // uniform: no row of the tile has these candidates
+  if (c0 >= row_cmax_s(g, imax)) return;  // uniform: no row of the tile has these candidates
+  const int64_t nbs = g.nbk * g.pool;     // scored candidates per key row
 
   const int tid = threadIdx.x;
   const int tr = tid / 16, tc = tid % 16;
@@ -100,9 +107,9 @@ __global__ __launch_bounds__(256) void route_score_kernel(
       if constexpr (EDGE) e3[a][c] = 0.0;
     }
 
-  const float* kv_mu = mu + (bk * g.nbk) * d;
-  const float* kv_var = var ? var + (bk * g.nbk) * d : nullptr;
-  const float* kv_m3 = EDGE ? m3 + (bk * g.nbk) * d : nullptr;
+  const float* kv_mu = mu + (bk * nbs) * d;
+  const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
+  const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
 
   for (int k0 = 0; k0 < d; k0 += kDK) {
     __syncthreads();
@@ -122,7 +129,7 @@ __global__ __launch_bounds__(256) void route_score_kernel(
       if constexpr (EDGE) Q3s[kk][rr] = q2 * q;
       const int64_t c = c0 + rr;
       float m = 0.0f, v = 0.0f, t = 0.0f;
-      if (c < g.nbk && kin) {
+      if (c < nbs && kin) {
         m = kv_mu[c * d + k0 + kk];
         if (kv_var) v = kv_var[c * d + k0 + kk];
         if constexpr (EDGE) t = kv_m3[c * d + k0 + kk];
@@ -170,8 +177,8 @@ __global__ __launch_bounds__(256) void route_score_kernel(
     if (r >= R) continue;
     const int64_t h = kvh * g.G + r / g.ni;
     const int64_t il = r % g.ni;
-    const int64_t cmax = row_cmax(g, g.i0 + il);
-    unsigned int* krow = keys + ((b * g.Hq + h) * g.ni + il) * g.nbk;
+    const int64_t cmax = row_cmax_s(g, g.i0 + il);
+    unsigned int* krow = keys + ((b * g.Hq + h) * g.ni + il) * nbs;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int64_t cand = c0 + tc + 16 * c;
@@ -208,15 +215,16 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
   const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
   const int64_t R = g.G * g.ni;
   const int64_t c0 = (int64_t)blockIdx.x * CPB;
-  if (c0 >= row_cmax(g, g.i0 + g.ni - 1)) return;  // uniform: beyond every row's candidates
+  if (c0 >= row_cmax_s(g, g.i0 + g.ni - 1)) return;  // uniform: beyond every row's candidates
+  const int64_t nbs = g.nbk * g.pool;
   const int tid = threadIdx.x;
   const int r = tid & (RP - 1);
   const int cl = tid >> rp_log2;
   const int64_t c = c0 + cl;
 
-  const float* kv_mu = mu + (bk * g.nbk) * d;
-  const float* kv_var = var ? var + (bk * g.nbk) * d : nullptr;
-  const float* kv_m3 = EDGE ? m3 + (bk * g.nbk) * d : nullptr;
+  const float* kv_mu = mu + (bk * nbs) * d;
+  const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
+  const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
   double e1 = 0.0, e2 = 0.0, e3 = 0.0;
   for (int k0 = 0; k0 < d; k0 += kDK) {
     __syncthreads();
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
       const int cc = idx / kDK, kk = idx % kDK;
       const int64_t cand = c0 + cc;
       float m = 0.0f, v = 0.0f, t = 0.0f;
-      if (cand < g.nbk && k0 + kk < d) {
+      if (cand < nbs && k0 + kk < d) {
         m = kv_mu[cand * d + k0 + kk];
         if (kv_var) v = kv_var[cand * d + k0 + kk];
         if constexpr (EDGE) t = kv_m3[cand * d + k0 + kk];
@@ -257,10 +265,10 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
   if (r >= R) return;
   const int64_t h = kvh * g.G + r / g.ni;
   const int64_t il = r % g.ni;
-  if (c >= row_cmax(g, g.i0 + il)) return;
+  if (c >= row_cmax_s(g, g.i0 + il)) return;
   float s = __fadd_rn((float)e1, __fmul_rn(coef2, (float)e2));
   if constexpr (EDGE) s = __fadd_rn(s, __fmul_rn(coef3, (float)e3));
-  keys[((b * g.Hq + h) * g.ni + il) * g.nbk + c] = score_key(s);
+  keys[((b * g.Hq + h) * g.ni + il) * nbs + c] = score_key(s);
 }
 
 // Block-wide exclusive scan of one int per thread (NT threads); returns the exclusive prefix
@@ -311,13 +319,24 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   const int64_t cmax = row_cmax(g, i);
   int64_t keep = row_keep(g, cmax);
   const int64_t K = keep < cmax ? keep : cmax;
-  const unsigned int* krow = keys + lrow * g.nbk;
+  const unsigned int* kraw = keys + lrow * g.nbk * g.pool;
+  // key of block c: the largest of its pool sub-block keys (keys order like the scores, so this is
+  // the key of the max-pooled score)
+  auto krow = [&](int64_t c) -> unsigned int {
+    if (g.pool == 1) return kraw[c];
+    unsigned int m = kraw[c * g.pool];
+    for (int64_t t = 1; t < g.pool; ++t) {
+      const unsigned int x = kraw[c * g.pool + t];
+      m = x > m ? x : m;
+    }
+    return m;
+  };
   const int nwords = (int)((g.nbk + 31) / 32);
 
   for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
   const bool cached = cmax <= kCacheKeys;  // whole row in LDS, index order
   if (cached && K > 0 && K < cmax)
-    for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow[c];
+    for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow(c);
   if (tid == 0) {
     sh_min = 0xffffffffu;
     sh_ncand = 0u;
@@ -333,7 +352,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
     unsigned int mx = 0u;
     for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = krow[c];
+      const unsigned int key = krow(c);
       mx = key > mx ? key : mx;
     }
     for (int off = 1; off < gs; off <<= 1) {
@@ -349,7 +368,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     __syncthreads();
     const unsigned int t0 = sh_min;
     for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = krow[c];
+      const unsigned int key = krow(c);
       if (key >= t0) {
         const unsigned int slot = atomicAdd(&sh_ncand, 1u);
         if (slot < (unsigned int)kCand) {
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     }
   }
   const bool src_lds = cached || filt;
-  auto src = [&](int64_t c) -> unsigned int { return src_lds ? cache[c] : krow[c]; };
+  auto src = [&](int64_t c) -> unsigned int { return src_lds ? cache[c] : krow(c); };
   auto mark = [&](int64_t c) {
     const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
     atomicOr(&bits[blk >> 5], 1u << (blk & 31));
@@ -429,7 +448,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
         const int64_t c = base + tid;
         int flag = 0;
         if (c < cmax) {
-          const unsigned int key = cached ? cache[c] : krow[c];
+          const unsigned int key = cached ? cache[c] : krow(c);
           flag = key == T;
         }
         int tot;
@@ -512,15 +531,30 @@ __global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
   }
 }
 
+// out[r][j] = fl32(sum_k x[r][k] * w[k][j]), accumulated in fp64 over k ascending (one rounding):
+// the projection of query-block means and key-block means for low-dimensional routing.
+__global__ __launch_bounds__(256) void project_rows_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ w,
+                                                           int64_t rows, int64_t din,
+                                                           int64_t dout, float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * dout) return;
+  const int64_t r = idx / dout, j = idx % dout;
+  double acc = 0.0;
+  for (int64_t k = 0; k < din; ++k) acc = fma((double)x[r * din + k], (double)w[k * dout + j], acc);
+  out[idx] = (float)acc;
+}
+
 }  // namespace
 
 // Routes every row; exposed to the decode step, which calls it with a single query row.
 int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
                int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
                int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
-               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
-               void* workspace, size_t workspace_bytes, hipStream_t stream) {
+               int64_t query_pos, int64_t block, int64_t pool, int32_t* kv_num, int32_t* kv_idx,
+               int64_t W, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SSA_REQUIRE(rows && mu && kv_num && kv_idx, SSA_ERR_INVALID, "route: NULL pointer argument");
+  SSA_REQUIRE(pool >= 1 && pool <= 64, SSA_ERR_INVALID, "route: pool must be in [1, 64]");
   SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && nbq > 0 && nbk > 0 && d > 0, SSA_ERR_INVALID,
               "route: sizes must be positive");
   SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "route: Hq=%lld not a multiple of Hkv=%lld",
@@ -539,7 +573,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
   const int64_t needW = ssa_route_width(mode, nbq, nbk, top_c, budget_frac, local, query_pos, block);
   SSA_REQUIRE(W >= needW, SSA_ERR_INVALID, "route: W=%lld below the required width %lld",
               (long long)W, (long long)needW);
-  const size_t row_bytes = (size_t)nbk * 4;
+  const size_t row_bytes = (size_t)nbk * (size_t)pool * 4;
   const size_t rows_per_i = (size_t)(B * Hq);
   SSA_REQUIRE(workspace != nullptr && workspace_bytes >= row_bytes * rows_per_i,
               SSA_ERR_WORKSPACE, "route: workspace of %zu bytes below the minimum %zu",
@@ -559,6 +593,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
   g.top_c = top_c;
   g.budget_frac = budget_frac;
   g.local = local;
+  g.pool = pool;
   unsigned int* keys = static_cast<unsigned int*>(workspace);
   for (int64_t i0 = 0; i0 < nbq; i0 += chunk) {
     g.i0 = i0;
@@ -566,7 +601,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     const int64_t R = g.G * g.ni;
     const int64_t row_tiles = (R + kTile - 1) / kTile;
     const int64_t imax = i0 + g.ni - 1;
-    int64_t cmax_all = row_cmax(g, imax);
+    const int64_t cmax_all = row_cmax_s(g, imax);  // scored candidates (sub-block units)
     const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
     if (cand_tiles > 0 && R <= 16) {
       int rp_log2 = 0;
@@ -621,6 +656,7 @@ extern "C" int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t t
   g.local = local < 0 ? 0 : local;
   g.query_pos = query_pos;
   g.block = block > 0 ? block : 1;
+  g.pool = 1;
   int64_t w = 1;
   // keep is monotone in cmax, and cmax is monotone in the row index: the last row is the widest
   // unless clipping by nbk makes several rows equal (still bounded by the last row).
@@ -645,8 +681,31 @@ extern "C" int ssa_route(const float* rows, const float* mu, const float* var, c
                          int32_t* kv_idx, int64_t W, void* workspace, size_t workspace_bytes,
                          ssa_stream_t stream) {
   return ssa::route_impl(rows, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c, budget_frac,
-                         local, coef2, coef3, query_pos, block, kv_num, kv_idx, W, workspace,
+                         local, coef2, coef3, query_pos, block, 1, kv_num, kv_idx, W, workspace,
                          workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ssa_route_pooled(const float* rows, const float* mu, const float* var,
+                                const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq,
+                                int64_t nbk, int64_t pool, int64_t d, int mode, int64_t top_c,
+                                float budget_frac, int64_t local, float coef2, float coef3,
+                                int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx,
+                                int64_t W, void* workspace, size_t workspace_bytes,
+                                ssa_stream_t stream) {
+  return ssa::route_impl(rows, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c, budget_frac,
+                         local, coef2, coef3, query_pos, block, pool, kv_num, kv_idx, W,
+                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ssa_project_rows(const float* x, const float* w, int64_t rows, int64_t din,
+                                int64_t dout, float* out, ssa_stream_t stream) {
+  SSA_REQUIRE(x && w && out, SSA_ERR_INVALID, "project_rows: NULL pointer argument");
+  SSA_REQUIRE(rows > 0 && din > 0 && dout > 0, SSA_ERR_INVALID, "project_rows: bad sizes");
+  const int64_t total = rows * dout;
+  SSA_REQUIRE((total + 255) / 256 < (1ll << 31), SSA_ERR_UNSUPPORTED, "project_rows: too large");
+  ssa::project_rows_kernel<<<(unsigned)((total + 255) / 256), 256, 0,
+                             static_cast<hipStream_t>(stream)>>>(x, w, rows, din, dout, out);
+  return ssa::launch_status("project_rows_kernel");
 }
 
 extern "C" int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t rows,

@@ -85,16 +85,21 @@ def route_width(mode: str, nbq: int, nbk: int, top_c: int | None, budget_frac: f
 def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: torch.Tensor | None,
           mode: str, top_c: int | None, budget_frac: float, local: int, coef2: float,
           coef3: float = 0.0, query_pos: int = 0, block: int = 1,
-          workspace_limit: int = 1 << 30):
+          workspace_limit: int = 1 << 30, pool: int = 1):
     """Cumulant router over precomputed summaries -> compact (kv_num, kv_idx).
 
     rows (B, Hq, nbq, d) fp32: query-block means (mode "budget"/"flat") or query vectors
-    ("query", row r at absolute position query_pos + r). mu/var/m3 (B, Hkv, nbk, d) fp32.
-    Returns kv_num (B, Hq, nbq) int32 and kv_idx (B, Hq, nbq, W) int32 (ascending, padded 0).
+    ("query", row r at absolute position query_pos + r). mu/var/m3 (B, Hkv, nbk*pool, d) fp32:
+    with pool > 1 they are sub-block summaries and a key block scores as the max of its pool
+    sub-blocks (ssa/ssa_kernel.py:100). Returns kv_num (B, Hq, nbq) int32 and
+    kv_idx (B, Hq, nbq, W) int32 (ascending, padded 0).
     """
     _lib.require_device(rows, mu, var, m3)
     B, Hq, nbq, d = rows.shape
-    Hkv, nbk = mu.shape[1], mu.shape[2]
+    Hkv, nbs = mu.shape[1], mu.shape[2]
+    if pool < 1 or nbs % pool:
+        raise ValueError(f"route: {nbs} summaries are not a multiple of pool={pool}")
+    nbk = nbs // pool
     rows, mu = rows.contiguous(), mu.contiguous()
     var = None if var is None else var.contiguous()
     m3 = None if m3 is None else m3.contiguous()
@@ -102,16 +107,32 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
     dev = rows.device
     kv_num = torch.empty(B, Hq, nbq, device=dev, dtype=torch.int32)
     kv_idx = torch.empty(B, Hq, nbq, W, device=dev, dtype=torch.int32)
-    full = int(_lib.query("ssa_route_workspace_size", B, Hq, nbq, nbk))
-    per_i = int(_lib.query("ssa_route_workspace_size", B, Hq, 1, nbk))
+    full = int(_lib.query("ssa_route_workspace_size", B, Hq, nbq, nbs))
+    per_i = int(_lib.query("ssa_route_workspace_size", B, Hq, 1, nbs))
     ws_bytes = max(per_i, min(full, workspace_limit // per_i * per_i))
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-    _lib.call("ssa_route", rows.data_ptr(), mu.data_ptr(), _lib.ptr(var), _lib.ptr(m3), B, Hq, Hkv,
-              nbq, nbk, d, _ROUTE_MODES[mode], -1 if top_c is None else int(top_c),
-              float(budget_frac), int(local), float(coef2), float(coef3), int(query_pos),
-              int(block), kv_num.data_ptr(), kv_idx.data_ptr(), W, ws.data_ptr(), ws_bytes,
-              _lib.stream_of(rows))
+    _lib.call("ssa_route_pooled", rows.data_ptr(), mu.data_ptr(), _lib.ptr(var), _lib.ptr(m3), B,
+              Hq, Hkv, nbq, nbk, int(pool), d, _ROUTE_MODES[mode],
+              -1 if top_c is None else int(top_c), float(budget_frac), int(local), float(coef2),
+              float(coef3), int(query_pos), int(block), kv_num.data_ptr(), kv_idx.data_ptr(), W,
+              ws.data_ptr(), ws_bytes, _lib.stream_of(rows))
     return kv_num, kv_idx
+
+
+def project_rows(x: torch.Tensor, w) -> torch.Tensor:
+    """x (..., din) fp32 @ w (din, dout) -> (..., dout) fp32, accumulated in fp64 and rounded once
+    (the projections of ssa/ssa_kernel.py:92-94)."""
+    _lib.require_device(x)
+    w = torch.as_tensor(w, dtype=torch.float32, device=x.device).contiguous()
+    din, dout = w.shape
+    if x.shape[-1] != din:
+        raise ValueError(f"project_rows: x has {x.shape[-1]} columns, w has {din} rows")
+    xc = x.float().contiguous()
+    rows = xc.numel() // din
+    out = torch.empty(*x.shape[:-1], dout, device=x.device, dtype=torch.float32)
+    _lib.call("ssa_project_rows", xc.data_ptr(), w.data_ptr(), rows, din, dout, out.data_ptr(),
+              _lib.stream_of(x))
+    return out
 
 
 def expand_selection(kv_num: torch.Tensor, kv_idx: torch.Tensor, nbk: int):
@@ -226,22 +247,28 @@ def block_route_budget(q, k, block=BLOCK, budget_frac=0.25, top_c=None, local=1,
     """Budget router with gemma_ssa's semantics: per query block i keep the top
     ceil(budget_frac·i) (or `top_c`) strictly-past key blocks by <q̄,μ> + ½β<q̄²,σ²>
     (+ β²/6<q̄³,m3> if edgeworth), always OR the own block + `local` predecessors.
-    `n_real` excludes pad keys from the block statistics. Returns (kv_num, kv_idx, sel).
+    `n_real` excludes pad keys from the block statistics. `sub` scores sub-blocks of that size and
+    max-pools them to the block; `proj` (a (d, d') matrix, or an object with W_q / W_k) routes
+    by the centroid score of the projected q̄ and μ. Returns (kv_num, kv_idx, sel).
     Reference: ssa/ssa_kernel.py:61-119."""
-    if proj is not None:
-        raise NotImplementedError("block_route_budget(proj=...) low-dimensional routing is not "
-                                  "implemented by ssa_amd")
-    if sub is not None and sub != block:
-        raise NotImplementedError("block_route_budget(sub=...) sub-block max-pooling is not "
-                                  "implemented by ssa_amd")
     B, H, n, d = q.shape
     if n % block:
         raise RuntimeError(f"block_route_budget: n={n} is not a multiple of block={block}")
     nb = n // block
+    sub_sz = block if sub is None else int(sub)
+    if sub_sz <= 0 or block % sub_sz:
+        raise RuntimeError(f"block_route_budget: sub={sub} does not divide block={block}")
+    pool = block // sub_sz  # sub-blocks per block, max-pooled (ssa/ssa_kernel.py:74-78,100)
     qbar = block_summary(q, block, "qmean")
-    mu, var, m3 = block_summary(k, block, "pop", n_real=n_real, with_m3=edgeworth)
-    kv_num, kv_idx = route(qbar, mu, var, m3, "budget", top_c, float(budget_frac), int(local),
-                           0.5 * beta, beta ** 2 / 6.0)
+    mu, var, m3 = block_summary(k, sub_sz, "pop", n_real=n_real,
+                                with_m3=edgeworth and proj is None)
+    if proj is not None:  # centroid score in the projected space (ssa/ssa_kernel.py:92-94)
+        wq, wk = (proj.W_q, proj.W_k) if hasattr(proj, "W_q") else (proj, proj)
+        kv_num, kv_idx = route(project_rows(qbar, wq), project_rows(mu, wk), None, None, "budget",
+                               top_c, float(budget_frac), int(local), 0.0, pool=pool)
+    else:
+        kv_num, kv_idx = route(qbar, mu, var, m3, "budget", top_c, float(budget_frac), int(local),
+                               0.5 * beta, beta ** 2 / 6.0, pool=pool)
     return _finish(kv_num, kv_idx, nb, compact)
 
 

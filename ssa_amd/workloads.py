@@ -136,6 +136,13 @@ def make(name: str, variant: str = "segmented", n: int | None = None):
     return {"cfg": cfg, "q": q, "k": k, "v": v, "needles": needles, "variant": variant}
 
 
+def proj_matrix(seed: int, din: int = 64, dout: int = 16) -> np.ndarray:
+    """Seeded routing projection (din, dout) float32 for block_route_budget(proj=...) cases:
+    N(0,1) / sqrt(din) from default_rng(seed)."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((din, dout)) / np.sqrt(din)).astype(np.float32)
+
+
 def to_device(x: np.ndarray, dtype: torch.dtype, device="cuda") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dtype)
 

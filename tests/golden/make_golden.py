@@ -18,6 +18,7 @@ from __future__ import annotations
 import hashlib
 import sys
 import time
+from types import SimpleNamespace
 from pathlib import Path
 
 import numpy as np
@@ -68,12 +69,19 @@ def route_case(name, cfg_name, variant="segmented", **kw):
     G = cfg.Hq // cfg.Hkv
     kk = repeat_kv(k, G) if G > 1 else k
     fn = kw.pop("fn", "budget")
+    rk = dict(kw)
+    if "proj_seed" in rk:      # one seeded (d, 16) projection used for queries and keys
+        rk["proj"] = torch.from_numpy(WL.proj_matrix(rk.pop("proj_seed"), cfg.d))
+    if "proj_pair_seed" in rk:  # an object with W_q / W_k (the trained-projection form)
+        s0 = rk.pop("proj_pair_seed")
+        rk["proj"] = SimpleNamespace(W_q=torch.from_numpy(WL.proj_matrix(s0, cfg.d)),
+                                     W_k=torch.from_numpy(WL.proj_matrix(s0 + 1, cfg.d)))
     t0 = time.time()
     with torch.no_grad():
         if fn == "budget":
-            kv_num, kv_idx, _ = RK.block_route_budget(q, kk, cfg.block, **kw)
+            kv_num, kv_idx, _ = RK.block_route_budget(q, kk, cfg.block, **rk)
         else:
-            kv_num, kv_idx, _ = RK.block_route(q, kk, cfg.block, **kw)
+            kv_num, kv_idx, _ = RK.block_route(q, kk, cfg.block, **rk)
     kn, ki = compact_from_full(kv_num, kv_idx)
     np.savez_compressed(HERE / f"{name}.npz", kv_num=kn, kv_idx=ki,
                         inputs_sha256=np.array(sha(p["q"], p["k"])),
@@ -170,6 +178,11 @@ CASES = {
                                         beta=2.0),
     "c3_budget_lit": lambda: route_case("c3_budget_lit", "C3", "literal", top_c=64, local=2,
                                         beta=2.0),
+    "c1_sub16": lambda: route_case("c1_sub16", "C1", top_c=8, local=1, beta=2.0, sub=16),
+    "c2_sub16": lambda: route_case("c2_sub16", "C2", top_c=32, local=2, beta=2.0, sub=16),
+    "c1_proj": lambda: route_case("c1_proj", "C1", top_c=8, local=1, proj_seed=31),
+    "c2_proj_pair": lambda: route_case("c2_proj_pair", "C2", top_c=32, local=2,
+                                       proj_pair_seed=41),
     "c4_query": lambda: query_case("c4_query"),
     "c1_flex_out": lambda: flex_case("c1_flex_out"),
     "analytic_gqa": lambda: analytic_case("analytic_gqa"),

@@ -17,7 +17,8 @@ from ssa_amd import ivf_decode as D
 from ssa_amd import ssa_kernel as K
 from ssa_amd import workloads as WL
 from tests import golden_util as GU
-from tests.test_oracle import ROUTE_CASES, certificate_inputs, oracle_route
+from tests.test_oracle import (ROUTE_CASES, certificate_d, certificate_inputs, oracle_route,
+                               resolve_kw)
 
 pytestmark = pytest.mark.gpu
 
@@ -71,6 +72,7 @@ def test_block_summary_strided_input(cuda):
 
 def gpu_route(p, mode, kw, cuda):
     cfg = p["cfg"]
+    kw = resolve_kw(cfg, kw, pair_as="object")
     q = dev(p["q"], cfg.dtype, cuda)
     k = dev(p["k"], cfg.dtype, cuda)
     if mode == "flat":
@@ -91,7 +93,8 @@ def test_route_bit_exact_vs_oracle_and_reference(cuda, case):
     assert (kv_num == onum).all()
     g = GU.load(case)
     r64, mag = certificate_inputs(p, mode, kw)
-    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag)
+    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag,
+                                                 d=certificate_d(p["cfg"], kw))
     print(f"{case}: {n} rows, {n_eq} identical to the reference, {n_cert} certified near-ties")
     assert not bad, bad[:3]
 
@@ -155,6 +158,44 @@ def test_route_long_rows_match_oracle(cuda, case):
         for r in range(3):
             sel = O.select_row(keys[0, h, r], r, "query", 64, 0.0, 1, pos0, block)
             assert gi[0, h, r, :gn[0, h, r]].tolist() == sel, (case, h, r)
+
+
+def test_block_route_budget_sub_identity_and_recall(cuda):
+    """sub=None is identical to the default; with centroid scores sub=32 finds a planted
+    coherent 32-key sub-block whose block mean is diluted (test_cascade_router.py:147-167)."""
+    rng = np.random.default_rng(23)
+    n, block = 8 * 128, 128
+    q = WL.round_to(rng.standard_normal((1, 1, n, 64)).astype(np.float32), torch.float16)
+    k = WL.round_to(rng.standard_normal((1, 1, n, 64)).astype(np.float32), torch.float16)
+    qt, kt = dev(q, torch.float16, cuda), dev(k, torch.float16, cuda)
+    a = K.block_route_budget(qt, kt, block, top_c=2, local=1)
+    b = K.block_route_budget(qt, kt, block, top_c=2, local=1, sub=None)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    u = rng.standard_normal(64)
+    u = (u / np.linalg.norm(u)).astype(np.float32)
+    q2, k2 = q.copy(), k.copy()
+    q2[0, 0, n - block:] = WL.round_to(u[None], torch.float16)   # last query block points at u
+    k2[0, 0, block:block + 32] = WL.round_to(u[None], torch.float16)  # block 1, sub-block 0
+    q2t, k2t = dev(q2, torch.float16, cuda), dev(k2, torch.float16, cuda)
+    qblk = (n - 1) // block
+    _, _, sub_sel = K.block_route_budget(q2t, k2t, block, top_c=1, local=0, sub=32, beta=0.0)
+    assert bool(sub_sel[0, 0, qblk, 1]), "sub-block routing should select the coherent block"
+    for beta in (0.0, 2.0):
+        on, oi = O.route_budget(q2, k2, block, top_c=1, local=0, sub=32, beta=beta)
+        gn, gi, _ = K.block_route_budget(q2t, k2t, block, top_c=1, local=0, sub=32, beta=beta,
+                                         compact=True)
+        assert (gn.cpu().numpy() == on).all() and (gi.cpu().numpy() == oi).all()
+
+
+def test_block_route_budget_proj_identity(cuda):
+    """proj = identity reproduces centroid-only (beta = 0) routing exactly
+    (test_share_route.py:27-37)."""
+    torch.manual_seed(0)
+    q = torch.randn(1, 1, 8 * 128, 64, device=cuda)
+    k = torch.randn_like(q)
+    a = K.block_route_budget(q, k, 128, top_c=3, local=1, proj=torch.eye(64))
+    b = K.block_route_budget(q, k, 128, top_c=3, local=1, beta=0.0)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[2], b[2])
 
 
 def test_route_reference_dense_outputs(cuda):

@@ -7,6 +7,7 @@
   budget == dense causal softmax, the needle known-answer test, the reference's invariants.
 """
 import math
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -24,11 +25,29 @@ ROUTE_CASES = {
     "c2_edgeworth": ("C2", "segmented", "budget", dict(top_c=32, local=2, beta=2.0, edgeworth=True)),
     "c3_budget_seg": ("C3", "segmented", "budget", dict(top_c=64, local=2, beta=2.0)),
     "c3_budget_lit": ("C3", "literal", "budget", dict(top_c=64, local=2, beta=2.0)),
+    "c1_sub16": ("C1", "segmented", "budget", dict(top_c=8, local=1, beta=2.0, sub=16)),
+    "c2_sub16": ("C2", "segmented", "budget", dict(top_c=32, local=2, beta=2.0, sub=16)),
+    "c1_proj": ("C1", "segmented", "budget", dict(top_c=8, local=1, proj_seed=31)),
+    "c2_proj_pair": ("C2", "segmented", "budget", dict(top_c=32, local=2, proj_pair_seed=41)),
 }
+
+
+def resolve_kw(cfg, kw, pair_as="tuple"):
+    """Case kwargs -> call kwargs: projection seeds become the seeded matrices (a (W_q, W_k)
+    tuple for the oracle, an object with W_q / W_k attributes like the reference accepts)."""
+    kw = dict(kw)
+    if "proj_seed" in kw:
+        kw["proj"] = WL.proj_matrix(kw.pop("proj_seed"), cfg.d)
+    if "proj_pair_seed" in kw:
+        s0 = kw.pop("proj_pair_seed")
+        wq, wk = WL.proj_matrix(s0, cfg.d), WL.proj_matrix(s0 + 1, cfg.d)
+        kw["proj"] = (wq, wk) if pair_as == "tuple" else SimpleNamespace(W_q=wq, W_k=wk)
+    return kw
 
 
 def oracle_route(p, mode, kw):
     cfg = p["cfg"]
+    kw = resolve_kw(cfg, kw)
     if mode == "flat":
         return O.route_flat(p["q"], p["k"], cfg.block, **kw)
     return O.route_budget(p["q"], p["k"], cfg.block, **kw)
@@ -40,10 +59,28 @@ def certificate_inputs(p, mode, kw):
     if mode == "flat":
         mu, var, _ = O.block_stats(p["k"], cfg.block, "unbiased")
         return O.exact_scores64(qb, mu, var, 0.5)
-    mu, var, m3 = O.block_stats(p["k"], cfg.block, "pop")
-    beta = kw.get("beta", 2.0)
-    return O.exact_scores64(qb, mu, var, 0.5 * beta, m3 if kw.get("edgeworth") else None,
-                            beta ** 2 / 6.0)
+    kw = resolve_kw(cfg, kw)
+    sub = kw.get("sub") or cfg.block
+    mu, var, m3 = O.block_stats(p["k"], sub, "pop")
+    if kw.get("proj") is not None:  # exact score of the unrounded projections
+        wq, wk = kw["proj"] if isinstance(kw["proj"], tuple) else (kw["proj"], kw["proj"])
+        G = cfg.Hq // cfg.Hkv
+        kh = np.arange(cfg.Hq) // G
+        qp, mp = qb.astype(np.float64) @ wq, (mu.astype(np.float64) @ wk)[:, kh]
+        qa, ma = np.abs(qb.astype(np.float64)) @ np.abs(wq), (np.abs(mu.astype(np.float64)) @ np.abs(wk))[:, kh]
+        r64 = np.einsum("bhid,bhcd->bhic", qp, mp)
+        mag = np.einsum("bhid,bhcd->bhic", qa, ma)
+    else:
+        beta = kw.get("beta", 2.0)
+        r64, mag = O.exact_scores64(qb, mu, var, 0.5 * beta, m3 if kw.get("edgeworth") else None,
+                                    beta ** 2 / 6.0)
+    pool = cfg.block // sub
+    return O.pool_max(r64, pool), O.pool_max(mag, pool)
+
+
+def certificate_d(cfg, kw):
+    """Length of the float32 dot products behind a case's scores (projections add d')."""
+    return cfg.d + (16 if ("proj_seed" in kw or "proj_pair_seed" in kw) else 0)
 
 
 @pytest.mark.parametrize("case", list(ROUTE_CASES))
@@ -54,7 +91,8 @@ def test_oracle_selection_matches_reference(case):
     assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"]), "generator drifted from the fixture"
     kv_num, kv_idx = oracle_route(p, mode, dict(kw))
     r64, mag = certificate_inputs(p, mode, kw)
-    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag)
+    n, n_eq, n_cert, bad = GU.compare_selections(kv_num, kv_idx, g["kv_num"], g["kv_idx"], r64, mag,
+                                                 d=certificate_d(p["cfg"], kw))
     print(f"{case}: {n} rows, {n_eq} identical, {n_cert} certified float32 near-ties")
     assert not bad, bad[:5]
     # the certificate must be rare: these inputs are not adversarial
@@ -241,3 +279,48 @@ def test_keys_order_and_special_values():
     assert k[2] == k[3]                                     # -0 == +0
     assert list(np.argsort(k[[0, 1, 3, 4, 5, 6, 7]], kind="stable")) == list(range(7))
     assert math.isnan(float(r[7])) and k[7] == np.uint32(0xFFFFFFFF)
+
+
+def test_oracle_sub_identity_and_planted_subblock():
+    """sub=None / sub=block are the default route; with centroid scores (beta = 0) sub=32 finds
+    a planted coherent 32-key sub-block whose block mean is diluted 4x (the reference's
+    test_cascade_router.py:147-167, which it skips; with beta = 2 the variance bonus of random
+    sub-blocks, ~|q|^2, hides the variance-free needle)."""
+    rng = np.random.default_rng(23)
+    n, block = 8 * 128, 128
+    q = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    a = O.route_budget(q, k, block, top_c=2, local=1)
+    for sub in (None, block):
+        b = O.route_budget(q, k, block, top_c=2, local=1, sub=sub)
+        assert (a[0] == b[0]).all() and (a[1] == b[1]).all()
+    u = rng.standard_normal(64)
+    u = (u / np.linalg.norm(u)).astype(np.float32)
+    q[0, 0, n - block:] = u
+    k[0, 0, block:block + 32] = u
+    qblk = (n - 1) // block
+    num, idx = O.route_budget(q, k, block, top_c=1, local=0, sub=32, beta=0.0)
+    assert idx[0, 0, qblk, :num[0, 0, qblk]].tolist() == [1, qblk]
+    qb = O.qmean(q, block)
+    mu, var, _ = O.block_stats(k, 32, "pop")
+    r = O.scores(qb, mu, var, 0.0)
+    # max-pooling by hand: the pooled score of block 1 is its best sub-block's score (~1), the
+    # block-mean score is diluted to ~1/4
+    assert O.pool_max(r, 4)[0, 0, qblk, 1] == r[0, 0, qblk, 4:8].max()
+    mub, _, _ = O.block_stats(k, block, "pop")
+    rb = O.scores(qb, mub, None, 0.0)
+    assert r[0, 0, qblk, 4] > 0.99 and 0.15 < rb[0, 0, qblk, 1] < 0.35
+
+
+def test_oracle_proj_identity_equals_centroid_routing():
+    """proj = I reproduces beta = 0 exactly (test_share_route.py:27-37); a projection to d'
+    columns equals routing on explicitly projected summaries."""
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 1, 8 * 128, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 8 * 128, 64)).astype(np.float32)
+    a = O.route_budget(q, k, 128, top_c=3, local=1, proj=np.eye(64, dtype=np.float32))
+    b = O.route_budget(q, k, 128, top_c=3, local=1, beta=0.0)
+    assert (a[0] == b[0]).all() and (a[1] == b[1]).all()
+    w = WL.proj_matrix(5)
+    qp = (q[0, 0].astype(np.float64) @ w)
+    assert np.array_equal(O.project(q[0, 0], w), qp.astype(np.float32))
