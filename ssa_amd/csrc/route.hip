@@ -76,12 +76,14 @@ __global__ __launch_bounds__(256) void route_score_kernel(
     const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
     unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
-  __shared__ float Qs[kDK][kTile + 1];
-  __shared__ float Q2s[kDK][kTile + 1];
-  __shared__ float Ms[kDK][kTile + 1];
-  __shared__ float Vs[kDK][kTile + 1];
-  __shared__ float Q3s[EDGE ? kDK : 1][kTile + 1];
-  __shared__ float M3s[EDGE ? kDK : 1][kTile + 1];
+  // operands staged as fp64 (converted once per element, not once per use)
+  constexpr int DK = 16;
+  __shared__ double Qs[DK][kTile + 1];
+  __shared__ double Q2s[DK][kTile + 1];
+  __shared__ double Ms[DK][kTile + 1];
+  __shared__ double Vs[DK][kTile + 1];
+  __shared__ double Q3s[EDGE ? DK : 1][kTile + 1];
+  __shared__ double M3s[EDGE ? DK : 1][kTile + 1];
 
   const int64_t bk = blockIdx.y;  // b * Hkv + kvh
   const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
@@ -111,10 +113,10 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
   const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
 
-  for (int k0 = 0; k0 < d; k0 += kDK) {
+  for (int k0 = 0; k0 < d; k0 += DK) {
     __syncthreads();
-    for (int idx = tid; idx < kTile * kDK; idx += 256) {
-      const int rr = idx / kDK, kk = idx % kDK;
+    for (int idx = tid; idx < kTile * DK; idx += 256) {
+      const int rr = idx / DK, kk = idx % DK;
       const int64_t r = r0 + rr;
       const bool kin = k0 + kk < d;
       float q = 0.0f;
@@ -123,10 +125,10 @@ __global__ __launch_bounds__(256) void route_score_kernel(
         const int64_t i = g.i0 + r % g.ni;
         q = rows[((b * g.Hq + h) * g.nbq + i) * d + k0 + kk];
       }
-      const float q2 = q * q;
-      Qs[kk][rr] = q;
-      Q2s[kk][rr] = q2;
-      if constexpr (EDGE) Q3s[kk][rr] = q2 * q;
+      const float q2 = q * q;  // rounded to fp32 like the reference's elementwise products
+      Qs[kk][rr] = (double)q;
+      Q2s[kk][rr] = (double)q2;
+      if constexpr (EDGE) Q3s[kk][rr] = (double)(q2 * q);
       const int64_t c = c0 + rr;
       float m = 0.0f, v = 0.0f, t = 0.0f;
       if (c < nbs && kin) {
@@ -134,20 +136,20 @@ __global__ __launch_bounds__(256) void route_score_kernel(
         if (kv_var) v = kv_var[c * d + k0 + kk];
         if constexpr (EDGE) t = kv_m3[c * d + k0 + kk];
       }
-      Ms[kk][rr] = m;
-      Vs[kk][rr] = v;
-      if constexpr (EDGE) M3s[kk][rr] = t;
+      Ms[kk][rr] = (double)m;
+      Vs[kk][rr] = (double)v;
+      if constexpr (EDGE) M3s[kk][rr] = (double)t;
     }
     __syncthreads();
-    const int kend = d - k0 < kDK ? d - k0 : kDK;
+    const int kend = d - k0 < DK ? d - k0 : DK;
     for (int kk = 0; kk < kend; ++kk) {
       double qd[4], q2d[4], md[4], vd[4];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        qd[a] = (double)Qs[kk][tr + 16 * a];
-        q2d[a] = (double)Q2s[kk][tr + 16 * a];
-        md[a] = (double)Ms[kk][tc + 16 * a];
-        vd[a] = (double)Vs[kk][tc + 16 * a];
+        qd[a] = Qs[kk][tr + 16 * a];
+        q2d[a] = Q2s[kk][tr + 16 * a];
+        md[a] = Ms[kk][tc + 16 * a];
+        vd[a] = Vs[kk][tc + 16 * a];
       }
 #pragma unroll
       for (int a = 0; a < 4; ++a)
@@ -160,8 +162,8 @@ __global__ __launch_bounds__(256) void route_score_kernel(
         double q3d[4], td[4];
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          q3d[a] = (double)Q3s[kk][tr + 16 * a];
-          td[a] = (double)M3s[kk][tc + 16 * a];
+          q3d[a] = Q3s[kk][tr + 16 * a];
+          td[a] = M3s[kk][tc + 16 * a];
         }
 #pragma unroll
         for (int a = 0; a < 4; ++a)
