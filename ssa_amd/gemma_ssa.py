@@ -23,12 +23,13 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, fields
+from types import SimpleNamespace
 
 import torch
 
 from . import _lib
 from .ivf_decode import attend_rows
-from .ssa_kernel import block_summary, route, sparse_attention
+from .ssa_kernel import block_summary, project_rows, route, sparse_attention
 
 
 @dataclass
@@ -65,16 +66,32 @@ def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
     return x[:, :, None, :, :].expand(b, h, n, s, d).reshape(b, h * n, s, d)
 
 
+def load_projection(path, device="cuda"):
+    """A trained routing projection saved as {"W_q": (d, d'), "W_k": (d, d'), "meta": {...}} by the
+    reference's RoutingProjection.save (ssa/routing_space.py:43-51), loaded with weights_only=True
+    (nothing in the file is executed). Returns an object with W_q / W_k (fp32, on `device`)."""
+    d = torch.load(path, map_location=device, weights_only=True)
+    return SimpleNamespace(W_q=d["W_q"].to(device).float(), W_k=d["W_k"].to(device).float(),
+                           meta=d.get("meta", {}))
+
+
 def _block_lists(query, key, cfg, dense, n):
-    """Query-block routing of a prefill (block_route_budget semantics with n_real = n)."""
+    """Query-block routing of a prefill (block_route_budget semantics with n_real = n; with a
+    loaded projection, the centroid score of the projected q̄ and μ, ssa/gemma_ssa.py:153-157)."""
     global ROUTE_MS
     blk = cfg.block
     if TIME_ROUTE:
         torch.cuda.synchronize()
         t0 = time.time()
     qbar = block_summary(query, blk, "qmean")
-    mu, var, m3 = block_summary(key, blk, "pop", n_real=n, with_m3=cfg.edgeworth and not dense)
-    if dense:
+    proj = _PROJ
+    mu, var, m3 = block_summary(key, blk, "pop", n_real=n,
+                                with_m3=cfg.edgeworth and not dense and proj is None)
+    if proj is not None:
+        kv = route(project_rows(qbar, proj.W_q), project_rows(mu, proj.W_k), None, None, "budget",
+                   None if dense else cfg.top_c, 1.0 if dense else cfg.budget_frac, cfg.local_w,
+                   0.0)
+    elif dense:
         kv = route(qbar, mu, var, None, "budget", None, 1.0, cfg.local_w, 0.5 * cfg.beta)
     else:
         kv = route(qbar, mu, var, m3, "budget", cfg.top_c, cfg.budget_frac, cfg.local_w,
@@ -163,8 +180,7 @@ def install_ssa(model, **cfg_kwargs):
     _SHARE["bm"] = None
     _PROJ = None
     if CFG.proj_path:
-        raise NotImplementedError("trained routing projections (proj_path) are not implemented "
-                                  "by ssa_amd")
+        _PROJ = load_projection(CFG.proj_path)
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
     prior = getattr(model.config, "_attn_implementation", None) or "sdpa"
     if prior == "ssa":

@@ -101,3 +101,15 @@ def test_cpu_tensors_raise():
     q = torch.randn(1, 1, 256, 64)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         K.ssa_flex(q, q, q)
+
+
+def test_routing_projection_file_loads_without_pickle(tmp_path):
+    """The reference's RoutingProjection.save format loads with weights_only=True."""
+    import torch
+
+    from ssa_amd import gemma_ssa as G
+    path = tmp_path / "p.pt"
+    wq, wk = torch.randn(64, 16), torch.randn(64, 16)
+    torch.save({"W_q": wq, "W_k": wk, "meta": {"steps": 10, "name": "x"}}, path)
+    p = G.load_projection(str(path), device="cpu")
+    assert torch.equal(p.W_q, wq) and torch.equal(p.W_k, wk) and p.meta["steps"] == 10
