@@ -54,7 +54,8 @@ enum ssa_stats_mode {
 enum ssa_route_mode {
   SSA_ROUTE_BUDGET = 0, /* block_route_budget: candidates strictly before the query block      */
   SSA_ROUTE_FLAT = 1,   /* block_route: candidates up to and including the query block          */
-  SSA_ROUTE_QUERY = 2   /* _selection_mask per query: candidates = blocks complete at the query */
+  SSA_ROUTE_QUERY = 2,  /* _selection_mask per query: candidates = blocks complete at the query */
+  SSA_ROUTE_STARTED = 3 /* ssa_swap.ssa_masked per query: candidates = blocks begun at the query */
 };
 
 int ssa_abi_version(void);
@@ -98,6 +99,9 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
  *           blocks complete at pos, c < (pos+1)/block; keep = top_c or
  *           max(1, ceil(fl32(budget_frac)*#candidates)); the "own" block is pos/block
  *           (ssa/gemma_ssa.py:104-131).
+ *   STARTED: row r is the query at pos = query_pos + r; candidates are the blocks that have begun,
+ *           c <= pos/block (its own, partial block included); keep as in QUERY; own = pos/block
+ *           (ssa/ssa_swap.py:44-51, whose block statistics also cover the own block's later keys).
  *   The top min(keep, #candidates) candidates are unioned with the own block and its `local`
  *   predecessors, clipped to [0, own], and written ascending: kv_num (B,Hq,nbq) and
  *   kv_idx (B,Hq,nbq,W) (ssa/ssa_kernel.py:113-118 without the dense argsort).
@@ -206,6 +210,31 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
                     const int64_t* strides, int64_t top_c, float budget_frac, int64_t local,
                     float coef2, float scale, int32_t* kv_num, int32_t* kv_idx, int64_t W,
                     void* workspace, size_t workspace_bytes, ssa_stream_t stream);
+
+/*
+ * Per-row block-sparse attention of ssa_swap.ssa_masked (ssa/ssa_swap.py:32-56), forward and
+ * backward, for continued training through the attention swap. Row r of head (b, h) is the query
+ * at position r of q (B, Hq, n, d); it attends the keys <= r of its listed blocks (kv_num (B,Hq,n)
+ * and kv_idx (B,Hq,n,W), e.g. from ssa_route with SSA_ROUTE_STARTED); k, v (B, Hkv, n, d).
+ * strides: 3 per tensor for q, k, v, out; dout uses the strides of out.
+ * forward: out in q's dtype and lse (B, Hq, n) fp32 (natural log of the row's softmax sum of the
+ *   scaled scores); workspace ssa_masked_attn_workspace_size() bytes.
+ * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) fp32 contiguous, written by the call (zeroed
+ *   first); accumulated with fp32 atomics, so the last bit depends on summation order.
+ *   workspace >= B*Hq*n*4 bytes (ssa_masked_attn_workspace_size() suffices).
+ */
+size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W, int64_t d);
+int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                        int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t d,
+                        int64_t block, const int64_t* strides, const int32_t* kv_num,
+                        const int32_t* kv_idx, int64_t W, float scale, void* workspace,
+                        size_t workspace_bytes, ssa_stream_t stream);
+int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                        const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                        int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t d,
+                        int64_t block, const int64_t* strides, const int32_t* kv_num,
+                        const int32_t* kv_idx, int64_t W, float scale, void* workspace,
+                        size_t workspace_bytes, ssa_stream_t stream);
 
 #ifdef __cplusplus
 }

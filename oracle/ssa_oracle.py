@@ -22,6 +22,10 @@ Pinning (what checks each function; details in tests/test_oracle.py):
   sparse_attention       reference golden outputs (FlexAttention / analytic path); full budget
                          == dense causal softmax; needle known-answer test.
   decode_attend          equals the prefill row for the same blocks; golden analytic q_len=1 rows.
+  masked_route /         reference ssa_masked fixtures (float32 forward and autograd gradients);
+  masked_forward /       planted slips (biased variance, pad rows dropped, complete-block
+  masked_grads           candidates) fail them; full selection == dense causal and torch autograd;
+                         central differences on a sparse GQA case.
 """
 from __future__ import annotations
 
@@ -132,7 +136,8 @@ def row_geometry(mode: str, i: int, nbk: int, top_c, budget_frac, query_pos=0, b
     """(cmax, keep, own) of row i: candidates are blocks [0, cmax), `keep` of them are kept (ties
     to the lowest index), and the own block with its `local` predecessors is always added.
     budget: c < i (ssa/ssa_kernel.py:101-106); flat: c <= i (ssa/ssa_kernel.py:48-52);
-    query: blocks complete at pos = query_pos + i (ssa/gemma_ssa.py:104-118)."""
+    query: blocks complete at pos = query_pos + i (ssa/gemma_ssa.py:104-118); started: blocks
+    begun at pos, its own included (ssa/ssa_swap.py:44-45)."""
     if mode == "budget":
         cmax, own = min(i, nbk), i
     elif mode == "flat":
@@ -140,6 +145,9 @@ def row_geometry(mode: str, i: int, nbk: int, top_c, budget_frac, query_pos=0, b
     elif mode == "query":
         pos = query_pos + i
         cmax, own = min((pos + 1) // block, nbk), pos // block
+    elif mode == "started":  # ssa/ssa_swap.py:44-45: block j visible once it has begun
+        pos = query_pos + i
+        cmax, own = min(pos // block + 1, nbk), pos // block
     else:
         raise ValueError(mode)
     if mode == "flat" or top_c is not None:
@@ -372,3 +380,78 @@ def attend_rows(q, k, v, kv_num, kv_idx, pos0, block, scale=None):
                 out[b, h, r] = decode_attend(q[b, h, r], k[b, h // G], v[b, h // G], ids, pos0 + r,
                                              block, scale)
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# f3: ssa_swap.ssa_masked (per-query routing + token-causal softmax) and its gradients
+# ---------------------------------------------------------------------------------------------
+
+
+def masked_route(q, k, block, top_c, local):
+    """Per-query selection of ssa_masked (ssa/ssa_swap.py:36-51): key blocks zero-padded to a
+    block multiple with their mean and UNBIASED variance (the zero rows count, :37-41), the
+    score <q, mu> + 1/2 <q*q, var> per query row (fp32 assembly of fp64 sums), candidates = blocks
+    begun at the query, top_c of them (ties to the lowest block), the own block and `local`
+    predecessors. q, k (B, H, n, d) -> list-of-lists (B, H, n)."""
+    B, H, n, d = q.shape
+    nb = -(-n // block)
+    kk = np.zeros((B, k.shape[1], nb * block, d), dtype=np.float32)
+    kk[:, :, :n] = k
+    mu, var, _ = block_stats(kk, block, "unbiased")
+    r = scores(q.astype(np.float32), mu, var, 0.5)
+    return select_rows(r, "started", top_c, 0.0, local, 0, block)
+
+
+def masked_forward(q, k, v, sel, block, scale=None):
+    """out (B, H, n, d) float64 and lse (B, H, n): softmax over the keys j <= i of row i's
+    selected blocks of scale * q_i.k_j, times v (ssa/ssa_swap.py:52-56); query head h reads key
+    head h // (H/Hkv)."""
+    B, H, n, d = q.shape
+    G = H // k.shape[1]
+    scale = d ** -0.5 if scale is None else scale
+    out = np.zeros((B, H, n, d))
+    lse = np.zeros((B, H, n))
+    for b in range(B):
+        for h in range(H):
+            K, V = k[b, h // G].astype(np.float64), v[b, h // G].astype(np.float64)
+            for i in range(n):
+                keys = _masked_keys(sel[b, h, i], i, block, n)
+                s = scale * (K[keys] @ q[b, h, i].astype(np.float64))
+                m = s.max()
+                p = np.exp(s - m)
+                out[b, h, i] = p @ V[keys] / p.sum()
+                lse[b, h, i] = m + math.log(p.sum())
+    return out, lse
+
+
+def _masked_keys(blocks, i, block, n):
+    return np.array([j for c in sorted(set(blocks)) for j in range(c * block, min((c + 1) * block, n))
+                     if j <= i], dtype=np.int64)
+
+
+def masked_grads(q, k, v, sel, g, block, scale=None):
+    """Gradients of sum(out * g) through masked_forward with the selection fixed:
+    P = softmax(S), dP = g V^T, dS = P (dP - rowsum(P dP)), dq = scale dS K, dk = scale dS^T q,
+    dv = P^T g (float64)."""
+    B, H, n, d = q.shape
+    Hkv = k.shape[1]
+    G = H // Hkv
+    scale = d ** -0.5 if scale is None else scale
+    dq = np.zeros((B, H, n, d))
+    dk = np.zeros((B, Hkv, n, d))
+    dv = np.zeros((B, Hkv, n, d))
+    for b in range(B):
+        for h in range(H):
+            K, V = k[b, h // G].astype(np.float64), v[b, h // G].astype(np.float64)
+            for i in range(n):
+                keys = _masked_keys(sel[b, h, i], i, block, n)
+                qi, gi = q[b, h, i].astype(np.float64), g[b, h, i].astype(np.float64)
+                s = scale * (K[keys] @ qi)
+                p = np.exp(s - s.max())
+                p /= p.sum()
+                dp = V[keys] @ gi
+                ds = p * (dp - (p * dp).sum())
+                dq[b, h, i] = scale * ds @ K[keys]
+                dk[b, h // G, keys] += scale * np.outer(ds, qi)
+                dv[b, h // G, keys] += np.outer(p, gi)
+    return dq, dk, dv

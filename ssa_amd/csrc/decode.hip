@@ -31,6 +31,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxDecodeBlock = 1024;
 constexpr int kMaxDecodeD = 256;
 
@@ -46,6 +47,7 @@ struct DecodeParams {
   int64_t W;
   float scale_log2;
   float* part;  // (B*Hq*nq, W, d + 2): m, l, o[d]
+  float* lse;   // optional (B*Hq*nq): natural-log sum of exp of the scaled scores of the row
 };
 
 template <int DT>
@@ -268,6 +270,119 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   for (int e = tid; e < p.d; e += 256)
     store_elem<DT>(p.o, b * p.osb + h * p.osh + r * p.osn + e,
                    (red[0][e] + red[1][e] + red[2][e] + red[3][e]) * inv);
+  if (p.lse != nullptr && tid == 0) p.lse[rowid] = L > 0.0f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Backward of the per-row block-sparse softmax attention (ssa_swap.ssa_masked): for query row i
+// with output O_i, upstream gradient dO_i and log-sum-exp lse_i, over its selected keys j <= pos:
+//   P_ij = exp(scale q_i.k_j - lse_i), dP_ij = dO_i.v_j, D_i = dO_i.O_i, dS_ij = P_ij (dP_ij - D_i)
+//   dq_i += scale sum_j dS_ij k_j,  dk_j += scale dS_ij q_i,  dv_j += P_ij dO_i.
+// One wave per (row, selected block) as in the forward; dq/dk/dv are fp32 and accumulated with
+// atomics (summation order varies from run to run at the last bit).
+// ---------------------------------------------------------------------------------------------
+struct BwdParams {
+  DecodeParams f;       // q, k, v, out (as o), strides, lists, sizes of the forward
+  const char* dout;     // upstream gradient, strides of out
+  const float* lse;
+  const float* delta;   // D_i (B*Hq*nq)
+  float* dq;            // (B, Hq, nq, d) fp32 contiguous
+  float* dk;            // (B, Hkv, cap, d) fp32 contiguous
+  float* dv;
+  int64_t Hkv;
+};
+
+// D_i = dO_i . O_i. grid (rows), one wave each.
+template <int DT>
+__global__ __launch_bounds__(64) void masked_delta_kernel(BwdParams bp) {
+  const DecodeParams& p = bp.f;
+  const int64_t rowid = blockIdx.x;
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq;
+  const int64_t off = b * p.osb + h * p.osh + r * p.osn;
+  float acc = 0.0f;
+  for (int e = threadIdx.x; e < p.d; e += 64)
+    acc = fmaf(load_elem<DT>(bp.dout, off + e), load_elem<DT>(p.o, off + e), acc);
+  acc = wave_sum(acc);
+  if (threadIdx.x == 0) const_cast<float*>(bp.delta)[rowid] = acc;
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    x[i] = 0.0f;
+}
+
+// grid (rows * W), one wave per (row, selected block).
+template <int DT>
+__global__ __launch_bounds__(64) void masked_bwd_kernel(BwdParams bp) {
+  const DecodeParams& p = bp.f;
+  __shared__ float qs[kMaxDecodeD];
+  __shared__ float gs[kMaxDecodeD];  // dO_i
+  __shared__ float ps[kMaxDecodeBlock];
+  __shared__ float dss[kMaxDecodeBlock];
+  const int lane = threadIdx.x;
+  const int64_t j = blockIdx.x % p.W;
+  const int64_t rowid = blockIdx.x / p.W;
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.G;
+  const int64_t pos = p.pos + r;
+  const int d = (int)p.d;
+  int cnt = p.kv_num[rowid];
+  if (cnt > p.W) cnt = (int)p.W;
+  if (j >= cnt) return;
+  const int32_t* list = p.kv_idx + rowid * p.W;
+  const int64_t c = list[j];
+  const int64_t nblk = (p.cap + p.block - 1) / p.block;
+  if (c < 0 || c >= nblk || c * p.block > pos) return;
+  for (int64_t jj = 0; jj < j; ++jj)  // a repeated id is attended (and differentiated) once
+    if (list[jj] == c) return;
+  const int64_t key0 = c * p.block;
+  int64_t key1 = key0 + p.block;
+  if (key1 > pos + 1) key1 = pos + 1;
+  if (key1 > p.cap) key1 = p.cap;
+  const int nk = (int)(key1 - key0);
+  const float lse2 = bp.lse[rowid] * kLog2e;  // log2 domain
+  const float Di = bp.delta[rowid];
+  const float scale = p.scale_log2 / kLog2e;
+
+  const int64_t qoff = b * p.qsb + h * p.qsh + r * p.qsn;
+  const int64_t goff = b * p.osb + h * p.osh + r * p.osn;
+  for (int e = lane; e < d; e += 64) {
+    qs[e] = load_elem<DT>(p.q, qoff + e);
+    gs[e] = load_elem<DT>(bp.dout, goff + e);
+  }
+  __syncthreads();
+  const int64_t koff = b * p.ksb + kvh * p.ksh, voff = b * p.vsb + kvh * p.vsh;
+  for (int kk = lane; kk < nk; kk += 64) {
+    float s = 0.0f, dp = 0.0f;
+    const int64_t kr = koff + (key0 + kk) * p.ksn, vr = voff + (key0 + kk) * p.vsn;
+    for (int e = 0; e < d; ++e) {
+      s = fmaf(qs[e], load_elem<DT>(p.k, kr + e), s);
+      dp = fmaf(gs[e], load_elem<DT>(p.v, vr + e), dp);
+    }
+    const float pk = exp2f(s * p.scale_log2 - lse2);
+    ps[kk] = pk;
+    dss[kk] = pk * (dp - Di);
+  }
+  __syncthreads();
+  // dq_i (lane = head dim): scale * sum_j dS_ij k_j
+  const int64_t dqoff = rowid * p.d;
+  for (int e = lane; e < d; e += 64) {
+    float acc = 0.0f;
+    for (int kk = 0; kk < nk; ++kk) acc = fmaf(dss[kk], load_elem<DT>(p.k, koff + (key0 + kk) * p.ksn + e), acc);
+    atomicAdd(bp.dq + dqoff + e, scale * acc);
+  }
+  // dk_j += scale dS_ij q_i, dv_j += P_ij dO_i (lane = head dim, coalesced rows)
+  const int64_t kvrow = (b * bp.Hkv + kvh) * p.cap;
+  for (int kk = 0; kk < nk; ++kk) {
+    const float dsk = scale * dss[kk], pk = ps[kk];
+    float* dkr = bp.dk + (kvrow + key0 + kk) * p.d;
+    float* dvr = bp.dv + (kvrow + key0 + kk) * p.d;
+    for (int e = lane; e < d; e += 64) {
+      if (dsk != 0.0f) atomicAdd(dkr + e, dsk * qs[e]);
+      if (pk != 0.0f) atomicAdd(dvr + e, pk * gs[e]);
+    }
+  }
 }
 
 // Element strides of the append: new token rows (b,h) and caches (b,h,n).
@@ -376,6 +491,7 @@ extern "C" int ssa_decode_attend(const void* q, const void* k, const void* v, vo
   p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
   p.scale_log2 = scale * kLog2e;
   p.part = static_cast<float*>(workspace);
+  p.lse = nullptr;
   return run_attend(dtype, p, static_cast<hipStream_t>(stream));
 }
 
@@ -473,5 +589,108 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
   p.scale_log2 = scale * kLog2e;
   p.part = part;
+  p.lse = nullptr;
   return run_attend(dtype, p, st);
+}
+
+extern "C" size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W,
+                                                 int64_t d) {
+  return ssa_decode_attend_workspace_size(B, Hq, n, W, d) + (size_t)B * Hq * n * 4u;
+}
+
+namespace {
+int masked_params(ssa::DecodeParams& p, const void* q, const void* k, const void* v,
+                  const void* out, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
+                  int64_t d, int64_t block, const int64_t* strides, const int32_t* kv_num,
+                  const int32_t* kv_idx, int64_t W, float scale) {
+  using namespace ssa;
+  SSA_REQUIRE(q && k && v && out && strides && kv_num && kv_idx, SSA_ERR_INVALID,
+              "masked_attn: NULL pointer argument");
+  SSA_TRY(check_decode(dtype, B, Hq, Hkv, n, n, d, block, 0, W, strides, 12));
+  SSA_REQUIRE(aligned16(k) && aligned16(v), SSA_ERR_UNSUPPORTED,
+              "masked_attn: k and v must be 16-byte aligned");
+  SSA_REQUIRE(scale > 0.0f, SSA_ERR_INVALID, "masked_attn: scale must be > 0");
+  p.q = static_cast<const char*>(q);
+  p.k = static_cast<const char*>(k);
+  p.v = static_cast<const char*>(v);
+  p.o = static_cast<char*>(const_cast<void*>(out));
+  p.qsb = strides[0]; p.qsh = strides[1]; p.qsn = strides[2];
+  p.ksb = strides[3]; p.ksh = strides[4]; p.ksn = strides[5];
+  p.vsb = strides[6]; p.vsh = strides[7]; p.vsn = strides[8];
+  p.osb = strides[9]; p.osh = strides[10]; p.osn = strides[11];
+  p.B = B; p.Hq = Hq; p.G = Hq / Hkv; p.nq = n; p.cap = n; p.d = d; p.block = block;
+  p.pos = 0;
+  p.kv_num = kv_num; p.kv_idx = kv_idx; p.W = W;
+  p.scale_log2 = scale * kLog2e;
+  return SSA_OK;
+}
+}  // namespace
+
+extern "C" int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, void* out,
+                                   float* lse, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                   int64_t n, int64_t d, int64_t block, const int64_t* strides,
+                                   const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
+                                   float scale, void* workspace, size_t workspace_bytes,
+                                   ssa_stream_t stream) {
+  using namespace ssa;
+  DecodeParams p;
+  SSA_TRY(masked_params(p, q, k, v, out, dtype, B, Hq, Hkv, n, d, block, strides, kv_num, kv_idx,
+                        W, scale));
+  SSA_REQUIRE(lse != nullptr, SSA_ERR_INVALID, "masked_attn_fwd: lse is NULL");
+  const size_t need = ssa_decode_attend_workspace_size(B, Hq, n, W, d);
+  SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
+              "masked_attn_fwd: workspace needs %zu bytes", need);
+  p.part = static_cast<float*>(workspace);
+  p.lse = lse;
+  return run_attend(dtype, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                                   const void* dout, const float* lse, float* dq, float* dk,
+                                   float* dv, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                   int64_t n, int64_t d, int64_t block, const int64_t* strides,
+                                   const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
+                                   float scale, void* workspace, size_t workspace_bytes,
+                                   ssa_stream_t stream) {
+  using namespace ssa;
+  BwdParams bp;
+  SSA_TRY(masked_params(bp.f, q, k, v, out, dtype, B, Hq, Hkv, n, d, block, strides, kv_num,
+                        kv_idx, W, scale));
+  SSA_REQUIRE(dout && lse && dq && dk && dv, SSA_ERR_INVALID, "masked_attn_bwd: NULL gradient");
+  const size_t need = (size_t)B * Hq * n * 4u;
+  SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
+              "masked_attn_bwd: workspace needs %zu bytes", need);
+  bp.f.part = nullptr;
+  bp.f.lse = nullptr;
+  bp.dout = static_cast<const char*>(dout);
+  bp.lse = lse;
+  bp.delta = static_cast<const float*>(workspace);
+  bp.dq = dq;
+  bp.dk = dk;
+  bp.dv = dv;
+  bp.Hkv = Hkv;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t rows = B * Hq * n;
+  SSA_REQUIRE(rows * W < (1ll << 31), SSA_ERR_UNSUPPORTED, "masked_attn_bwd: grid too large");
+  const int64_t nq_el = rows * d, nk_el = B * Hkv * n * d;
+  zero_f32_kernel<<<(unsigned)((nq_el + 255) / 256 < 4096 ? (nq_el + 255) / 256 : 4096), 256, 0, st>>>(dq, nq_el);
+  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(dk, nk_el);
+  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(dv, nk_el);
+  SSA_TRY(launch_status("zero_f32_kernel"));
+  const unsigned g1 = (unsigned)rows, g2 = (unsigned)(rows * W);
+  switch (dtype) {
+    case SSA_F32:
+      masked_delta_kernel<SSA_F32><<<g1, 64, 0, st>>>(bp);
+      masked_bwd_kernel<SSA_F32><<<g2, 64, 0, st>>>(bp);
+      break;
+    case SSA_F16:
+      masked_delta_kernel<SSA_F16><<<g1, 64, 0, st>>>(bp);
+      masked_bwd_kernel<SSA_F16><<<g2, 64, 0, st>>>(bp);
+      break;
+    default:
+      masked_delta_kernel<SSA_BF16><<<g1, 64, 0, st>>>(bp);
+      masked_bwd_kernel<SSA_BF16><<<g2, 64, 0, st>>>(bp);
+      break;
+  }
+  return launch_status("masked_bwd_kernel");
 }

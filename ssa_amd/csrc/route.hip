@@ -48,6 +48,7 @@ __host__ __device__ inline int64_t row_cmax(const RouteGeom& g, int64_t i) {
   int64_t c;
   if (g.mode == SSA_ROUTE_BUDGET) c = i;
   else if (g.mode == SSA_ROUTE_FLAT) c = i + 1;
+  else if (g.mode == SSA_ROUTE_STARTED) c = (g.query_pos + i) / g.block + 1;
   else c = (g.query_pos + i + 1) / g.block;
   if (c > g.nbk) c = g.nbk;
   return c < 0 ? 0 : c;
@@ -59,7 +60,8 @@ __host__ __device__ inline int64_t row_cmax_s(const RouteGeom& g, int64_t i) {
 }
 
 __host__ __device__ inline int64_t row_own(const RouteGeom& g, int64_t i) {
-  return g.mode == SSA_ROUTE_QUERY ? (g.query_pos + i) / g.block : i;
+  return g.mode == SSA_ROUTE_QUERY || g.mode == SSA_ROUTE_STARTED ? (g.query_pos + i) / g.block
+                                                                  : i;
 }
 
 // keep count before clipping to the candidate count. Budget: ceil(fp32(frac) * nvis) in fp32,
@@ -561,12 +563,14 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
               "route: sizes must be positive");
   SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "route: Hq=%lld not a multiple of Hkv=%lld",
               (long long)Hq, (long long)Hkv);
-  SSA_REQUIRE(mode == SSA_ROUTE_BUDGET || mode == SSA_ROUTE_FLAT || mode == SSA_ROUTE_QUERY,
+  SSA_REQUIRE(mode == SSA_ROUTE_BUDGET || mode == SSA_ROUTE_FLAT || mode == SSA_ROUTE_QUERY ||
+                  mode == SSA_ROUTE_STARTED,
               SSA_ERR_INVALID, "route: unknown mode %d", mode);
   SSA_REQUIRE(local >= 0, SSA_ERR_INVALID, "route: local must be >= 0");
   SSA_REQUIRE(mode != SSA_ROUTE_FLAT || top_c >= 0, SSA_ERR_INVALID, "route: flat mode needs top_c");
   SSA_REQUIRE(top_c >= 0 || budget_frac >= 0.0f, SSA_ERR_INVALID, "route: budget_frac < 0");
-  SSA_REQUIRE(mode != SSA_ROUTE_QUERY || (query_pos >= 0 && block > 0), SSA_ERR_INVALID,
+  SSA_REQUIRE((mode != SSA_ROUTE_QUERY && mode != SSA_ROUTE_STARTED) || (query_pos >= 0 && block > 0),
+              SSA_ERR_INVALID,
               "route: query mode needs query_pos >= 0 and block > 0");
   SSA_REQUIRE(var != nullptr || coef2 == 0.0f, SSA_ERR_INVALID, "route: var is NULL, coef2 != 0");
   SSA_REQUIRE(nbk <= kMaxNbk, SSA_ERR_UNSUPPORTED, "route: %lld key blocks exceed %d",

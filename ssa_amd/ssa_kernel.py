@@ -72,7 +72,8 @@ def block_summary(x: torch.Tensor, block: int, mode: str = "pop", n_real: int | 
     return mu, var, m3
 
 
-_ROUTE_MODES = {"budget": _lib.ROUTE_BUDGET, "flat": _lib.ROUTE_FLAT, "query": _lib.ROUTE_QUERY}
+_ROUTE_MODES = {"budget": _lib.ROUTE_BUDGET, "flat": _lib.ROUTE_FLAT, "query": _lib.ROUTE_QUERY,
+                "started": _lib.ROUTE_STARTED}
 
 
 def route_width(mode: str, nbq: int, nbk: int, top_c: int | None, budget_frac: float,
@@ -89,7 +90,8 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
     """Cumulant router over precomputed summaries -> compact (kv_num, kv_idx).
 
     rows (B, Hq, nbq, d) fp32: query-block means (mode "budget"/"flat") or query vectors
-    ("query", row r at absolute position query_pos + r). mu/var/m3 (B, Hkv, nbk*pool, d) fp32:
+    ("query": blocks complete at position query_pos + r; "started": blocks begun there, own
+    included). mu/var/m3 (B, Hkv, nbk*pool, d) fp32:
     with pool > 1 they are sub-block summaries and a key block scores as the max of its pool
     sub-blocks (ssa/ssa_kernel.py:100). Returns kv_num (B, Hq, nbq) int32 and
     kv_idx (B, Hq, nbq, W) int32 (ascending, padded 0).

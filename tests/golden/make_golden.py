@@ -9,9 +9,10 @@ Run once in the build container (the reference is not present on GPU boxes):
 Each fixture is a small .npz of outputs only (selections as int16 compact lists, attention rows
 as float32/float64) plus the sha256 of the inputs, which the tests regenerate from the same
 seeded generators (ssa_amd.workloads / the seeds recorded here) and check against the hash.
-Reference functions used (ssa/ssa_kernel.py, ssa/gemma_ssa.py):
+Reference functions used (ssa/ssa_kernel.py, ssa/gemma_ssa.py, ssa/ssa_swap.py):
   block_route_budget :61-119, block_route :37-58, ssa_flex :122-126,
-  _selection_mask :85-137, ssa_attention_forward :183-241 (impl="analytic").
+  _selection_mask :85-137, ssa_attention_forward :183-241 (impl="analytic"),
+  ssa_masked :32-56 (forward and autograd backward).
 """
 from __future__ import annotations
 
@@ -30,6 +31,7 @@ sys.path.insert(0, str(ROOT))
 REFERENCE = Path("/root/reference")
 
 from ssa_amd import workloads as WL  # noqa: E402
+from tests import golden_util as GU  # noqa: E402
 
 
 def sha(*arrays) -> str:
@@ -167,6 +169,25 @@ def analytic_case(name, budget_frac=0.5, block=64):
     print(f"{name}: out {tuple(full.shape)}")
 
 
+def masked_case(name):
+    """ssa_swap.ssa_masked in float32 on CPU: forward output and the gradients of sum(out * g)
+    with respect to q, k and v (torch autograd through the reference's masked dense form)."""
+    sys.path.insert(0, str(REFERENCE))
+    from ssa import ssa_swap as RS  # noqa: E402
+    seed, (b, h, n, d), block, top_c, local = GU.MASKED_CASES[name]
+    q, k, v, g = GU.masked_inputs(seed, b, h, n, d)
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    t0 = time.time()
+    out = RS.ssa_masked(tq, tk, tv, block, top_c, local)
+    out.backward(torch.from_numpy(g))
+    np.savez_compressed(HERE / f"{name}.npz", out=out.detach().numpy(), dq=tq.grad.numpy(),
+                        dk=tk.grad.numpy(), dv=tv.grad.numpy(),
+                        inputs_sha256=np.array(sha(q, k, v, g)),
+                        meta=np.array(repr({"seed": seed, "shape": (b, h, n, d), "block": block,
+                                            "top_c": top_c, "local": local})))
+    print(f"{name}: out {tuple(out.shape)} ({time.time() - t0:.1f}s)")
+
+
 CASES = {
     "c1_budget": lambda: route_case("c1_budget", "C1", top_c=8, local=1, beta=2.0),
     "c1_frac": lambda: route_case("c1_frac", "C1", budget_frac=0.25, local=1, beta=2.0),
@@ -186,6 +207,8 @@ CASES = {
     "c4_query": lambda: query_case("c4_query"),
     "c1_flex_out": lambda: flex_case("c1_flex_out"),
     "analytic_gqa": lambda: analytic_case("analytic_gqa"),
+    "swap_masked_b16": lambda: masked_case("swap_masked_b16"),
+    "swap_masked_b64": lambda: masked_case("swap_masked_b64"),
 }
 
 if __name__ == "__main__":

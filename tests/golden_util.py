@@ -23,6 +23,20 @@ def sha(*arrays) -> str:
     return h.hexdigest()
 
 
+# ssa_swap.ssa_masked fixtures: name -> (seed, (b, h, n, d), block, top_c, local)
+MASKED_CASES = {
+    "swap_masked_b16": (5, (2, 3, 300, 64), 16, 3, 1),
+    "swap_masked_b64": (6, (1, 2, 200, 64), 64, 1, 0),
+}
+
+
+def masked_inputs(seed, b, h, n, d):
+    """q, k, v and the upstream gradient g (b, h, n, d) float32 of an ssa_masked fixture."""
+    rng = np.random.default_rng(seed)
+    q, k, v, g = (rng.standard_normal((b, h, n, d)).astype(np.float32) for _ in range(4))
+    return q, k, v, g
+
+
 def row_sets(kv_num, kv_idx):
     kv_num = np.asarray(kv_num)
     kv_idx = np.asarray(kv_idx)

@@ -324,3 +324,87 @@ def test_oracle_proj_identity_equals_centroid_routing():
     w = WL.proj_matrix(5)
     qp = (q[0, 0].astype(np.float64) @ w)
     assert np.array_equal(O.project(q[0, 0], w), qp.astype(np.float32))
+
+
+# ---- f3: ssa_swap.ssa_masked -------------------------------------------------------------------
+
+def _masked_case(name):
+    seed, (b, h, n, d), block, top_c, local = GU.MASKED_CASES[name]
+    q, k, v, g = GU.masked_inputs(seed, b, h, n, d)
+    ref = GU.load(name)
+    assert GU.sha(q, k, v, g) == str(ref["inputs_sha256"])
+    return q, k, v, g, block, top_c, local, ref
+
+
+@pytest.mark.parametrize("name", list(GU.MASKED_CASES))
+def test_oracle_masked_matches_reference(name):
+    """Selection, forward and q/k/v gradients of ssa_masked (ssa/ssa_swap.py:32-56, the
+    reference run in float32 with torch autograd) against the float64 oracle."""
+    q, k, v, g, block, top_c, local, ref = _masked_case(name)
+    sel = O.masked_route(q, k, block, top_c, local)
+    out, _ = O.masked_forward(q, k, v, sel, block)
+    dq, dk, dv = O.masked_grads(q, k, v, sel, g, block)
+    for got, key in ((out, "out"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert np.abs(got - ref[key]).max() < 1e-5, key
+
+
+def test_oracle_masked_planted_mistakes_fail():
+    """Each plausible slip in the routing statistics or geometry changes the output of the b16
+    fixture far beyond the 1e-5 bar: biased variance, pad rows left out of the statistics,
+    complete-block (rather than begun-block) candidates."""
+    q, k, v, g, block, top_c, local, ref = _masked_case("swap_masked_b16")
+    n = q.shape[2]
+    kp = np.pad(k, ((0, 0), (0, 0), (0, -n % block), (0, 0)))
+    variants = {
+        "biased": (O.block_stats(kp, block, "pop"), "started"),
+        "pad_excluded": (O.block_stats(k, block, "unbiased", n_real=n), "started"),
+        "complete_blocks": (O.block_stats(kp, block, "unbiased"), "query"),
+    }
+    for nm, ((mu, var, _), mode) in variants.items():
+        sel = O.select_rows(O.scores(q, mu, var, 0.5), mode, top_c, 0.0, local, 0, block)
+        out, _ = O.masked_forward(q, k, v, sel, block)
+        assert np.abs(out - ref["out"]).max() > 1e-2, nm
+
+
+def test_masked_full_selection_equals_dense_and_autograd():
+    """top_c >= number of blocks: every begun block is kept, so the masked forward is dense
+    causal softmax, and its gradients equal torch autograd of dense causal attention (float64)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    q, k, v, g = (rng.standard_normal((1, 2, 70, 16)) for _ in range(4))
+    sel = O.masked_route(q.astype(np.float32), k.astype(np.float32), 16, 99, 0)
+    assert [len(x) for x in sel[0, 0]] == [i // 16 + 1 for i in range(70)]
+    out, lse = O.masked_forward(q, k, v, sel, 16)
+    assert np.abs(out - O.dense_causal(q, k, v)).max() < 1e-12
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    s = (tq @ tk.transpose(-1, -2)) * 0.25
+    s = s.masked_fill(torch.ones(70, 70, dtype=torch.bool).triu(1), float("-inf"))
+    assert np.abs(torch.logsumexp(s, -1).detach().numpy() - lse).max() < 1e-12
+    (torch.softmax(s, -1) @ tv).backward(torch.from_numpy(g))
+    dq, dk, dv = O.masked_grads(q, k, v, sel, g, 16)
+    for got, t in ((dq, tq), (dk, tk), (dv, tv)):
+        assert np.abs(got - t.grad.numpy()).max() < 1e-12
+
+
+def test_masked_grads_finite_differences():
+    """Gradients of sum(out * g) with the selection held fixed, by central differences on a
+    sparse selection with GQA 2:1 (top_c=1, local=0)."""
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, 4, 40, 8))
+    k, v = (rng.standard_normal((1, 2, 40, 8)) for _ in range(2))
+    g = rng.standard_normal((1, 4, 40, 8))
+    sel = O.masked_route(q.astype(np.float32), k.astype(np.float32), 8, 1, 0)
+    assert max(len(x) for x in sel.ravel()) == 2 and min(len(x) for x in sel.ravel()) == 1
+    dq, dk, dv = O.masked_grads(q, k, v, sel, g, 8)
+
+    def loss(q_, k_, v_):
+        return float((O.masked_forward(q_, k_, v_, sel, 8)[0] * g).sum())
+
+    eps = 1e-6
+    for arr, grad, which in ((q, dq, 0), (k, dk, 1), (v, dv, 2)):
+        for idx in [(0, 1, 5, 3), (0, 1, 33, 0), (0, 0, 17, 7)]:
+            plus, minus = [x.copy() for x in (q, k, v)], [x.copy() for x in (q, k, v)]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            fd = (loss(*plus) - loss(*minus)) / (2 * eps)
+            assert abs(fd - grad[idx]) < 1e-6 * max(1.0, abs(fd)), (which, idx, fd, grad[idx])
