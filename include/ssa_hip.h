@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 2
+#define SSA_ABI_VERSION 3
 
 typedef void* ssa_stream_t; /* hipStream_t */
 
@@ -218,12 +218,16 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
  * and kv_idx (B,Hq,n,W), e.g. from ssa_route with SSA_ROUTE_STARTED); k, v (B, Hkv, n, d).
  * strides: 3 per tensor for q, k, v, out; dout uses the strides of out.
  * forward: out in q's dtype and lse (B, Hq, n) fp32 (natural log of the row's softmax sum of the
- *   scaled scores); workspace ssa_masked_attn_workspace_size() bytes.
- * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) fp32 contiguous, written by the call (zeroed
- *   first); accumulated with fp32 atomics, so the last bit depends on summation order.
- *   workspace >= B*Hq*n*4 bytes (ssa_masked_attn_workspace_size() suffices).
+ *   scaled scores).
+ * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) fp32 contiguous, written by the call.
+ * Both take ssa_masked_attn_workspace_size(B, Hq, n, W, d, block) bytes of workspace.
+ * d = 64 with at most 8192 key blocks runs the tiled MFMA kernels (per (64-row query tile, key
+ *   block) row masks; q, k, v, out, dout, dq, dk, dv 16-byte aligned; deterministic). Other head
+ *   dims (multiple of 8, <= 256) run one wave per (row, selected block); their backward
+ *   accumulates with fp32 atomics, so its last bit depends on summation order.
  */
-size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W, int64_t d);
+size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W, int64_t d,
+                                      int64_t block);
 int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
                         int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t d,
                         int64_t block, const int64_t* strides, const int32_t* kv_num,

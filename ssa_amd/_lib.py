@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
@@ -46,7 +46,7 @@ _SIGNATURES = {
                                   _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_sz, _c_p]),
     "ssa_project_rows": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "ssa_expand_selection": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
-    "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ssa_masked_attn_fwd": (_c_int, [_c_p] * 5 + [_c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
     "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int] + [_c_i64] * 6 +

@@ -28,6 +28,20 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
                int64_t query_pos, int64_t block, int64_t pool, int32_t* kv_num, int32_t* kv_idx,
                int64_t W, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+bool masked_tiled_ok(int64_t d, int64_t block, int64_t n);
+size_t masked_tiled_workspace(int64_t B, int64_t Hq, int64_t n, int64_t block);
+int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                     int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
+                     const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
+                     int64_t W, float scale, void* workspace, size_t workspace_bytes,
+                     hipStream_t st);
+int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* out,
+                     const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                     int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
+                     const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
+                     int64_t W, float scale, void* workspace, size_t workspace_bytes,
+                     hipStream_t st);
+
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -594,7 +608,8 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
 }
 
 extern "C" size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W,
-                                                 int64_t d) {
+                                                 int64_t d, int64_t block) {
+  if (ssa::masked_tiled_ok(d, block, n)) return ssa::masked_tiled_workspace(B, Hq, n, block);
   return ssa_decode_attend_workspace_size(B, Hq, n, W, d) + (size_t)B * Hq * n * 4u;
 }
 
@@ -637,6 +652,10 @@ extern "C" int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_TRY(masked_params(p, q, k, v, out, dtype, B, Hq, Hkv, n, d, block, strides, kv_num, kv_idx,
                         W, scale));
   SSA_REQUIRE(lse != nullptr, SSA_ERR_INVALID, "masked_attn_fwd: lse is NULL");
+  if (masked_tiled_ok(d, block, n))
+    return masked_tiled_fwd(q, k, v, out, lse, dtype, B, Hq, Hkv, n, block, strides, kv_num,
+                            kv_idx, W, scale, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
   const size_t need = ssa_decode_attend_workspace_size(B, Hq, n, W, d);
   SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
               "masked_attn_fwd: workspace needs %zu bytes", need);
@@ -657,6 +676,10 @@ extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, 
   SSA_TRY(masked_params(bp.f, q, k, v, out, dtype, B, Hq, Hkv, n, d, block, strides, kv_num,
                         kv_idx, W, scale));
   SSA_REQUIRE(dout && lse && dq && dk && dv, SSA_ERR_INVALID, "masked_attn_bwd: NULL gradient");
+  if (masked_tiled_ok(d, block, n))
+    return masked_tiled_bwd(q, k, v, out, dout, lse, dq, dk, dv, dtype, B, Hq, Hkv, n, block,
+                            strides, kv_num, kv_idx, W, scale, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
   const size_t need = (size_t)B * Hq * n * 4u;
   SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
               "masked_attn_bwd: workspace needs %zu bytes", need);

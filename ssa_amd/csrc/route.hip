@@ -11,6 +11,7 @@
 //   finds the keep-th largest key T; keys > T are taken, and keys == T in increasing block order
 //   until keep is reached (ties -> lowest block index). The selection, the own block and its
 //   `local` predecessors are OR-ed into an LDS bitmap that is compacted in ascending order.
+//   With at most 256 key blocks, route_select_small_kernel does the same with one wave per row.
 //
 // Reference: ssa/ssa_kernel.py:45-57 (block_route), :92-118 (block_route_budget),
 // ssa/gemma_ssa.py:99-131 (_selection_mask).
@@ -493,6 +494,90 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   if (tid == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
+// Rows of at most kSmallNbk key blocks: one wave per row, lane l holds candidates l + 64 j. The
+// keep-th largest key T is found bit by bit from the top (count of keys >= T | bit by ballots),
+// keys > T are taken, and keys == T in increasing block order until keep is reached; the
+// selection plus the local window is compacted in ascending order from the per-j ballots.
+constexpr int kSmallJ = 4;
+constexpr int kSmallNbk = 64 * kSmallJ;
+
+__global__ __launch_bounds__(256) void route_select_small_kernel(
+    const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
+    int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t lrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (lrow >= nrows) return;  // whole wave
+  const int64_t bh = lrow / g.ni, il = lrow % g.ni;
+  const int64_t i = g.i0 + il;
+  const int64_t cmax = row_cmax(g, i);
+  const int64_t keep = row_keep(g, cmax);
+  const int64_t K = keep < cmax ? keep : cmax;
+  const unsigned int* kraw = keys + lrow * g.nbk * g.pool;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  unsigned int key[kSmallJ];
+  bool cand[kSmallJ];
+#pragma unroll
+  for (int j = 0; j < kSmallJ; ++j) {
+    const int64_t c = lane + 64 * j;
+    cand[j] = c < cmax;
+    unsigned int m = 0u;
+    if (cand[j]) {
+      m = kraw[c * g.pool];
+      for (int64_t t = 1; t < g.pool; ++t) {
+        const unsigned int x = kraw[c * g.pool + t];
+        m = x > m ? x : m;
+      }
+    }
+    key[j] = m;
+  }
+  bool sel[kSmallJ];
+  if (K >= cmax) {
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) sel[j] = cand[j];
+  } else if (K <= 0) {
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) sel[j] = false;
+  } else {
+    unsigned int T = 0u;  // largest T with #{keys >= T} >= K: the K-th largest key
+    for (int bit = 31; bit >= 0; --bit) {
+      const unsigned int t = T | (1u << bit);
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < kSmallJ; ++j) cnt += __popcll(__ballot(cand[j] && key[j] >= t));
+      if (cnt >= K) T = t;
+    }
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) above += __popcll(__ballot(cand[j] && key[j] > T));
+    int need = (int)K - above;  // keys equal to T to take, lowest block first
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) {
+      const bool eq = cand[j] && key[j] == T;
+      const unsigned long long be = __ballot(eq);
+      sel[j] = (cand[j] && key[j] > T) || (eq && __popcll(be & lt) < need);
+      need -= __popcll(be);
+    }
+  }
+  const int64_t own = row_own(g, i);
+  int64_t lo = own - g.local;
+  if (lo < 0) lo = 0;
+  const int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
+  int32_t* out = kv_idx + (bh * g.nbq + i) * W;
+  int pos = 0;
+#pragma unroll
+  for (int j = 0; j < kSmallJ; ++j) {
+    const int64_t c = lane + 64 * j;
+    const bool take = sel[j] || (c >= lo && c <= hi);
+    const unsigned long long b = __ballot(take);
+    const int p = pos + __popcll(b & lt);
+    if (take && p < W) out[p] = (int32_t)c;
+    pos += __popcll(b);
+  }
+  const int64_t num = pos < W ? pos : W;
+  for (int64_t p = num + lane; p < W; p += 64) out[p] = 0;
+  if (lane == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
+}
+
 __global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
     const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int64_t W,
     int64_t nbk, uint8_t* __restrict__ sel, int32_t* __restrict__ kv_full) {
@@ -638,7 +723,10 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     }
     const int64_t nrows = B * Hq * g.ni;
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
-    if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
+    if (nbk <= kSmallNbk)  // few candidates: a wave per row
+      route_select_small_kernel<<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(keys, g, kv_num,
+                                                                             kv_idx, W, nrows);
+    else if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
       route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W);
     else
       route_select_kernel<kSelThreads><<<(unsigned)nrows, kSelThreads, 0, stream>>>(keys, g, kv_num,

@@ -55,7 +55,7 @@ class _MaskedAttention(torch.autograd.Function):
         W = kv_idx.shape[-1]
         out = torch.empty(B, Hq, n, d, device=q.device, dtype=q.dtype)
         lse = torch.empty(B, Hq, n, device=q.device, dtype=torch.float32)
-        wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d))
+        wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d, int(block)))
         ws = torch.empty(wsb, device=q.device, dtype=torch.uint8)
         _lib.call("ssa_masked_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                   lse.data_ptr(), _lib.dtype_code(q.dtype), B, Hq, Hkv, n, d, int(block),
@@ -75,7 +75,7 @@ class _MaskedAttention(torch.autograd.Function):
         dq = torch.empty(B, Hq, n, d, device=q.device, dtype=torch.float32)
         dk = torch.empty(B, Hkv, n, d, device=q.device, dtype=torch.float32)
         dv = torch.empty_like(dk)
-        wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d))
+        wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d, ctx.block))
         ws = torch.empty(wsb, device=q.device, dtype=torch.uint8)
         _lib.call("ssa_masked_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                   dout.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
@@ -92,7 +92,8 @@ def ssa_masked(q, k, v, block, top_c, local):
     _lib.require_device(q, k, v)
     if q.shape[1] % k.shape[1]:
         raise ValueError("ssa_masked: query heads must be a multiple of key heads")
-    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    q, k, v = (t if t.stride(-1) == 1 and t.data_ptr() % 16 == 0 else t.contiguous()
+               for t in (q, k, v))
     with torch.no_grad():
         kv_num, kv_idx = route_masked(q.detach(), k.detach(), block, top_c, local)
     return _MaskedAttention.apply(q, k, v, kv_num, kv_idx, int(block), q.shape[-1] ** -0.5)
