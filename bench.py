@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
     ap.add_argument("--no-decode", action="store_true", help="skip the C4 decode step")
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 12M-token prefill")
+    ap.add_argument("--no-swap", action="store_true",
+                    help="skip the trainable swap (ssa_masked forward + backward)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC byte-count calibration)")
     return ap.parse_args()
@@ -126,6 +128,41 @@ def cpu_baseline(p, kv_num_all, threads):
                    f"pairs ({sample_kv} of {total_kv} selected tiles, {t_sample:.2f} s), "
                    f"extrapolated by sum(kv_num) to {t_total:.1f} s per layer"),
     }
+
+
+def swap_bench(torch, dev):
+    """ssa_swap.ssa_masked training step at the reference's swap configuration (GPT-2 attention:
+    batch 4, 12 heads, context 1024, d 64, fp32; block 64, top_c 4, local 2): router, forward and
+    backward on HIP events, against torch SDPA dense causal forward + backward; also in bf16."""
+    from ssa_amd import ssa_swap as S
+    out = {"workload": "ssa_masked training step: B=4, H=12, n=1024, d=64 (GPT-2 attention), "
+                       "block 64, top_c 4, local 2; q/k/v ~ N(0,1)"}
+    for dt, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        g = torch.Generator(device=dev).manual_seed(0)
+        q, k, v, go = (torch.randn(4, 12, 1024, 64, device=dev, dtype=dt, generator=g)
+                       for _ in range(4))
+        for t in (q, k, v):
+            t.requires_grad_(True)
+        tm = Timer(torch)
+        for rep in range(8):
+            tmr = tm if rep >= 3 else Timer(torch)
+            kv_num, kv_idx = tmr.run("route", S.route_masked, q.detach(), k.detach(), 64, 4, 2)
+            o = tmr.run("fwd", S._MaskedAttention.apply, q, k, v, kv_num, kv_idx, 64, 0.125)
+            tmr.run("bwd", o.backward, go)
+            q.grad = k.grad = v.grad = None
+            d_o = tmr.run("sdpa_fwd", torch.nn.functional.scaled_dot_product_attention, q, k, v,
+                          is_causal=True)
+            tmr.run("sdpa_bwd", d_o.backward, go)
+            q.grad = k.grad = v.grad = None
+        torch.cuda.synchronize()
+        ms = {x: tm.mean_ms(x) for x in ("route", "fwd", "bwd", "sdpa_fwd", "sdpa_bwd")}
+        total = ms["route"] + ms["fwd"] + ms["bwd"]
+        dense = ms["sdpa_fwd"] + ms["sdpa_bwd"]
+        out[tag] = {**{f"{x}_ms": y for x, y in ms.items()}, "step_ms": total,
+                    "sdpa_step_ms": dense, "speedup_vs_sdpa": dense / total,
+                    "mean_blocks_per_row": float(kv_num.float().mean().item())}
+        del q, k, v, go, o, d_o
+    return out
 
 
 def main():
@@ -262,6 +299,10 @@ def main():
             "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
         }
         del kd, vd, qd, dec
+
+    if not args.no_swap:
+        log("bench: attention swap (ssa_masked forward + backward)")
+        result["swap"] = swap_bench(torch, dev)
 
     if not args.no_c5:
         log("bench: C5 12M-token prefill")

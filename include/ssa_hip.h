@@ -67,8 +67,10 @@ int ssa_device_supported(int device);
  * Per-block summaries of x (B, H, n, d): out (B, H, nb, d) fp32 contiguous, nb = ceil(n/block).
  * Sums are accumulated in fp64 and rounded once to fp32; the variance is two-pass about the
  * fp64 mean.
- *   POP:      rows r < min(n, n_real) of a block are counted; cnt = max(1, #counted);
+ *   POP:      rows r < n_real of a block are counted; cnt = max(1, #counted);
  *             mu = sum/cnt, var = sum((x-mu)^2)/cnt, m3 = sum((x-mu)^3)/cnt (m3 may be NULL).
+ *             n_real > n counts the rows [n, n_real) as zero rows, up to the end of the last
+ *             block (the zero padding before the statistics of ssa/ssa_swap.py:37-41).
  *             Replaces ssa/ssa_kernel.py:78-91 (block_route_budget, incl. the n_real branch
  *             :80-87) and ssa/gemma_ssa.py:65-82 (_block_stats).
  *   UNBIASED: var = sum((x-mu)^2)/(cnt-1). Replaces ssa/ssa_kernel.py:42-43,47 (kb.var(3)).

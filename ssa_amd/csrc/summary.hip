@@ -43,11 +43,12 @@ __device__ inline void reduce_columns(const double* red, double* colv, int d, in
 template <int DT>
 __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     const char* __restrict__ x, int64_t H, int d, int64_t sb, int64_t sh, int64_t sn,
-    int64_t block, int64_t rows_counted, int mode, float* __restrict__ mu,
+    int64_t block, int64_t n_rows, int64_t rows_counted, int mode, float* __restrict__ mu,
     float* __restrict__ var, float* __restrict__ m3, int64_t nb) {
   constexpr int ES = DT == SSA_F32 ? 4 : 2;
   __shared__ double red[kSumThreads * 8];
   __shared__ double colv[kMaxD];
+  __shared__ double colm[kMaxD];  // fp64 column means
 
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / H, h = bh % H;
@@ -62,6 +63,11 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   int64_t end = start + block;
   if (end > rows_counted) end = rows_counted;
   const int64_t cnt_rows = end > start ? end - start : 0;
+  // rows [n_rows, end) are zero rows that count (rows_counted > n_rows): they add nothing to the
+  // sums and (0 - mean)^p to the centred moments
+  const int64_t rend = end < n_rows ? end : n_rows;
+  const int64_t zrows = end - (start > rend ? start : rend);
+  const double z = zrows > 0 ? (double)zrows : 0.0;
   const char* base = x + (b * sb + h * sh) * ES + (int64_t)cv * 8 * ES;
   const int64_t out_row = (bh * nb + c) * d;
 
@@ -69,7 +75,7 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   double acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0;
-  for (int64_t r = start + r0; r < end; r += rpp) {
+  for (int64_t r = start + r0; r < rend; r += rpp) {
     float v[8];
     load_row8<DT>(base + r * sn * ES, v);
 #pragma unroll
@@ -86,7 +92,10 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     return;
   }
   const double cnt = cnt_rows > 0 ? (double)cnt_rows : 1.0;
-  for (int t = tid; t < d; t += kSumThreads) mu[out_row + t] = (float)(colv[t] / cnt);
+  for (int t = tid; t < d; t += kSumThreads) {
+    colm[t] = colv[t] / cnt;
+    mu[out_row + t] = (float)(colv[t] / cnt);
+  }
   double mean[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) mean[j] = colv[cv * 8 + j] / cnt;
@@ -96,7 +105,7 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   double a2[8], a3[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) a2[j] = a3[j] = 0.0;
-  for (int64_t r = start + r0; r < end; r += rpp) {
+  for (int64_t r = start + r0; r < rend; r += rpp) {
     float v[8];
     load_row8<DT>(base + r * sn * ES, v);
 #pragma unroll
@@ -114,7 +123,8 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     reduce_columns(red, colv, d, rpp, tid);
     __syncthreads();
     const double vden = mode == SSA_STATS_UNBIASED ? cnt - 1.0 : cnt;
-    for (int t = tid; t < d; t += kSumThreads) var[out_row + t] = (float)(colv[t] / vden);
+    for (int t = tid; t < d; t += kSumThreads)
+      var[out_row + t] = (float)((colv[t] + z * colm[t] * colm[t]) / vden);
     __syncthreads();
   }
   if (m3 != nullptr) {
@@ -123,7 +133,8 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     __syncthreads();
     reduce_columns(red, colv, d, rpp, tid);
     __syncthreads();
-    for (int t = tid; t < d; t += kSumThreads) m3[out_row + t] = (float)(colv[t] / cnt);
+    for (int t = tid; t < d; t += kSumThreads)
+      m3[out_row + t] = (float)((colv[t] - z * colm[t] * colm[t] * colm[t]) / cnt);
   }
 }
 
@@ -135,7 +146,9 @@ int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t
                          int mode, float* mu, float* var, float* m3, int64_t nb_out,
                          int64_t block_offset, hipStream_t stream) {
   const int64_t nb = (n + block - 1) / block;
-  const int64_t rows_counted = mode == SSA_STATS_QMEAN ? n : (n_real < n ? n_real : n);
+  // n_real > n: rows [n, n_real) count as zero rows (capped at the last block's end)
+  int64_t rows_counted = mode == SSA_STATS_QMEAN ? n : n_real;
+  if (rows_counted > nb * block) rows_counted = nb * block;
   dim3 grid((unsigned)nb, (unsigned)(B * H));
   float* mu_o = mu + block_offset * d;
   float* var_o = var ? var + block_offset * d : nullptr;
@@ -144,15 +157,15 @@ int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t
   switch (dtype) {
     case SSA_F32:
       block_summary_kernel<SSA_F32><<<grid, kSumThreads, 0, stream>>>(
-          xp, H, (int)d, sb, sh, sn, block, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
+          xp, H, (int)d, sb, sh, sn, block, n, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
       break;
     case SSA_F16:
       block_summary_kernel<SSA_F16><<<grid, kSumThreads, 0, stream>>>(
-          xp, H, (int)d, sb, sh, sn, block, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
+          xp, H, (int)d, sb, sh, sn, block, n, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
       break;
     default:
       block_summary_kernel<SSA_BF16><<<grid, kSumThreads, 0, stream>>>(
-          xp, H, (int)d, sb, sh, sn, block, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
+          xp, H, (int)d, sb, sh, sn, block, n, rows_counted, mode, mu_o, var_o, m3_o, nb_out);
       break;
   }
   return launch_status("block_summary_kernel");

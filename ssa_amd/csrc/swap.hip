@@ -28,8 +28,6 @@
 // rows the previous product's accumulators already hold in each half.
 #include <math.h>
 
-#include <type_traits>
-
 #include "common.h"
 
 namespace ssa {
@@ -555,6 +553,413 @@ __global__ __launch_bounds__(256) void swap_dkdv_kernel(SwapArgs a) {
     }
 }
 
+// ---- 16-bit inputs: v_mfma_f32_32x32x16_{bf16,f16} ------------------------------------------
+// Tiles stay 16-bit in LDS (row-major stride kRS16, transposed stride kTS16 halves); P and dS are
+// rounded to the input type for the second products, as flash attention does. Operand layout
+// (32x32x16): lane l supplies A[l%32][8*(l/32) + j] and B[8*(l/32) + j][l%32], j = 0..7.
+// Head-dim steps t = 0..3 use d = 32*(l/32) + 8t + j; key (query) steps u = 0..1 over a wave's
+// 32 accumulator rows use the rows its registers e = 8u + j hold: 16u + 8*(j/4) + 4*(l/32) + j%4.
+
+constexpr int kRS16 = 72;  // 144 B rows: conflict-free 16-byte reads
+constexpr int kTS16 = 68;  // 136 B rows: conflict-free 8-byte reads
+
+template <int DT>
+struct Mma16;
+template <>
+struct Mma16<SSA_BF16> {
+  typedef bf16x8 vec;
+  __device__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(vec, a),
+                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
+  }
+  __device__ static unsigned int bits(float x) { return __builtin_bit_cast(unsigned short, (__bf16)x); }
+};
+template <>
+struct Mma16<SSA_F16> {
+  typedef f16x8 vec;
+  __device__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(vec, a),
+                                                  __builtin_bit_cast(vec, b), c, 0, 0, 0);
+  }
+  __device__ static unsigned int bits(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+};
+
+// 8 fp32 values (x[0..7]) rounded and packed as one 16-byte operand
+template <int DT>
+__device__ inline u32x4 pack8(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = Mma16<DT>::bits(x[2 * i]) | (Mma16<DT>::bits(x[2 * i + 1]) << 16);
+  return r;
+}
+
+// Stages rows [r0, r0 + 64) of a 16-bit (rows, 64) matrix without conversion (256 threads).
+__device__ inline void stage16(const char* base, int64_t rs, int64_t r0, int64_t nrows,
+                               unsigned short* dst, unsigned short* dstT, int tid) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i, row = c >> 3, col = (c & 7) * 8;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (r0 + row < nrows)
+      w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned short*>(base) + (r0 + row) * rs + col);
+    if (dst) *reinterpret_cast<u32x4*>(dst + row * kRS16 + col) = w;
+    if (dstT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        dstT[(col + j) * kTS16 + row] = (unsigned short)((j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xffffu));
+    }
+  }
+}
+
+__device__ inline u32x4 lds16(const unsigned short* p) { return *reinterpret_cast<const u32x4*>(p); }
+// halves p[0..3] and p[8..11] of a transposed tile row
+__device__ inline u32x4 lds_pair(const unsigned short* p) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 x = *reinterpret_cast<const u32x2*>(p), y = *reinterpret_cast<const u32x2*>(p + 8);
+  return u32x4{x[0], x[1], y[0], y[1]};
+}
+
+// one row's 32 halves [32*hi, 32*hi + 32) as 4 packed operands (zeros when !valid)
+__device__ inline void load_row16(const char* base, int64_t off, bool valid, u32x4* out) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (valid) w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned short*>(base) + off + 8 * t);
+    out[t] = w;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swap_fwd16_kernel(SwapArgs a) {
+  // K and V^T tiles (17920 B), later the 34 x 128-float merge buffer (17408 B)
+  __shared__ __attribute__((aligned(16))) char smem[64 * kRS16 * 2 + 64 * kTS16 * 2];
+  static_assert(64 * kRS16 * 2 + 64 * kTS16 * 2 >= 34 * 128 * 4, "merge buffer");
+  unsigned short* ks = reinterpret_cast<unsigned short*>(smem);  // K [key][d]
+  unsigned short* vt = ks + 64 * kRS16;                          // V [d][key]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hi = lane >> 5, lo = lane & 31;
+  const int qh = w & 1, kh = w >> 1;
+  const int64_t nbh = a.B * a.Hq;
+  const int64_t bh = blockIdx.x % nbh, qt = a.nqt - 1 - blockIdx.x / nbh;
+  const int64_t b = bh / a.Hq, h = bh % a.Hq, kvh = h / a.G;
+  const int64_t q0 = qt * 64;
+  const int r = 32 * qh + lo;
+  const int64_t qi = q0 + r;
+  const bool qvalid = qi < a.n;
+  u32x4 qv[4];
+  load_row16(a.q, b * a.qsb + h * a.qsh + qi * a.qsn + 32 * hi, qvalid, qv);
+  const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
+  const char* kb = a.k + (b * a.ksb + kvh * a.ksh) * 2;
+  const char* vb = a.v + (b * a.vsb + kvh * a.vsh) * 2;
+  const float sl2 = a.scale_log2;
+
+  float m = -INFINITY, l = 0.0f;
+  f32x16 o[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[x][e] = 0.0f;
+  int64_t qlast = q0 + 63;
+  if (qlast > a.n - 1) qlast = a.n - 1;
+  const int64_t nkt = qlast / 64 + 1;
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = kt * 64;
+    unsigned long long any, keys;
+    tile_bits(mrow, k0, a.block, a.nb, qvalid ? r : -1, any, keys);
+    if (any == 0ull) continue;
+    __syncthreads();
+    stage16(kb, a.ksn, k0, a.n, ks, nullptr, tid);
+    stage16(vb, a.vsn, k0, a.n, nullptr, vt, tid);
+    __syncthreads();
+    f32x16 s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      s = Mma16<DT>::mma(lds16(ks + (32 * kh + lo) * kRS16 + 32 * hi + 8 * t), qv[t], s);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kk = 32 * kh + (e >> 2) * 8 + hi * 4 + (e & 3);
+      const bool ok = ((keys >> kk) & 1ull) && (k0 + kk <= qi);
+      s[e] = ok ? s[e] * sl2 : -INFINITY;
+      mx = fmaxf(mx, s[e]);
+    }
+    mx = pair_max(mx);
+    const float mnew = fmaxf(m, mx);
+    const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+    float p[16];
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = s[e] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[e] - mnew);
+      ps += p[e];
+    }
+    l = l * alpha + ps;
+    m = mnew;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[x][e] *= alpha;
+    const u32x4 p0 = pack8<DT>(p), p1 = pack8<DT>(p + 8);
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) {
+      const unsigned short* vrow = vt + (32 * dh + lo) * kTS16 + 32 * kh + 4 * hi;
+      o[dh] = Mma16<DT>::mma(lds_pair(vrow), p0, o[dh]);
+      o[dh] = Mma16<DT>::mma(lds_pair(vrow + 16), p1, o[dh]);
+    }
+  }
+  l = pair_sum(l);
+  __syncthreads();
+  float* buf = reinterpret_cast<float*>(smem);  // 34 x 128 floats
+  const int slot = qh * 64 + lane;
+  if (kh == 1) {
+    buf[slot] = m;
+    buf[128 + slot] = l;
+#pragma unroll
+    for (int x = 0; x < 32; ++x) buf[(2 + x) * 128 + slot] = o[x >> 4][x & 15];
+  }
+  __syncthreads();
+  if (kh == 1 || !qvalid) return;
+  const float m1 = buf[slot], l1 = buf[128 + slot];
+  const float M = fmaxf(m, m1);
+  const float a0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+  const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
+  const float lt = l * a0 + l1 * a1;
+  const float inv = 1.0f / lt;
+  float of[32];
+#pragma unroll
+  for (int x = 0; x < 32; ++x) of[x] = (o[x >> 4][x & 15] * a0 + buf[(2 + x) * 128 + slot] * a1) * inv;
+  const int64_t ooff = b * a.osb + h * a.osh + qi * a.osn;
+#pragma unroll
+  for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * dh + 8 * g + 4 * hi, x = 16 * dh + 4 * g;
+      store4<DT>(a.o, ooff + d0, of[x], of[x + 1], of[x + 2], of[x + 3]);
+    }
+  if (hi == 0) a.lse[bh * a.n + qi] = (M + log2f(lt)) * kLn2S;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swap_dq16_kernel(SwapArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * 64 * kRS16 * 2 + 64 * kTS16 * 2];
+  static_assert(2 * 64 * kRS16 * 2 + 64 * kTS16 * 2 >= 32 * 128 * 4, "merge buffer");
+  unsigned short* ks = reinterpret_cast<unsigned short*>(smem);  // K [key][d]
+  unsigned short* vs = ks + 64 * kRS16;                          // V [key][d]
+  unsigned short* kt_ = vs + 64 * kRS16;                         // K [d][key]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hi = lane >> 5, lo = lane & 31;
+  const int qh = w & 1, kh = w >> 1;
+  const int64_t nbh = a.B * a.Hq;
+  const int64_t bh = blockIdx.x % nbh, qt = a.nqt - 1 - blockIdx.x / nbh;
+  const int64_t b = bh / a.Hq, h = bh % a.Hq, kvh = h / a.G;
+  const int64_t q0 = qt * 64;
+  const int r = 32 * qh + lo;
+  const int64_t qi = q0 + r;
+  const bool qvalid = qi < a.n;
+  u32x4 qv[4], gv[4];
+  load_row16(a.q, b * a.qsb + h * a.qsh + qi * a.qsn + 32 * hi, qvalid, qv);
+  const int64_t ooff = b * a.osb + h * a.osh + qi * a.osn + 32 * hi;
+  load_row16(a.dout, ooff, qvalid, gv);
+  float Di;
+  {
+    float orow[32], grow[32];
+    load_row32<DT>(a.o, ooff, qvalid, orow);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) unpack8(gv[t], grow + 8 * t, DT == SSA_BF16);
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) acc = fmaf(grow[t], orow[t], acc);
+    Di = pair_sum(acc);
+  }
+  const int64_t rid = bh * a.n + qi;
+  const float lse2 = qvalid ? a.lse[rid] * kLog2eS : 0.0f;
+  if (qvalid && kh == 0 && hi == 0) a.delta[rid] = Di;
+  const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
+  const char* kb = a.k + (b * a.ksb + kvh * a.ksh) * 2;
+  const char* vb = a.v + (b * a.vsb + kvh * a.vsh) * 2;
+  const float sl2 = a.scale_log2;
+
+  f32x16 dqa[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqa[x][e] = 0.0f;
+  int64_t qlast = q0 + 63;
+  if (qlast > a.n - 1) qlast = a.n - 1;
+  const int64_t nkt = qlast / 64 + 1;
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = kt * 64;
+    unsigned long long any, keys;
+    tile_bits(mrow, k0, a.block, a.nb, qvalid ? r : -1, any, keys);
+    if (any == 0ull) continue;
+    __syncthreads();
+    stage16(kb, a.ksn, k0, a.n, ks, kt_, tid);
+    stage16(vb, a.vsn, k0, a.n, vs, nullptr, tid);
+    __syncthreads();
+    f32x16 s, dp;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      s[e] = 0.0f;
+      dp[e] = 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int off = (32 * kh + lo) * kRS16 + 32 * hi + 8 * t;
+      s = Mma16<DT>::mma(lds16(ks + off), qv[t], s);
+      dp = Mma16<DT>::mma(lds16(vs + off), gv[t], dp);
+    }
+    float ds[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kk = 32 * kh + (e >> 2) * 8 + hi * 4 + (e & 3);
+      const bool ok = ((keys >> kk) & 1ull) && (k0 + kk <= qi);
+      const float p = ok ? __builtin_amdgcn_exp2f(fmaf(s[e], sl2, -lse2)) : 0.0f;
+      ds[e] = p * (dp[e] - Di);
+    }
+    const u32x4 d0 = pack8<DT>(ds), d1 = pack8<DT>(ds + 8);
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) {
+      const unsigned short* krow = kt_ + (32 * dh + lo) * kTS16 + 32 * kh + 4 * hi;
+      dqa[dh] = Mma16<DT>::mma(lds_pair(krow), d0, dqa[dh]);
+      dqa[dh] = Mma16<DT>::mma(lds_pair(krow + 16), d1, dqa[dh]);
+    }
+  }
+  __syncthreads();
+  float* buf = reinterpret_cast<float*>(smem);  // 32 x 128 floats
+  const int slot = qh * 64 + lane;
+  if (kh == 1) {
+#pragma unroll
+    for (int x = 0; x < 32; ++x) buf[x * 128 + slot] = dqa[x >> 4][x & 15];
+  }
+  __syncthreads();
+  if (kh == 1 || !qvalid) return;
+  float* dqr = a.dq + rid * 64;
+#pragma unroll
+  for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = 32 * dh + 8 * g + 4 * hi, x = 16 * dh + 4 * g;
+      f32x4 val;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) val[j] = (dqa[dh][4 * g + j] + buf[(x + j) * 128 + slot]) * a.scale;
+      *reinterpret_cast<f32x4*>(dqr + dd) = val;
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * 64 * kRS16 * 2 + 2 * 64 * kTS16 * 2];
+  static_assert(2 * 64 * kRS16 * 2 + 2 * 64 * kTS16 * 2 >= 2 * 32 * 128 * 4, "merge buffers");
+  __shared__ float lse_s[64], del_s[64];
+  unsigned short* qs = reinterpret_cast<unsigned short*>(smem);  // Q [q][d]
+  unsigned short* gs = qs + 64 * kRS16;                          // dO [q][d]
+  unsigned short* qtT = gs + 64 * kRS16;                         // Q [d][q]
+  unsigned short* gtT = qtT + 64 * kTS16;                        // dO [d][q]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hi = lane >> 5, lo = lane & 31;
+  const int kq = w & 1, qp = w >> 1;
+  const int64_t nbkv = a.B * a.Hkv;
+  const int64_t bkv = blockIdx.x % nbkv, kt = blockIdx.x / nbkv;
+  const int64_t b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+  const int64_t k0 = kt * 64;
+  const int64_t key = k0 + 32 * kq + lo;
+  const bool kvalid = key < a.n;
+  u32x4 kv[4], vv[4];
+  load_row16(a.k, b * a.ksb + kvh * a.ksh + key * a.ksn + 32 * hi, kvalid, kv);
+  load_row16(a.v, b * a.vsb + kvh * a.vsh + key * a.vsn + 32 * hi, kvalid, vv);
+  const int64_t ck = kvalid ? key / a.block : 0;
+  const float sl2 = a.scale_log2;
+
+  f32x16 dka[2], dva[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      dka[x][e] = 0.0f;
+      dva[x][e] = 0.0f;
+    }
+  for (int64_t g = 0; g < a.G; ++g) {
+    const int64_t hq = kvh * a.G + g, bh = b * a.Hq + hq;
+    const char* qb = a.q + (b * a.qsb + hq * a.qsh) * 2;
+    const char* gb = a.dout + (b * a.osb + hq * a.osh) * 2;
+    for (int64_t qt = k0 / 64; qt < a.nqt; ++qt) {
+      const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
+      unsigned long long any, unused;
+      tile_bits(mrow, k0, a.block, a.nb, -1, any, unused);
+      if (any == 0ull) continue;
+      const unsigned long long mw = kvalid ? mrow[ck] : 0ull;
+      const int64_t q0 = qt * 64;
+      __syncthreads();
+      stage16(qb, a.qsn, q0, a.n, qs, qtT, tid);
+      stage16(gb, a.osn, q0, a.n, gs, gtT, tid);
+      if (tid < 64) {
+        const bool ok = q0 + tid < a.n;
+        lse_s[tid] = ok ? a.lse[bh * a.n + q0 + tid] * kLog2eS : 0.0f;
+        del_s[tid] = ok ? a.delta[bh * a.n + q0 + tid] : 0.0f;
+      }
+      __syncthreads();
+      f32x16 s, dp;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        s[e] = 0.0f;
+        dp[e] = 0.0f;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int off = (32 * qp + lo) * kRS16 + 32 * hi + 8 * t;
+        s = Mma16<DT>::mma(lds16(qs + off), kv[t], s);
+        dp = Mma16<DT>::mma(lds16(gs + off), vv[t], dp);
+      }
+      float p[16], ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int qq = 32 * qp + (e >> 2) * 8 + hi * 4 + (e & 3);
+        const bool ok = ((mw >> qq) & 1ull) && (key <= q0 + qq);
+        p[e] = ok ? __builtin_amdgcn_exp2f(fmaf(s[e], sl2, -lse_s[qq])) : 0.0f;
+        ds[e] = p[e] * (dp[e] - del_s[qq]);
+      }
+      const u32x4 p0 = pack8<DT>(p), p1 = pack8<DT>(p + 8);
+      const u32x4 d0 = pack8<DT>(ds), d1 = pack8<DT>(ds + 8);
+#pragma unroll
+      for (int dh = 0; dh < 2; ++dh) {
+        const int off = (32 * dh + lo) * kTS16 + 32 * qp + 4 * hi;
+        dva[dh] = Mma16<DT>::mma(lds_pair(gtT + off), p0, dva[dh]);
+        dva[dh] = Mma16<DT>::mma(lds_pair(gtT + off + 16), p1, dva[dh]);
+        dka[dh] = Mma16<DT>::mma(lds_pair(qtT + off), d0, dka[dh]);
+        dka[dh] = Mma16<DT>::mma(lds_pair(qtT + off + 16), d1, dka[dh]);
+      }
+    }
+  }
+  __syncthreads();
+  float* bk = reinterpret_cast<float*>(smem);  // 32 x 128 floats each
+  float* bv = bk + 32 * 128;
+  const int slot = kq * 64 + lane;
+  if (qp == 1) {
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+      bk[x * 128 + slot] = dka[x >> 4][x & 15];
+      bv[x * 128 + slot] = dva[x >> 4][x & 15];
+    }
+  }
+  __syncthreads();
+  if (qp == 1 || !kvalid) return;
+  float* dkr = a.dk + (bkv * a.n + key) * 64;
+  float* dvr = a.dv + (bkv * a.n + key) * 64;
+#pragma unroll
+  for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int dd = 32 * dh + 8 * g + 4 * hi, x = 16 * dh + 4 * g;
+      f32x4 kv4, vv4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kv4[j] = (dka[dh][4 * g + j] + bk[(x + j) * 128 + slot]) * a.scale;
+        vv4[j] = dva[dh][4 * g + j] + bv[(x + j) * 128 + slot];
+      }
+      *reinterpret_cast<f32x4*>(dkr + dd) = kv4;
+      *reinterpret_cast<f32x4*>(dvr + dd) = vv4;
+    }
+}
+
 int fill_args(SwapArgs& a, const void* q, const void* k, const void* v, const void* out,
               int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
               const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
@@ -599,13 +1004,6 @@ size_t masked_tiled_workspace(int64_t B, int64_t Hq, int64_t n, int64_t block) {
   return (size_t)B * Hq * nqt * nb * 8u + (size_t)B * Hq * n * 4u;
 }
 
-template <typename F>
-static void by_dtype(int dtype, F&& f) {
-  if (dtype == SSA_F32) f(std::integral_constant<int, SSA_F32>());
-  else if (dtype == SSA_F16) f(std::integral_constant<int, SSA_F16>());
-  else f(std::integral_constant<int, SSA_BF16>());
-}
-
 int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
                      int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
                      const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
@@ -618,7 +1016,9 @@ int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, flo
   const unsigned grid = (unsigned)(B * Hq * a.nqt);
   row_block_masks_kernel<<<grid, 256, 0, st>>>(a);
   SSA_TRY(launch_status("row_block_masks_kernel"));
-  by_dtype(dtype, [&](auto dt) { swap_fwd_kernel<decltype(dt)::value><<<grid, 256, 0, st>>>(a); });
+  if (dtype == SSA_F32) swap_fwd_kernel<SSA_F32><<<grid, 256, 0, st>>>(a);
+  else if (dtype == SSA_F16) swap_fwd16_kernel<SSA_F16><<<grid, 256, 0, st>>>(a);
+  else swap_fwd16_kernel<SSA_BF16><<<grid, 256, 0, st>>>(a);
   return launch_status("swap_fwd_kernel");
 }
 
@@ -639,10 +1039,16 @@ int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* ou
   const unsigned gq = (unsigned)(B * Hq * a.nqt), gk = (unsigned)(B * Hkv * a.nkt);
   row_block_masks_kernel<<<gq, 256, 0, st>>>(a);
   SSA_TRY(launch_status("row_block_masks_kernel"));
-  by_dtype(dtype, [&](auto dt) {
-    swap_dq_kernel<decltype(dt)::value><<<gq, 256, 0, st>>>(a);
-    swap_dkdv_kernel<decltype(dt)::value><<<gk, 256, 0, st>>>(a);
-  });
+  if (dtype == SSA_F32) {
+    swap_dq_kernel<SSA_F32><<<gq, 256, 0, st>>>(a);
+    swap_dkdv_kernel<SSA_F32><<<gk, 256, 0, st>>>(a);
+  } else if (dtype == SSA_F16) {
+    swap_dq16_kernel<SSA_F16><<<gq, 256, 0, st>>>(a);
+    swap_dkdv16_kernel<SSA_F16><<<gk, 256, 0, st>>>(a);
+  } else {
+    swap_dq16_kernel<SSA_BF16><<<gq, 256, 0, st>>>(a);
+    swap_dkdv16_kernel<SSA_BF16><<<gk, 256, 0, st>>>(a);
+  }
   return launch_status("swap_dkdv_kernel");
 }
 

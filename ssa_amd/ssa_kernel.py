@@ -52,7 +52,8 @@ def block_summary(x: torch.Tensor, block: int, mode: str = "pop", n_real: int | 
     """Per-block summaries of x (B, H, n, d) -> fp32 (B, H, ceil(n/block), d) tensors.
 
     mode "pop": (mu, var, m3|None) over rows < n_real (ssa/ssa_kernel.py:80-91,
-    ssa/gemma_ssa.py:65-82); "unbiased": (mu, var) with var/(cnt-1) (ssa/ssa_kernel.py:43,47);
+    ssa/gemma_ssa.py:65-82; n_real > n counts rows [n, n_real) as zeros, the padding of
+    ssa/ssa_swap.py:37-41); "unbiased": (mu, var) with var/(cnt-1) (ssa/ssa_kernel.py:43,47);
     "qmean": the query-block mean sum(rows)/block (ssa/ssa_kernel.py:44,79).
     """
     _lib.require_device(x)

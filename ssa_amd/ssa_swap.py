@@ -36,11 +36,10 @@ def route_masked(q: torch.Tensor, k: torch.Tensor, block: int, top_c: int, local
     (B, H, n) / (B, H, n, W): statistics of the zero-padded key blocks (unbiased variance),
     candidates = blocks begun at the query, top_c by score (ties: lowest block), own block and
     `local` predecessors."""
-    B, H, n, d = q.shape
+    n = q.shape[2]
     nb = -(-n // block)
-    pad = nb * block - n
-    kk = F.pad(k, (0, 0, 0, pad)) if pad else k  # the reference counts the zero rows
-    mu, var, _ = block_summary(kk, block, "unbiased")
+    # the reference zero-pads k to nb * block rows and counts the zero rows in the statistics
+    mu, var, _ = block_summary(k, block, "unbiased", n_real=nb * block)
     return route(q.float(), mu, var, None, "started", int(top_c), 0.0, int(local), 0.5,
                  query_pos=0, block=block)
 

@@ -58,6 +58,24 @@ def test_block_summary_matches_oracle(cuda, dtype):
     assert ulp_diff(np_of(qb), O.qmean(x, 128)).max() <= 1
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_summary_counts_zero_rows_past_n(cuda, dtype):
+    """n_real > n: rows [n, n_real) count as zero rows (the zero padding ssa_swap applies before
+    its block statistics) -- equal to the statistics of the explicitly zero-padded tensor."""
+    rng = np.random.default_rng(9)
+    x = WL.round_to(rng.standard_normal((1, 2, 300, 64)).astype(np.float32) + 0.5, dtype)
+    xp = np.zeros((1, 2, 320, 64), dtype=np.float32)
+    xp[:, :, :300] = x
+    for mode in ("pop", "unbiased"):
+        mu, var, m3 = K.block_summary(dev(x, dtype, cuda), 64, mode, n_real=320, with_m3=True)
+        omu, ovar, om3 = O.block_stats(xp, 64, mode)
+        assert ulp_diff(np_of(mu), omu).max() <= 1 and ulp_diff(np_of(var), ovar).max() <= 1
+        assert np.abs(np_of(m3) - om3).max() <= 1e-6 * np.abs(om3).max()
+        # n_real beyond the last block is capped there
+        mu2, var2, _ = K.block_summary(dev(x, dtype, cuda), 64, mode, n_real=10**6)
+        assert torch.equal(mu2, mu) and torch.equal(var2, var)
+
+
 def test_block_summary_strided_input(cuda):
     """A (b, n, h, d) buffer viewed as (b, h, n, d) needs no copy and gives the same stats."""
     rng = np.random.default_rng(8)
