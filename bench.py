@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 12M-token prefill")
     ap.add_argument("--no-swap", action="store_true",
                     help="skip the trainable swap (ssa_masked forward + backward)")
+    ap.add_argument("--swap-only", action="store_true",
+                    help="run only the swap arm and print its JSON (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (PMC byte-count calibration)")
     return ap.parse_args()
@@ -182,6 +184,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.swap_only:
+        print(json.dumps({"swap": swap_bench(torch, dev)}), flush=True)
+        return
     log("bench: generating C3 inputs")
     p = WL.make("C3", args.variant)
     cfg = p["cfg"]

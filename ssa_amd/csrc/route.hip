@@ -579,91 +579,112 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
   if (lane == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
-// Rows of at most 64 key blocks without pooling or m3: one wave per row scores and selects in
-// one pass, no score workspace. S = 2^s_log2 lanes per candidate (c = lane / S) each sum a
-// contiguous ceil(d / S) slice of the head dims in fp64, combined by shuffles; the fp32 score is
-// assembled as in route_score_kernel. A candidate is kept when fewer than keep candidates rank
-// above it (larger key, or equal key and lower block index); the kept blocks and the local
-// window are compacted in ascending order by ballot.
-__global__ __launch_bounds__(256) void route_rows_small_kernel(
+// Rows of at most 64 key blocks without pooling or m3: a workgroup takes kFusedRows rows of one
+// query head, stages the key head's mu / var rows in LDS (row stride d + 4 floats) and each wave
+// scores and selects one row, no score workspace. S = 2^s_log2 lanes per candidate
+// (c = lane / S) each sum a contiguous ceil(d / S) slice of the head dims in fp64, combined by
+// shuffles; the fp32 score is assembled as in route_score_kernel. A candidate is kept when fewer
+// than keep candidates rank above it (larger key, or equal key and lower block index); the kept
+// blocks and the local window are compacted in ascending order by ballot.
+constexpr int kFusedRows = 8;       // rows (waves) per workgroup
+constexpr int kFusedLds = 64 * 68;  // floats per staged array: nbk * (d + 4) must fit
+
+__global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
     const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     RouteGeom g, int d, float coef2, int s_log2, bool vec4, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows) {
-  const int lane = threadIdx.x & 63;
-  const int64_t lrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b*Hq + h)*nbq + i
-  if (lrow >= nrows) return;  // whole wave
-  const int64_t bh = lrow / g.nbq, i = lrow % g.nbq;
+    int32_t* __restrict__ kv_idx, int64_t W) {
+  extern __shared__ __attribute__((aligned(16))) float fused_lds[];  // 2 * nbk * (d + 4) floats
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t bh = blockIdx.y;  // b * Hq + h
   const int64_t b = bh / g.Hq, h = bh % g.Hq, kvh = h / g.G;
+  const int ds = d + 4, nk = (int)g.nbk;
+  float* ms = fused_lds;
+  float* vs = fused_lds + nk * ds;
+  const float* kmu = mu + (b * g.Hkv + kvh) * g.nbk * d;
+  const float* kvar = var ? var + (b * g.Hkv + kvh) * g.nbk * d : nullptr;
+  for (int idx = tid; idx < nk * d; idx += 64 * kFusedRows) {
+    const int c = idx / d, t = idx - c * d;
+    ms[c * ds + t] = kmu[idx];
+    vs[c * ds + t] = kvar ? kvar[idx] : 0.0f;
+  }
+  __syncthreads();
   const int S = 1 << s_log2;
   const int c = lane >> s_log2, part = lane & (S - 1);
-  const int64_t cmax = row_cmax(g, i);
-  const bool cand = c < cmax;
-  double e1 = 0.0, e2 = 0.0;
-  if (cand) {
-    const int dl = (d + S - 1) >> s_log2;
-    const int k0 = part * dl, k1 = k0 + dl < d ? k0 + dl : d;
-    const float* q = rows + lrow * d;
-    const int64_t moff = ((b * g.Hkv + kvh) * g.nbk + c) * d;
-    if (vec4) {  // d a multiple of 4 * S, 16-byte aligned rows: 16-byte loads
+  const int dl = (d + S - 1) >> s_log2;
+  const int k0 = part * dl, k1 = k0 + dl < d ? k0 + dl : d;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int64_t i_first = (int64_t)blockIdx.x * kFusedRows;
+  {
+    const int64_t i = i_first + wave;
+    if (i >= g.nbq) return;  // whole wave
+    const int64_t lrow = bh * g.nbq + i;
+    const int64_t cmax = row_cmax(g, i);
+    const bool cand = c < cmax;
+    double e1 = 0.0, e2 = 0.0;
+    if (cand) {
+      const float* q = rows + lrow * d;
+      const float* mrow = ms + c * ds;
+      const float* vrow = vs + c * ds;
+      if (vec4) {  // d a multiple of 4 * S: 16-byte loads
 #pragma unroll 4
-      for (int t = k0; t < k1; t += 4) {
-        const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
-        const f32x4 ma = *reinterpret_cast<const f32x4*>(mu + moff + t);
-        f32x4 va = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (var) va = *reinterpret_cast<const f32x4*>(var + moff + t);
+        for (int t = k0; t < k1; t += 4) {
+          const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
+          const f32x4 ma = *reinterpret_cast<const f32x4*>(mrow + t);
+          const f32x4 va = *reinterpret_cast<const f32x4*>(vrow + t);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float q2 = qa[j] * qa[j];  // rounded to fp32 like the reference's product
-          e1 = fma((double)qa[j], (double)ma[j], e1);
-          e2 = fma((double)q2, (double)va[j], e2);
+          for (int j = 0; j < 4; ++j) {
+            const float q2 = qa[j] * qa[j];  // rounded to fp32 like the reference's product
+            e1 = fma((double)qa[j], (double)ma[j], e1);
+            e2 = fma((double)q2, (double)va[j], e2);
+          }
+        }
+      } else {
+        for (int t = k0; t < k1; ++t) {
+          const float qf = q[t];
+          const float q2 = qf * qf;
+          e1 = fma((double)qf, (double)mrow[t], e1);
+          e2 = fma((double)q2, (double)vrow[t], e2);
         }
       }
+    }
+    for (int off = 1; off < S; off <<= 1) {
+      e1 += __shfl_xor(e1, off, 64);
+      e2 += __shfl_xor(e2, off, 64);
+    }
+    const bool lead = part == 0;
+    const bool live = lead && cand;
+    const unsigned int key =
+        live ? score_key(__fadd_rn((float)e1, __fmul_rn(coef2, (float)e2))) : 0u;
+    const int64_t keep = row_keep(g, cmax);
+    const int64_t K = keep < cmax ? keep : cmax;
+    bool sel;
+    if (K >= cmax) {
+      sel = live;
+    } else if (K <= 0) {
+      sel = false;
     } else {
-      for (int t = k0; t < k1; ++t) {
-        const float qf = q[t];
-        const float q2 = qf * qf;
-        e1 = fma((double)qf, (double)mu[moff + t], e1);
-        if (var) e2 = fma((double)q2, (double)var[moff + t], e2);
+      // rank = candidates with a larger key, or an equal key and a lower block index
+      int rank = 0;
+      for (int j = 0; j < (int)cmax; ++j) {
+        const unsigned int kj = __shfl(key, j << s_log2, 64);
+        rank += (kj > key) || (kj == key && j < c);
       }
+      sel = live && rank < K;
     }
+    const int64_t own = row_own(g, i);
+    int64_t lo = own - g.local;
+    if (lo < 0) lo = 0;
+    const int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
+    const bool take = lead && (sel || (c >= lo && c <= hi));
+    const unsigned long long bt = __ballot(take);
+    int32_t* out = kv_idx + lrow * W;
+    const int p = __popcll(bt & lt);
+    if (take && p < W) out[p] = c;
+    const int tot = __popcll(bt);
+    const int64_t num = tot < W ? tot : W;
+    for (int64_t x = num + lane; x < W; x += 64) out[x] = 0;
+    if (lane == 0) kv_num[lrow] = (int32_t)num;
   }
-  for (int off = 1; off < S; off <<= 1) {
-    e1 += __shfl_xor(e1, off, 64);
-    e2 += __shfl_xor(e2, off, 64);
-  }
-  const bool lead = part == 0;
-  const bool live = lead && cand;
-  const unsigned int key = live ? score_key(__fadd_rn((float)e1, __fmul_rn(coef2, (float)e2))) : 0u;
-  const int64_t keep = row_keep(g, cmax);
-  const int64_t K = keep < cmax ? keep : cmax;
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  bool sel;
-  if (K >= cmax) {
-    sel = live;
-  } else if (K <= 0) {
-    sel = false;
-  } else {
-    // rank = candidates with a larger key, or an equal key and a lower block index
-    int rank = 0;
-    for (int j = 0; j < (int)cmax; ++j) {
-      const unsigned int kj = __shfl(key, j << s_log2, 64);
-      rank += (kj > key) || (kj == key && j < c);
-    }
-    sel = live && rank < K;
-  }
-  const int64_t own = row_own(g, i);
-  int64_t lo = own - g.local;
-  if (lo < 0) lo = 0;
-  const int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
-  const bool take = lead && (sel || (c >= lo && c <= hi));
-  const unsigned long long bt = __ballot(take);
-  int32_t* out = kv_idx + lrow * W;
-  const int p = __popcll(bt & lt);
-  if (take && p < W) out[p] = c;
-  const int tot = __popcll(bt);
-  const int64_t num = tot < W ? tot : W;
-  for (int64_t q = num + lane; q < W; q += 64) out[q] = 0;
-  if (lane == 0) kv_num[lrow] = (int32_t)num;
 }
 
 __global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
@@ -773,7 +794,8 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
   g.budget_frac = budget_frac;
   g.local = local;
   g.pool = pool;
-  if (nbk <= 64 && pool == 1 && m3 == nullptr) {  // score + select fused, a wave per row
+  if (nbk <= 64 && nbk * (d + 4) <= kFusedLds && pool == 1 && m3 == nullptr &&
+      B * Hq < 65536) {  // score + select fused, a wave per row
     g.i0 = 0;
     g.ni = nbq;
     int p_log2 = 0;
@@ -781,12 +803,14 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     int s_log2 = 6 - p_log2, d_log2 = 0;
     while ((1ll << d_log2) < d) ++d_log2;
     if (s_log2 > d_log2) s_log2 = d_log2;
-    const int64_t nrows = B * Hq * nbq;
-    SSA_REQUIRE((nrows + 3) / 4 < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
     const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    const bool vec4 = d % (4ll << s_log2) == 0 && a16(rows) && a16(mu) && (!var || a16(var));
-    route_rows_small_kernel<<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
-        rows, mu, var, g, (int)d, coef2, s_log2, vec4, kv_num, kv_idx, W, nrows);
+    const bool vec4 = d % (4ll << s_log2) == 0 && a16(rows);
+    const int64_t chunks = (nbq + kFusedRows - 1) / kFusedRows;
+    SSA_REQUIRE(chunks < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
+    const size_t lds = (size_t)2 * nbk * (d + 4) * sizeof(float);
+    route_rows_small_kernel<<<dim3((unsigned)chunks, (unsigned)(B * Hq)), 64 * kFusedRows, lds,
+                              stream>>>(rows, mu, var, g, (int)d, coef2, s_log2, vec4, kv_num,
+                                        kv_idx, W);
     return launch_status("route_rows_small_kernel");
   }
   unsigned int* keys = static_cast<unsigned int*>(workspace);
