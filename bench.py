@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 12M-token prefill")
     ap.add_argument("--no-swap", action="store_true",
                     help="skip the trainable swap (ssa_masked forward + backward)")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the whole-model prefill timing (Qwen2.5-0.5B architecture)")
     ap.add_argument("--swap-only", action="store_true",
                     help="run only the swap arm and print its JSON (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -308,6 +310,20 @@ def main():
     if not args.no_swap:
         log("bench: attention swap (ssa_masked forward + backward)")
         result["swap"] = swap_bench(torch, dev)
+
+    if not args.no_prefill:
+        log("bench: whole-model prefill (Qwen2.5-0.5B architecture, random weights)")
+        try:
+            from ssa_amd import longctx_swap as L
+            res = L.run([32768, 131072], [1.0, 0.25, 0.12, 0.06], log=log)
+            res["workload"] = ("model(ids, logits_to_keep=1) of the 24-layer Qwen2.5-0.5B "
+                               "architecture in bf16 (random weights, random tokens; YaRN x4 "
+                               "for both arms), dense = torch SDPA, hip = install_ssa(impl='hip', "
+                               "block 128, beta 2, budget_frac); median of 3 after 2 warm-ups")
+            result["prefill"] = res
+        except Exception as e:  # reported, never fatal to the headline line
+            result["prefill"] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.empty_cache()
 
     if not args.no_c5:
         log("bench: C5 12M-token prefill")

@@ -160,3 +160,17 @@ def test_gpt2_swap_trains(cuda):
         S.uninstall()
         S._SSA.clear()
         S._SSA.update(saved)
+
+
+def test_longctx_prefill_timing_and_smoke_gate(cuda):
+    """ssa_amd.longctx_swap on a 2-layer Qwen2.5-0.5B-shaped model (random weights): the dense
+    row, the smoke gate (full-budget swap reproduces the dense loss within 5e-2) and the budget
+    rows run end to end (ssa/longctx_swap.py:61-79,136-179)."""
+    from ssa_amd import gemma_ssa as G
+    from ssa_amd import longctx_swap as L
+    res = L.run([2048], [1.0, 0.25], layers=2, warmup=1, reps=1, log=lambda *a: None)
+    assert res["smoke"]["passed"], res["smoke"]
+    impls = [(r["impl"], r["budget"]) for r in res["rows"]]
+    assert impls == [("dense", 1.0), ("hip", 1.0), ("hip", 0.25)]
+    assert all(r["prefill_ms"] > 0 for r in res["rows"])
+    G.CFG.__dict__.update(G.SSAConfig().__dict__)
