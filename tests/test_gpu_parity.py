@@ -520,6 +520,50 @@ def test_gemma_flex_no_future_leak_and_sharing(cuda):
     assert G._SHARE["bm"] is bm0
 
 
+def test_gemma_full_budget_shared_equals_dense(cuda):
+    """test_share_route.py:61-74 restated: full budget with cross-layer sharing still reproduces
+    dense causal attention on the consumer layer; a forward of another shape is not served the
+    stashed selection (the signature check), and layers below the donor route on their own."""
+    torch.manual_seed(0)
+    n, d = 384, 64
+    q = torch.randn(1, 1, n, d, device=cuda, dtype=torch.float16)
+    k = torch.randn(1, 1, n, d, device=cuda, dtype=torch.float16)
+    v = torch.randn_like(k)
+    G.CFG = G.SSAConfig(block=128, budget_frac=1.0, impl="flex", share_route_from=0)
+    G._SHARE["sig"] = None
+    G._SHARE["bm"] = None
+    G.ssa_attention_forward(_mod(groups=1, layer_idx=0), q, k, v, scaling=1.0 / d ** 0.5)
+    out, _ = G.ssa_attention_forward(_mod(groups=1, layer_idx=1), q, k, v, scaling=1.0 / d ** 0.5)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True).transpose(1, 2)
+    assert (out.float() - ref.float()).abs().max().item() < 2e-2
+    # budget 0.25: a consumer of another length routes itself (matches an unshared forward)
+    G.CFG = G.SSAConfig(block=128, budget_frac=0.25, impl="flex", share_route_from=0)
+    G.ssa_attention_forward(_mod(groups=1, layer_idx=0), q, k, v, scaling=1.0 / d ** 0.5)
+    q2, k2, v2 = q[:, :, :256], k[:, :, :256], v[:, :, :256]
+    shared, _ = G.ssa_attention_forward(_mod(groups=1, layer_idx=1), q2, k2, v2,
+                                        scaling=1.0 / d ** 0.5)
+    G.CFG = G.SSAConfig(block=128, budget_frac=0.25, impl="flex")
+    own, _ = G.ssa_attention_forward(_mod(groups=1, layer_idx=1), q2, k2, v2,
+                                     scaling=1.0 / d ** 0.5)
+    assert torch.equal(shared, own)
+
+
+def test_gemma_decode_ignores_sharing(cuda):
+    """test_share_route.py:77-84 restated: with sharing configured, a q_len = 1 step takes the
+    per-query path and equals the per-query prefill's last row (sharing is prefill-only)."""
+    torch.manual_seed(4)
+    q = torch.randn(1, 4, 160 * 4, 64, device=cuda, dtype=torch.float32)
+    k = torch.randn(1, 2, 160 * 4, 64, device=cuda, dtype=torch.float32)
+    v = torch.randn_like(k)
+    G.CFG = G.SSAConfig(block=32, budget_frac=0.5, impl="analytic", share_route_from=0)
+    G._SHARE["sig"] = None
+    G._SHARE["bm"] = None
+    full, _ = G.ssa_attention_forward(_mod(groups=2, layer_idx=2), q, k, v, scaling=1.0)
+    inc, _ = G.ssa_attention_forward(_mod(groups=2, layer_idx=2), q[:, :, -1:], k, v, scaling=1.0)
+    assert (inc[:, 0] - full[:, -1]).abs().max().item() < 1e-5
+    assert G._SHARE["bm"] is None  # nothing stashed outside the prefill kernel path
+
+
 def test_gemma_proj_path_identity_equals_centroid_routing(cuda, tmp_path):
     """A routing projection saved in the reference's RoutingProjection format is loaded at
     install time (weights_only) and used by the prefill router; identity projections give the
