@@ -225,7 +225,7 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
  * Both take ssa_masked_attn_workspace_size(B, Hq, n, W, d, block) bytes of workspace.
  * d = 64 with at most 8192 key blocks runs the tiled MFMA kernels (per (64-row query tile, key
  *   block) row masks; q, k, v, out, dout, dq, dk, dv 16-byte aligned; deterministic). Other head
- *   dims (multiple of 8, <= 256) run one wave per (row, selected block); their backward
+ *   dims (multiple of 8, <= 512) run one wave per (row, selected block); their backward
  *   accumulates with fp32 atomics, so its last bit depends on summation order.
  */
 size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W, int64_t d,

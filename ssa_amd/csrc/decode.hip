@@ -47,7 +47,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxDecodeBlock = 1024;
-constexpr int kMaxDecodeD = 256;
+constexpr int kMaxDecodeD = 512;
 
 struct DecodeParams {
   const char* q;
@@ -457,7 +457,7 @@ int check_decode(int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t nq, int6
               "decode: query positions [%lld,%lld) outside the cache [0,%lld)", (long long)pos,
               (long long)(pos + nq), (long long)cap);
   SSA_REQUIRE(d % 8 == 0 && d >= 8 && d <= kMaxDecodeD, SSA_ERR_UNSUPPORTED,
-              "decode: head_dim %lld unsupported (multiple of 8, <= 256)", (long long)d);
+              "decode: head_dim %lld unsupported (multiple of 8, <= %d)", (long long)d, kMaxDecodeD);
   SSA_REQUIRE(block <= kMaxDecodeBlock, SSA_ERR_UNSUPPORTED, "decode: block > %d", kMaxDecodeBlock);
   SSA_REQUIRE(W < 65536, SSA_ERR_UNSUPPORTED, "decode: W too large");
   const int64_t vec = dtype == SSA_F32 ? 4 : 8;

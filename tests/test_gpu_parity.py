@@ -564,6 +564,81 @@ def test_gemma_decode_ignores_sharing(cuda):
     assert G._SHARE["bm"] is None  # nothing stashed outside the prefill kernel path
 
 
+def _dense_ref(q, k, v, scaling):
+    G_ = q.shape[1] // k.shape[1]
+    kr = k.repeat_interleave(G_, dim=1).double()
+    vr = v.repeat_interleave(G_, dim=1).double()
+    s = (q.double() @ kr.transpose(-1, -2)) * scaling
+    n = q.shape[2]
+    s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device=q.device).triu(1), float("-inf"))
+    return (torch.softmax(s, -1) @ vr).transpose(1, 2)
+
+
+def test_gemma_needle_known_answer_d512(cuda):
+    """test_gemma_ssa.py:100-121 restated on the HIP per-query path at the Gemma head size
+    (d = 512): with top_c = 1 and no local window, the probe query at the last position routes to
+    the block holding a key 12x aligned with it, and its output is that key's value."""
+    torch.manual_seed(0)
+    n, d = 128, 512
+    q = torch.randn(1, 1, n, d, device=cuda, dtype=torch.float32)
+    k = torch.randn(1, 1, n, d, device=cuda, dtype=torch.float32)
+    v = torch.randn(1, 1, n, d, device=cuda, dtype=torch.float32)
+    u = F.normalize(torch.randn(d, device=cuda), dim=0)
+    q[0, 0, n - 1] = u
+    k[0, 0, 40] = 12.0 * u
+    v[0, 0, 40] = torch.arange(d, device=cuda, dtype=torch.float32) / d
+    G.CFG = G.SSAConfig(block=32, top_c=1, local_w=0, beta=2.0)
+    out, _ = G.ssa_attention_forward(_mod(groups=1), q, k, v, scaling=1.0)
+    ref = _dense_ref(q, k, v, 1.0)
+    assert (out[0, n - 1].double() - ref[0, n - 1]).abs().max().item() < 3e-3
+    assert (out[0, n - 1] - v[0, 0, 40]).abs().max().item() < 3e-3
+
+
+def test_gemma_d512_gqa_full_budget_and_budget_monotone(cuda):
+    """test_gemma_ssa.py:45-84,156-168 restated at d = 512, GQA 2:1 on the per-query path: full
+    budget (and top_c >= blocks) equals dense causal attention; the attended key count shrinks
+    strictly with the budget."""
+    torch.manual_seed(1)
+    n, d = 160, 512
+    q = torch.randn(1, 4, n, d, device=cuda, dtype=torch.float32)
+    k = torch.randn(1, 2, n, d, device=cuda, dtype=torch.float32)
+    v = torch.randn(1, 2, n, d, device=cuda, dtype=torch.float32)
+    ref = _dense_ref(q, k, v, 1.0 / math.sqrt(d))
+    for cfg in (G.SSAConfig(block=32, budget_frac=1.0), G.SSAConfig(block=32, top_c=99)):
+        G.CFG = cfg
+        out, _ = G.ssa_attention_forward(_mod(groups=2), q, k, v, scaling=1.0 / math.sqrt(d))
+        assert (out.double() - ref).abs().max().item() < 1e-5
+    counts = []
+    mu, var, _ = K.block_summary(k, 32, "pop", n_real=n)
+    for frac in (1.0, 0.5, 0.25, 0.1):
+        kn, ki = K.route(q.float(), mu, var, None, "query", None, frac, 0, 1.0, query_pos=0,
+                         block=32)
+        sets = GU.row_sets(kn.cpu().numpy(), ki.cpu().numpy())
+        # attended keys: keys <= row of the selected blocks
+        tot = 0
+        for r, blocks in enumerate(sets):
+            i = r % n
+            tot += sum(min(32, i + 1 - 32 * c) for c in blocks if 32 * c <= i)
+        counts.append(tot)
+    assert counts[0] > counts[1] > counts[2] > counts[3], counts
+
+
+def test_gemma_sliding_layer_falls_back(cuda):
+    """test_gemma_ssa.py:146-153: a sliding layer defers to the installed fallback untouched."""
+    G.CFG = G.SSAConfig(block=32, budget_frac=0.1, route_full_only=True)
+    sentinel = object()
+    saved = G._FALLBACK
+    try:
+        G._FALLBACK = lambda module, q, k, v, mask=None, scaling=None, dropout=0.0, **kw: (sentinel, None)
+        from types import SimpleNamespace
+        mod = SimpleNamespace(num_key_value_groups=1, is_sliding=True, scaling=1.0, layer_idx=0)
+        q = torch.randn(1, 1, 64, 64, device=cuda)
+        out, _ = G.ssa_attention_forward(mod, q, q, q, scaling=1.0)
+        assert out is sentinel
+    finally:
+        G._FALLBACK = saved
+
+
 def test_gemma_proj_path_identity_equals_centroid_routing(cuda, tmp_path):
     """A routing projection saved in the reference's RoutingProjection format is loaded at
     install time (weights_only) and used by the prefill router; identity projections give the
