@@ -11,7 +11,7 @@
 //   finds the keep-th largest key T; keys > T are taken, and keys == T in increasing block order
 //   until keep is reached (ties -> lowest block index). The selection, the own block and its
 //   `local` predecessors are OR-ed into an LDS bitmap that is compacted in ascending order.
-//   With at most 256 key blocks, route_select_small_kernel does the same with one wave per row;
+//   With at most 1024 key blocks, route_select_small_kernel does the same with one wave per row;
 //   with at most 64 (no pooling, no m3) route_rows_small_kernel scores and selects in one pass.
 //
 // Reference: ssa/ssa_kernel.py:45-57 (block_route), :92-118 (block_route_budget),
@@ -495,13 +495,13 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   if (tid == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
-// Rows of at most kSmallNbk key blocks: one wave per row, lane l holds candidates l + 64 j. The
+// Rows of at most 64 * J key blocks: one wave per row, lane l holds candidates l + 64 j. The
 // keep-th largest key T is found bit by bit from the top (count of keys >= T | bit by ballots),
 // keys > T are taken, and keys == T in increasing block order until keep is reached; the
 // selection plus the local window is compacted in ascending order from the per-j ballots.
-constexpr int kSmallJ = 4;
-constexpr int kSmallNbk = 64 * kSmallJ;
+constexpr int kSmallNbk = 1024;  // J = 16
 
+template <int kSmallJ>
 __global__ __launch_bounds__(256) void route_select_small_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
     int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows) {
@@ -540,11 +540,11 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     for (int j = 0; j < kSmallJ; ++j) sel[j] = false;
   } else {
     unsigned int T = 0u;  // largest T with #{keys >= T} >= K: the K-th largest key
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 0; --bit) {  // non-candidates hold key 0 < t
       const unsigned int t = T | (1u << bit);
       int cnt = 0;
 #pragma unroll
-      for (int j = 0; j < kSmallJ; ++j) cnt += __popcll(__ballot(cand[j] && key[j] >= t));
+      for (int j = 0; j < kSmallJ; ++j) cnt += __popcll(__ballot(key[j] >= t));
       if (cnt >= K) T = t;
     }
     int above = 0;
@@ -851,9 +851,12 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     }
     const int64_t nrows = B * Hq * g.ni;
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
-    if (nbk <= kSmallNbk)  // few candidates: a wave per row
-      route_select_small_kernel<<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(keys, g, kv_num,
-                                                                             kv_idx, W, nrows);
+    if (nbk <= 256)  // few candidates: a wave per row
+      route_select_small_kernel<4><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
+          keys, g, kv_num, kv_idx, W, nrows);
+    else if (nbk <= kSmallNbk)
+      route_select_small_kernel<16><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
+          keys, g, kv_num, kv_idx, W, nrows);
     else if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
       route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W);
     else
