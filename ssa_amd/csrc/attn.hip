@@ -36,6 +36,9 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.0f;
+// Rows whose scores provably stay within +-kFastBound (log2 units) take the softmax without a
+// running max: 2^s neither overflows nor underflows fp32 / bf16 there.
+constexpr float kFastBound = 100.0f;
 
 struct AttnParams {
   const char* q;
@@ -50,6 +53,7 @@ struct AttnParams {
   int64_t W;
   float scale_log2;
   float* lse;
+  const float* kmax2;  // per (b, kv head): largest squared key norm (NULL: no bound)
   int64_t qsub;   // query sub-tiles per query block
   int64_t total;  // logical workgroups
   int64_t group;  // logical workgroups placed together on one XCD
@@ -129,6 +133,44 @@ struct Mfma<SSA_F16> {
     return acc;
   }
 };
+
+// Largest squared key norm per (b, kv head): grid (chunks, B*Hkv), 256 threads, one key row per
+// thread per pass; non-negative floats order like their bit patterns, so the workgroup maxima are
+// merged with an unsigned atomicMax into out (zeroed by the caller's fill launch).
+__global__ __launch_bounds__(256) void key_norm_max_kernel(const unsigned short* __restrict__ k,
+                                                           int64_t Hkv, int64_t n, int64_t ksb,
+                                                           int64_t ksh, int64_t ksn, bool bf16,
+                                                           float* __restrict__ out) {
+  __shared__ float red[4];
+  const int64_t bk = blockIdx.y;
+  const int64_t b = bk / Hkv, kvh = bk % Hkv;
+  const unsigned short* base = k + b * ksb + kvh * ksh;
+  float mx = 0.0f;
+  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < n; r += (int64_t)gridDim.x * 256) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(base + r * ksn + c * 8);
+      float x[8];
+      unpack8(w, x, bf16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(x[j], x[j], acc);
+    }
+    mx = fmaxf(mx, acc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    atomicMax(reinterpret_cast<unsigned int*>(out) + bk, __float_as_uint(m));
+  }
+}
+
+__global__ __launch_bounds__(64) void zero_floats_kernel(float* x, int64_t n) {
+  for (int64_t i = threadIdx.x; i < n; i += 64) x[i] = 0.0f;
+}
 
 // V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n. grid (n_pad/64, B*Hkv).
 __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict__ v,
@@ -288,7 +330,10 @@ __device__ inline int swz(int r) { return (r >> 1) & 7; }
 // of NW waves owns ROWS = 32*CG*NW rows of one query block and walks its selected key blocks in
 // 64-key sub-tiles. K and V^T sub-tiles (64 rows x 128 B each, swizzled) go HBM -> LDS directly
 // (global_load_lds_dwordx4, no staging registers) into a 2-stage ring, one barrier per sub-tile.
-template <int DT, int NW, int CG, int WPE>
+// MODE 0: every workgroup, exact online softmax. MODE 1: only workgroups whose rows are all
+// bounded (P = 2^S without a running max). MODE 2: only the others, exact. Modes 1 and 2 are
+// launched back to back and together cover every workgroup.
+template <int DT, int NW, int CG, int WPE, int MODE>
 __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
@@ -346,6 +391,48 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       u32x4 wv = {0u, 0u, 0u, 0u};
       if (qpos[c] < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
       qf[c][kd] = M::from_bits(wv);
+    }
+  }
+
+  // Bounded rows: when |q| |k|max scale log2e < kFastBound for every row of the wave, the scores
+  // (log2 units) lie in (-kFastBound, kFastBound), so P = 2^S needs no running max. Q is then
+  // pre-scaled by scale log2e (rounded to the input type) and the softmax is exp2 of the raw
+  // MFMA output; numerator and denominator share the implicit max 0.
+  constexpr bool fast = MODE == 1;
+  if constexpr (MODE != 0) {
+    __shared__ int wg_bounded;
+    const float km2 = p.kmax2[b * p.Hkv + kvh];
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      float qn2 = 0.0f;
+#pragma unroll
+      for (int kd = 0; kd < 4; ++kd)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = (float)qf[c][kd][j];
+          qn2 = fmaf(x, x, qn2);
+        }
+      qn2 = pair_sum(qn2);
+      const float qn = sqrtf(qn2);
+      ok = ok && (p.scale_log2 * qn * sqrtf(km2) < kFastBound) && (p.scale_log2 * qn < 1.0e4f);
+    }
+    if (tid == 0) wg_bounded = 1;
+    __syncthreads();
+    if (!__all(ok) && lane == 0) wg_bounded = 0;
+    __syncthreads();
+    const bool bounded = wg_bounded != 0;
+    if (bounded != fast) return;  // the other launch takes this workgroup
+    if constexpr (fast) {
+#pragma unroll
+      for (int c = 0; c < CG; ++c)
+#pragma unroll
+        for (int kd = 0; kd < 4; ++kd) {
+          float x[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[j] = (float)qf[c][kd][j] * p.scale_log2;
+          qf[c][kd] = M::pack(x);
+        }
     }
   }
 
@@ -426,7 +513,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   float m_run[CG], l_part[CG];
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
-    m_run[c] = -INFINITY;
+    m_run[c] = fast ? 0.0f : -INFINITY;
     l_part[c] = 0.0f;
   }
   const float c2 = p.scale_log2;
@@ -474,6 +561,34 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
             if (key > lim) sacc[tt][c][r] = -INFINITY;
           }
       }
+    }
+    if constexpr (fast) {  // ---- bounded rows: P^T = 2^(S^T), O^T += V^T P^T ----
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s < 2) {
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt)
+            va[s + 2][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s + 2] + dt * 4096);
+        }
+        vec pb[CG];
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          float pv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            pv[j] = __builtin_amdgcn_exp2f(sacc[s >> 1][c][8 * (s & 1) + j]);
+          pb[c] = M::pack(pv);
+          l_part[c] = M::rowsum(pb[c], l_part[c]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int c = 0; c < CG; ++c)
+            oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
+      }
+      __builtin_amdgcn_s_setprio(0);
+      return;
     }
     // ---- online softmax (lazy rescale) ----
     float m_use[CG], m_cand[CG];
@@ -589,10 +704,16 @@ int launch_mfma(AttnParams& p, hipStream_t stream) {
   p.total = p.nbq * p.B * p.Hkv * p.G * p.qsub;
   const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
   SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-  if (b64)
-    sparse_attn_dma_kernel<DT, 2, 1, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
-  else
-    sparse_attn_dma_kernel<DT, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+  if (p.kmax2 == nullptr) {
+    if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
+    else sparse_attn_dma_kernel<DT, 2, 2, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
+  } else if (b64) {
+    sparse_attn_dma_kernel<DT, 2, 1, 2, 1><<<(unsigned)grid, 128, 0, stream>>>(p);
+    sparse_attn_dma_kernel<DT, 2, 1, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+  } else {
+    sparse_attn_dma_kernel<DT, 2, 2, 2, 1><<<(unsigned)grid, 128, 0, stream>>>(p);
+    sparse_attn_dma_kernel<DT, 2, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+  }
   return launch_status("sparse_attn_dma_kernel");
 }
 
@@ -603,7 +724,8 @@ extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t H
                                                  int64_t d, int64_t block) {
   if (dtype == SSA_F32 || block <= 0) return 0;
   const int64_t n_pad = (n + block - 1) / block * block;
-  return (size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u;
+  const size_t vt = ((size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u + 255) / 256 * 256;
+  return vt + ((size_t)B * (size_t)Hkv * 4u + 255) / 256 * 256;  // V^T, then the key-norm bounds
 }
 
 extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
@@ -677,6 +799,7 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.lse = lse;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
+  p.kmax2 = nullptr;
   if (dtype == SSA_F32) {
     p.vt = nullptr;
     p.qsub = block / 64;
@@ -693,6 +816,21 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   if (!(flags & SSA_ATTN_VT_READY))
     SSA_TRY(ssa_transpose_v(v, dtype, B, Hkv, n, d, block, p.vsb, p.vsh, p.vsn, workspace,
                             workspace_bytes, stream));
+  {  // largest key norm per (b, kv head) into the slot after V^T
+    const size_t vt_bytes =
+        ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
+    float* kmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
+    zero_floats_kernel<<<1, 64, 0, st>>>(kmax2, B * Hkv);
+    SSA_TRY(launch_status("zero_floats_kernel"));
+    int64_t chunks = (n + 256 * 16 - 1) / (256 * 16);
+    if (chunks > 1024) chunks = 1024;
+    SSA_REQUIRE(B * Hkv < 65536, SSA_ERR_UNSUPPORTED, "sparse_attn: too many key heads");
+    key_norm_max_kernel<<<dim3((unsigned)chunks, (unsigned)(B * Hkv)), 256, 0, st>>>(
+        static_cast<const unsigned short*>(k), Hkv, n, p.ksb, p.ksh, p.ksn, dtype == SSA_BF16,
+        kmax2);
+    SSA_TRY(launch_status("key_norm_max_kernel"));
+    p.kmax2 = kmax2;
+  }
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, st);
   return launch_mfma<SSA_F16>(p, st);
 }

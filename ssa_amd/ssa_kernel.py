@@ -162,7 +162,10 @@ def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
     dt = _lib.dtype_code(v.dtype)
     nbytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
     n_pad = -(-n // block) * block
-    vt = torch.empty(B, Hkv, d, n_pad, device=v.device, dtype=v.dtype)
+    # the whole attention workspace (V^T first, then the kernel's per-head key-norm slots),
+    # returned as its V^T view
+    ws = torch.empty(nbytes, device=v.device, dtype=torch.uint8)
+    vt = ws[:B * Hkv * d * n_pad * v.element_size()].view(v.dtype).view(B, Hkv, d, n_pad)
     _lib.call("ssa_transpose_v", v.data_ptr(), dt, B, Hkv, n, d, block, *_bhn_strides(v),
               vt.data_ptr(), nbytes, _lib.stream_of(v))
     return vt
@@ -203,7 +206,8 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
     ws_bytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
     flags = 0
     if vt is not None and dt != _lib.F32:
-        if vt.numel() * vt.element_size() < ws_bytes or not vt.is_contiguous():
+        room = vt.untyped_storage().nbytes() - vt.storage_offset() * vt.element_size()
+        if room < ws_bytes or not vt.is_contiguous():
             raise ValueError("vt is not a V^T workspace for this v (use transpose_v(v, block))")
         ws, flags = vt, _lib.ATTN_VT_READY
     else:
