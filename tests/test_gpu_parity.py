@@ -263,6 +263,29 @@ def test_sparse_attention_matches_oracle(cuda, cfg_name, n, qblocks):
     assert torch.isfinite(out).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("block", [64, 128])
+def test_unbounded_rows_take_the_exact_path(cuda, dtype, block):
+    """Query blocks whose |q| max|k| bound exceeds the fp32-safe range (every other block scaled
+    by 40: scaled logits up to ~500) run the exact running-max softmax, the others the bounded
+    path: every row matches the float64 oracle, and the scaled rows stay finite."""
+    rng = np.random.default_rng(12)
+    n, G = 1024, 2
+    q = rng.standard_normal((1, 2 * G, n, 64)).astype(np.float32)
+    for i in range(0, n // block, 2):
+        q[:, :, i * block:(i + 1) * block] *= 40.0
+    q = WL.round_to(q, dtype)
+    k = WL.round_to(rng.standard_normal((1, 2, n, 64)).astype(np.float32), dtype)
+    v = WL.round_to(rng.standard_normal((1, 2, n, 64)).astype(np.float32), dtype)
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=4, local=1, beta=2.0,
+                                             compact=True)
+    out = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block)
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), block)
+    assert torch.isfinite(out).all()
+    assert np.abs(np_of(out) - ref).max() < TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("block", [64, 128, 256])
 def test_full_budget_matches_dense_sdpa(cuda, dtype, block):
