@@ -116,19 +116,27 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   const float* kv_mu = mu + (bk * nbs) * d;
   const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
   const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
+  // element offset of each tile row in `rows` (-1: past the chunk), computed once
+  __shared__ int64_t row_off[kTile];
+  if (tid < kTile) {
+    const int64_t r = r0 + tid;
+    int64_t off = -1;
+    if (r < R) {
+      const int64_t h = kvh * g.G + r / g.ni;
+      const int64_t i = g.i0 + r % g.ni;
+      off = ((b * g.Hq + h) * g.nbq + i) * d;
+    }
+    row_off[tid] = off;
+  }
 
   for (int k0 = 0; k0 < d; k0 += DK) {
     __syncthreads();
     for (int idx = tid; idx < kTile * DK; idx += 256) {
       const int rr = idx / DK, kk = idx % DK;
-      const int64_t r = r0 + rr;
       const bool kin = k0 + kk < d;
       float q = 0.0f;
-      if (r < R && kin) {
-        const int64_t h = kvh * g.G + r / g.ni;
-        const int64_t i = g.i0 + r % g.ni;
-        q = rows[((b * g.Hq + h) * g.nbq + i) * d + k0 + kk];
-      }
+      const int64_t roff = row_off[rr];
+      if (roff >= 0 && kin) q = rows[roff + k0 + kk];
       const float q2 = q * q;  // rounded to fp32 like the reference's elementwise products
       Qs[kk][rr] = (double)q;
       Q2s[kk][rr] = (double)q2;
