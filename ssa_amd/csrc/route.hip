@@ -587,20 +587,22 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
   if (lane == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
-// Rows of at most 64 key blocks without pooling or m3: a workgroup takes kFusedRows rows of one
-// query head, stages the key head's mu / var rows in LDS (row stride d + 4 floats) and each wave
-// scores and selects one row, no score workspace. S = 2^s_log2 lanes per candidate
-// (c = lane / S) each sum a contiguous ceil(d / S) slice of the head dims in fp64, combined by
-// shuffles; the fp32 score is assembled as in route_score_kernel. A candidate is kept when fewer
-// than keep candidates rank above it (larger key, or equal key and lower block index); the kept
-// blocks and the local window are compacted in ascending order by ballot.
-constexpr int kFusedRows = 8;       // rows (waves) per workgroup
+// Rows of at most 64 key blocks without pooling or m3: a workgroup of kFusedRows waves takes
+// rows of one query head and stages the key head's mu / var rows in LDS (row stride d + 4
+// floats); each wave scores and selects 2^r_log2 rows at once, 64 >> r_log2 lanes per row, no
+// score workspace. Within a row, S = 2^s_log2 lanes per candidate each sum a contiguous
+// ceil(d / S) slice of the head dims in fp64, combined by shuffles (the host uses S = 1 and the
+// most rows per wave that still give every candidate a lane); the fp32 score is assembled as in
+// route_score_kernel. A candidate is kept when fewer than keep candidates rank above it (larger
+// key, or equal key and lower block index); the kept blocks and the local window are compacted
+// in ascending order by ballot.
+constexpr int kFusedRows = 8;       // waves per workgroup
 constexpr int kFusedLds = 64 * 68;  // floats per staged array: nbk * (d + 4) must fit
 
 __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
     const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
-    RouteGeom g, int d, float coef2, int s_log2, bool vec4, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int64_t W) {
+    RouteGeom g, int d, float coef2, int r_log2, int s_log2, bool vec4,
+    int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx, int64_t W) {
   extern __shared__ __attribute__((aligned(16))) float fused_lds[];  // 2 * nbk * (d + 4) floats
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.y;  // b * Hq + h
@@ -616,83 +618,80 @@ __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
     vs[c * ds + t] = kvar ? kvar[idx] : 0.0f;
   }
   __syncthreads();
+  // the wave holds 2^r_log2 rows, Lr lanes each: lane = (row rr, candidate c, head-dim part)
+  const int lr_log2 = 6 - r_log2, Lr = 1 << lr_log2;
+  const int rr = lane >> lr_log2, ll = lane & (Lr - 1);
   const int S = 1 << s_log2;
-  const int c = lane >> s_log2, part = lane & (S - 1);
+  const int P = Lr >> s_log2;  // candidate capacity of a row (>= nbk)
+  const int c = ll >> s_log2, part = ll & (S - 1);
   const int dl = (d + S - 1) >> s_log2;
   const int k0 = part * dl, k1 = k0 + dl < d ? k0 + dl : d;
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  const int64_t i_first = (int64_t)blockIdx.x * kFusedRows;
-  {
-    const int64_t i = i_first + wave;
-    if (i >= g.nbq) return;  // whole wave
-    const int64_t lrow = bh * g.nbq + i;
-    const int64_t cmax = row_cmax(g, i);
-    const bool cand = c < cmax;
-    double e1 = 0.0, e2 = 0.0;
-    if (cand) {
-      const float* q = rows + lrow * d;
-      const float* mrow = ms + c * ds;
-      const float* vrow = vs + c * ds;
-      if (vec4) {  // d a multiple of 4 * S: 16-byte loads
+  const unsigned long long gmask = Lr == 64 ? ~0ull : ((1ull << Lr) - 1ull);
+  const unsigned long long lt = (1ull << ll) - 1ull;
+  const int64_t i = ((int64_t)blockIdx.x * kFusedRows + wave) * (1 << r_log2) + rr;
+  const bool row_ok = i < g.nbq;
+  const int64_t lrow = bh * g.nbq + (row_ok ? i : 0);
+  const int64_t cmax = row_ok ? row_cmax(g, i) : 0;
+  const bool cand = c < cmax;
+  double e1 = 0.0, e2 = 0.0;
+  if (cand) {
+    const float* q = rows + lrow * d;
+    const float* mrow = ms + c * ds;
+    const float* vrow = vs + c * ds;
+    if (vec4) {  // d a multiple of 4 * S: 16-byte loads
 #pragma unroll 4
-        for (int t = k0; t < k1; t += 4) {
-          const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
-          const f32x4 ma = *reinterpret_cast<const f32x4*>(mrow + t);
-          const f32x4 va = *reinterpret_cast<const f32x4*>(vrow + t);
+      for (int t = k0; t < k1; t += 4) {
+        const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
+        const f32x4 ma = *reinterpret_cast<const f32x4*>(mrow + t);
+        const f32x4 va = *reinterpret_cast<const f32x4*>(vrow + t);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float q2 = qa[j] * qa[j];  // rounded to fp32 like the reference's product
-            e1 = fma((double)qa[j], (double)ma[j], e1);
-            e2 = fma((double)q2, (double)va[j], e2);
-          }
-        }
-      } else {
-        for (int t = k0; t < k1; ++t) {
-          const float qf = q[t];
-          const float q2 = qf * qf;
-          e1 = fma((double)qf, (double)mrow[t], e1);
-          e2 = fma((double)q2, (double)vrow[t], e2);
+        for (int j = 0; j < 4; ++j) {
+          const float q2 = qa[j] * qa[j];  // rounded to fp32 like the reference's product
+          e1 = fma((double)qa[j], (double)ma[j], e1);
+          e2 = fma((double)q2, (double)va[j], e2);
         }
       }
-    }
-    for (int off = 1; off < S; off <<= 1) {
-      e1 += __shfl_xor(e1, off, 64);
-      e2 += __shfl_xor(e2, off, 64);
-    }
-    const bool lead = part == 0;
-    const bool live = lead && cand;
-    const unsigned int key =
-        live ? score_key(__fadd_rn((float)e1, __fmul_rn(coef2, (float)e2))) : 0u;
-    const int64_t keep = row_keep(g, cmax);
-    const int64_t K = keep < cmax ? keep : cmax;
-    bool sel;
-    if (K >= cmax) {
-      sel = live;
-    } else if (K <= 0) {
-      sel = false;
     } else {
-      // rank = candidates with a larger key, or an equal key and a lower block index
-      int rank = 0;
-      for (int j = 0; j < (int)cmax; ++j) {
-        const unsigned int kj = __shfl(key, j << s_log2, 64);
-        rank += (kj > key) || (kj == key && j < c);
+      for (int t = k0; t < k1; ++t) {
+        const float qf = q[t];
+        const float q2 = qf * qf;
+        e1 = fma((double)qf, (double)mrow[t], e1);
+        e2 = fma((double)q2, (double)vrow[t], e2);
       }
-      sel = live && rank < K;
     }
-    const int64_t own = row_own(g, i);
-    int64_t lo = own - g.local;
-    if (lo < 0) lo = 0;
-    const int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
-    const bool take = lead && (sel || (c >= lo && c <= hi));
-    const unsigned long long bt = __ballot(take);
-    int32_t* out = kv_idx + lrow * W;
-    const int p = __popcll(bt & lt);
-    if (take && p < W) out[p] = c;
-    const int tot = __popcll(bt);
-    const int64_t num = tot < W ? tot : W;
-    for (int64_t x = num + lane; x < W; x += 64) out[x] = 0;
-    if (lane == 0) kv_num[lrow] = (int32_t)num;
   }
+  for (int off = 1; off < S; off <<= 1) {
+    e1 += __shfl_xor(e1, off, 64);
+    e2 += __shfl_xor(e2, off, 64);
+  }
+  const bool lead = part == 0;
+  const bool live = lead && cand;
+  const unsigned int key = live ? score_key(__fadd_rn((float)e1, __fmul_rn(coef2, (float)e2))) : 0u;
+  const int64_t keep = row_keep(g, cmax);
+  const int64_t K = keep < cmax ? keep : cmax;
+  // rank = candidates of the row with a larger key, or an equal key and a lower block index
+  // (uniform loop over the row capacity; non-candidates hold key 0 and are not counted)
+  int rank = 0;
+  const int base = rr << lr_log2;
+  for (int j = 0; j < P; ++j) {
+    const unsigned int kj = __shfl(key, base + (j << s_log2), 64);
+    rank += (j < cmax) && ((kj > key) || (kj == key && j < c));
+  }
+  const bool sel = K >= cmax ? live : (K > 0 && live && rank < K);
+  const int64_t own = row_own(g, i);
+  int64_t lo = own - g.local;
+  if (lo < 0) lo = 0;
+  const int64_t hi = own < g.nbk - 1 ? own : g.nbk - 1;
+  const bool take = row_ok && lead && (sel || (c >= lo && c <= hi));
+  const unsigned long long bt = (__ballot(take) >> base) & gmask;
+  if (!row_ok) return;
+  int32_t* out = kv_idx + lrow * W;
+  const int p = __popcll(bt & lt);
+  if (take && p < W) out[p] = c;
+  const int tot = __popcll(bt);
+  const int64_t num = tot < W ? tot : W;
+  for (int64_t x = num + ll; x < W; x += Lr) out[x] = 0;
+  if (ll == 0) kv_num[lrow] = (int32_t)num;
 }
 
 __global__ __launch_bounds__(kSelThreads) void expand_selection_kernel(
@@ -806,19 +805,19 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
       B * Hq < 65536) {  // score + select fused, a wave per row
     g.i0 = 0;
     g.ni = nbq;
+    // rows per wave 2^r_log2 with one lane per candidate (capacity P = 64 >> r_log2 >= nbk)
     int p_log2 = 0;
     while ((1ll << p_log2) < nbk) ++p_log2;
-    int s_log2 = 6 - p_log2, d_log2 = 0;
-    while ((1ll << d_log2) < d) ++d_log2;
-    if (s_log2 > d_log2) s_log2 = d_log2;
+    const int r_log2 = 6 - p_log2, s_log2 = 0;
     const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    const bool vec4 = d % (4ll << s_log2) == 0 && a16(rows);
-    const int64_t chunks = (nbq + kFusedRows - 1) / kFusedRows;
+    const bool vec4 = d % 4 == 0 && a16(rows);
+    const int64_t rows_per_wg = (int64_t)kFusedRows << r_log2;
+    const int64_t chunks = (nbq + rows_per_wg - 1) / rows_per_wg;
     SSA_REQUIRE(chunks < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
     const size_t lds = (size_t)2 * nbk * (d + 4) * sizeof(float);
     route_rows_small_kernel<<<dim3((unsigned)chunks, (unsigned)(B * Hq)), 64 * kFusedRows, lds,
-                              stream>>>(rows, mu, var, g, (int)d, coef2, s_log2, vec4, kv_num,
-                                        kv_idx, W);
+                              stream>>>(rows, mu, var, g, (int)d, coef2, r_log2, s_log2, vec4,
+                                        kv_num, kv_idx, W);
     return launch_status("route_rows_small_kernel");
   }
   unsigned int* keys = static_cast<unsigned int*>(workspace);
