@@ -75,37 +75,39 @@ __host__ __device__ inline int64_t row_keep(const RouteGeom& g, int64_t cmax) {
   return k < 1 ? 1 : k;
 }
 
-template <bool EDGE>
+template <bool EDGE, int RT>
 __global__ __launch_bounds__(256) void route_score_kernel(
     const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
     unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
   // operands staged as fp64 (converted once per element, not once per use)
+  // RT rows x kTile candidates per workgroup; a thread owns RA = RT/16 rows x 4 candidates
   constexpr int DK = 16;
-  __shared__ double Qs[DK][kTile + 1];
-  __shared__ double Q2s[DK][kTile + 1];
+  constexpr int RA = RT / 16;
+  __shared__ double Qs[DK][RT + 1];
+  __shared__ double Q2s[DK][RT + 1];
   __shared__ double Ms[DK][kTile + 1];
   __shared__ double Vs[DK][kTile + 1];
-  __shared__ double Q3s[EDGE ? DK : 1][kTile + 1];
+  __shared__ double Q3s[EDGE ? DK : 1][RT + 1];
   __shared__ double M3s[EDGE ? DK : 1][kTile + 1];
 
   const int64_t bk = blockIdx.y;  // b * Hkv + kvh
   const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
   const int64_t rt = blockIdx.x / cand_tiles, ct = blockIdx.x % cand_tiles;
   const int64_t R = g.G * g.ni;  // rows of this key head in the chunk
-  const int64_t r0 = rt * kTile;
+  const int64_t r0 = rt * RT;
   const int64_t c0 = ct * kTile;
   if (r0 >= R) return;
-  int64_t r_last = r0 + kTile - 1 < R ? r0 + kTile - 1 : R - 1;
+  int64_t r_last = r0 + RT - 1 < R ? r0 + RT - 1 : R - 1;
   const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
   if (c0 >= row_cmax_s(g, imax)) return;  // uniform: no row of the tile has these candidates
   const int64_t nbs = g.nbk * g.pool;     // scored candidates per key row
 
   const int tid = threadIdx.x;
   const int tr = tid / 16, tc = tid % 16;
-  double e1[4][4], e2[4][4], e3[EDGE ? 4 : 1][EDGE ? 4 : 1];
+  double e1[RA][4], e2[RA][4], e3[EDGE ? RA : 1][EDGE ? 4 : 1];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < RA; ++a)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       e1[a][c] = 0.0;
@@ -117,8 +119,8 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
   const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
   // element offset of each tile row in `rows` (-1: past the chunk), computed once
-  __shared__ int64_t row_off[kTile];
-  if (tid < kTile) {
+  __shared__ int64_t row_off[RT];
+  if (tid < RT) {
     const int64_t r = r0 + tid;
     int64_t off = -1;
     if (r < R) {
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(256) void route_score_kernel(
 
   for (int k0 = 0; k0 < d; k0 += DK) {
     __syncthreads();
-    for (int idx = tid; idx < kTile * DK; idx += 256) {
+    for (int idx = tid; idx < RT * DK; idx += 256) {
       const int rr = idx / DK, kk = idx % DK;
       const bool kin = k0 + kk < d;
       float q = 0.0f;
@@ -141,6 +143,10 @@ __global__ __launch_bounds__(256) void route_score_kernel(
       Qs[kk][rr] = (double)q;
       Q2s[kk][rr] = (double)q2;
       if constexpr (EDGE) Q3s[kk][rr] = (double)(q2 * q);
+    }
+    for (int idx = tid; idx < kTile * DK; idx += 256) {
+      const int rr = idx / DK, kk = idx % DK;
+      const bool kin = k0 + kk < d;
       const int64_t c = c0 + rr;
       float m = 0.0f, v = 0.0f, t = 0.0f;
       if (c < nbs && kin) {
@@ -155,30 +161,32 @@ __global__ __launch_bounds__(256) void route_score_kernel(
     __syncthreads();
     const int kend = d - k0 < DK ? d - k0 : DK;
     for (int kk = 0; kk < kend; ++kk) {
-      double qd[4], q2d[4], md[4], vd[4];
+      double qd[RA], q2d[RA], md[4], vd[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
+      for (int a = 0; a < RA; ++a) {
         qd[a] = Qs[kk][tr + 16 * a];
         q2d[a] = Q2s[kk][tr + 16 * a];
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
         md[a] = Ms[kk][tc + 16 * a];
         vd[a] = Vs[kk][tc + 16 * a];
       }
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int a = 0; a < RA; ++a)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           e1[a][c] = fma(qd[a], md[c], e1[a][c]);
           e2[a][c] = fma(q2d[a], vd[c], e2[a][c]);
         }
       if constexpr (EDGE) {
-        double q3d[4], td[4];
+        double q3d[RA], td[4];
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          q3d[a] = Q3s[kk][tr + 16 * a];
-          td[a] = M3s[kk][tc + 16 * a];
-        }
+        for (int a = 0; a < RA; ++a) q3d[a] = Q3s[kk][tr + 16 * a];
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < 4; ++a) td[a] = M3s[kk][tc + 16 * a];
+#pragma unroll
+        for (int a = 0; a < RA; ++a)
 #pragma unroll
           for (int c = 0; c < 4; ++c) e3[a][c] = fma(q3d[a], td[c], e3[a][c]);
       }
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(256) void route_score_kernel(
   }
 
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
+  for (int a = 0; a < RA; ++a) {
     const int64_t r = r0 + tr + 16 * a;
     if (r >= R) continue;
     const int64_t h = kvh * g.G + r / g.ni;
@@ -826,6 +834,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     g.ni = nbq - i0 < chunk ? nbq - i0 : chunk;
     const int64_t R = g.G * g.ni;
     const int64_t row_tiles = (R + kTile - 1) / kTile;
+    const int64_t row_tiles2 = (R + 2 * kTile - 1) / (2 * kTile);  // 128-row tiles
     const int64_t imax = i0 + g.ni - 1;
     const int64_t cmax_all = row_cmax_s(g, imax);  // scored candidates (sub-block units)
     const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
@@ -847,13 +856,15 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     } else if (cand_tiles > 0) {
       SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
                   "route: score grid too large");
-      dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
-      if (m3 != nullptr)
-        route_score_kernel<true><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,
-                                                           coef3, keys, row_tiles, cand_tiles);
-      else
-        route_score_kernel<false><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,
-                                                            coef3, keys, row_tiles, cand_tiles);
+      if (m3 != nullptr) {
+        dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
+        route_score_kernel<true, kTile><<<grid, 256, 0, stream>>>(
+            rows, mu, var, m3, g, (int)d, coef2, coef3, keys, row_tiles, cand_tiles);
+      } else {
+        dim3 grid((unsigned)(row_tiles2 * cand_tiles), (unsigned)(B * Hkv));
+        route_score_kernel<false, 2 * kTile><<<grid, 256, 0, stream>>>(
+            rows, mu, var, m3, g, (int)d, coef2, coef3, keys, row_tiles2, cand_tiles);
+      }
       SSA_TRY(launch_status("route_score_kernel"));
     }
     const int64_t nrows = B * Hq * g.ni;
