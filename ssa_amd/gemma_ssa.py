@@ -66,6 +66,52 @@ def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
     return x[:, :, None, :, :].expand(b, h, n, s, d).reshape(b, h * n, s, d)
 
 
+NEG = -1e30  # additive mask value of a dropped key (the reference's NEG)
+
+
+def _block_stats(k: torch.Tensor, block: int):
+    """Per-block mean / population variance / third central moment of the keys over the rows that
+    exist (ssa/gemma_ssa.py:65-82): k (b, h, n, d) -> mu, var, m3 (b, h, nb, d) fp32 and nb."""
+    n = k.shape[2]
+    mu, var, m3 = block_summary(k, block, "pop", n_real=n, with_m3=True)
+    return mu, var.clamp(min=0.0), m3, mu.shape[2]
+
+
+def _selection_mask(q, k, cfg: SSAConfig, qpos=None, kpos=None):
+    """Additive (0 / NEG) mask (b, hq, q_len, kv_len) of the per-query router
+    (ssa/gemma_ssa.py:85-137): the top-budget blocks among those complete at each query's
+    position, its own block and cfg.local_w predecessors, token-causal. Routing runs on the HIP
+    router (SSA_ROUTE_QUERY); the dense mask is assembled on the device from its lists.
+    `qpos` must be consecutive positions (the reference's default is the last q_len of a
+    left-aligned sequence); `kpos` defaults to 0..kv_len-1."""
+    _lib.require_device(q, k)
+    b, hq, q_len, d = q.shape
+    kv_len = k.shape[2]
+    if qpos is None:
+        pos0 = kv_len - q_len
+    else:
+        qp = torch.as_tensor(qpos).detach().to("cpu", torch.int64).view(-1)
+        pos0 = int(qp[0])
+        if qp.numel() != q_len or not torch.equal(qp, torch.arange(pos0, pos0 + q_len)):
+            raise NotImplementedError("ssa_amd needs consecutive query positions")
+    kpos_t = (torch.arange(kv_len, device=q.device) if kpos is None
+              else torch.as_tensor(kpos, device=q.device).long())
+    mu, var, m3 = block_summary(k, cfg.block, "pop", n_real=kv_len, with_m3=cfg.edgeworth)
+    nb = mu.shape[2]
+    kv_num, kv_idx = route(q.float(), mu, var, m3 if cfg.edgeworth else None, "query",
+                           cfg.top_c, cfg.budget_frac, cfg.local_w, 0.5 * cfg.beta,
+                           cfg.beta ** 2 / 6.0 if cfg.edgeworth else 0.0, query_pos=pos0,
+                           block=cfg.block)
+    W = kv_idx.shape[-1]
+    valid = torch.arange(W, device=q.device) < kv_num[..., None].long()
+    sel = torch.zeros(b, hq, q_len, nb + 1, dtype=torch.bool, device=q.device)
+    sel.scatter_(-1, torch.where(valid, kv_idx.long(), nb), True)
+    key_sel = sel[..., :nb][..., kpos_t // cfg.block]
+    qpos_t = torch.arange(pos0, pos0 + q_len, device=q.device)
+    allow = key_sel & (qpos_t[:, None] >= kpos_t[None, :])[None, None]
+    return torch.where(allow, 0.0, torch.tensor(NEG, device=q.device))
+
+
 def load_projection(path, device="cuda"):
     """A trained routing projection saved as {"W_q": (d, d'), "W_k": (d, d'), "meta": {...}} by the
     reference's RoutingProjection.save (ssa/routing_space.py:43-51), loaded with weights_only=True

@@ -646,6 +646,38 @@ def test_gemma_d512_gqa_full_budget_and_budget_monotone(cuda):
     assert counts[0] > counts[1] > counts[2] > counts[3], counts
 
 
+def test_gemma_selection_mask_matches_attention_and_budget(cuda):
+    """G._selection_mask (ssa/gemma_ssa.py:85-137) on the HIP router: masked dense softmax with it
+    equals the per-query attention path, its kept blocks equal the oracle's route, and the
+    attended key count shrinks strictly with the budget (test_gemma_ssa.py:156-168)."""
+    torch.manual_seed(5)
+    n, d = 256, 64
+    q = torch.randn(1, 2, n, d, device=cuda, dtype=torch.float32)
+    k = torch.randn(1, 2, n, d, device=cuda, dtype=torch.float32)
+    v = torch.randn(1, 2, n, d, device=cuda, dtype=torch.float32)
+    G.CFG = G.SSAConfig(block=32, budget_frac=0.25, local_w=1)
+    m = G._selection_mask(q, k, G.CFG)
+    s = (q @ k.transpose(-1, -2)) * 0.125 + m
+    ref = (torch.softmax(s, -1) @ v).transpose(1, 2)
+    out, _ = G.ssa_attention_forward(_mod(groups=1), q, k, v, scaling=0.125)
+    assert (out - ref).abs().max().item() < 1e-5
+    onum, oidx = O.route_query(np_of(q), np_of(k), 32, 0, top_c=None, budget_frac=0.25, local=1,
+                               beta=2.0)
+    first = np_of(m)[..., ::32] == 0.0  # first key of each block kept <=> block selected
+    for r in (40, 100, 255):
+        want = set(oidx[0, 0, r, :onum[0, 0, r]].tolist())
+        got = {c for c in range(n // 32) if first[0, 0, r, c] and 32 * c <= r}
+        assert got == want, (r, got, want)
+    counts = []
+    for frac in (1.0, 0.5, 0.25, 0.1):
+        G.CFG = G.SSAConfig(block=32, budget_frac=frac, local_w=0)
+        counts.append(int((G._selection_mask(q[:, :1], k[:, :1], G.CFG) == 0.0).sum().item()))
+    assert counts[0] > counts[1] > counts[2] > counts[3], counts
+    mu, var, m3, nb = G._block_stats(k, 48)
+    omu, ovar, om3 = O.block_stats(np_of(k), 48, "pop")
+    assert nb == 6 and ulp_diff(np_of(mu), omu).max() <= 1 and ulp_diff(np_of(var), ovar).max() <= 1
+
+
 def test_gemma_sliding_layer_falls_back(cuda):
     """test_gemma_ssa.py:146-153: a sliding layer defers to the installed fallback untouched."""
     G.CFG = G.SSAConfig(block=32, budget_frac=0.1, route_full_only=True)
