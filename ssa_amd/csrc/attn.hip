@@ -28,6 +28,8 @@
 // mask_mod = (kv <= q) & (kv < n) -- ssa/ssa_kernel.py:33-34,125-126; ssa/gemma_ssa.py:159-162,179.
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace ssa {
@@ -39,6 +41,11 @@ constexpr float kRescaleSlack = 8.0f;
 // Rows whose scores provably stay within +-kFastBound (log2 units) take the softmax without a
 // running max: 2^s neither overflows nor underflows fp32 / bf16 there.
 constexpr float kFastBound = 100.0f;
+// The key-norm bound is folded into kKeySlots partial maxima per key head, each on its own
+// 128-byte line (slot s of key head bk at s * round_up(B*Hkv, 32) + bk), so that the atomics of
+// thousands of workgroups do not queue on one address.
+constexpr int kKeySlots = 16;
+__host__ __device__ inline int64_t key_slot_stride(int64_t BH) { return (BH + 31) / 32 * 32; }
 
 struct AttnParams {
   const char* q;
@@ -53,7 +60,8 @@ struct AttnParams {
   int64_t W;
   float scale_log2;
   float* lse;
-  const float* kmax2;  // per (b, kv head): largest squared key norm (NULL: no bound)
+  const float* kmax2;  // kKeySlots partial maxima of the squared key norms (NULL: no bound)
+  int* unbounded;      // per (b, kv head): set by mode 1 when one of its workgroups is not bounded
   int64_t qsub;   // query sub-tiles per query block
   int64_t total;  // logical workgroups
   int64_t group;  // logical workgroups placed together on one XCD
@@ -134,54 +142,79 @@ struct Mfma<SSA_F16> {
   }
 };
 
-// Largest squared key norm per (b, kv head): grid (chunks, B*Hkv), 256 threads, one key row per
-// thread per pass; non-negative floats order like their bit patterns, so the workgroup maxima are
-// merged with an unsigned atomicMax into out (zeroed by the caller's fill launch).
-__global__ __launch_bounds__(256) void key_norm_max_kernel(const unsigned short* __restrict__ k,
-                                                           int64_t Hkv, int64_t n, int64_t ksb,
-                                                           int64_t ksh, int64_t ksn, bool bf16,
-                                                           float* __restrict__ out) {
+// Key-norm bound of the attention call: the largest squared norm of key rows k0..k0+63 of one
+// key head (rows >= n count 0), folded into slot blockIdx.x % kKeySlots of key head (b, kvh) with
+// an unsigned atomicMax (non-negative floats order like their bit patterns; the slots are zeroed
+// by a fill launch first). The slot is read first and the atomic skipped when it already holds as
+// much: the value only grows, so a stale read can only cause a redundant atomic. 256 threads;
+// lanes 8r..8r+7 of a pass read row r's 8 16-byte chunks.
+struct KeyNorm {
+  const unsigned short* k;  // NULL: no key norms
+  int64_t ksb, ksh, ksn;
+  bool bf16;
+  float* kmax2;  // kKeySlots * key_slot_stride(B*Hkv) floats, zeroed before the launch
+  int64_t BH;    // B * Hkv
+};
+
+__device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t kvh,
+                                         int64_t Hkv, int64_t k0, int64_t n) {
   __shared__ float red[4];
-  const int64_t bk = blockIdx.y;
-  const int64_t b = bk / Hkv, kvh = bk % Hkv;
-  const unsigned short* base = k + b * ksb + kvh * ksh;
+  const int tid = threadIdx.x;
+  const unsigned short* base = kn.k + b * kn.ksb + kvh * kn.ksh;
   float mx = 0.0f;
-  for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < n; r += (int64_t)gridDim.x * 256) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = tid + 256 * j;
+    const int row = q >> 3, ch = q & 7;
     float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(base + r * ksn + c * 8);
+    if (k0 + row < n) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(base + (k0 + row) * kn.ksn + ch * 8);
       float x[8];
-      unpack8(w, x, bf16);
+      unpack8(w, x, kn.bf16);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(x[j], x[j], acc);
+      for (int e = 0; e < 8; ++e) acc = fmaf(x[e], x[e], acc);
     }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 4, 64);
     mx = fmaxf(mx, acc);
   }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  for (int off = 8; off <= 32; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    atomicMax(reinterpret_cast<unsigned int*>(out) + bk, __float_as_uint(m));
+    unsigned int* slot = reinterpret_cast<unsigned int*>(kn.kmax2) +
+                         (blockIdx.x % kKeySlots) * key_slot_stride(kn.BH) + b * Hkv + kvh;
+    const unsigned int mb = __float_as_uint(m);
+    if (mb > __atomic_load_n(slot, __ATOMIC_RELAXED)) atomicMax(slot, mb);
   }
 }
 
-__global__ __launch_bounds__(64) void zero_floats_kernel(float* x, int64_t n) {
-  for (int64_t i = threadIdx.x; i < n; i += 64) x[i] = 0.0f;
+// Key norms alone (V^T supplied by the caller). grid (n_pad/64, B*Hkv).
+__global__ __launch_bounds__(256) void key_norm_max_kernel(KeyNorm kn, int64_t Hkv, int64_t n) {
+  const int64_t bk = blockIdx.y;
+  key_tile_norm_max(kn, bk / Hkv, bk % Hkv, Hkv, (int64_t)blockIdx.x * 64, n);
 }
 
-// V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n. grid (n_pad/64, B*Hkv).
+__global__ __launch_bounds__(256) void zero_floats_kernel(float* x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    x[i] = 0.0f;
+}
+
+// V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n; with kn.k set, also the
+// key-norm bound of the same 64 rows. grid (n_pad/64, B*Hkv).
 __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict__ v,
                                                           char* __restrict__ vt, int64_t Hkv,
                                                           int64_t n, int64_t n_pad, int64_t vsb,
-                                                          int64_t vsh, int64_t vsn) {
+                                                          int64_t vsh, int64_t vsn, KeyNorm kn) {
   __shared__ unsigned short t[64][64 + 2];
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / Hkv, kvh = bk % Hkv;
   const int64_t k0 = (int64_t)blockIdx.x * 64;
   const int tid = threadIdx.x;
+  if (kn.k != nullptr) key_tile_norm_max(kn, b, kvh, Hkv, k0, n);
   const unsigned short* src = reinterpret_cast<const unsigned short*>(v) + b * vsb + kvh * vsh;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -359,6 +392,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   L /= p.B;
   const int64_t i = p.nbq - 1 - L;
   const int64_t h = kvh * p.G + hg;
+  if constexpr (MODE == 2)
+    if (p.unbounded[b * p.Hkv + kvh] == 0) return;  // mode 1 ran every workgroup of this head
 
   const int64_t q0 = i * p.block + qs * ROWS;
   if (q0 >= p.n) return;
@@ -401,7 +436,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   constexpr bool fast = MODE == 1;
   if constexpr (MODE != 0) {
     __shared__ int wg_bounded;
-    const float km2 = p.kmax2[b * p.Hkv + kvh];
+    float km2 = 0.0f;
+    for (int s = 0; s < kKeySlots; ++s)
+      km2 = fmaxf(km2, p.kmax2[s * key_slot_stride(p.B * p.Hkv) + b * p.Hkv + kvh]);
     bool ok = true;
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
@@ -422,7 +459,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     if (!__all(ok) && lane == 0) wg_bounded = 0;
     __syncthreads();
     const bool bounded = wg_bounded != 0;
-    if (bounded != fast) return;  // the other launch takes this workgroup
+    if (bounded != fast) {  // the other launch takes this workgroup
+      if (fast && tid == 0) p.unbounded[b * p.Hkv + kvh] = 1;
+      return;
+    }
     if constexpr (fast) {
 #pragma unroll
       for (int c = 0; c < CG; ++c)
@@ -725,7 +765,9 @@ extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t H
   if (dtype == SSA_F32 || block <= 0) return 0;
   const int64_t n_pad = (n + block - 1) / block * block;
   const size_t vt = ((size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u + 255) / 256 * 256;
-  return vt + ((size_t)B * (size_t)Hkv * 4u + 255) / 256 * 256;  // V^T, then the key-norm bounds
+  // V^T, then the key-norm slots (float) and one unbounded-workgroup flag (int) per key head
+  const size_t tail = (size_t)(ssa::kKeySlots * ssa::key_slot_stride(B * Hkv) + B * Hkv) * 4u;
+  return vt + (tail + 255) / 256 * 256;
 }
 
 extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
@@ -747,9 +789,10 @@ extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv,
   SSA_REQUIRE(B * Hkv < 65536 && n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "transpose_v: grid too large");
   dim3 tg((unsigned)(n_pad / 64), (unsigned)(B * Hkv));
+  KeyNorm none{};
   transpose_v_kernel<<<tg, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const char*>(v), static_cast<char*>(vt), Hkv, n, n_pad, stride_b, stride_h,
-      stride_n);
+      stride_n, none);
   return launch_status("transpose_v_kernel");
 }
 
@@ -813,24 +856,28 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(workspace != nullptr && workspace_bytes >= need && aligned16(workspace),
               SSA_ERR_WORKSPACE, "sparse_attn: workspace needs %zu bytes (16-byte aligned)", need);
   p.vt = static_cast<const char*>(workspace);
-  if (!(flags & SSA_ATTN_VT_READY))
-    SSA_TRY(ssa_transpose_v(v, dtype, B, Hkv, n, d, block, p.vsb, p.vsh, p.vsn, workspace,
-                            workspace_bytes, stream));
-  {  // largest key norm per (b, kv head) into the slot after V^T
-    const size_t vt_bytes =
-        ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
-    float* kmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
-    zero_floats_kernel<<<1, 64, 0, st>>>(kmax2, B * Hkv);
-    SSA_TRY(launch_status("zero_floats_kernel"));
-    int64_t chunks = (n + 256 * 16 - 1) / (256 * 16);
-    if (chunks > 1024) chunks = 1024;
-    SSA_REQUIRE(B * Hkv < 65536, SSA_ERR_UNSUPPORTED, "sparse_attn: too many key heads");
-    key_norm_max_kernel<<<dim3((unsigned)chunks, (unsigned)(B * Hkv)), 256, 0, st>>>(
-        static_cast<const unsigned short*>(k), Hkv, n, p.ksb, p.ksh, p.ksn, dtype == SSA_BF16,
-        kmax2);
+  SSA_REQUIRE(B * Hkv < 65536 && p.n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
+              "sparse_attn: grid too large");
+  // after V^T: the key-norm slots, then mode 1's unbounded flags
+  const size_t vt_bytes = ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
+  float* kmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
+  const int64_t slots = kKeySlots * key_slot_stride(B * Hkv);
+  const int64_t zn = slots + B * Hkv;  // int 0 and float 0 share their bits
+  zero_floats_kernel<<<(unsigned)std::min<int64_t>((zn + 255) / 256, 1024), 256, 0, st>>>(kmax2, zn);
+  SSA_TRY(launch_status("zero_floats_kernel"));
+  KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, kmax2,
+             B * Hkv};
+  const dim3 tg((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv));
+  if (flags & SSA_ATTN_VT_READY) {
+    key_norm_max_kernel<<<tg, 256, 0, st>>>(kn, Hkv, n);
     SSA_TRY(launch_status("key_norm_max_kernel"));
-    p.kmax2 = kmax2;
+  } else {  // V^T and the key norms in one pass
+    transpose_v_kernel<<<tg, 256, 0, st>>>(static_cast<const char*>(v), static_cast<char*>(workspace),
+                                           Hkv, n, p.n_pad, p.vsb, p.vsh, p.vsn, kn);
+    SSA_TRY(launch_status("transpose_v_kernel"));
   }
+  p.kmax2 = kmax2;
+  p.unbounded = reinterpret_cast<int*>(kmax2 + slots);
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, st);
   return launch_mfma<SSA_F16>(p, st);
 }
