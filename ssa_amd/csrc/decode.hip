@@ -3,8 +3,8 @@
 // decode_partial_kernel: one wave per (query row, selected block) -- the gather is split over
 //   every selected block of every head, so a step's ~30 MB of K/V are read by ~1000 waves in
 //   parallel. Each wave computes its block's scores (one key per lane per pass, 16-byte row
-//   loads), the block's running max / sum in fp32 and its unnormalised output row (lane = head
-//   dim, coalesced V row reads), and writes (m, l, o) to the workspace.
+//   loads; for blocks of <= 128 keys the V rows are loaded before the scores), the block's max /
+//   sum in fp32 and its unnormalised output row, and writes (m, l, o) to the workspace.
 // decode_combine_kernel: merges a row's partials with the usual max-rescaling (4 waves per row).
 // decode_step: append the new token and convert the query rows (one launch) -> summarise a
 //   just-completed block -> route the query over the complete blocks (route_impl,
@@ -94,45 +94,37 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// grid (rows * W): block x handles selected block j = x % W of query row x / W, one wave each.
+// Partial softmax attention of query row (b, h, r) over key block c: (m, l, o[d]) into part.
 template <int DT>
-__global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
-  __shared__ float qs[kMaxDecodeD];
-  __shared__ float ps[kMaxDecodeBlock];
+__device__ inline void block_partial(const DecodeParams& p, float* part, float* qs, float* ps,
+                                     int64_t b, int64_t h, int64_t kvh, int64_t r, int64_t pos,
+                                     int64_t c) {
   const int lane = threadIdx.x;
-  const int64_t j = blockIdx.x % p.W;
-  const int64_t rowid = blockIdx.x / p.W;  // (b*Hq + h)*nq + r
-  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
-  const int64_t b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.G;
-  const int64_t pos = p.pos + r;
   const int d = (int)p.d;
-  float* part = p.part + (rowid * p.W + j) * (p.d + 2);
-
-  int cnt = p.kv_num[rowid];
-  if (cnt > p.W) cnt = (int)p.W;
-  const int32_t* list = p.kv_idx + rowid * p.W;
-  bool empty = j >= cnt;
-  int64_t c = 0;
-  if (!empty) {
-    c = list[j];
-    const int64_t nblk = (p.cap + p.block - 1) / p.block;
-    if (c < 0 || c >= nblk || c * p.block > pos) empty = true;
-    for (int64_t jj = 0; jj < j && !empty; ++jj)  // a repeated id is attended once
-      if (list[jj] == c) empty = true;
-  }
-  if (empty) {
-    if (lane == 0) {
-      part[0] = -INFINITY;
-      part[1] = 0.0f;
-    }
-    for (int e = lane; e < d; e += 64) part[2 + e] = 0.0f;
-    return;
-  }
   const int64_t key0 = c * p.block;
   int64_t key1 = key0 + p.block;
   if (key1 > pos + 1) key1 = pos + 1;
   if (key1 > p.cap) key1 = p.cap;
   const int nk = (int)(key1 - key0);
+  // PV lane layout (16-bit): key group kg = lane / 8, 16-byte chunk ch = lane % 8 of the V row.
+  // Blocks of at most 8 * kPre keys with d <= 64 load their V rows up front, in flight while the
+  // scores are computed.
+  constexpr int kPre = 16;
+  const int kg = lane >> 3, ch = lane & 7;
+  const int64_t voff = b * p.vsb + kvh * p.vsh;
+  const bool pre = DT != SSA_F32 && d <= 64 && nk <= 8 * kPre;
+  u32x4 vpre[kPre];
+  if constexpr (DT != SSA_F32) {
+    if (pre) {
+      const unsigned short* vb = reinterpret_cast<const unsigned short*>(p.v) + voff;
+#pragma unroll
+      for (int t = 0; t < kPre; ++t) {
+        const int kk = kg + 8 * t;
+        vpre[t] = u32x4{0u, 0u, 0u, 0u};
+        if (kk < nk && ch * 8 < d) vpre[t] = *reinterpret_cast<const u32x4*>(vb + (key0 + kk) * p.vsn + ch * 8);
+      }
+    }
+  }
 
   const char* qb = p.q;
   const int64_t qoff = b * p.qsb + h * p.qsh + r * p.qsn;
@@ -176,7 +168,6 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
   }
   const float l = wave_sum(lloc);
   __syncthreads();
-  const int64_t voff = b * p.vsb + kvh * p.vsh;
   if constexpr (DT == SSA_F32) {
     for (int e = lane; e < d; e += 64) {
       float acc = 0.0f;
@@ -184,10 +175,34 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
         acc = fmaf(ps[kk], load_elem<DT>(p.v, voff + (key0 + kk) * p.vsn + e), acc);
       part[2 + e] = acc;
     }
+  } else if (pre) {  // the prefetched V rows; the 8 key groups summed with shuffles
+    float acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kPre; ++t) {
+      const int kk = kg + 8 * t;
+      if (kk < nk) {
+        float vv[8];
+        unpack8(vpre[t], vv, DT == SSA_BF16);
+        const float pk = ps[kk];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(pk, vv[e], acc[e]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      float x = acc[t];
+      x += __shfl_xor(x, 8, 64);
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[t] = x;
+    }
+    if (kg == 0 && ch * 8 < d)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) part[2 + ch * 8 + t] = acc[t];
   } else {
-    // lane = (key group kg = lane / 8, 16-byte chunk ch = lane % 8): 8 keys per pass, 16-byte V
-    // row loads; the 8 key groups are summed with cross-lane shuffles.
-    const int kg = lane >> 3, ch = lane & 7;
+    // 8 keys per pass, 16-byte V row loads; the 8 key groups are summed with shuffles.
     const unsigned short* vb = reinterpret_cast<const unsigned short*>(p.v) + voff;
     for (int e0 = 0; e0 < d; e0 += 64) {
       const bool on = e0 + ch * 8 < d;
@@ -224,54 +239,57 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
   }
 }
 
-// grid (B*Hq*nq), 4 waves per row: weights of 256 partials at a time in LDS, each wave sums a
-// quarter of the partials for every head dim (coalesced rows), then the waves are added.
+// grid (B*Hq*nq), 4 waves per row: wave w merges partials [w * q, (w + 1) * q) of the row (q =
+// ceil(cnt / 4)) with the usual max-rescaling, loading 8 partial rows at a time (one memory
+// latency per batch, not per partial); the waves' sums are then added through LDS.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-  __shared__ float wts[256];
   __shared__ float red[4][kMaxDecodeD];
   __shared__ float sm[4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t rowid = blockIdx.x;
-  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
-  const int64_t b = bh / p.Hq, h = bh % p.Hq;
   int cnt = p.kv_num[rowid];
   if (cnt > p.W) cnt = (int)p.W;
+  if (cnt < 0) cnt = 0;
   const int64_t stride = p.d + 2;
-  const float* part = p.part + rowid * p.W * stride;
+  const float* rp = p.part + rowid * p.W * stride;
   float M = -INFINITY;
-  for (int j = tid; j < cnt; j += 256) M = fmaxf(M, part[j * stride]);
+  for (int j = tid; j < cnt; j += 256) M = fmaxf(M, rp[j * stride]);
   M = wave_max(M);
   if (lane == 0) sm[wv] = M;
   __syncthreads();
   M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
   __syncthreads();
+  const int qn = (cnt + 3) / 4;
+  const int ja = wv * qn, jz = ja + qn < cnt ? ja + qn : cnt;
   float L = 0.0f;
   float acc[kMaxDecodeD / 64];
 #pragma unroll
   for (int k = 0; k < kMaxDecodeD / 64; ++k) acc[k] = 0.0f;
-  for (int j0 = 0; j0 < cnt; j0 += 256) {
-    const int j = j0 + tid;
-    float wj = 0.0f;
-    if (j < cnt) {
-      const float mj = part[j * stride];
-      if (mj != -INFINITY) {
-        wj = exp2f(mj - M);
-        L += part[j * stride + 1] * wj;
+  for (int j0 = ja; j0 < jz; j0 += 64) {
+    const int jl = j0 + lane;
+    float mj = -INFINITY, lj = 0.0f;
+    if (jl < jz) {
+      mj = rp[jl * stride];
+      lj = rp[jl * stride + 1];
+    }
+    const float wl = mj == -INFINITY ? 0.0f : exp2f(mj - M);  // empty partials: weight 0
+    L += lj * wl;
+    const int jn = jz - j0 < 64 ? jz - j0 : 64;
+    for (int jb = 0; jb < jn; jb += 8) {
+#pragma unroll
+      for (int k = 0; k < kMaxDecodeD / 64; ++k) {
+        if (64 * k >= p.d) break;  // uniform
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool in = jb + u < jn && lane + 64 * k < p.d;
+          x[u] = in ? rp[(j0 + jb + u) * stride + 2 + lane + 64 * k] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[k] = fmaf(x[u], __shfl(wl, (jb + u) & 63, 64), acc[k]);
       }
     }
-    wts[tid] = wj;
-    __syncthreads();
-    const int jn = cnt - j0 < 256 ? cnt - j0 : 256;
-    for (int jj = wv; jj < jn; jj += 4) {
-      const float w = wts[jj];
-      if (w == 0.0f) continue;  // wave-uniform
-      const float* pr = part + (j0 + jj) * stride + 2;
-#pragma unroll
-      for (int k = 0; k < kMaxDecodeD / 64; ++k)
-        if (lane + 64 * k < p.d) acc[k] = fmaf(pr[lane + 64 * k], w, acc[k]);
-    }
-    __syncthreads();
   }
   L = wave_sum(L);
   if (lane == 0) sm[wv] = L;
@@ -281,10 +299,49 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
   __syncthreads();
   L = sm[0] + sm[1] + sm[2] + sm[3];
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq;
   for (int e = tid; e < p.d; e += 256)
     store_elem<DT>(p.o, b * p.osb + h * p.osh + r * p.osn + e,
                    (red[0][e] + red[1][e] + red[2][e] + red[3][e]) * inv);
   if (p.lse != nullptr && tid == 0) p.lse[rowid] = L > 0.0f ? (M + log2f(L)) * kLn2 : -INFINITY;
+}
+
+// grid (rows * W): block x handles selected block j = x % W of query row x / W, one wave each.
+template <int DT>
+__global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
+  __shared__ float qs[kMaxDecodeD];
+  __shared__ float ps[kMaxDecodeBlock];
+  const int lane = threadIdx.x;
+  const int64_t j = blockIdx.x % p.W;
+  const int64_t rowid = blockIdx.x / p.W;  // (b*Hq + h)*nq + r
+  const int64_t bh = rowid / p.nq, r = rowid % p.nq;
+  const int64_t b = bh / p.Hq, h = bh % p.Hq, kvh = h / p.G;
+  const int64_t pos = p.pos + r;
+  const int d = (int)p.d;
+  float* part = p.part + (rowid * p.W + j) * (p.d + 2);
+
+  int cnt = p.kv_num[rowid];
+  if (cnt > p.W) cnt = (int)p.W;
+  const int32_t* list = p.kv_idx + rowid * p.W;
+  bool empty = j >= cnt;
+  int64_t c = 0;
+  if (!empty) {
+    c = list[j];
+    const int64_t nblk = (p.cap + p.block - 1) / p.block;
+    if (c < 0 || c >= nblk || c * p.block > pos) empty = true;
+    for (int64_t jj = 0; jj < j && !empty; ++jj)  // a repeated id is attended once
+      if (list[jj] == c) empty = true;
+  }
+  if (empty) {
+    if (lane == 0) {
+      part[0] = -INFINITY;
+      part[1] = 0.0f;
+    }
+    for (int e = lane; e < d; e += 64) part[2 + e] = 0.0f;
+  } else {
+    block_partial<DT>(p, part, qs, ps, b, h, kvh, r, pos, c);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -317,6 +317,50 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return base + incl - v;
 }
 
+// The K largest of a wave's entries (lane l, slot j: entry l + 64 j; cand marks the ncand real
+// ones) under the order (key desc, entry asc). The K-th largest key T is found bit by bit from
+// the top (count of keys >= T | bit by ballots); keys > T are taken, and keys == T in increasing
+// entry order until K are taken. Non-candidates must hold key 0: they never reach a threshold
+// >= 1, and at T = 0 the candidate flag keeps them out.
+template <int J>
+__device__ inline void wave_select_top(const unsigned int (&key)[J], const bool (&cand)[J],
+                                       int64_t K, int64_t ncand, bool (&sel)[J]) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  if (K >= ncand) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) sel[j] = cand[j];
+    return;
+  }
+  if (K <= 0) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) sel[j] = false;
+    return;
+  }
+  unsigned int T = 0u;  // largest T with #{keys >= T} >= K: the K-th largest key
+  for (int bit = 31; bit >= 0; --bit) {
+    const unsigned int t = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= t));
+    if (cnt >= K) T = t;
+  }
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) above += __popcll(__ballot(cand[j] && key[j] > T));
+  int need = (int)K - above;  // keys equal to T to take, lowest entry first
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool eq = cand[j] && key[j] == T;
+    const unsigned long long be = __ballot(eq);
+    // (int) casts: __popcll is unsigned, and need turns negative once the ties are taken
+    sel[j] = (cand[j] && key[j] > T) || (eq && (int)__popcll(be & lt) < need);
+    need -= (int)__popcll(be);
+  }
+}
+
+constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
+
 // Top-K of one row of score keys (K = min(keep, cmax)), ties to the lowest block index, then the
 // row's local window, compacted ascending into kv_idx (pad 0) with kv_num.
 // Rows of at most kCacheKeys candidates are staged in LDS; longer rows (more than kFilterMin) are
@@ -511,11 +555,9 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   if (tid == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
-// Rows of at most 64 * J key blocks: one wave per row, lane l holds candidates l + 64 j. The
-// keep-th largest key T is found bit by bit from the top (count of keys >= T | bit by ballots),
-// keys > T are taken, and keys == T in increasing block order until keep is reached; the
-// selection plus the local window is compacted in ascending order from the per-j ballots.
-constexpr int kSmallNbk = 1024;  // J = 16
+// Rows of at most 64 * J key blocks: one wave per row, lane l holds candidates l + 64 j
+// (wave_select_top); the selection plus the local window is compacted in ascending order from
+// the per-j ballots.
 
 template <int kSmallJ>
 __global__ __launch_bounds__(256) void route_select_small_kernel(
@@ -548,33 +590,7 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     key[j] = m;
   }
   bool sel[kSmallJ];
-  if (K >= cmax) {
-#pragma unroll
-    for (int j = 0; j < kSmallJ; ++j) sel[j] = cand[j];
-  } else if (K <= 0) {
-#pragma unroll
-    for (int j = 0; j < kSmallJ; ++j) sel[j] = false;
-  } else {
-    unsigned int T = 0u;  // largest T with #{keys >= T} >= K: the K-th largest key
-    for (int bit = 31; bit >= 0; --bit) {  // non-candidates hold key 0 < t
-      const unsigned int t = T | (1u << bit);
-      int cnt = 0;
-#pragma unroll
-      for (int j = 0; j < kSmallJ; ++j) cnt += __popcll(__ballot(key[j] >= t));
-      if (cnt >= K) T = t;
-    }
-    int above = 0;
-#pragma unroll
-    for (int j = 0; j < kSmallJ; ++j) above += __popcll(__ballot(cand[j] && key[j] > T));
-    int need = (int)K - above;  // keys equal to T to take, lowest block first
-#pragma unroll
-    for (int j = 0; j < kSmallJ; ++j) {
-      const bool eq = cand[j] && key[j] == T;
-      const unsigned long long be = __ballot(eq);
-      sel[j] = (cand[j] && key[j] > T) || (eq && __popcll(be & lt) < need);
-      need -= __popcll(be);
-    }
-  }
+  wave_select_top<kSmallJ>(key, cand, K, cmax, sel);
   const int64_t own = row_own(g, i);
   int64_t lo = own - g.local;
   if (lo < 0) lo = 0;

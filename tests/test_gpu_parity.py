@@ -149,13 +149,16 @@ def test_route_ties_take_lowest_index(cuda):
         assert s == frozenset(list(range(min(3, i))) + [i]), (i, s)
 
 
+@pytest.mark.parametrize("nbk", [200, 300, 3000, 12000, 20000])
 @pytest.mark.parametrize("case", ["random", "top_ties", "all_equal"])
-def test_route_long_rows_match_oracle(cuda, case):
-    """Rows with more candidates than fit in LDS (12000 key blocks): the filtered select (random
-    scores), its tie handling (100 identical best blocks, 64 kept: lowest indices) and the
-    fallback when the filter keeps too much (all scores equal)."""
+def test_route_long_rows_match_oracle(cuda, case, nbk):
+    """Query rows over 200 to 20000 key blocks, keep 64, through every select: one wave per row
+    (200, 300), the two-stage chunked select (3000, 12000) and the filtered radix select (20000,
+    more than fit in LDS). Random scores, ties at the top (100 identical best blocks: the lowest
+    indices win) and all scores equal (ties spread over every lane and slot; for 20000 the
+    filter keeps too much and the select falls back to the whole row)."""
     rng = np.random.default_rng(21)
-    nbk, d, block = 12000, 64, 64
+    d, block = 64, 64
     mu = rng.standard_normal((1, 1, nbk, d)).astype(np.float32)
     var = rng.uniform(0.5, 1.5, (1, 1, nbk, d)).astype(np.float32)
     rows = rng.standard_normal((1, 2, 3, d)).astype(np.float32)
