@@ -363,10 +363,12 @@ constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
 
 // Top-K of one row of score keys (K = min(keep, cmax)), ties to the lowest block index, then the
 // row's local window, compacted ascending into kv_idx (pad 0) with kv_num.
-// Rows of at most kCacheKeys candidates are staged in LDS; longer rows (more than kFilterMin) are
-// first filtered: the keys are split into P >= K disjoint groups, so the smallest group maximum
-// T0 is <= the K-th largest key; the keys >= T0 (with their indices) go to LDS and the radix
-// select runs on them (rows whose filter keeps more than kCand keys use the full row).
+// Rows of at most kCacheKeys candidates are staged in LDS. Rows of more than kFilterMin are first
+// filtered: the keys are split into P >= K disjoint groups, so the smallest group maximum T0 is
+// <= the K-th largest key; the indices of the keys >= T0 (and, for rows not staged, the keys)
+// go to LDS and the radix select runs on them (rows whose filter keeps more than kCand keys use
+// the full row). Filtering also pays for staged rows: the digit histograms of a few hundred
+// survivors see far fewer same-bin atomics than those of thousands of similar keys.
 template <int NT>
 __global__ __launch_bounds__(NT) void route_select_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
@@ -412,13 +414,13 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   // keys the radix select runs over: src[0, nsel), block index of entry c: filt ? cidx[c] : c
   bool filt = false;
   int64_t nsel = cmax;
-  if (!cached && K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
+  if (K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
     int pk = 1;
     while (pk < K) pk <<= 1;
     const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
     unsigned int mx = 0u;
     for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = krow(c);
+      const unsigned int key = cached ? cache[c] : krow(c);
       mx = key > mx ? key : mx;
     }
     for (int off = 1; off < gs; off <<= 1) {
@@ -434,11 +436,11 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     __syncthreads();
     const unsigned int t0 = sh_min;
     for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = krow(c);
+      const unsigned int key = cached ? cache[c] : krow(c);
       if (key >= t0) {
         const unsigned int slot = atomicAdd(&sh_ncand, 1u);
         if (slot < (unsigned int)kCand) {
-          cache[slot] = key;
+          if (!cached) cache[slot] = key;  // a cached row keeps its keys in place
           cidx[slot] = (unsigned int)c;
         }
       }
@@ -449,8 +451,10 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
       nsel = sh_ncand;
     }
   }
-  const bool src_lds = cached || filt;
-  auto src = [&](int64_t c) -> unsigned int { return src_lds ? cache[c] : krow(c); };
+  auto src = [&](int64_t c) -> unsigned int {
+    if (filt) return cached ? cache[cidx[c]] : cache[c];
+    return cached ? cache[c] : krow(c);
+  };
   auto mark = [&](int64_t c) {
     const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
     atomicOr(&bits[blk >> 5], 1u << (blk & 31));
