@@ -247,17 +247,30 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
   const float* kv_mu = mu + (bk * nbs) * d;
   const float* kv_var = var ? var + (bk * nbs) * d : nullptr;
   const float* kv_m3 = EDGE ? m3 + (bk * nbs) * d : nullptr;
+  // per row of the tile (once, not per element: 64-bit divisions are long instruction sequences)
+  // the element offset of its query vector (-1: past the chunk), its key buffer and candidates
+  __shared__ int64_t row_off[kMaxR], row_key[kMaxR], row_cm[kMaxR];
+  if (tid < kMaxR) {
+    int64_t off = -1, kofs = 0, cm = 0;
+    if (tid < R) {
+      const int64_t h = kvh * g.G + tid / g.ni;
+      const int64_t il = tid % g.ni;
+      off = ((b * g.Hq + h) * g.nbq + g.i0 + il) * d;
+      kofs = ((b * g.Hq + h) * g.ni + il) * nbs;
+      cm = row_cmax_s(g, g.i0 + il);
+    }
+    row_off[tid] = off;
+    row_key[tid] = kofs;
+    row_cm[tid] = cm;
+  }
   double e1 = 0.0, e2 = 0.0, e3 = 0.0;
   for (int k0 = 0; k0 < d; k0 += kDK) {
     __syncthreads();
     for (int idx = tid; idx < kMaxR * kDK; idx += 256) {
       const int rr = idx / kDK, kk = idx % kDK;
       float q = 0.0f;
-      if (rr < R && k0 + kk < d) {
-        const int64_t h = kvh * g.G + rr / g.ni;
-        const int64_t i = g.i0 + rr % g.ni;
-        q = rows[((b * g.Hq + h) * g.nbq + i) * d + k0 + kk];
-      }
+      const int64_t roff = row_off[rr];
+      if (roff >= 0 && k0 + kk < d) q = rows[roff + k0 + kk];
       const float q2 = q * q;
       Qs[rr][kk] = q;
       Q2s[rr][kk] = q2;
@@ -285,12 +298,10 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
     }
   }
   if (r >= R) return;
-  const int64_t h = kvh * g.G + r / g.ni;
-  const int64_t il = r % g.ni;
-  if (c >= row_cmax_s(g, g.i0 + il)) return;
+  if (c >= row_cm[r]) return;
   float s = __fadd_rn((float)e1, __fmul_rn(coef2, (float)e2));
   if constexpr (EDGE) s = __fadd_rn(s, __fmul_rn(coef3, (float)e3));
-  keys[((b * g.Hq + h) * g.ni + il) * nbs + c] = score_key(s);
+  keys[row_key[r] + c] = score_key(s);
 }
 
 // Block-wide exclusive scan of one int per thread (NT threads); returns the exclusive prefix
