@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 3
+#define SSA_ABI_VERSION 4
 
 typedef void* ssa_stream_t; /* hipStream_t */
 
@@ -223,7 +223,9 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
  * strides: 3 per tensor for q, k, v, out; dout uses the strides of out.
  * forward: out in q's dtype and lse (B, Hq, n) fp32 (natural log of the row's softmax sum of the
  *   scaled scores).
- * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) fp32 contiguous, written by the call.
+ * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) contiguous, written by the call, in
+ *   grad_dtype: SSA_F32, or the input dtype (tiled path only; the per-row path returns
+ *   SSA_ERR_UNSUPPORTED for it), which spares the caller a conversion pass.
  * Both take ssa_masked_attn_workspace_size(B, Hq, n, W, d, block) bytes of workspace.
  * d = 64 with at most 8192 key blocks runs the tiled MFMA kernels (per (64-row query tile, key
  *   block) row masks; q, k, v, out, dout, dq, dk, dv 16-byte aligned; deterministic). Other head
@@ -238,8 +240,9 @@ int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, void* out, 
                         const int32_t* kv_idx, int64_t W, float scale, void* workspace,
                         size_t workspace_bytes, ssa_stream_t stream);
 int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
-                        const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                        int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t d,
+                        const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                        int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
+                        int64_t d,
                         int64_t block, const int64_t* strides, const int32_t* kv_num,
                         const int32_t* kv_idx, int64_t W, float scale, void* workspace,
                         size_t workspace_bytes, ssa_stream_t stream);

@@ -7,13 +7,14 @@ ssa_last_error(). There is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
@@ -49,7 +50,7 @@ _SIGNATURES = {
     "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ssa_masked_attn_fwd": (_c_int, [_c_p] * 5 + [_c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
-    "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int] + [_c_i64] * 6 +
+    "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int, _c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
     "ssa_sparse_attn_workspace_size": (_c_sz, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ssa_transpose_v": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
@@ -115,8 +116,11 @@ def call(name: str, *args) -> int:
     return rc
 
 
+@functools.lru_cache(maxsize=4096)
 def query(name: str, *args):
-    """Calls a size/width query (no status)."""
+    """Calls a size/width query (no status). The queries are pure functions of their arguments,
+    so results are cached (a ctypes call per training step costs more than the kernels of a
+    small one)."""
     return getattr(lib(), name)(*args)
 
 

@@ -36,8 +36,9 @@ int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, flo
                      int64_t W, float scale, void* workspace, size_t workspace_bytes,
                      hipStream_t st);
 int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* out,
-                     const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                     int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
+                     const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                     int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
+                     int64_t block,
                      const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
                      int64_t W, float scale, void* workspace, size_t workspace_bytes,
                      hipStream_t st);
@@ -722,8 +723,9 @@ extern "C" int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, 
 }
 
 extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
-                                   const void* dout, const float* lse, float* dq, float* dk,
-                                   float* dv, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                   const void* dout, const float* lse, void* dq, void* dk,
+                                   void* dv, int dtype, int grad_dtype, int64_t B, int64_t Hq,
+                                   int64_t Hkv,
                                    int64_t n, int64_t d, int64_t block, const int64_t* strides,
                                    const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
                                    float scale, void* workspace, size_t workspace_bytes,
@@ -734,9 +736,12 @@ extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, 
                         kv_idx, W, scale));
   SSA_REQUIRE(dout && lse && dq && dk && dv, SSA_ERR_INVALID, "masked_attn_bwd: NULL gradient");
   if (masked_tiled_ok(d, block, n))
-    return masked_tiled_bwd(q, k, v, out, dout, lse, dq, dk, dv, dtype, B, Hq, Hkv, n, block,
+    return masked_tiled_bwd(q, k, v, out, dout, lse, dq, dk, dv, dtype, grad_dtype, B, Hq, Hkv,
+                            n, block,
                             strides, kv_num, kv_idx, W, scale, workspace, workspace_bytes,
                             static_cast<hipStream_t>(stream));
+  SSA_REQUIRE(grad_dtype == SSA_F32, SSA_ERR_UNSUPPORTED,
+              "masked_attn_bwd: the per-row path (d != 64) accumulates fp32 gradients only");
   const size_t need = (size_t)B * Hq * n * 4u;
   SSA_REQUIRE(workspace && workspace_bytes >= need, SSA_ERR_WORKSPACE,
               "masked_attn_bwd: workspace needs %zu bytes", need);
@@ -745,17 +750,17 @@ extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, 
   bp.dout = static_cast<const char*>(dout);
   bp.lse = lse;
   bp.delta = static_cast<const float*>(workspace);
-  bp.dq = dq;
-  bp.dk = dk;
-  bp.dv = dv;
+  bp.dq = static_cast<float*>(dq);
+  bp.dk = static_cast<float*>(dk);
+  bp.dv = static_cast<float*>(dv);
   bp.Hkv = Hkv;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t rows = B * Hq * n;
   SSA_REQUIRE(rows * W < (1ll << 31), SSA_ERR_UNSUPPORTED, "masked_attn_bwd: grid too large");
   const int64_t nq_el = rows * d, nk_el = B * Hkv * n * d;
-  zero_f32_kernel<<<(unsigned)((nq_el + 255) / 256 < 4096 ? (nq_el + 255) / 256 : 4096), 256, 0, st>>>(dq, nq_el);
-  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(dk, nk_el);
-  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(dv, nk_el);
+  zero_f32_kernel<<<(unsigned)((nq_el + 255) / 256 < 4096 ? (nq_el + 255) / 256 : 4096), 256, 0, st>>>(bp.dq, nq_el);
+  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(bp.dk, nk_el);
+  zero_f32_kernel<<<(unsigned)((nk_el + 255) / 256 < 4096 ? (nk_el + 255) / 256 : 4096), 256, 0, st>>>(bp.dv, nk_el);
   SSA_TRY(launch_status("zero_f32_kernel"));
   const unsigned g1 = (unsigned)rows, g2 = (unsigned)(rows * W);
   switch (dtype) {

@@ -50,9 +50,10 @@ struct SwapArgs {
   const char* dout;  // strides of o
   float* lse;        // (B*Hq*n)
   float* delta;      // (B*Hq*n)
-  float* dq;         // (B, Hq, n, 64) fp32 contiguous
-  float* dk;         // (B, Hkv, n, 64)
-  float* dv;
+  void* dq;          // (B, Hq, n, 64) contiguous, fp32 or (grad16) the input type
+  void* dk;          // (B, Hkv, n, 64)
+  void* dv;
+  bool grad16;       // gradients stored in the 16-bit input type (16-bit kernels only)
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   int64_t B, Hq, Hkv, G, n, block, nqt, nkt, nb;
   const int32_t* kv_num;
@@ -73,6 +74,24 @@ __device__ inline f32x16 mfma(float a, float b, f32x16 c) {
 
 __device__ inline float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
 __device__ inline float pair_sum(float x) { return x + __shfl_xor(x, 32, 64); }
+
+// 4 consecutive gradient values of a row: fp32, or rounded to the 16-bit input type DT
+template <int DT>
+__device__ inline void store_grad4(void* base, int64_t off, const f32x4& v, bool grad16) {
+  if (DT != SSA_F32 && grad16) {
+    unsigned int w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = DT == SSA_BF16 ? (unsigned int)__builtin_bit_cast(unsigned short, (__bf16)v[j])
+                            : (unsigned int)__builtin_bit_cast(unsigned short, (_Float16)v[j]);
+    uint2 u;
+    u.x = w[0] | (w[1] << 16);
+    u.y = w[2] | (w[3] << 16);
+    *reinterpret_cast<uint2*>(static_cast<unsigned short*>(base) + off) = u;
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + off) = v;
+  }
+}
 
 // Stages rows [r0, r0 + 64) (rows >= nrows read as zeros) of a (rows, 64) matrix with row stride
 // rs elements into LDS as fp32 with 256 threads: row-major into dst and/or transposed into dstT.
@@ -419,7 +438,6 @@ __global__ __launch_bounds__(256) void swap_dq_kernel(SwapArgs a) {
   }
   __syncthreads();
   if (kh == 1 || !qvalid) return;
-  float* dqr = a.dq + rid * 64;
 #pragma unroll
   for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
@@ -428,7 +446,7 @@ __global__ __launch_bounds__(256) void swap_dq_kernel(SwapArgs a) {
       f32x4 val;
 #pragma unroll
       for (int j = 0; j < 4; ++j) val[j] = (dqa[dh][4 * g + j] + buf[(x + j) * 128 + slot]) * a.scale;
-      *reinterpret_cast<f32x4*>(dqr + d0) = val;
+      store_grad4<SSA_F32>(a.dq, rid * 64 + d0, val, false);
     }
 }
 
@@ -535,8 +553,7 @@ __global__ __launch_bounds__(256) void swap_dkdv_kernel(SwapArgs a) {
   }
   __syncthreads();
   if (qp == 1 || !kvalid) return;
-  float* dkr = a.dk + (bkv * a.n + key) * 64;
-  float* dvr = a.dv + (bkv * a.n + key) * 64;
+  const int64_t krow = (bkv * a.n + key) * 64;
 #pragma unroll
   for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
@@ -548,8 +565,8 @@ __global__ __launch_bounds__(256) void swap_dkdv_kernel(SwapArgs a) {
         kv4[j] = (dka[dh][4 * g + j] + bk[(x + j) * 128 + slot]) * a.scale;
         vv4[j] = dva[dh][4 * g + j] + bv[(x + j) * 128 + slot];
       }
-      *reinterpret_cast<f32x4*>(dkr + d0) = kv4;
-      *reinterpret_cast<f32x4*>(dvr + d0) = vv4;
+      store_grad4<SSA_F32>(a.dk, krow + d0, kv4, false);
+      store_grad4<SSA_F32>(a.dv, krow + d0, vv4, false);
     }
 }
 
@@ -833,7 +850,6 @@ __global__ __launch_bounds__(256) void swap_dq16_kernel(SwapArgs a) {
   }
   __syncthreads();
   if (kh == 1 || !qvalid) return;
-  float* dqr = a.dq + rid * 64;
 #pragma unroll
   for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
@@ -842,7 +858,7 @@ __global__ __launch_bounds__(256) void swap_dq16_kernel(SwapArgs a) {
       f32x4 val;
 #pragma unroll
       for (int j = 0; j < 4; ++j) val[j] = (dqa[dh][4 * g + j] + buf[(x + j) * 128 + slot]) * a.scale;
-      *reinterpret_cast<f32x4*>(dqr + dd) = val;
+      store_grad4<DT>(a.dq, rid * 64 + dd, val, a.grad16);
     }
 }
 
@@ -942,8 +958,7 @@ __global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
   }
   __syncthreads();
   if (qp == 1 || !kvalid) return;
-  float* dkr = a.dk + (bkv * a.n + key) * 64;
-  float* dvr = a.dv + (bkv * a.n + key) * 64;
+  const int64_t krow = (bkv * a.n + key) * 64;
 #pragma unroll
   for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
@@ -955,8 +970,8 @@ __global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
         kv4[j] = (dka[dh][4 * g + j] + bk[(x + j) * 128 + slot]) * a.scale;
         vv4[j] = dva[dh][4 * g + j] + bv[(x + j) * 128 + slot];
       }
-      *reinterpret_cast<f32x4*>(dkr + dd) = kv4;
-      *reinterpret_cast<f32x4*>(dvr + dd) = vv4;
+      store_grad4<DT>(a.dk, krow + dd, kv4, a.grad16);
+      store_grad4<DT>(a.dv, krow + dd, vv4, a.grad16);
     }
 }
 
@@ -988,6 +1003,7 @@ int fill_args(SwapArgs& a, const void* q, const void* k, const void* v, const vo
   a.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                      (size_t)B * Hq * a.nqt * a.nb * 8u);
   a.lse = nullptr; a.dout = nullptr; a.dq = a.dk = a.dv = nullptr;
+  a.grad16 = false;
   SSA_REQUIRE(B * Hq * a.nqt < (1ll << 31) && B * Hkv * a.nkt < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "masked_attn: grid too large");
   return SSA_OK;
@@ -1023,8 +1039,8 @@ int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, flo
 }
 
 int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* out,
-                     const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                     int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
+                     const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                     int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
                      const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
                      int64_t W, float scale, void* workspace, size_t workspace_bytes,
                      hipStream_t st) {
@@ -1035,7 +1051,10 @@ int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* ou
               SSA_ERR_UNSUPPORTED, "masked_attn_bwd: dout, dq, dk, dv must be 16-byte aligned");
   a.dout = static_cast<const char*>(dout);
   a.lse = const_cast<float*>(lse);
+  SSA_REQUIRE(grad_dtype == SSA_F32 || grad_dtype == dtype, SSA_ERR_INVALID,
+              "masked_attn_bwd: gradients must be fp32 or the input type");
   a.dq = dq; a.dk = dk; a.dv = dv;
+  a.grad16 = grad_dtype != SSA_F32;
   const unsigned gq = (unsigned)(B * Hq * a.nqt), gk = (unsigned)(B * Hkv * a.nkt);
   row_block_masks_kernel<<<gq, 256, 0, st>>>(a);
   SSA_TRY(launch_status("row_block_masks_kernel"));

@@ -71,16 +71,28 @@ class _MaskedAttention(torch.autograd.Function):
         Hkv = k.shape[1]
         W = kv_idx.shape[-1]
         dout = dout.to(out.dtype).contiguous()  # described by out's (contiguous) strides
-        dq = torch.empty(B, Hq, n, d, device=q.device, dtype=torch.float32)
-        dk = torch.empty(B, Hkv, n, d, device=q.device, dtype=torch.float32)
-        dv = torch.empty_like(dk)
         wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d, ctx.block))
         ws = torch.empty(wsb, device=q.device, dtype=torch.uint8)
-        _lib.call("ssa_masked_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                  dout.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                  _lib.dtype_code(q.dtype), B, Hq, Hkv, n, d, ctx.block, _strides(q, k, v, out),
-                  kv_num.data_ptr(), kv_idx.data_ptr(), W, ctx.scale, ws.data_ptr(), wsb,
-                  _lib.stream_of(q))
+        dt = _lib.dtype_code(q.dtype)
+        strides = _strides(q, k, v, out)
+
+        def run(gdt):
+            dq = torch.empty(B, Hq, n, d, device=q.device, dtype=gdt)
+            dk = torch.empty(B, Hkv, n, d, device=q.device, dtype=gdt)
+            dv = torch.empty_like(dk)
+            _lib.call("ssa_masked_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                      out.data_ptr(), dout.data_ptr(), lse.data_ptr(), dq.data_ptr(),
+                      dk.data_ptr(), dv.data_ptr(), dt, _lib.dtype_code(gdt), B, Hq, Hkv, n, d,
+                      ctx.block, strides, kv_num.data_ptr(), kv_idx.data_ptr(), W, ctx.scale,
+                      ws.data_ptr(), wsb, _lib.stream_of(q))
+            return dq, dk, dv
+
+        try:  # gradients written in the input type by the tiled kernels
+            dq, dk, dv = run(q.dtype)
+        except _lib.SSAError as e:
+            if e.status != _lib.SSA_ERR_UNSUPPORTED or q.dtype == torch.float32:
+                raise
+            dq, dk, dv = run(torch.float32)  # per-row kernels: fp32 accumulation
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None
 
 
