@@ -298,12 +298,35 @@ def main():
         kvn = int(dec.kv_num.sum().item())
         nbk = dec.pos // c4.block
         dbytes = c4.Hkv * nbk * 2 * c4.d * 4 + kvn * c4.block * c4.d * 2 * 2
+        # dense baseline (ssa/ivf_decode.py:65-74 at this shape): one SDPA call over the whole
+        # cache prefix, the 7 query heads of a key head stacked as 7 query rows of it (no mask is
+        # needed at decode, and K/V are read once, not repeated per query head)
+        npre = dec.pos
+        G4 = c4.Hq // c4.Hkv
+        qd1 = qd[:, :, 8].reshape(1, c4.Hkv, G4, c4.d)
+        kpre, vpre = dec.kcache[:, :, :npre], dec.vcache[:, :, :npre]
+        sdpa = torch.nn.functional.scaled_dot_product_attention
+        for _ in range(3):
+            sdpa(qd1, kpre, vpre)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(32):
+            sdpa(qd1, kpre, vpre)
+        torch.cuda.synchronize()
+        dense_dms = (time.perf_counter() - t0) / 32 * 1000.0
         result["decode"] = {
             "workload": "C4: routed decode step, bf16, 14q/2kv, d=64, KV cache 1,048,576 tokens "
                         "(+ appended steps), block 128, top_c 64 + last 2 blocks, beta 2",
             "ms_per_step": dms, "steps": args.decode_steps,
             "bytes_per_step": dbytes, "achieved_gbs": dbytes / (dms / 1e3) / 1e9,
             "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
+            # torch SDPA has no split-KV decode path on ROCm: its grid is (query tiles x
+            # heads), 2 workgroups here, so the HBM floor of a dense step is reported beside it
+            "dense_sdpa_ms_per_step": dense_dms,
+            "speedup_vs_dense_sdpa": dense_dms / dms,
+            "dense_bytes_per_step": 2 * c4.Hkv * npre * c4.d * 2,
+            "dense_hbm_floor_ms": 2 * c4.Hkv * npre * c4.d * 2 / (PEAK_HBM_GBS * 1e6),
+            "speedup_vs_dense_hbm_floor": 2 * c4.Hkv * npre * c4.d * 2 / (PEAK_HBM_GBS * 1e6) / dms,
         }
         del kd, vd, qd, dec
 

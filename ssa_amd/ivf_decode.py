@@ -77,6 +77,17 @@ def dense_decode(qvec, k, v, pos):
     return out.view(d)
 
 
+@torch.no_grad()
+def dense_decode_naive(qvec, k, v, pos):
+    """The reference's earlier dense decode (ssa/ivf_decode.py:77-85): the prefix K/V [0..pos]
+    upcast to fp32 every step, softmax(q.K^T / sqrt(d)) V in fp32, cast to qvec's dtype. Kept as
+    the side-by-side check of dense_decode, as the reference keeps it."""
+    d = qvec.shape[-1]
+    kp, vp = k[:pos + 1].float(), v[:pos + 1].float()
+    w = torch.softmax((qvec.float() @ kp.T) / math.sqrt(d), dim=-1)
+    return (w @ vp).to(qvec.dtype)
+
+
 class RoutedDecoder:
     """A KV cache with resident block summaries and the fused routed decode step.
 

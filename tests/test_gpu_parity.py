@@ -434,6 +434,23 @@ def test_decode_attend_matches_oracle_and_prefill_row(cuda):
     assert np.abs(np_of(row2) - ref2).max() < 2e-2
 
 
+def test_dense_decode_baselines_agree_with_full_selection(cuda):
+    """The dense decode baselines (ssa/ivf_decode.py:65-85; the reference pins dense_decode
+    against dense_decode_naive) equal each other, the oracle's softmax row and decode_attend over
+    every block of the prefix."""
+    rng = np.random.default_rng(17)
+    n, block, pos = 9 * 128, 128, 9 * 128 - 40
+    q, k, v = (WL.round_to(rng.standard_normal(s).astype(np.float32), torch.bfloat16)
+               for s in ((64,), (n, 64), (n, 64)))
+    qt, kt, vt = (dev(x, torch.bfloat16, cuda) for x in (q, k, v))
+    a = D.dense_decode(qt, kt, vt, pos)
+    b = D.dense_decode_naive(qt, kt, vt, pos)
+    c = D.decode_attend(qt, kt, vt, list(range(9)), pos, block)
+    ref = O.decode_attend(q, k, v, list(range(9)), pos, block)
+    for got in (a, b, c):
+        assert got.dtype == torch.bfloat16 and np.abs(np_of(got) - ref).max() < 2e-2
+
+
 def test_routed_decoder_matches_reference_router_and_oracle(cuda):
     """RoutedDecoder on a C4-shaped cache: the selection at each fixture position equals the
     reference _selection_mask (float32) and the oracle; the output matches the oracle row."""
