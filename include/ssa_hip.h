@@ -85,8 +85,10 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
                       ssa_stream_t stream);
 
 /*
- * Cumulant router. rows: (B, Hq, nbq, d) fp32 (query-block means, or query vectors in
- * SSA_ROUTE_QUERY mode); mu, var (and m3): (B, Hkv, nbk, d) fp32; q-head h reads key head
+ * Cumulant router. rows: (B, Hq, nbq, d) contiguous, of type rows_dtype (SSA_F32, or SSA_F16 /
+ * SSA_BF16, which convert to fp32 exactly, so a 16-bit q needs no fp32 copy): query-block means,
+ * or query vectors in SSA_ROUTE_QUERY / SSA_ROUTE_STARTED mode; mu, var (and m3):
+ * (B, Hkv, nbk, d) fp32; q-head h reads key head
  * h / (Hq/Hkv). Score of row i against key block c, in the reference's evaluation order:
  *   r = fl32( fl32(<q,mu_c>) + fl32(coef2 * fl32(<q*q, var_c>)) )
  *       [ + fl32(coef3 * fl32(<q*q*q, m3_c>)) when m3 != NULL ]
@@ -114,8 +116,8 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
 int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c, float budget_frac,
                         int64_t local, int64_t query_pos, int64_t block);
 size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk);
-int ssa_route(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
-              int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
+int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,
+              const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
               int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
               int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx, int64_t W,
               void* workspace, size_t workspace_bytes, ssa_stream_t stream);
@@ -127,8 +129,8 @@ int ssa_route(const float* rows, const float* mu, const float* var, const float*
  * The workspace needs ssa_route_workspace_size(B, Hq, nbq, nbk * pool) bytes for one pass
  * (any multiple of ssa_route_workspace_size(B, Hq, 1, nbk * pool) works). pool = 1 is ssa_route.
  */
-int ssa_route_pooled(const float* rows, const float* mu, const float* var, const float* m3,
-                     int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t pool,
+int ssa_route_pooled(const void* rows, int rows_dtype, const float* mu, const float* var,
+                     const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t pool,
                      int64_t d, int mode, int64_t top_c, float budget_frac, int64_t local,
                      float coef2, float coef3, int64_t query_pos, int64_t block, int32_t* kv_num,
                      int32_t* kv_idx, int64_t W, void* workspace, size_t workspace_bytes,

@@ -39,12 +39,12 @@ _SIGNATURES = {
                                    _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p]),
     "ssa_route_width": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64, _c_f, _c_i64, _c_i64, _c_i64]),
     "ssa_route_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
-    "ssa_route": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-                           _c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64, _c_i64, _c_p, _c_p,
-                           _c_i64, _c_p, _c_sz, _c_p]),
-    "ssa_route_pooled": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-                                  _c_i64, _c_i64, _c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64,
-                                  _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_sz, _c_p]),
+    "ssa_route": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_p] + [_c_i64] * 6 +
+                  [_c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
+                   _c_p, _c_sz, _c_p]),
+    "ssa_route_pooled": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_p] + [_c_i64] * 7 +
+                         [_c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64, _c_i64, _c_p, _c_p,
+                          _c_i64, _c_p, _c_sz, _c_p]),
     "ssa_project_rows": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "ssa_expand_selection": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),

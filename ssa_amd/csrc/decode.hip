@@ -22,7 +22,8 @@ int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t
                          int64_t sb, int64_t sh, int64_t sn, int64_t block, int64_t n_real,
                          int mode, float* mu, float* var, float* m3, int64_t nb_out,
                          int64_t block_offset, hipStream_t stream);
-int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
+int route_impl(const void* rows, int rows_dt, const float* mu, const float* var, const float* m3,
+               int64_t B,
                int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
                int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
                int64_t query_pos, int64_t block, int64_t pool, int32_t* kv_num, int32_t* kv_idx,
@@ -642,7 +643,7 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   }
 
   // 3. route the queries over the complete blocks
-  SSA_TRY(route_impl(qf, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
+  SSA_TRY(route_impl(qf, SSA_F32, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
                      budget_frac, local, coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys,
                      key_bytes, st));
 

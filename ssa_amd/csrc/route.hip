@@ -43,7 +43,16 @@ struct RouteGeom {
   float budget_frac;
   int64_t local;
   int64_t pool;  // scored candidates per key block (sub-blocks max-pooled to the block; 1 = none)
+  int rows_dt;   // element type of the query rows: SSA_F32, SSA_F16 or SSA_BF16 (exact in fp32)
 };
+
+// Element idx of the query rows as fp32 (16-bit types convert exactly).
+__device__ inline float load_row(const void* rows, int64_t idx, int dt) {
+  if (dt == SSA_F32) return static_cast<const float*>(rows)[idx];
+  const unsigned short u = static_cast<const unsigned short*>(rows)[idx];
+  if (dt == SSA_BF16) return __uint_as_float((unsigned int)u << 16);
+  return (float)__builtin_bit_cast(_Float16, u);
+}
 
 // Number of candidates of query row i: budget -> c < i, flat -> c <= i, query -> complete blocks.
 __host__ __device__ inline int64_t row_cmax(const RouteGeom& g, int64_t i) {
@@ -77,7 +86,7 @@ __host__ __device__ inline int64_t row_keep(const RouteGeom& g, int64_t cmax) {
 
 template <bool EDGE, int RT>
 __global__ __launch_bounds__(256) void route_score_kernel(
-    const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
     unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
   // operands staged as fp64 (converted once per element, not once per use)
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(256) void route_score_kernel(
       const bool kin = k0 + kk < d;
       float q = 0.0f;
       const int64_t roff = row_off[rr];
-      if (roff >= 0 && kin) q = rows[roff + k0 + kk];
+      if (roff >= 0 && kin) q = load_row(rows, roff + k0 + kk, g.rows_dt);
       const float q2 = q * q;  // rounded to fp32 like the reference's elementwise products
       Qs[kk][rr] = (double)q;
       Q2s[kk][rr] = (double)q2;
@@ -220,7 +229,7 @@ __global__ __launch_bounds__(256) void route_score_kernel(
 // fp32 assembly as route_score_kernel.
 template <bool EDGE>
 __global__ __launch_bounds__(256) void route_score_rows_kernel(
-    const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
     unsigned int* __restrict__ keys, int rp_log2) {
   constexpr int kMaxR = 16;
@@ -270,7 +279,7 @@ __global__ __launch_bounds__(256) void route_score_rows_kernel(
       const int rr = idx / kDK, kk = idx % kDK;
       float q = 0.0f;
       const int64_t roff = row_off[rr];
-      if (roff >= 0 && k0 + kk < d) q = rows[roff + k0 + kk];
+      if (roff >= 0 && k0 + kk < d) q = load_row(rows, roff + k0 + kk, g.rows_dt);
       const float q2 = q * q;
       Qs[rr][kk] = q;
       Q2s[rr][kk] = q2;
@@ -639,7 +648,7 @@ constexpr int kFusedRows = 8;       // waves per workgroup
 constexpr int kFusedLds = 64 * 68;  // floats per staged array: nbk * (d + 4) must fit
 
 __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
-    const float* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     RouteGeom g, int d, float coef2, int r_log2, int s_log2, bool vec4,
     int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx, int64_t W) {
   extern __shared__ __attribute__((aligned(16))) float fused_lds[];  // 2 * nbk * (d + 4) floats
@@ -674,10 +683,22 @@ __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
   const bool cand = c < cmax;
   double e1 = 0.0, e2 = 0.0;
   if (cand) {
-    const float* q = rows + lrow * d;
+    const float* q = static_cast<const float*>(rows) + lrow * d;
     const float* mrow = ms + c * ds;
     const float* vrow = vs + c * ds;
-    if (vec4) {  // d a multiple of 4 * S: 16-byte loads
+    if (vec4 && g.rows_dt != SSA_F32) {  // 16-bit rows, d a multiple of 8 * S: 16-byte loads
+      const unsigned short* q16 = static_cast<const unsigned short*>(rows) + lrow * d;
+      for (int t = k0; t < k1; t += 8) {
+        float qa[8];
+        unpack8(*reinterpret_cast<const u32x4*>(q16 + t), qa, g.rows_dt == SSA_BF16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float q2 = qa[j] * qa[j];
+          e1 = fma((double)qa[j], (double)mrow[t + j], e1);
+          e2 = fma((double)q2, (double)vrow[t + j], e2);
+        }
+      }
+    } else if (vec4) {  // d a multiple of 4 * S: 16-byte loads
 #pragma unroll 4
       for (int t = k0; t < k1; t += 4) {
         const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
@@ -692,7 +713,7 @@ __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
       }
     } else {
       for (int t = k0; t < k1; ++t) {
-        const float qf = q[t];
+        const float qf = load_row(rows, lrow * d + t, g.rows_dt);
         const float q2 = qf * qf;
         e1 = fma((double)qf, (double)mrow[t], e1);
         e2 = fma((double)q2, (double)vrow[t], e2);
@@ -792,12 +813,15 @@ __global__ __launch_bounds__(256) void project_rows_kernel(const float* __restri
 }  // namespace
 
 // Routes every row; exposed to the decode step, which calls it with a single query row.
-int route_impl(const float* rows, const float* mu, const float* var, const float* m3, int64_t B,
+int route_impl(const void* rows, int rows_dt, const float* mu, const float* var, const float* m3,
+               int64_t B,
                int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
                int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
                int64_t query_pos, int64_t block, int64_t pool, int32_t* kv_num, int32_t* kv_idx,
                int64_t W, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SSA_REQUIRE(rows && mu && kv_num && kv_idx, SSA_ERR_INVALID, "route: NULL pointer argument");
+  SSA_REQUIRE(rows_dt == SSA_F32 || rows_dt == SSA_F16 || rows_dt == SSA_BF16, SSA_ERR_UNSUPPORTED,
+              "route: unknown rows dtype %d", rows_dt);
   SSA_REQUIRE(pool >= 1 && pool <= 64, SSA_ERR_INVALID, "route: pool must be in [1, 64]");
   SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && nbq > 0 && nbk > 0 && d > 0, SSA_ERR_INVALID,
               "route: sizes must be positive");
@@ -840,6 +864,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
   g.budget_frac = budget_frac;
   g.local = local;
   g.pool = pool;
+  g.rows_dt = rows_dt;
   if (nbk <= 64 && nbk * (d + 4) <= kFusedLds && pool == 1 && m3 == nullptr &&
       B * Hq < 65536) {  // score + select fused, a wave per row
     g.i0 = 0;
@@ -849,7 +874,7 @@ int route_impl(const float* rows, const float* mu, const float* var, const float
     while ((1ll << p_log2) < nbk) ++p_log2;
     const int r_log2 = 6 - p_log2, s_log2 = 0;
     const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    const bool vec4 = d % 4 == 0 && a16(rows);
+    const bool vec4 = d % (rows_dt == SSA_F32 ? 4 : 8) == 0 && a16(rows);
     const int64_t rows_per_wg = (int64_t)kFusedRows << r_log2;
     const int64_t chunks = (nbq + rows_per_wg - 1) / rows_per_wg;
     SSA_REQUIRE(chunks < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
@@ -948,27 +973,27 @@ extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, i
   return (size_t)B * (size_t)Hq * (size_t)nbq * (size_t)nbk * 4u;
 }
 
-extern "C" int ssa_route(const float* rows, const float* mu, const float* var, const float* m3,
-                         int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d,
+extern "C" int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,
+                         const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d,
                          int mode, int64_t top_c, float budget_frac, int64_t local, float coef2,
                          float coef3, int64_t query_pos, int64_t block, int32_t* kv_num,
                          int32_t* kv_idx, int64_t W, void* workspace, size_t workspace_bytes,
                          ssa_stream_t stream) {
-  return ssa::route_impl(rows, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c, budget_frac,
-                         local, coef2, coef3, query_pos, block, 1, kv_num, kv_idx, W, workspace,
-                         workspace_bytes, static_cast<hipStream_t>(stream));
+  return ssa::route_impl(rows, rows_dtype, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c,
+                         budget_frac, local, coef2, coef3, query_pos, block, 1, kv_num, kv_idx, W,
+                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int ssa_route_pooled(const float* rows, const float* mu, const float* var,
-                                const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq,
+extern "C" int ssa_route_pooled(const void* rows, int rows_dtype, const float* mu,
+                                const float* var, const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq,
                                 int64_t nbk, int64_t pool, int64_t d, int mode, int64_t top_c,
                                 float budget_frac, int64_t local, float coef2, float coef3,
                                 int64_t query_pos, int64_t block, int32_t* kv_num, int32_t* kv_idx,
                                 int64_t W, void* workspace, size_t workspace_bytes,
                                 ssa_stream_t stream) {
-  return ssa::route_impl(rows, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c, budget_frac,
-                         local, coef2, coef3, query_pos, block, pool, kv_num, kv_idx, W,
-                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return ssa::route_impl(rows, rows_dtype, mu, var, m3, B, Hq, Hkv, nbq, nbk, d, mode, top_c,
+                         budget_frac, local, coef2, coef3, query_pos, block, pool, kv_num, kv_idx,
+                         W, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ssa_project_rows(const float* x, const float* w, int64_t rows, int64_t din,

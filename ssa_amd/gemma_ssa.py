@@ -66,7 +66,13 @@ def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
     return x[:, :, None, :, :].expand(b, h, n, s, d).reshape(b, h * n, s, d)
 
 
-NEG = -1e30  # additive mask value of a dropped key (the reference's NEG)
+NEG = -1e30
+
+
+def _router_rows(x):
+    """Query rows as the router reads them: 16-bit types as they are (their fp32 values are
+    exact), anything else as fp32."""
+    return x if x.dtype in (torch.float16, torch.bfloat16) else x.float()  # additive mask value of a dropped key (the reference's NEG)
 
 
 def _block_stats(k: torch.Tensor, block: int):
@@ -98,7 +104,7 @@ def _selection_mask(q, k, cfg: SSAConfig, qpos=None, kpos=None):
               else torch.as_tensor(kpos, device=q.device).long())
     mu, var, m3 = block_summary(k, cfg.block, "pop", n_real=kv_len, with_m3=cfg.edgeworth)
     nb = mu.shape[2]
-    kv_num, kv_idx = route(q.float(), mu, var, m3 if cfg.edgeworth else None, "query",
+    kv_num, kv_idx = route(_router_rows(q), mu, var, m3 if cfg.edgeworth else None, "query",
                            cfg.top_c, cfg.budget_frac, cfg.local_w, 0.5 * cfg.beta,
                            cfg.beta ** 2 / 6.0 if cfg.edgeworth else 0.0, query_pos=pos0,
                            block=cfg.block)
@@ -201,7 +207,7 @@ def ssa_attention_forward(module, query, key, value, attention_mask=None, scalin
     if pos0 + q_len > kv_len or pos0 < 0:
         raise ValueError("query positions exceed the key length")
     mu, var, _ = block_summary(key, cfg.block, "pop", n_real=kv_len)
-    rows = query.float()
+    rows = _router_rows(query)
     if is_dense:
         top_c, frac = nb_layer, 0.0
     else:

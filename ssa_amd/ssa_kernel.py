@@ -90,7 +90,8 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
           workspace_limit: int = 1 << 30, pool: int = 1):
     """Cumulant router over precomputed summaries -> compact (kv_num, kv_idx).
 
-    rows (B, Hq, nbq, d) fp32: query-block means (mode "budget"/"flat") or query vectors
+    rows (B, Hq, nbq, d) fp32, fp16 or bf16 (16-bit rows are read as their exact fp32 values, so
+    a 16-bit q needs no fp32 copy): query-block means (mode "budget"/"flat") or query vectors
     ("query": blocks complete at position query_pos + r; "started": blocks begun there, own
     included). mu/var/m3 (B, Hkv, nbk*pool, d) fp32:
     with pool > 1 they are sub-block summaries and a key block scores as the max of its pool
@@ -114,7 +115,8 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
     per_i = int(_lib.query("ssa_route_workspace_size", B, Hq, 1, nbs))
     ws_bytes = max(per_i, min(full, workspace_limit // per_i * per_i))
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-    _lib.call("ssa_route_pooled", rows.data_ptr(), mu.data_ptr(), _lib.ptr(var), _lib.ptr(m3), B,
+    _lib.call("ssa_route_pooled", rows.data_ptr(), _lib.dtype_code(rows.dtype), mu.data_ptr(),
+              _lib.ptr(var), _lib.ptr(m3), B,
               Hq, Hkv, nbq, nbk, int(pool), d, _ROUTE_MODES[mode],
               -1 if top_c is None else int(top_c), float(budget_frac), int(local), float(coef2),
               float(coef3), int(query_pos), int(block), kv_num.data_ptr(), kv_idx.data_ptr(), W,

@@ -40,8 +40,8 @@ def route_masked(q: torch.Tensor, k: torch.Tensor, block: int, top_c: int, local
     nb = -(-n // block)
     # the reference zero-pads k to nb * block rows and counts the zero rows in the statistics
     mu, var, _ = block_summary(k, block, "unbiased", n_real=nb * block)
-    return route(q.float(), mu, var, None, "started", int(top_c), 0.0, int(local), 0.5,
-                 query_pos=0, block=block)
+    return route(q, mu, var, None, "started", int(top_c), 0.0, int(local), 0.5, query_pos=0,
+                 block=block)
 
 
 class _MaskedAttention(torch.autograd.Function):

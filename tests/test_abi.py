@@ -62,10 +62,12 @@ def test_invalid_arguments_are_rejected():
                  _lib.STATS_QMEAN, fake, fake, None, None)
     assert rc == _lib.SSA_ERR_INVALID
     # route: W below the required width, then a too-small workspace
-    rc = _status("ssa_route", fake, fake, fake, None, 1, 1, 1, 16, 16, 64, _lib.ROUTE_BUDGET, 4,
+    rc = _status("ssa_route", fake, _lib.F32, fake, fake, None, 1, 1, 1, 16, 16, 64,
+                 _lib.ROUTE_BUDGET, 4,
                  0.0, 1, 1.0, 0.0, 0, 1, fake, fake, 2, fake, 1 << 20, None)
     assert rc == _lib.SSA_ERR_INVALID
-    rc = _status("ssa_route", fake, fake, fake, None, 1, 1, 1, 16, 16, 64, _lib.ROUTE_BUDGET, 4,
+    rc = _status("ssa_route", fake, _lib.F32, fake, fake, None, 1, 1, 1, 16, 16, 64,
+                 _lib.ROUTE_BUDGET, 4,
                  0.0, 1, 1.0, 0.0, 0, 1, fake, fake, 6, fake, 8, None)
     assert rc == _lib.SSA_ERR_WORKSPACE
     # decode: position outside the cache

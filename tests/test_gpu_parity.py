@@ -149,6 +149,27 @@ def test_route_ties_take_lowest_index(cuda):
         assert s == frozenset(list(range(min(3, i))) + [i]), (i, s)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(4, 1, 3, 40, "started"), (2, 1, 1, 500, "query"),
+                                   (4, 2, 24, 300, "query"), (1, 1, 200, 200, "budget")])
+def test_route_16bit_rows_equal_fp32_rows(cuda, dtype, shape):
+    """The router reads fp16 / bf16 query rows directly (their fp32 values are exact): the same
+    lists as for the fp32 copy, on each score kernel (fused <= 64 blocks, few rows, tiles)."""
+    hq, hkv, nbq, nbk, mode = shape
+    rng = np.random.default_rng(31)
+    rows = WL.round_to(rng.standard_normal((1, hq, nbq, 64)).astype(np.float32), dtype)
+    mu = rng.standard_normal((1, hkv, nbk, 64)).astype(np.float32)
+    var = rng.uniform(0.5, 1.5, (1, hkv, nbk, 64)).astype(np.float32)
+    r16, r32 = dev(rows, dtype, cuda), dev(rows, torch.float32, cuda)
+    assert r16.dtype == dtype
+    kw = dict(query_pos=nbk * 64 - nbq - 5, block=64) if mode != "budget" else {}
+    a = K.route(r16, dev(mu, torch.float32, cuda), dev(var, torch.float32, cuda), None, mode, 8,
+                0.0, 1, 1.0, **kw)
+    b = K.route(r32, dev(mu, torch.float32, cuda), dev(var, torch.float32, cuda), None, mode, 8,
+                0.0, 1, 1.0, **kw)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 @pytest.mark.parametrize("nbk", [200, 300, 3000, 12000, 20000])
 @pytest.mark.parametrize("case", ["random", "top_ties", "all_equal"])
 def test_route_long_rows_match_oracle(cuda, case, nbk):
