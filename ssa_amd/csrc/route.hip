@@ -636,8 +636,8 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
 }
 
 // Rows of at most 64 key blocks without pooling or m3: a workgroup of kFusedRows waves takes
-// rows of one query head and stages the key head's mu / var rows in LDS (row stride d + 4
-// floats); each wave scores and selects 2^r_log2 rows at once, 64 >> r_log2 lanes per row, no
+// rows of one query head and stages the key head's mu / var rows in LDS as fp64 (row stride
+// d + 1 doubles); each wave scores and selects 2^r_log2 rows at once, 64 >> r_log2 lanes per row, no
 // score workspace. Within a row, S = 2^s_log2 lanes per candidate each sum a contiguous
 // ceil(d / S) slice of the head dims in fp64, combined by shuffles (the host uses S = 1 and the
 // most rows per wave that still give every candidate a lane); the fp32 score is assembled as in
@@ -645,25 +645,27 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
 // key, or equal key and lower block index); the kept blocks and the local window are compacted
 // in ascending order by ballot.
 constexpr int kFusedRows = 8;       // waves per workgroup
-constexpr int kFusedLds = 64 * 68;  // floats per staged array: nbk * (d + 4) must fit
+constexpr int kFusedLds = 64 * 68;  // staged elements per array: nbk * (d + 4) must fit
 
 __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
     const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     RouteGeom g, int d, float coef2, int r_log2, int s_log2, bool vec4,
     int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx, int64_t W) {
-  extern __shared__ __attribute__((aligned(16))) float fused_lds[];  // 2 * nbk * (d + 4) floats
+  // the key head's mu / var, converted to fp64 once per workgroup (not once per row): row
+  // stride d + 1 doubles, so the 16-byte-apart candidates of a read fall in distinct banks
+  extern __shared__ __attribute__((aligned(16))) double fused_lds_d[];  // 2 * nbk * (d + 1)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.y;  // b * Hq + h
   const int64_t b = bh / g.Hq, h = bh % g.Hq, kvh = h / g.G;
-  const int ds = d + 4, nk = (int)g.nbk;
-  float* ms = fused_lds;
-  float* vs = fused_lds + nk * ds;
+  const int ds = d + 1, nk = (int)g.nbk;
+  double* ms = fused_lds_d;
+  double* vs = fused_lds_d + nk * ds;
   const float* kmu = mu + (b * g.Hkv + kvh) * g.nbk * d;
   const float* kvar = var ? var + (b * g.Hkv + kvh) * g.nbk * d : nullptr;
   for (int idx = tid; idx < nk * d; idx += 64 * kFusedRows) {
     const int c = idx / d, t = idx - c * d;
-    ms[c * ds + t] = kmu[idx];
-    vs[c * ds + t] = kvar ? kvar[idx] : 0.0f;
+    ms[c * ds + t] = (double)kmu[idx];
+    vs[c * ds + t] = kvar ? (double)kvar[idx] : 0.0;
   }
   __syncthreads();
   // the wave holds 2^r_log2 rows, Lr lanes each: lane = (row rr, candidate c, head-dim part)
@@ -684,8 +686,8 @@ __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
   double e1 = 0.0, e2 = 0.0;
   if (cand) {
     const float* q = static_cast<const float*>(rows) + lrow * d;
-    const float* mrow = ms + c * ds;
-    const float* vrow = vs + c * ds;
+    const double* mrow = ms + c * ds;
+    const double* vrow = vs + c * ds;
     if (vec4 && g.rows_dt != SSA_F32) {  // 16-bit rows, d a multiple of 8 * S: 16-byte loads
       const unsigned short* q16 = static_cast<const unsigned short*>(rows) + lrow * d;
       for (int t = k0; t < k1; t += 8) {
@@ -694,29 +696,27 @@ __global__ __launch_bounds__(64 * kFusedRows) void route_rows_small_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float q2 = qa[j] * qa[j];
-          e1 = fma((double)qa[j], (double)mrow[t + j], e1);
-          e2 = fma((double)q2, (double)vrow[t + j], e2);
+          e1 = fma((double)qa[j], mrow[t + j], e1);
+          e2 = fma((double)q2, vrow[t + j], e2);
         }
       }
     } else if (vec4) {  // d a multiple of 4 * S: 16-byte loads
 #pragma unroll 4
       for (int t = k0; t < k1; t += 4) {
         const f32x4 qa = *reinterpret_cast<const f32x4*>(q + t);
-        const f32x4 ma = *reinterpret_cast<const f32x4*>(mrow + t);
-        const f32x4 va = *reinterpret_cast<const f32x4*>(vrow + t);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float q2 = qa[j] * qa[j];  // rounded to fp32 like the reference's product
-          e1 = fma((double)qa[j], (double)ma[j], e1);
-          e2 = fma((double)q2, (double)va[j], e2);
+          e1 = fma((double)qa[j], mrow[t + j], e1);
+          e2 = fma((double)q2, vrow[t + j], e2);
         }
       }
     } else {
       for (int t = k0; t < k1; ++t) {
         const float qf = load_row(rows, lrow * d + t, g.rows_dt);
         const float q2 = qf * qf;
-        e1 = fma((double)qf, (double)mrow[t], e1);
-        e2 = fma((double)q2, (double)vrow[t], e2);
+        e1 = fma((double)qf, mrow[t], e1);
+        e2 = fma((double)q2, vrow[t], e2);
       }
     }
   }
@@ -878,7 +878,7 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     const int64_t rows_per_wg = (int64_t)kFusedRows << r_log2;
     const int64_t chunks = (nbq + rows_per_wg - 1) / rows_per_wg;
     SSA_REQUIRE(chunks < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
-    const size_t lds = (size_t)2 * nbk * (d + 4) * sizeof(float);
+    const size_t lds = (size_t)2 * nbk * (d + 1) * sizeof(double);
     route_rows_small_kernel<<<dim3((unsigned)chunks, (unsigned)(B * Hq)), 64 * kFusedRows, lds,
                               stream>>>(rows, mu, var, g, (int)d, coef2, r_log2, s_log2, vec4,
                                         kv_num, kv_idx, W);
