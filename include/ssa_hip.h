@@ -227,7 +227,9 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
  *   scaled scores).
  * backward: dq (B, Hq, n, d), dk, dv (B, Hkv, n, d) contiguous, written by the call, in
  *   grad_dtype: SSA_F32, or the input dtype (tiled path only; the per-row path returns
- *   SSA_ERR_UNSUPPORTED for it), which spares the caller a conversion pass.
+ *   SSA_ERR_UNSUPPORTED for it), which spares the caller a conversion pass. flags =
+ *   SSA_MASKED_MASKS_READY: the workspace is the one the forward call used with the same lists
+ *   (it still holds the forward's row masks, which the backward then does not rebuild).
  * Both take ssa_masked_attn_workspace_size(B, Hq, n, W, d, block) bytes of workspace.
  * d = 64 with at most 8192 key blocks runs the tiled MFMA kernels (per (64-row query tile, key
  *   block) row masks; q, k, v, out, dout, dq, dk, dv 16-byte aligned; deterministic). Other head
@@ -241,10 +243,11 @@ int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, void* out, 
                         int64_t block, const int64_t* strides, const int32_t* kv_num,
                         const int32_t* kv_idx, int64_t W, float scale, void* workspace,
                         size_t workspace_bytes, ssa_stream_t stream);
+enum { SSA_MASKED_MASKS_READY = 1 };
 int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                         const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                        int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
-                        int64_t d,
+                        int dtype, int grad_dtype, int flags, int64_t B, int64_t Hq, int64_t Hkv,
+                        int64_t n, int64_t d,
                         int64_t block, const int64_t* strides, const int32_t* kv_num,
                         const int32_t* kv_idx, int64_t W, float scale, void* workspace,
                         size_t workspace_bytes, ssa_stream_t stream);

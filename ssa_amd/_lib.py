@@ -21,6 +21,7 @@ F32, F16, BF16 = 0, 1, 2
 STATS_POP, STATS_UNBIASED, STATS_QMEAN = 0, 1, 2
 ROUTE_BUDGET, ROUTE_FLAT, ROUTE_QUERY, ROUTE_STARTED = 0, 1, 2, 3
 ATTN_VT_READY = 1
+MASKED_MASKS_READY = 1
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -50,7 +51,7 @@ _SIGNATURES = {
     "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ssa_masked_attn_fwd": (_c_int, [_c_p] * 5 + [_c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
-    "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int, _c_int] + [_c_i64] * 6 +
+    "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int, _c_int, _c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
     "ssa_sparse_attn_workspace_size": (_c_sz, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ssa_transpose_v": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,

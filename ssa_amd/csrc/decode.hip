@@ -38,8 +38,8 @@ int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, flo
                      hipStream_t st);
 int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* out,
                      const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                     int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n,
-                     int64_t block,
+                     int dtype, int grad_dtype, int flags, int64_t B, int64_t Hq, int64_t Hkv,
+                     int64_t n, int64_t block,
                      const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
                      int64_t W, float scale, void* workspace, size_t workspace_bytes,
                      hipStream_t st);
@@ -725,8 +725,8 @@ extern "C" int ssa_masked_attn_fwd(const void* q, const void* k, const void* v, 
 
 extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                                    const void* dout, const float* lse, void* dq, void* dk,
-                                   void* dv, int dtype, int grad_dtype, int64_t B, int64_t Hq,
-                                   int64_t Hkv,
+                                   void* dv, int dtype, int grad_dtype, int flags, int64_t B,
+                                   int64_t Hq, int64_t Hkv,
                                    int64_t n, int64_t d, int64_t block, const int64_t* strides,
                                    const int32_t* kv_num, const int32_t* kv_idx, int64_t W,
                                    float scale, void* workspace, size_t workspace_bytes,
@@ -736,9 +736,11 @@ extern "C" int ssa_masked_attn_bwd(const void* q, const void* k, const void* v, 
   SSA_TRY(masked_params(bp.f, q, k, v, out, dtype, B, Hq, Hkv, n, d, block, strides, kv_num,
                         kv_idx, W, scale));
   SSA_REQUIRE(dout && lse && dq && dk && dv, SSA_ERR_INVALID, "masked_attn_bwd: NULL gradient");
+  SSA_REQUIRE((flags & ~SSA_MASKED_MASKS_READY) == 0, SSA_ERR_INVALID,
+              "masked_attn_bwd: unknown flags");
   if (masked_tiled_ok(d, block, n))
-    return masked_tiled_bwd(q, k, v, out, dout, lse, dq, dk, dv, dtype, grad_dtype, B, Hq, Hkv,
-                            n, block,
+    return masked_tiled_bwd(q, k, v, out, dout, lse, dq, dk, dv, dtype, grad_dtype, flags, B, Hq,
+                            Hkv, n, block,
                             strides, kv_num, kv_idx, W, scale, workspace, workspace_bytes,
                             static_cast<hipStream_t>(stream));
   SSA_REQUIRE(grad_dtype == SSA_F32, SSA_ERR_UNSUPPORTED,

@@ -1040,7 +1040,7 @@ int masked_tiled_fwd(const void* q, const void* k, const void* v, void* out, flo
 
 int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* out,
                      const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                     int dtype, int grad_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
+                     int dtype, int grad_dtype, int flags, int64_t B, int64_t Hq, int64_t Hkv, int64_t n, int64_t block,
                      const int64_t* strides, const int32_t* kv_num, const int32_t* kv_idx,
                      int64_t W, float scale, void* workspace, size_t workspace_bytes,
                      hipStream_t st) {
@@ -1056,8 +1056,10 @@ int masked_tiled_bwd(const void* q, const void* k, const void* v, const void* ou
   a.dq = dq; a.dk = dk; a.dv = dv;
   a.grad16 = grad_dtype != SSA_F32;
   const unsigned gq = (unsigned)(B * Hq * a.nqt), gk = (unsigned)(B * Hkv * a.nkt);
-  row_block_masks_kernel<<<gq, 256, 0, st>>>(a);
-  SSA_TRY(launch_status("row_block_masks_kernel"));
+  if (!(flags & SSA_MASKED_MASKS_READY)) {  // else the forward's masks are in the workspace
+    row_block_masks_kernel<<<gq, 256, 0, st>>>(a);
+    SSA_TRY(launch_status("row_block_masks_kernel"));
+  }
   if (dtype == SSA_F32) {
     swap_dq_kernel<SSA_F32><<<gq, 256, 0, st>>>(a);
     swap_dkdv_kernel<SSA_F32><<<gk, 256, 0, st>>>(a);

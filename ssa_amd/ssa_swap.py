@@ -62,6 +62,7 @@ class _MaskedAttention(torch.autograd.Function):
                   ws.data_ptr(), wsb, _lib.stream_of(q))
         ctx.save_for_backward(q, k, v, out, lse, kv_num, kv_idx)
         ctx.block, ctx.scale = int(block), float(scale)
+        ctx.ws = ws  # its row masks serve the backward too
         return out
 
     @staticmethod
@@ -72,7 +73,7 @@ class _MaskedAttention(torch.autograd.Function):
         W = kv_idx.shape[-1]
         dout = dout.to(out.dtype).contiguous()  # described by out's (contiguous) strides
         wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, Hq, n, W, d, ctx.block))
-        ws = torch.empty(wsb, device=q.device, dtype=torch.uint8)
+        ws = ctx.ws  # the forward's workspace: its row masks are reused
         dt = _lib.dtype_code(q.dtype)
         strides = _strides(q, k, v, out)
 
@@ -82,7 +83,8 @@ class _MaskedAttention(torch.autograd.Function):
             dv = torch.empty_like(dk)
             _lib.call("ssa_masked_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
                       out.data_ptr(), dout.data_ptr(), lse.data_ptr(), dq.data_ptr(),
-                      dk.data_ptr(), dv.data_ptr(), dt, _lib.dtype_code(gdt), B, Hq, Hkv, n, d,
+                      dk.data_ptr(), dv.data_ptr(), dt, _lib.dtype_code(gdt),
+                      _lib.MASKED_MASKS_READY, B, Hq, Hkv, n, d,
                       ctx.block, strides, kv_num.data_ptr(), kv_idx.data_ptr(), W, ctx.scale,
                       ws.data_ptr(), wsb, _lib.stream_of(q))
             return dq, dk, dv

@@ -77,6 +77,39 @@ def test_ssa_masked_matches_oracle(cuda, dtype, shape):
         assert np.abs(np_of(got) - want).max() < tol * scale, nm
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_masked_bwd_fresh_workspace_equals_reused_masks(cuda, dtype):
+    """ssa_masked_attn_bwd on a fresh workspace (flags 0: it builds the row masks itself), with
+    fp32 gradients, equals the autograd backward, which reuses the forward's masks and writes
+    the gradients in the input type."""
+    from ssa_amd import _lib
+    rng = np.random.default_rng(23)
+    B, H, n, d, block = 1, 2, 200, 64, 32
+    q, k, v, g = (rng.standard_normal((B, H, n, d)).astype(np.float32) for _ in range(4))
+    out, dq, dk, dv = run_masked(q, k, v, g, block, 2, 1, dtype, cuda)
+    tq, tk, tv, tg = (WL.to_device(x, dtype, cuda) for x in (q, k, v, g))
+    kv_num, kv_idx = S.route_masked(tq, tk, block, 2, 1)
+    W = kv_idx.shape[-1]
+    o2, lse = torch.empty_like(tq), torch.empty(B, H, n, device=cuda, dtype=torch.float32)
+    wsb = int(_lib.query("ssa_masked_attn_workspace_size", B, H, n, W, d, block))
+    strides = S._strides(tq, tk, tv, o2)
+    dt = _lib.dtype_code(dtype)
+    ws = torch.empty(wsb, device=cuda, dtype=torch.uint8)
+    _lib.call("ssa_masked_attn_fwd", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o2.data_ptr(),
+              lse.data_ptr(), dt, B, H, H, n, d, block, strides, kv_num.data_ptr(),
+              kv_idx.data_ptr(), W, d ** -0.5, ws.data_ptr(), wsb, _lib.stream_of(tq))
+    grads = [torch.empty(B, H, n, d, device=cuda, dtype=torch.float32) for _ in range(3)]
+    fresh = torch.empty(wsb, device=cuda, dtype=torch.uint8)
+    _lib.call("ssa_masked_attn_bwd", tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o2.data_ptr(),
+              tg.data_ptr(), lse.data_ptr(), *(x.data_ptr() for x in grads), dt, _lib.F32, 0,
+              B, H, H, n, d, block, strides, kv_num.data_ptr(), kv_idx.data_ptr(), W, d ** -0.5,
+              fresh.data_ptr(), wsb, _lib.stream_of(tq))
+    torch.cuda.synchronize()
+    assert torch.equal(o2, out)
+    for got, ref in zip(grads, (dq, dk, dv)):
+        assert torch.equal(got.to(dtype), ref)
+
+
 def test_ssa_masked_strided_views(cuda):
     """GPT-2 hands SDPA q/k/v as head-transposed views of one fused projection: the same
     results as on contiguous copies, without a copy of the inputs."""
