@@ -285,14 +285,15 @@ def main():
                               dtype=c4.dtype, device=dev)
         kd, vd = WL.to_device(ds["k"], c4.dtype, dev), WL.to_device(ds["v"], c4.dtype, dev)
         qd = WL.to_device(ds["q"], c4.dtype, dev)
+        qd = qd.permute(2, 0, 1, 3).contiguous()  # (steps, B, Hq, d): each step's q contiguous
         dec.prefill(kd[:, :, :ncache], vd[:, :, :ncache])
         out_d = torch.empty(1, c4.Hq, c4.d, device=dev, dtype=c4.dtype)
         for t in range(8):
-            dec.step(qd[:, :, t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+            dec.step(qd[t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for t in range(8, 8 + args.decode_steps):
-            dec.step(qd[:, :, t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+            dec.step(qd[t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
         torch.cuda.synchronize()
         dms = (time.perf_counter() - t0) / args.decode_steps * 1000.0
         kvn = int(dec.kv_num.sum().item())
@@ -303,7 +304,7 @@ def main():
         # needed at decode, and K/V are read once, not repeated per query head)
         npre = dec.pos
         G4 = c4.Hq // c4.Hkv
-        qd1 = qd[:, :, 8].reshape(1, c4.Hkv, G4, c4.d)
+        qd1 = qd[8].reshape(1, c4.Hkv, G4, c4.d)
         kpre, vpre = dec.kcache[:, :, :npre], dec.vcache[:, :, :npre]
         sdpa = torch.nn.functional.scaled_dot_product_attention
         for _ in range(3):

@@ -64,6 +64,13 @@ struct DecodeParams {
   float scale_log2;
   float* part;  // (B*Hq*nq, W, d + 2): m, l, o[d]
   float* lse;   // optional (B*Hq*nq): natural-log sum of exp of the scaled scores of the row
+  // decode step with the append folded in: the token at pos is not yet in the caches; its key /
+  // value rows are read from k_new / v_new (B, Hkv, d), and one workgroup per key head writes
+  // them into the caches (no workgroup of the launch reads cache row pos)
+  int fused_append = 0;
+  const char* k_new = nullptr;
+  const char* v_new = nullptr;
+  int64_t knb = 0, knh = 0, vnb = 0, vnh = 0;
 };
 
 template <int DT>
@@ -114,16 +121,27 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   constexpr int kPre = 16;
   const int kg = lane >> 3, ch = lane & 7;
   const int64_t voff = b * p.vsb + kvh * p.vsh;
+  const int64_t koff = b * p.ksb + kvh * p.ksh;
   const bool pre = DT != SSA_F32 && d <= 64 && nk <= 8 * kPre;
+  // row pointers of key `key` (the token being appended comes from k_new / v_new)
+  constexpr int es = DT == SSA_F32 ? 4 : 2;
+  const int64_t newkey = p.fused_append ? pos : -1;
+  auto krow = [&](int64_t key) -> const char* {
+    return key == newkey ? p.k_new + (b * p.knb + kvh * p.knh) * es : p.k + (koff + key * p.ksn) * es;
+  };
+  auto vrow = [&](int64_t key) -> const char* {
+    return key == newkey ? p.v_new + (b * p.vnb + kvh * p.vnh) * es : p.v + (voff + key * p.vsn) * es;
+  };
   u32x4 vpre[kPre];
   if constexpr (DT != SSA_F32) {
     if (pre) {
-      const unsigned short* vb = reinterpret_cast<const unsigned short*>(p.v) + voff;
 #pragma unroll
       for (int t = 0; t < kPre; ++t) {
         const int kk = kg + 8 * t;
         vpre[t] = u32x4{0u, 0u, 0u, 0u};
-        if (kk < nk && ch * 8 < d) vpre[t] = *reinterpret_cast<const u32x4*>(vb + (key0 + kk) * p.vsn + ch * 8);
+        if (kk < nk && ch * 8 < d)
+          vpre[t] = *reinterpret_cast<const u32x4*>(
+              reinterpret_cast<const unsigned short*>(vrow(key0 + kk)) + ch * 8);
       }
     }
   }
@@ -133,14 +151,13 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   for (int e = lane; e < d; e += 64) qs[e] = load_elem<DT>(qb, qoff + e);
   __syncthreads();
 
-  const int64_t koff = b * p.ksb + kvh * p.ksh;
   float mloc = -INFINITY;
   for (int kk = lane; kk < nk; kk += 64) {
-    const int64_t roff = koff + (key0 + kk) * p.ksn;
+    const char* kr = krow(key0 + kk);
     float s = 0.0f;
     if constexpr (DT == SSA_F32) {
       for (int e = 0; e < d; e += 4) {
-        const f32x4 kv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.k) + roff + e);
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(kr) + e);
         s = fmaf(qs[e], kv[0], s);
         s = fmaf(qs[e + 1], kv[1], s);
         s = fmaf(qs[e + 2], kv[2], s);
@@ -149,7 +166,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     } else {
       for (int e = 0; e < d; e += 8) {
         const u32x4 w =
-            *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned short*>(p.k) + roff + e);
+            *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned short*>(kr) + e);
         float kv[8];
         unpack8(w, kv, DT == SSA_BF16);
 #pragma unroll
@@ -174,7 +191,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     for (int e = lane; e < d; e += 64) {
       float acc = 0.0f;
       for (int kk = 0; kk < nk; ++kk)
-        acc = fmaf(ps[kk], load_elem<DT>(p.v, voff + (key0 + kk) * p.vsn + e), acc);
+        acc = fmaf(ps[kk], load_elem<DT>(vrow(key0 + kk), e), acc);
       part[2 + e] = acc;
     }
   } else if (pre) {  // the prefetched V rows; the 8 key groups summed with shuffles
@@ -205,7 +222,6 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
       for (int t = 0; t < 8; ++t) part[2 + ch * 8 + t] = acc[t];
   } else {
     // 8 keys per pass, 16-byte V row loads; the 8 key groups are summed with shuffles.
-    const unsigned short* vb = reinterpret_cast<const unsigned short*>(p.v) + voff;
     for (int e0 = 0; e0 < d; e0 += 64) {
       const bool on = e0 + ch * 8 < d;
       float acc[8];
@@ -214,7 +230,8 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
       if (on) {
 #pragma unroll 4
         for (int kk = kg; kk < nk; kk += 8) {
-          const u32x4 wv = *reinterpret_cast<const u32x4*>(vb + (key0 + kk) * p.vsn + e0 + ch * 8);
+          const u32x4 wv = *reinterpret_cast<const u32x4*>(
+              reinterpret_cast<const unsigned short*>(vrow(key0 + kk)) + e0 + ch * 8);
           float vv[8];
           unpack8(wv, vv, DT == SSA_BF16);
           const float pk = ps[kk];
@@ -343,6 +360,16 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
     for (int e = lane; e < d; e += 64) part[2 + e] = 0.0f;
   } else {
     block_partial<DT>(p, part, qs, ps, b, h, kvh, r, pos, c);
+  }
+  // folded append: workgroup (j = 0) of the first query head of each key head writes the new
+  // token into the caches; every read of that row in this launch comes from k_new / v_new
+  if (p.fused_append && j == 0 && r == 0 && h % p.G == 0) {
+    for (int e = lane; e < d; e += 64) {
+      store_elem<DT>(const_cast<char*>(p.k), b * p.ksb + kvh * p.ksh + pos * p.ksn + e,
+                     load_elem<DT>(p.k_new, b * p.knb + kvh * p.knh + e));
+      store_elem<DT>(const_cast<char*>(p.v), b * p.vsb + kvh * p.vsh + pos * p.vsn + e,
+                     load_elem<DT>(p.v_new, b * p.vnb + kvh * p.vnh + e));
+    }
   }
 }
 
@@ -606,7 +633,12 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   void* keys = ws + qf_bytes;
   float* part = reinterpret_cast<float*>(ws + qf_bytes + key_bytes);
 
-  // 1. append the new token and convert the query rows (one launch)
+  // 1. append the new token and convert the query rows (one launch) -- unless the step can fold
+  //    the append into the attend launch: no block completes at pos (its summary would need the
+  //    token in the cache first) and the query rows are contiguous, so the router reads them as
+  //    they are
+  const bool completes = (pos + 1) % block == 0;
+  const bool fold = !completes && strides[1] == d && strides[0] == Hq * d;
   AppendStrides as;
   as.knb = strides[2]; as.knh = strides[3]; as.vnb = strides[4]; as.vnh = strides[5];
   as.kcb = strides[6]; as.kch = strides[7]; as.kcn = strides[8];
@@ -618,21 +650,23 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   const unsigned gr = (unsigned)(B * Hq);
   const char* qc = static_cast<const char*>(q);
   const int64_t G = Hq / Hkv;
-  switch (dtype) {
-    case SSA_F32:
-      decode_prep_kernel<SSA_F32><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
-                                                      strides[1], pos, as);
-      break;
-    case SSA_F16:
-      decode_prep_kernel<SSA_F16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
-                                                      strides[1], pos, as);
-      break;
-    default:
-      decode_prep_kernel<SSA_BF16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
-                                                       strides[1], pos, as);
-      break;
+  if (!fold) {
+    switch (dtype) {
+      case SSA_F32:
+        decode_prep_kernel<SSA_F32><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                        strides[1], pos, as);
+        break;
+      case SSA_F16:
+        decode_prep_kernel<SSA_F16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                        strides[1], pos, as);
+        break;
+      default:
+        decode_prep_kernel<SSA_BF16><<<gr, 64, 0, st>>>(qc, qf, kn, vn, kc, vc, Hq, G, d, strides[0],
+                                                         strides[1], pos, as);
+        break;
+    }
+    SSA_TRY(launch_status("decode_prep_kernel"));
   }
-  SSA_TRY(launch_status("decode_prep_kernel"));
 
   // 2. a block completed at pos: its population summary becomes routable
   if ((pos + 1) % block == 0) {
@@ -643,9 +677,9 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   }
 
   // 3. route the queries over the complete blocks
-  SSA_TRY(route_impl(qf, SSA_F32, mu, var, nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c,
-                     budget_frac, local, coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys,
-                     key_bytes, st));
+  SSA_TRY(route_impl(fold ? static_cast<const void*>(qc) : qf, fold ? dtype : SSA_F32, mu, var,
+                     nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c, budget_frac, local,
+                     coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys, key_bytes, st));
 
   // 4. attend
   DecodeParams p;
@@ -663,6 +697,12 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
   p.scale_log2 = scale * kLog2e;
   p.part = part;
   p.lse = nullptr;
+  if (fold) {
+    p.fused_append = 1;
+    p.k_new = kn;
+    p.v_new = vn;
+    p.knb = as.knb; p.knh = as.knh; p.vnb = as.vnb; p.vnh = as.vnh;
+  }
   return run_attend(dtype, p, st);
 }
 

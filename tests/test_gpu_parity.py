@@ -472,6 +472,34 @@ def test_dense_decode_baselines_agree_with_full_selection(cuda):
         assert got.dtype == torch.bfloat16 and np.abs(np_of(got) - ref).max() < 2e-2
 
 
+def test_decoder_folded_append_equals_separate_append(cuda):
+    """RoutedDecoder.step with contiguous query rows folds the cache append into the attend
+    launch (no prep launch; the router reads the bf16 q); with strided rows it appends and
+    converts in a launch of its own. Over steps that complete a block and steps that do not,
+    both give identical selections, outputs and caches."""
+    rng = np.random.default_rng(29)
+    hq, hkv, d, block, n0, steps = 4, 2, 64, 64, 64 * 5 + 60, 10
+    k, v = (WL.round_to(rng.standard_normal((1, hkv, n0 + steps, d)).astype(np.float32),
+                        torch.bfloat16) for _ in range(2))
+    q = WL.round_to(rng.standard_normal((steps, 1, hq, d)).astype(np.float32), torch.bfloat16)
+    kt, vt = dev(k, torch.bfloat16, cuda), dev(v, torch.bfloat16, cuda)
+    qc = dev(q, torch.bfloat16, cuda)                        # step t: qc[t] contiguous
+    qs = qc.permute(1, 2, 0, 3).contiguous().permute(2, 0, 1, 3)  # same values, strided rows
+    assert qc[0].is_contiguous() and not qs[0].is_contiguous()
+    decs = [D.RoutedDecoder(1, hq, hkv, d, n0 + steps, block=block, top_c=3, local=1,
+                            dtype=torch.bfloat16, device=cuda) for _ in range(2)]
+    for dec in decs:
+        dec.prefill(kt[:, :, :n0], vt[:, :, :n0])
+    for t in range(steps):  # positions 380..389: the step at 383 completes block 5
+        outs = [dec.step(qq[t], kt[:, :, n0 + t], vt[:, :, n0 + t])
+                for dec, qq in zip(decs, (qc, qs))]
+        assert torch.equal(outs[0], outs[1]), t
+        assert torch.equal(decs[0].kv_num, decs[1].kv_num) and torch.equal(decs[0].kv_idx, decs[1].kv_idx)
+    for a, b in ((decs[0].kcache, decs[1].kcache), (decs[0].vcache, decs[1].vcache)):
+        assert torch.equal(a[:, :, :n0 + steps], b[:, :, :n0 + steps])
+    assert torch.equal(decs[0].kcache[:, :, :n0 + steps], kt)
+
+
 def test_routed_decoder_matches_reference_router_and_oracle(cuda):
     """RoutedDecoder on a C4-shaped cache: the selection at each fixture position equals the
     reference _selection_mask (float32) and the oracle; the output matches the oracle row."""
