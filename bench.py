@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "routed prefill tokens/s @128K (Qwen-0.5B shape); decode ms/step @1M ctx"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+PEAK_FP64_TFLOPS = 78.6
 TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
 
 
@@ -88,17 +89,61 @@ class Timer:
 
 
 def read_traffic():
+    """(HBM bytes per launch, L2 hit rate) of the attention kernel from the committed rocprofv3
+    counter summary, or (None, None)."""
     if not TRAFFIC_FILE.exists():
-        return None
+        return None, None
     kv = {}
     for line in TRAFFIC_FILE.read_text().splitlines():
         if ":" in line and not line.lstrip().startswith("#"):
             key, val = line.split(":", 1)
             kv[key.strip()] = val.strip()
     try:
-        return float(kv["hbm_bytes_per_launch"])
+        traffic = float(kv["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
-        return None
+        traffic = None
+    try:
+        hit, miss = float(kv["tcc_hit_per_launch"]), float(kv["tcc_miss_per_launch"])
+        l2 = hit / (hit + miss)
+    except (KeyError, ValueError, ZeroDivisionError):
+        l2 = None
+    return traffic, l2
+
+
+def device_info(torch, dev):
+    """The box's own figures: CU count and clock (rocminfo) -> derived bf16 MFMA peak, and the
+    achievable HBM rate of a plain 2 GiB device copy."""
+    props = torch.cuda.get_device_properties(dev)
+    info = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
+            "cus": props.multi_processor_count}
+    try:
+        import re
+        import subprocess
+        txt = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+        clocks = [int(m.group(1)) for agent in re.split(r"\n\*+\s*\nAgent \d+", txt)
+                  if re.search(r"Device Type:\s+GPU", agent)
+                  for m in [re.search(r"Max Clock Freq\. \(MHz\):\s+(\d+)", agent)] if m]
+        gpu_clk = max(clocks) if clocks else None
+    except (OSError, subprocess.SubprocessError):
+        gpu_clk = None
+    if gpu_clk:
+        info["max_sclk_mhz"] = gpu_clk
+        # gfx950: 4 SIMDs x 1024 bf16 FLOP per clock per SIMD (dense MFMA)
+        info["bf16_mfma_peak_derived_tflops"] = props.multi_processor_count * 4096 * gpu_clk / 1e6
+    src = torch.empty(1 << 31, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    gbs = 2 * src.numel() * 5 / (time.perf_counter() - t0) / 1e9
+    info["hbm_copy_gbs"] = gbs
+    info["hbm_copy_frac_of_8tbs"] = gbs / PEAK_HBM_GBS
+    del src, dst
+    return info
 
 
 def cpu_baseline(p, kv_num_all, threads):
@@ -108,20 +153,24 @@ def cpu_baseline(p, kv_num_all, threads):
 
     from oracle import ssa_oracle as O
     cfg = p["cfg"]
-    t0 = time.perf_counter()
-    onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
-                                beta=cfg.beta)
-    t_route = time.perf_counter() - t0
     rng = np.random.default_rng(0)
     nb = cfg.nb
     blocks = sorted(set(np.linspace(0, nb - 1, 24).astype(int).tolist()))
     heads = [int(h) for h in rng.integers(0, cfg.Hq, size=len(blocks))]
-    t0 = time.perf_counter()
-    sample_kv = 0
-    for i, h in zip(blocks, heads):
-        O.sparse_attention(p["q"], p["k"], p["v"], onum, oidx, cfg.block, qblocks=[i], heads=[h])
-        sample_kv += int(onum[0, h, i])
-    t_sample = time.perf_counter() - t0
+    routes, samples = [], []
+    for _ in range(3):  # median of 3 runs of the sample
+        t0 = time.perf_counter()
+        onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                    beta=cfg.beta)
+        routes.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        sample_kv = 0
+        for i, h in zip(blocks, heads):
+            O.sparse_attention(p["q"], p["k"], p["v"], onum, oidx, cfg.block, qblocks=[i],
+                               heads=[h])
+            sample_kv += int(onum[0, h, i])
+        samples.append(time.perf_counter() - t0)
+    t_route, t_sample = sorted(routes)[1], sorted(samples)[1]
     total_kv = int(kv_num_all)
     t_attn = t_sample * total_kv / sample_kv
     t_total = t_route + t_attn
@@ -130,7 +179,7 @@ def cpu_baseline(p, kv_num_all, threads):
         "sample": (f"oracle (NumPy float64) C3 router over all {cfg.Hq * nb} query-block rows "
                    f"({t_route:.2f} s) + exact attention for {len(blocks)} (head, query-block) "
                    f"pairs ({sample_kv} of {total_kv} selected tiles, {t_sample:.2f} s), "
-                   f"extrapolated by sum(kv_num) to {t_total:.1f} s per layer"),
+                   f"extrapolated by sum(kv_num) to {t_total:.1f} s per layer; median of 3 runs"),
     }
 
 
@@ -223,10 +272,11 @@ def main():
     flops = 4.0 * blk * blk * cfg.d * sum_kv
     t_attn = parts["attention"] / 1e3
     achieved = flops / t_attn / 1e12
-    traffic = read_traffic()
+    traffic, l2_hit = read_traffic()
     diag = cfg.Hq * cfg.nb
     flops_causal = 4.0 * cfg.d * (blk * blk * (sum_kv - diag) + diag * blk * (blk + 1) / 2)
     summary_bytes = (cfg.Hkv + cfg.Hq) * n * cfg.d * 2 + (2 * cfg.Hkv + cfg.Hq) * cfg.nb * cfg.d * 4
+    router_flops = 2.0 * (2 * cfg.d) * cfg.Hq * cfg.nb * (cfg.nb - 1) / 2
     log(f"bench: {ms_step:.3f} ms/step; parts {parts}; sum kv_num {sum_kv}")
 
     result = {
@@ -245,10 +295,22 @@ def main():
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "flops_per_launch": flops, "flops_causal_exact": flops_causal,
-                     "sum_kv_num": sum_kv},
+                     "sum_kv_num": sum_kv, "l2_hit_rate": l2_hit,
+                     "gathered_kv_bytes": sum_kv * 2 * blk * cfg.d * 2},
         "breakdown_ms": parts,
         "summaries_gbs": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3) / 1e9,
+        "summaries": {"bytes": summary_bytes, "ms": parts["qmean"] + parts["kstats"],
+                      "hbm_frac": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3)
+                      / 1e9 / PEAK_HBM_GBS},
+        # the router's inner products accumulate in fp64 on the VALU (exact selections); its
+        # FLOPs are set against the bf16 MFMA peak as asked, and against the fp64 peak it runs at
+        "router": {"flops": router_flops, "ms": parts["route"],
+                   "tflops": router_flops / (parts["route"] / 1e3) / 1e12,
+                   "frac_bf16_mfma_peak": router_flops / (parts["route"] / 1e3) / 1e12
+                   / PEAK_BF16_TFLOPS,
+                   "frac_fp64_peak": router_flops / (parts["route"] / 1e3) / 1e12 / PEAK_FP64_TFLOPS},
     }
+    result["device"] = device_info(torch, dev)
 
     if not args.no_dense:
         log("bench: dense baselines")
