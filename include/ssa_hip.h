@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 4
+#define SSA_ABI_VERSION 5
 
 typedef void* ssa_stream_t; /* hipStream_t */
 
@@ -152,6 +152,38 @@ int ssa_project_rows(const float* x, const float* w, int64_t rows, int64_t din, 
  */
 int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t rows, int64_t W,
                          int64_t nbk, uint8_t* sel, int32_t* kv_full, ssa_stream_t stream);
+
+/*
+ * IVF router over block means: the sub-linear router that replaces the faiss GpuIndexIVFFlat
+ * route of ssa/ivf_kernel.py:63-119 (build_ivf, _route_head, ivf_route), deterministic.
+ * mu, qb: (BH, nb, d) fp32 contiguous key- and query-block means (ssa_block_summary, QMEAN),
+ * d a multiple of 32 and at most 256, 1 <= nlist <= min(nb, 2048).
+ *
+ * ssa_ivf_build (build_ivf: train + add, :63-69): per head, nlist centroids start at the
+ *   normalised mu[c * nb / nlist] and run niter rounds of spherical k-means (assign each block
+ *   mean to its largest-inner-product centroid, ties to the lower centroid; each centroid <- the
+ *   normalised sum of its members, unchanged without members); a last assignment fills the
+ *   lists. The index buffer (ssa_ivf_index_size bytes, 256-byte aligned) starts with, each
+ *   region 256-byte aligned: centroids (BH, nlist, d) fp32; list sizes (BH, nlist) int32; list
+ *   offsets (BH, nlist + 1) int32; member block ids (BH, nb) int32, list by list, ascending
+ *   within a list; then scratch of the build.
+ * ssa_ivf_route (_route_head, :72-99): per query block i, the min(nprobe, nlist) lists of
+ *   largest <qb_i, centroid>, the min(search_k, nb) members of those lists of largest
+ *   <qb_i, mu_j> (at most 1024), of these the top_c largest with j <= i, OR blocks
+ *   i - local .. i; kv_num (BH, nb), kv_idx (BH, nb, W) ascending padded with 0,
+ *   W >= min(top_c + local + 1, nb), min(top_c, search_k) + min(local, nb - 1) + 1 <= 2048.
+ * Inner products are accumulated in fp64 in dimension order and rounded once to fp32; ties go
+ * to the lower block index.
+ */
+size_t ssa_ivf_index_size(int64_t BH, int64_t nb, int64_t nlist, int64_t d);
+
+int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d, int64_t nlist,
+                  int64_t niter, void* index, size_t index_bytes, ssa_stream_t stream);
+
+int ssa_ivf_route(const void* index, const float* mu, const float* qb, int64_t BH, int64_t nb,
+                  int64_t d, int64_t nlist, int64_t nprobe, int64_t search_k, int64_t top_c,
+                  int64_t local, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+                  ssa_stream_t stream);
 
 /*
  * Block-sparse causal attention forward (replaces FlexAttention with

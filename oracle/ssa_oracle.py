@@ -26,6 +26,14 @@ Pinning (what checks each function; details in tests/test_oracle.py):
   masked_forward /       planted slips (biased variance, pad rows dropped, complete-block
   masked_grads           candidates) fail them; full selection == dense causal and torch autograd;
                          central differences on a sparse GQA case.
+  ivf_build / ivf_search  (faiss, the reference's IVF dependency, is absent: no fixtures.) Every
+  / ivf_route            list probed and search_k = nb reduces the search to brute-force top_c
+                         of <q̄_i, μ_j> over j <= i; a hand-built case where the search_k cut
+                         holds only future blocks (filtering before the cut would select past
+                         ones); full budget -> all causal blocks; planted well-separated
+                         clusters are recovered exactly; the final lists partition the blocks,
+                         ascending, each member at its argmax centroid; Jaccard >= 0.6 against
+                         the flat router on the clustered geometry of the reference's own test.
 """
 from __future__ import annotations
 
@@ -455,3 +463,104 @@ def masked_grads(q, k, v, sel, g, block, scale=None):
                 dk[b, h // G, keys] += scale * np.outer(ds, qi)
                 dv[b, h // G, keys] += np.outer(p, gi)
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------------------------
+# f4: IVF router over block means (the faiss-free restatement of ssa/ivf_kernel.py:63-119)
+# ---------------------------------------------------------------------------------------------
+
+
+def ivf_nlist(nb: int) -> int:
+    """Default list count of build_ivf (ssa/ivf_kernel.py:66): min(nb, max(4, floor(sqrt nb)))."""
+    return min(nb, max(4, int(nb ** 0.5)))
+
+
+def _dot_seq(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """(R, d) x (C, d) float32 -> (R, C) float32: each <a_r, b_c> accumulated in float64 in
+    dimension order (a product of two float32 values is exact in float64, so every step rounds
+    once, as an fma does) and rounded once to float32."""
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    acc = np.zeros((a.shape[0], b.shape[0]))
+    for t in range(a.shape[1]):
+        acc = acc + np.outer(a64[:, t], b64[:, t])
+    return acc.astype(np.float32)
+
+
+def ivf_keys(score: np.ndarray, idx) -> np.ndarray:
+    """Unique uint64 ordering keys: larger score first, then the lower index."""
+    idx = np.broadcast_to(np.asarray(idx, dtype=np.uint64), score.shape)
+    return (score_keys(score).astype(np.uint64) << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+
+
+def _normalised(s64: np.ndarray) -> np.ndarray:
+    """fl32(s / sqrt(sum_t s_t^2)) with the squares summed in dimension order; s when zero."""
+    nrm = np.add.accumulate(s64 * s64)[-1]
+    return (s64 / np.sqrt(nrm) if nrm > 0 else s64).astype(np.float32)
+
+
+def ivf_build(mu: np.ndarray, nlist: int, niter: int = 10):
+    """One head's IVF index over its key-block means (build_ivf = faiss train + add,
+    ssa/ivf_kernel.py:63-69; faiss clusters an inner-product IVF with spherical k-means).
+    mu (nb, d) float32 -> (centroids (nlist, d) float32, lists: nlist ascending int64 arrays).
+    Centroid c starts at the normalised mu[c * nb // nlist]; each of niter rounds assigns every
+    block mean to its largest-<mu_j, c> centroid (ties to the lower c) and sets each centroid with
+    members to the normalised float64 sum of its members in ascending order; a last assignment
+    fills the lists. (faiss starts from a random sample and splits empty clusters; both choices
+    here are deterministic instead.)"""
+    nb, d = mu.shape
+    m64 = mu.astype(np.float64)
+    cent = np.stack([_normalised(m64[(c * nb) // nlist]) for c in range(nlist)])
+    for it in range(niter + 1):
+        a = ivf_keys(_dot_seq(mu, cent), np.arange(nlist)[None, :]).argmax(1)
+        if it == niter:
+            break
+        for c in range(nlist):
+            mem = np.nonzero(a == c)[0]
+            if len(mem):
+                s = np.add.accumulate(m64[mem], axis=0)[-1]
+                if np.add.accumulate(s * s)[-1] > 0:
+                    cent[c] = _normalised(s)
+    return cent, [np.nonzero(a == c)[0] for c in range(nlist)]
+
+
+def ivf_search(qb: np.ndarray, mu: np.ndarray, cent: np.ndarray, lists, nprobe: int,
+               search_k: int, top_c: int, local: int):
+    """_route_head of ssa/ivf_kernel.py:72-99 for one head: per query block i, the
+    min(nprobe, nlist) lists of largest <qb_i, c>, the min(search_k, nb) members of those lists
+    of largest <qb_i, mu_j> (faiss's search, :82), the first top_c of them in that order with
+    j <= i (:84-85), OR blocks i-local..i (:87-89), deduplicated and ascending (:90-95).
+    qb, mu (nb, d) float32 -> list of nb ascending block lists."""
+    nb = mu.shape[0]
+    nlist = cent.shape[0]
+    npb, sk = min(nprobe, nlist), min(search_k, nb)
+    ck = ivf_keys(_dot_seq(qb, cent), np.arange(nlist)[None, :])
+    fine = _dot_seq(qb, mu)
+    out = []
+    for i in range(nb):
+        probes = np.argsort(ck[i])[::-1][:npb]
+        cand = np.concatenate([lists[c] for c in probes]).astype(np.int64)
+        top = cand[np.argsort(ivf_keys(fine[i, cand], cand))[::-1][:sk]]
+        hits = top[top <= i][:max(top_c, 0)]
+        out.append(sorted(set(hits.tolist()) | set(range(max(0, i - local), i + 1))))
+    return out
+
+
+def ivf_route(qb: np.ndarray, mu: np.ndarray, top_c=8, local=1, nprobe=4, search_k=None,
+              nlist=None, niter=10):
+    """ivf_route (ssa/ivf_kernel.py:102-119) over block means: qb, mu (B, H, nb, d) ->
+    (lists (B, H, nb) of ascending block lists, centroids (B, H, nlist, d), inverted lists)."""
+    B, H, nb, d = mu.shape
+    nlist = ivf_nlist(nb) if nlist is None else nlist
+    search_k = min(2 * top_c, nb) if search_k is None else search_k
+    sel = np.empty((B, H, nb), dtype=object)
+    cents = np.zeros((B, H, nlist, d), dtype=np.float32)
+    inv = {}
+    for b in range(B):
+        for h in range(H):
+            cent, lists = ivf_build(mu[b, h], nlist, niter)
+            cents[b, h] = cent
+            inv[b, h] = lists
+            for i, s in enumerate(ivf_search(qb[b, h], mu[b, h], cent, lists, nprobe, search_k,
+                                             top_c, local)):
+                sel[b, h, i] = s
+    return sel, cents, inv

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
@@ -48,6 +48,9 @@ _SIGNATURES = {
                           _c_i64, _c_p, _c_sz, _c_p]),
     "ssa_project_rows": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "ssa_expand_selection": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "ssa_ivf_index_size": (_c_sz, [_c_i64] * 4),
+    "ssa_ivf_build": (_c_int, [_c_p] + [_c_i64] * 5 + [_c_p, _c_sz, _c_p]),
+    "ssa_ivf_route": (_c_int, [_c_p, _c_p, _c_p] + [_c_i64] * 8 + [_c_p, _c_p, _c_i64, _c_p]),
     "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ssa_masked_attn_fwd": (_c_int, [_c_p] * 5 + [_c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),

@@ -78,6 +78,27 @@ def test_invalid_arguments_are_rejected():
     assert b"outside the cache" in _lib.lib().ssa_last_error()
 
 
+def test_ivf_arguments_are_rejected():
+    fake = ctypes.c_void_p(1 << 20)
+    # index size grows with every dimension; zero for an empty shape
+    assert _lib.query("ssa_ivf_index_size", 1, 1024, 32, 64) > 32 * 64 * 4 + 1024 * 4
+    assert _lib.query("ssa_ivf_index_size", 0, 1024, 32, 64) == 0
+    # d not a multiple of 32, nlist above nb, a small index buffer
+    assert _status("ssa_ivf_build", fake, 1, 64, 48, 8, 10, fake, 1 << 30, None) == \
+        _lib.SSA_ERR_UNSUPPORTED
+    assert _status("ssa_ivf_build", fake, 1, 64, 64, 65, 10, fake, 1 << 30, None) == \
+        _lib.SSA_ERR_UNSUPPORTED
+    assert _status("ssa_ivf_build", fake, 1, 64, 64, 8, 10, fake, 64, None) == \
+        _lib.SSA_ERR_WORKSPACE
+    # route: search_k above 1024, the window above the LDS union, W too small
+    args = lambda sk, top_c, local, W: (fake, fake, fake, 1, 4096, 64, 64, 4, sk, top_c, local,
+                                        fake, fake, W, None)
+    assert _status("ssa_ivf_route", *args(2048, 8, 1, 10)) == _lib.SSA_ERR_UNSUPPORTED
+    assert _status("ssa_ivf_route", *args(1024, 1024, 2000, 4096)) == _lib.SSA_ERR_UNSUPPORTED
+    assert _status("ssa_ivf_route", *args(16, 8, 1, 9)) == _lib.SSA_ERR_INVALID
+    assert b"W=9" in _lib.lib().ssa_last_error()
+
+
 def test_route_width():
     w = lambda *a: _lib.query("ssa_route_width", *a)  # noqa: E731
     # budget, top_c=64, local=2, 1024 blocks -> 64 + 3
