@@ -35,6 +35,7 @@ METRIC = "routed prefill tokens/s @128K (Qwen-0.5B shape); decode ms/step @1M ct
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 PEAK_FP64_TFLOPS = 78.6
+IVF_NPROBE = 4          # build_ivf's default (ssa/ivf_kernel.py:63)
 TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
 
 
@@ -230,6 +231,7 @@ def main():
     import torch
 
     from ssa_amd import ivf_decode as D
+    from ssa_amd import ivf_kernel as IV
     from ssa_amd import ssa_kernel as K
     from ssa_amd import workloads as WL
 
@@ -418,6 +420,7 @@ def main():
         d5 = WL.make_c5_device(dev)
         c5 = d5["cfg"]
         q5, k5, v5 = d5["q"], d5["k"], d5["v"]
+        nb5 = c5.n // c5.block
         t5 = Timer(torch)
         for rep in range(4):
             tmr = t5 if rep else Timer(torch)
@@ -427,7 +430,25 @@ def main():
                                c5.local, 0.5 * c5.beta)
             vt5 = tmr.run("transpose_v", K.transpose_v, v5, c5.block)
             tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block, vt=vt5)
+            # the IVF router (sub-linear, approximate) on the same summaries, and the attention
+            # over its lists
+            idx5 = tmr.run("ivf_build", IV.build_ivf, mu5.view(1, nb5, c5.d), None, IVF_NPROBE)
+            ivn, ivi = tmr.run("ivf_route", IV.search, idx5, qb5.view(1, nb5, c5.d), c5.top_c,
+                               c5.local, IVF_NPROBE, 2 * c5.top_c)
+            ivn4, ivi4 = ivn.view(1, 1, nb5), ivi.view(1, 1, nb5, -1)
+            tmr.run("ivf_attention", K.sparse_attention, q5, k5, v5, ivn4, ivi4, c5.block, vt=vt5)
         torch.cuda.synchronize()
+        rows5 = np.linspace(c5.top_c, nb5 - 1, 256).astype(np.int64)
+        kn_h, ki_h = kn5[0, 0].cpu().numpy(), ki5[0, 0].cpu().numpy()
+        ivn_h, ivi_h = ivn[0].cpu().numpy(), ivi[0].cpu().numpy()
+        jac5 = []
+        for i in rows5:
+            a = set(ki_h[i, :kn_h[i]].tolist())
+            b = set(ivi_h[i, :ivn_h[i]].tolist())
+            jac5.append(len(a & b) / max(1, len(a | b)))
+        ivf_router = (t5.mean_ms("summaries") + t5.mean_ms("summaries_k") +
+                      t5.mean_ms("ivf_build") + t5.mean_ms("ivf_route"))
+        ivf_total = ivf_router + t5.mean_ms("transpose_v") + t5.mean_ms("ivf_attention")
         router = t5.mean_ms("summaries") + t5.mean_ms("summaries_k") + t5.mean_ms("route")
         attn = t5.mean_ms("transpose_v") + t5.mean_ms("attention")
         kv5 = int(kn5.sum().item())
@@ -440,8 +461,19 @@ def main():
             "route_ms": t5.mean_ms("route"), "attention_kernel_ms": t5.mean_ms("attention"),
             "attention_tflops": 4.0 * c5.block * c5.block * c5.d * kv5 / (t5.mean_ms("attention") / 1e3) / 1e12,
             "sum_kv_num": kv5,
+            "ivf": {
+                "router": f"IVF over the 49152 key-block means: nlist {idx5.nlist} lists by "
+                          f"10 rounds of spherical k-means, nprobe {IVF_NPROBE}, search_k "
+                          f"{2 * c5.top_c}, top_c {c5.top_c} + local {c5.local}",
+                "build_ms": t5.mean_ms("ivf_build"), "route_ms": t5.mean_ms("ivf_route"),
+                "router_ms": ivf_router, "attention_kernel_ms": t5.mean_ms("ivf_attention"),
+                "total_ms": ivf_total, "tokens_per_s": c5.n / (ivf_total / 1e3),
+                "router_speedup_vs_flat": router / ivf_router,
+                "sum_kv_num": int(ivn.sum().item()),
+                "jaccard_vs_flat_256_rows": float(np.mean(jac5)),
+            },
         }
-        del q5, k5, v5, d5, vt5
+        del q5, k5, v5, d5, vt5, idx5
         torch.cuda.empty_cache()
 
     if args.calibrate_copy:

@@ -166,7 +166,8 @@ int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t r
  *   lists. The index buffer (ssa_ivf_index_size bytes, 256-byte aligned) starts with, each
  *   region 256-byte aligned: centroids (BH, nlist, d) fp32; list sizes (BH, nlist) int32; list
  *   offsets (BH, nlist + 1) int32; member block ids (BH, nb) int32, list by list, ascending
- *   within a list; then scratch of the build.
+ *   within a list; then the build's copies for the route (transposed centroids, the block
+ *   means list by list) and its scratch. The route reads only the index and qb.
  * ssa_ivf_route (_route_head, :72-99): per query block i, the min(nprobe, nlist) lists of
  *   largest <qb_i, centroid>, the min(search_k, nb) members of those lists of largest
  *   <qb_i, mu_j> (at most 1024), of these the top_c largest with j <= i, OR blocks
@@ -180,10 +181,9 @@ size_t ssa_ivf_index_size(int64_t BH, int64_t nb, int64_t nlist, int64_t d);
 int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d, int64_t nlist,
                   int64_t niter, void* index, size_t index_bytes, ssa_stream_t stream);
 
-int ssa_ivf_route(const void* index, const float* mu, const float* qb, int64_t BH, int64_t nb,
-                  int64_t d, int64_t nlist, int64_t nprobe, int64_t search_k, int64_t top_c,
-                  int64_t local, int32_t* kv_num, int32_t* kv_idx, int64_t W,
-                  ssa_stream_t stream);
+int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t nb, int64_t d,
+                  int64_t nlist, int64_t nprobe, int64_t search_k, int64_t top_c, int64_t local,
+                  int32_t* kv_num, int32_t* kv_idx, int64_t W, ssa_stream_t stream);
 
 /*
  * Block-sparse causal attention forward (replaces FlexAttention with

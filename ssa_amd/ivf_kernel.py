@@ -86,9 +86,7 @@ def build_ivf(mu: torch.Tensor, nlist: int | None = None, nprobe: int = 4, res=N
     buf = torch.empty(size, device=mu.device, dtype=torch.uint8)
     _lib.call("ssa_ivf_build", mu3.data_ptr(), BH, nb, d, nlist, int(niter), buf.data_ptr(), size,
               _lib.stream_of(mu3))
-    idx = IVFIndex(buf, BH, nb, nlist, d, min(int(nprobe), nlist))
-    idx.mu = mu3                     # the route reads the members' block means
-    return idx
+    return IVFIndex(buf, BH, nb, nlist, d, min(int(nprobe), nlist))
 
 
 def search(index: IVFIndex, qb: torch.Tensor, top_c: int = 8, local: int = 1,
@@ -103,9 +101,9 @@ def search(index: IVFIndex, qb: torch.Tensor, top_c: int = 8, local: int = 1,
     W = min(top_c + local + 1, nb)
     kv_num = torch.empty(index.BH, nb, device=qb.device, dtype=torch.int32)
     kv_idx = torch.empty(index.BH, nb, W, device=qb.device, dtype=torch.int32)
-    _lib.call("ssa_ivf_route", index.buf.data_ptr(), index.mu.data_ptr(), qb.data_ptr(),
-              index.BH, nb, index.d, index.nlist, nprobe, search_k, int(top_c), int(local),
-              kv_num.data_ptr(), kv_idx.data_ptr(), W, _lib.stream_of(qb))
+    _lib.call("ssa_ivf_route", index.buf.data_ptr(), qb.data_ptr(), index.BH, nb, index.d,
+              index.nlist, nprobe, search_k, int(top_c), int(local), kv_num.data_ptr(),
+              kv_idx.data_ptr(), W, _lib.stream_of(qb))
     return kv_num, kv_idx
 
 
