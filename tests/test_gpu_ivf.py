@@ -37,6 +37,7 @@ BUILD_CASES = [  # (BH, nb, d, nlist, niter)
     (3, 1000, 128, 31, 10),
     (1, 40, 64, 40, 4),
     (2, 513, 256, 5, 6),
+    (3, 1, 64, 1, 10),                   # one block per head
 ]
 
 
@@ -65,6 +66,8 @@ ROUTE_CASES = [  # (nb, d, nlist, nprobe, search_k, top_c, local)
     (200, 64, 12, 3, 40, 0, 1),          # top_c = 0: the local window only
     (257, 128, 16, 5, 1024, 300, 3),     # search_k above nb, top_c above search_k
     (4096, 64, 8, 8, 64, 16, 1),         # 4096 candidates: two passes through LDS
+    (1, 64, 1, 4, 8, 8, 1),              # one block: the own block only
+    (5, 32, 4, 2, 1, 1, 0),              # search_k 1, no local window
 ]
 
 
