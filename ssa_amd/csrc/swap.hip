@@ -863,10 +863,11 @@ __global__ __launch_bounds__(256) void swap_dq16_kernel(SwapArgs a) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
+__global__ __launch_bounds__(256, 2) void swap_dkdv16_kernel(SwapArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * 64 * kRS16 * 2 + 2 * 64 * kTS16 * 2];
   static_assert(2 * 64 * kRS16 * 2 + 2 * 64 * kTS16 * 2 >= 2 * 32 * 128 * 4, "merge buffers");
   __shared__ float lse_s[64], del_s[64];
+  __shared__ unsigned long long act_s[4];
   unsigned short* qs = reinterpret_cast<unsigned short*>(smem);  // Q [q][d]
   unsigned short* gs = qs + 64 * kRS16;                          // dO [q][d]
   unsigned short* qtT = gs + 64 * kRS16;                         // Q [d][q]
@@ -897,14 +898,40 @@ __global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
     const int64_t hq = kvh * a.G + g, bh = b * a.Hq + hq;
     const char* qb = a.q + (b * a.qsb + hq * a.qsh) * 2;
     const char* gb = a.dout + (b * a.osb + hq * a.osh) * 2;
-    for (int64_t qt = k0 / 64; qt < a.nqt; ++qt) {
+    // the query tiles with a selected (row, key) pair in this key tile, in order, from a bitmap
+    // of 256 tiles that the workgroup's threads evaluate together
+    int64_t chunk = -1;
+    auto next_active = [&](int64_t qt) {
+      while (qt < a.nqt) {
+        const int64_t c0 = qt & ~int64_t(255);
+        if (c0 != chunk) {  // uniform: every thread walks the same tiles
+          const int64_t t = c0 + tid;
+          bool on = false;
+          if (t >= k0 / 64 && t < a.nqt) {
+            unsigned long long any, unused;
+            tile_bits(a.masks + (bh * a.nqt + t) * a.nb, k0, a.block, a.nb, -1, any, unused);
+            on = any != 0ull;
+          }
+          const unsigned long long bal = __ballot(on);
+          __syncthreads();  // the previous chunk's bitmap is no longer read
+          if (lane == 0) act_s[w] = bal;
+          __syncthreads();
+          chunk = c0;
+        }
+        const int r = (int)(qt - c0);
+        const unsigned long long rest = act_s[r >> 6] & (~0ull << (r & 63));
+        if (rest != 0ull) return c0 + (r & ~63) + (int64_t)__builtin_ctzll(rest);
+        qt = c0 + (r & ~63) + 64;  // no active tile left in this 64-tile word
+      }
+      return a.nqt;
+    };
+    int64_t qt = next_active(k0 / 64);
+    while (qt < a.nqt) {
+      const int64_t nxt = next_active(qt + 1);
       const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
-      unsigned long long any, unused;
-      tile_bits(mrow, k0, a.block, a.nb, -1, any, unused);
-      if (any == 0ull) continue;
       const unsigned long long mw = kvalid ? mrow[ck] : 0ull;
       const int64_t q0 = qt * 64;
-      __syncthreads();
+      __syncthreads();  // the previous tile's compute is done with the LDS tiles
       stage16(qb, a.qsn, q0, a.n, qs, qtT, tid);
       stage16(gb, a.osn, q0, a.n, gs, gtT, tid);
       if (tid < 64) {
@@ -943,6 +970,7 @@ __global__ __launch_bounds__(256) void swap_dkdv16_kernel(SwapArgs a) {
         dka[dh] = Mma16<DT>::mma(lds_pair(qtT + off), d0, dka[dh]);
         dka[dh] = Mma16<DT>::mma(lds_pair(qtT + off + 16), d1, dka[dh]);
       }
+      qt = nxt;
     }
   }
   __syncthreads();
