@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void swap_fwd_kernel(SwapArgs a) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void swap_dq_kernel(SwapArgs a) {
+__global__ __launch_bounds__(256, 2) void swap_dq_kernel(SwapArgs a) {
   __shared__ float ks[kTileFloats];   // K [key][d]
   __shared__ float vs[kTileFloats];   // V [key][d]
   __shared__ float kt_[kTileFloats];  // K [d][key]
@@ -450,13 +450,45 @@ __global__ __launch_bounds__(256) void swap_dq_kernel(SwapArgs a) {
     }
 }
 
+// The next query tile >= qt (in order) holding a selected (row, key) pair of key tile k0 for
+// head bh, or a.nqt. The workgroup's 256 threads test 256 tiles at a time into a bitmap in
+// LDS (act: 4 words; chunk: the first tile of the bitmap held, -1 at first), so a walk over
+// mostly unselected tiles costs one round of loads per 256 tiles. Called uniformly.
+__device__ inline int64_t next_active_tile(const SwapArgs& a, int64_t bh, int64_t k0, int64_t qt,
+                                           unsigned long long* act, int64_t& chunk) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  while (qt < a.nqt) {
+    const int64_t c0 = qt & ~int64_t(255);
+    if (c0 != chunk) {
+      const int64_t t = c0 + tid;
+      bool on = false;
+      if (t >= k0 / 64 && t < a.nqt) {
+        unsigned long long any, unused;
+        tile_bits(a.masks + (bh * a.nqt + t) * a.nb, k0, a.block, a.nb, -1, any, unused);
+        on = any != 0ull;
+      }
+      const unsigned long long bal = __ballot(on);
+      __syncthreads();  // the previous bitmap is no longer read
+      if (lane == 0) act[w] = bal;
+      __syncthreads();
+      chunk = c0;
+    }
+    const int r = (int)(qt - c0);
+    const unsigned long long rest = act[r >> 6] & (~0ull << (r & 63));
+    if (rest != 0ull) return c0 + (r & ~63) + (int64_t)__builtin_ctzll(rest);
+    qt = c0 + (r & ~63) + 64;  // no active tile left in this 64-tile word
+  }
+  return a.nqt;
+}
+
 template <int DT>
-__global__ __launch_bounds__(256) void swap_dkdv_kernel(SwapArgs a) {
+__global__ __launch_bounds__(256, 2) void swap_dkdv_kernel(SwapArgs a) {
   __shared__ float qs[kTileFloats];   // Q [q][d]
   __shared__ float gs[kTileFloats];   // dO [q][d]
   __shared__ float qtT[kTileFloats];  // Q [d][q]
   __shared__ float gtT[kTileFloats];  // dO [d][q]
   __shared__ float lse_s[64], del_s[64];
+  __shared__ unsigned long long act_s[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hi = lane >> 5, lo = lane & 31;
   const int kq = w & 1, qp = w >> 1;
   const int64_t nbkv = a.B * a.Hkv;
@@ -483,11 +515,10 @@ __global__ __launch_bounds__(256) void swap_dkdv_kernel(SwapArgs a) {
     const int64_t hq = kvh * a.G + g, bh = b * a.Hq + hq;
     const char* qb = a.q + (b * a.qsb + hq * a.qsh) * dtype_size_dev<DT>();
     const char* gb = a.dout + (b * a.osb + hq * a.osh) * dtype_size_dev<DT>();
-    for (int64_t qt = k0 / 64; qt < a.nqt; ++qt) {
+    int64_t chunk = -1;
+    for (int64_t qt = next_active_tile(a, bh, k0, k0 / 64, act_s, chunk); qt < a.nqt;
+         qt = next_active_tile(a, bh, k0, qt + 1, act_s, chunk)) {
       const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
-      unsigned long long any, unused;
-      tile_bits(mrow, k0, a.block, a.nb, -1, any, unused);
-      if (any == 0ull) continue;
       const unsigned long long mw = kvalid ? mrow[ck] : 0ull;
       const int64_t q0 = qt * 64;
       __syncthreads();
@@ -898,36 +929,10 @@ __global__ __launch_bounds__(256, 2) void swap_dkdv16_kernel(SwapArgs a) {
     const int64_t hq = kvh * a.G + g, bh = b * a.Hq + hq;
     const char* qb = a.q + (b * a.qsb + hq * a.qsh) * 2;
     const char* gb = a.dout + (b * a.osb + hq * a.osh) * 2;
-    // the query tiles with a selected (row, key) pair in this key tile, in order, from a bitmap
-    // of 256 tiles that the workgroup's threads evaluate together
     int64_t chunk = -1;
-    auto next_active = [&](int64_t qt) {
-      while (qt < a.nqt) {
-        const int64_t c0 = qt & ~int64_t(255);
-        if (c0 != chunk) {  // uniform: every thread walks the same tiles
-          const int64_t t = c0 + tid;
-          bool on = false;
-          if (t >= k0 / 64 && t < a.nqt) {
-            unsigned long long any, unused;
-            tile_bits(a.masks + (bh * a.nqt + t) * a.nb, k0, a.block, a.nb, -1, any, unused);
-            on = any != 0ull;
-          }
-          const unsigned long long bal = __ballot(on);
-          __syncthreads();  // the previous chunk's bitmap is no longer read
-          if (lane == 0) act_s[w] = bal;
-          __syncthreads();
-          chunk = c0;
-        }
-        const int r = (int)(qt - c0);
-        const unsigned long long rest = act_s[r >> 6] & (~0ull << (r & 63));
-        if (rest != 0ull) return c0 + (r & ~63) + (int64_t)__builtin_ctzll(rest);
-        qt = c0 + (r & ~63) + 64;  // no active tile left in this 64-tile word
-      }
-      return a.nqt;
-    };
-    int64_t qt = next_active(k0 / 64);
+    int64_t qt = next_active_tile(a, bh, k0, k0 / 64, act_s, chunk);
     while (qt < a.nqt) {
-      const int64_t nxt = next_active(qt + 1);
+      const int64_t nxt = next_active_tile(a, bh, k0, qt + 1, act_s, chunk);
       const unsigned long long* mrow = a.masks + (bh * a.nqt + qt) * a.nb;
       const unsigned long long mw = kvalid ? mrow[ck] : 0ull;
       const int64_t q0 = qt * 64;
