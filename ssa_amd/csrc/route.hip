@@ -890,7 +890,6 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     g.ni = nbq - i0 < chunk ? nbq - i0 : chunk;
     const int64_t R = g.G * g.ni;
     const int64_t row_tiles = (R + kTile - 1) / kTile;
-    const int64_t row_tiles2 = (R + 2 * kTile - 1) / (2 * kTile);  // 128-row tiles
     const int64_t imax = i0 + g.ni - 1;
     const int64_t cmax_all = row_cmax_s(g, imax);  // scored candidates (sub-block units)
     const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
@@ -917,9 +916,9 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
         route_score_kernel<true, kTile><<<grid, 256, 0, stream>>>(
             rows, mu, var, m3, g, (int)d, coef2, coef3, keys, row_tiles, cand_tiles);
       } else {
-        dim3 grid((unsigned)(row_tiles2 * cand_tiles), (unsigned)(B * Hkv));
-        route_score_kernel<false, 2 * kTile><<<grid, 256, 0, stream>>>(
-            rows, mu, var, m3, g, (int)d, coef2, coef3, keys, row_tiles2, cand_tiles);
+        dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
+        route_score_kernel<false, kTile><<<grid, 256, 0, stream>>>(
+            rows, mu, var, m3, g, (int)d, coef2, coef3, keys, row_tiles, cand_tiles);
       }
       SSA_TRY(launch_status("route_score_kernel"));
     }
