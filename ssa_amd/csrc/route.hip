@@ -357,13 +357,19 @@ __device__ inline void wave_select_top(const unsigned int (&key)[J], const bool 
     for (int j = 0; j < J; ++j) sel[j] = false;
     return;
   }
-  unsigned int T = 0u;  // largest T with #{keys >= T} >= K: the K-th largest key
+  // T: the largest value with #{keys >= T} >= K (the K-th largest key), or the first prefix
+  // found with exactly K keys >= T -- then no tie straddles the cut, and the tie step below
+  // takes every key equal to T (none, or all of them)
+  unsigned int T = 0u;
   for (int bit = 31; bit >= 0; --bit) {
     const unsigned int t = T | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= t));
-    if (cnt >= K) T = t;
+    if (cnt >= K) {
+      T = t;
+      if (cnt == K) break;  // wave-uniform
+    }
   }
   int above = 0;
 #pragma unroll
