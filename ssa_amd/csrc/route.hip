@@ -404,7 +404,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   __shared__ unsigned int cidx[kCand];        // candidate block indices (filtered rows)
   __shared__ unsigned int hist[256];
   __shared__ int wave_sums[NT / 64];
-  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand;
+  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand, sh_whole;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
@@ -491,6 +491,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   } else if (K > 0) {
     unsigned int prefix = 0u, pmask = 0u;
     unsigned int kk = (unsigned int)K;  // rank of T among keys matching the prefix
+    bool whole = false;
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int t = tid; t < 256; t += NT) hist[t] = 0u;
       __syncthreads();
@@ -518,6 +519,7 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
           if (above < kk && kk <= above + v[j]) {
             sh_digit = (unsigned int)(4 * tid + j);
             sh_above = above;
+            sh_whole = kk == above + v[j];
           }
           above += v[j];
         }
@@ -526,11 +528,15 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
       prefix |= sh_digit << shift;
       pmask |= 0xffu << shift;
       kk -= sh_above;
+      whole = sh_whole != 0u;
       __syncthreads();
+      // the digit's whole bin is taken: exactly K keys are >= prefix (lower bits zero), so no
+      // tie straddles the cut and the remaining digits need not be resolved
+      if (whole) break;
     }
     const unsigned int T = prefix;
-    const unsigned int need_eq = kk;           // keys equal to T still to take
-    const unsigned int n_eq = hist[T & 255u];  // keys equal to T (all of them are >= T0)
+    const unsigned int need_eq = kk;                   // keys equal to T still to take
+    const unsigned int n_eq = whole ? kk : hist[T & 255u];  // keys equal to T (all >= T0)
     __syncthreads();
     if (need_eq == n_eq) {
       for (int64_t c = tid; c < nsel; c += NT)
