@@ -158,3 +158,58 @@ def test_ivf_route_rejects_oversized_search(cuda):
     index = I.build_ivf(mu)
     with pytest.raises(_lib.SSAError, match="exceeds 1024"):
         I.search(index, mu, top_c=8, local=1, search_k=2048)
+
+
+def test_ivf_c5_scale_properties_and_sampled_rows(cuda):
+    """The C5 router shape (49,152 key blocks, d 64, nlist 221, nprobe 4, search_k 128, top_c 64,
+    local 1): every list and every row checked for the contract's invariants on the device, and
+    sampled members / rows bit-exact against the oracle's assignment and search run on the
+    device's own centroids and lists."""
+    nb, d, top_c, local, nprobe, sk = 49152, 64, 64, 1, 4, 128
+    mu = _means(1, nb, d, 21, cuda, clustered=True)
+    qb = _means(1, nb, d, 22, cuda, clustered=True)
+    index = I.build_ivf(mu, None, nprobe)
+    kv_num, kv_idx = I.search(index, qb, top_c, local, nprobe, sk)
+    torch.cuda.synchronize()
+    nl = index.nlist
+    assert nl == 221
+    sizes, offs, ids = index.list_sizes[0], index.list_offsets[0], index.list_ids[0]
+    # the lists partition the blocks, each ascending
+    assert int(sizes.sum()) == nb and int(offs[-1]) == nb
+    assert torch.equal(torch.sort(ids.long()).values, torch.arange(nb, device=cuda))
+    lid = torch.repeat_interleave(torch.arange(nl, device=cuda), sizes.long())
+    step = ids[1:].long() - ids[:-1].long()
+    assert bool(((step > 0) | (lid[1:] != lid[:-1])).all())
+    # every row: own block kept, causal, ascending and unique, padded with 0
+    W = kv_idx.shape[-1]
+    kn, ki = kv_num[0].long(), kv_idx[0].long()
+    rows = torch.arange(nb, device=cuda)
+    pos = torch.arange(W, device=cuda)[None, :]
+    live = pos < kn[:, None]
+    assert bool((kn >= 1).all()) and bool((kn <= W).all())
+    assert bool(((ki <= rows[:, None]) | ~live).all())
+    assert bool(((ki == rows[:, None]) & live).any(1).all())
+    inc = (ki[:, 1:] > ki[:, :-1]) | ~live[:, 1:]
+    assert bool(inc.all())
+    assert bool(((ki == 0) | live).all())
+    # sampled members at their argmax centroid (oracle keys on the device centroids)
+    cent = np_of(index.centroids[0])
+    m, q = np_of(mu[0]), np_of(qb[0])
+    ids_h, offs_h = np_of(ids), np_of(offs)
+    member_list = np.repeat(np.arange(nl), np_of(sizes))
+    rng = np.random.default_rng(5)
+    pick = rng.choice(nb, 256, replace=False)
+    keys = O.ivf_keys(O._dot_seq(m[ids_h[pick]], cent), np.arange(nl)[None, :])
+    assert (keys.argmax(1) == member_list[pick]).all()
+    # sampled rows against the oracle's search over the device index
+    lists = [ids_h[offs_h[c]:offs_h[c + 1]].astype(np.int64) for c in range(nl)]
+    kn_h, ki_h = np_of(kv_num[0]), np_of(kv_idx[0])
+    for i in list(rng.choice(nb, 24, replace=False)) + [0, 1, 65, nb - 1]:
+        ck = O.ivf_keys(O._dot_seq(q[i:i + 1], cent)[0], np.arange(nl))
+        probes = np.argsort(ck)[::-1][:nprobe]
+        cand = np.concatenate([lists[c] for c in probes])
+        fine = O._dot_seq(q[i:i + 1], m[cand])[0]
+        top = cand[np.argsort(O.ivf_keys(fine, cand))[::-1][:sk]]
+        hits = top[top <= i][:top_c]
+        want = sorted(set(hits.tolist()) | set(range(max(0, i - local), i + 1)))
+        assert ki_h[i, :kn_h[i]].tolist() == want, i
