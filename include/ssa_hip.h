@@ -168,7 +168,10 @@ int ssa_expand_selection(const int32_t* kv_num, const int32_t* kv_idx, int64_t r
  *   offsets (BH, nlist + 1) int32; member block ids (BH, nb) int32, list by list, ascending
  *   within a list; then the build's copies for the route (transposed centroids, the block
  *   means list by list) and its scratch. The route reads only the index and qb.
- * ssa_ivf_route (_route_head, :72-99): per query block i, the min(nprobe, nlist) lists of
+ * ssa_ivf_route (_route_head, :72-99): qb, kv_num and kv_idx hold BH * G query heads, query
+ *   head h searching index head h / G (G = 1: the reference's one index per head; G > 1: the
+ *   query heads of a key head share its index, as in grouped-query attention). Per query
+ *   block i, the min(nprobe, nlist) lists of
  *   largest <qb_i, centroid>, the min(search_k, nb) members of those lists of largest
  *   <qb_i, mu_j> (at most 1024), of these the top_c largest with j <= i, OR blocks
  *   i - local .. i; kv_num (BH, nb), kv_idx (BH, nb, W) ascending padded with 0,
@@ -181,9 +184,10 @@ size_t ssa_ivf_index_size(int64_t BH, int64_t nb, int64_t nlist, int64_t d);
 int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d, int64_t nlist,
                   int64_t niter, void* index, size_t index_bytes, ssa_stream_t stream);
 
-int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t nb, int64_t d,
-                  int64_t nlist, int64_t nprobe, int64_t search_k, int64_t top_c, int64_t local,
-                  int32_t* kv_num, int32_t* kv_idx, int64_t W, ssa_stream_t stream);
+int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int64_t nb,
+                  int64_t d, int64_t nlist, int64_t nprobe, int64_t search_k, int64_t top_c,
+                  int64_t local, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+                  ssa_stream_t stream);
 
 /*
  * Block-sparse causal attention forward (replaces FlexAttention with

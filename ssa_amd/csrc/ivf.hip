@@ -454,7 +454,7 @@ struct IvfRouteArgs {
   const int32_t* off;
   const int32_t* ids;
   const float* qb;
-  int64_t nb, d, nlist, nprobe, search_k, top_c, local, W;
+  int64_t nb, d, nlist, nprobe, search_k, top_c, local, W, G;
   int32_t* kv_num;
   int32_t* kv_idx;
 };
@@ -482,7 +482,7 @@ __device__ inline int block_compact(const T* v, int n, T* dst, int* ws, F take) 
   return total;
 }
 
-// One workgroup per (query block i, head bh).
+// One workgroup per (query block i, query head bh); query head bh searches index head bh / G.
 __global__ __launch_bounds__(256) void ivf_route_kernel(IvfRouteArgs a) {
   __shared__ unsigned long long buf[kIvfCap];
   __shared__ int lst[kIvfCap];         // probed lists, then the selected blocks and their union
@@ -492,13 +492,13 @@ __global__ __launch_bounds__(256) void ivf_route_kernel(IvfRouteArgs a) {
   __shared__ unsigned int shv[3];
   __shared__ int ws[4];
   const int tid = threadIdx.x;
-  const int64_t i = blockIdx.x, bh = blockIdx.y;
+  const int64_t i = blockIdx.x, bh = blockIdx.y, bk = bh / a.G;
   const int64_t nb = a.nb, d = a.d, nlist = a.nlist;
   for (int64_t t = tid; t < d; t += 256) qs[t] = a.qb[(bh * nb + i) * d + t];
   __syncthreads();
 
   // coarse search: the nprobe centroids of largest <qb_i, c>
-  const float* cT = a.centT + bh * d * nlist;
+  const float* cT = a.centT + bk * d * nlist;
   for (int64_t c = tid; c < nlist; c += 256) buf[c] = ivf_key(dot_strided(qs, cT + c, nlist, d), c);
   __syncthreads();
   unsigned long long T = 0ull;
@@ -518,9 +518,9 @@ __global__ __launch_bounds__(256) void ivf_route_kernel(IvfRouteArgs a) {
   }
   __syncthreads();
   // member prefix over the probed lists
-  const int32_t* cnt = a.count + bh * nlist;
-  const int32_t* off = a.off + bh * (nlist + 1);
-  const int32_t* ids = a.ids + bh * nb;
+  const int32_t* cnt = a.count + bk * nlist;
+  const int32_t* off = a.off + bk * (nlist + 1);
+  const int32_t* ids = a.ids + bk * nb;
   {
     int running = 0;
     for (int p0 = 0; p0 < nprobed; p0 += 256) {
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(256) void ivf_route_kernel(IvfRouteArgs a) {
   const int64_t M = aux[nprobed];
 
   // fine search: stream the members through buf, keeping the search_k largest keys
-  const float* mL = a.muL + bh * nb * d;
+  const float* mL = a.muL + bk * nb * d;
   int nk = 0;
   for (int64_t m0 = 0; m0 < M;) {
     const int room = kIvfCap - nk;
@@ -702,11 +702,13 @@ extern "C" int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d,
   return ssa::launch_status("ivf_transpose_cent_kernel");
 }
 
-extern "C" int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t nb,
-                             int64_t d, int64_t nlist, int64_t nprobe, int64_t search_k,
-                             int64_t top_c, int64_t local, int32_t* kv_num, int32_t* kv_idx,
-                             int64_t W, ssa_stream_t stream) {
+extern "C" int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G,
+                             int64_t nb, int64_t d, int64_t nlist, int64_t nprobe,
+                             int64_t search_k, int64_t top_c, int64_t local, int32_t* kv_num,
+                             int32_t* kv_idx, int64_t W, ssa_stream_t stream) {
   SSA_TRY(check_ivf_shape("ivf_route", qb, BH, nb, d, nlist));
+  SSA_REQUIRE(G >= 1 && BH * G <= 65535, SSA_ERR_INVALID,
+              "ivf_route: G=%lld must be >= 1 with BH * G <= 65535", (long long)G);
   SSA_REQUIRE(index != nullptr && (reinterpret_cast<uintptr_t>(index) & 255u) == 0,
               SSA_ERR_INVALID, "ivf_route: index must be a 256-byte aligned device pointer");
   SSA_REQUIRE(kv_num != nullptr && kv_idx != nullptr, SSA_ERR_INVALID,
@@ -742,9 +744,10 @@ extern "C" int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int
   a.top_c = top_c;
   a.local = local;
   a.W = W;
+  a.G = G;
   a.kv_num = kv_num;
   a.kv_idx = kv_idx;
-  ssa::ivf_route_kernel<<<dim3((unsigned)nb, (unsigned)BH), 256, 0,
+  ssa::ivf_route_kernel<<<dim3((unsigned)nb, (unsigned)(BH * G)), 256, 0,
                           static_cast<hipStream_t>(stream)>>>(a);
   return ssa::launch_status("ivf_route_kernel");
 }

@@ -8,7 +8,8 @@ choices where faiss is not: spherical k-means starts from the evenly spaced bloc
 mu[c * nb / nlist] instead of a random sample, runs `niter` (default 10) rounds, and leaves a
 centroid without members where it is instead of splitting a large cluster; inner products are
 fp64-accumulated and ties go to the lower index. `res` (a faiss resources object) is accepted
-and ignored. Heads are batched: one build and one route call cover all B*H heads.
+and ignored. Heads are batched: one build and one route call cover all heads; with grouped
+query heads (Hq = G * Hkv) each key head's index serves its G query heads.
 """
 from __future__ import annotations
 
@@ -91,17 +92,23 @@ def build_ivf(mu: torch.Tensor, nlist: int | None = None, nprobe: int = 4, res=N
 
 def search(index: IVFIndex, qb: torch.Tensor, top_c: int = 8, local: int = 1,
            nprobe: int | None = None, search_k: int | None = None):
-    """Routes every query block of qb (BH, nb, d) through `index` (_route_head,
-    ssa/ivf_kernel.py:72-99) -> (kv_num (BH, nb), kv_idx (BH, nb, W)) int32."""
+    """Routes every query block of qb (BH * G, nb, d) through `index` (_route_head,
+    ssa/ivf_kernel.py:72-99) -> (kv_num (BH * G, nb), kv_idx (BH * G, nb, W)) int32. Query head
+    h searches index head h // G (G = 1: one index per head, as the reference builds)."""
     _lib.require_device(qb)
-    qb = qb.reshape(index.BH, index.nb, index.d).to(torch.float32).contiguous()
+    rows = qb.numel() // (index.nb * index.d)
+    if rows * index.nb * index.d != qb.numel() or rows % index.BH:
+        raise ValueError(f"search: qb {tuple(qb.shape)} is not (BH*G, {index.nb}, {index.d}) "
+                         f"for an index of BH={index.BH} heads")
+    G = rows // index.BH
+    qb = qb.reshape(rows, index.nb, index.d).to(torch.float32).contiguous()
     nb = index.nb
     nprobe = index.nprobe if nprobe is None else int(nprobe)
     search_k = min(2 * top_c, nb) if search_k is None else int(search_k)
     W = min(top_c + local + 1, nb)
-    kv_num = torch.empty(index.BH, nb, device=qb.device, dtype=torch.int32)
-    kv_idx = torch.empty(index.BH, nb, W, device=qb.device, dtype=torch.int32)
-    _lib.call("ssa_ivf_route", index.buf.data_ptr(), qb.data_ptr(), index.BH, nb, index.d,
+    kv_num = torch.empty(rows, nb, device=qb.device, dtype=torch.int32)
+    kv_idx = torch.empty(rows, nb, W, device=qb.device, dtype=torch.int32)
+    _lib.call("ssa_ivf_route", index.buf.data_ptr(), qb.data_ptr(), index.BH, G, nb, index.d,
               index.nlist, nprobe, search_k, int(top_c), int(local), kv_num.data_ptr(),
               kv_idx.data_ptr(), W, _lib.stream_of(qb))
     return kv_num, kv_idx
@@ -109,15 +116,18 @@ def search(index: IVFIndex, qb: torch.Tensor, top_c: int = 8, local: int = 1,
 
 def ivf_route(q, k, block=BLOCK, top_c=8, local=1, nprobe=4, search_k=None, res=None,
               nlist=None, niter=10):
-    """(B, H, n, d) q, k -> (kv_num (B, H, nb) int32, kv_idx (B, H, nb, W) int32) for the
-    block-sparse attention (ssa/ivf_kernel.py:102-119): one index per (b, h) over that head's key
-    block means, searched with its query block means; W = min(top_c + local + 1, nb)."""
+    """(B, Hq, n, d) q, (B, Hkv, n, d) k -> (kv_num (B, Hq, nb) int32, kv_idx (B, Hq, nb, W)
+    int32) for the block-sparse attention (ssa/ivf_kernel.py:102-119): one index per (b, key
+    head) over that head's key block means, searched with the query block means of each query
+    head it serves (Hq a multiple of Hkv; the reference has Hq = Hkv); W = min(top_c + local + 1,
+    nb)."""
     B, H, n, d = q.shape
-    if k.shape[:2] != (B, H) or k.shape[2] != n:
-        raise ValueError("ivf_route: q and k must share (B, H, n)")
+    Hkv = k.shape[1]
+    if k.shape[0] != B or k.shape[2] != n or H % Hkv:
+        raise ValueError("ivf_route: k must be (B, Hkv, n, d) with Hq a multiple of Hkv")
     nb = n // block
     qb = block_means(q, block).reshape(B * H, nb, d)
-    mu = block_means(k, block).reshape(B * H, nb, d)
+    mu = block_means(k, block).reshape(B * Hkv, nb, d)
     index = build_ivf(mu, nlist, nprobe, res, niter)
     kv_num, kv_idx = search(index, qb, top_c, local, nprobe,
                             min(2 * top_c, nb) if search_k is None else search_k)

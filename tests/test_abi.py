@@ -91,7 +91,7 @@ def test_ivf_arguments_are_rejected():
     assert _status("ssa_ivf_build", fake, 1, 64, 64, 8, 10, fake, 64, None) == \
         _lib.SSA_ERR_WORKSPACE
     # route: search_k above 1024, the window above the LDS union, W too small
-    args = lambda sk, top_c, local, W: (fake, fake, 1, 4096, 64, 64, 4, sk, top_c, local,
+    args = lambda sk, top_c, local, W: (fake, fake, 1, 1, 4096, 64, 64, 4, sk, top_c, local,
                                         fake, fake, W, None)
     assert _status("ssa_ivf_route", *args(2048, 8, 1, 10)) == _lib.SSA_ERR_UNSUPPORTED
     assert _status("ssa_ivf_route", *args(1024, 1024, 2000, 4096)) == _lib.SSA_ERR_UNSUPPORTED

@@ -94,6 +94,38 @@ def test_ivf_route_matches_oracle(cuda, case):
             assert (ki[h, i, kn[h, i]:] == 0).all()
 
 
+def test_ivf_grouped_query_heads_match_oracle(cuda):
+    """Hq = 7 * Hkv: each key head's index serves its 7 query heads (query head h -> index head
+    h // 7), every selection equal to the oracle search of that head's index."""
+    B, Hkv, G, nb, d = 1, 2, 7, 300, 64
+    mu = _means(B * Hkv, nb, d, 31, cuda, clustered=True)
+    qb = _means(B * Hkv * G, nb, d, 32, cuda, clustered=True)
+    index = I.build_ivf(mu, None, 4)
+    kv_num, kv_idx = I.search(index, qb, 8, 1, 4, 16)
+    torch.cuda.synchronize()
+    assert kv_num.shape == (B * Hkv * G, nb)
+    kn, ki, m, q = np_of(kv_num), np_of(kv_idx), np_of(mu), np_of(qb)
+    for hk in range(B * Hkv):
+        cent, lists = O.ivf_build(m[hk], index.nlist, 10)
+        for g in range(G):
+            h = hk * G + g
+            want = O.ivf_search(q[h], m[hk], cent, lists, 4, 16, 8, 1)
+            for i in range(nb):
+                assert ki[h, i, :kn[h, i]].tolist() == want[i], (h, i)
+    # the same through ivf_route on (B, Hq, n, d) / (B, Hkv, n, d) tensors
+    n = 8 * K.BLOCK
+    qt = torch.randn(1, 14, n, 64, device=cuda, dtype=torch.bfloat16)
+    kt = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.bfloat16)
+    kn2, ki2 = I.ivf_route(qt, kt, top_c=2, local=1)
+    assert kn2.shape == (1, 14, 8) and (kn2 >= 1).all()
+    # full budget with grouped heads: every causal block, i.e. dense causal attention over the
+    # key head of each query head
+    vt = torch.randn_like(kt)
+    out = I.ssa_flex_ivf(qt, kt, vt, top_c=8, local=8, nprobe=8, search_k=8)
+    ref = K.dense(qt, kt.repeat_interleave(7, 1).contiguous(), vt.repeat_interleave(7, 1).contiguous())
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2)
+
+
 def test_ivf_full_budget_matches_dense(cuda):
     """ssa/tests/test_ivf_kernel.py:29-42: exhaustive IVF (every causal block selectable) equals
     dense causal attention."""
