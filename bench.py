@@ -314,6 +314,26 @@ def main():
     }
     result["device"] = device_info(torch, dev)
 
+    # the IVF router (f4) at the headline shape, after the timed steps: each key head's index
+    # serves its 7 query heads; compared with the flat router's time above
+    ti = Timer(torch)
+    nb3 = cfg.n // blk
+    qb3 = K.block_summary(q, blk, "qmean").view(cfg.Hq, nb3, cfg.d)
+    mu3 = K.block_summary(k, blk, "pop")[0].view(cfg.Hkv, nb3, cfg.d)
+    for rep in range(4):
+        tmr = ti if rep else Timer(torch)
+        idx3 = tmr.run("ivf_build", IV.build_ivf, mu3, None, IVF_NPROBE)
+        tmr.run("ivf_route", IV.search, idx3, qb3, cfg.top_c, cfg.local, IVF_NPROBE,
+                2 * cfg.top_c)
+    torch.cuda.synchronize()
+    result["c3_ivf"] = {
+        "router": f"IVF over each key head's {nb3} block means: nlist {idx3.nlist}, nprobe "
+                  f"{IVF_NPROBE}, search_k {2 * cfg.top_c}, top_c {cfg.top_c} + local {cfg.local}",
+        "build_ms": ti.mean_ms("ivf_build"), "route_ms": ti.mean_ms("ivf_route"),
+        "flat_route_ms": parts["route"],
+    }
+    del idx3, qb3, mu3
+
     if not args.no_dense:
         log("bench: dense baselines")
         kr, vr = k.repeat_interleave(cfg.Hq // cfg.Hkv, dim=1), v.repeat_interleave(cfg.Hq // cfg.Hkv, dim=1)
