@@ -201,8 +201,9 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
  * The 16-bit paths read V transposed, (B, Hkv, d, n_pad) with n_pad = ceil(n/block)*block, from
  * the workspace (ssa_sparse_attn_workspace_size() bytes). flags = 0: the call first writes V^T
  * there itself; flags = SSA_ATTN_VT_READY: the workspace already holds V^T of this v (from
- * ssa_transpose_v), e.g. kept resident across calls. After V^T the workspace holds 8 bytes per
- * (b, kv head) of per-call state (the largest key norm, a flag), rewritten by every call, so
+ * ssa_transpose_v), e.g. kept resident across calls. After V^T the workspace holds per-call state
+ * (the largest squared key norm of every 64-key tile, one flag per (b, kv head)), rewritten by
+ * every call, so
  * calls sharing one workspace must not overlap. The fp32 path needs no workspace.
  */
 enum { SSA_ATTN_VT_READY = 1 };

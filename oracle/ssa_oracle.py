@@ -255,11 +255,22 @@ def route_flat(q, k, block, top_c=8, local=1, routing="cumulant"):
 
 
 def route_query(qrows, k, block, pos0, top_c=None, budget_frac=0.25, local=1, beta=2.0,
-                kv_len=None):
+                kv_len=None, edgeworth=False):
     """Per-query router of ssa/gemma_ssa.py:85-131: rows qrows (B,Hq,nq,d) at positions
-    pos0 + r over the complete blocks of k[:, :, :kv_len] -> (kv_num, kv_idx compact)."""
+    pos0 + r over the complete blocks of k[:, :, :kv_len] -> (kv_num, kv_idx compact).
+    `edgeworth` adds beta^2/6 <q^3, m3> to the score (ssa/gemma_ssa.py:101-102)."""
     kv_len = k.shape[2] if kv_len is None else kv_len
-    mu, var, _ = block_stats(k[:, :, :kv_len], block, "pop")
+    mu, var, m3 = block_stats(k[:, :, :kv_len], block, "pop")
+    r = scores(qrows, mu, var, 0.5 * beta, m3 if edgeworth else None, beta ** 2 / 6.0)
+    return compact(select_rows(r, "query", top_c, budget_frac, local, pos0, block))
+
+
+def route_query_summaries(qrows, mu, var, block, pos0, top_c=None, budget_frac=0.25, local=1,
+                          beta=2.0):
+    """route_query over precomputed population summaries mu, var (B, Hkv, nbk, d) of a cache
+    whose blocks complete at the rows' positions are final: the per-query router of
+    ssa/gemma_ssa.py:85-131 with the statistics computed once for several decode positions
+    (candidates are still only the blocks complete at each position)."""
     r = scores(qrows, mu, var, 0.5 * beta)
     return compact(select_rows(r, "query", top_c, budget_frac, local, pos0, block))
 

@@ -30,30 +30,47 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libssa_hip.so)")
 
 
-def compile_cmd(out: Path) -> list[str]:
-    return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-Wall", "-Wno-unused-function",
-        f"-I{INCLUDE}", f"-I{CSRC}",
-        *[str(CSRC / s) for s in SOURCES],
-        "-o", str(out),
-    ]
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wall", "-Wno-unused-function"]
+
+
+def compile_cmd(src: Path, obj: Path) -> list[str]:
+    return [hipcc(), f"--offload-arch={ARCH}", *FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src),
+            "-o", str(obj)]
+
+
+def _filtered(res) -> str:
+    return "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                     if "packed-fp32-ops" not in l)
 
 
 def build(verbose: bool = False) -> Path:
-    """Compiles every source into LIB (atomically replaced). Raises on a compiler error."""
+    """Compiles every source (in parallel, one object each) and links LIB (atomically replaced).
+    Raises on a compiler or linker error."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = ROOT / "_build" / f"obj{os.getpid()}"
+    objdir.mkdir(parents=True, exist_ok=True)
+    objs = [objdir / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [compile_cmd(CSRC / s, o) for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+        results = list(pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds))
+    msgs = [_filtered(r) for r in results]
+    for cmd, res, msg in zip(cmds, results, msgs):
+        if res.returncode != 0:
+            shutil.rmtree(objdir, ignore_errors=True)
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{msg}")
     tmp = LIB.with_name(LIB.name + f".tmp{os.getpid()}")
-    cmd = compile_cmd(tmp)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    msgs = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
-                     if "packed-fp32-ops" not in l)
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(link, capture_output=True, text=True)
+    shutil.rmtree(objdir, ignore_errors=True)
     if res.returncode != 0:
         if tmp.exists():
             tmp.unlink()
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{msgs}")
-    if verbose and msgs.strip():
-        print(msgs, file=sys.stderr)
+        raise RuntimeError(f"link failed ({res.returncode}):\n{' '.join(link)}\n{_filtered(res)}")
+    if verbose:
+        for m in msgs + [_filtered(res)]:
+            if m.strip():
+                print(m, file=sys.stderr)
     os.replace(tmp, LIB)
     return LIB
 

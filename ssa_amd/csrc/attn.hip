@@ -38,14 +38,26 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.0f;
-// Rows whose scores provably stay within +-kFastBound (log2 units) take the softmax without a
-// running max: 2^s neither overflows nor underflows fp32 / bf16 there.
-constexpr float kFastBound = 100.0f;
-// The key-norm bound is folded into kKeySlots partial maxima per key head, each on its own
-// 128-byte line (slot s of key head bk at s * round_up(B*Hkv, 32) + bk), so that the atomics of
-// thousands of workgroups do not queue on one address.
-constexpr int kKeySlots = 16;
-__host__ __device__ inline int64_t key_slot_stride(int64_t BH) { return (BH + 31) / 32 * 32; }
+// Rows whose scores provably stay within +-fast_bound<DT>() (log2 units) take the softmax without
+// a running max: P = 2^s is packed into the MFMA input type, so the bound must keep P inside that
+// type's range. fp16's largest finite value is 65504 < 2^16 and its smallest normal 2^-14: with
+// |s| < 15, P lies in (2^-15, 2^15), finite, and at worst one bit short of full precision at the
+// bottom. bf16 has fp32's exponent range; its bound is set by precision instead: the bounded path
+// pre-scales q by scale*log2e and rounds it to bf16 (relative error <= 2^-9 per element), which
+// moves a score by at most 2^-9 * |q| |k| scale log2e < 2^-9 * bound = 1/16 log2 unit at 32 (a
+// relative change of P of at most 4.4 %, typically ~0.5 % since the rounding errors of the 64
+// elements have random signs) -- the size of the query's own bf16 rounding. Rows beyond the bound
+// take the exact running-max path, whose scores are the fp32 products.
+constexpr float kFastBoundBf16 = 32.0f;
+constexpr float kFastBoundF16 = 15.0f;
+template <int DT>
+__device__ constexpr float fast_bound() {
+  return DT == SSA_F16 ? kFastBoundF16 : kFastBoundBf16;
+}
+// Key norms enter the bound per 64-key tile: tile t of key head bk holds the largest squared key
+// norm of rows 64t..64t+63 at tmax2[bk * ntile + t]. A workgroup bounds its scores with the tiles
+// it attends only, so its choice of path depends on no key it does not read (in particular on no
+// key after its query block).
 
 struct AttnParams {
   const char* q;
@@ -60,7 +72,8 @@ struct AttnParams {
   int64_t W;
   float scale_log2;
   float* lse;
-  const float* kmax2;  // kKeySlots partial maxima of the squared key norms (NULL: no bound)
+  const float* tmax2;  // per-tile maxima of the squared key norms (NULL: exact path only)
+  int64_t ntile;       // 64-key tiles per key head (n_pad / 64)
   int* unbounded;      // per (b, kv head): set by mode 1 when one of its workgroups is not bounded
   int64_t qsub;   // query sub-tiles per query block
   int64_t total;  // logical workgroups
@@ -143,17 +156,16 @@ struct Mfma<SSA_F16> {
 };
 
 // Key-norm bound of the attention call: the largest squared norm of key rows k0..k0+63 of one
-// key head (rows >= n count 0), folded into slot blockIdx.x % kKeySlots of key head (b, kvh) with
-// an unsigned atomicMax (non-negative floats order like their bit patterns; the slots are zeroed
-// by a fill launch first). The slot is read first and the atomic skipped when it already holds as
-// much: the value only grows, so a stale read can only cause a redundant atomic. 256 threads;
-// lanes 8r..8r+7 of a pass read row r's 8 16-byte chunks.
+// key head (rows >= n count 0) into its tile's slot; the first tile's workgroup also clears the
+// head's unbounded flag for the mode-1 launch. 256 threads; lanes 8r..8r+7 of a pass read row
+// r's 8 16-byte chunks.
 struct KeyNorm {
   const unsigned short* k;  // NULL: no key norms
   int64_t ksb, ksh, ksn;
   bool bf16;
-  float* kmax2;  // kKeySlots * key_slot_stride(B*Hkv) floats, zeroed before the launch
-  int64_t BH;    // B * Hkv
+  float* tmax2;    // (B*Hkv, ntile)
+  int* unbounded;  // (B*Hkv)
+  int64_t ntile;
 };
 
 __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t kvh,
@@ -184,11 +196,9 @@ __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t k
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   if (tid == 0) {
-    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    unsigned int* slot = reinterpret_cast<unsigned int*>(kn.kmax2) +
-                         (blockIdx.x % kKeySlots) * key_slot_stride(kn.BH) + b * Hkv + kvh;
-    const unsigned int mb = __float_as_uint(m);
-    if (mb > __atomic_load_n(slot, __ATOMIC_RELAXED)) atomicMax(slot, mb);
+    const int64_t bk = b * Hkv + kvh;
+    kn.tmax2[bk * kn.ntile + k0 / 64] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (k0 == 0) kn.unbounded[bk] = 0;
   }
 }
 
@@ -196,11 +206,6 @@ __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t k
 __global__ __launch_bounds__(256) void key_norm_max_kernel(KeyNorm kn, int64_t Hkv, int64_t n) {
   const int64_t bk = blockIdx.y;
   key_tile_norm_max(kn, bk / Hkv, bk % Hkv, Hkv, (int64_t)blockIdx.x * 64, n);
-}
-
-__global__ __launch_bounds__(256) void zero_floats_kernel(float* x, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    x[i] = 0.0f;
 }
 
 // V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n; with kn.k set, also the
@@ -429,16 +434,28 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     }
   }
 
-  // Bounded rows: when |q| |k|max scale log2e < kFastBound for every row of the wave, the scores
-  // (log2 units) lie in (-kFastBound, kFastBound), so P = 2^S needs no running max. Q is then
+  // Bounded rows: when |q| |k|max scale log2e < fast_bound<DT>() for every row of the wave, the
+  // scores (log2 units) lie in (-bound, bound), so P = 2^S needs no running max. Q is then
   // pre-scaled by scale log2e (rounded to the input type) and the softmax is exp2 of the raw
   // MFMA output; numerator and denominator share the implicit max 0.
   constexpr bool fast = MODE == 1;
   if constexpr (MODE != 0) {
     __shared__ int wg_bounded;
+    // largest squared key norm over the tiles this workgroup attends (its list's blocks, tiles
+    // starting at or before its last query row)
     float km2 = 0.0f;
-    for (int s = 0; s < kKeySlots; ++s)
-      km2 = fmaxf(km2, p.kmax2[s * key_slot_stride(p.B * p.Hkv) + b * p.Hkv + kvh]);
+    {
+      const float* tm = p.tmax2 + (b * p.Hkv + kvh) * p.ntile;
+      const int64_t tpb = p.block / 64;  // tiles per key block
+      for (int e = lane; e < cnt; e += 64) {
+        const int32_t c = list[e];
+        if (c < 0 || (int64_t)c >= p.nbq) continue;
+        for (int64_t t = 0; t < tpb; ++t)
+          if ((int64_t)c * p.block + t * 64 <= qmax) km2 = fmaxf(km2, tm[(int64_t)c * tpb + t]);
+      }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) km2 = fmaxf(km2, __shfl_xor(km2, off, 64));
+    }
     bool ok = true;
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
@@ -452,7 +469,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         }
       qn2 = pair_sum(qn2);
       const float qn = sqrtf(qn2);
-      ok = ok && (p.scale_log2 * qn * sqrtf(km2) < kFastBound) && (p.scale_log2 * qn < 1.0e4f);
+      ok = ok && (p.scale_log2 * qn * sqrtf(km2) < fast_bound<DT>()) && (p.scale_log2 * qn < 1.0e4f);
     }
     if (tid == 0) wg_bounded = 1;
     __syncthreads();
@@ -744,7 +761,7 @@ int launch_mfma(AttnParams& p, hipStream_t stream) {
   p.total = p.nbq * p.B * p.Hkv * p.G * p.qsub;
   const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
   SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-  if (p.kmax2 == nullptr) {
+  if (p.tmax2 == nullptr) {
     if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
     else sparse_attn_dma_kernel<DT, 2, 2, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
   } else if (b64) {
@@ -765,8 +782,9 @@ extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t H
   if (dtype == SSA_F32 || block <= 0) return 0;
   const int64_t n_pad = (n + block - 1) / block * block;
   const size_t vt = ((size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u + 255) / 256 * 256;
-  // V^T, then the key-norm slots (float) and one unbounded-workgroup flag (int) per key head
-  const size_t tail = (size_t)(ssa::kKeySlots * ssa::key_slot_stride(B * Hkv) + B * Hkv) * 4u;
+  // V^T, then the per-tile key-norm maxima (float) and one unbounded-workgroup flag (int) per
+  // key head
+  const size_t tail = (size_t)(B * Hkv * (n_pad / 64) + B * Hkv) * 4u;
   return vt + (tail + 255) / 256 * 256;
 }
 
@@ -842,7 +860,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.lse = lse;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  p.kmax2 = nullptr;
+  p.tmax2 = nullptr;
+  p.ntile = p.n_pad / 64;
   if (dtype == SSA_F32) {
     p.vt = nullptr;
     p.qsub = block / 64;
@@ -858,15 +877,13 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.vt = static_cast<const char*>(workspace);
   SSA_REQUIRE(B * Hkv < 65536 && p.n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "sparse_attn: grid too large");
-  // after V^T: the key-norm slots, then mode 1's unbounded flags
+  // after V^T: the per-tile key-norm maxima, then mode 1's unbounded flags (both written by the
+  // key-norm pass below, every entry every call)
   const size_t vt_bytes = ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
-  float* kmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
-  const int64_t slots = kKeySlots * key_slot_stride(B * Hkv);
-  const int64_t zn = slots + B * Hkv;  // int 0 and float 0 share their bits
-  zero_floats_kernel<<<(unsigned)std::min<int64_t>((zn + 255) / 256, 1024), 256, 0, st>>>(kmax2, zn);
-  SSA_TRY(launch_status("zero_floats_kernel"));
-  KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, kmax2,
-             B * Hkv};
+  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
+  int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
+  KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
+             unbounded, p.ntile};
   const dim3 tg((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv));
   if (flags & SSA_ATTN_VT_READY) {
     key_norm_max_kernel<<<tg, 256, 0, st>>>(kn, Hkv, n);
@@ -876,8 +893,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
                                            Hkv, n, p.n_pad, p.vsb, p.vsh, p.vsn, kn);
     SSA_TRY(launch_status("transpose_v_kernel"));
   }
-  p.kmax2 = kmax2;
-  p.unbounded = reinterpret_cast<int*>(kmax2 + slots);
+  p.tmax2 = tmax2;
+  p.unbounded = unbounded;
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, st);
   return launch_mfma<SSA_F16>(p, st);
 }

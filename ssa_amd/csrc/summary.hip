@@ -39,7 +39,8 @@ __device__ inline void reduce_columns(const double* red, double* colv, int d, in
   }
 }
 
-// grid (nb, B*H); each thread owns 8 consecutive columns (cv) of every rpp-th row of the block.
+// grid (nb, B*H); each thread owns 8 consecutive columns (cv) of every rpp-th row of the block
+// (rpp = 256 / (d/8) row groups; with d/8 not dividing 256 the last 256 % (d/8) threads idle).
 template <int DT>
 __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     const char* __restrict__ x, int64_t H, int d, int64_t sb, int64_t sh, int64_t sn,
@@ -58,6 +59,7 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   const int tid = threadIdx.x;
   const int cv = tid % ncv;
   const int r0 = tid / ncv;
+  const bool active = r0 < rpp;
 
   const int64_t start = c * block;
   int64_t end = start + block;
@@ -75,14 +77,15 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   double acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0;
-  for (int64_t r = start + r0; r < rend; r += rpp) {
+  for (int64_t r = start + r0; active && r < rend; r += rpp) {
     float v[8];
     load_row8<DT>(base + r * sn * ES, v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] += (double)v[j];
   }
+  if (active)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = acc[j];
+    for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = acc[j];
   __syncthreads();
   reduce_columns(red, colv, d, rpp, tid);
   __syncthreads();
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
   double a2[8], a3[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) a2[j] = a3[j] = 0.0;
-  for (int64_t r = start + r0; r < rend; r += rpp) {
+  for (int64_t r = start + r0; active && r < rend; r += rpp) {
     float v[8];
     load_row8<DT>(base + r * sn * ES, v);
 #pragma unroll
@@ -117,8 +120,9 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     }
   }
   if (var != nullptr) {
+    if (active)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = a2[j];
+      for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = a2[j];
     __syncthreads();
     reduce_columns(red, colv, d, rpp, tid);
     __syncthreads();
@@ -128,8 +132,9 @@ __global__ __launch_bounds__(kSumThreads) void block_summary_kernel(
     __syncthreads();
   }
   if (m3 != nullptr) {
+    if (active)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = a3[j];
+      for (int j = 0; j < 8; ++j) red[r0 * d + cv * 8 + j] = a3[j];
     __syncthreads();
     reduce_columns(red, colv, d, rpp, tid);
     __syncthreads();
@@ -178,8 +183,8 @@ int check_summary_args(const void* x, int dtype, int64_t B, int64_t H, int64_t n
   SSA_REQUIRE(B > 0 && H > 0 && n > 0 && block > 0, SSA_ERR_INVALID,
               "block_summary: B=%lld H=%lld n=%lld block=%lld must be positive", (long long)B,
               (long long)H, (long long)n, (long long)block);
-  SSA_REQUIRE(d % 8 == 0 && d >= 8 && d <= kMaxD && kSumThreads % (d / 8) == 0,
-              SSA_ERR_UNSUPPORTED, "block_summary: head_dim %lld unsupported (8..512, power of 2)",
+  SSA_REQUIRE(d % 8 == 0 && d >= 8 && d <= kMaxD, SSA_ERR_UNSUPPORTED,
+              "block_summary: head_dim %lld unsupported (a multiple of 8, 8..512)",
               (long long)d);
   const int64_t vec = dtype == SSA_F32 ? 4 : 8;  // elements per 16 bytes
   SSA_REQUIRE(aligned16(x) && sb % vec == 0 && sh % vec == 0 && sn % vec == 0,

@@ -66,13 +66,13 @@ def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
     return x[:, :, None, :, :].expand(b, h, n, s, d).reshape(b, h * n, s, d)
 
 
-NEG = -1e30
+NEG = float("-inf")  # additive mask value of a dropped key, as the reference's NEG
 
 
 def _router_rows(x):
     """Query rows as the router reads them: 16-bit types as they are (their fp32 values are
     exact), anything else as fp32."""
-    return x if x.dtype in (torch.float16, torch.bfloat16) else x.float()  # additive mask value of a dropped key (the reference's NEG)
+    return x if x.dtype in (torch.float16, torch.bfloat16) else x.float()
 
 
 def _block_stats(k: torch.Tensor, block: int):
@@ -206,14 +206,18 @@ def ssa_attention_forward(module, query, key, value, attention_mask=None, scalin
         pos0 = kv_len - q_len
     if pos0 + q_len > kv_len or pos0 < 0:
         raise ValueError("query positions exceed the key length")
-    mu, var, _ = block_summary(key, cfg.block, "pop", n_real=kv_len)
+    # the edgeworth (third-cumulant) term joins the score as in ssa/gemma_ssa.py:101-102; a
+    # dense call selects every causal block, so it needs no score terms beyond the first
+    edge = cfg.edgeworth and not is_dense
+    mu, var, m3 = block_summary(key, cfg.block, "pop", n_real=kv_len, with_m3=edge)
     rows = _router_rows(query)
     if is_dense:
         top_c, frac = nb_layer, 0.0
     else:
         top_c, frac = cfg.top_c, cfg.budget_frac
-    kv_num, kv_idx = route(rows, mu, var, None, "query", top_c, frac, cfg.local_w,
-                           0.5 * cfg.beta, 0.0, query_pos=pos0, block=cfg.block)
+    kv_num, kv_idx = route(rows, mu, var, m3 if edge else None, "query", top_c, frac,
+                           cfg.local_w, 0.5 * cfg.beta, cfg.beta ** 2 / 6.0 if edge else 0.0,
+                           query_pos=pos0, block=cfg.block)
     attend_rows(query, key, value, kv_num, kv_idx, pos0, cfg.block, scale=scaling,
                 out=out.transpose(1, 2))
     return out, None

@@ -150,8 +150,21 @@ class RoutedDecoder:
         _lib.require_device(q, k_new, v_new)
         if self.pos >= self.capacity:
             raise RuntimeError("KV cache is full")
+        for name, t, shape in (("q", q, (self.B, self.Hq, self.d)),
+                               ("k_new", k_new, (self.B, self.Hkv, self.d)),
+                               ("v_new", v_new, (self.B, self.Hkv, self.d))):
+            if t.dtype != self.dtype:
+                raise TypeError(f"step: {name} is {t.dtype}, the cache holds {self.dtype}")
+            if tuple(t.shape) != shape:
+                raise ValueError(f"step: {name} has shape {tuple(t.shape)}, expected {shape}")
+            if t.stride(-1) != 1:
+                raise ValueError(f"step: {name} needs a contiguous last dimension")
         if out is None:
             out = torch.empty(self.B, self.Hq, self.d, device=q.device, dtype=self.dtype)
+        elif (out.dtype != self.dtype or tuple(out.shape) != (self.B, self.Hq, self.d)
+              or out.stride(-1) != 1):
+            raise ValueError(f"step: out must be a ({self.B}, {self.Hq}, {self.d}) {self.dtype} "
+                             "tensor with a contiguous last dimension")
         kc, vc = self.kcache, self.vcache
         strides = _lib.i64_array([q.stride(0), q.stride(1), k_new.stride(0), k_new.stride(1),
                                   v_new.stride(0), v_new.stride(1), kc.stride(0), kc.stride(1),

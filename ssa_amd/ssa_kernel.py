@@ -164,7 +164,7 @@ def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
     dt = _lib.dtype_code(v.dtype)
     nbytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
     n_pad = -(-n // block) * block
-    # the whole attention workspace (V^T first, then the kernel's per-head key-norm slots),
+    # the whole attention workspace (V^T first, then the kernel's per-tile key-norm maxima),
     # returned as its V^T view
     ws = torch.empty(nbytes, device=v.device, dtype=torch.uint8)
     vt = ws[:B * Hkv * d * n_pad * v.element_size()].view(v.dtype).view(B, Hkv, d, n_pad)
@@ -203,14 +203,23 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
         scale = 1.0 / math.sqrt(d)
     kv_num = kv_num.to(torch.int32).contiguous()
     kv_idx = kv_idx.to(torch.int32).contiguous()
+    if d not in TILED_HEAD_DIMS or not (block == 64 or block % 128 == 0):
+        if return_lse:
+            raise NotImplementedError(f"sparse_attention: return_lse needs head_dim in "
+                                      f"{TILED_HEAD_DIMS} and block 64 or a multiple of 128, "
+                                      f"got head_dim {d}, block {block}")
+        return _sparse_attention_rows(q, k, v, kv_num, kv_idx, block, scale, out)
     lse = torch.empty(B, Hq, n, device=q.device, dtype=torch.float32) if return_lse else None
     dt = _lib.dtype_code(q.dtype)
     ws_bytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
     flags = 0
     if vt is not None and dt != _lib.F32:
+        n_pad = -(-n // block) * block
         room = vt.untyped_storage().nbytes() - vt.storage_offset() * vt.element_size()
-        if room < ws_bytes or not vt.is_contiguous():
-            raise ValueError("vt is not a V^T workspace for this v (use transpose_v(v, block))")
+        if (tuple(vt.shape) != (B, Hkv, d, n_pad) or vt.dtype != v.dtype or room < ws_bytes
+                or not vt.is_contiguous()):
+            raise ValueError(f"vt {tuple(vt.shape)} {vt.dtype} is not the V^T workspace of this v "
+                             f"(expected {(B, Hkv, d, n_pad)} {v.dtype} from transpose_v(v, {block}))")
         ws, flags = vt, _lib.ATTN_VT_READY
     else:
         ws = torch.empty(max(ws_bytes, 16), device=q.device, dtype=torch.uint8)
@@ -221,6 +230,32 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
               kv_idx.shape[-1], float(scale), _lib.ptr(lse), flags, ws.data_ptr(), ws_bytes,
               _lib.stream_of(q))
     return (out, lse) if return_lse else out
+
+
+# head dims the tiled MFMA prefill kernel serves (with block 64 or a multiple of 128); other
+# head dims and blocks take the per-row kernel
+TILED_HEAD_DIMS = (64,)
+_ROWS_WORKSPACE_LIMIT = 1 << 28
+
+
+def _sparse_attention_rows(q, k, v, kv_num, kv_idx, block, scale, out):
+    """The block-sparse prefill for head dims the tiled kernel does not serve: every query row of
+    query block i takes block i's list, and the per-row kernel (ssa_decode_attend) attends the
+    keys j <= t, j < n of those blocks -- the same mask_mod (kv <= q) & (kv < n). Query blocks
+    are processed in chunks so that the per-row partials stay within _ROWS_WORKSPACE_LIMIT."""
+    from .ivf_decode import attend_rows
+    B, Hq, n, d = q.shape
+    nb, W = kv_num.shape[-1], kv_idx.shape[-1]
+    per_row = B * Hq * W * (d + 2) * 4
+    chunk = max(1, _ROWS_WORKSPACE_LIMIT // (per_row * block))
+    for i0 in range(0, nb, chunk):
+        i1 = min(nb, i0 + chunk)
+        r0, r1 = i0 * block, min(n, i1 * block)
+        num = kv_num[:, :, i0:i1].repeat_interleave(block, dim=2)[:, :, :r1 - r0]
+        idx = kv_idx[:, :, i0:i1].repeat_interleave(block, dim=2)[:, :, :r1 - r0]
+        attend_rows(q[:, :, r0:r1], k, v, num, idx, r0, block, scale=scale,
+                    out=out[:, :, r0:r1])
+    return out
 
 
 # ---------------------------------------------------------------------------------------------

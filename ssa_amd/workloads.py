@@ -174,6 +174,21 @@ def make_c5_device(device="cuda", n: int | None = None):
     return {"cfg": cfg, "q": q, "k": k, "v": v, "needles": np.array(rec, dtype=np.int64)}
 
 
+def make_c5_prefix(n: int = 2_097_152, seed: int = 104, nneedle: int = 170):
+    """C5's geometry (1 head, fp16, d 64, block 256) on a host-drawn prefix for the router's
+    reference fixture: q, k, v (1, 1, n, 64) ~ N(0,1) from default_rng(seed), rounded to fp16,
+    with `nneedle` needles (C5's density: 1024 per 12.6M tokens) planted as in make_c5_device
+    (key = 3 * q_probe/|q_probe| at least one block before the probe's block, value one-hot)."""
+    cfg = C5
+    rng = np.random.default_rng(seed)
+    q = _normal(rng, (1, 1, n, cfg.d))
+    k = _normal(rng, (1, 1, n, cfg.d))
+    v = _normal(rng, (1, 1, n, cfg.d))
+    needles = _plant(q, k, v, rng, nneedle, 3.0, 1, cfg.block, 2, 4 * cfg.block)
+    q, k, v = (round_to(x, cfg.dtype) for x in (q, k, v))
+    return {"cfg": cfg, "q": q, "k": k, "v": v, "needles": needles}
+
+
 def make_decode(n_cache: int | None = None, steps: int = 64):
     """C4 decode inputs: a KV prefix of n_cache tokens (K from the segmented Gaussian mixture,
     V ~ N(0,1), 8 needles per key head planted for the decode queries) plus `steps` tokens to

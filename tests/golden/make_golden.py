@@ -11,7 +11,8 @@ as float32/float64) plus the sha256 of the inputs, which the tests regenerate fr
 seeded generators (ssa_amd.workloads / the seeds recorded here) and check against the hash.
 Reference functions used (ssa/ssa_kernel.py, ssa/gemma_ssa.py, ssa/ssa_swap.py):
   block_route_budget :61-119, block_route :37-58, ssa_flex :122-126,
-  _selection_mask :85-137, ssa_attention_forward :183-241 (impl="analytic"),
+  _selection_mask :85-137 (also over the full 1M-token C4 cache),
+  ssa_attention_forward :183-241 (impl="analytic", with and without edgeworth),
   ssa_masked :32-56 (forward and autograd backward).
 """
 from __future__ import annotations
@@ -140,33 +141,91 @@ def query_case(name, n_cache=65536, positions=(65535, 65600, 65663)):
     print(f"{name}: positions={positions} W={W} ({time.time() - t0:.1f}s)")
 
 
-def analytic_inputs(seed=11, b=1, hq=4, hkv=2, n=300, d=64):
-    rng = np.random.default_rng(seed)
-    q = rng.standard_normal((b, hq, n, d))
-    k = rng.standard_normal((b, hkv, n, d))
-    v = rng.standard_normal((b, hkv, n, d))
-    return q, k, v
-
-
-def analytic_case(name, budget_frac=0.5, block=64):
+def analytic_case(name, budget_frac=0.5, block=64, seed=11, skew=0.0, edgeworth=False):
     """ssa_attention_forward(impl='analytic') in float64: per-query routing + masked softmax,
-    GQA 2:1, n not a multiple of the block; prefill and a q_len=1 decode row."""
+    GQA 2:1, n not a multiple of the block; prefill and a q_len=1 decode row. With `edgeworth`
+    the third-cumulant term joins the per-query score (ssa/gemma_ssa.py:101-102); `skew` gives
+    the keys a skewed component so that the term changes selections."""
     _, RG = reference()
     from types import SimpleNamespace
-    q, k, v = analytic_inputs()
+    q, k, v = GU.analytic_inputs(seed, skew=skew)
     mod = SimpleNamespace(num_key_value_groups=q.shape[1] // k.shape[1], is_sliding=False,
                           scaling=0.125, layer_idx=0)
     RG.CFG = RG.SSAConfig(block=block, budget_frac=budget_frac, local_w=1, beta=2.0,
-                          impl="analytic")
+                          impl="analytic", edgeworth=edgeworth)
     tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
     with torch.no_grad():
         full, _ = RG.ssa_attention_forward(mod, tq, tk, tv, scaling=0.125)
         inc, _ = RG.ssa_attention_forward(mod, tq[:, :, -1:], tk, tv, scaling=0.125)
     np.savez_compressed(HERE / f"{name}.npz", out=full.numpy(), out_last=inc.numpy(),
                         inputs_sha256=np.array(sha(q, k, v)),
-                        meta=np.array(repr({"seed": 11, "block": block, "budget_frac": budget_frac,
-                                            "local_w": 1, "beta": 2.0, "scaling": 0.125})))
+                        meta=np.array(repr({"seed": seed, "skew": skew, "block": block,
+                                            "budget_frac": budget_frac, "local_w": 1,
+                                            "beta": 2.0, "scaling": 0.125,
+                                            "edgeworth": edgeworth})))
     print(f"{name}: out {tuple(full.shape)}")
+
+
+def query_1m_case(name, steps=GU.C4_1M_STEPS, ts=GU.C4_1M_TS):
+    """_selection_mask at q_len=1 in float32 over the FULL C4 decode cache: the 1,048,576-token
+    prefix of workloads.make_decode (the bench's decode workload) plus the appended tokens, at
+    decode steps t (position n_cache + t; t = 127 completes a block)."""
+    _, RG = reference()
+    p = WL.make_decode(steps=steps)
+    cfg = p["cfg"]
+    n = p["n_cache"]
+    G = cfg.Hq // cfg.Hkv
+    q = torch.from_numpy(p["q"])
+    k = torch.from_numpy(p["k"])
+    scfg = RG.SSAConfig(block=cfg.block, top_c=cfg.top_c, local_w=cfg.local, beta=cfg.beta)
+    lists = []
+    t0 = time.time()
+    with torch.no_grad():
+        for t in ts:
+            pos = n + t
+            m = RG._selection_mask(q[:, :, t:t + 1], repeat_kv(k[:, :, :pos + 1], G), scfg)
+            nb = -(-(pos + 1) // cfg.block)
+            first = m[0, :, 0, ::cfg.block][:, :nb]
+            lists.append([np.flatnonzero((first[h] == 0).numpy()).astype(np.int16)
+                          for h in range(cfg.Hq)])
+            del m
+    W = max(len(x) for row in lists for x in row)
+    kv_num = np.array([[len(x) for x in row] for row in lists], dtype=np.int16)
+    kv_idx = np.zeros((len(ts), cfg.Hq, W), dtype=np.int16)
+    for a, row in enumerate(lists):
+        for h, x in enumerate(row):
+            kv_idx[a, h, :len(x)] = x
+    np.savez_compressed(HERE / f"{name}.npz", kv_num=kv_num, kv_idx=kv_idx,
+                        steps=np.array(ts, dtype=np.int64),
+                        positions=np.array([n + t for t in ts], dtype=np.int64),
+                        inputs_sha256=np.array(sha(p["q"], p["k"])),
+                        meta=np.array(repr({"cfg": "C4", "n_cache": n, "decode_steps": steps,
+                                            "fn": "_selection_mask", "top_c": cfg.top_c,
+                                            "local_w": cfg.local})))
+    print(f"{name}: steps={ts} W={W} ({time.time() - t0:.1f}s)")
+
+
+def c5_prefix_case(name):
+    """block_route_budget at C5's geometry (fp16, block 256, top_c 64, local 1, beta 2) on a
+    2,097,152-token prefix (8192 blocks) drawn by workloads.make_c5_prefix: causality makes each
+    query block's selection independent of the tokens after it, so these rows are C5's rows on
+    these inputs."""
+    RK, _ = reference()
+    p = WL.make_c5_prefix()
+    cfg = p["cfg"]
+    q, k = torch.from_numpy(p["q"]), torch.from_numpy(p["k"])
+    t0 = time.time()
+    with torch.no_grad():
+        kv_num, kv_idx, _ = RK.block_route_budget(q.half(), k.half(), cfg.block, top_c=cfg.top_c,
+                                                  local=cfg.local, beta=cfg.beta)
+    kn, ki = compact_from_full(kv_num, kv_idx)
+    np.savez_compressed(HERE / f"{name}.npz", kv_num=kn, kv_idx=ki,
+                        inputs_sha256=np.array(sha(p["q"], p["k"])),
+                        meta=np.array(repr({"cfg": "C5 prefix", "n": p["q"].shape[2],
+                                            "dtype": "fp16", "block": cfg.block,
+                                            "top_c": cfg.top_c, "local": cfg.local,
+                                            "beta": cfg.beta})))
+    print(f"{name}: rows={kn.size} W={ki.shape[-1]} ({time.time() - t0:.1f}s)")
 
 
 def masked_case(name):
@@ -207,6 +266,10 @@ CASES = {
     "c4_query": lambda: query_case("c4_query"),
     "c1_flex_out": lambda: flex_case("c1_flex_out"),
     "analytic_gqa": lambda: analytic_case("analytic_gqa"),
+    "analytic_gqa_edgeworth": lambda: analytic_case("analytic_gqa_edgeworth", seed=12, skew=0.7,
+                                                    edgeworth=True),
+    "c4_query_1m": lambda: query_1m_case("c4_query_1m"),
+    "c5_prefix": lambda: c5_prefix_case("c5_prefix"),
     "swap_masked_b16": lambda: masked_case("swap_masked_b16"),
     "swap_masked_b64": lambda: masked_case("swap_masked_b64"),
 }

@@ -58,6 +58,20 @@ def test_block_summary_matches_oracle(cuda, dtype):
     assert ulp_diff(np_of(qb), O.qmean(x, 128)).max() <= 1
 
 
+@pytest.mark.parametrize("d", [24, 96, 200, 512])
+def test_block_summary_other_head_dims(cuda, d):
+    """Head dims whose 8-column groups do not divide the 256 threads (the last threads idle)."""
+    rng = np.random.default_rng(8)
+    x = WL.round_to(rng.standard_normal((1, 2, 700, d)).astype(np.float32) * 2 - 1, torch.bfloat16)
+    xt = dev(x, torch.bfloat16, cuda)
+    mu, var, m3 = K.block_summary(xt, 64, "pop", n_real=690, with_m3=True)
+    omu, ovar, om3 = O.block_stats(x, 64, "pop", n_real=690)
+    assert ulp_diff(np_of(mu), omu).max() <= 1
+    assert ulp_diff(np_of(var), ovar).max() <= 1
+    assert np.abs(np_of(m3) - om3).max() <= 1e-6 * np.abs(om3).max()
+    assert ulp_diff(np_of(K.block_summary(xt, 64, "qmean")), O.qmean(x, 64)).max() <= 1
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_block_summary_counts_zero_rows_past_n(cuda, dtype):
     """n_real > n: rows [n, n_real) count as zero rows (the zero padding ssa_swap applies before
@@ -267,6 +281,7 @@ def test_ssa_flex_c1_fp32_matches_reference_flexattention(cuda):
 
 
 @pytest.mark.parametrize("cfg_name,n,qblocks", [("C2", 8192, [0, 1, 5, 63, 127]),
+                                                ("C2", 32768, [0, 2, 100, 311, 511]),
                                                 ("C3", 131072, [0, 3, 64, 511, 1023])])
 def test_sparse_attention_matches_oracle(cuda, cfg_name, n, qblocks):
     p = WL.make(cfg_name, n=n)
@@ -306,6 +321,47 @@ def test_unbounded_rows_take_the_exact_path(cuda, dtype, block):
                                              compact=True)
     out = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block)
     ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), block)
+    assert torch.isfinite(out).all()
+    assert np.abs(np_of(out) - ref).max() < TOL[dtype]
+
+
+# admission bounds of the bounded-row path (log2 units of scale * q.k): attn.hip fast_bound<DT>
+FAST_BOUND = {torch.float16: 15.0, torch.bfloat16: 32.0}
+
+
+@pytest.mark.parametrize("dtype,target", [(torch.float16, 14.0), (torch.float16, 22.0),
+                                          (torch.float16, 40.0), (torch.float16, 60.0),
+                                          (torch.bfloat16, 31.0), (torch.bfloat16, 60.0)])
+def test_rows_near_the_fast_path_bound(cuda, dtype, target):
+    """Every row's |q| is set so that the key-norm bound scale*log2e*|q|*max|k| equals `target`:
+    just under the dtype's admission bound the rows take the bounded path (fp16: P = 2^S packed
+    in fp16 must stay finite; bf16: the pre-scaled q's rounding must stay within tolerance), just
+    over it the exact path. Keys are aligned with the queries' direction to reach the bound
+    (largest scores near `target`, a peaked softmax), and the output must be finite and within
+    2e-2 of the float64 oracle either way."""
+    rng = np.random.default_rng(21)
+    n, block, scale = 1024, 128, 0.125
+    q = rng.standard_normal((1, 2, n, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    # a shared direction u: keys lean on it so that some scores approach the Cauchy-Schwarz bound
+    u = rng.standard_normal(64).astype(np.float32)
+    u /= np.linalg.norm(u)
+    q += 2.0 * u
+    k += 1.5 * rng.standard_normal((1, 1, n, 1)).astype(np.float32) * u
+    k = WL.round_to(k, dtype)
+    kmax = float(np.sqrt((k.astype(np.float64) ** 2).sum(-1)).max())
+    qn = np.sqrt((q.astype(np.float64) ** 2).sum(-1, keepdims=True))
+    q = q / qn * (target / (scale * math.log2(math.e) * kmax))
+    q, v = WL.round_to(q, dtype), WL.round_to(v, dtype)
+    bound = scale * math.log2(math.e) * float(np.sqrt((q.astype(np.float64) ** 2).sum(-1)).max()) * kmax
+    assert (bound < FAST_BOUND[dtype]) == (target < FAST_BOUND[dtype]), bound
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=3, local=1, beta=2.0,
+                                             compact=True)
+    out = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, scale=scale)
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), block,
+                             scale=scale)
     assert torch.isfinite(out).all()
     assert np.abs(np_of(out) - ref).max() < TOL[dtype]
 
@@ -356,18 +412,26 @@ def test_hf_layout_output_without_copies(cuda):
     assert torch.equal(outb.transpose(1, 2), ref)
 
 
-def test_no_future_leak(cuda):
-    """Perturbing keys/values after position `cut` leaves outputs <= cut unchanged."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_no_future_leak(cuda, dtype):
+    """Perturbing keys/values after position `cut` leaves outputs <= cut unchanged: bit for bit
+    in the query blocks that end before `cut`'s block (no key they read changed, and their
+    softmax path is chosen from the keys they read), and within the reference's own bar
+    (test_flex_swap.py:78-91, atol 2e-2) in `cut`'s block, whose rows share one workgroup with
+    later rows and may take the other softmax path when the perturbed keys raise its bound. The
+    perturbation (+5, |k| ~ 40) pushes the bound past both dtypes' fast-path limits."""
     torch.manual_seed(0)
-    n, cut = 1024, 300
-    q = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.bfloat16)
+    n, cut, block = 1024, 300, 128
+    q = torch.randn(1, 2, n, 64, device=cuda, dtype=dtype)
     k, v = torch.randn_like(q), torch.randn_like(q)
-    o1 = K.ssa_flex(q, k, v, block=128, top_c=2, local=1)
+    o1 = K.ssa_flex(q, k, v, block=block, top_c=2, local=1)
     k2, v2 = k.clone(), v.clone()
     k2[:, :, cut + 1:] += 5
     v2[:, :, cut + 1:] += 5
-    o2 = K.ssa_flex(q, k2, v2, block=128, top_c=2, local=1)
-    assert torch.equal(o1[:, :, :cut + 1], o2[:, :, :cut + 1])
+    o2 = K.ssa_flex(q, k2, v2, block=block, top_c=2, local=1)
+    whole = cut // block * block
+    assert torch.equal(o1[:, :, :whole], o2[:, :, :whole])
+    assert (o1[:, :, :cut + 1].float() - o2[:, :, :cut + 1].float()).abs().max().item() < 2e-2
 
 
 def test_c5_full_length_properties_and_sampled_rows(cuda):
@@ -536,6 +600,86 @@ def test_routed_decoder_matches_reference_router_and_oracle(cuda):
             assert np.abs(np_of(out[0, h]) - ref).max() < 2e-2
 
 
+def test_routed_decoder_full_1m_cache_matches_reference(cuda):
+    """RoutedDecoder over the bench's C4 decode workload at its full size: a 1,048,576-token
+    cache, then decode steps t = 0..127 appending one token each (8193 complete blocks by the
+    last). At the fixture steps (t = 127 completes a block) the selection equals the reference's
+    float32 _selection_mask (or differs on a certified near-tie) and the oracle's bit for bit,
+    and every head's output is within 2e-2 of the oracle's decode_attend."""
+    g = GU.load("c4_query_1m")
+    p = WL.make_decode(steps=GU.C4_1M_STEPS)
+    cfg, n = p["cfg"], p["n_cache"]
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"])
+    steps = g["steps"].tolist()
+    print(f"c4 1M decode: cache {n}, steps up to {steps[-1]}", flush=True)
+    dec = D.RoutedDecoder(1, cfg.Hq, cfg.Hkv, cfg.d, n + GU.C4_1M_STEPS, block=cfg.block,
+                          top_c=cfg.top_c, local=cfg.local, beta=cfg.beta, dtype=cfg.dtype,
+                          device=cuda)
+    kd, vd = dev(p["k"], cfg.dtype, cuda), dev(p["v"], cfg.dtype, cuda)
+    qd = dev(p["q"], cfg.dtype, cuda)
+    dec.prefill(kd[:, :, :n], vd[:, :, :n])
+    G_ = cfg.Hq // cfg.Hkv
+    # summaries of every block complete at the checked steps (all lie in the first n + 128)
+    assert steps[-1] < 128
+    mu, var, _ = O.block_stats(p["k"][:, :, :n + 128], cfg.block, "pop")
+    for t in range(steps[-1] + 1):
+        out = dec.step(qd[:, :, t].contiguous(), kd[:, :, n + t].contiguous(),
+                       vd[:, :, n + t].contiguous())
+        if t not in steps:
+            continue
+        a, pos = steps.index(t), n + t
+        kn, ki = dec.kv_num.cpu().numpy(), dec.kv_idx.cpu().numpy()
+        qrow = p["q"][:, :, t:t + 1]
+        onum, oidx = O.route_query_summaries(qrow, mu, var, cfg.block, pos, top_c=cfg.top_c,
+                                             local=cfg.local, beta=cfg.beta)
+        n_, n_eq, _, bad = GU.compare_selections(kn, ki, onum[:, :, 0], oidx[:, :, 0])
+        assert n_eq == n_, (t, bad)
+        r64, mag = O.exact_scores64(qrow, mu, var, 0.5 * cfg.beta)
+        n_, n_eq, n_cert, bad = GU.compare_selections(kn, ki, g["kv_num"][a][None],
+                                                      g["kv_idx"][a][None], r64[:, :, 0],
+                                                      mag[:, :, 0])
+        print(f"step {t}: {n_eq}/{n_} heads identical to the reference, {n_cert} certified",
+              flush=True)
+        assert not bad, (t, bad)
+        o = np_of(out)
+        for h in range(cfg.Hq):
+            ref = O.decode_attend(p["q"][0, h, t], p["k"][0, h // G_], p["v"][0, h // G_],
+                                  ki[0, h, :kn[0, h]], pos, cfg.block)
+            assert np.abs(o[0, h] - ref).max() < 2e-2, (t, h)
+
+
+def test_c5_geometry_prefix_router_matches_reference(cuda):
+    """The router at C5's geometry (fp16, block 256, top_c 64 + local 1, beta 2) over a
+    2,097,152-token prefix (8192 query blocks x 8192 candidate blocks): bit-exact against the
+    oracle and equal to the reference's float32 block_route_budget except on certified near-ties;
+    sampled query blocks' attention within 2e-2 of the oracle."""
+    g = GU.load("c5_prefix")
+    p = WL.make_c5_prefix()
+    cfg = p["cfg"]
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"])
+    q, k, v = (dev(p[x], cfg.dtype, cuda) for x in ("q", "k", "v"))
+    kv_num, kv_idx, _ = K.block_route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                             beta=cfg.beta, compact=True)
+    kn, ki = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                beta=cfg.beta)
+    n, n_eq, _, bad = GU.compare_selections(kn, ki, onum, oidx)
+    assert n_eq == n, bad[:3]
+    qb = O.qmean(p["q"], cfg.block)
+    mu, var, _ = O.block_stats(p["k"], cfg.block, "pop")
+    r64, mag = O.exact_scores64(qb, mu, var, 0.5 * cfg.beta)
+    n, n_eq, n_cert, bad = GU.compare_selections(kn, ki, g["kv_num"], g["kv_idx"], r64, mag)
+    print(f"c5 prefix: {n} rows, {n_eq} identical to the reference, {n_cert} certified")
+    assert not bad, bad[:3]
+    out = K.sparse_attention(q, k, v, kv_num, kv_idx, cfg.block)
+    blocks = [0, 1, 64, 4095, 8191]
+    ref = O.sparse_attention(p["q"], p["k"], p["v"], kn, ki, cfg.block, qblocks=blocks)
+    o = np_of(out)
+    for i in blocks:
+        sl = slice(i * cfg.block, (i + 1) * cfg.block)
+        assert np.abs(o[0, 0, sl] - ref[0, 0, sl]).max() < 2e-2, i
+
+
 # ---- a9 real-model boundary --------------------------------------------------------------------
 
 def _mod(groups=1, scaling=0.125, layer_idx=0):
@@ -573,6 +717,71 @@ def test_gemma_analytic_matches_reference_fixture(cuda):
     assert np.abs(np_of(out) - g["out"]).max() < 1e-5
     inc, _ = G.ssa_attention_forward(_mod(groups=2), qt[:, :, -1:], kt, vt, scaling=0.125)
     assert np.abs(np_of(inc) - g["out_last"]).max() < 1e-5
+
+
+def test_gemma_analytic_edgeworth_matches_reference_fixture(cuda):
+    """ssa_attention_forward(impl='analytic', edgeworth=True): the per-query router adds
+    beta^2/6 <q^3, m3> (ssa/gemma_ssa.py:101-102 via :237) on skewed keys, where the term changes
+    the selection of 418 of the 1200 (head, query) rows; prefill rows and a q_len = 1 row match
+    the reference's float64 output within 1e-5."""
+    g = GU.load("analytic_gqa_edgeworth")
+    q, k, v = GU.analytic_inputs(12, skew=0.7)
+    assert GU.sha(q, k, v) == str(g["inputs_sha256"])
+    G.CFG = G.SSAConfig(block=64, budget_frac=0.5, local_w=1, beta=2.0, impl="analytic",
+                        edgeworth=True)
+    qt, kt, vt = (torch.from_numpy(x).float().to(cuda) for x in (q, k, v))
+    out, _ = G.ssa_attention_forward(_mod(groups=2), qt, kt, vt, scaling=0.125)
+    assert np.abs(np_of(out) - g["out"]).max() < 1e-5
+    inc, _ = G.ssa_attention_forward(_mod(groups=2), qt[:, :, -1:], kt, vt, scaling=0.125)
+    assert np.abs(np_of(inc) - g["out_last"]).max() < 1e-5
+    # without the term the output differs from the fixture (the fixture pins the term)
+    G.CFG = G.SSAConfig(block=64, budget_frac=0.5, local_w=1, beta=2.0, impl="analytic")
+    plain, _ = G.ssa_attention_forward(_mod(groups=2), qt, kt, vt, scaling=0.125)
+    assert np.abs(np_of(plain) - g["out"]).max() > 1e-2
+
+
+@pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (256, torch.float16),
+                                     (96, torch.bfloat16), (128, torch.float32)])
+def test_prefill_other_head_dims_match_oracle(cuda, d, dtype):
+    """impl='flex' prefill at head dims other than 64 (the reference's flex branch serves any
+    head size, ssa/gemma_ssa.py:169-180): ragged n, GQA 2:1, against the oracle."""
+    rng = np.random.default_rng(33)
+    n, block = 700, 128
+    q = WL.round_to(rng.standard_normal((1, 4, n, d)).astype(np.float32), dtype)
+    k = WL.round_to(rng.standard_normal((1, 2, n, d)).astype(np.float32), dtype)
+    v = WL.round_to(rng.standard_normal((1, 2, n, d)).astype(np.float32), dtype)
+    G.CFG = G.SSAConfig(block=block, budget_frac=0.5, local_w=1, beta=2.0, impl="flex")
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    out, _ = G.ssa_attention_forward(_mod(groups=2), qt, kt, vt, scaling=d ** -0.5)
+    kv_num, kv_idx = O.route_budget(q, k, block, budget_frac=0.5, local=1, beta=2.0, n_real=n)
+    ref = O.sparse_attention(q, k, v, kv_num, kv_idx, block, scale=d ** -0.5)
+    assert np.abs(np_of(out).transpose(0, 2, 1, 3) - ref).max() < TOL[dtype]
+
+
+def test_attention_and_decoder_reject_mismatched_arguments(cuda):
+    """A V^T of another length or dtype, and decode inputs of the wrong dtype or shape, raise
+    instead of being read as the cache's layout."""
+    q = torch.randn(1, 2, 512, 64, device=cuda, dtype=torch.bfloat16)
+    k, v = torch.randn_like(q), torch.randn_like(q)
+    kv_num, kv_idx, _ = K.block_route_budget(q, k, 128, top_c=2, local=1, compact=True)
+    with pytest.raises(ValueError):
+        K.sparse_attention(q, k, v, kv_num, kv_idx, 128, vt=K.transpose_v(v[:, :, :384], 128))
+    with pytest.raises(ValueError):
+        K.sparse_attention(q, k, v, kv_num, kv_idx, 128, vt=K.transpose_v(v.half(), 128))
+    out = K.sparse_attention(q, k, v, kv_num, kv_idx, 128, vt=K.transpose_v(v, 128))
+    assert torch.equal(out, K.sparse_attention(q, k, v, kv_num, kv_idx, 128))
+    dec = D.RoutedDecoder(1, 2, 1, 64, 512, block=128, top_c=2, dtype=torch.bfloat16, device=cuda)
+    qd = torch.randn(1, 2, 64, device=cuda, dtype=torch.bfloat16)
+    kn = torch.randn(1, 1, 64, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        dec.step(qd.float(), kn, kn)
+    with pytest.raises(ValueError):
+        dec.step(qd[:, :1], kn, kn)
+    with pytest.raises(ValueError):
+        dec.step(torch.randn(1, 2, 128, device=cuda, dtype=torch.bfloat16)[..., ::2], kn, kn)
+    assert dec.pos == 0
+    dec.step(qd, kn, kn)
+    assert dec.pos == 1
 
 
 def test_gemma_decode_equals_prefill_last_row(cuda):

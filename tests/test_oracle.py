@@ -146,6 +146,76 @@ def test_oracle_analytic_path_matches_reference():
     assert np.abs(out[:, :, -1] - g["out_last"][:, 0]).max() < 2e-6
 
 
+def test_oracle_analytic_edgeworth_matches_reference():
+    """The per-query router with the edgeworth term (ssa/gemma_ssa.py:101-102) on skewed keys:
+    the oracle's routing + masked softmax equals the reference's float64 analytic output, and
+    dropping the term (a plausible slip) fails the same fixture."""
+    g = GU.load("analytic_gqa_edgeworth")
+    q, k, v = GU.analytic_inputs(12, skew=0.7)
+    assert GU.sha(q, k, v) == str(g["inputs_sha256"])
+    ref = g["out"].transpose(0, 2, 1, 3)
+    outs = {}
+    for edge in (True, False):
+        kv_num, kv_idx = O.route_query(q, k, 64, 0, top_c=None, budget_frac=0.5, local=1,
+                                       beta=2.0, edgeworth=edge)
+        outs[edge] = O.attend_rows(q, k, v, kv_num, kv_idx, 0, 64, scale=0.125)
+    assert np.abs(outs[True] - ref).max() < 2e-6
+    assert np.abs(outs[True][:, :, -1] - g["out_last"][:, 0]).max() < 2e-6
+    assert np.abs(outs[False] - ref).max() > 1e-2
+
+
+def test_oracle_c5_geometry_prefix_matches_reference():
+    """block_route_budget at C5's geometry (fp16, block 256, top_c 64, local 1, beta 2) on the
+    2,097,152-token prefix (8192 query blocks): the oracle's selections equal the reference's
+    float32 selections except on certified float32 near-ties."""
+    g = GU.load("c5_prefix")
+    p = WL.make_c5_prefix()
+    cfg = p["cfg"]
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"])
+    onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                beta=cfg.beta)
+    qb = O.qmean(p["q"], cfg.block)
+    mu, var, _ = O.block_stats(p["k"], cfg.block, "pop")
+    r64, mag = O.exact_scores64(qb, mu, var, 0.5 * cfg.beta)
+    n, n_eq, n_cert, bad = GU.compare_selections(onum, oidx, g["kv_num"], g["kv_idx"], r64, mag)
+    print(f"c5_prefix: {n} rows, {n_eq} identical, {n_cert} certified near-ties")
+    assert not bad, bad[:3]
+    assert n_eq >= n - 8
+
+
+def test_oracle_decode_router_full_1m_cache_matches_reference():
+    """_selection_mask at q_len = 1 over the full 1,048,576-token C4 cache (plus the appended
+    tokens) at three decode steps, the last completing a block: the oracle's per-query router
+    equals the reference's float32 selection on every head (or differs on a certified
+    near-tie)."""
+    g = GU.load("c4_query_1m")
+    p = WL.make_decode(steps=GU.C4_1M_STEPS)
+    cfg, n = p["cfg"], p["n_cache"]
+    assert GU.sha(p["q"], p["k"]) == str(g["inputs_sha256"])
+    # every block complete at the checked steps is complete in the first n + 128 tokens
+    mu, var, _ = O.block_stats(p["k"][:, :, :n + 128], cfg.block, "pop")
+    steps = g["steps"].tolist()
+    assert max(steps) < 128
+    # the summary shortcut equals the per-position restatement (checked on the first step)
+    t0 = steps[0]
+    a0 = O.route_query(p["q"][:, :, t0:t0 + 1], p["k"], cfg.block, n + t0, top_c=cfg.top_c,
+                       local=cfg.local, beta=cfg.beta, kv_len=n + t0 + 1)
+    b0 = O.route_query_summaries(p["q"][:, :, t0:t0 + 1], mu, var, cfg.block, n + t0,
+                                 top_c=cfg.top_c, local=cfg.local, beta=cfg.beta)
+    assert all((x == y).all() for x, y in zip(a0, b0))
+    for a, t in enumerate(steps):
+        pos = n + t
+        qrow = p["q"][:, :, t:t + 1]
+        onum, oidx = O.route_query_summaries(qrow, mu, var, cfg.block, pos, top_c=cfg.top_c,
+                                             local=cfg.local, beta=cfg.beta)
+        r64, mag = O.exact_scores64(qrow, mu, var, 0.5 * cfg.beta)
+        n_, n_eq, n_cert, bad = GU.compare_selections(onum[:, :, 0], oidx[:, :, 0],
+                                                      g["kv_num"][a][None], g["kv_idx"][a][None],
+                                                      r64[:, :, 0], mag[:, :, 0])
+        assert not bad, (t, bad)
+        assert int(onum.max()) <= cfg.top_c + cfg.local + 1
+
+
 # ---- mathematics -------------------------------------------------------------------------------
 
 def test_block_stats_closed_form():
