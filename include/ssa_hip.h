@@ -255,6 +255,28 @@ int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* k
                     void* workspace, size_t workspace_bytes, ssa_stream_t stream);
 
 /*
+ * ssa_decode_step without a workspace argument. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
+ * must not call hipMalloc). The step's scratch (the query rows in fp32, the router's score keys,
+ * the per-block partial outputs) lives in a static device array of the library,
+ * SSA_DECODE_STATIC_SCRATCH_BYTES on every device the library runs on, held until the process
+ * ends; the call allocates nothing. Steps needing more scratch than that
+ * (ssa_decode_step_workspace_size(...) > SSA_DECODE_STATIC_SCRATCH_BYTES) return
+ * SSA_ERR_WORKSPACE. Every call on a device uses that device's one array: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialised by the caller. Nothing in
+ * the scratch needs to start at zero (every call writes what it reads). The device is the
+ * stream's (the current device for the null stream). Arguments and results otherwise as
+ * ssa_decode_step.
+ */
+#define SSA_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
+int ssa_decode_step_static(const void* q, const void* k_new, const void* v_new, void* kcache,
+                           void* vcache, float* mu, float* var, void* out, int dtype, int64_t B,
+                           int64_t Hq, int64_t Hkv, int64_t cap, int64_t d, int64_t block,
+                           int64_t pos, const int64_t* strides, int64_t top_c, float budget_frac,
+                           int64_t local, float coef2, float scale, int32_t* kv_num,
+                           int32_t* kv_idx, int64_t W, ssa_stream_t stream);
+
+/*
  * Per-row block-sparse attention of ssa_swap.ssa_masked (ssa/ssa_swap.py:32-56), forward and
  * backward, for continued training through the attention swap. Row r of head (b, h) is the query
  * at position r of q (B, Hq, n, d); it attends the keys <= r of its listed blocks (kv_num (B,Hq,n)

@@ -22,6 +22,7 @@ STATS_POP, STATS_UNBIASED, STATS_QMEAN = 0, 1, 2
 ROUTE_BUDGET, ROUTE_FLAT, ROUTE_QUERY, ROUTE_STARTED = 0, 1, 2, 3
 ATTN_VT_READY = 1
 MASKED_MASKS_READY = 1
+DECODE_STATIC_SCRATCH_BYTES = 16 << 20  # SSA_DECODE_STATIC_SCRATCH_BYTES
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -70,6 +71,10 @@ _SIGNATURES = {
     "ssa_decode_step": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int, _c_i64,
                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_f,
                                  _c_i64, _c_f, _c_f, _c_p, _c_p, _c_i64, _c_p, _c_sz, _c_p]),
+    "ssa_decode_step_static": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_int,
+                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        _c_p, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_p, _c_p, _c_i64,
+                                        _c_p]),
 }
 
 _lock = threading.Lock()

@@ -14,6 +14,8 @@
 // ssa/gemma_ssa.py:85-137,225-240 (exact per-query router and softmax at q_len = 1).
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace ssa {
@@ -605,13 +607,15 @@ extern "C" size_t ssa_decode_step_workspace_size(int64_t B, int64_t Hq, int64_t 
   return qf + keys + ssa_decode_attend_workspace_size(B, Hq, 1, W, d);
 }
 
-extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* kcache,
-                               void* vcache, float* mu, float* var, void* out, int dtype,
-                               int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t d,
-                               int64_t block, int64_t pos, const int64_t* strides, int64_t top_c,
-                               float budget_frac, int64_t local, float coef2, float scale,
-                               int32_t* kv_num, int32_t* kv_idx, int64_t W, void* workspace,
-                               size_t workspace_bytes, ssa_stream_t stream) {
+namespace {
+// The body of ssa_decode_step and ssa_decode_step_static: `workspace` is the caller's buffer or
+// the library's static scratch.
+int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* kcache,
+                     void* vcache, float* mu, float* var, void* out, int dtype, int64_t B,
+                     int64_t Hq, int64_t Hkv, int64_t cap, int64_t d, int64_t block, int64_t pos,
+                     const int64_t* strides, int64_t top_c, float budget_frac, int64_t local,
+                     float coef2, float scale, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+                     void* workspace, size_t workspace_bytes, ssa_stream_t stream) {
   using namespace ssa;
   SSA_REQUIRE(q && k_new && v_new && kcache && vcache && mu && var && out && strides && kv_num &&
                   kv_idx,
@@ -704,6 +708,76 @@ extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_n
     p.knb = as.knb; p.knh = as.knh; p.vnb = as.vnb; p.vnh = as.vnh;
   }
   return run_attend(dtype, p, st);
+}
+
+// Scratch of ssa_decode_step_static: device memory the library itself holds, one copy on every
+// device it runs on, for the process's lifetime. In host code `decode_scratch` names a host-side
+// stand-in, not the device copy: kernels and copies use the address hipGetSymbolAddress returns
+// for the device, looked up once per device (with that device current) and kept in
+// g_scratch_ptr.
+__device__ __align__(256) unsigned char decode_scratch[SSA_DECODE_STATIC_SCRATCH_BYTES];
+constexpr int kMaxScratchDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_of_device(hipStream_t st, void** ptr) {
+  using namespace ssa;
+  int dev = -1;
+  if (st != nullptr) {
+    SSA_TRY(hip_status(hipStreamGetDevice(st, &dev), "hipStreamGetDevice"));
+  } else {
+    SSA_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  }
+  SSA_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, SSA_ERR_UNSUPPORTED,
+              "decode_step_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    SSA_TRY(hip_status(hipGetDevice(&cur), "hipGetDevice"));
+    if (cur != dev) SSA_TRY(hip_status(hipSetDevice(dev), "hipSetDevice"));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(decode_scratch));
+    if (cur != dev) SSA_TRY(hip_status(hipSetDevice(cur), "hipSetDevice"));
+    SSA_TRY(hip_status(e, "hipGetSymbolAddress(decode_scratch)"));
+    SSA_REQUIRE(p != nullptr, SSA_ERR_HIP, "decode_step_static: no scratch address on device %d",
+                dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return SSA_OK;
+}
+}  // namespace
+
+extern "C" int ssa_decode_step(const void* q, const void* k_new, const void* v_new, void* kcache,
+                               void* vcache, float* mu, float* var, void* out, int dtype,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t cap, int64_t d,
+                               int64_t block, int64_t pos, const int64_t* strides, int64_t top_c,
+                               float budget_frac, int64_t local, float coef2, float scale,
+                               int32_t* kv_num, int32_t* kv_idx, int64_t W, void* workspace,
+                               size_t workspace_bytes, ssa_stream_t stream) {
+  return decode_step_impl(q, k_new, v_new, kcache, vcache, mu, var, out, dtype, B, Hq, Hkv, cap, d,
+                          block, pos, strides, top_c, budget_frac, local, coef2, scale, kv_num,
+                          kv_idx, W, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ssa_decode_step_static(const void* q, const void* k_new, const void* v_new,
+                                      void* kcache, void* vcache, float* mu, float* var,
+                                      void* out, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                      int64_t cap, int64_t d, int64_t block, int64_t pos,
+                                      const int64_t* strides, int64_t top_c, float budget_frac,
+                                      int64_t local, float coef2, float scale, int32_t* kv_num,
+                                      int32_t* kv_idx, int64_t W, ssa_stream_t stream) {
+  using namespace ssa;
+  const size_t need = ssa_decode_step_workspace_size(B, Hq, cap, d, block, W);
+  SSA_REQUIRE(need <= (size_t)SSA_DECODE_STATIC_SCRATCH_BYTES, SSA_ERR_WORKSPACE,
+              "decode_step_static: this step needs %zu bytes of scratch, more than the static "
+              "%zu (use ssa_decode_step with a workspace)",
+              need, (size_t)SSA_DECODE_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  SSA_TRY(scratch_of_device(static_cast<hipStream_t>(stream), &ws));
+  return decode_step_impl(q, k_new, v_new, kcache, vcache, mu, var, out, dtype, B, Hq, Hkv, cap, d,
+                          block, pos, strides, top_c, budget_frac, local, coef2, scale, kv_num,
+                          kv_idx, W, ws, (size_t)SSA_DECODE_STATIC_SCRATCH_BYTES, stream);
 }
 
 extern "C" size_t ssa_masked_attn_workspace_size(int64_t B, int64_t Hq, int64_t n, int64_t W,

@@ -98,7 +98,8 @@ class RoutedDecoder:
     """
 
     def __init__(self, batch, hq, hkv, d, capacity, block=BLOCK, top_c=64, budget_frac=None,
-                 local=1, beta=2.0, dtype=torch.bfloat16, device="cuda", scale=None):
+                 local=1, beta=2.0, dtype=torch.bfloat16, device="cuda", scale=None,
+                 static_scratch=False):
         if hq % hkv:
             raise ValueError("hq must be a multiple of hkv")
         if top_c is None and budget_frac is None:
@@ -114,17 +115,24 @@ class RoutedDecoder:
         self.scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
         self.dtype = dtype
         dev = torch.device(device)
+        self.W = route_width("query", 1, self.nbk, None if top_c is None else top_c,
+                             self.budget_frac, self.local, self.capacity - 1, block)
+        ws = int(_lib.query("ssa_decode_step_workspace_size", batch, hq, self.capacity, d, block,
+                            self.W))
+        # static_scratch: steps run ssa_decode_step_static, whose scratch is the library's own
+        # device array (no workspace here; steps with step(out=...) allocate nothing)
+        self.static_scratch = bool(static_scratch)
+        if self.static_scratch and ws > _lib.DECODE_STATIC_SCRATCH_BYTES:
+            raise ValueError(f"a step needs {ws} bytes of scratch, more than the library's static "
+                             f"{_lib.DECODE_STATIC_SCRATCH_BYTES}")
         self.kcache = torch.zeros(batch, hkv, self.capacity, d, device=dev, dtype=dtype)
         self.vcache = torch.zeros_like(self.kcache)
         self.mu = torch.zeros(batch, hkv, self.nbk, d, device=dev, dtype=torch.float32)
         self.var = torch.zeros_like(self.mu)
-        self.W = route_width("query", 1, self.nbk, None if top_c is None else top_c,
-                             self.budget_frac, self.local, self.capacity - 1, block)
         self.kv_num = torch.zeros(batch, hq, device=dev, dtype=torch.int32)
         self.kv_idx = torch.zeros(batch, hq, self.W, device=dev, dtype=torch.int32)
-        ws = int(_lib.query("ssa_decode_step_workspace_size", batch, hq, self.capacity, d, block,
-                            self.W))
-        self.workspace = torch.empty(ws, device=dev, dtype=torch.uint8)
+        self.workspace = None if self.static_scratch else torch.empty(ws, device=dev,
+                                                                      dtype=torch.uint8)
         self.pos = 0
 
     @torch.no_grad()
@@ -170,12 +178,15 @@ class RoutedDecoder:
                                   v_new.stride(0), v_new.stride(1), kc.stride(0), kc.stride(1),
                                   kc.stride(2), vc.stride(0), vc.stride(1), vc.stride(2),
                                   out.stride(0), out.stride(1)])
-        _lib.call("ssa_decode_step", q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
-                  kc.data_ptr(), vc.data_ptr(), self.mu.data_ptr(), self.var.data_ptr(),
-                  out.data_ptr(), _lib.dtype_code(self.dtype), self.B, self.Hq, self.Hkv,
-                  self.capacity, self.d, self.block, self.pos, strides, self.top_c,
-                  self.budget_frac, self.local, self.coef2, self.scale, self.kv_num.data_ptr(),
-                  self.kv_idx.data_ptr(), self.W, self.workspace.data_ptr(),
-                  self.workspace.numel(), _lib.stream_of(q))
+        args = (q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                self.mu.data_ptr(), self.var.data_ptr(), out.data_ptr(),
+                _lib.dtype_code(self.dtype), self.B, self.Hq, self.Hkv, self.capacity, self.d,
+                self.block, self.pos, strides, self.top_c, self.budget_frac, self.local,
+                self.coef2, self.scale, self.kv_num.data_ptr(), self.kv_idx.data_ptr(), self.W)
+        if self.static_scratch:
+            _lib.call("ssa_decode_step_static", *args, _lib.stream_of(q))
+        else:
+            _lib.call("ssa_decode_step", *args, self.workspace.data_ptr(), self.workspace.numel(),
+                      _lib.stream_of(q))
         self.pos += 1
         return out

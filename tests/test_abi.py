@@ -112,9 +112,10 @@ def test_route_width():
 
 
 def test_workspace_queries():
-    # V^T (256-byte aligned), then one fp32 key-norm bound per (b, kv head)
+    # V^T (256-byte aligned), then the fp32 key-norm maximum of every 64-key tile (2 heads x 6
+    # tiles) and one flag per (b, kv head), rounded up to 256 bytes
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.BF16, 1, 2, 300, 64, 128) == \
-        2 * 64 * 384 * 2 + 2304  # V^T, then 16 key-norm slots of 32 floats and 2 flags
+        2 * 64 * 384 * 2 + 256
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F32, 1, 2, 300, 64, 128) == 0
     assert _lib.query("ssa_route_workspace_size", 1, 14, 1024, 1024) == 14 * 1024 * 1024 * 4
     assert _lib.query("ssa_decode_attend_workspace_size", 1, 14, 1, 66, 64) == 14 * 66 * 66 * 4
