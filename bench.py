@@ -13,8 +13,9 @@ Also reported on the same line: per-kernel times (HIP events on the stream the k
 the roofline of the dominant kernel (selected-block FLOPs = 4*b^2*d*sum(kv_num) per launch
 against the 2.5 PFLOP/s bf16 dense MFMA peak; HBM traffic from the committed rocprofv3 PMC
 summary when present), the dense causal baseline (torch SDPA) and this kernel at full budget,
-the routed decode step at a 1M-token cache ("C4", ms/step), and the CPU baseline: the NumPy
-oracle (oracle/ssa_oracle.py) timed on this host's cores on a bounded sample.
+the routed decode step at a 1M-token cache ("C4", ms/step), and the CPU baseline: the
+reference's path restated in torch float32 (oracle/cpu_path.py) on this host's cores -- the C3
+router in full, attention on a stated sample, C4 decode steps.
 
 Only one GPU is used: --gpus N > 1 exits with a message.
 """
@@ -147,41 +148,80 @@ def device_info(torch, dev):
     return info
 
 
-def cpu_baseline(p, kv_num_all, threads):
-    """The oracle on the host: the C3 router in full plus attention for a stratified sample of
-    query blocks, extrapolated by sum(kv_num)."""
-    import numpy as np
+def cpu_threads(torch):
+    """Host threads for the CPU baseline: the cores this process may use (OMP_NUM_THREADS caps
+    it where set, as on the GPU boxes)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    torch.set_num_threads(n)
+    return torch.get_num_threads()
 
-    from oracle import ssa_oracle as O
+
+def cpu_baseline(p, dec):
+    """The reference's path restated in torch float32 on this host's cores (oracle/cpu_path.py;
+    ssa/ssa_kernel.py:61-119 and the FlexAttention softmax, ssa/ivf_decode.py:49-62 with the
+    router of ssa/gemma_ssa.py:99-131): the C3 router in full (median of 3 runs), attention over a
+    stratified sample of (query head, query block) pairs extrapolated by sum(kv_num), and C4
+    decode steps over the full 1,048,576-token cache (median step time of 3 runs of 8 steps)."""
+    import torch
+
+    from oracle import cpu_path as C
+    threads = cpu_threads(torch)
     cfg = p["cfg"]
-    rng = np.random.default_rng(0)
-    nb = cfg.nb
-    blocks = sorted(set(np.linspace(0, nb - 1, 24).astype(int).tolist()))
-    heads = [int(h) for h in rng.integers(0, cfg.Hq, size=len(blocks))]
-    routes, samples = [], []
-    for _ in range(3):  # median of 3 runs of the sample
+    q, k, v = (torch.from_numpy(p[x]).to(torch.bfloat16) for x in ("q", "k", "v"))
+    routes = []
+    for _ in range(3):
         t0 = time.perf_counter()
-        onum, oidx = O.route_budget(p["q"], p["k"], cfg.block, top_c=cfg.top_c, local=cfg.local,
-                                    beta=cfg.beta)
+        kv_num, kv_idx, _ = C.route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                           beta=cfg.beta)
         routes.append(time.perf_counter() - t0)
+    t_route = sorted(routes)[1]
+    nb = cfg.nb
+    pairs = [(i % cfg.Hq, i) for i in range(nb)]  # every query block once, heads in turn
+    sample_kv = sum(int(kv_num[0, h, i]) for h, i in pairs)
+    total_kv = int(kv_num.sum())
+    samples = []
+    for _ in range(3):
         t0 = time.perf_counter()
-        sample_kv = 0
-        for i, h in zip(blocks, heads):
-            O.sparse_attention(p["q"], p["k"], p["v"], onum, oidx, cfg.block, qblocks=[i],
-                               heads=[h])
-            sample_kv += int(onum[0, h, i])
+        C.attend_blocks(q, k, v, kv_num, kv_idx, cfg.block, pairs)
         samples.append(time.perf_counter() - t0)
-    t_route, t_sample = sorted(routes)[1], sorted(samples)[1]
-    total_kv = int(kv_num_all)
+    t_sample = sorted(samples)[1]
     t_attn = t_sample * total_kv / sample_kv
     t_total = t_route + t_attn
-    return {
+    out = {
         "value": cfg.n / t_total, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": (f"oracle (NumPy float64) C3 router over all {cfg.Hq * nb} query-block rows "
-                   f"({t_route:.2f} s) + exact attention for {len(blocks)} (head, query-block) "
-                   f"pairs ({sample_kv} of {total_kv} selected tiles, {t_sample:.2f} s), "
-                   f"extrapolated by sum(kv_num) to {t_total:.1f} s per layer; median of 3 runs"),
+        "sample": (f"torch float32 on the host (oracle/cpu_path.py): the reference's "
+                   f"block_route_budget op sequence over all {cfg.Hq * nb} query-block rows "
+                   f"({t_route:.2f} s, median of 3) + block-sparse softmax for {len(pairs)} "
+                   f"(head, query-block) pairs ({sample_kv} of {total_kv} selected tiles = "
+                   f"{100.0 * sample_kv / total_kv:.2f} %, {t_sample:.2f} s) extrapolated by "
+                   f"sum(kv_num) to {t_attn:.1f} s: {t_total:.1f} s per layer"),
+        "c3_router_s": t_route, "c3_attention_s_extrapolated": t_attn,
+        "c3_attention_sample_fraction": sample_kv / total_kv,
     }
+    if dec is not None:
+        c4 = dec["cfg"]
+        n0 = dec["n_cache"]
+        kc = torch.from_numpy(dec["k"][0]).to(torch.bfloat16)
+        vc = torch.from_numpy(dec["v"][0]).to(torch.bfloat16)
+        qd = torch.from_numpy(dec["q"][0]).to(torch.bfloat16)  # (Hq, steps, d)
+        ncomp = (n0 + 8) // c4.block
+        kb = kc[:, :ncomp * c4.block].float().reshape(c4.Hkv, ncomp, c4.block, c4.d)
+        mu, var = kb.mean(2), kb.var(2, unbiased=False)  # resident summaries (not timed)
+        del kb
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for t in range(8):
+                C.decode_step(qd[:, t], kc, vc, mu, var, n0 + t, c4.block, c4.top_c, c4.local,
+                              c4.beta)
+            runs.append((time.perf_counter() - t0) / 8)
+        out["c4_decode_ms_per_step"] = sorted(runs)[1] * 1000.0
+        out["c4_sample"] = (f"{c4.Hq} query heads over the {n0}-token cache (resident block "
+                            f"summaries, as the GPU step), 8 steps per run, median of 3 runs")
+    return out
 
 
 def swap_bench(torch, dev):
@@ -359,6 +399,7 @@ def main():
         }
         del kr, vr
 
+    dec_host = None
     if not args.no_decode:
         log("bench: C4 decode")
         ds = WL.make_decode(steps=args.decode_steps + 8)
@@ -414,6 +455,7 @@ def main():
             "speedup_vs_dense_hbm_floor": 2 * c4.Hkv * npre * c4.d * 2 / (PEAK_HBM_GBS * 1e6) / dms,
         }
         del kd, vd, qd, dec
+        dec_host = ds
 
     if not args.no_swap:
         log("bench: attention swap (ssa_masked forward + backward)")
@@ -505,16 +547,8 @@ def main():
         result["copy_calibration_bytes"] = x.numel() * 2
 
     if not args.no_cpu:
-        threads = len(os.sched_getaffinity(0))
-        try:
-            from threadpoolctl import threadpool_info
-            nt = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
-            if nt:
-                threads = int(max(nt))
-        except Exception:
-            pass
-        log(f"bench: CPU baseline on {threads} threads")
-        result["cpu_baseline"] = cpu_baseline(p, sum_kv, threads)
+        log("bench: CPU baseline (torch float32 restatement of the reference path)")
+        result["cpu_baseline"] = cpu_baseline(p, dec_host)
         try:
             model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
                          if l.startswith("model name"))
