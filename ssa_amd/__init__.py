@@ -9,5 +9,6 @@ API so callers switch by import path:
     ssa.ivf_decode  -> ssa_amd.ivf_decode   (decode_attend, dense_decode, RoutedDecoder)
 """
 from . import _lib  # noqa: F401
+from . import torch_ops  # noqa: F401  (registers the ssa_amd:: custom ops for torch.compile)
 
 __all__ = ["ssa_kernel", "gemma_ssa", "ivf_decode", "workloads"]

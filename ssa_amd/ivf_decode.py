@@ -28,6 +28,18 @@ def attend_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: torch
     """Per-query sparse attention: q (B, Hq, nq, d); caches k, v (B, Hkv, cap, d); row r of
     head (b, h) sits at absolute position pos + r and attends keys <= pos + r of the blocks
     kv_idx[b, h, r, :kv_num[b, h, r]] (fp32 softmax, output in q's dtype)."""
+    if torch.compiler.is_compiling():
+        from . import torch_ops as T
+        sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
+        o = T.attend_rows(q, k, v, kv_num, kv_idx, int(pos), int(block), sc)
+        if out is not None:
+            out.copy_(o)
+            o = out
+        return o
+    return _attend_rows_impl(q, k, v, kv_num, kv_idx, pos, block, scale, out)
+
+
+def _attend_rows_impl(q, k, v, kv_num, kv_idx, pos, block, scale=None, out=None):
     _lib.require_device(q, k, v, kv_num, kv_idx)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share a dtype")
@@ -167,6 +179,16 @@ class RoutedDecoder:
                 raise ValueError(f"step: {name} has shape {tuple(t.shape)}, expected {shape}")
             if t.stride(-1) != 1:
                 raise ValueError(f"step: {name} needs a contiguous last dimension")
+        if torch.compiler.is_compiling():
+            from . import torch_ops as T
+            o = T.decode_step(q, k_new, v_new, self.kcache, self.vcache, self.mu, self.var,
+                              self.kv_num, self.kv_idx, self.workspace, self.pos, self.block,
+                              self.top_c, self.budget_frac, self.local, self.coef2, self.scale)
+            self.pos += 1
+            if out is not None:
+                out.copy_(o)
+                o = out
+            return o
         if out is None:
             out = torch.empty(self.B, self.Hq, self.d, device=q.device, dtype=self.dtype)
         elif (out.dtype != self.dtype or tuple(out.shape) != (self.B, self.Hq, self.d)

@@ -56,6 +56,17 @@ def block_summary(x: torch.Tensor, block: int, mode: str = "pop", n_real: int | 
     ssa/ssa_swap.py:37-41); "unbiased": (mu, var) with var/(cnt-1) (ssa/ssa_kernel.py:43,47);
     "qmean": the query-block mean sum(rows)/block (ssa/ssa_kernel.py:44,79).
     """
+    if torch.compiler.is_compiling():
+        from . import torch_ops as T
+        if mode == "qmean":
+            return T.block_qmean(x, block)
+        mu, var, m3 = T.block_stats(x, block, mode == "unbiased",
+                                    -1 if n_real is None else int(n_real), bool(with_m3))
+        return mu, var, (m3 if with_m3 else None)
+    return _block_summary_impl(x, block, mode, n_real, with_m3)
+
+
+def _block_summary_impl(x, block, mode, n_real, with_m3):
     _lib.require_device(x)
     x = _aligned(x)
     B, H, n, d = x.shape
@@ -98,6 +109,17 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
     sub-blocks (ssa/ssa_kernel.py:100). Returns kv_num (B, Hq, nbq) int32 and
     kv_idx (B, Hq, nbq, W) int32 (ascending, padded 0).
     """
+    if torch.compiler.is_compiling():
+        from . import torch_ops as T
+        return T.route(rows, mu, var, m3, mode, -1 if top_c is None else int(top_c),
+                       float(budget_frac), int(local), float(coef2), float(coef3),
+                       int(query_pos), int(block), int(pool))
+    return _route_impl(rows, mu, var, m3, mode, top_c, budget_frac, local, coef2, coef3,
+                       query_pos, block, workspace_limit, pool)
+
+
+def _route_impl(rows, mu, var, m3, mode, top_c, budget_frac, local, coef2, coef3, query_pos,
+                block, workspace_limit=1 << 30, pool=1):
     _lib.require_device(rows, mu, var, m3)
     B, Hq, nbq, d = rows.shape
     Hkv, nbs = mu.shape[1], mu.shape[2]
@@ -186,6 +208,22 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
     (B, n, Hq, d) buffer). `vt` is an optional V^T from transpose_v(v, block).
     Returns out (and lse (B, Hq, n) fp32 if requested).
     """
+    if torch.compiler.is_compiling():  # V^T is rebuilt inside the op (vt is a cache only)
+        from . import torch_ops as T
+        sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else float(scale)
+        if return_lse:
+            o, lse = T.sparse_attention_lse(q, k, v, kv_num, kv_idx, int(block), sc)
+        else:
+            o, lse = T.sparse_attention(q, k, v, kv_num, kv_idx, int(block), sc), None
+        if out is not None:
+            out.copy_(o)
+            o = out
+        return (o, lse) if return_lse else o
+    return _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale, out, return_lse, vt)
+
+
+def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
+                           return_lse=False, vt=None):
     _lib.require_device(q, k, v, kv_num, kv_idx)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share a dtype")

@@ -139,3 +139,35 @@ def test_routing_projection_file_loads_without_pickle(tmp_path):
     torch.save({"W_q": wq, "W_k": wk, "meta": {"steps": 10, "name": "x"}}, path)
     p = G.load_projection(str(path), device="cpu")
     assert torch.equal(p.W_q, wq) and torch.equal(p.W_k, wk) and p.meta["steps"] == 10
+
+
+def test_custom_op_fake_shapes():
+    """The torch.library registrations (torch.compile's view of the kernels) give the shapes and
+    dtypes of the real entry points; checked on meta tensors (their fake implementations)."""
+    import torch
+    import ssa_amd  # noqa: F401  (registers the ops)
+    ops = torch.ops.ssa_amd
+    m = dict(device="meta")
+    q = torch.empty(1, 14, 1000, 64, dtype=torch.bfloat16, **m)
+    k = torch.empty(1, 2, 1000, 64, dtype=torch.bfloat16, **m)
+    assert ops.block_qmean(q, 128).shape == (1, 14, 8, 64)
+    mu, var, m3 = ops.block_stats(k, 128, False, 1000, True)
+    assert mu.shape == var.shape == m3.shape == (1, 2, 8, 64) and mu.dtype == torch.float32
+    assert ops.block_stats(k, 128, False, -1, False)[2].numel() == 0
+    qb = torch.empty(1, 14, 8, 64, dtype=torch.float32, **m)
+    kv_num, kv_idx = ops.route(qb, mu, var, None, "budget", 4, 0.0, 2, 1.0, 0.0, 0, 1, 1)
+    assert kv_num.shape == (1, 14, 8) and kv_idx.shape == (1, 14, 8, 7)
+    assert kv_idx.dtype == torch.int32
+    out = ops.sparse_attention(q, k, k, kv_num, kv_idx, 128, 0.125)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    o2, lse = ops.sparse_attention_lse(q, k, k, kv_num, kv_idx, 128, 0.125)
+    assert lse.shape == (1, 14, 1000) and lse.dtype == torch.float32
+    qd = torch.empty(1, 14, 64, dtype=torch.bfloat16, **m)
+    kc = torch.empty(1, 2, 4096, 64, dtype=torch.bfloat16, **m)
+    kn = torch.empty(1, 2, 64, dtype=torch.bfloat16, **m)
+    mus = torch.empty(1, 2, 32, 64, dtype=torch.float32, **m)
+    num = torch.empty(1, 14, dtype=torch.int32, **m)
+    idx = torch.empty(1, 14, 67, dtype=torch.int32, **m)
+    o = ops.decode_step(qd, kn, kn, kc, kc, mus, mus, num, idx, None, 100, 128, 64, 0.0, 1, 1.0,
+                        0.125)
+    assert o.shape == (1, 14, 64)
