@@ -418,7 +418,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   if (cnt < 0) cnt = 0;
   const int32_t* list = p.kv_idx + row * p.W;
   const int S = (int)(p.block / KT);
-  const int T = cnt * S;
 
   // Q fragments (B operands of S^T = K Q^T) of the column groups
   vec qf[CG][4];
@@ -506,31 +505,38 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   const uint32_t vgo = (uint32_t)(lr * p.n_pad + lc * 8);
   const int64_t kstep = 8 * NW * p.ksn, vstep = 8 * NW * p.n_pad;
 
-  // The row's block list, 64 entries at a time in one VGPR (entry lbase + e in lane e), read
-  // with v_readlane: no memory wait per sub-tile.
+  // Tile cursor over the row's block list: entry ce, sub-tile cs (key0 = list[ce]*block + cs*KT).
+  // The list is held 64 entries at a time in one VGPR (entry lbase + j in lane j), read with
+  // v_readlane: no memory wait per sub-tile. Key arithmetic is 32-bit (the host checks n < 2^31).
+  const int n32 = (int)p.n, blk32 = (int)p.block, nbq32 = (int)p.nbq, qmax32 = (int)qmax;
   int lbase = 0;
   int32_t lreg = lane < cnt ? list[lane] : -1;
-  auto tile_key0 = [&](int t) -> int64_t {
-    const int e = t / S;
-    if (e - lbase >= 64) {  // wave-uniform; once per 64 list entries
-      lbase = e;
-      lreg = e + lane < cnt ? list[e + lane] : -1;
+  int ce = 0, cs = -1;
+  // advances the cursor to the next tile that starts at or before the last query row and before
+  // n; returns its first key, or -1 past the list
+  auto next_tile = [&]() -> int {
+    while (true) {
+      if (++cs == S) {
+        cs = 0;
+        ++ce;
+      }
+      if (ce >= cnt) return -1;
+      if (ce - lbase >= 64) {  // wave-uniform; once per 64 list entries
+        lbase = ce;
+        lreg = ce + lane < cnt ? list[ce + lane] : -1;
+      }
+      const int c = __builtin_amdgcn_readlane(lreg, ce - lbase);
+      if (c >= 0 && c < nbq32) {
+        const int k0 = c * blk32 + cs * KT;
+        if (k0 <= qmax32 && k0 < n32) return k0;
+      }
+      cs = S - 1;  // later sub-tiles of this entry start later still (or the entry is invalid)
     }
-    const int32_t c = __builtin_amdgcn_readlane(lreg, e - lbase);
-    if (c < 0 || (int64_t)c >= p.nbq) return -1;
-    return (int64_t)c * p.block + (int64_t)(t % S) * KT;
   };
-  auto next_valid = [&](int t) -> int {
-    for (; t < T; ++t) {
-      const int64_t k0 = tile_key0(t);
-      if (k0 >= 0 && k0 <= qmax && k0 < p.n) break;
-    }
-    return t;
-  };
-  auto issue = [&](unsigned char* kdst, unsigned char* vdst, int64_t key0) {
+  auto issue = [&](unsigned char* kdst, unsigned char* vdst, int key0) {
     const unsigned short* kt = kbase + key0 * p.ksn;
     const unsigned short* vt = vtbase + key0;
-    if (key0 + KT <= p.n) {
+    if (key0 + KT <= n32) {
 #pragma unroll
       for (int j = 0; j < LPW; ++j)
         __builtin_amdgcn_global_load_lds(kt + j * kstep + kgo, kdst + j * 1024 * NW + w * 1024,
@@ -575,7 +581,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   }
   const float c2 = p.scale_log2;
 
-  auto compute = [&](const unsigned char* ks, const unsigned char* vs, int64_t key0) {
+  auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0) {
     // ---- S^T = K Q^T ----
     u32x4 ka[2][4];
 #pragma unroll
@@ -584,7 +590,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       for (int kd = 0; kd < 4; ++kd)
         ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * 4096);
     f32x16 sacc[2][CG];  // [tt][c]
-    __builtin_amdgcn_s_setprio(1);
+    if constexpr (!fast) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -595,7 +601,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         for (int kd = 0; kd < 4; ++kd)
           sacc[tt][c] = M::mma(M::from_bits(ka[tt][kd]), qf[c][kd], sacc[tt][c]);
       }
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (!fast) __builtin_amdgcn_s_setprio(0);
     // V^T fragments of the first two key steps, in flight during the softmax
     u32x4 va[4][2];
 #pragma unroll
@@ -604,11 +610,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       for (int dt = 0; dt < 2; ++dt)
         va[s][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s] + dt * 4096);
     // ---- mask (diagonal / ragged tail sub-tiles only) ----
-    if (key0 + KT - 1 > qw0 || key0 + KT > p.n) {
+    if (key0 + KT - 1 > (int)qw0 || key0 + KT > n32) {
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
-        const int lim_q = (int)(qpos[c] - key0);
-        const int lim_n = (int)(p.n - 1 - key0);
+        const int lim_q = (int)qpos[c] - key0;
+        const int lim_n = n32 - 1 - key0;
         const int lim = lim_q < lim_n ? lim_q : lim_n;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
@@ -620,7 +626,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       }
     }
     if constexpr (fast) {  // ---- bounded rows: P^T = 2^(S^T), O^T += V^T P^T ----
-      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (s < 2) {
@@ -644,7 +649,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
           for (int c = 0; c < CG; ++c)
             oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
       }
-      __builtin_amdgcn_s_setprio(0);
       return;
     }
     // ---- online softmax (lazy rescale) ----
@@ -706,24 +710,22 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   };
 
   // 2-stage ring, statically unrolled by two so each LDS access names its stage's array.
-  int t = next_valid(0);
-  int64_t key0 = t < T ? tile_key0(t) : 0;
-  if (t < T) issue(kst0, vst0, key0);
-  while (t < T) {
+  // (the cursor advances before each barrier: scalar work off the path from the barrier to
+  // the next tile's loads)
+  const int wlast = (int)qw0 + 32 * CG - 1;  // this wave's last query row
+  int key0 = next_tile();
+  if (key0 >= 0) issue(kst0, vst0, key0);
+  while (key0 >= 0) {
+    int key0n = next_tile();
     __syncthreads();  // stage 0 landed for all waves; stage 1 no longer read
-    int tn = next_valid(t + 1);
-    int64_t key0n = tn < T ? tile_key0(tn) : 0;
-    if (tn < T) issue(kst1, vst1, key0n);
-    if (key0 <= qw0 + 32 * CG - 1) compute(kst0, vst0, key0);
-    t = tn;
+    if (key0n >= 0) issue(kst1, vst1, key0n);
+    if (key0 <= wlast) compute(kst0, vst0, key0);
     key0 = key0n;
-    if (t >= T) break;
+    if (key0 < 0) break;
+    key0n = next_tile();
     __syncthreads();  // stage 1 landed; stage 0 no longer read
-    tn = next_valid(t + 1);
-    key0n = tn < T ? tile_key0(tn) : 0;
-    if (tn < T) issue(kst0, vst0, key0n);
-    if (key0 <= qw0 + 32 * CG - 1) compute(kst1, vst1, key0);
-    t = tn;
+    if (key0n >= 0) issue(kst0, vst0, key0n);
+    if (key0 <= wlast) compute(kst1, vst1, key0);
     key0 = key0n;
   }
 
@@ -833,6 +835,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(block == 64 || (block > 0 && block % 128 == 0), SSA_ERR_UNSUPPORTED,
               "sparse_attn: block %lld unsupported (64 or a multiple of 128)", (long long)block);
   SSA_REQUIRE(B * Hq < (1ll << 24), SSA_ERR_UNSUPPORTED, "sparse_attn: too many heads");
+  SSA_REQUIRE(n + block < (1ll << 31), SSA_ERR_UNSUPPORTED,
+              "sparse_attn: n = %lld too large (key positions are 32-bit)", (long long)n);
   SSA_REQUIRE((flags & ~SSA_ATTN_VT_READY) == 0, SSA_ERR_INVALID, "sparse_attn: unknown flags");
   const int64_t vec = dtype == SSA_F32 ? 4 : 8;
   for (int s = 0; s < 12; ++s)
