@@ -337,11 +337,350 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return base + incl - v;
 }
 
-// The K largest of a wave's entries (lane l, slot j: entry l + 64 j; cand marks the ncand real
-// ones) under the order (key desc, entry asc). The K-th largest key T is found bit by bit from
-// the top (count of keys >= T | bit by ballots); keys > T are taken, and keys == T in increasing
-// entry order until K are taken. Non-candidates must hold key 0: they never reach a threshold
-// >= 1, and at T = 0 the candidate flag keeps them out.
+// ---- certified scoring -------------------------------------------------------------------------
+// With approximate (fp32-MFMA) keys, a select kernel certifies its selection: with e a bound on
+// |approximate - exact| for every score of the row, and T~ the keep-th largest approximate score,
+// the exact keep-th largest lies within e of T~, so a candidate scoring above T~ + 2e is in the
+// exact top-keep and one below T~ - 2e is out; the candidates in between are rescored with the
+// exact formula (fp64 sums, fp32 assembly as route_score_kernel) and the remaining places go to
+// the best of them by (exact key, lowest block index) -- the exact router's selection.
+// e = (K + 16) u (1 + 2^-10) (|q| |mu|max + |c2| |q^2| |var|max + |c3| |q^3| |m3|max) + 2^-100:
+// a K-term fp32 dot product (K = 2d or 3d) is within K u sum|a_k b_k| of its exact value, the
+// pre-multiplied c2 q^2 and c3 q^3 add u each, the exact score's own roundings at most 5u of
+// sum|a_k b_k|, which Cauchy-Schwarz bounds by the norm products (the norm maxima are over the
+// 64-candidate tiles holding the row's candidates, in fp32 with the (1 + 2^-10) margin; 2^-100
+// covers flushed denormals). A non-finite bound or threshold makes every candidate uncertain.
+struct CertArgs {
+  int on;               // the keys are fp32-MFMA approximations to certify
+  const void* rows;     // (B, Hq, nbq, d) query rows of type g.rows_dt
+  const float* mu;
+  const float* var;     // may be NULL (coef2 = 0)
+  const float* m3;      // may be NULL
+  const float* tnorm;   // (B*Hkv, ntile, 4): max squared norms of mu, var, m3 per 64-candidate tile
+  int64_t ntile;
+  int d;
+  float coef2, coef3;
+};
+
+constexpr int kNormTile = 64;  // candidates (sub-block units) per norm tile
+constexpr int kBand = 512;     // capacity of a row's certificate band (larger: rescore the row)
+constexpr int kMaxQReg = 8;    // head dims per lane in the exact rescoring (d <= 512)
+
+// Bytes of the per-tile candidate norms at the start of a route workspace (4 floats per tile per
+// key head; B*Hq bounds B*Hkv).
+inline size_t route_norm_bytes(int64_t B, int64_t Hq, int64_t nbs) {
+  const size_t n = (size_t)B * (size_t)Hq * (size_t)((nbs + kNormTile - 1) / kNormTile) * 16u;
+  return (n + 255) / 256 * 256;
+}
+
+// Largest squared norms of the candidates' mu, var and m3 rows per 64-candidate tile (the
+// certificate's bound): grid (ceil(nbs / 64), B*Hkv), one wave, a lane per candidate.
+__global__ __launch_bounds__(64) void route_cand_norm_kernel(
+    const float* __restrict__ mu, const float* __restrict__ var, const float* __restrict__ m3,
+    int64_t nbs, int d, float* __restrict__ tnorm, int64_t ntile) {
+  const int64_t bk = blockIdx.y, t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t c = t * kNormTile + lane;
+  float n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+  if (c < nbs) {
+    const int64_t off = (bk * nbs + c) * d;
+    for (int k = 0; k < d; ++k) {
+      const float x = mu[off + k];
+      n1 = fmaf(x, x, n1);
+      if (var) {
+        const float y = var[off + k];
+        n2 = fmaf(y, y, n2);
+      }
+      if (m3) {
+        const float z = m3[off + k];
+        n3 = fmaf(z, z, n3);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    n1 = fmaxf(n1, __shfl_xor(n1, off, 64));
+    n2 = fmaxf(n2, __shfl_xor(n2, off, 64));
+    n3 = fmaxf(n3, __shfl_xor(n3, off, 64));
+  }
+  if (lane == 0) {
+    float* p = tnorm + (bk * ntile + t) * 4;
+    p[0] = n1;
+    p[1] = n2;
+    p[2] = n3;
+    p[3] = 0.0f;
+  }
+}
+
+// Approximate scores for the certified router: one fp32-MFMA contraction of the query rows
+// [q | c2 fl32(q*q) | c3 fl32(q*q*q)] against the candidates' [mu | var | m3] (K = 2d, 3d with
+// m3, d without var), 64 rows x 64 candidates per workgroup, each of the 4 waves a 32 x 32 block
+// on v_mfma_f32_32x32x2_f32 (lane l supplies A[l%32][l/32] and B[l/32][l%32]; accumulator j of
+// lane l is C[(j/4)*8 + (l/32)*4 + j%4][l%32]). Operands are staged in LDS 32 head dims at a
+// time, rows of 33 floats (conflict-free column reads). Same tile geometry and causal tile skip
+// as route_score_kernel; the keys are stored in the same workspace layout.
+template <bool EDGE, bool VEC>
+__global__ __launch_bounds__(256) void route_score_mfma_kernel(
+    const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
+    const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
+    unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
+  constexpr int KC = 32;
+  __shared__ float As[kTile][KC + 1];
+  __shared__ float Bs[kTile][KC + 1];
+  __shared__ int64_t row_off[kTile];
+
+  const int64_t bk = blockIdx.y;  // b * Hkv + kvh
+  const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
+  const int64_t rt = blockIdx.x / cand_tiles, ct = blockIdx.x % cand_tiles;
+  const int64_t R = g.G * g.ni;
+  const int64_t r0 = rt * kTile;
+  const int64_t c0 = ct * kTile;
+  if (r0 >= R) return;
+  const int64_t r_last = r0 + kTile - 1 < R ? r0 + kTile - 1 : R - 1;
+  const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
+  if (c0 >= row_cmax_s(g, imax)) return;  // uniform: no row of the tile has these candidates
+  const int64_t nbs = g.nbk * g.pool;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wr = w & 1, wc = w >> 1;
+  if (tid < kTile) {
+    const int64_t r = r0 + tid;
+    int64_t off = -1;
+    if (r < R) {
+      const int64_t h = kvh * g.G + r / g.ni;
+      const int64_t ii = g.i0 + r % g.ni;
+      off = ((b * g.Hq + h) * g.nbq + ii) * d;
+    }
+    row_off[tid] = off;
+  }
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  for (int term = 0; term < (EDGE ? 3 : 2); ++term) {
+    if (term == 1 && var == nullptr) continue;  // centroid routing: no variance term
+    const float* src = (term == 0 ? mu : term == 1 ? var : m3) + (bk * nbs) * d;
+    const float cf = term == 0 ? 1.0f : term == 1 ? coef2 : coef3;
+    for (int k0 = 0; k0 < d; k0 += KC) {
+      __syncthreads();
+      if (VEC) {  // thread: 8 consecutive head dims of one row and of one candidate (16-byte loads)
+        const int rr = tid >> 2, k8 = (tid & 3) * 8;
+        const int64_t roff = row_off[rr];
+        float q[8], bv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = bv[e] = 0.0f;
+        if (roff >= 0 && k0 + k8 < d) {
+          if (g.rows_dt == SSA_F32) {
+            const f32x4* pq = reinterpret_cast<const f32x4*>(static_cast<const float*>(rows) + roff + k0 + k8);
+            const f32x4 x0 = pq[0], x1 = pq[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              q[e] = x0[e];
+              q[4 + e] = x1[e];
+            }
+          } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(
+                static_cast<const unsigned short*>(rows) + roff + k0 + k8);
+            unpack8(w, q, g.rows_dt == SSA_BF16);
+          }
+        }
+        const int64_t cand = c0 + rr;
+        if (cand < nbs && k0 + k8 < d) {
+          const f32x4* pb = reinterpret_cast<const f32x4*>(src + cand * d + k0 + k8);
+          const f32x4 y0 = pb[0], y1 = pb[1];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bv[e] = y0[e];
+            bv[4 + e] = y1[e];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float a = q[e];
+          if (term == 1) a = cf * (q[e] * q[e]);
+          else if (term == 2) a = cf * ((q[e] * q[e]) * q[e]);
+          As[rr][k8 + e] = a;
+          Bs[rr][k8 + e] = bv[e];
+        }
+      } else {
+#pragma unroll
+        for (int idx = tid; idx < kTile * KC; idx += 256) {
+          const int rr = idx / KC, kk = idx % KC;
+          const int64_t roff = row_off[rr];
+          float q = 0.0f;
+          if (roff >= 0 && k0 + kk < d) q = load_row(rows, roff + k0 + kk, g.rows_dt);
+          float a = q;
+          if (term == 1) a = cf * (q * q);
+          else if (term == 2) a = cf * ((q * q) * q);
+          As[rr][kk] = a;
+          const int64_t cand = c0 + rr;
+          Bs[rr][kk] = (cand < nbs && k0 + kk < d) ? src[cand * d + k0 + kk] : 0.0f;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < KC; kk += 2) {
+        const float a = As[wr * 32 + (lane & 31)][kk + (lane >> 5)];
+        const float bb = Bs[wc * 32 + (lane & 31)][kk + (lane >> 5)];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+      }
+    }
+  }
+  const int64_t cand = c0 + wc * 32 + (lane & 31);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int64_t r = r0 + wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+    if (r >= R) continue;
+    const int64_t h = kvh * g.G + r / g.ni;
+    const int64_t il = r % g.ni;
+    if (cand >= row_cmax_s(g, g.i0 + il)) continue;
+    keys[((b * g.Hq + h) * g.ni + il) * nbs + cand] = score_key(acc[j]);
+  }
+}
+
+
+// Inverse of score_key.
+__device__ inline float key_value(unsigned int k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ inline double wave_sum_f64(double x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// The wave loads query row `roff` (element offset) into qreg (lane l: dims l + 64 t) and returns
+// the norms |q|, |q^2|, |q^3| of its fp32 elementwise powers (every lane).
+__device__ inline void cert_load_row(const CertArgs& ca, int rows_dt, int64_t roff,
+                                     float (&qreg)[kMaxQReg], float* n1, float* n2, float* n3) {
+  const int lane = threadIdx.x & 63;
+  float s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+  for (int t = 0; t < kMaxQReg; ++t) {
+    const int k = lane + 64 * t;
+    float q = 0.0f;
+    if (k < ca.d) q = load_row(ca.rows, roff + k, rows_dt);
+    qreg[t] = q;
+    const float q2 = q * q, q3 = q2 * q;
+    s1 = fmaf(q, q, s1);
+    s2 = fmaf(q2, q2, s2);
+    s3 = fmaf(q3, q3, s3);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    s1 += __shfl_xor(s1, off, 64);
+    s2 += __shfl_xor(s2, off, 64);
+    s3 += __shfl_xor(s3, off, 64);
+  }
+  *n1 = sqrtf(s1);
+  *n2 = sqrtf(s2);
+  *n3 = sqrtf(s3);
+}
+
+// Largest squared candidate norms over the norm tiles of candidates [0, cmax_s) of key head bk,
+// reduced by `nthreads` threads starting at thread `t0` (results via the returned maxima of each
+// thread; the caller reduces).
+__device__ inline void cert_tile_max(const CertArgs& ca, int64_t bk, int64_t cmax_s, int tid,
+                                     int nthreads, float* m1, float* m2, float* m3) {
+  const int64_t nt = (cmax_s + kNormTile - 1) / kNormTile;
+  float a = 0.0f, b = 0.0f, c = 0.0f;
+  for (int64_t t = tid; t < nt; t += nthreads) {
+    const float* p = ca.tnorm + (bk * ca.ntile + t) * 4;
+    a = fmaxf(a, p[0]);
+    b = fmaxf(b, p[1]);
+    c = fmaxf(c, p[2]);
+  }
+  *m1 = a;
+  *m2 = b;
+  *m3 = c;
+}
+
+// (lo, hi) score keys of the certificate band around the approximate threshold key T.
+__device__ inline void cert_band(const CertArgs& ca, unsigned int T, float qn1, float qn2,
+                                 float qn3, float max1, float max2, float max3,
+                                 unsigned int* lo, unsigned int* hi) {
+  const int K = (1 + (ca.var ? 1 : 0) + (ca.m3 ? 1 : 0)) * ca.d;
+  const double u = 5.9604644775390625e-08;  // 2^-24
+  const double mag = (double)qn1 * sqrt((double)max1) +
+                     fabs((double)ca.coef2) * (double)qn2 * sqrt((double)max2) +
+                     fabs((double)ca.coef3) * (double)qn3 * sqrt((double)max3);
+  const double e = (K + 16) * u * (1.0 + 0x1p-10) * mag + 0x1p-100;
+  const double tau = (double)key_value(T);
+  if (!(e < 1e300) || !(fabs(tau) < 1e300)) {  // non-finite: certify nothing
+    *lo = 0u;
+    *hi = 0xffffffffu;
+    return;
+  }
+  const double lod = tau - 2.0 * e, hid = tau + 2.0 * e;
+  float lof = (float)lod, hif = (float)hid;
+  // round outward: the adjacent float below / above (x finite)
+  if ((double)lof > lod) {
+    const unsigned int ub = __float_as_uint(lof);
+    lof = lof > 0.0f ? __uint_as_float(ub - 1u) : lof < 0.0f ? __uint_as_float(ub + 1u)
+                                                              : -__uint_as_float(1u);
+  }
+  if ((double)hif < hid) {
+    const unsigned int ub = __float_as_uint(hif);
+    hif = hif > 0.0f ? __uint_as_float(ub + 1u) : hif < 0.0f ? __uint_as_float(ub - 1u)
+                                                              : __uint_as_float(1u);
+  }
+  *lo = score_key(lof);
+  *hi = score_key(hif);
+}
+
+// Exact score key of candidate block c of the row held in qreg (its key head's summaries at
+// element offset cbase of candidate 0): the fp64-accumulated formula of route_score_kernel, the
+// max over the block's pool sub-blocks, computed by one wave.
+__device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&qreg)[kMaxQReg],
+                                              int64_t cbase, int64_t c, int64_t pool) {
+  const int lane = threadIdx.x & 63;
+  unsigned int best = 0u;
+  for (int64_t s = 0; s < pool; ++s) {
+    const int64_t off = cbase + (c * pool + s) * ca.d;
+    double e1 = 0.0, e2 = 0.0, e3 = 0.0;
+#pragma unroll
+    for (int t = 0; t < kMaxQReg; ++t) {
+      const int k = lane + 64 * t;
+      if (k < ca.d) {
+        const float q = qreg[t], q2 = q * q;
+        e1 = fma((double)q, (double)ca.mu[off + k], e1);
+        if (ca.var) e2 = fma((double)q2, (double)ca.var[off + k], e2);
+        if (ca.m3) e3 = fma((double)(q2 * q), (double)ca.m3[off + k], e3);
+      }
+    }
+    e1 = wave_sum_f64(e1);
+    e2 = wave_sum_f64(e2);
+    float sc = __fadd_rn((float)e1, __fmul_rn(ca.coef2, (float)e2));
+    if (ca.m3) sc = __fadd_rn(sc, __fmul_rn(ca.coef3, (float)wave_sum_f64(e3)));
+    const unsigned int k = score_key(sc);
+    best = k > best ? k : best;
+  }
+  return best;
+}
+
+// The K-th largest of a wave's entries (lane l, slot j: entry l + 64 j; non-candidates hold
+// key 0), found bit by bit from the top (count of keys >= T | bit by ballots), or the first
+// prefix with exactly K keys >= T -- then no tie straddles the cut. Requires 0 < K < #candidates.
+template <int J>
+__device__ inline unsigned int wave_kth_key(const unsigned int (&key)[J], int64_t K) {
+  unsigned int T = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const unsigned int t = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= t));
+    if (cnt >= K) {
+      T = t;
+      if (cnt == K) break;  // wave-uniform
+    }
+  }
+  return T;
+}
+
+// The K largest of a wave's entries (cand marks the ncand real ones) under the order (key desc,
+// entry asc): keys > T (the K-th largest) are taken, and keys == T in increasing entry order until
+// K are taken. Non-candidates must hold key 0: they never reach a threshold >= 1, and at T = 0
+// the candidate flag keeps them out.
 template <int J>
 __device__ inline void wave_select_top(const unsigned int (&key)[J], const bool (&cand)[J],
                                        int64_t K, int64_t ncand, bool (&sel)[J]) {
@@ -357,20 +696,7 @@ __device__ inline void wave_select_top(const unsigned int (&key)[J], const bool 
     for (int j = 0; j < J; ++j) sel[j] = false;
     return;
   }
-  // T: the largest value with #{keys >= T} >= K (the K-th largest key), or the first prefix
-  // found with exactly K keys >= T -- then no tie straddles the cut, and the tie step below
-  // takes every key equal to T (none, or all of them)
-  unsigned int T = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
-    const unsigned int t = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= t));
-    if (cnt >= K) {
-      T = t;
-      if (cnt == K) break;  // wave-uniform
-    }
-  }
+  const unsigned int T = wave_kth_key<J>(key, K);
   int above = 0;
 #pragma unroll
   for (int j = 0; j < J; ++j) above += __popcll(__ballot(cand[j] && key[j] > T));
@@ -395,25 +721,31 @@ constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
 // go to LDS and the radix select runs on them (rows whose filter keeps more than kCand keys use
 // the full row). Filtering also pays for staged rows: the digit histograms of a few hundred
 // survivors see far fewer same-bin atomics than those of thousands of similar keys.
+// Approximate keys (ca.on) are certified: the band candidates, collected in block order, are
+// rescored exactly and the remaining places chosen among them by a second radix select; a band
+// of more than kCand candidates falls back to rescoring the whole row into the workspace and
+// selecting on the exact keys.
 template <int NT>
 __global__ __launch_bounds__(NT) void route_select_kernel(
-    const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int64_t W) {
+    unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
+    int32_t* __restrict__ kv_idx, int64_t W, CertArgs ca) {
   __shared__ unsigned int bits[kMaxNbk / 32];
   __shared__ unsigned int cache[kCacheKeys];  // the row's keys, or the filtered candidates
   __shared__ unsigned int cidx[kCand];        // candidate block indices (filtered rows)
   __shared__ unsigned int hist[256];
   __shared__ int wave_sums[NT / 64];
-  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand, sh_whole;
+  __shared__ unsigned int bidx[kBand], bkey[kBand];  // the certificate band
+  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand, sh_whole, sh_nin, sh_nunc;
+  __shared__ float sh_norm[3 * (NT / 64)];
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
   const int64_t bh = lrow / g.ni, il = lrow % g.ni;
   const int64_t i = g.i0 + il;
   const int64_t cmax = row_cmax(g, i);
   int64_t keep = row_keep(g, cmax);
   const int64_t K = keep < cmax ? keep : cmax;
-  const unsigned int* kraw = keys + lrow * g.nbk * g.pool;
+  unsigned int* kraw = keys + lrow * g.nbk * g.pool;
   // key of block c: the largest of its pool sub-block keys (keys order like the scores, so this is
   // the key of the max-pooled score)
   auto krow = [&](int64_t c) -> unsigned int {
@@ -426,76 +758,19 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     return m;
   };
   const int nwords = (int)((g.nbk + 31) / 32);
-
-  for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
   const bool cached = cmax <= kCacheKeys;  // whole row in LDS, index order
-  if (cached && K > 0 && K < cmax)
-    for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow(c);
-  if (tid == 0) {
-    sh_min = 0xffffffffu;
-    sh_ncand = 0u;
-  }
-  __syncthreads();
+  bool cert = ca.on && K > 0 && K < cmax;
 
-  // keys the radix select runs over: src[0, nsel), block index of entry c: filt ? cidx[c] : c
-  bool filt = false;
-  int64_t nsel = cmax;
-  if (K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
-    int pk = 1;
-    while (pk < K) pk <<= 1;
-    const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
-    unsigned int mx = 0u;
-    for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = cached ? cache[c] : krow(c);
-      mx = key > mx ? key : mx;
-    }
-    for (int off = 1; off < gs; off <<= 1) {
-      const unsigned int o = __shfl_xor(mx, off, 64);
-      mx = o > mx ? o : mx;
-    }
-    // every lane now holds its group's maximum: T0 = the minimum over all lanes
-    for (int off = 1; off < 64; off <<= 1) {
-      const unsigned int o = __shfl_xor(mx, off, 64);
-      mx = o < mx ? o : mx;
-    }
-    if (lane == 0) atomicMin(&sh_min, mx);
-    __syncthreads();
-    const unsigned int t0 = sh_min;
-    for (int64_t c = tid; c < cmax; c += NT) {
-      const unsigned int key = cached ? cache[c] : krow(c);
-      if (key >= t0) {
-        const unsigned int slot = atomicAdd(&sh_ncand, 1u);
-        if (slot < (unsigned int)kCand) {
-          if (!cached) cache[slot] = key;  // a cached row keeps its keys in place
-          cidx[slot] = (unsigned int)c;
-        }
-      }
-    }
-    __syncthreads();
-    if (sh_ncand <= (unsigned int)kCand) {
-      filt = true;
-      nsel = sh_ncand;
-    }
-  }
-  auto src = [&](int64_t c) -> unsigned int {
-    if (filt) return cached ? cache[cidx[c]] : cache[c];
-    return cached ? cache[c] : krow(c);
-  };
-  auto mark = [&](int64_t c) {
-    const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
-    atomicOr(&bits[blk >> 5], 1u << (blk & 31));
-  };
-
-  if (K >= cmax) {
-    for (int64_t c = tid; c < cmax; c += NT) atomicOr(&bits[c >> 5], 1u << (c & 31));
-  } else if (K > 0) {
+  // radix select of the K-th largest of src(0..n): returns T, with *rank = the rank of T among
+  // the keys equal to it that is still to take, *whole = every key equal to T is taken
+  auto radix_kth = [&](auto src, int64_t n, unsigned int kk, unsigned int* rank,
+                       bool* whole_out) -> unsigned int {
     unsigned int prefix = 0u, pmask = 0u;
-    unsigned int kk = (unsigned int)K;  // rank of T among keys matching the prefix
     bool whole = false;
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int t = tid; t < 256; t += NT) hist[t] = 0u;
       __syncthreads();
-      for (int64_t c = tid; c < nsel; c += NT) {
+      for (int64_t c = tid; c < n; c += NT) {
         const unsigned int key = src(c);
         if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
@@ -534,31 +809,183 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
       // tie straddles the cut and the remaining digits need not be resolved
       if (whole) break;
     }
-    const unsigned int T = prefix;
-    const unsigned int need_eq = kk;                   // keys equal to T still to take
-    const unsigned int n_eq = whole ? kk : hist[T & 255u];  // keys equal to T (all >= T0)
+    *rank = kk;
+    *whole_out = whole;
+    return prefix;
+  };
+
+  for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (cached && K > 0 && K < cmax)
+      for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow(c);
+    if (tid == 0) {
+      sh_min = 0xffffffffu;
+      sh_ncand = 0u;
+    }
     __syncthreads();
-    if (need_eq == n_eq) {
-      for (int64_t c = tid; c < nsel; c += NT)
-        if (src(c) >= T) mark(c);
-    } else {
-      for (int64_t c = tid; c < nsel; c += NT)
-        if (src(c) > T) mark(c);
-      // ties at T: the lowest block indices first (scan in index order)
-      unsigned int taken = 0;
-      for (int64_t base = 0; base < cmax && taken < need_eq; base += NT) {
-        const int64_t c = base + tid;
-        int flag = 0;
-        if (c < cmax) {
-          const unsigned int key = cached ? cache[c] : krow(c);
-          flag = key == T;
+
+    // keys the radix select runs over: src[0, nsel), block index of entry c: filt ? cidx[c] : c
+    bool filt = false;
+    int64_t nsel = cmax;
+    if (K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
+      int pk = 1;
+      while (pk < K) pk <<= 1;
+      const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
+      unsigned int mx = 0u;
+      for (int64_t c = tid; c < cmax; c += NT) {
+        const unsigned int key = cached ? cache[c] : krow(c);
+        mx = key > mx ? key : mx;
+      }
+      for (int off = 1; off < gs; off <<= 1) {
+        const unsigned int o = __shfl_xor(mx, off, 64);
+        mx = o > mx ? o : mx;
+      }
+      // every lane now holds its group's maximum: T0 = the minimum over all lanes
+      for (int off = 1; off < 64; off <<= 1) {
+        const unsigned int o = __shfl_xor(mx, off, 64);
+        mx = o < mx ? o : mx;
+      }
+      if (lane == 0) atomicMin(&sh_min, mx);
+      __syncthreads();
+      const unsigned int t0 = sh_min;
+      for (int64_t c = tid; c < cmax; c += NT) {
+        const unsigned int key = cached ? cache[c] : krow(c);
+        if (key >= t0) {
+          const unsigned int slot = atomicAdd(&sh_ncand, 1u);
+          if (slot < (unsigned int)kCand) {
+            if (!cached) cache[slot] = key;  // a cached row keeps its keys in place
+            cidx[slot] = (unsigned int)c;
+          }
         }
-        int tot;
-        int pre = block_exclusive_scan<NT>(flag, wave_sums, &tot);
-        if (flag && taken + (unsigned int)pre < need_eq) atomicOr(&bits[c >> 5], 1u << (c & 31));
-        taken += (unsigned int)tot;
+      }
+      __syncthreads();
+      if (sh_ncand <= (unsigned int)kCand) {
+        filt = true;
+        nsel = sh_ncand;
       }
     }
+    auto src = [&](int64_t c) -> unsigned int {
+      if (filt) return cached ? cache[cidx[c]] : cache[c];
+      return cached ? cache[c] : krow(c);
+    };
+    auto mark = [&](int64_t c) {
+      const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
+      atomicOr(&bits[blk >> 5], 1u << (blk & 31));
+    };
+    auto rowkey = [&](int64_t c) -> unsigned int { return cached ? cache[c] : krow(c); };
+
+    if (K >= cmax) {
+      for (int64_t c = tid; c < cmax; c += NT) atomicOr(&bits[c >> 5], 1u << (c & 31));
+      break;
+    }
+    if (K <= 0) break;
+    unsigned int need_eq;
+    bool whole;
+    const unsigned int T = radix_kth(src, nsel, (unsigned int)K, &need_eq, &whole);
+    if (!cert) {
+      const unsigned int n_eq = whole ? need_eq : hist[T & 255u];  // keys equal to T
+      __syncthreads();
+      if (need_eq == n_eq) {
+        for (int64_t c = tid; c < nsel; c += NT)
+          if (src(c) >= T) mark(c);
+      } else {
+        for (int64_t c = tid; c < nsel; c += NT)
+          if (src(c) > T) mark(c);
+        // ties at T: the lowest block indices first (scan in index order)
+        unsigned int taken = 0;
+        for (int64_t base = 0; base < cmax && taken < need_eq; base += NT) {
+          const int64_t c = base + tid;
+          const int flag = c < cmax && rowkey(c) == T;
+          int tot;
+          int pre = block_exclusive_scan<NT>(flag, wave_sums, &tot);
+          if (flag && taken + (unsigned int)pre < need_eq)
+            atomicOr(&bits[c >> 5], 1u << (c & 31));
+          taken += (unsigned int)tot;
+        }
+      }
+      break;
+    }
+
+    // ---- certify the approximate selection ----
+    const int64_t b = bh / g.Hq, h = bh % g.Hq;
+    const int64_t bk = b * g.Hkv + h / g.G;
+    const int64_t cbase = bk * g.nbk * g.pool * ca.d;
+    float qreg[kMaxQReg], qn1, qn2, qn3;
+    cert_load_row(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg, &qn1, &qn2, &qn3);
+    {
+      float a, bb, c3;
+      cert_tile_max(ca, bk, cmax * g.pool, tid, NT, &a, &bb, &c3);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        a = fmaxf(a, __shfl_xor(a, off, 64));
+        bb = fmaxf(bb, __shfl_xor(bb, off, 64));
+        c3 = fmaxf(c3, __shfl_xor(c3, off, 64));
+      }
+      if (lane == 0) {
+        sh_norm[3 * wv] = a;
+        sh_norm[3 * wv + 1] = bb;
+        sh_norm[3 * wv + 2] = c3;
+      }
+      if (tid == 0) {
+        sh_nin = 0u;
+        sh_nunc = 0u;
+      }
+      __syncthreads();
+    }
+    float mx1 = 0.0f, mx2 = 0.0f, mx3 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      mx1 = fmaxf(mx1, sh_norm[3 * w]);
+      mx2 = fmaxf(mx2, sh_norm[3 * w + 1]);
+      mx3 = fmaxf(mx3, sh_norm[3 * w + 2]);
+    }
+    unsigned int lo, hi;
+    cert_band(ca, T, qn1, qn2, qn3, mx1, mx2, mx3, &lo, &hi);
+    // classify: above the band -> taken; in the band -> listed for exact rescoring. When the band
+    // lies above the filter threshold, the filtered list holds every candidate it can contain.
+    const bool in_list = filt && lo >= sh_min;
+    const int64_t nscan = in_list ? nsel : cmax;
+    for (int64_t c = tid; c < nscan; c += NT) {
+      const unsigned int key = in_list ? src(c) : rowkey(c);
+      const unsigned int blk = in_list ? cidx[c] : (unsigned int)c;
+      if (key > hi) {
+        atomicOr(&bits[blk >> 5], 1u << (blk & 31));
+        atomicAdd(&sh_nin, 1u);
+      } else if (key >= lo) {
+        const unsigned int slot = atomicAdd(&sh_nunc, 1u);
+        if (slot < (unsigned int)kBand) bidx[slot] = blk;
+      }
+    }
+    __syncthreads();
+    const unsigned int nin = sh_nin, nunc = sh_nunc;
+    if (nunc <= (unsigned int)kBand) {
+      // rescore the band exactly (a wave per candidate)
+      for (unsigned int u = wv; u < nunc; u += NT / 64) {
+        const unsigned int k = cert_exact_key(ca, qreg, cbase, bidx[u], g.pool);
+        if (lane == 0) bkey[u] = k;
+      }
+      __syncthreads();
+      // the band's best K - nin by (exact key, lowest block): taken when fewer rank above
+      const unsigned int m = (unsigned int)K - nin;
+      for (unsigned int u = tid; u < nunc; u += NT) {
+        const unsigned int ku = bkey[u], cu = bidx[u];
+        unsigned int above = 0;
+        for (unsigned int v = 0; v < nunc; ++v)
+          above += (bkey[v] > ku || (bkey[v] == ku && bidx[v] < cu)) ? 1u : 0u;
+        if (above < m) atomicOr(&bits[cu >> 5], 1u << (cu & 31));
+      }
+      break;
+    }
+    // a wide band: rescore the whole row exactly into its keys and select again
+    for (int64_t c = wv; c < cmax; c += NT / 64) {
+      const unsigned int k = cert_exact_key(ca, qreg, cbase, c, g.pool);
+      if (lane == 0)
+        for (int64_t t = 0; t < g.pool; ++t) kraw[c * g.pool + t] = k;
+    }
+    __threadfence_block();
+    for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
+    __syncthreads();
+    cert = false;
   }
   __syncthreads();
   // own block and its `local` predecessors, clipped to [0, own] and to existing blocks
@@ -593,12 +1020,13 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
 
 // Rows of at most 64 * J key blocks: one wave per row, lane l holds candidates l + 64 j
 // (wave_select_top); the selection plus the local window is compacted in ascending order from
-// the per-j ballots.
-
+// the per-j ballots. Approximate keys (ca.on) are certified in place: band candidates are
+// rescored exactly (a wave per candidate), those above the band take the largest key, those
+// below leave the candidates, and the selection runs again on the patched keys.
 template <int kSmallJ>
 __global__ __launch_bounds__(256) void route_select_small_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows) {
+    int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows, CertArgs ca) {
   const int lane = threadIdx.x & 63;
   const int64_t lrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (lrow >= nrows) return;  // whole wave
@@ -626,7 +1054,62 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     key[j] = m;
   }
   bool sel[kSmallJ];
-  wave_select_top<kSmallJ>(key, cand, K, cmax, sel);
+  if (ca.on && K > 0 && K < cmax) {
+    const unsigned int T = wave_kth_key<kSmallJ>(key, K);
+    const int64_t b = bh / g.Hq, h = bh % g.Hq;
+    const int64_t bk = b * g.Hkv + h / g.G;
+    float qreg[kMaxQReg], qn1, qn2, qn3;
+    cert_load_row(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg, &qn1, &qn2, &qn3);
+    float m1, m2, m3;
+    cert_tile_max(ca, bk, cmax * g.pool, lane, 64, &m1, &m2, &m3);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      m1 = fmaxf(m1, __shfl_xor(m1, off, 64));
+      m2 = fmaxf(m2, __shfl_xor(m2, off, 64));
+      m3 = fmaxf(m3, __shfl_xor(m3, off, 64));
+    }
+    unsigned int lo, hi;
+    cert_band(ca, T, qn1, qn2, qn3, m1, m2, m3, &lo, &hi);
+    const int64_t cbase = bk * g.nbk * g.pool * ca.d;
+    // above the band: taken; in the band: rescored exactly; below: out
+    bool unc[kSmallJ];
+    int nin = 0;
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) {
+      sel[j] = cand[j] && key[j] > hi;
+      unc[j] = cand[j] && !sel[j] && key[j] >= lo;
+      nin += __popcll(__ballot(sel[j]));
+      unsigned long long bu = __ballot(unc[j]);
+      while (bu) {  // wave-uniform loop over the band candidates of this slot
+        const int src_lane = __ffsll((long long)bu) - 1;
+        bu &= bu - 1;
+        const unsigned int k = cert_exact_key(ca, qreg, cbase, src_lane + 64 * j, g.pool);
+        if (lane == src_lane) key[j] = k;
+      }
+    }
+    // the band's best K - nin by (exact key, lowest block): a band candidate is taken when fewer
+    // than K - nin band candidates rank above it (a wave-uniform loop over the band candidates)
+    const int m = (int)K - nin;
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) {
+      unsigned long long bu = __ballot(unc[j]);
+      while (bu) {
+        const int src_lane = __ffsll((long long)bu) - 1;
+        bu &= bu - 1;
+        const unsigned int kc = __shfl(key[j], src_lane, 64);
+        const int cc = src_lane + 64 * j;
+        int above = 0;
+#pragma unroll
+        for (int jj = 0; jj < kSmallJ; ++jj) {
+          const int c2 = lane + 64 * jj;
+          above += __popcll(__ballot(unc[jj] && (key[jj] > kc || (key[jj] == kc && c2 < cc))));
+        }
+        if (lane == src_lane) sel[j] = above < m;
+      }
+    }
+  } else {
+    wave_select_top<kSmallJ>(key, cand, K, cmax, sel);
+  }
   const int64_t own = row_own(g, i);
   int64_t lo = own - g.local;
   if (lo < 0) lo = 0;
@@ -860,7 +1343,21 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
   SSA_REQUIRE(workspace != nullptr && workspace_bytes >= row_bytes * rows_per_i,
               SSA_ERR_WORKSPACE, "route: workspace of %zu bytes below the minimum %zu",
               workspace_bytes, row_bytes * rows_per_i);
-  int64_t chunk = (int64_t)(workspace_bytes / (row_bytes * rows_per_i));
+  // The certified fp32-MFMA scoring needs the per-tile candidate norms in front of the keys;
+  // without room for them (a workspace sized for the keys alone) the fp64 scoring runs.
+  const int64_t nbs = nbk * pool;
+  const int64_t ntile = (nbs + kNormTile - 1) / kNormTile;
+  const size_t norm_bytes = route_norm_bytes(B, Hq, nbs);
+  const bool mfma_ok = d <= 64 * kMaxQReg && workspace_bytes >= norm_bytes + row_bytes * rows_per_i;
+  char* ws = static_cast<char*>(workspace);
+  size_t key_bytes = workspace_bytes;
+  float* tnorm = nullptr;
+  if (mfma_ok) {
+    tnorm = reinterpret_cast<float*>(ws);
+    ws += norm_bytes;
+    key_bytes -= norm_bytes;
+  }
+  int64_t chunk = (int64_t)(key_bytes / (row_bytes * rows_per_i));
   if (chunk > nbq) chunk = nbq;
 
   RouteGeom g;
@@ -896,7 +1393,10 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                                         kv_num, kv_idx, W);
     return launch_status("route_rows_small_kernel");
   }
-  unsigned int* keys = static_cast<unsigned int*>(workspace);
+  unsigned int* keys = reinterpret_cast<unsigned int*>(ws);
+  CertArgs ca{};
+  ca.on = 0;
+  bool norms_done = false;
   for (int64_t i0 = 0; i0 < nbq; i0 += chunk) {
     g.i0 = i0;
     g.ni = nbq - i0 < chunk ? nbq - i0 : chunk;
@@ -906,6 +1406,7 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     const int64_t cmax_all = row_cmax_s(g, imax);  // scored candidates (sub-block units)
     const int64_t cand_tiles = cmax_all > 0 ? (cmax_all + kTile - 1) / kTile : 0;
     if (cand_tiles > 0 && R <= 16) {
+      ca.on = 0;
       int rp_log2 = 0;
       while ((1 << rp_log2) < R) ++rp_log2;
       const int64_t cpb = 256 >> rp_log2;
@@ -920,9 +1421,47 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
         route_score_rows_kernel<false><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d,
                                                                  coef2, coef3, keys, rp_log2);
       SSA_TRY(launch_status("route_score_rows_kernel"));
+    } else if (cand_tiles > 0 && mfma_ok) {
+      SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536 && ntile < (1ll << 31),
+                  SSA_ERR_UNSUPPORTED, "route: score grid too large");
+      if (!norms_done) {
+        route_cand_norm_kernel<<<dim3((unsigned)ntile, (unsigned)(B * Hkv)), 64, 0, stream>>>(
+            mu, var, m3, nbs, (int)d, tnorm, ntile);
+        SSA_TRY(launch_status("route_cand_norm_kernel"));
+        norms_done = true;
+      }
+      ca.on = 1;
+      ca.rows = rows;
+      ca.mu = mu;
+      ca.var = var;
+      ca.m3 = m3;
+      ca.tnorm = tnorm;
+      ca.ntile = ntile;
+      ca.d = (int)d;
+      ca.coef2 = coef2;
+      ca.coef3 = coef3;
+      dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
+      // 16-byte staging loads: d a multiple of 8 and 16-byte aligned rows and summaries
+      const bool vec = d % 8 == 0 && (reinterpret_cast<uintptr_t>(rows) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(mu) & 15u) == 0 &&
+                       (var == nullptr || (reinterpret_cast<uintptr_t>(var) & 15u) == 0) &&
+                       (m3 == nullptr || (reinterpret_cast<uintptr_t>(m3) & 15u) == 0);
+#define SSA_SCORE_MFMA(E, V)                                                                       \
+  route_score_mfma_kernel<E, V><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,    \
+                                                          coef3, keys, row_tiles, cand_tiles)
+      if (m3 != nullptr) {
+        if (vec) SSA_SCORE_MFMA(true, true);
+        else SSA_SCORE_MFMA(true, false);
+      } else {
+        if (vec) SSA_SCORE_MFMA(false, true);
+        else SSA_SCORE_MFMA(false, false);
+      }
+#undef SSA_SCORE_MFMA
+      SSA_TRY(launch_status("route_score_mfma_kernel"));
     } else if (cand_tiles > 0) {
       SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
                   "route: score grid too large");
+      ca.on = 0;
       if (m3 != nullptr) {
         dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
         route_score_kernel<true, kTile><<<grid, 256, 0, stream>>>(
@@ -938,15 +1477,16 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
     if (nbk <= 256)  // few candidates: a wave per row
       route_select_small_kernel<4><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
-          keys, g, kv_num, kv_idx, W, nrows);
+          keys, g, kv_num, kv_idx, W, nrows, ca);
     else if (nbk <= kSmallNbk)
       route_select_small_kernel<16><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
-          keys, g, kv_num, kv_idx, W, nrows);
+          keys, g, kv_num, kv_idx, W, nrows, ca);
     else if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
-      route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W);
+      route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W,
+                                                                       ca);
     else
-      route_select_kernel<kSelThreads><<<(unsigned)nrows, kSelThreads, 0, stream>>>(keys, g, kv_num,
-                                                                                  kv_idx, W);
+      route_select_kernel<kSelThreads><<<(unsigned)nrows, kSelThreads, 0, stream>>>(
+          keys, g, kv_num, kv_idx, W, ca);
     SSA_TRY(launch_status("route_select_kernel"));
   }
   return SSA_OK;
@@ -981,7 +1521,7 @@ extern "C" int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t t
 }
 
 extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk) {
-  return (size_t)B * (size_t)Hq * (size_t)nbq * (size_t)nbk * 4u;
+  return ssa::route_norm_bytes(B, Hq, nbk) + (size_t)B * (size_t)Hq * (size_t)nbq * (size_t)nbk * 4u;
 }
 
 extern "C" int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,
