@@ -338,96 +338,99 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
 }
 
 // ---- certified scoring -------------------------------------------------------------------------
-// With approximate (fp32-MFMA) keys, a select kernel certifies its selection: with e a bound on
+// With approximate (MFMA) keys, a select kernel certifies its selection: with e a bound on
 // |approximate - exact| for every score of the row, and T~ the keep-th largest approximate score,
 // the exact keep-th largest lies within e of T~, so a candidate scoring above T~ + 2e is in the
-// exact top-keep and one below T~ - 2e is out; the candidates in between are rescored with the
-// exact formula (fp64 sums, fp32 assembly as route_score_kernel) and the remaining places go to
-// the best of them by (exact key, lowest block index) -- the exact router's selection.
-// e = (K + 16) u (1 + 2^-10) (|q| |mu|max + |c2| |q^2| |var|max + |c3| |q^3| |m3|max) + 2^-100:
-// a K-term fp32 dot product (K = 2d or 3d) is within K u sum|a_k b_k| of its exact value, the
-// pre-multiplied c2 q^2 and c3 q^3 add u each, the exact score's own roundings at most 5u of
-// sum|a_k b_k|, which Cauchy-Schwarz bounds by the norm products (the norm maxima are over the
-// 64-candidate tiles holding the row's candidates, in fp32 with the (1 + 2^-10) margin; 2^-100
-// covers flushed denormals). A non-finite bound or threshold makes every candidate uncertain.
+// exact top-keep and one below T~ - 2e is out; the candidates in between (the band) are rescored
+// with the exact formula (fp64 sums, fp32 assembly as route_score_kernel) and the remaining
+// places go to the best of them by (exact key, lowest block index) -- the exact router's
+// selection. When the band holds exactly the remaining places (the usual case: the keep-th
+// candidate alone), they are taken without rescoring.
+// The approximation is one MFMA contraction of the rows' A = [q | c2 fl32(q*q) | c3 fl32(q*q*q)]
+// against the candidates' B = [mu | var | m3] (route_score_mfma_kernel, n products per score).
+// For a row and a 64-candidate tile the score kernel stores
+//   emag = sum_t |A_t| max_c |B_t,c| + 2^-56 sum_t (|A_t| + max|B_t|)
+// (norms from fp32 squares; their relative error, below d 2^-24, is covered by the margin below);
+// the select takes M = the largest emag over the row's tiles and
+//   e = ecoef (1 + 2^-10) M + 2^-100,  ecoef = 1.03 (3n + 16) 2^-23 + 2^-14:
+// the 3n bf16 products are exact and their fp32 sum, in any order with each addition rounded or
+// truncated (2^-23 per operation), is within 3n 2^-23 of the sum of their magnitudes (at most
+// 1.02 sum|a_k b_k|); the bf16 split and the dropped lo.lo products add under 3.1 2^-16
+// sum|a_k b_k|; the pre-multiplied c2 q^2, c3 q^3 and the exact score's own fp32 roundings a few
+// 2^-24 sum|a_k b_k|, inside the 16; Cauchy-Schwarz bounds sum|a_k b_k| by sum_t |A_t||B_t|.
+// Inputs or products flushed below 2^-126 move the sum by less than n 2^-126 (max|A| + max|B|)
+// + n 2^-126, covered by the 2^-56 term and 2^-100. A non-finite bound or threshold makes every
+// candidate uncertain.
 struct CertArgs {
-  int on;               // the keys are fp32-MFMA approximations to certify
-  const void* rows;     // (B, Hq, nbq, d) query rows of type g.rows_dt
+  int on;                      // the keys are MFMA approximations to certify
+  const void* rows;            // (B, Hq, nbq, d) query rows of type g.rows_dt
   const float* mu;
-  const float* var;     // may be NULL (coef2 = 0)
-  const float* m3;      // may be NULL
-  const float* tnorm;   // (B*Hkv, ntile, 4): max squared norms of mu, var, m3 per 64-candidate tile
+  const float* var;            // may be NULL (coef2 = 0)
+  const float* m3;             // may be NULL
+  const float* emag;           // (chunk rows, ntile) error magnitude per row and candidate tile
+  const unsigned int* tmax;    // (chunk rows, ntile) largest key per row and tile, or NULL
   int64_t ntile;
   int d;
+  double ecoef;                // e = ecoef (1 + 2^-10) M + 2^-100 (M: the row's largest emag)
   float coef2, coef3;
 };
 
-constexpr int kNormTile = 64;  // candidates (sub-block units) per norm tile
+constexpr int kNormTile = 64;  // candidates (sub-block units) per score tile of emag / tmax
 constexpr int kBand = 512;     // capacity of a row's certificate band (larger: rescore the row)
 constexpr int kMaxQReg = 8;    // head dims per lane in the exact rescoring (d <= 512)
+// The select kernels are instantiated for QR = ceil(d / 64) head dims per lane (1, 2, 4, 8).
+constexpr int kMaxTiles = kMaxNbk / kNormTile;  // tile maxima of a row staged by the select
 
-// Bytes of the per-tile candidate norms at the start of a route workspace (4 floats per tile per
-// key head; B*Hq bounds B*Hkv).
-inline size_t route_norm_bytes(int64_t B, int64_t Hq, int64_t nbs) {
-  const size_t n = (size_t)B * (size_t)Hq * (size_t)((nbs + kNormTile - 1) / kNormTile) * 16u;
-  return (n + 255) / 256 * 256;
+// Bytes per routed row of the certified router's workspace: the keys, then emag and tmax.
+inline size_t route_row_bytes(int64_t nbs) {
+  return (size_t)nbs * 4u + (size_t)((nbs + kNormTile - 1) / kNormTile) * 8u;
 }
 
-// Largest squared norms of the candidates' mu, var and m3 rows per 64-candidate tile (the
-// certificate's bound): grid (ceil(nbs / 64), B*Hkv), one wave, a lane per candidate.
-__global__ __launch_bounds__(64) void route_cand_norm_kernel(
-    const float* __restrict__ mu, const float* __restrict__ var, const float* __restrict__ m3,
-    int64_t nbs, int d, float* __restrict__ tnorm, int64_t ntile) {
-  const int64_t bk = blockIdx.y, t = blockIdx.x;
-  const int lane = threadIdx.x;
-  const int64_t c = t * kNormTile + lane;
-  float n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
-  if (c < nbs) {
-    const int64_t off = (bk * nbs + c) * d;
-    for (int k = 0; k < d; ++k) {
-      const float x = mu[off + k];
-      n1 = fmaf(x, x, n1);
-      if (var) {
-        const float y = var[off + k];
-        n2 = fmaf(y, y, n2);
-      }
-      if (m3) {
-        const float z = m3[off + k];
-        n3 = fmaf(z, z, n3);
-      }
-    }
-  }
+// Approximate scores for the certified router: one MFMA contraction of the query rows
+// A = [q | c2 fl32(q*q) | c3 fl32(q*q*q)] against the candidates' B = [mu | var | m3] (n = 2d, 3d
+// with m3, d without var), each fp32 operand split into bf16 hi + lo parts (hi = bf16(x),
+// lo = bf16(x - hi), |x - hi - lo| <= 2^-16 |x|) and a.b taken as hi.hi + hi.lo + lo.hi on
+// v_mfma_f32_32x32x16_bf16 (the products are exact in fp32; dropping lo.lo and the split errors
+// leave under 3.1 2^-16 |a||b|). A workgroup scores 64 rows x 64 candidates, each of its 4 waves a
+// 32 x 32 block (lane l supplies A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32] per 16 head
+// dims; accumulator j of lane l is C[(j/4)*8 + (l/32)*4 + j%4][l%32]). Operands are staged in LDS
+// 32 head dims at a time as bf16 rows of 40 (80 bytes: the 16 lanes of a ds_read_b128 phase, 16
+// consecutive rows, cover the 64 banks once), a thread loading 8 consecutive head dims of one row
+// and of one candidate (16-byte loads: d % 8 == 0, aligned operands). Same tile geometry and
+// causal tile skip as route_score_kernel; the keys are stored in the same layout. Per row and
+// tile it also stores emag (the certificate's error magnitude) and, with TMAX, the largest key
+// over the row's candidates in the tile.
+constexpr int kStageLd = 40;  // bf16 per staged row (32 head dims + 8 pad)
+
+// hi / lo bf16 parts of 8 fp32 values, packed in pairs (element 2e in the low half of word e).
+__device__ inline void split_bf16x8(const float (&x)[8], u32x4& hi, u32x4& lo) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    n1 = fmaxf(n1, __shfl_xor(n1, off, 64));
-    n2 = fmaxf(n2, __shfl_xor(n2, off, 64));
-    n3 = fmaxf(n3, __shfl_xor(n3, off, 64));
-  }
-  if (lane == 0) {
-    float* p = tnorm + (bk * ntile + t) * 4;
-    p[0] = n1;
-    p[1] = n2;
-    p[2] = n3;
-    p[3] = 0.0f;
+  for (int e = 0; e < 4; ++e) {
+    const __bf16 h0 = (__bf16)x[2 * e], h1 = (__bf16)x[2 * e + 1];
+    const __bf16 l0 = (__bf16)(x[2 * e] - (float)h0), l1 = (__bf16)(x[2 * e + 1] - (float)h1);
+    hi[e] = (unsigned int)__builtin_bit_cast(unsigned short, h0) |
+            ((unsigned int)__builtin_bit_cast(unsigned short, h1) << 16);
+    lo[e] = (unsigned int)__builtin_bit_cast(unsigned short, l0) |
+            ((unsigned int)__builtin_bit_cast(unsigned short, l1) << 16);
   }
 }
 
-// Approximate scores for the certified router: one fp32-MFMA contraction of the query rows
-// [q | c2 fl32(q*q) | c3 fl32(q*q*q)] against the candidates' [mu | var | m3] (K = 2d, 3d with
-// m3, d without var), 64 rows x 64 candidates per workgroup, each of the 4 waves a 32 x 32 block
-// on v_mfma_f32_32x32x2_f32 (lane l supplies A[l%32][l/32] and B[l/32][l%32]; accumulator j of
-// lane l is C[(j/4)*8 + (l/32)*4 + j%4][l%32]). Operands are staged in LDS 32 head dims at a
-// time, rows of 33 floats (conflict-free column reads). Same tile geometry and causal tile skip
-// as route_score_kernel; the keys are stored in the same workspace layout.
-template <bool EDGE, bool VEC>
+template <bool EDGE, bool TMAX>
 __global__ __launch_bounds__(256) void route_score_mfma_kernel(
     const void* __restrict__ rows, const float* __restrict__ mu, const float* __restrict__ var,
     const float* __restrict__ m3, RouteGeom g, int d, float coef2, float coef3,
-    unsigned int* __restrict__ keys, int64_t row_tiles, int64_t cand_tiles) {
+    unsigned int* __restrict__ keys, float* __restrict__ emag, unsigned int* __restrict__ tmax,
+    int64_t ntile, int64_t row_tiles, int64_t cand_tiles) {
   constexpr int KC = 32;
-  __shared__ float As[kTile][KC + 1];
-  __shared__ float Bs[kTile][KC + 1];
-  __shared__ int64_t row_off[kTile];
+  // staging: A hi, A lo, B hi, B lo, [kTile][kStageLd] bf16 each; after the last contraction,
+  // TMAX reuses it as a [kTile][kTile + 1] array of keys
+  static_assert(4 * kTile * kStageLd * 2 >= kTile * (kTile + 1) * 4, "stage too small");
+  __shared__ __attribute__((aligned(16))) unsigned short stage[4][kTile][kStageLd];
+  __shared__ int64_t row_off[kTile];  // element offset of the tile's rows in `rows` (-1: none)
+  __shared__ int64_t row_key[kTile];  // chunk row index (b*Hq + h)*ni + il of the tile's rows
+  __shared__ int64_t row_cm[kTile];   // scored candidates of the tile's rows (0: none)
+  __shared__ float sqa[3][kTile], sqb[3][kTile];  // squared norms per term: rows, candidates
+  __shared__ unsigned int smax[kTile];
 
   const int64_t bk = blockIdx.y;  // b * Hkv + kvh
   const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
@@ -443,97 +446,159 @@ __global__ __launch_bounds__(256) void route_score_mfma_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wr = w & 1, wc = w >> 1;
-  if (tid < kTile) {
+  if (tid < kTile) {  // per-row geometry, once per tile (64-bit divisions)
     const int64_t r = r0 + tid;
-    int64_t off = -1;
+    int64_t off = -1, lr = 0, cm = 0;
     if (r < R) {
       const int64_t h = kvh * g.G + r / g.ni;
-      const int64_t ii = g.i0 + r % g.ni;
-      off = ((b * g.Hq + h) * g.nbq + ii) * d;
+      const int64_t il = r % g.ni;
+      off = ((b * g.Hq + h) * g.nbq + g.i0 + il) * d;
+      lr = (b * g.Hq + h) * g.ni + il;
+      cm = row_cmax_s(g, g.i0 + il);
     }
     row_off[tid] = off;
+    row_key[tid] = lr;
+    row_cm[tid] = cm;
+  }
+  if (tid < 3 * kTile) {
+    sqa[tid / kTile][tid % kTile] = 0.0f;
+    sqb[tid / kTile][tid % kTile] = 0.0f;
   }
   f32x16 acc;
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  const int rr = tid >> 2, k8 = (tid & 3) * 8;  // staging: row / candidate rr, dims k8..k8+7
   for (int term = 0; term < (EDGE ? 3 : 2); ++term) {
     if (term == 1 && var == nullptr) continue;  // centroid routing: no variance term
     const float* src = (term == 0 ? mu : term == 1 ? var : m3) + (bk * nbs) * d;
     const float cf = term == 0 ? 1.0f : term == 1 ? coef2 : coef3;
+    float sa = 0.0f, sb = 0.0f;
     for (int k0 = 0; k0 < d; k0 += KC) {
       __syncthreads();
-      if (VEC) {  // thread: 8 consecutive head dims of one row and of one candidate (16-byte loads)
-        const int rr = tid >> 2, k8 = (tid & 3) * 8;
-        const int64_t roff = row_off[rr];
-        float q[8], bv[8];
+      const int64_t roff = row_off[rr];
+      float q[8], bv[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q[e] = bv[e] = 0.0f;
-        if (roff >= 0 && k0 + k8 < d) {
-          if (g.rows_dt == SSA_F32) {
-            const f32x4* pq = reinterpret_cast<const f32x4*>(static_cast<const float*>(rows) + roff + k0 + k8);
-            const f32x4 x0 = pq[0], x1 = pq[1];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              q[e] = x0[e];
-              q[4 + e] = x1[e];
-            }
-          } else {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(
-                static_cast<const unsigned short*>(rows) + roff + k0 + k8);
-            unpack8(w, q, g.rows_dt == SSA_BF16);
-          }
-        }
-        const int64_t cand = c0 + rr;
-        if (cand < nbs && k0 + k8 < d) {
-          const f32x4* pb = reinterpret_cast<const f32x4*>(src + cand * d + k0 + k8);
-          const f32x4 y0 = pb[0], y1 = pb[1];
+      for (int e = 0; e < 8; ++e) q[e] = bv[e] = 0.0f;
+      if (roff >= 0 && k0 + k8 < d) {
+        if (g.rows_dt == SSA_F32) {
+          const f32x4* pq =
+              reinterpret_cast<const f32x4*>(static_cast<const float*>(rows) + roff + k0 + k8);
+          const f32x4 x0 = pq[0], x1 = pq[1];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            bv[e] = y0[e];
-            bv[4 + e] = y1[e];
+            q[e] = x0[e];
+            q[4 + e] = x1[e];
           }
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float a = q[e];
-          if (term == 1) a = cf * (q[e] * q[e]);
-          else if (term == 2) a = cf * ((q[e] * q[e]) * q[e]);
-          As[rr][k8 + e] = a;
-          Bs[rr][k8 + e] = bv[e];
-        }
-      } else {
-#pragma unroll
-        for (int idx = tid; idx < kTile * KC; idx += 256) {
-          const int rr = idx / KC, kk = idx % KC;
-          const int64_t roff = row_off[rr];
-          float q = 0.0f;
-          if (roff >= 0 && k0 + kk < d) q = load_row(rows, roff + k0 + kk, g.rows_dt);
-          float a = q;
-          if (term == 1) a = cf * (q * q);
-          else if (term == 2) a = cf * ((q * q) * q);
-          As[rr][kk] = a;
-          const int64_t cand = c0 + rr;
-          Bs[rr][kk] = (cand < nbs && k0 + kk < d) ? src[cand * d + k0 + kk] : 0.0f;
+        } else {
+          const u32x4 wq = *reinterpret_cast<const u32x4*>(
+              static_cast<const unsigned short*>(rows) + roff + k0 + k8);
+          unpack8(wq, q, g.rows_dt == SSA_BF16);
         }
       }
+      const int64_t cand = c0 + rr;
+      if (cand < nbs && k0 + k8 < d) {
+        const f32x4* pb = reinterpret_cast<const f32x4*>(src + cand * d + k0 + k8);
+        const f32x4 y0 = pb[0], y1 = pb[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bv[e] = y0[e];
+          bv[4 + e] = y1[e];
+        }
+      }
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a[e] = q[e];
+        if (term == 1) a[e] = cf * (q[e] * q[e]);
+        else if (term == 2) a[e] = cf * ((q[e] * q[e]) * q[e]);
+        sa = fmaf(a[e], a[e], sa);
+        sb = fmaf(bv[e], bv[e], sb);
+      }
+      u32x4 ahi, alo, bhi, blo;
+      split_bf16x8(a, ahi, alo);
+      split_bf16x8(bv, bhi, blo);
+      *reinterpret_cast<u32x4*>(&stage[0][rr][k8]) = ahi;
+      *reinterpret_cast<u32x4*>(&stage[1][rr][k8]) = alo;
+      *reinterpret_cast<u32x4*>(&stage[2][rr][k8]) = bhi;
+      *reinterpret_cast<u32x4*>(&stage[3][rr][k8]) = blo;
       __syncthreads();
 #pragma unroll
-      for (int kk = 0; kk < KC; kk += 2) {
-        const float a = As[wr * 32 + (lane & 31)][kk + (lane >> 5)];
-        const float bb = Bs[wc * 32 + (lane & 31)][kk + (lane >> 5)];
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+      for (int s = 0; s < KC / 16; ++s) {
+        const int kk = s * 16 + (lane >> 5) * 8;
+        const int ra = wr * 32 + (lane & 31), rb = wc * 32 + (lane & 31);
+        const bf16x8 xah = *reinterpret_cast<const bf16x8*>(&stage[0][ra][kk]);
+        const bf16x8 xal = *reinterpret_cast<const bf16x8*>(&stage[1][ra][kk]);
+        const bf16x8 xbh = *reinterpret_cast<const bf16x8*>(&stage[2][rb][kk]);
+        const bf16x8 xbl = *reinterpret_cast<const bf16x8*>(&stage[3][rb][kk]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xah, xbh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xah, xbl, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xal, xbh, acc, 0, 0, 0);
       }
+    }
+    // the 4 staging threads of row / candidate rr are adjacent lanes
+    sa += __shfl_xor(sa, 1, 64);
+    sa += __shfl_xor(sa, 2, 64);
+    sb += __shfl_xor(sb, 1, 64);
+    sb += __shfl_xor(sb, 2, 64);
+    if ((tid & 3) == 0) {
+      sqa[term][rr] = sa;
+      sqb[term][rr] = sb;
     }
   }
   const int64_t cand = c0 + wc * 32 + (lane & 31);
+  unsigned int mk[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const int64_t r = r0 + wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-    if (r >= R) continue;
-    const int64_t h = kvh * g.G + r / g.ni;
-    const int64_t il = r % g.ni;
-    if (cand >= row_cmax_s(g, g.i0 + il)) continue;
-    keys[((b * g.Hq + h) * g.ni + il) * nbs + cand] = score_key(acc[j]);
+    const int rl = wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+    mk[j] = 0u;
+    if (cand >= row_cm[rl]) continue;  // past the row's candidates (or no row: 0)
+    const unsigned int k = score_key(acc[j]);
+    keys[row_key[rl] * nbs + cand] = k;
+    mk[j] = k;
+  }
+  if constexpr (TMAX) {
+    // row maxima: the tile's keys go to LDS as [row][candidate], 4 threads reduce each row
+    unsigned int* red = reinterpret_cast<unsigned int*>(&stage[0][0][0]);
+    __syncthreads();  // every wave is past its last contraction
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      red[(wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3)) * (kTile + 1) + wc * 32 +
+          (lane & 31)] = mk[j];
+    __syncthreads();
+    const unsigned int* pr = red + (tid >> 2) * (kTile + 1) + (tid & 3) * 16;
+    unsigned int mx = 0u;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = pr[e] > mx ? pr[e] : mx;
+    unsigned int o = __shfl_xor(mx, 1, 64);
+    mx = o > mx ? o : mx;
+    o = __shfl_xor(mx, 2, 64);
+    mx = o > mx ? o : mx;
+    if ((tid & 3) == 0) smax[tid >> 2] = mx;
+  }
+  __syncthreads();
+  if (w == 0) {
+    float M[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      M[t] = sqb[t][lane];  // zero for candidates past nbs (staged as zeros)
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) M[t] = fmaxf(M[t], __shfl_xor(M[t], off, 64));
+    }
+    if (c0 < row_cm[lane]) {
+      double mag = 0.0, nsum = 0.0;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const double a = sqrt((double)sqa[t][lane]), bb = sqrt((double)M[t]);
+        mag += a * bb;
+        nsum += a + bb;
+      }
+      mag += 0x1p-56 * nsum;
+      float f = (float)mag;
+      if ((double)f < mag) f = __uint_as_float(__float_as_uint(f) + 1u);  // round up (f >= 0)
+      const int64_t lrow = row_key[lane];
+      emag[lrow * ntile + ct] = f;
+      if constexpr (TMAX) tmax[lrow * ntile + ct] = smax[lane];
+    }
   }
 }
 
@@ -549,62 +614,34 @@ __device__ inline double wave_sum_f64(double x) {
   return x;
 }
 
-// The wave loads query row `roff` (element offset) into qreg (lane l: dims l + 64 t) and returns
-// the norms |q|, |q^2|, |q^3| of its fp32 elementwise powers (every lane).
-__device__ inline void cert_load_row(const CertArgs& ca, int rows_dt, int64_t roff,
-                                     float (&qreg)[kMaxQReg], float* n1, float* n2, float* n3) {
+// The wave loads query row `roff` (element offset) into qreg (lane l: dims l + 64 t).
+template <int QR>
+__device__ inline void cert_load_q(const CertArgs& ca, int rows_dt, int64_t roff,
+                                   float (&qreg)[QR]) {
   const int lane = threadIdx.x & 63;
-  float s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
-  for (int t = 0; t < kMaxQReg; ++t) {
+  for (int t = 0; t < QR; ++t) {
     const int k = lane + 64 * t;
-    float q = 0.0f;
-    if (k < ca.d) q = load_row(ca.rows, roff + k, rows_dt);
-    qreg[t] = q;
-    const float q2 = q * q, q3 = q2 * q;
-    s1 = fmaf(q, q, s1);
-    s2 = fmaf(q2, q2, s2);
-    s3 = fmaf(q3, q3, s3);
+    qreg[t] = k < ca.d ? load_row(ca.rows, roff + k, rows_dt) : 0.0f;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    s1 += __shfl_xor(s1, off, 64);
-    s2 += __shfl_xor(s2, off, 64);
-    s3 += __shfl_xor(s3, off, 64);
-  }
-  *n1 = sqrtf(s1);
-  *n2 = sqrtf(s2);
-  *n3 = sqrtf(s3);
 }
 
-// Largest squared candidate norms over the norm tiles of candidates [0, cmax_s) of key head bk,
-// reduced by `nthreads` threads starting at thread `t0` (results via the returned maxima of each
-// thread; the caller reduces).
-__device__ inline void cert_tile_max(const CertArgs& ca, int64_t bk, int64_t cmax_s, int tid,
-                                     int nthreads, float* m1, float* m2, float* m3) {
+// Largest emag over the score tiles of candidates [0, cmax_s) of chunk row lrow, over `nthreads`
+// threads from `tid` (each thread's partial maximum; the caller reduces).
+__device__ inline float cert_emag_max(const CertArgs& ca, int64_t lrow, int64_t cmax_s, int tid,
+                                      int nthreads) {
   const int64_t nt = (cmax_s + kNormTile - 1) / kNormTile;
-  float a = 0.0f, b = 0.0f, c = 0.0f;
-  for (int64_t t = tid; t < nt; t += nthreads) {
-    const float* p = ca.tnorm + (bk * ca.ntile + t) * 4;
-    a = fmaxf(a, p[0]);
-    b = fmaxf(b, p[1]);
-    c = fmaxf(c, p[2]);
-  }
-  *m1 = a;
-  *m2 = b;
-  *m3 = c;
+  const float* p = ca.emag + lrow * ca.ntile;
+  float m = 0.0f;
+  for (int64_t t = tid; t < nt; t += nthreads) m = fmaxf(m, p[t]);
+  return m;
 }
 
-// (lo, hi) score keys of the certificate band around the approximate threshold key T.
-__device__ inline void cert_band(const CertArgs& ca, unsigned int T, float qn1, float qn2,
-                                 float qn3, float max1, float max2, float max3,
-                                 unsigned int* lo, unsigned int* hi) {
-  const int K = (1 + (ca.var ? 1 : 0) + (ca.m3 ? 1 : 0)) * ca.d;
-  const double u = 5.9604644775390625e-08;  // 2^-24
-  const double mag = (double)qn1 * sqrt((double)max1) +
-                     fabs((double)ca.coef2) * (double)qn2 * sqrt((double)max2) +
-                     fabs((double)ca.coef3) * (double)qn3 * sqrt((double)max3);
-  const double e = (K + 16) * u * (1.0 + 0x1p-10) * mag + 0x1p-100;
+// (lo, hi) score keys of the certificate band around the approximate threshold key T, given M,
+// the row's largest emag.
+__device__ inline void cert_band(const CertArgs& ca, unsigned int T, float M, unsigned int* lo,
+                                 unsigned int* hi) {
+  const double e = ca.ecoef * (1.0 + 0x1p-10) * (double)M + 0x1p-100;
   const double tau = (double)key_value(T);
   if (!(e < 1e300) || !(fabs(tau) < 1e300)) {  // non-finite: certify nothing
     *lo = 0u;
@@ -631,7 +668,8 @@ __device__ inline void cert_band(const CertArgs& ca, unsigned int T, float qn1, 
 // Exact score key of candidate block c of the row held in qreg (its key head's summaries at
 // element offset cbase of candidate 0): the fp64-accumulated formula of route_score_kernel, the
 // max over the block's pool sub-blocks, computed by one wave.
-__device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&qreg)[kMaxQReg],
+template <int QR>
+__device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&qreg)[QR],
                                               int64_t cbase, int64_t c, int64_t pool) {
   const int lane = threadIdx.x & 63;
   unsigned int best = 0u;
@@ -639,7 +677,7 @@ __device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&
     const int64_t off = cbase + (c * pool + s) * ca.d;
     double e1 = 0.0, e2 = 0.0, e3 = 0.0;
 #pragma unroll
-    for (int t = 0; t < kMaxQReg; ++t) {
+    for (int t = 0; t < QR; ++t) {
       const int k = lane + 64 * t;
       if (k < ca.d) {
         const float q = qreg[t], q2 = q * q;
@@ -661,10 +699,29 @@ __device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&
 // The K-th largest of a wave's entries (lane l, slot j: entry l + 64 j; non-candidates hold
 // key 0), found bit by bit from the top (count of keys >= T | bit by ballots), or the first
 // prefix with exactly K keys >= T -- then no tie straddles the cut. Requires 0 < K < #candidates.
+// The search starts below the leading bits that every nonzero key shares (the K-th largest
+// shares them when at least K keys are nonzero).
 template <int J>
 __device__ inline unsigned int wave_kth_key(const unsigned int (&key)[J], int64_t K) {
-  unsigned int T = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
+  unsigned int all = 0xffffffffu, any = 0u;
+  int nz = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    all &= key[j] ? key[j] : 0xffffffffu;
+    any |= key[j];
+    nz += __popcll(__ballot(key[j] != 0u));
+  }
+  if (nz < K) return 0u;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    all &= __shfl_xor(all, off, 64);
+    any |= __shfl_xor(any, off, 64);
+  }
+  const unsigned int diff = all ^ any;  // bits on which nonzero keys differ
+  if (diff == 0u) return all;           // one distinct nonzero key
+  const int top = 31 - __clz(diff);
+  unsigned int T = top == 31 ? 0u : all & ~((2u << top) - 1u);
+  for (int bit = top; bit >= 0; --bit) {
     const unsigned int t = T | (1u << bit);
     int cnt = 0;
 #pragma unroll
@@ -677,38 +734,34 @@ __device__ inline unsigned int wave_kth_key(const unsigned int (&key)[J], int64_
   return T;
 }
 
-// The K largest of a wave's entries (cand marks the ncand real ones) under the order (key desc,
-// entry asc): keys > T (the K-th largest) are taken, and keys == T in increasing entry order until
-// K are taken. Non-candidates must hold key 0: they never reach a threshold >= 1, and at T = 0
-// the candidate flag keeps them out.
+// The K largest of a wave's candidates (bit j of the lane's mask cm: entry lane + 64 j is one;
+// non-candidates must hold key 0) under the order (key desc, entry asc), as a per-lane mask:
+// keys > T (the K-th largest) are taken, and keys == T in increasing entry order until K are
+// taken. ncand is the number of candidates.
 template <int J>
-__device__ inline void wave_select_top(const unsigned int (&key)[J], const bool (&cand)[J],
-                                       int64_t K, int64_t ncand, bool (&sel)[J]) {
+__device__ inline unsigned int wave_select_top(const unsigned int (&key)[J], unsigned int cm,
+                                               int64_t K, int64_t ncand) {
   const int lane = threadIdx.x & 63;
   const unsigned long long lt = (1ull << lane) - 1ull;
-  if (K >= ncand) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) sel[j] = cand[j];
-    return;
-  }
-  if (K <= 0) {
-#pragma unroll
-    for (int j = 0; j < J; ++j) sel[j] = false;
-    return;
-  }
+  if (K >= ncand) return cm;
+  if (K <= 0) return 0u;
   const unsigned int T = wave_kth_key<J>(key, K);
   int above = 0;
 #pragma unroll
-  for (int j = 0; j < J; ++j) above += __popcll(__ballot(cand[j] && key[j] > T));
+  for (int j = 0; j < J; ++j) above += __popcll(__ballot(((cm >> j) & 1u) && key[j] > T));
   int need = (int)K - above;  // keys equal to T to take, lowest entry first
+  unsigned int selm = 0u;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const bool eq = cand[j] && key[j] == T;
+    const bool cd = (cm >> j) & 1u;
+    const bool eq = cd && key[j] == T;
     const unsigned long long be = __ballot(eq);
     // (int) casts: __popcll is unsigned, and need turns negative once the ties are taken
-    sel[j] = (cand[j] && key[j] > T) || (eq && (int)__popcll(be & lt) < need);
+    const bool take = (cd && key[j] > T) || (eq && (int)__popcll(be & lt) < need);
+    selm |= (take ? 1u : 0u) << j;
     need -= (int)__popcll(be);
   }
+  return selm;
 }
 
 constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
@@ -725,7 +778,7 @@ constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
 // rescored exactly and the remaining places chosen among them by a second radix select; a band
 // of more than kCand candidates falls back to rescoring the whole row into the workspace and
 // selecting on the exact keys.
-template <int NT>
+template <int NT, int QR>
 __global__ __launch_bounds__(NT) void route_select_kernel(
     unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
     int32_t* __restrict__ kv_idx, int64_t W, CertArgs ca) {
@@ -735,8 +788,8 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   __shared__ unsigned int hist[256];
   __shared__ int wave_sums[NT / 64];
   __shared__ unsigned int bidx[kBand], bkey[kBand];  // the certificate band
-  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand, sh_whole, sh_nin, sh_nunc;
-  __shared__ float sh_norm[3 * (NT / 64)];
+  __shared__ unsigned int sh_digit, sh_above, sh_min, sh_ncand, sh_whole, sh_nin, sh_nunc, sh_nq;
+  __shared__ float sh_norm[NT / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
@@ -758,7 +811,6 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     return m;
   };
   const int nwords = (int)((g.nbk + 31) / 32);
-  const bool cached = cmax <= kCacheKeys;  // whole row in LDS, index order
   bool cert = ca.on && K > 0 && K < cmax;
 
   // radix select of the K-th largest of src(0..n): returns T, with *rank = the rank of T among
@@ -815,19 +867,73 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   };
 
   for (int w = tid; w < nwords; w += NT) bits[w] = 0u;
+  const int64_t nt = (cmax * g.pool + kNormTile - 1) / kNormTile;  // score tiles of the row
   for (int pass = 0; pass < 2; ++pass) {
+    // tile filter: certified keys with per-tile maxima, more tiles than places
+    const bool tilef = cert && ca.tmax != nullptr && g.pool == 1 && K <= NT && nt > K &&
+                       cmax > kFilterMin;
+    const bool cached = cmax <= kCacheKeys && !tilef;  // whole row in LDS, index order
     if (cached && K > 0 && K < cmax)
       for (int64_t c = tid; c < cmax; c += NT) cache[c] = krow(c);
     if (tid == 0) {
       sh_min = 0xffffffffu;
       sh_ncand = 0u;
+      sh_nq = 0u;
     }
     __syncthreads();
+    auto rowkey = [&](int64_t c) -> unsigned int { return cached ? cache[c] : krow(c); };
 
     // keys the radix select runs over: src[0, nsel), block index of entry c: filt ? cidx[c] : c
     bool filt = false;
     int64_t nsel = cmax;
-    if (K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
+    if (tilef) {
+      // T0 = the K-th largest tile maximum: K distinct tiles hold a key >= T0, so T0 <= the K-th
+      // largest key, and only tiles whose maximum reaches T0 hold keys >= T0. Tile maxima and
+      // the list of those tiles live in the part of `cache` past the kCand candidates.
+      unsigned int* tk = cache + kCand;
+      unsigned int* qt = cache + kCand + kMaxTiles;
+      const unsigned int* tm = ca.tmax + lrow * ca.ntile;
+      for (int64_t t = tid; t < nt; t += NT) tk[t] = tm[t];
+      __syncthreads();
+      unsigned int rk;
+      bool wh;
+      const unsigned int t0 = radix_kth([&](int64_t t) { return tk[t]; }, nt, (unsigned int)K,
+                                        &rk, &wh);
+      for (int64_t t = tid; t < nt; t += NT)
+        if (tk[t] >= t0) qt[atomicAdd(&sh_nq, 1u)] = (unsigned int)t;
+      if (tid == 0) sh_min = t0;
+      __syncthreads();
+      const unsigned int nq = sh_nq;
+      const unsigned long long lt = (1ull << lane) - 1ull;
+      // a wave per tile, a lane per candidate, 4 tiles in flight
+      for (unsigned int q0 = 4u * wv; q0 < nq; q0 += 4u * (NT / 64)) {
+        unsigned int kq[4];
+        int64_t cq[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          cq[u] = q0 + u < nq ? (int64_t)qt[q0 + u] * kNormTile + lane : cmax;
+          kq[u] = cq[u] < cmax ? kraw[cq[u]] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool take = cq[u] < cmax && kq[u] >= t0;
+          const unsigned long long bm = __ballot(take);
+          unsigned int base = 0u;
+          if (lane == 0 && bm) base = atomicAdd(&sh_ncand, (unsigned int)__popcll(bm));
+          base = __shfl(base, 0, 64);
+          const unsigned int slot = base + (unsigned int)__popcll(bm & lt);
+          if (take && slot < (unsigned int)kCand) {
+            cache[slot] = kq[u];
+            cidx[slot] = (unsigned int)cq[u];
+          }
+        }
+      }
+      __syncthreads();
+      if (sh_ncand <= (unsigned int)kCand) {
+        filt = true;
+        nsel = sh_ncand;
+      }
+    } else if (K > 0 && K < cmax && K <= NT && cmax > kFilterMin) {
       int pk = 1;
       while (pk < K) pk <<= 1;
       const int gs = NT / pk < 64 ? NT / pk : 64;  // threads per group (a power of two <= 64)
@@ -872,7 +978,6 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
       const unsigned int blk = filt ? cidx[c] : (unsigned int)c;
       atomicOr(&bits[blk >> 5], 1u << (blk & 31));
     };
-    auto rowkey = [&](int64_t c) -> unsigned int { return cached ? cache[c] : krow(c); };
 
     if (K >= cmax) {
       for (int64_t c = tid; c < cmax; c += NT) atomicOr(&bits[c >> 5], 1u << (c & 31));
@@ -907,47 +1012,45 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
     }
 
     // ---- certify the approximate selection ----
-    const int64_t b = bh / g.Hq, h = bh % g.Hq;
-    const int64_t bk = b * g.Hkv + h / g.G;
-    const int64_t cbase = bk * g.nbk * g.pool * ca.d;
-    float qreg[kMaxQReg], qn1, qn2, qn3;
-    cert_load_row(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg, &qn1, &qn2, &qn3);
     {
-      float a, bb, c3;
-      cert_tile_max(ca, bk, cmax * g.pool, tid, NT, &a, &bb, &c3);
+      float M = cert_emag_max(ca, lrow, cmax * g.pool, tid, NT);
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        a = fmaxf(a, __shfl_xor(a, off, 64));
-        bb = fmaxf(bb, __shfl_xor(bb, off, 64));
-        c3 = fmaxf(c3, __shfl_xor(c3, off, 64));
-      }
-      if (lane == 0) {
-        sh_norm[3 * wv] = a;
-        sh_norm[3 * wv + 1] = bb;
-        sh_norm[3 * wv + 2] = c3;
-      }
+      for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+      if (lane == 0) sh_norm[wv] = M;
       if (tid == 0) {
         sh_nin = 0u;
         sh_nunc = 0u;
       }
       __syncthreads();
     }
-    float mx1 = 0.0f, mx2 = 0.0f, mx3 = 0.0f;
+    float M = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) {
-      mx1 = fmaxf(mx1, sh_norm[3 * w]);
-      mx2 = fmaxf(mx2, sh_norm[3 * w + 1]);
-      mx3 = fmaxf(mx3, sh_norm[3 * w + 2]);
-    }
+    for (int w = 0; w < NT / 64; ++w) M = fmaxf(M, sh_norm[w]);
+    // A filtered list holds exactly the keys >= T0 (sh_min). When the radix select stopped at a
+    // digit prefix below T0, the list holds exactly K keys, so exactly K keys of the row are
+    // >= T0: T0 is then the threshold (no key of the row lies in [T, T0) outside the list).
+    const unsigned int Tc = filt && T < sh_min ? sh_min : T;
     unsigned int lo, hi;
-    cert_band(ca, T, qn1, qn2, qn3, mx1, mx2, mx3, &lo, &hi);
-    // classify: above the band -> taken; in the band -> listed for exact rescoring. When the band
-    // lies above the filter threshold, the filtered list holds every candidate it can contain.
+    cert_band(ca, Tc, M, &lo, &hi);
+    // Every candidate that can hold a key >= lo: the filtered list when the band lies above its
+    // threshold, else the tiles whose maximum reaches lo (tile filter), else the whole row.
     const bool in_list = filt && lo >= sh_min;
-    const int64_t nscan = in_list ? nsel : cmax;
-    for (int64_t c = tid; c < nscan; c += NT) {
-      const unsigned int key = in_list ? src(c) : rowkey(c);
-      const unsigned int blk = in_list ? cidx[c] : (unsigned int)c;
+    auto for_band_candidates = [&](auto fn) {
+      if (in_list) {
+        for (int64_t c = tid; c < nsel; c += NT) fn(src(c), cidx[c]);
+      } else if (tilef) {
+        const unsigned int* tk = cache + kCand;
+        for (int64_t t = wv; t < nt; t += NT / 64) {
+          if (tk[t] < lo) continue;  // wave-uniform
+          const int64_t c = t * kNormTile + lane;
+          if (c < cmax) fn(kraw[c], (unsigned int)c);
+        }
+      } else {
+        for (int64_t c = tid; c < cmax; c += NT) fn(rowkey(c), (unsigned int)c);
+      }
+    };
+    // classify: above the band -> taken; in the band -> listed for exact ranking
+    for_band_candidates([&](unsigned int key, unsigned int blk) {
       if (key > hi) {
         atomicOr(&bits[blk >> 5], 1u << (blk & 31));
         atomicAdd(&sh_nin, 1u);
@@ -955,9 +1058,25 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
         const unsigned int slot = atomicAdd(&sh_nunc, 1u);
         if (slot < (unsigned int)kBand) bidx[slot] = blk;
       }
-    }
+    });
     __syncthreads();
     const unsigned int nin = sh_nin, nunc = sh_nunc;
+    const unsigned int m = (unsigned int)K - nin;  // places left for the band
+    if (nunc <= m) {  // the band fills them exactly
+      if (nunc <= (unsigned int)kBand) {
+        for (unsigned int u = tid; u < nunc; u += NT) atomicOr(&bits[bidx[u] >> 5], 1u << (bidx[u] & 31));
+      } else {
+        for_band_candidates([&](unsigned int key, unsigned int blk) {
+          if (key >= lo && key <= hi) atomicOr(&bits[blk >> 5], 1u << (blk & 31));
+        });
+      }
+      break;
+    }
+    const int64_t b = bh / g.Hq, h = bh % g.Hq;
+    const int64_t bk = b * g.Hkv + h / g.G;
+    const int64_t cbase = bk * g.nbk * g.pool * ca.d;
+    float qreg[QR];
+    cert_load_q(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg);
     if (nunc <= (unsigned int)kBand) {
       // rescore the band exactly (a wave per candidate)
       for (unsigned int u = wv; u < nunc; u += NT / 64) {
@@ -966,7 +1085,6 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
       }
       __syncthreads();
       // the band's best K - nin by (exact key, lowest block): taken when fewer rank above
-      const unsigned int m = (unsigned int)K - nin;
       for (unsigned int u = tid; u < nunc; u += NT) {
         const unsigned int ku = bkey[u], cu = bidx[u];
         unsigned int above = 0;
@@ -1020,10 +1138,10 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
 
 // Rows of at most 64 * J key blocks: one wave per row, lane l holds candidates l + 64 j
 // (wave_select_top); the selection plus the local window is compacted in ascending order from
-// the per-j ballots. Approximate keys (ca.on) are certified in place: band candidates are
-// rescored exactly (a wave per candidate), those above the band take the largest key, those
-// below leave the candidates, and the selection runs again on the patched keys.
-template <int kSmallJ>
+// the per-j ballots. Approximate keys (ca.on) are certified: candidates above the band are
+// taken, those below are not; when the band holds more candidates than places remain, they are
+// rescored exactly (a wave per candidate) and ranked by (exact key, lowest block).
+template <int kSmallJ, int QR>
 __global__ __launch_bounds__(256) void route_select_small_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
     int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows, CertArgs ca) {
@@ -1037,14 +1155,14 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
   const int64_t K = keep < cmax ? keep : cmax;
   const unsigned int* kraw = keys + lrow * g.nbk * g.pool;
   const unsigned long long lt = (1ull << lane) - 1ull;
+  // entry lane + 64 j: block c; non-candidates hold key 0. Per-slot flags are kept as per-lane
+  // bit masks (bit j), not as arrays of wave masks.
   unsigned int key[kSmallJ];
-  bool cand[kSmallJ];
 #pragma unroll
   for (int j = 0; j < kSmallJ; ++j) {
     const int64_t c = lane + 64 * j;
-    cand[j] = c < cmax;
     unsigned int m = 0u;
-    if (cand[j]) {
+    if (c < cmax) {
       m = kraw[c * g.pool];
       for (int64_t t = 1; t < g.pool; ++t) {
         const unsigned int x = kraw[c * g.pool + t];
@@ -1053,62 +1171,88 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     }
     key[j] = m;
   }
-  bool sel[kSmallJ];
+  unsigned int selm;
   if (ca.on && K > 0 && K < cmax) {
+    float M = cert_emag_max(ca, lrow, cmax * g.pool, lane, 64);
     const unsigned int T = wave_kth_key<kSmallJ>(key, K);
-    const int64_t b = bh / g.Hq, h = bh % g.Hq;
-    const int64_t bk = b * g.Hkv + h / g.G;
-    float qreg[kMaxQReg], qn1, qn2, qn3;
-    cert_load_row(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg, &qn1, &qn2, &qn3);
-    float m1, m2, m3;
-    cert_tile_max(ca, bk, cmax * g.pool, lane, 64, &m1, &m2, &m3);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      m1 = fmaxf(m1, __shfl_xor(m1, off, 64));
-      m2 = fmaxf(m2, __shfl_xor(m2, off, 64));
-      m3 = fmaxf(m3, __shfl_xor(m3, off, 64));
-    }
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     unsigned int lo, hi;
-    cert_band(ca, T, qn1, qn2, qn3, m1, m2, m3, &lo, &hi);
-    const int64_t cbase = bk * g.nbk * g.pool * ca.d;
-    // above the band: taken; in the band: rescored exactly; below: out
-    bool unc[kSmallJ];
-    int nin = 0;
+    cert_band(ca, T, M, &lo, &hi);
+    // above the band: taken; in the band: to rank exactly; below: out
+    unsigned int uncm = 0u;
+    int nin = 0, nunc = 0;
+    selm = 0u;
 #pragma unroll
     for (int j = 0; j < kSmallJ; ++j) {
-      sel[j] = cand[j] && key[j] > hi;
-      unc[j] = cand[j] && !sel[j] && key[j] >= lo;
-      nin += __popcll(__ballot(sel[j]));
-      unsigned long long bu = __ballot(unc[j]);
-      while (bu) {  // wave-uniform loop over the band candidates of this slot
-        const int src_lane = __ffsll((long long)bu) - 1;
-        bu &= bu - 1;
-        const unsigned int k = cert_exact_key(ca, qreg, cbase, src_lane + 64 * j, g.pool);
-        if (lane == src_lane) key[j] = k;
-      }
+      const bool cd = lane + 64 * j < cmax;
+      const bool s = cd && key[j] > hi;
+      const bool u = cd && !s && key[j] >= lo;
+      selm |= (s ? 1u : 0u) << j;
+      uncm |= (u ? 1u : 0u) << j;
+      nin += __popcll(__ballot(s));
+      nunc += __popcll(__ballot(u));
     }
-    // the band's best K - nin by (exact key, lowest block): a band candidate is taken when fewer
-    // than K - nin band candidates rank above it (a wave-uniform loop over the band candidates)
     const int m = (int)K - nin;
+    if (nunc <= m) {  // the band fills the remaining places exactly
+      selm |= uncm;
+    } else {
+      // rescore the band exactly, one candidate at a time in block order (a wave-uniform loop),
+      // then take its best m by (exact key, lowest block)
+      const int64_t b = bh / g.Hq, h = bh % g.Hq;
+      const int64_t bk = b * g.Hkv + h / g.G;
+      float qreg[QR];
+      cert_load_q(ca, g.rows_dt, ((b * g.Hq + h) * g.nbq + i) * ca.d, qreg);
+      const int64_t cbase = bk * g.nbk * g.pool * ca.d;
 #pragma unroll
-    for (int j = 0; j < kSmallJ; ++j) {
-      unsigned long long bu = __ballot(unc[j]);
-      while (bu) {
-        const int src_lane = __ffsll((long long)bu) - 1;
-        bu &= bu - 1;
-        const unsigned int kc = __shfl(key[j], src_lane, 64);
-        const int cc = src_lane + 64 * j;
+      for (int j = 0; j < kSmallJ; ++j)
+        if (!((uncm >> j) & 1u)) key[j] = 0u;
+      unsigned int rem = uncm;
+      while (true) {
+        const int lj = rem ? __ffs(rem) - 1 : 32;  // the lane's first band slot
+        int jmin = lj;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) jmin = min(jmin, __shfl_xor(jmin, off, 64));
+        if (jmin == 32) break;
+        const int src_lane = __ffsll((long long)__ballot(lj == jmin)) - 1;
+        const int64_t c = src_lane + 64 * jmin;
+        const unsigned int k = cert_exact_key(ca, qreg, cbase, c, g.pool);
+        if (lane == src_lane) rem &= ~(1u << jmin);
+#pragma unroll
+        for (int j = 0; j < kSmallJ; ++j)
+          if (lane + 64 * j == c) key[j] = k;
+      }
+      // rank: a band candidate is taken when fewer than m band candidates rank above it
+      unsigned int rem2 = uncm;
+      while (true) {
+        const int lj = rem2 ? __ffs(rem2) - 1 : 32;
+        int jmin = lj;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) jmin = min(jmin, __shfl_xor(jmin, off, 64));
+        if (jmin == 32) break;
+        const int src_lane = __ffsll((long long)__ballot(lj == jmin)) - 1;
+        const int cc = src_lane + 64 * jmin;
+        unsigned int kc = 0u;
+#pragma unroll
+        for (int j = 0; j < kSmallJ; ++j)
+          if (j == jmin) kc = key[j];
+        kc = __shfl(kc, src_lane, 64);
         int above = 0;
 #pragma unroll
-        for (int jj = 0; jj < kSmallJ; ++jj) {
-          const int c2 = lane + 64 * jj;
-          above += __popcll(__ballot(unc[jj] && (key[jj] > kc || (key[jj] == kc && c2 < cc))));
+        for (int jj = 0; jj < kSmallJ; ++jj)
+          above += __popcll(__ballot(((uncm >> jj) & 1u) &&
+                                     (key[jj] > kc || (key[jj] == kc && lane + 64 * jj < cc))));
+        if (lane == src_lane) {
+          rem2 &= ~(1u << jmin);
+          if (above < m) selm |= 1u << jmin;
         }
-        if (lane == src_lane) sel[j] = above < m;
       }
     }
   } else {
-    wave_select_top<kSmallJ>(key, cand, K, cmax, sel);
+    unsigned int cm = 0u;
+#pragma unroll
+    for (int j = 0; j < kSmallJ; ++j) cm |= (lane + 64 * j < cmax ? 1u : 0u) << j;
+    selm = wave_select_top<kSmallJ>(key, cm, K, cmax);
   }
   const int64_t own = row_own(g, i);
   int64_t lo = own - g.local;
@@ -1119,7 +1263,7 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
 #pragma unroll
   for (int j = 0; j < kSmallJ; ++j) {
     const int64_t c = lane + 64 * j;
-    const bool take = sel[j] || (c >= lo && c <= hi);
+    const bool take = ((selm >> j) & 1u) || (c >= lo && c <= hi);
     const unsigned long long b = __ballot(take);
     const int p = pos + __popcll(b & lt);
     if (take && p < W) out[p] = (int32_t)c;
@@ -1343,22 +1487,23 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
   SSA_REQUIRE(workspace != nullptr && workspace_bytes >= row_bytes * rows_per_i,
               SSA_ERR_WORKSPACE, "route: workspace of %zu bytes below the minimum %zu",
               workspace_bytes, row_bytes * rows_per_i);
-  // The certified fp32-MFMA scoring needs the per-tile candidate norms in front of the keys;
-  // without room for them (a workspace sized for the keys alone) the fp64 scoring runs.
+  // The certified MFMA scoring stores per-tile error magnitudes and key maxima after the keys
+  // (route_row_bytes per row); with a workspace sized for the keys alone, or operands that the
+  // 16-byte staging cannot load, the fp64 scoring runs instead.
   const int64_t nbs = nbk * pool;
   const int64_t ntile = (nbs + kNormTile - 1) / kNormTile;
-  const size_t norm_bytes = route_norm_bytes(B, Hq, nbs);
-  const bool mfma_ok = d <= 64 * kMaxQReg && workspace_bytes >= norm_bytes + row_bytes * rows_per_i;
-  char* ws = static_cast<char*>(workspace);
-  size_t key_bytes = workspace_bytes;
-  float* tnorm = nullptr;
-  if (mfma_ok) {
-    tnorm = reinterpret_cast<float*>(ws);
-    ws += norm_bytes;
-    key_bytes -= norm_bytes;
-  }
-  int64_t chunk = (int64_t)(key_bytes / (row_bytes * rows_per_i));
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool vec = d % 8 == 0 && a16(rows) && a16(mu) && (var == nullptr || a16(var)) &&
+                   (m3 == nullptr || a16(m3));
+  const bool mfma_ok = vec && d <= 64 * kMaxQReg &&
+                       workspace_bytes >= route_row_bytes(nbs) * rows_per_i;
+  const size_t per_row = mfma_ok ? route_row_bytes(nbs) : row_bytes;
+  int64_t chunk = (int64_t)(workspace_bytes / (per_row * rows_per_i));
   if (chunk > nbq) chunk = nbq;
+  unsigned int* keys = static_cast<unsigned int*>(workspace);
+  float* emag = reinterpret_cast<float*>(keys + (size_t)chunk * rows_per_i * (size_t)nbs);
+  unsigned int* tmaxp =
+      reinterpret_cast<unsigned int*>(emag + (size_t)chunk * rows_per_i * (size_t)ntile);
 
   RouteGeom g;
   g.mode = mode;
@@ -1393,10 +1538,8 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                                         kv_num, kv_idx, W);
     return launch_status("route_rows_small_kernel");
   }
-  unsigned int* keys = reinterpret_cast<unsigned int*>(ws);
   CertArgs ca{};
   ca.on = 0;
-  bool norms_done = false;
   for (int64_t i0 = 0; i0 < nbq; i0 += chunk) {
     g.i0 = i0;
     g.ni = nbq - i0 < chunk ? nbq - i0 : chunk;
@@ -1422,38 +1565,36 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                                                                  coef2, coef3, keys, rp_log2);
       SSA_TRY(launch_status("route_score_rows_kernel"));
     } else if (cand_tiles > 0 && mfma_ok) {
-      SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536 && ntile < (1ll << 31),
-                  SSA_ERR_UNSUPPORTED, "route: score grid too large");
-      if (!norms_done) {
-        route_cand_norm_kernel<<<dim3((unsigned)ntile, (unsigned)(B * Hkv)), 64, 0, stream>>>(
-            mu, var, m3, nbs, (int)d, tnorm, ntile);
-        SSA_TRY(launch_status("route_cand_norm_kernel"));
-        norms_done = true;
-      }
+      SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
+                  "route: score grid too large");
+      // tile maxima feed the tile filter of route_select_kernel (pool 1, rows of > kSmallNbk)
+      const bool tm = nbk > kSmallNbk && pool == 1;
       ca.on = 1;
       ca.rows = rows;
       ca.mu = mu;
       ca.var = var;
       ca.m3 = m3;
-      ca.tnorm = tnorm;
+      ca.emag = emag;
+      ca.tmax = tm ? tmaxp : nullptr;
       ca.ntile = ntile;
       ca.d = (int)d;
+      {  // 3n exact bf16 products summed in fp32 (1.02: their magnitudes over |a||b|), the split
+         // and dropped lo.lo terms (3.1 2^-16), the exact score's own roundings (the 16)
+        const double n = (double)((1 + (var ? 1 : 0) + (m3 ? 1 : 0)) * d);
+        ca.ecoef = 1.03 * (3.0 * n + 16.0) * 0x1p-23 + 0x1p-14;
+      }
       ca.coef2 = coef2;
       ca.coef3 = coef3;
       dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
-      // 16-byte staging loads: d a multiple of 8 and 16-byte aligned rows and summaries
-      const bool vec = d % 8 == 0 && (reinterpret_cast<uintptr_t>(rows) & 15u) == 0 &&
-                       (reinterpret_cast<uintptr_t>(mu) & 15u) == 0 &&
-                       (var == nullptr || (reinterpret_cast<uintptr_t>(var) & 15u) == 0) &&
-                       (m3 == nullptr || (reinterpret_cast<uintptr_t>(m3) & 15u) == 0);
-#define SSA_SCORE_MFMA(E, V)                                                                       \
-  route_score_mfma_kernel<E, V><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,    \
-                                                          coef3, keys, row_tiles, cand_tiles)
+#define SSA_SCORE_MFMA(E, T)                                                                       \
+  route_score_mfma_kernel<E, T><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,    \
+                                                          coef3, keys, emag, tmaxp, ntile,         \
+                                                          row_tiles, cand_tiles)
       if (m3 != nullptr) {
-        if (vec) SSA_SCORE_MFMA(true, true);
+        if (tm) SSA_SCORE_MFMA(true, true);
         else SSA_SCORE_MFMA(true, false);
       } else {
-        if (vec) SSA_SCORE_MFMA(false, true);
+        if (tm) SSA_SCORE_MFMA(false, true);
         else SSA_SCORE_MFMA(false, false);
       }
 #undef SSA_SCORE_MFMA
@@ -1475,18 +1616,27 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     }
     const int64_t nrows = B * Hq * g.ni;
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
-    if (nbk <= 256)  // few candidates: a wave per row
-      route_select_small_kernel<4><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
-          keys, g, kv_num, kv_idx, W, nrows, ca);
-    else if (nbk <= kSmallNbk)
-      route_select_small_kernel<16><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(
-          keys, g, kv_num, kv_idx, W, nrows, ca);
-    else if (nrows < 1024)  // few rows (e.g. a decode step): more threads per row
-      route_select_kernel<1024><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, W,
-                                                                       ca);
-    else
-      route_select_kernel<kSelThreads><<<(unsigned)nrows, kSelThreads, 0, stream>>>(
-          keys, g, kv_num, kv_idx, W, ca);
+    const int qr = d <= 64 ? 1 : d <= 128 ? 2 : d <= 256 ? 4 : 8;  // (cert rows: d <= 512)
+#define SSA_SELECT(QR)                                                                             \
+  do {                                                                                             \
+    if (nbk <= 256) /* few candidates: a wave per row */                                           \
+      route_select_small_kernel<4, QR><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(          \
+          keys, g, kv_num, kv_idx, W, nrows, ca);                                                  \
+    else if (nbk <= kSmallNbk)                                                                     \
+      route_select_small_kernel<16, QR><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(         \
+          keys, g, kv_num, kv_idx, W, nrows, ca);                                                  \
+    else if (nrows < 1024) /* few rows (e.g. a decode step): more threads per row */               \
+      route_select_kernel<1024, QR><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, \
+                                                                           W, ca);                 \
+    else                                                                                           \
+      route_select_kernel<kSelThreads, QR><<<(unsigned)nrows, kSelThreads, 0, stream>>>(          \
+          keys, g, kv_num, kv_idx, W, ca);                                                         \
+  } while (0)
+    if (!ca.on || qr == 1) SSA_SELECT(1);
+    else if (qr == 2) SSA_SELECT(2);
+    else if (qr == 4) SSA_SELECT(4);
+    else SSA_SELECT(8);
+#undef SSA_SELECT
     SSA_TRY(launch_status("route_select_kernel"));
   }
   return SSA_OK;
@@ -1521,7 +1671,7 @@ extern "C" int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t t
 }
 
 extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk) {
-  return ssa::route_norm_bytes(B, Hq, nbk) + (size_t)B * (size_t)Hq * (size_t)nbq * (size_t)nbk * 4u;
+  return (size_t)B * (size_t)Hq * (size_t)nbq * ssa::route_row_bytes(nbk);
 }
 
 extern "C" int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,

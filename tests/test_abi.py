@@ -117,10 +117,10 @@ def test_workspace_queries():
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.BF16, 1, 2, 300, 64, 128) == \
         2 * 64 * 384 * 2 + 256
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F32, 1, 2, 300, 64, 128) == 0
-    # the per-64-candidate-tile norms of the certified scoring (16 bytes per tile per head,
-    # rounded up to 256 bytes), then the score keys
+    # per routed row: the score keys, then the certified scoring's error magnitude and largest
+    # key per 64-candidate tile
     assert _lib.query("ssa_route_workspace_size", 1, 14, 1024, 1024) == \
-        14 * 16 * 16 + 14 * 1024 * 1024 * 4
+        14 * 1024 * (1024 * 4 + 16 * 8)
     assert _lib.query("ssa_decode_attend_workspace_size", 1, 14, 1, 66, 64) == 14 * 66 * 66 * 4
 
 
