@@ -36,6 +36,28 @@ METRIC = "routed prefill tokens/s @128K (Qwen-0.5B shape); decode ms/step @1M ct
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 PEAK_FP64_TFLOPS = 78.6
+
+
+def router_fields(Hq, Hkv, nb, d, ms):
+    """Budget-mode router work at Hq/Hkv heads over nb blocks: the reference einsum's FLOPs
+    (2 * 2d per routable pair, row i against blocks c < i) and the bf16 MFMA FLOPs the score kernel
+    issues: per key head, the Hq/Hkv heads' rows in 64-row tiles against the 64-candidate tiles
+    below the tile's last row, three products per pair and head dim."""
+    G = Hq // Hkv
+    flops = 2.0 * (2 * d) * Hq * nb * (nb - 1) / 2
+    R = G * nb
+    tiles = 0
+    for r0 in range(0, R, 64):
+        r_last = min(r0 + 63, R - 1)
+        imax = nb - 1 if r0 // nb != r_last // nb else r_last % nb
+        tiles += -(-imax // 64)
+    mfma = 3.0 * 2.0 * (2 * d) * 64 * 64 * tiles * Hkv
+    s = ms / 1e3
+    return {"ms": ms, "flops": flops, "mfma_flops": mfma, "tflops": flops / s / 1e12,
+            "mfma_tflops": mfma / s / 1e12, "frac_bf16_mfma_peak": mfma / s / 1e12 / PEAK_BF16_TFLOPS,
+            "method": "bf16-split MFMA scores (3 products per fp32 product), certified: the "
+                      "candidates within the error bound of the keep-th score are ranked by the "
+                      "exact fp64-accumulated score"}
 IVF_NPROBE = 4          # build_ivf's default (ssa/ivf_kernel.py:63)
 TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
 
@@ -318,7 +340,6 @@ def main():
     diag = cfg.Hq * cfg.nb
     flops_causal = 4.0 * cfg.d * (blk * blk * (sum_kv - diag) + diag * blk * (blk + 1) / 2)
     summary_bytes = (cfg.Hkv + cfg.Hq) * n * cfg.d * 2 + (2 * cfg.Hkv + cfg.Hq) * cfg.nb * cfg.d * 4
-    router_flops = 2.0 * (2 * cfg.d) * cfg.Hq * cfg.nb * (cfg.nb - 1) / 2
     log(f"bench: {ms_step:.3f} ms/step; parts {parts}; sum kv_num {sum_kv}")
 
     result = {
@@ -336,6 +357,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "sparse_attn_dma_kernel",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "traffic_source": f"committed rocprofv3 FETCH/WRITE_SIZE profile "
+                                       f"({TRAFFIC_FILE.name}), not measured in this run",
                      "flops_per_launch": flops, "flops_causal_exact": flops_causal,
                      "sum_kv_num": sum_kv, "l2_hit_rate": l2_hit,
                      "gathered_kv_bytes": sum_kv * 2 * blk * cfg.d * 2},
@@ -344,13 +367,11 @@ def main():
         "summaries": {"bytes": summary_bytes, "ms": parts["qmean"] + parts["kstats"],
                       "hbm_frac": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3)
                       / 1e9 / PEAK_HBM_GBS},
-        # the router's inner products accumulate in fp64 on the VALU (exact selections); its
-        # FLOPs are set against the bf16 MFMA peak as asked, and against the fp64 peak it runs at
-        "router": {"flops": router_flops, "ms": parts["route"],
-                   "tflops": router_flops / (parts["route"] / 1e3) / 1e12,
-                   "frac_bf16_mfma_peak": router_flops / (parts["route"] / 1e3) / 1e12
-                   / PEAK_BF16_TFLOPS,
-                   "frac_fp64_peak": router_flops / (parts["route"] / 1e3) / 1e12 / PEAK_FP64_TFLOPS},
+        # the router scores on bf16 MFMA (each fp32 product as three bf16 products of a hi/lo
+        # split) and certifies its selection, ranking the error band exactly; "flops" counts the
+        # reference's einsum (2 * 2d per routable pair), "mfma_flops" what the score kernel
+        # issues (its 64 x 64 tiles, three products each); ms is the whole route (score + select)
+        "router": router_fields(cfg.Hq, cfg.Hkv, cfg.nb, cfg.d, parts["route"]),
     }
     result["device"] = device_info(torch, dev)
 
@@ -367,6 +388,8 @@ def main():
                 2 * cfg.top_c)
     torch.cuda.synchronize()
     result["c3_ivf"] = {
+        "note": "approximate (sub-linear) IVF router timing, beside the exact router's; its "
+                "selections differ from the exact ones",
         "router": f"IVF over each key head's {nb3} block means: nlist {idx3.nlist}, nprobe "
                   f"{IVF_NPROBE}, search_k {2 * cfg.top_c}, top_c {cfg.top_c} + local {cfg.local}",
         "build_ms": ti.mean_ms("ivf_build"), "route_ms": ti.mean_ms("ivf_route"),
@@ -521,9 +544,13 @@ def main():
             "tokens_per_s": c5.n / ((router + attn) / 1e3),
             "summaries_ms": t5.mean_ms("summaries") + t5.mean_ms("summaries_k"),
             "route_ms": t5.mean_ms("route"), "attention_kernel_ms": t5.mean_ms("attention"),
+            "router": router_fields(1, 1, nb5, c5.d, t5.mean_ms("route")),
             "attention_tflops": 4.0 * c5.block * c5.block * c5.d * kv5 / (t5.mean_ms("attention") / 1e3) / 1e12,
             "sum_kv_num": kv5,
             "ivf": {
+                "note": "approximate (sub-linear) IVF router timing on C5's inputs, not a C5 "
+                        "result: its selections differ from the exact router's (Jaccard "
+                        "similarity below)",
                 "router": f"IVF over the 49152 key-block means: nlist {idx5.nlist} lists by "
                           f"10 rounds of spherical k-means, nprobe {IVF_NPROBE}, search_k "
                           f"{2 * c5.top_c}, top_c {c5.top_c} + local {c5.local}",

@@ -109,9 +109,12 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
  *   The top min(keep, #candidates) candidates are unioned with the own block and its `local`
  *   predecessors, clipped to [0, own], and written ascending: kv_num (B,Hq,nbq) and
  *   kv_idx (B,Hq,nbq,W) (ssa/ssa_kernel.py:113-118 without the dense argsort).
- * W must be >= the largest row count (ssa_route_width() computes it). The workspace holds the
- * score keys of a chunk of rows; ssa_route_workspace_size() gives the size that routes every
- * row in one pass, and any size >= ssa_route_workspace_size(B, Hq, 1, nbk, ...) works.
+ * W must be >= the largest row count (ssa_route_width() computes it). The workspace holds, for a
+ * chunk of rows, the score keys and per 64-candidate tile an error magnitude and a key maximum;
+ * ssa_route_workspace_size() gives the size that routes every row in one pass, and any size
+ * >= ssa_route_workspace_size(B, Hq, 1, nbk) works. With at least B*Hq*nbk*4 bytes but less
+ * than ssa_route_workspace_size(B, Hq, 1, nbk) the scores are computed exactly in fp64 instead
+ * of by the certified MFMA contraction (the selection is the same either way).
  */
 int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c, float budget_frac,
                         int64_t local, int64_t query_pos, int64_t block);

@@ -163,6 +163,60 @@ def test_route_ties_take_lowest_index(cuda):
         assert s == frozenset(list(range(min(3, i))) + [i]), (i, s)
 
 
+@pytest.mark.parametrize("nbk", [600, 6000])
+@pytest.mark.parametrize("case", ["near_ties", "exact_ties", "distinct_tiles", "boundary_tie"])
+def test_certified_router_band_cases(cuda, nbk, case):
+    """The certified MFMA router (more than 16 rows per key head: 2 query heads x 40 rows) on
+    inputs that stress its certificate, against the exact oracle selection row by row.
+    near_ties: every candidate mean lies within 1e-6 relative of one vector, so every score
+    falls inside the error band -- the whole row is ranked exactly (a wave-uniform rescoring
+    loop for 600 blocks, the wide-band fallback for 6000). exact_ties: 100 identical best blocks
+    straddle the keep-th place (lowest indices win). distinct_tiles: 64 planted winners, one per
+    64-block tile at 6000 blocks, so the tile-maximum filter keeps exactly keep candidates and
+    the band reaches below its threshold (at 600 blocks, 9 tiles, the winners lie anywhere).
+    boundary_tie: as distinct_tiles plus an exact copy of the weakest winner outside the winners'
+    tiles (a band of two, ranked by index)."""
+    rng = np.random.default_rng(31)
+    d, block, keep, rows_per_head = 64, 64, 64, 40
+    q = rng.standard_normal((1, 2, rows_per_head, d)).astype(np.float32)
+    mu = rng.standard_normal((1, 1, nbk, d)).astype(np.float32) * 0.1
+    var = rng.uniform(0.5, 1.5, (1, 1, nbk, d)).astype(np.float32)
+    if case == "near_ties":
+        base = rng.standard_normal(d).astype(np.float32)
+        mu[0, 0] = base * (1.0 + 1e-6 * rng.standard_normal((nbk, 1))).astype(np.float32)
+        var[:] = 1.0
+    elif case == "exact_ties":
+        best = rng.choice(nbk, 100, replace=False)
+        var[0, 0, best] = 4.0
+        mu[0, 0, best] = 0.0
+    else:
+        if nbk // 64 >= keep:
+            tiles = rng.choice(nbk // 64, keep, replace=False)
+            won = tiles * 64 + rng.integers(0, 64, keep)
+        else:  # fewer tiles than winners (the one-wave select): winners anywhere
+            won = rng.choice(nbk, keep, replace=False)
+            tiles = np.unique(won // 64)
+        var[0, 0, won] = (6.0 + 0.01 * np.arange(keep))[:, None]
+        mu[0, 0, won] = 0.0
+        if case == "boundary_tie":
+            weakest = won[0]
+            free = np.setdiff1d(np.arange(nbk), won)
+            free_tiles = np.setdiff1d(np.arange(nbk // 64), tiles)
+            twin = free_tiles[0] * 64 + 5 if len(free_tiles) else free[0]
+            var[0, 0, twin] = var[0, 0, weakest]
+            mu[0, 0, twin] = mu[0, 0, weakest]
+    pos0 = nbk * block - rows_per_head
+    kv_num, kv_idx = K.route(dev(q, torch.float32, cuda), dev(mu, torch.float32, cuda),
+                             dev(var, torch.float32, cuda), None, "query", keep, 0.0, 1, 1.0,
+                             query_pos=pos0, block=block)
+    gn, gi = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    keys = O.score_keys(O.scores(q, mu, var, 1.0))
+    for h in range(2):
+        for r in range(rows_per_head):
+            sel = O.select_row(keys[0, h, r], r, "query", keep, 0.0, 1, pos0, block)
+            assert gi[0, h, r, :gn[0, h, r]].tolist() == sel, (case, nbk, h, r)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(4, 1, 3, 40, "started"), (2, 1, 1, 500, "query"),
                                    (4, 2, 24, 300, "query"), (1, 1, 200, 200, "budget")])
