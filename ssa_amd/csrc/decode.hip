@@ -17,8 +17,11 @@
 #include <mutex>
 
 #include "common.h"
+#include "select.h"
 
 namespace ssa {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 int launch_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n, int64_t d,
                          int64_t sb, int64_t sh, int64_t sn, int64_t block, int64_t n_real,
@@ -105,12 +108,34 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// Partial softmax attention of query row (b, h, r) over key block c: (m, l, o[d]) into part.
-template <int DT>
+// Orders one wave's LDS writes before its later LDS reads (other lanes' data).
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stores of a partial result: plain, or (FUSED) relaxed agent-scope atomic stores, which are
+// performed at the device's coherence point, so a workgroup on another XCD can read them with
+// agent-scope loads once the writer's stores have completed.
+template <bool FUSED>
+__device__ inline void put_part(float* p, float x) {
+  if constexpr (FUSED) __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = x;
+}
+
+// Partial softmax attention of query row (b, h, r) over key block c: (m, l, o[d]) into part,
+// computed by one wave (qs, ps: that wave's LDS). FUSED: the wave is one of several in its
+// workgroup (wave-local LDS ordering) and stores with put_part<true>.
+template <int DT, bool FUSED = false>
 __device__ inline void block_partial(const DecodeParams& p, float* part, float* qs, float* ps,
                                      int64_t b, int64_t h, int64_t kvh, int64_t r, int64_t pos,
                                      int64_t c) {
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  auto lds_sync = []() {
+    if constexpr (FUSED) wave_lds_sync();
+    else __syncthreads();
+  };
   const int d = (int)p.d;
   const int64_t key0 = c * p.block;
   int64_t key1 = key0 + p.block;
@@ -134,27 +159,89 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   auto vrow = [&](int64_t key) -> const char* {
     return key == newkey ? p.v_new + (b * p.vnb + kvh * p.vnh) * es : p.v + (voff + key * p.vsn) * es;
   };
+  const char* qb = p.q;
+  const int64_t qoff = b * p.qsb + h * p.qsh + r * p.qsn;
+  // FUSED: the query elements are loaded first and staged after the K / V loads are issued, so
+  // that staging waits for the query only
+  float qx[2] = {0.0f, 0.0f};
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (lane + 64 * u < d) qx[u] = load_elem<DT>(qb, qoff + lane + 64 * u);
+  }
   u32x4 vpre[kPre];
   if constexpr (DT != SSA_F32) {
     if (pre) {
+      if constexpr (FUSED) {  // unconditional loads (past the block: its last key, unused)
+        const int chc = ch * 8 < d ? ch : d / 8 - 1;
 #pragma unroll
-      for (int t = 0; t < kPre; ++t) {
-        const int kk = kg + 8 * t;
-        vpre[t] = u32x4{0u, 0u, 0u, 0u};
-        if (kk < nk && ch * 8 < d)
+        for (int t = 0; t < kPre; ++t) {
+          const int kk = kg + 8 * t < nk ? kg + 8 * t : nk - 1;
           vpre[t] = *reinterpret_cast<const u32x4*>(
-              reinterpret_cast<const unsigned short*>(vrow(key0 + kk)) + ch * 8);
+              reinterpret_cast<const unsigned short*>(vrow(key0 + kk)) + chc * 8);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < kPre; ++t) {
+          const int kk = kg + 8 * t;
+          vpre[t] = u32x4{0u, 0u, 0u, 0u};
+          if (kk < nk && ch * 8 < d)
+            vpre[t] = *reinterpret_cast<const u32x4*>(
+                reinterpret_cast<const unsigned short*>(vrow(key0 + kk)) + ch * 8);
+        }
       }
     }
   }
 
-  const char* qb = p.q;
-  const int64_t qoff = b * p.qsb + h * p.qsh + r * p.qsn;
-  for (int e = lane; e < d; e += 64) qs[e] = load_elem<DT>(qb, qoff + e);
-  __syncthreads();
+  // FUSED (one wave of several per CU: registers to spare): the lane's K rows of such a block
+  // (keys lane, lane + 64) are loaded with the V rows, before the query row is staged
+  u32x4 kpre[2][8];
+  if constexpr (FUSED && DT != SSA_F32) {
+    if (pre) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int kk = lane + 64 * t < nk ? lane + 64 * t : nk - 1;
+        const unsigned short* kr = reinterpret_cast<const unsigned short*>(krow(key0 + kk));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          kpre[t][e] = *reinterpret_cast<const u32x4*>(kr + (e * 8 < d ? e : d / 8 - 1) * 8);
+      }
+    }
+  }
+
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (lane + 64 * u < d) qs[lane + 64 * u] = qx[u];
+  } else {
+    for (int e = lane; e < d; e += 64) qs[e] = load_elem<DT>(qb, qoff + e);
+  }
+  lds_sync();
 
   float mloc = -INFINITY;
-  for (int kk = lane; kk < nk; kk += 64) {
+  if constexpr (FUSED && DT != SSA_F32) {
+    if (pre) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int kk = lane + 64 * t;
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (e * 8 >= d) break;  // uniform
+          float kv[8];
+          unpack8(kpre[t][e], kv, DT == SSA_BF16);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) s = fmaf(qs[e * 8 + u], kv[u], s);
+        }
+        if (kk < nk) {
+          const float sl = s * p.scale_log2;
+          ps[kk] = sl;
+          mloc = fmaxf(mloc, sl);
+        }
+      }
+    }
+  }
+  for (int kk = lane; kk < nk && !(FUSED && DT != SSA_F32 && pre); kk += 64) {
     const char* kr = krow(key0 + kk);
     float s = 0.0f;
     if constexpr (DT == SSA_F32) {
@@ -180,7 +267,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     mloc = fmaxf(mloc, sl);
   }
   const float m = wave_max(mloc);
-  __syncthreads();
+  lds_sync();
   float lloc = 0.0f;
   for (int kk = lane; kk < nk; kk += 64) {
     const float pk = exp2f(ps[kk] - m);
@@ -188,13 +275,13 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     lloc += pk;
   }
   const float l = wave_sum(lloc);
-  __syncthreads();
+  lds_sync();
   if constexpr (DT == SSA_F32) {
     for (int e = lane; e < d; e += 64) {
       float acc = 0.0f;
       for (int kk = 0; kk < nk; ++kk)
         acc = fmaf(ps[kk], load_elem<DT>(vrow(key0 + kk), e), acc);
-      part[2 + e] = acc;
+      put_part<FUSED>(&part[2 + e], acc);
     }
   } else if (pre) {  // the prefetched V rows; the 8 key groups summed with shuffles
     float acc[8];
@@ -221,7 +308,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     }
     if (kg == 0 && ch * 8 < d)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) part[2 + ch * 8 + t] = acc[t];
+      for (int t = 0; t < 8; ++t) put_part<FUSED>(&part[2 + ch * 8 + t], acc[t]);
   } else {
     // 8 keys per pass, 16-byte V row loads; the 8 key groups are summed with shuffles.
     for (int e0 = 0; e0 < d; e0 += 64) {
@@ -251,12 +338,12 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
       }
       if (kg == 0 && on)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) part[2 + e0 + ch * 8 + t] = acc[t];
+        for (int t = 0; t < 8; ++t) put_part<FUSED>(&part[2 + e0 + ch * 8 + t], acc[t]);
     }
   }
   if (lane == 0) {
-    part[0] = m;
-    part[1] = l;
+    put_part<FUSED>(&part[0], m);
+    put_part<FUSED>(&part[1], l);
   }
 }
 
@@ -372,6 +459,506 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
       store_elem<DT>(const_cast<char*>(p.v), b * p.vsb + kvh * p.vsh + pos * p.vsn + e,
                      load_elem<DT>(p.v_new, b * p.vnb + kvh * p.vnh + e));
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Fused decode step: two launches per step.
+// decode_route_kernel: grid (ceil(ncand / kDChunk), B*Hkv). A workgroup scores kDChunk candidate
+//   blocks of one key head for all G query rows of that head -- exact: fp64 sums over the head
+//   dim from the fp32 operands (q, fl32(q*q) broadcast from LDS), the fp32 score assembled as
+//   route_score_kernel does -- and keeps each row's chunk top-K by (key desc, block asc) with the
+//   chunk's K-th key. A chunk's top-K holds every candidate of the chunk that can be in the
+//   row's top-K (one it drops has K candidates of its chunk ranked above it). Workgroup (0, 0)
+//   also clears the arrival counters of the attend launch.
+// decode_attend_fused_kernel: grid (ceil(W / 4), B*Hq), 4 waves. Every workgroup of a row merges
+//   the row's chunk lists: T_lb = the largest chunk K-th key bounds the row's K-th key from
+//   below, so only entries >= T_lb (every member of the top-K) go to LDS; a block-wide bit search
+//   finds the K-th key T, keys > T are taken and ties at T by lowest block index (a tie bitmap
+//   scanned in order), the own block and its `local` predecessors are added, and the list is
+//   compacted ascending. Wave w then attends slot 4*blockIdx.x + w of the list (block_partial)
+//   and stores its partial with agent-scope stores; after each wave's stores have completed, an
+//   agent-scope arrival counter per row picks the row's last workgroup, which reads the partials
+//   with agent-scope loads, combines them, and writes the output row and (kv_num, kv_idx).
+// ---------------------------------------------------------------------------------------------
+constexpr int kDChunk = 256;     // candidate blocks per route workgroup
+constexpr int kDTop = 64;        // largest keep of the fused step
+constexpr int kDMaxRows = 16;    // query rows per key head (G)
+constexpr int kDMaxD = 128;      // head dim
+constexpr int kDMaxBlock = 512;  // keys per block
+constexpr int kDSurv = 4096;     // merged entries held in LDS (nchunk * K <= kDSurv)
+constexpr int kDBitWords = 1024; // bitmap words: blocks <= own < 32768
+constexpr int kDMaxW = 128;
+
+struct FusedStep {
+  const char* q;  // (B, Hq, d) query rows of the step
+  int64_t qsb, qsh;
+  const float* mu;
+  const float* var;
+  int64_t B, Hq, Hkv, G, d, nbk, ncand, K, local, pos, block, W;
+  float coef2;
+  int nchunk, ngroups;
+  unsigned int* arrive;  // (B*Hq) arrival counters
+  unsigned int* ckth;    // (B*Hq, nchunk): entries the chunk kept (min(K, its candidates))
+  unsigned int* ckey;    // (B*Hq, nchunk, kDTop): the chunk's kept keys, best first, then 0
+  unsigned int* cidx;
+  int32_t* kv_num;       // (B*Hq)
+  int32_t* kv_idx;       // (B*Hq, W)
+};
+
+// Bitonic sort of one (key, block) pair per lane across the wave: descending keys, ties by
+// ascending block (the router's order); lane j ends with the (j+1)-th.
+__device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      const unsigned int ok = __shfl_xor(key, j, 64), ob = __shfl_xor(blk, j, 64);
+      // does the partner rank before this lane's pair?
+      const bool before = ok > key || (ok == key && ob < blk);
+      const bool lower = (lane & j) == 0, desc = (lane & k) == 0;
+      // the lower lane of a descending pair keeps the better pair, and so on
+      const bool take = (lower == desc) ? before : !before;
+      if (take) {
+        key = ok;
+        blk = ob;
+      }
+    }
+}
+
+template <int DT, int DQ>
+__global__ __launch_bounds__(1024) void decode_route_kernel(FusedStep f) {
+  __shared__ double qd[kDMaxRows][kDMaxD + 1];   // q as fp64 (rows padded: conflict-free reads)
+  __shared__ double q2d[kDMaxRows][kDMaxD + 1];  // fl32(q*q) as fp64
+  __shared__ unsigned int skey[kDMaxRows][kDChunk];
+  __shared__ unsigned int sbuf[16][2][64];       // per wave: a row's kept entries
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t bk = blockIdx.y, b = bk / f.Hkv, kvh = bk % f.Hkv;
+  const int64_t c0 = (int64_t)blockIdx.x * kDChunk;
+  const int G = (int)f.G;
+  constexpr int d = 4 * DQ;
+  if (blockIdx.x == 0 && blockIdx.y == 0)
+    for (int64_t t = tid; t < f.B * f.Hq; t += 1024)
+      __hip_atomic_store(&f.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the query element of this thread first (row tid / d, dim tid % d; 16 * d <= 2048 elements),
+  // then the candidate operands, so that staging the query waits for the query load only
+  float qx[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int idx = tid + 1024 * u, r = idx / d, k = idx % d;
+    qx[u] = idx < kDMaxRows * d && r < G ? load_elem<DT>(f.q, b * f.qsb + (kvh * G + r) * f.qsh + k)
+                                          : 0.0f;
+  }
+  // Scores on v_mfma_f64_16x16x4_f64 (lane l supplies A[l%16][l/16] and B[l/16][l%16];
+  // accumulator j of lane l is C[4j + l/16][l%16]): A = the G query rows (padded to 16), B = 16
+  // candidates per wave, the 4-wide k of step s being head dims g*DQ + s of lane group g = l/16:
+  // lane l holds dims [g*DQ, +DQ) of candidate l%16 in registers, loaded up front as 16-byte
+  // vectors (a candidate past the last one reads the last one; its score is discarded).
+  // E1 = <q, mu> and E2 = <q*q, var> accumulate in fp64 in two chains.
+  const int g = lane >> 4, n16 = lane & 15;
+  const int64_t c = c0 + wv * 16 + n16;
+  const bool cv = c < f.ncand;
+  const int64_t cl = cv ? c : (f.ncand > 0 ? f.ncand - 1 : 0);
+  float mm[DQ], vv[DQ];
+  {
+    const float* pm = f.mu + (bk * f.nbk + cl) * d + g * DQ;
+    const float* pv = f.var + (bk * f.nbk + cl) * d + g * DQ;
+#pragma unroll
+    for (int e = 0; e < DQ; e += 4) {
+      const f32x4 m4 = *reinterpret_cast<const f32x4*>(pm + e);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(pv + e);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        mm[e + t] = m4[t];
+        vv[e + t] = v4[t];
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int idx = tid + 1024 * u, r = idx / d, k = idx % d;
+    if (idx < kDMaxRows * d) {
+      qd[r][k] = (double)qx[u];
+      q2d[r][k] = (double)(qx[u] * qx[u]);  // rounded to fp32 like the reference's product
+    }
+  }
+  __syncthreads();
+  typedef double f64x4 __attribute__((ext_vector_type(4)));
+  f64x4 a1 = {0.0, 0.0, 0.0, 0.0}, a2 = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int s = 0; s < DQ; ++s) {
+    a1 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[n16][g * DQ + s], (double)mm[s], a1, 0, 0, 0);
+    a2 = __builtin_amdgcn_mfma_f64_16x16x4f64(q2d[n16][g * DQ + s], (double)vv[s], a2, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * j + g;
+    if (r < G)
+      skey[r][wv * 16 + n16] =
+          cv ? score_key(__fadd_rn((float)a1[j], __fmul_rn(f.coef2, (float)a2[j]))) : 0u;
+  }
+  __syncthreads();
+  const int64_t nvalid = f.ncand - c0 < kDChunk ? f.ncand - c0 : kDChunk;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int r = wv; r < G; r += 16) {
+    unsigned int key[4], cm = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      key[j] = skey[r][lane + 64 * j];
+      cm |= (lane + 64 * j < nvalid ? 1u : 0u) << j;
+    }
+    const unsigned int selm = wave_select_top<4>(key, cm, f.K, nvalid);
+    // the kept entries (at most K <= 64) to one lane each, sorted, then stored: entry j of a
+    // chunk list is its (j+1)-th best, key 0 past its kept entries
+    int at = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool take = (selm >> j) & 1u;
+      const unsigned long long bt = __ballot(take);
+      if (take) {
+        const int slot = at + (int)__popcll(bt & lt);
+        sbuf[wv][0][slot] = key[j];
+        sbuf[wv][1][slot] = (unsigned int)(c0 + lane + 64 * j);
+      }
+      at += (int)__popcll(bt);
+    }
+    wave_lds_sync();
+    unsigned int sk = lane < at ? sbuf[wv][0][lane] : 0u, sb = lane < at ? sbuf[wv][1][lane] : 0u;
+    wave_lds_sync();
+    wave_sort_desc(sk, sb);
+    const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + blockIdx.x;
+    f.ckey[cb * kDTop + lane] = sk;
+    f.cidx[cb * kDTop + lane] = sb;
+    if (lane == 0) f.ckth[cb] = (unsigned int)at;  // entries kept
+  }
+}
+
+__device__ inline unsigned int block_sum_u32(unsigned int x, unsigned int* red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  __syncthreads();
+  if (lane == 0) red[wv] = x;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, DecodeParams p) {
+  __shared__ unsigned int skey[kDSurv], sidx[kDSurv];
+  __shared__ unsigned int sel[kDBitWords], tie[kDBitWords];
+  __shared__ int32_t list[kDMaxW];
+  __shared__ __attribute__((aligned(16))) float qs[4][kDMaxD];
+  __shared__ float ps[4][kDMaxBlock];
+  __shared__ float wgt[kDMaxW];
+  __shared__ unsigned int red[4], rand_[4], hist[256];  // (hist: also reduction scratch)
+  __shared__ unsigned int sh_n, sh_last;
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t row = blockIdx.y;  // b*Hq + h
+  const int64_t b = row / f.Hq, h = row % f.Hq, kvh = h / f.G;
+  const int64_t pos = f.pos;
+  const int64_t own = pos / f.block;
+  const int nwords = (int)((own + 32) / 32);  // bits of blocks 0..own
+  const unsigned long long lt = (1ull << lane) - 1ull;
+
+  // ---- merge the row's chunk lists ----
+  // T_lb, a lower bound of the row's K-th key from the sorted chunk lists: the best chunk's K-th
+  // key, and the smallest r-th key over the chunks that kept K entries (nf of them, r = ceil(K /
+  // nf): nf * r >= K entries reach it). Every chunk but the last holds kDChunk > K candidates,
+  // so nf is nchunk or nchunk - 1: both r are loaded in the same round.
+  for (int w = tid; w < nwords; w += 256) {
+    sel[w] = 0u;
+    tie[w] = 0u;
+  }
+  if (tid == 0) sh_n = 0u;
+  const int64_t K = f.K;
+  const int nch = f.nchunk;
+  const int rn = K > 0 ? (int)((K + nch - 1) / nch) : 1;
+  const int rn1 = K > 0 && nch > 1 ? (int)((K + nch - 2) / (nch - 1)) : rn;
+  unsigned int t1 = 0u, tn = 0xffffffffu, tn1 = 0xffffffffu, nf = 0u;
+  if (K > 0) {
+    for (int c = tid; c < nch; c += 256) {
+      const unsigned int cnt = f.ckth[row * nch + c];
+      const unsigned int* L = f.ckey + (row * nch + c) * kDTop;
+      const unsigned int k1 = L[K - 1], kn = L[rn - 1], kn1 = L[rn1 - 1];
+      if (cnt >= (unsigned int)K) {
+        ++nf;
+        t1 = k1 > t1 ? k1 : t1;
+        tn = kn < tn ? kn : tn;
+        tn1 = kn1 < tn1 ? kn1 : tn1;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned int o1 = __shfl_xor(t1, off, 64), o2 = __shfl_xor(tn, off, 64);
+    const unsigned int o3 = __shfl_xor(tn1, off, 64);
+    t1 = o1 > t1 ? o1 : t1;
+    tn = o2 < tn ? o2 : tn;
+    tn1 = o3 < tn1 ? o3 : tn1;
+    nf += __shfl_xor(nf, off, 64);
+  }
+  if (lane == 0) {
+    red[wv] = t1;
+    rand_[wv] = tn;
+    hist[wv] = tn1;
+    hist[4 + wv] = nf;
+  }
+  __syncthreads();
+  unsigned int tlb = max(max(red[0], red[1]), max(red[2], red[3]));
+  {
+    const unsigned int nfa = hist[4] + hist[5] + hist[6] + hist[7];
+    const unsigned int tna = min(min(rand_[0], rand_[1]), min(rand_[2], rand_[3]));
+    const unsigned int tn1a = min(min(hist[0], hist[1]), min(hist[2], hist[3]));
+    if (nfa == (unsigned int)nch) tlb = max(tlb, tna);
+    else if (nch > 1 && nfa == (unsigned int)(nch - 1)) tlb = max(tlb, tn1a);
+  }
+  __syncthreads();
+  {
+    // every entry of the row's chunk lists at once (kDSurv / 256 per thread; an index past the
+    // lists reads entry 0 and is dropped); unused entries (key 0) and entries below T_lb are
+    // dropped (real keys are nonzero)
+    constexpr int kE = kDSurv / 256;
+    const int ne = nch * kDTop;
+    const unsigned int floor_ = tlb > 1u ? tlb : 1u;
+    unsigned int kk[kE], ci[kE];
+#pragma unroll
+    for (int u = 0; u < kE; ++u) {
+      const int i = tid + 256 * u;
+      kk[u] = f.ckey[row * ne + (i < ne ? i : 0)];
+      ci[u] = f.cidx[row * ne + (i < ne ? i : 0)];
+    }
+#pragma unroll
+    for (int u = 0; u < kE; ++u) {
+      const bool take = tid + 256 * u < ne && kk[u] >= floor_;
+      const unsigned long long bt = __ballot(take);
+      unsigned int base = 0u;
+      if (lane == 0 && bt) base = atomicAdd(&sh_n, (unsigned int)__popcll(bt));
+      base = __shfl(base, 0, 64);
+      if (take) {
+        const unsigned int s = base + (unsigned int)__popcll(bt & lt);
+        skey[s] = kk[u];
+        sidx[s] = ci[u];
+      }
+    }
+  }
+  __syncthreads();
+  const int n = (int)sh_n;
+  if (K >= n) {  // every candidate is taken
+    for (int i = tid; i < n; i += 256) atomicOr(&sel[sidx[i] >> 5], 1u << (sidx[i] & 31));
+  } else if (K > 0) {
+    unsigned int T;
+    if (n <= 512) {  // one wave: 4 or 8 entries per lane
+      if (wv == 0) {
+        unsigned int t;
+        if (n <= 256) {
+          unsigned int key[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) key[j] = lane + 64 * j < n ? skey[lane + 64 * j] : 0u;
+          t = wave_kth_key<4>(key, K);
+        } else {
+          unsigned int key[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) key[j] = lane + 64 * j < n ? skey[lane + 64 * j] : 0u;
+          t = wave_kth_key<8>(key, K);
+        }
+        if (lane == 0) red[0] = t;
+      }
+      __syncthreads();
+      T = red[0];
+      __syncthreads();
+    } else {  // 8-bit digits from the top: a 256-bin histogram per digit
+      unsigned int prefix = 0u, pmask = 0u, kk = (unsigned int)K;
+      for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[tid] = 0u;
+        __syncthreads();
+        for (int i = tid; i < n; i += 256) {
+          const unsigned int k = skey[i];
+          if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+          unsigned int v[4], t = 0u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[j] = hist[4 * tid + j];
+            t += v[j];
+          }
+          unsigned int suf = t;  // inclusive suffix over lanes >= tid
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) {
+            const unsigned int o = __shfl_down(suf, off, 64);
+            if (tid + off < 64) suf += o;
+          }
+          unsigned int above = suf - t;  // keys in the bins of higher lanes
+#pragma unroll
+          for (int j = 3; j >= 0; --j) {
+            if (above < kk && kk <= above + v[j]) {
+              rand_[0] = (unsigned int)(4 * tid + j);
+              rand_[1] = above;
+              rand_[2] = kk == above + v[j] ? 1u : 0u;
+            }
+            above += v[j];
+          }
+        }
+        __syncthreads();
+        prefix |= rand_[0] << shift;
+        pmask |= 0xffu << shift;
+        kk -= rand_[1];
+        const bool whole = rand_[2] != 0u;
+        __syncthreads();
+        // the digit's whole bin is taken: exactly K keys are >= prefix (lower bits zero)
+        if (whole) break;
+      }
+      T = prefix;
+    }
+    unsigned int above = 0u;
+    for (int i = tid; i < n; i += 256) {
+      const unsigned int k = skey[i], c = sidx[i];
+      if (k > T) {
+        atomicOr(&sel[c >> 5], 1u << (c & 31));
+        ++above;
+      } else if (k == T) {
+        atomicOr(&tie[c >> 5], 1u << (c & 31));
+      }
+    }
+    above = block_sum_u32(above, red);
+    // ties at T: the lowest block indices, in order over the tie bitmap
+    const int need = (int)K - (int)above;
+    const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+    int tc = 0;
+    for (int w = w0; w < w0 + wpt && w < nwords; ++w) tc += __popc(tie[w]);
+    int tot;
+    int pre = block_exclusive_scan<256>(tc, wsum, &tot);
+    for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+      unsigned int m = tie[w];
+      while (m) {
+        const int bit = __ffs(m) - 1;
+        m &= m - 1;
+        if (pre < need) atomicOr(&sel[w], 1u << bit);
+        ++pre;
+      }
+    }
+  }
+  __syncthreads();
+  // own block and its `local` predecessors
+  {
+    int64_t lo = own - f.local;
+    if (lo < 0) lo = 0;
+    const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
+    for (int64_t c = lo + tid; c <= hi; c += 256) atomicOr(&sel[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  int num;
+  {
+    const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+    int cnt = 0;
+    for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(sel[w]);
+    int total;
+    int at = block_exclusive_scan<256>(cnt, wsum, &total);
+    for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+      unsigned int m = sel[w];
+      while (m) {
+        const int bit = __ffs(m) - 1;
+        m &= m - 1;
+        if (at < f.W) list[at] = w * 32 + bit;
+        ++at;
+      }
+    }
+    num = total < f.W ? total : (int)f.W;
+  }
+  __syncthreads();
+
+  // ---- attend slot 4*blockIdx.x + w ----
+  const int64_t s = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t stride = f.d + 2;
+  float* prow = p.part + row * f.W * stride;
+  if (s < num) {
+    block_partial<DT, true>(p, prow + s * stride, qs[wv], ps[wv], b, h, kvh, 0, pos, list[s]);
+  }
+  // folded append: workgroup 0 of the first query head of each key head writes the new token
+  // into the caches (every read of that row in this launch comes from k_new / v_new)
+  if (p.fused_append && blockIdx.x == 0 && h % f.G == 0 && wv == 0) {
+    for (int e = lane; e < f.d; e += 64) {
+      store_elem<DT>(const_cast<char*>(p.k), b * p.ksb + kvh * p.ksh + pos * p.ksn + e,
+                     load_elem<DT>(p.k_new, b * p.knb + kvh * p.knh + e));
+      store_elem<DT>(const_cast<char*>(p.v), b * p.vsb + kvh * p.vsh + pos * p.vsn + e,
+                     load_elem<DT>(p.v_new, b * p.vnb + kvh * p.vnh + e));
+    }
+  }
+  // every wave's stores complete before the workgroup arrives
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int old =
+        __hip_atomic_fetch_add(&f.arrive[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = old == (unsigned int)(f.ngroups - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!sh_last) return;  // uniform
+
+  // ---- the row's last workgroup: combine the partials ----
+  // (m_j, l_j) loaded by thread j together with the first batch of partials: partial j = w + 4u
+  // (u < kB) of wave w, lane e owning head dims e, e + 64; loads are unconditional (indices past
+  // the partials / head dims read the last one and get weight 0 / are not stored)
+  constexpr int kDE = kDMaxD / 64, kB = 17;
+  const int jc = tid < num ? tid : num - 1;
+  const float mj0 = __hip_atomic_load(&prow[jc * stride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float lj0 = __hip_atomic_load(&prow[jc * stride + 1], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+  const int nb = (num - wv + 3) / 4;  // partials of this wave
+  float acc[kDE];
+#pragma unroll
+  for (int t = 0; t < kDE; ++t) acc[t] = 0.0f;
+  float M = 0.0f, L = 0.0f;
+  for (int u0 = 0; u0 < nb || u0 == 0; u0 += kB) {
+    float x[kB][kDE];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int jw = wv + 4 * (u0 + u), j = jw < num ? jw : num - 1;  // num >= 1 (own block)
+#pragma unroll
+      for (int t = 0; t < kDE; ++t) {
+        const int e = lane + 64 * t < f.d ? lane + 64 * t : (int)f.d - 1;
+        x[u][t] = __hip_atomic_load(&prow[j * stride + 2 + e], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (u0 == 0) {  // the weights, once the first batch is in flight
+      const float mj = tid < num ? mj0 : -INFINITY, lj = tid < num ? lj0 : 0.0f;
+      M = wave_max(mj);
+      if (lane == 0) ps[0][wv] = M;
+      __syncthreads();
+      M = fmaxf(fmaxf(ps[0][0], ps[0][1]), fmaxf(ps[0][2], ps[0][3]));
+      const float wj = mj == -INFINITY ? 0.0f : exp2f(mj - M);  // empty partials: weight 0
+      if (tid < num) wgt[tid] = wj;
+      L = wave_sum(lj * wj);
+      if (lane == 0) ps[1][wv] = L;
+      __syncthreads();
+      L = ps[1][0] + ps[1][1] + ps[1][2] + ps[1][3];
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const float w = u0 + u < nb ? wgt[wv + 4 * (u0 + u)] : 0.0f;
+#pragma unroll
+      for (int t = 0; t < kDE; ++t) acc[t] = fmaf(x[u][t], w, acc[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kDE; ++t)
+    if (lane + 64 * t < f.d) qs[wv][lane + 64 * t] = acc[t];
+  __syncthreads();
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  for (int e = tid; e < f.d; e += 256)
+    store_elem<DT>(p.o, b * p.osb + h * p.osh + e, (qs[0][e] + qs[1][e] + qs[2][e] + qs[3][e]) * inv);
+  int32_t* out = f.kv_idx + row * f.W;
+  for (int j = tid; j < f.W; j += 256) out[j] = j < num ? list[j] : 0;
+  if (tid == 0) {
+    f.kv_num[row] = num;
+    __hip_atomic_store(&f.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -637,12 +1224,7 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   void* keys = ws + qf_bytes;
   float* part = reinterpret_cast<float*>(ws + qf_bytes + key_bytes);
 
-  // 1. append the new token and convert the query rows (one launch) -- unless the step can fold
-  //    the append into the attend launch: no block completes at pos (its summary would need the
-  //    token in the cache first) and the query rows are contiguous, so the router reads them as
-  //    they are
   const bool completes = (pos + 1) % block == 0;
-  const bool fold = !completes && strides[1] == d && strides[0] == Hq * d;
   AppendStrides as;
   as.knb = strides[2]; as.knh = strides[3]; as.vnb = strides[4]; as.vnh = strides[5];
   as.kcb = strides[6]; as.kch = strides[7]; as.kcn = strides[8];
@@ -654,6 +1236,34 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   const unsigned gr = (unsigned)(B * Hq);
   const char* qc = static_cast<const char*>(q);
   const int64_t G = Hq / Hkv;
+
+  // The fused two-launch step (decode_route_kernel + decode_attend_fused_kernel) serves the
+  // common shapes; its workspace lives inside the regions of the general step's.
+  const int64_t ncand = (pos + 1) / block < nbk ? (pos + 1) / block : nbk;  // complete blocks
+  int64_t keep = top_c;
+  if (top_c < 0) {
+    keep = (int64_t)ceilf(budget_frac * (float)ncand);
+    if (keep < 1) keep = 1;
+  }
+  const int64_t Kf = keep < ncand ? keep : ncand;
+  const int64_t nchunk = ncand > 0 ? (ncand + kDChunk - 1) / kDChunk : 1;
+  const int64_t own = pos / block;
+  const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t rows = (size_t)(B * Hq);
+  const size_t f_arrive = r256(rows * 4u), f_kth = r256(rows * nchunk * 4u);
+  const size_t f_list = r256(rows * nchunk * kDTop * 4u);
+  const bool fused = G <= kDMaxRows && (d == 32 || d == 64 || d == 128) && block <= kDMaxBlock &&
+                     Kf <= kDTop &&
+                     nchunk * Kf <= kDSurv && own < (int64_t)kDBitWords * 32 && W <= kDMaxW &&
+                     aligned16(mu) && aligned16(var) &&
+                     f_arrive + f_kth + 2 * f_list <= qf_bytes + key_bytes &&
+                     nchunk < 65536 && B * Hkv < 65536 && B * Hq < 65536;
+
+  // 1. append the new token (and convert the query rows for the general router) in a launch of
+  //    its own when the step completes a block (its summary needs the token in the cache) or the
+  //    general step's router cannot read the query rows as they are; otherwise the append rides
+  //    in the attend launch
+  const bool fold = !completes && (fused || (strides[1] == d && strides[0] == Hq * d));
   if (!fold) {
     switch (dtype) {
       case SSA_F32:
@@ -673,19 +1283,13 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   }
 
   // 2. a block completed at pos: its population summary becomes routable
-  if ((pos + 1) % block == 0) {
+  if (completes) {
     const int64_t c = pos / block;
     const char* blk = kc + c * block * as.kcn * es;
     SSA_TRY(launch_block_summary(blk, dtype, B, Hkv, block, d, as.kcb, as.kch, as.kcn, block, block,
                                  SSA_STATS_POP, mu, var, nullptr, nbk, c, st));
   }
 
-  // 3. route the queries over the complete blocks
-  SSA_TRY(route_impl(fold ? static_cast<const void*>(qc) : qf, fold ? dtype : SSA_F32, mu, var,
-                     nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c, budget_frac, local,
-                     coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys, key_bytes, st));
-
-  // 4. attend
   DecodeParams p;
   p.q = qc;
   p.k = kc;
@@ -707,6 +1311,49 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
     p.v_new = vn;
     p.knb = as.knb; p.knh = as.knh; p.vnb = as.vnb; p.vnh = as.vnh;
   }
+
+  if (fused) {
+    // 3+4. route (exact scores, chunk top-K) -> merge, attend, combine
+    FusedStep f;
+    f.q = qc;
+    f.qsb = strides[0];
+    f.qsh = strides[1];
+    f.mu = mu;
+    f.var = var;
+    f.B = B; f.Hq = Hq; f.Hkv = Hkv; f.G = G; f.d = d; f.nbk = nbk; f.ncand = ncand; f.K = Kf;
+    f.local = local; f.pos = pos; f.block = block; f.W = W;
+    f.coef2 = coef2;
+    f.nchunk = (int)nchunk;
+    f.ngroups = (int)((W + 3) / 4);
+    f.arrive = reinterpret_cast<unsigned int*>(ws);
+    f.ckth = reinterpret_cast<unsigned int*>(ws + f_arrive);
+    f.ckey = reinterpret_cast<unsigned int*>(ws + f_arrive + f_kth);
+    f.cidx = reinterpret_cast<unsigned int*>(ws + f_arrive + f_kth + f_list);
+    f.kv_num = kv_num;
+    f.kv_idx = kv_idx;
+    const dim3 g1((unsigned)nchunk, (unsigned)(B * Hkv)), g2((unsigned)f.ngroups, (unsigned)(B * Hq));
+#define SSA_FUSED_STEP(DT)                                                                        \
+  do {                                                                                            \
+    if (d == 32) decode_route_kernel<DT, 8><<<g1, 1024, 0, st>>>(f);                              \
+    else if (d == 64) decode_route_kernel<DT, 16><<<g1, 1024, 0, st>>>(f);                        \
+    else decode_route_kernel<DT, 32><<<g1, 1024, 0, st>>>(f);                                     \
+    decode_attend_fused_kernel<DT><<<g2, 256, 0, st>>>(f, p);                                     \
+  } while (0)
+    switch (dtype) {
+      case SSA_F32: SSA_FUSED_STEP(SSA_F32); break;
+      case SSA_F16: SSA_FUSED_STEP(SSA_F16); break;
+      default: SSA_FUSED_STEP(SSA_BF16); break;
+    }
+#undef SSA_FUSED_STEP
+    return launch_status("decode_attend_fused_kernel");
+  }
+
+  // 3. route the queries over the complete blocks
+  SSA_TRY(route_impl(fold ? static_cast<const void*>(qc) : qf, fold ? dtype : SSA_F32, mu, var,
+                     nullptr, B, Hq, Hkv, 1, nbk, d, SSA_ROUTE_QUERY, top_c, budget_frac, local,
+                     coef2, 0.0f, pos, block, 1, kv_num, kv_idx, W, keys, key_bytes, st));
+
+  // 4. attend
   return run_attend(dtype, p, st);
 }
 
