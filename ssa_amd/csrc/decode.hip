@@ -14,6 +14,8 @@
 // ssa/gemma_ssa.py:85-137,225-240 (exact per-query router and softmax at q_len = 1).
 #include <math.h>
 
+#include <type_traits>
+
 #include <mutex>
 
 #include "common.h"
@@ -464,8 +466,10 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // Fused decode step: two launches per step.
-// decode_route_kernel: grid (ceil(ncand / kDChunk), B*Hkv). A workgroup scores kDChunk candidate
-//   blocks of one key head for all G query rows of that head -- exact: fp64 sums over the head
+// decode_route_kernel<DT, DQ, NW>: grid (ceil(ncand / (16 NW)), B*Hkv), NW waves of 16
+//   candidates. A workgroup scores a chunk of 16 NW candidate blocks (128 or 256: the smaller
+//   chunk spreads the scoring over twice the CUs, when the merge below can hold its lists) of one
+//   key head for all G query rows of that head -- exact: fp64 sums over the head
 //   dim from the fp32 operands (q, fl32(q*q) broadcast from LDS), the fp32 score assembled as
 //   route_score_kernel does -- and keeps each row's chunk top-K by (key desc, block asc) with the
 //   chunk's K-th key. A chunk's top-K holds every candidate of the chunk that can be in the
@@ -481,7 +485,7 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
 //   agent-scope arrival counter per row picks the row's last workgroup, which reads the partials
 //   with agent-scope loads, combines them, and writes the output row and (kv_num, kv_idx).
 // ---------------------------------------------------------------------------------------------
-constexpr int kDChunk = 256;     // candidate blocks per route workgroup
+constexpr int kDChunk = 256;     // largest chunk of candidate blocks per route workgroup
 constexpr int kDTop = 64;        // largest keep of the fused step
 constexpr int kDMaxRows = 16;    // query rows per key head (G)
 constexpr int kDMaxD = 128;      // head dim
@@ -527,26 +531,28 @@ __device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
     }
 }
 
-template <int DT, int DQ>
-__global__ __launch_bounds__(1024) void decode_route_kernel(FusedStep f) {
+template <int DT, int DQ, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
+  constexpr int NT = NW * 64, CH = NW * 16;  // threads, candidates per workgroup
+  constexpr int NQ = kDMaxRows * kDMaxD / NT;  // query elements staged per thread
   __shared__ double qd[kDMaxRows][kDMaxD + 1];   // q as fp64 (rows padded: conflict-free reads)
   __shared__ double q2d[kDMaxRows][kDMaxD + 1];  // fl32(q*q) as fp64
-  __shared__ unsigned int skey[kDMaxRows][kDChunk];
-  __shared__ unsigned int sbuf[16][2][64];       // per wave: a row's kept entries
+  __shared__ unsigned int skey[kDMaxRows][CH];
+  __shared__ unsigned int sbuf[NW][2][64];       // per wave: a row's kept entries
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t bk = blockIdx.y, b = bk / f.Hkv, kvh = bk % f.Hkv;
-  const int64_t c0 = (int64_t)blockIdx.x * kDChunk;
+  const int64_t c0 = (int64_t)blockIdx.x * CH;
   const int G = (int)f.G;
   constexpr int d = 4 * DQ;
   if (blockIdx.x == 0 && blockIdx.y == 0)
-    for (int64_t t = tid; t < f.B * f.Hq; t += 1024)
+    for (int64_t t = tid; t < f.B * f.Hq; t += NT)
       __hip_atomic_store(&f.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // the query element of this thread first (row tid / d, dim tid % d; 16 * d <= 2048 elements),
   // then the candidate operands, so that staging the query waits for the query load only
-  float qx[2];
+  float qx[NQ];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int idx = tid + 1024 * u, r = idx / d, k = idx % d;
+  for (int u = 0; u < NQ; ++u) {
+    const int idx = tid + NT * u, r = idx / d, k = idx % d;
     qx[u] = idx < kDMaxRows * d && r < G ? load_elem<DT>(f.q, b * f.qsb + (kvh * G + r) * f.qsh + k)
                                           : 0.0f;
   }
@@ -576,8 +582,8 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(FusedStep f) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int idx = tid + 1024 * u, r = idx / d, k = idx % d;
+  for (int u = 0; u < NQ; ++u) {
+    const int idx = tid + NT * u, r = idx / d, k = idx % d;
     if (idx < kDMaxRows * d) {
       qd[r][k] = (double)qx[u];
       q2d[r][k] = (double)(qx[u] * qx[u]);  // rounded to fp32 like the reference's product
@@ -599,21 +605,22 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(FusedStep f) {
           cv ? score_key(__fadd_rn((float)a1[j], __fmul_rn(f.coef2, (float)a2[j]))) : 0u;
   }
   __syncthreads();
-  const int64_t nvalid = f.ncand - c0 < kDChunk ? f.ncand - c0 : kDChunk;
+  const int64_t nvalid = f.ncand - c0 < CH ? f.ncand - c0 : CH;
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int r = wv; r < G; r += 16) {
-    unsigned int key[4], cm = 0u;
+  constexpr int J = CH / 64;
+  for (int r = wv; r < G; r += NW) {
+    unsigned int key[J], cm = 0u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       key[j] = skey[r][lane + 64 * j];
       cm |= (lane + 64 * j < nvalid ? 1u : 0u) << j;
     }
-    const unsigned int selm = wave_select_top<4>(key, cm, f.K, nvalid);
+    const unsigned int selm = wave_select_top<J>(key, cm, f.K, nvalid);
     // the kept entries (at most K <= 64) to one lane each, sorted, then stored: entry j of a
     // chunk list is its (j+1)-th best, key 0 past its kept entries
     int at = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       const bool take = (selm >> j) & 1u;
       const unsigned long long bt = __ballot(take);
       if (take) {
@@ -655,6 +662,8 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   __shared__ unsigned int red[4], rand_[4], hist[256];  // (hist: also reduction scratch)
   __shared__ unsigned int sh_n, sh_last;
   __shared__ int wsum[4];
+  __shared__ unsigned int rth[7][64];  // r-th key of every chunk, r = 1, 2, 4, ..., 64
+  __shared__ unsigned int rbound[8];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t row = blockIdx.y;  // b*Hq + h
   const int64_t b = row / f.Hq, h = row % f.Hq, kvh = h / f.G;
@@ -664,10 +673,13 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   const unsigned long long lt = (1ull << lane) - 1ull;
 
   // ---- merge the row's chunk lists ----
-  // T_lb, a lower bound of the row's K-th key from the sorted chunk lists: the best chunk's K-th
-  // key, and the smallest r-th key over the chunks that kept K entries (nf of them, r = ceil(K /
-  // nf): nf * r >= K entries reach it). Every chunk but the last holds kDChunk > K candidates,
-  // so nf is nchunk or nchunk - 1: both r are loaded in the same round.
+  // Every entry of the row's chunk lists is loaded at once (kDSurv / 256 per thread; an index
+  // past the lists reads entry 0 and is dropped): thread (wave w, lane l) holds entry l of chunks
+  // w + 4u, so a chunk's r-th key is lane r-1's value of one register.
+  // T_lb, a lower bound of the row's K-th key from the sorted chunk lists: for r = 1, 2, 4, ...,
+  // 64, the ceil(K / r)-th largest of the chunks' r-th keys (that many chunks hold r keys at or
+  // above it: at least K entries reach it), the largest of these bounds. Real keys are nonzero;
+  // key 0 past a chunk's kept entries.
   for (int w = tid; w < nwords; w += 256) {
     sel[w] = 0u;
     tie[w] = 0u;
@@ -675,107 +687,144 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   if (tid == 0) sh_n = 0u;
   const int64_t K = f.K;
   const int nch = f.nchunk;
-  const int rn = K > 0 ? (int)((K + nch - 1) / nch) : 1;
-  const int rn1 = K > 0 && nch > 1 ? (int)((K + nch - 2) / (nch - 1)) : rn;
-  unsigned int t1 = 0u, tn = 0xffffffffu, tn1 = 0xffffffffu, nf = 0u;
-  if (K > 0) {
-    for (int c = tid; c < nch; c += 256) {
-      const unsigned int cnt = f.ckth[row * nch + c];
-      const unsigned int* L = f.ckey + (row * nch + c) * kDTop;
-      const unsigned int k1 = L[K - 1], kn = L[rn - 1], kn1 = L[rn1 - 1];
-      if (cnt >= (unsigned int)K) {
-        ++nf;
-        t1 = k1 > t1 ? k1 : t1;
-        tn = kn < tn ? kn : tn;
-        tn1 = kn1 < tn1 ? kn1 : tn1;
-      }
-    }
-  }
+  constexpr int kE = kDSurv / 256;
+  const int ne = nch * kDTop;
+  unsigned int kk[kE], ci[kE];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const unsigned int o1 = __shfl_xor(t1, off, 64), o2 = __shfl_xor(tn, off, 64);
-    const unsigned int o3 = __shfl_xor(tn1, off, 64);
-    t1 = o1 > t1 ? o1 : t1;
-    tn = o2 < tn ? o2 : tn;
-    tn1 = o3 < tn1 ? o3 : tn1;
-    nf += __shfl_xor(nf, off, 64);
+  for (int u = 0; u < kE; ++u) {
+    const int i = tid + 256 * u;
+    kk[u] = f.ckey[row * ne + (i < ne ? i : 0)];
+    ci[u] = f.cidx[row * ne + (i < ne ? i : 0)];
   }
-  if (lane == 0) {
-    red[wv] = t1;
-    rand_[wv] = tn;
-    hist[wv] = tn1;
-    hist[4 + wv] = nf;
+  // the r-th keys to LDS (chunk c = wv + 4u is lane r-1's register u)
+#pragma unroll
+  for (int u = 0; u < kE; ++u) {
+    const int c = wv + 4 * u;  // wave-uniform
+    const int lg = __popc(lane + 1) == 1 ? 31 - __clz(lane + 1) : -1;  // lane = r - 1, r = 2^lg
+    if (c < 64 && lg >= 0) rth[lg][c] = c < nch ? kk[u] : 0u;
   }
   __syncthreads();
-  unsigned int tlb = max(max(red[0], red[1]), max(red[2], red[3]));
-  {
-    const unsigned int nfa = hist[4] + hist[5] + hist[6] + hist[7];
-    const unsigned int tna = min(min(rand_[0], rand_[1]), min(rand_[2], rand_[3]));
-    const unsigned int tn1a = min(min(hist[0], hist[1]), min(hist[2], hist[3]));
-    if (nfa == (unsigned int)nch) tlb = max(tlb, tna);
-    else if (nch > 1 && nfa == (unsigned int)(nch - 1)) tlb = max(tlb, tn1a);
+  for (int lg = wv; lg < 7; lg += 4) {
+    const unsigned int r = 1u << lg;
+    const int64_t m = K > 0 ? (K + r - 1) / r : 0;  // chunks needed
+    unsigned int v[1] = {rth[lg][lane]};
+    unsigned int bnd = 0u;
+    if (m > 0 && m <= 64) bnd = wave_kth_key<1>(v, m);  // 0 when fewer than m chunks hold r keys
+    if (lane == 0) rbound[lg] = bnd;
   }
   __syncthreads();
+  unsigned int tlb = 0u;
+#pragma unroll
+  for (int lg = 0; lg < 7; ++lg) tlb = rbound[lg] > tlb ? rbound[lg] : tlb;
+  // Survivors (keys >= T_lb, real keys nonzero) go to their wave's own LDS segment
+  // [1024 w, 1024 w + n_w) in ballot order -- no atomics; survivor i of the row is entry
+  // phys(i) of the concatenated segments.
   {
-    // every entry of the row's chunk lists at once (kDSurv / 256 per thread; an index past the
-    // lists reads entry 0 and is dropped); unused entries (key 0) and entries below T_lb are
-    // dropped (real keys are nonzero)
-    constexpr int kE = kDSurv / 256;
-    const int ne = nch * kDTop;
     const unsigned int floor_ = tlb > 1u ? tlb : 1u;
-    unsigned int kk[kE], ci[kE];
-#pragma unroll
-    for (int u = 0; u < kE; ++u) {
-      const int i = tid + 256 * u;
-      kk[u] = f.ckey[row * ne + (i < ne ? i : 0)];
-      ci[u] = f.cidx[row * ne + (i < ne ? i : 0)];
-    }
+    int at = 0;
 #pragma unroll
     for (int u = 0; u < kE; ++u) {
       const bool take = tid + 256 * u < ne && kk[u] >= floor_;
       const unsigned long long bt = __ballot(take);
-      unsigned int base = 0u;
-      if (lane == 0 && bt) base = atomicAdd(&sh_n, (unsigned int)__popcll(bt));
-      base = __shfl(base, 0, 64);
       if (take) {
-        const unsigned int s = base + (unsigned int)__popcll(bt & lt);
-        skey[s] = kk[u];
-        sidx[s] = ci[u];
+        const int sl = wv * (kDSurv / 4) + at + (int)__popcll(bt & lt);
+        skey[sl] = kk[u];
+        sidx[sl] = ci[u];
       }
+      at += (int)__popcll(bt);
     }
+    if (lane == 0) wsum[wv] = at;
   }
   __syncthreads();
-  const int n = (int)sh_n;
-  if (K >= n) {  // every candidate is taken
-    for (int i = tid; i < n; i += 256) atomicOr(&sel[sidx[i] >> 5], 1u << (sidx[i] & 31));
-  } else if (K > 0) {
-    unsigned int T;
-    if (n <= 512) {  // one wave: 4 or 8 entries per lane
-      if (wv == 0) {
-        unsigned int t;
-        if (n <= 256) {
-          unsigned int key[4];
+  const int s0 = wsum[0], s1 = s0 + wsum[1], s2 = s1 + wsum[2];
+  const int n = s2 + wsum[3];
+  auto phys = [&](int i) -> int {  // survivor i -> its LDS entry
+    constexpr int SEG = kDSurv / 4;
+    return i < s0 ? i : i < s1 ? SEG + (i - s0) : i < s2 ? 2 * SEG + (i - s1) : 3 * SEG + (i - s2);
+  };
+  // one wave (J survivors per lane): K-th key, ties by lowest block, own block + local
+  // predecessors, and the ascending list from the bitmap -- no workgroup barrier until the list
+  // is done
+  auto one_wave = [&](auto jc) {
+    constexpr int J = decltype(jc)::value;
+    if (wv == 0) {
+      unsigned int key[J], blk[J];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) key[j] = lane + 64 * j < n ? skey[lane + 64 * j] : 0u;
-          t = wave_kth_key<4>(key, K);
-        } else {
-          unsigned int key[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) key[j] = lane + 64 * j < n ? skey[lane + 64 * j] : 0u;
-          t = wave_kth_key<8>(key, K);
-        }
-        if (lane == 0) red[0] = t;
+      for (int j = 0; j < J; ++j) {
+        const int i = lane + 64 * j;
+        key[j] = i < n ? skey[phys(i)] : 0u;
+        blk[j] = i < n ? sidx[phys(i)] : 0u;
       }
-      __syncthreads();
-      T = red[0];
-      __syncthreads();
-    } else {  // 8-bit digits from the top: a 256-bin histogram per digit
-      unsigned int prefix = 0u, pmask = 0u, kk = (unsigned int)K;
+      unsigned int takem = 0u;
+      if (K >= n) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) takem |= (lane + 64 * j < n ? 1u : 0u) << j;
+      } else if (K > 0) {
+        const unsigned int T = wave_kth_key<J>(key, K);
+        int above = 0, nt = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          above += (int)__popcll(__ballot(key[j] > T));
+          nt += (int)__popcll(__ballot(key[j] == T));
+        }
+        const int need = (int)K - above;  // ties at T to take, lowest block first
+        unsigned int tk[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) tk[j] = key[j] == T ? ~blk[j] : 0u;  // larger = lower block
+        const unsigned int T2 = need < nt ? wave_kth_key<J>(tk, need) : 1u;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          takem |= (key[j] > T || (key[j] == T && tk[j] >= T2) ? 1u : 0u) << j;
+      }
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if ((takem >> j) & 1u) atomicOr(&sel[blk[j] >> 5], 1u << (blk[j] & 31));
+      {
+        int64_t lo = own - f.local;
+        if (lo < 0) lo = 0;
+        const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
+        for (int64_t c = lo + lane; c <= hi; c += 64) atomicOr(&sel[c >> 5], 1u << (c & 31));
+      }
+      wave_lds_sync();
+      const int wpl = (nwords + 63) / 64, w0 = lane * wpl;
+      int cnt = 0;
+      for (int w = w0; w < w0 + wpl && w < nwords; ++w) cnt += __popc(sel[w]);
+      int incl = cnt;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      int at = incl - cnt;
+      for (int w = w0; w < w0 + wpl && w < nwords; ++w) {
+        unsigned int m = sel[w];
+        while (m) {
+          const int bit = __ffs(m) - 1;
+          m &= m - 1;
+          if (at < f.W) list[at] = w * 32 + bit;
+          ++at;
+        }
+      }
+      if (lane == 63) sh_n = (unsigned int)incl;
+    }
+    __syncthreads();
+  };
+  if (n <= 128) {
+    one_wave(std::integral_constant<int, 2>{});
+  } else if (n <= 256) {
+    one_wave(std::integral_constant<int, 4>{});
+  } else if (n <= 512) {
+    one_wave(std::integral_constant<int, 8>{});
+  } else {
+    // more survivors: workgroup-wide radix search for the K-th key and bitmaps
+    unsigned int T = 0u;
+    if (K > 0) {
+      unsigned int prefix = 0u, pmask = 0u, kk_ = (unsigned int)K;
       for (int shift = 24; shift >= 0; shift -= 8) {
         hist[tid] = 0u;
         __syncthreads();
         for (int i = tid; i < n; i += 256) {
-          const unsigned int k = skey[i];
+          const unsigned int k = skey[phys(i)];
           if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
         }
         __syncthreads();
@@ -795,10 +844,10 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
           unsigned int above = suf - t;  // keys in the bins of higher lanes
 #pragma unroll
           for (int j = 3; j >= 0; --j) {
-            if (above < kk && kk <= above + v[j]) {
+            if (above < kk_ && kk_ <= above + v[j]) {
               rand_[0] = (unsigned int)(4 * tid + j);
               rand_[1] = above;
-              rand_[2] = kk == above + v[j] ? 1u : 0u;
+              rand_[2] = kk_ == above + v[j] ? 1u : 0u;
             }
             above += v[j];
           }
@@ -806,70 +855,70 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
         __syncthreads();
         prefix |= rand_[0] << shift;
         pmask |= 0xffu << shift;
-        kk -= rand_[1];
+        kk_ -= rand_[1];
         const bool whole = rand_[2] != 0u;
         __syncthreads();
         // the digit's whole bin is taken: exactly K keys are >= prefix (lower bits zero)
         if (whole) break;
       }
       T = prefix;
-    }
-    unsigned int above = 0u;
-    for (int i = tid; i < n; i += 256) {
-      const unsigned int k = skey[i], c = sidx[i];
-      if (k > T) {
-        atomicOr(&sel[c >> 5], 1u << (c & 31));
-        ++above;
-      } else if (k == T) {
-        atomicOr(&tie[c >> 5], 1u << (c & 31));
+      unsigned int above = 0u;
+      for (int i = tid; i < n; i += 256) {
+        const unsigned int k = skey[phys(i)], c = sidx[phys(i)];
+        if (k > T) {
+          atomicOr(&sel[c >> 5], 1u << (c & 31));
+          ++above;
+        } else if (k == T) {
+          atomicOr(&tie[c >> 5], 1u << (c & 31));
+        }
+      }
+      above = block_sum_u32(above, red);
+      // ties at T: the lowest block indices, in order over the tie bitmap
+      const int need = (int)K - (int)above;
+      const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+      int tc = 0;
+      for (int w = w0; w < w0 + wpt && w < nwords; ++w) tc += __popc(tie[w]);
+      int tot;
+      int pre = block_exclusive_scan<256>(tc, wsum, &tot);
+      for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+        unsigned int m = tie[w];
+        while (m) {
+          const int bit = __ffs(m) - 1;
+          m &= m - 1;
+          if (pre < need) atomicOr(&sel[w], 1u << bit);
+          ++pre;
+        }
       }
     }
-    above = block_sum_u32(above, red);
-    // ties at T: the lowest block indices, in order over the tie bitmap
-    const int need = (int)K - (int)above;
-    const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
-    int tc = 0;
-    for (int w = w0; w < w0 + wpt && w < nwords; ++w) tc += __popc(tie[w]);
-    int tot;
-    int pre = block_exclusive_scan<256>(tc, wsum, &tot);
-    for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
-      unsigned int m = tie[w];
-      while (m) {
-        const int bit = __ffs(m) - 1;
-        m &= m - 1;
-        if (pre < need) atomicOr(&sel[w], 1u << bit);
-        ++pre;
-      }
+    __syncthreads();
+    // own block and its `local` predecessors
+    {
+      int64_t lo = own - f.local;
+      if (lo < 0) lo = 0;
+      const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
+      for (int64_t c = lo + tid; c <= hi; c += 256) atomicOr(&sel[c >> 5], 1u << (c & 31));
     }
-  }
-  __syncthreads();
-  // own block and its `local` predecessors
-  {
-    int64_t lo = own - f.local;
-    if (lo < 0) lo = 0;
-    const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
-    for (int64_t c = lo + tid; c <= hi; c += 256) atomicOr(&sel[c >> 5], 1u << (c & 31));
-  }
-  __syncthreads();
-  int num;
-  {
-    const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
-    int cnt = 0;
-    for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(sel[w]);
-    int total;
-    int at = block_exclusive_scan<256>(cnt, wsum, &total);
-    for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
-      unsigned int m = sel[w];
-      while (m) {
-        const int bit = __ffs(m) - 1;
-        m &= m - 1;
-        if (at < f.W) list[at] = w * 32 + bit;
-        ++at;
+    __syncthreads();
+    {
+      const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+      int cnt = 0;
+      for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(sel[w]);
+      int total;
+      int at = block_exclusive_scan<256>(cnt, wsum, &total);
+      for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
+        unsigned int m = sel[w];
+        while (m) {
+          const int bit = __ffs(m) - 1;
+          m &= m - 1;
+          if (at < f.W) list[at] = w * 32 + bit;
+          ++at;
+        }
       }
+      if (tid == 0) sh_n = (unsigned int)total;
     }
-    num = total < f.W ? total : (int)f.W;
+    __syncthreads();
   }
-  __syncthreads();
+  const int num = (int)sh_n < f.W ? (int)sh_n : (int)f.W;
 
   // ---- attend slot 4*blockIdx.x + w ----
   const int64_t s = (int64_t)blockIdx.x * 4 + wv;
@@ -1246,18 +1295,28 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
     if (keep < 1) keep = 1;
   }
   const int64_t Kf = keep < ncand ? keep : ncand;
-  const int64_t nchunk = ncand > 0 ? (ncand + kDChunk - 1) / kDChunk : 1;
   const int64_t own = pos / block;
   const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t rows = (size_t)(B * Hq);
+  // chunks of 128 candidates when the merge can hold their lists, else 256
+  auto fused_fits = [&](int64_t chunk, int64_t* nch_out) {
+    const int64_t nch = ncand > 0 ? (ncand + chunk - 1) / chunk : 1;
+    const size_t fa = r256(rows * 4u), fk = r256(rows * nch * 4u), fl = r256(rows * nch * kDTop * 4u);
+    *nch_out = nch;
+    return nch * Kf <= kDSurv && fa + fk + 2 * fl <= qf_bytes + key_bytes && nch < 65536;
+  };
+  int64_t nchunk = 1, chunk = kDChunk / 2;
+  bool fits = fused_fits(chunk, &nchunk);
+  if (!fits) {
+    chunk = kDChunk;
+    fits = fused_fits(chunk, &nchunk);
+  }
   const size_t f_arrive = r256(rows * 4u), f_kth = r256(rows * nchunk * 4u);
   const size_t f_list = r256(rows * nchunk * kDTop * 4u);
-  const bool fused = G <= kDMaxRows && (d == 32 || d == 64 || d == 128) && block <= kDMaxBlock &&
-                     Kf <= kDTop &&
-                     nchunk * Kf <= kDSurv && own < (int64_t)kDBitWords * 32 && W <= kDMaxW &&
-                     aligned16(mu) && aligned16(var) &&
-                     f_arrive + f_kth + 2 * f_list <= qf_bytes + key_bytes &&
-                     nchunk < 65536 && B * Hkv < 65536 && B * Hq < 65536;
+  const bool fused = fits && G <= kDMaxRows && (d == 32 || d == 64 || d == 128) &&
+                     block <= kDMaxBlock && Kf <= kDTop && own < (int64_t)kDBitWords * 32 &&
+                     W <= kDMaxW && aligned16(mu) && aligned16(var) && B * Hkv < 65536 &&
+                     B * Hq < 65536;
 
   // 1. append the new token (and convert the query rows for the general router) in a launch of
   //    its own when the step completes a block (its summary needs the token in the cache) or the
@@ -1332,11 +1391,16 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
     f.kv_num = kv_num;
     f.kv_idx = kv_idx;
     const dim3 g1((unsigned)nchunk, (unsigned)(B * Hkv)), g2((unsigned)f.ngroups, (unsigned)(B * Hq));
+#define SSA_FUSED_ROUTE(DT, NW)                                                                   \
+  do {                                                                                            \
+    if (d == 32) decode_route_kernel<DT, 8, NW><<<g1, NW * 64, 0, st>>>(f);                       \
+    else if (d == 64) decode_route_kernel<DT, 16, NW><<<g1, NW * 64, 0, st>>>(f);                 \
+    else decode_route_kernel<DT, 32, NW><<<g1, NW * 64, 0, st>>>(f);                              \
+  } while (0)
 #define SSA_FUSED_STEP(DT)                                                                        \
   do {                                                                                            \
-    if (d == 32) decode_route_kernel<DT, 8><<<g1, 1024, 0, st>>>(f);                              \
-    else if (d == 64) decode_route_kernel<DT, 16><<<g1, 1024, 0, st>>>(f);                        \
-    else decode_route_kernel<DT, 32><<<g1, 1024, 0, st>>>(f);                                     \
+    if (chunk == kDChunk) SSA_FUSED_ROUTE(DT, 16);                                                \
+    else SSA_FUSED_ROUTE(DT, 8);                                                                  \
     decode_attend_fused_kernel<DT><<<g2, 256, 0, st>>>(f, p);                                     \
   } while (0)
     switch (dtype) {
@@ -1345,6 +1409,7 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
       default: SSA_FUSED_STEP(SSA_BF16); break;
     }
 #undef SSA_FUSED_STEP
+#undef SSA_FUSED_ROUTE
     return launch_status("decode_attend_fused_kernel");
   }
 

@@ -812,6 +812,47 @@ def test_prefill_other_head_dims_match_oracle(cuda, d, dtype):
     assert np.abs(np_of(out).transpose(0, 2, 1, 3) - ref).max() < TOL[dtype]
 
 
+@pytest.mark.parametrize("case", ["all_equal", "top_ties", "random"])
+def test_fused_decode_step_ties_match_oracle(cuda, case):
+    """The fused two-launch decode step on exact score ties (identical key blocks have identical
+    summaries, so identical scores for any query): the lowest block indices win, as in the
+    oracle. all_equal: every complete block holds one pattern -- every chunk keeps K equal keys
+    and the row's survivors exceed what one wave holds (the workgroup-wide search runs);
+    top_ties: 100 identical copies of a block aligned with the key head's queries among random
+    blocks (ties straddle the K-th key); random: no ties. 3000 candidate blocks of 16 keys (24
+    route chunks), top_c 64 + local 1. Selections bit-exact against the oracle; outputs within
+    2e-2 of the oracle's decode_attend."""
+    rng = np.random.default_rng(43)
+    hq, hkv, d, block, nblk, top_c = 4, 2, 64, 16, 3000, 64
+    G_ = hq // hkv
+    n0 = nblk * block + 5  # the step's position: 3000 complete blocks before it
+    k = rng.standard_normal((1, hkv, n0 + 1, d)).astype(np.float32)
+    v = rng.standard_normal((1, hkv, n0 + 1, d)).astype(np.float32)
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    if case == "all_equal":
+        pat = rng.standard_normal((hkv, block, d)).astype(np.float32)
+        k[0, :, :nblk * block] = np.tile(pat, (1, nblk, 1))
+    elif case == "top_ties":
+        for kvh in range(hkv):
+            qd_ = q[0, kvh * G_:(kvh + 1) * G_].sum(0)
+            pat = 2.5 * qd_ / np.linalg.norm(qd_) + 0.3 * rng.standard_normal((block, d))
+            for c in rng.choice(nblk, 100, replace=False):
+                k[0, kvh, c * block:(c + 1) * block] = pat
+    k, v, q = (WL.round_to(x, torch.bfloat16) for x in (k, v, q))
+    dec = D.RoutedDecoder(1, hq, hkv, d, n0 + 1, block=block, top_c=top_c, local=1,
+                          dtype=torch.bfloat16, device=cuda)
+    dec.prefill(dev(k[:, :, :n0], torch.bfloat16, cuda), dev(v[:, :, :n0], torch.bfloat16, cuda))
+    out = dec.step(dev(q, torch.bfloat16, cuda), dev(k[:, :, n0], torch.bfloat16, cuda),
+                   dev(v[:, :, n0], torch.bfloat16, cuda))
+    kn, ki = dec.kv_num.cpu().numpy(), dec.kv_idx.cpu().numpy()
+    onum, oidx = O.route_query(q[:, :, None], k, block, n0, top_c=top_c, local=1, kv_len=n0 + 1)
+    for h in range(hq):
+        sel = ki[0, h, :kn[0, h]].tolist()
+        assert sel == oidx[0, h, 0, :onum[0, h, 0]].tolist(), (case, h)
+        ref = O.decode_attend(q[0, h], k[0, h // G_], v[0, h // G_], sel, n0, block)
+        assert np.abs(np_of(out[0, h]) - ref).max() < 2e-2, (case, h)
+
+
 def test_attention_and_decoder_reject_mismatched_arguments(cuda):
     """A V^T of another length or dtype, and decode inputs of the wrong dtype or shape, raise
     instead of being read as the cache's layout."""
