@@ -200,14 +200,15 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
  * the keys j <= t, j < n, of the blocks kv_idx[b,h,i,:kv_num[b,h,i]] with
  * softmax(scale * q.k) in fp32; out has q's dtype. strides[12] = q(b,h,n), k(b,h,n), v(b,h,n),
  * out(b,h,n) in elements. lse (B, Hq, n) fp32 natural-log sum-exp, may be NULL.
- * dtype: SSA_BF16 / SSA_F16 (MFMA, d = 64) or SSA_F32 (d = 64). block: 64 or a multiple of 128.
+ * dtype: SSA_BF16 / SSA_F16 (MFMA, d = 64, 128 or 256) or SSA_F32 (d = 64). block: 64 or a
+ * multiple of 128.
  * The 16-bit paths read V transposed, (B, Hkv, d, n_pad) with n_pad = ceil(n/block)*block, from
  * the workspace (ssa_sparse_attn_workspace_size() bytes). flags = 0: the call first writes V^T
  * there itself; flags = SSA_ATTN_VT_READY: the workspace already holds V^T of this v (from
  * ssa_transpose_v), e.g. kept resident across calls. After V^T the workspace holds per-call state
- * (the largest squared key norm of every 64-key tile, one flag per (b, kv head)), rewritten by
- * every call, so
- * calls sharing one workspace must not overlap. The fp32 path needs no workspace.
+ * (d = 64: the largest squared key norm of every 64-key tile, one flag per (b, kv head)),
+ * rewritten by every call, so calls sharing one workspace must not overlap. The fp32 path needs
+ * no workspace.
  */
 enum { SSA_ATTN_VT_READY = 1 };
 size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,

@@ -60,7 +60,9 @@ def build(verbose: bool = False) -> Path:
             shutil.rmtree(objdir, ignore_errors=True)
             raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{msg}")
     tmp = LIB.with_name(LIB.name + f".tmp{os.getpid()}")
-    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # --no-undefined: a kernel whose host stub the compiler did not emit fails here, not at load
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined",
+            *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(link, capture_output=True, text=True)
     shutil.rmtree(objdir, ignore_errors=True)
     if res.returncode != 0:

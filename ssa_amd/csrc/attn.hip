@@ -208,19 +208,23 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(KeyNorm kn, int64_t H
   key_tile_norm_max(kn, bk / Hkv, bk % Hkv, Hkv, (int64_t)blockIdx.x * 64, n);
 }
 
-// V (B, Hkv, n, 64) -> V^T (B, Hkv, 64, n_pad), zero for keys >= n; with kn.k set, also the
-// key-norm bound of the same 64 rows. grid (n_pad/64, B*Hkv).
+// V (B, Hkv, n, d) -> V^T (B, Hkv, d, n_pad), zero for keys >= n, in 64 x 64 tiles (head dims
+// 64 z .. 64 z + 63 of keys 64 x ..); with kn.k set (head dim 64), also the key-norm bound of the
+// same 64 rows. grid (n_pad/64, B*Hkv, d/64).
 __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict__ v,
                                                           char* __restrict__ vt, int64_t Hkv,
                                                           int64_t n, int64_t n_pad, int64_t vsb,
-                                                          int64_t vsh, int64_t vsn, KeyNorm kn) {
+                                                          int64_t vsh, int64_t vsn, int64_t d,
+                                                          KeyNorm kn) {
   __shared__ unsigned short t[64][64 + 2];
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / Hkv, kvh = bk % Hkv;
   const int64_t k0 = (int64_t)blockIdx.x * 64;
+  const int64_t z = blockIdx.z;
   const int tid = threadIdx.x;
   if (kn.k != nullptr) key_tile_norm_max(kn, b, kvh, Hkv, k0, n);
-  const unsigned short* src = reinterpret_cast<const unsigned short*>(v) + b * vsb + kvh * vsh;
+  const unsigned short* src =
+      reinterpret_cast<const unsigned short*>(v) + b * vsb + kvh * vsh + z * 64;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int q = tid + 256 * j;
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict
     }
   }
   __syncthreads();
-  unsigned short* dst = reinterpret_cast<unsigned short*>(vt) + bk * 64 * n_pad;
+  unsigned short* dst = reinterpret_cast<unsigned short*>(vt) + (bk * d + z * 64) * n_pad;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int q = tid + 256 * j;
@@ -360,25 +364,42 @@ __global__ __launch_bounds__(64) void sparse_attn_f32_kernel(AttnParams p) {
   }
 }
 
-// 16-byte chunk c of LDS tile row r is stored at chunk c ^ swz(r): the 16 lanes served together
-// by one ds_read_b128 of an MFMA operand (16 distinct rows) then hit all 64 banks once.
-__device__ inline int swz(int r) { return (r >> 1) & 7; }
+// 16-byte chunk c of an LDS tile row r of RB bytes is stored at chunk c ^ swz<RB>(r): the 16
+// lanes served together by one ds_read_b128 of an MFMA operand (16 distinct rows r0..r0+15, the
+// same logical chunk) then hit all 64 banks once -- their addresses are distinct mod 256 bytes:
+// RB = 128 (two rows per 256 bytes): row parity x chunk ^ ((r >> 1) & 7); RB = 64: r & 3 x
+// chunk ^ ((r >> 2) & 3); RB >= 256 (rows a multiple of 256 bytes): chunk ^ (r & 15).
+template <int RB>
+__device__ inline int swz(int r) {
+  if constexpr (RB == 64) return (r >> 2) & 3;
+  else if constexpr (RB == 128) return (r >> 1) & 7;
+  else return r & 15;
+}
 
 // A wave owns CG groups of 32 query rows (every LDS operand fragment feeds CG MFMAs); a workgroup
 // of NW waves owns ROWS = 32*CG*NW rows of one query block and walks its selected key blocks in
-// 64-key sub-tiles. K and V^T sub-tiles (64 rows x 128 B each, swizzled) go HBM -> LDS directly
-// (global_load_lds_dwordx4, no staging registers) into a 2-stage ring, one barrier per sub-tile.
+// KT-key sub-tiles (KT = 64, or 32 for head dim 256). K sub-tiles (KT rows of D elements) and V^T
+// sub-tiles (D rows of KT keys), swizzled, go HBM -> LDS directly (global_load_lds_dwordx4, no
+// staging registers) into a 2-stage ring, one barrier per sub-tile.
 // MODE 0: every workgroup, exact online softmax. MODE 1: only workgroups whose rows are all
 // bounded (P = 2^S without a running max). MODE 2: only the others, exact. Modes 1 and 2 are
-// launched back to back and together cover every workgroup.
-template <int DT, int NW, int CG, int WPE, int MODE>
+// launched back to back and together cover every workgroup (head dim 64 only).
+template <int DT, int NW, int CG, int WPE, int MODE, int D = 64, int KT = 64>
 __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
-  constexpr int KT = 64;
-  constexpr int TILE = KT * 128;      // bytes of one K or V^T sub-tile
+  static_assert(D % 64 == 0 && (KT == 32 || KT == 64), "head dim a multiple of 64, KT 32 or 64");
+  static_assert(MODE == 0 || D == 64, "the bounded-row path is built for head dim 64");
+  constexpr int TILE = KT * D * 2;    // bytes of one K or V^T sub-tile
+  constexpr int KRB = D * 2;          // bytes of a K tile row (one key)
+  constexpr int VRB = KT * 2;         // bytes of a V^T tile row (one head dim)
+  constexpr int KD = D / 16;          // 16-element k-steps of the QK product
+  constexpr int DTN = D / 32;         // 32-row output tiles of the PV product
+  constexpr int TT = KT / 32;         // 32-key groups of a sub-tile
+  constexpr int SS = KT / 16;         // 16-key steps of the PV product
   constexpr int ROWS = 32 * CG * NW;  // query rows per workgroup
-  constexpr int LPW = 8 / NW;         // 1 KB load instructions per wave per operand per sub-tile
+  constexpr int LPW = TILE / 1024 / NW;  // 1 KB load instructions per wave per operand per sub-tile
+  static_assert(LPW >= 1 && TILE % (1024 * NW) == 0, "sub-tile loads must split over the waves");
   __shared__ __attribute__((aligned(1024))) unsigned char kst0[TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char vst0[TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char kst1[TILE];
@@ -420,13 +441,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   const int S = (int)(p.block / KT);
 
   // Q fragments (B operands of S^T = K Q^T) of the column groups
-  vec qf[CG][4];
+  vec qf[CG][KD];
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
     const unsigned short* src = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
                                 h * p.qsh + qpos[c] * p.qsn + half * 8;
 #pragma unroll
-    for (int kd = 0; kd < 4; ++kd) {
+    for (int kd = 0; kd < KD; ++kd) {
       u32x4 wv = {0u, 0u, 0u, 0u};
       if (qpos[c] < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
       qf[c][kd] = M::from_bits(wv);
@@ -460,7 +481,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     for (int c = 0; c < CG; ++c) {
       float qn2 = 0.0f;
 #pragma unroll
-      for (int kd = 0; kd < 4; ++kd)
+      for (int kd = 0; kd < KD; ++kd)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float x = (float)qf[c][kd][j];
@@ -483,7 +504,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 #pragma unroll
       for (int c = 0; c < CG; ++c)
 #pragma unroll
-        for (int kd = 0; kd < 4; ++kd) {
+        for (int kd = 0; kd < KD; ++kd) {
           float x[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) x[j] = (float)qf[c][kd][j] * p.scale_log2;
@@ -495,15 +516,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   const unsigned short* kbase =
       reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
   const unsigned short* vtbase =
-      reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * 64 * p.n_pad;
+      reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * D * p.n_pad;
 
-  // Load plan: instruction j of wave w fills tile rows j*8*NW + w*8 + [0,8) (1 KB, LDS offset
-  // j*1024*NW + w*1024); lane -> row lr (+ j*8*NW), physical chunk lane%8 = logical lc ^ swz(row).
-  const int lr = w * 8 + (lane >> 3);
-  const int lc = (lane & 7) ^ swz(lr);
-  const uint32_t kgo = (uint32_t)(lr * p.ksn + lc * 8);
-  const uint32_t vgo = (uint32_t)(lr * p.n_pad + lc * 8);
-  const int64_t kstep = 8 * NW * p.ksn, vstep = 8 * NW * p.n_pad;
+  // Load plan: instruction j of wave w fills 1 KB of the tile at LDS offset j*1024*NW + w*1024:
+  // K rows j*KR*NW + w*KR + [0, KR) (KR = 1024 / KRB keys), V^T rows j*VR*NW + w*VR + [0, VR)
+  // (VR = 1024 / VRB head dims); lane -> row lr (+ j*KR*NW), physical chunk = lane % chunks per
+  // row, loading logical chunk physical ^ swz(row) (the swizzles repeat every 16 rows, so the
+  // chunk of instruction j depends on j only when it advances by a row count not a multiple of
+  // 16: K rows at head dim 256).
+  constexpr int KR = 1024 / KRB, VR = 1024 / VRB, KC = KRB / 16, VC = VRB / 16;
+  const int lr = w * KR + lane / KC;
+  const int vr = w * VR + lane / VC;
+  static_assert((VR * NW) % 16 == 0, "V^T rows per load instruction keep the swizzle");
+  const int vc = (lane % VC) ^ swz<VRB>(vr);
+  const uint32_t vgo = (uint32_t)(vr * p.n_pad + vc * 8);
+  const int64_t kstep = KR * NW * p.ksn, vstep = VR * NW * p.n_pad;
 
   // Tile cursor over the row's block list: entry ce, sub-tile cs (key0 = list[ce]*block + cs*KT).
   // The list is held 64 entries at a time in one VGPR (entry lbase + j in lane j), read with
@@ -538,15 +565,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     const unsigned short* vt = vtbase + key0;
     if (key0 + KT <= n32) {
 #pragma unroll
-      for (int j = 0; j < LPW; ++j)
-        __builtin_amdgcn_global_load_lds(kt + j * kstep + kgo, kdst + j * 1024 * NW + w * 1024,
-                                         16, 0, 0);
+      for (int j = 0; j < LPW; ++j) {
+        const int lcj = (lane % KC) ^ swz<KRB>(lr + j * KR * NW);
+        __builtin_amdgcn_global_load_lds(kt + j * kstep + (uint32_t)(lr * p.ksn + lcj * 8),
+                                         kdst + j * 1024 * NW + w * 1024, 16, 0, 0);
+      }
     } else {  // ragged tail: rows >= n re-read row n-1 (their scores are masked)
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        int64_t r = key0 + j * 8 * NW + lr;
+        int64_t r = key0 + j * KR * NW + lr;
         if (r > p.n - 1) r = p.n - 1;
-        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lc * 8,
+        const int lcj = (lane % KC) ^ swz<KRB>(lr + j * KR * NW);
+        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lcj * 8,
                                          kdst + j * 1024 * NW + w * 1024, 16, 0, 0);
       }
     }
@@ -557,18 +587,20 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   };
 
   // per-lane LDS read offsets: K row tt*32 + sigma32(col), V^T row dt*32 + col; chunk
-  // (2*step + half) ^ swz(row); tt / dt add 4096 (an immediate).
+  // (2*step + half) ^ swz(row) (the swizzles repeat every 16 rows); tt / dt add 32 rows (an
+  // immediate).
   const int krow = sigma32(col);
-  uint32_t koff[4], voff[4];
+  uint32_t koff[KD], voff[SS];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    koff[s] = (uint32_t)(krow * 128 + (((2 * s + half) ^ swz(krow)) * 16));
-    voff[s] = (uint32_t)(col * 128 + (((2 * s + half) ^ swz(col)) * 16));
-  }
+  for (int s = 0; s < KD; ++s)
+    koff[s] = (uint32_t)(krow * KRB + (((2 * s + half) ^ swz<KRB>(krow)) * 16));
+#pragma unroll
+  for (int s = 0; s < SS; ++s)
+    voff[s] = (uint32_t)(col * VRB + (((2 * s + half) ^ swz<VRB>(col)) * 16));
 
-  f32x16 oacc[2][CG];  // [dt][c]
+  f32x16 oacc[DTN][CG];  // [dt][c]
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
     for (int c = 0; c < CG; ++c)
 #pragma unroll
@@ -583,32 +615,32 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 
   auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0) {
     // ---- S^T = K Q^T ----
-    u32x4 ka[2][4];
+    u32x4 ka[TT][KD];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int kd = 0; kd < 4; ++kd)
-        ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * 4096);
-    f32x16 sacc[2][CG];  // [tt][c]
+      for (int kd = 0; kd < KD; ++kd)
+        ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * (32 * KRB));
+    f32x16 sacc[TT][CG];  // [tt][c]
     if constexpr (!fast) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[tt][c][r] = 0.0f;
 #pragma unroll
-        for (int kd = 0; kd < 4; ++kd)
+        for (int kd = 0; kd < KD; ++kd)
           sacc[tt][c] = M::mma(M::from_bits(ka[tt][kd]), qf[c][kd], sacc[tt][c]);
       }
     if constexpr (!fast) __builtin_amdgcn_s_setprio(0);
     // V^T fragments of the first two key steps, in flight during the softmax
-    u32x4 va[4][2];
+    u32x4 va[SS][DTN];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < (SS < 2 ? SS : 2); ++s)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-        va[s][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s] + dt * 4096);
+      for (int dt = 0; dt < DTN; ++dt)
+        va[s][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s] + dt * (32 * VRB));
     // ---- mask (diagonal / ragged tail sub-tiles only) ----
     if (key0 + KT - 1 > (int)qw0 || key0 + KT > n32) {
 #pragma unroll
@@ -617,7 +649,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         const int lim_n = n32 - 1 - key0;
         const int lim = lim_q < lim_n ? lim_q : lim_n;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = tt * 32 + (r >> 3) * 16 + half * 8 + (r & 7);
@@ -627,11 +659,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     }
     if constexpr (fast) {  // ---- bounded rows: P^T = 2^(S^T), O^T += V^T P^T ----
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s < 2) {
+      for (int s = 0; s < SS; ++s) {
+        if (s + 2 < SS) {
 #pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-            va[s + 2][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s + 2] + dt * 4096);
+          for (int dt = 0; dt < DTN; ++dt)
+            va[(s + 2) % SS][dt] = *reinterpret_cast<const u32x4*>(vs + voff[(s + 2) % SS] + dt * (32 * VRB));
         }
         vec pb[CG];
 #pragma unroll
@@ -644,7 +676,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
           l_part[c] = M::rowsum(pb[c], l_part[c]);
         }
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
+        for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
           for (int c = 0; c < CG; ++c)
             oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
@@ -659,7 +691,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     for (int c = 0; c < CG; ++c) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][c][r]);
       mx = pair_max(mx);
@@ -673,7 +705,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         const float alpha = grew[c] ? __builtin_amdgcn_exp2f(m_run[c] - m_cand[c]) : 1.0f;
         l_part[c] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
+        for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[dt][c][r] *= alpha;
         m_run[c] = grew[c] ? m_cand[c] : m_run[c];
@@ -684,11 +716,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     // ---- P^T (registers) and O^T += V^T P^T ----
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s < 2) {
+    for (int s = 0; s < SS; ++s) {
+      if (s + 2 < SS) {
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-          va[s + 2][dt] = *reinterpret_cast<const u32x4*>(vs + voff[s + 2] + dt * 4096);
+        for (int dt = 0; dt < DTN; ++dt)
+          va[(s + 2) % SS][dt] = *reinterpret_cast<const u32x4*>(vs + voff[(s + 2) % SS] + dt * (32 * VRB));
       }
       vec pb[CG];
 #pragma unroll
@@ -701,7 +733,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         l_part[c] = M::rowsum(pb[c], l_part[c]);
       }
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
         for (int c = 0; c < CG; ++c)
           oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
@@ -738,7 +770,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       unsigned short* op =
           reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos[c] * p.osn;
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
           const int d0 = dt * 32 + rg * 8 + half * 4;
@@ -755,15 +787,22 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 }
 
 template <int DT>
-int launch_mfma(AttnParams& p, hipStream_t stream) {
-  // block 64: 2 waves x 32 rows = one query block; otherwise 2 waves x 64 rows per workgroup
+int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
+  // head dim 64: 2 waves x 32 rows per workgroup for block 64 (one query block), otherwise
+  // 2 waves x 64 rows; head dims 128 / 256 (exact path): 2 or 4 waves x 32 rows
   const bool b64 = p.block == 64;
   p.qsub = b64 ? 1 : p.block / 128;
   p.group = p.G * p.qsub;
   p.total = p.nbq * p.B * p.Hkv * p.G * p.qsub;
   const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
   SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
-  if (p.tmax2 == nullptr) {
+  if (d == 128) {
+    if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0, 128, 64><<<(unsigned)grid, 128, 0, stream>>>(p);
+    else sparse_attn_dma_kernel<DT, 4, 1, 2, 0, 128, 64><<<(unsigned)grid, 256, 0, stream>>>(p);
+  } else if (d == 256) {
+    if (b64) sparse_attn_dma_kernel<DT, 2, 1, 1, 0, 256, 32><<<(unsigned)grid, 128, 0, stream>>>(p);
+    else sparse_attn_dma_kernel<DT, 4, 1, 1, 0, 256, 32><<<(unsigned)grid, 256, 0, stream>>>(p);
+  } else if (p.tmax2 == nullptr) {
     if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
     else sparse_attn_dma_kernel<DT, 2, 2, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
   } else if (b64) {
@@ -798,7 +837,8 @@ extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv,
   SSA_REQUIRE(dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
               "transpose_v: 16-bit dtypes only");
   SSA_REQUIRE(B > 0 && Hkv > 0 && n > 0 && block > 0, SSA_ERR_INVALID, "transpose_v: bad sizes");
-  SSA_REQUIRE(d == 64, SSA_ERR_UNSUPPORTED, "transpose_v: head_dim must be 64");
+  SSA_REQUIRE(d == 64 || d == 128 || d == 256, SSA_ERR_UNSUPPORTED,
+              "transpose_v: head_dim must be 64, 128 or 256");
   SSA_REQUIRE(block % 64 == 0, SSA_ERR_UNSUPPORTED, "transpose_v: block must be a multiple of 64");
   SSA_REQUIRE(aligned16(v) && aligned16(vt) && stride_b % 8 == 0 && stride_h % 8 == 0 &&
                   stride_n % 8 == 0,
@@ -808,11 +848,11 @@ extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv,
   const int64_t n_pad = (n + block - 1) / block * block;
   SSA_REQUIRE(B * Hkv < 65536 && n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "transpose_v: grid too large");
-  dim3 tg((unsigned)(n_pad / 64), (unsigned)(B * Hkv));
+  dim3 tg((unsigned)(n_pad / 64), (unsigned)(B * Hkv), (unsigned)(d / 64));
   KeyNorm none{};
   transpose_v_kernel<<<tg, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const char*>(v), static_cast<char*>(vt), Hkv, n, n_pad, stride_b, stride_h,
-      stride_n, none);
+      stride_n, d, none);
   return launch_status("transpose_v_kernel");
 }
 
@@ -830,7 +870,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && n > 0 && W > 0, SSA_ERR_INVALID,
               "sparse_attn: sizes must be positive");
   SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "sparse_attn: Hq not a multiple of Hkv");
-  SSA_REQUIRE(d == 64, SSA_ERR_UNSUPPORTED, "sparse_attn: head_dim %lld unsupported (64)",
+  SSA_REQUIRE(d == 64 || ((d == 128 || d == 256) && dtype != SSA_F32), SSA_ERR_UNSUPPORTED,
+              "sparse_attn: head_dim %lld unsupported (64; 128 and 256 for 16-bit inputs)",
               (long long)d);
   SSA_REQUIRE(block == 64 || (block > 0 && block % 128 == 0), SSA_ERR_UNSUPPORTED,
               "sparse_attn: block %lld unsupported (64 or a multiple of 128)", (long long)block);
@@ -888,17 +929,29 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
   KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
              unbounded, p.ntile};
+  if (d != 64) {  // exact path only: V^T (unless supplied), no key norms
+    if (!(flags & SSA_ATTN_VT_READY)) {
+      KeyNorm none{};
+      const dim3 tz((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv), (unsigned)(d / 64));
+      transpose_v_kernel<<<tz, 256, 0, st>>>(static_cast<const char*>(v),
+                                             static_cast<char*>(workspace), Hkv, n, p.n_pad,
+                                             p.vsb, p.vsh, p.vsn, d, none);
+      SSA_TRY(launch_status("transpose_v_kernel"));
+    }
+    if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, d, st);
+    return launch_mfma<SSA_F16>(p, d, st);
+  }
   const dim3 tg((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv));
   if (flags & SSA_ATTN_VT_READY) {
     key_norm_max_kernel<<<tg, 256, 0, st>>>(kn, Hkv, n);
     SSA_TRY(launch_status("key_norm_max_kernel"));
   } else {  // V^T and the key norms in one pass
     transpose_v_kernel<<<tg, 256, 0, st>>>(static_cast<const char*>(v), static_cast<char*>(workspace),
-                                           Hkv, n, p.n_pad, p.vsb, p.vsh, p.vsn, kn);
+                                           Hkv, n, p.n_pad, p.vsb, p.vsh, p.vsn, 64, kn);
     SSA_TRY(launch_status("transpose_v_kernel"));
   }
   p.tmax2 = tmax2;
   p.unbounded = unbounded;
-  if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, st);
-  return launch_mfma<SSA_F16>(p, st);
+  if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, 64, st);
+  return launch_mfma<SSA_F16>(p, 64, st);
 }

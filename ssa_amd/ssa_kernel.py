@@ -177,9 +177,9 @@ def expand_selection(kv_num: torch.Tensor, kv_idx: torch.Tensor, nbk: int):
 
 
 def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
-    """V (B, Hkv, n, 64) 16-bit -> the V^T workspace (B, Hkv, 64, ceil(n/block)*block) that the
-    16-bit attention kernels read (keys >= n zero-filled). Pass it to sparse_attention(vt=...)
-    to skip the per-call transpose."""
+    """V (B, Hkv, n, d) 16-bit, d in 64 / 128 / 256 -> the V^T workspace (B, Hkv, d,
+    ceil(n/block)*block) that the 16-bit attention kernels read (keys >= n zero-filled). Pass it
+    to sparse_attention(vt=...) to skip the per-call transpose."""
     _lib.require_device(v)
     v = _aligned(v)
     B, Hkv, n, d = v.shape
@@ -241,10 +241,11 @@ def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
         scale = 1.0 / math.sqrt(d)
     kv_num = kv_num.to(torch.int32).contiguous()
     kv_idx = kv_idx.to(torch.int32).contiguous()
-    if d not in TILED_HEAD_DIMS or not (block == 64 or block % 128 == 0):
+    tiled = TILED_HEAD_DIMS_F32 if q.dtype == torch.float32 else TILED_HEAD_DIMS
+    if d not in tiled or not (block == 64 or block % 128 == 0):
         if return_lse:
             raise NotImplementedError(f"sparse_attention: return_lse needs head_dim in "
-                                      f"{TILED_HEAD_DIMS} and block 64 or a multiple of 128, "
+                                      f"{tiled} and block 64 or a multiple of 128, "
                                       f"got head_dim {d}, block {block}")
         return _sparse_attention_rows(q, k, v, kv_num, kv_idx, block, scale, out)
     lse = torch.empty(B, Hq, n, device=q.device, dtype=torch.float32) if return_lse else None
@@ -270,9 +271,10 @@ def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
     return (out, lse) if return_lse else out
 
 
-# head dims the tiled MFMA prefill kernel serves (with block 64 or a multiple of 128); other
-# head dims and blocks take the per-row kernel
-TILED_HEAD_DIMS = (64,)
+# head dims the tiled prefill kernels serve (with block 64 or a multiple of 128): the MFMA
+# kernel (bf16 / fp16) and the fp32 kernel; other head dims and blocks take the per-row kernel
+TILED_HEAD_DIMS = (64, 128, 256)
+TILED_HEAD_DIMS_F32 = (64,)
 _ROWS_WORKSPACE_LIMIT = 1 << 28
 
 

@@ -812,6 +812,51 @@ def test_prefill_other_head_dims_match_oracle(cuda, d, dtype):
     assert np.abs(np_of(out).transpose(0, 2, 1, 3) - ref).max() < TOL[dtype]
 
 
+def _lse64(q, k, kv_num, kv_idx, block, scale):
+    """Natural-log sum-exp of every query row over its selected keys j <= t, j < n (float64)."""
+    B, Hq, n, d = q.shape
+    G_ = Hq // k.shape[1]
+    out = np.empty((B, Hq, n))
+    for b, h, i in np.ndindex(B, Hq, kv_num.shape[2]):
+        t0, t1 = i * block, min(n, (i + 1) * block)
+        keys = np.concatenate([np.arange(c * block, min(n, (c + 1) * block))
+                               for c in kv_idx[b, h, i, :kv_num[b, h, i]]])
+        s = scale * (q[b, h, t0:t1].astype(np.float64) @ k[b, h // G_, keys].astype(np.float64).T)
+        s = np.where(keys[None, :] <= np.arange(t0, t1)[:, None], s, -np.inf)
+        m = s.max(axis=1, keepdims=True)
+        out[b, h, t0:t1] = (m + np.log(np.exp(s - m).sum(axis=1, keepdims=True)))[:, 0]
+    return out
+
+
+@pytest.mark.parametrize("d,dtype,block", [(128, torch.bfloat16, 128), (128, torch.float16, 64),
+                                           (128, torch.bfloat16, 256), (256, torch.bfloat16, 256),
+                                           (256, torch.float16, 128), (256, torch.bfloat16, 64)])
+def test_tiled_prefill_wide_head_dims_match_oracle(cuda, d, dtype, block):
+    """The tiled MFMA prefill kernel at head dims 128 and 256 (4 waves x 32 query rows per
+    128-row query tile, 2 waves for block 64; 64-key sub-tiles, 32-key at head dim 256; exact
+    running-max softmax): ragged n, GQA 3:1, the oracle router's lists (budget 0.4 + local 1),
+    every query row against the oracle within 2e-2, lse within 2^-8 of the float64 log-sum-exp
+    (the row sum adds each P after rounding it to the 16-bit input type, a relative error of at
+    most 2^-9 per term, so |d lse| <= 2^-9 plus fp32 accumulation), and a caller-supplied V^T
+    (transpose_v) giving the identical output."""
+    rng = np.random.default_rng(35 + d + block)
+    n, hq, hkv = 1500, 6, 2
+    q, k, v = (WL.round_to(rng.standard_normal((1, h_, n, d)).astype(np.float32), dtype)
+               for h_ in (hq, hkv, hkv))
+    kv_num, kv_idx = O.route_budget(q, k, block, budget_frac=0.4, local=1, beta=2.0, n_real=n)
+    qt, kt, vt_ = (dev(x, dtype, cuda) for x in (q, k, v))
+    num_t = torch.from_numpy(kv_num).to(cuda)
+    idx_t = torch.from_numpy(kv_idx).to(cuda)
+    scale = d ** -0.5
+    out, lse = K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, return_lse=True)
+    ref = O.sparse_attention(q, k, v, kv_num, kv_idx, block, scale=scale)
+    assert np.abs(np_of(out) - ref).max() < TOL[dtype]
+    assert np.abs(np_of(lse) - _lse64(q, k, kv_num, kv_idx, block, scale)).max() < 2.0 ** -8
+    vtr = K.transpose_v(vt_, block)
+    out2 = K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, vt=vtr)
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("case", ["all_equal", "top_ties", "random"])
 def test_fused_decode_step_ties_match_oracle(cuda, case):
     """The fused two-launch decode step on exact score ties (identical key blocks have identical
