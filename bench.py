@@ -417,6 +417,9 @@ def main():
         result["dense"] = {
             "sdpa_causal_ms": dense_ms, "own_kernel_full_budget_ms": own_full,
             "speedup_vs_sdpa": dense_ms / ms_step, "attention_speedup_vs_sdpa": dense_ms / parts["attention"],
+            # the same kernel at full budget (every causal block): the routed call's speedup over
+            # dense attention by this build's own kernel, bounded by the FLOP ratio
+            "attention_speedup_vs_own_full_budget": own_full / parts["attention"],
             "sdpa_tflops": dense_flops / (dense_ms / 1e3) / 1e12,
             "own_full_tflops": 4.0 * blk * blk * cfg.d * int(fnum.sum().item()) / (own_full / 1e3) / 1e12,
         }
