@@ -69,6 +69,37 @@ __device__ inline void unpack8(const u32x4& w, float* out, bool is_bf16) {
   }
 }
 
+// The value of lane (lane ^ j) of the wave, for j = 1, 2, 4, 8, 16, 32: DPP quad permutes and
+// row rotations within 16-lane rows, the gfx950 permlane swaps across rows and halves -- VALU
+// operations of a few cycles, where __shfl_xor goes through the LDS unit (ds_bpermute, ~100+
+// cycles of latency per step of a dependent chain). j must be a compile-time constant after
+// unrolling (the switch folds). Lane mapping checked against lane ^ j on the GPU.
+__device__ inline unsigned int lane_xor(unsigned int x, int j) {
+  const int lane = threadIdx.x & 63;
+  switch (j) {
+    case 1: return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+    case 2: return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+    case 4: {
+      const unsigned int up = __builtin_amdgcn_update_dpp(0u, x, 0x12C, 0xf, 0xf, false);  // ror 12
+      const unsigned int dn = __builtin_amdgcn_update_dpp(0u, x, 0x124, 0xf, 0xf, false);  // ror 4
+      return (lane & 4) ? dn : up;
+    }
+    case 8: return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xf, 0xf, false);  // row_ror 8
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      return (lane & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return (lane & 32) ? r[0] : r[1];
+    }
+  }
+}
+__device__ inline float lane_xor(float x, int j) {
+  return __uint_as_float(lane_xor(__float_as_uint(x), j));
+}
+__device__ inline int lane_xor(int x, int j) { return (int)lane_xor((unsigned int)x, j); }
+
 // Order-preserving map of an fp32 score to uint32 (larger score -> larger key). -0 is folded
 // onto +0 so the two compare equal, as they do for torch.topk; NaN maps above +inf (torch.topk
 // treats NaN as the largest value).

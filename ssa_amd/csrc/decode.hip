@@ -101,12 +101,12 @@ __device__ inline void store_elem(char* base, int64_t idx, float x) {
 
 __device__ inline float wave_max(float x) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, lane_xor(x, off));
   return x;
 }
 __device__ inline float wave_sum(float x) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  for (int off = 32; off >= 1; off >>= 1) x += lane_xor(x, off);
   return x;
 }
 
@@ -303,9 +303,9 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       float x = acc[t];
-      x += __shfl_xor(x, 8, 64);
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
+      x += lane_xor(x, 8);
+      x += lane_xor(x, 16);
+      x += lane_xor(x, 32);
       acc[t] = x;
     }
     if (kg == 0 && ch * 8 < d)
@@ -333,9 +333,9 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         float x = acc[t];
-        x += __shfl_xor(x, 8, 64);
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
+        x += lane_xor(x, 8);
+        x += lane_xor(x, 16);
+        x += lane_xor(x, 32);
         acc[t] = x;
       }
       if (kg == 0 && on)
@@ -518,7 +518,7 @@ __device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
   for (int k = 2; k <= 64; k <<= 1)
 #pragma unroll
     for (int j = k >> 1; j >= 1; j >>= 1) {
-      const unsigned int ok = __shfl_xor(key, j, 64), ob = __shfl_xor(blk, j, 64);
+      const unsigned int ok = lane_xor(key, j), ob = lane_xor(blk, j);
       // does the partner rank before this lane's pair?
       const bool before = ok > key || (ok == key && ob < blk);
       const bool lower = (lane & j) == 0, desc = (lane & k) == 0;
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
 __device__ inline unsigned int block_sum_u32(unsigned int x, unsigned int* red) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  for (int off = 32; off >= 1; off >>= 1) x += lane_xor(x, off);
   __syncthreads();
   if (lane == 0) red[wv] = x;
   __syncthreads();

@@ -24,8 +24,8 @@ __device__ inline unsigned int wave_kth_key(const unsigned int (&key)[J], int64_
   if (nz < K) return 0u;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    all &= __shfl_xor(all, off, 64);
-    any |= __shfl_xor(any, off, 64);
+    all &= lane_xor(all, off);
+    any |= lane_xor(any, off);
   }
   const unsigned int diff = all ^ any;  // bits on which nonzero keys differ
   if (diff == 0u) return all;           // one distinct nonzero key
