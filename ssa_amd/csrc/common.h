@@ -99,6 +99,12 @@ __device__ inline float lane_xor(float x, int j) {
   return __uint_as_float(lane_xor(__float_as_uint(x), j));
 }
 __device__ inline int lane_xor(int x, int j) { return (int)lane_xor((unsigned int)x, j); }
+__device__ inline double lane_xor(double x, int j) {
+  const unsigned long long u = __double_as_longlong(x);
+  const unsigned int lo = lane_xor((unsigned int)(u & 0xffffffffu), j);
+  const unsigned int hi = lane_xor((unsigned int)(u >> 32), j);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
 
 // Order-preserving map of an fp32 score to uint32 (larger score -> larger key). -0 is folded
 // onto +0 so the two compare equal, as they do for torch.topk; NaN maps above +inf (torch.topk
