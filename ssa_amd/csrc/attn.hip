@@ -810,10 +810,11 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
     sparse_attn_dma_kernel<DT, 2, 1, 2, 1><<<(unsigned)grid, 128, 0, stream>>>(p);
     sparse_attn_dma_kernel<DT, 2, 1, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
   } else {
-    // bounded rows: 4 waves x 32 rows (one score-fragment set per wave: 160 VGPRs, 3-4 % faster
-    // at C3 than 2 waves x 64 rows, the same at C5); the exact path keeps 2 waves x 64 rows (same
-    // 128-row workgroups, so the two launches partition the same logical items)
-    sparse_attn_dma_kernel<DT, 4, 1, 2, 1><<<(unsigned)grid, 256, 0, stream>>>(p);
+    // bounded rows: 4 waves x 32 rows, 4 waves per SIMD (one score-fragment set per wave in 128
+    // VGPRs: 4-6 % faster at C3 than 2 waves x 64 rows, the same at C5); the exact path keeps 2
+    // waves x 64 rows (1 % faster there; same 128-row workgroups, so the two launches partition
+    // the same logical items)
+    sparse_attn_dma_kernel<DT, 4, 1, 4, 1><<<(unsigned)grid, 256, 0, stream>>>(p);
     sparse_attn_dma_kernel<DT, 2, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
   }
   return launch_status("sparse_attn_dma_kernel");
