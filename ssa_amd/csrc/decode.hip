@@ -651,6 +651,22 @@ __device__ inline unsigned int block_sum_u32(unsigned int x, unsigned int* red) 
   return red[0] + red[1] + red[2] + red[3];
 }
 
+// Bitonic sort of one value per lane across the wave, ascending: lane j ends with the (j+1)-th
+// smallest.
+__device__ inline unsigned int wave_sort_asc(unsigned int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      const unsigned int o = lane_xor(v, j);
+      // the lower lane of an ascending pair keeps the smaller value, and so on
+      const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+      v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+    }
+  return v;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, DecodeParams p) {
   __shared__ unsigned int skey[kDSurv], sidx[kDSurv];
@@ -742,9 +758,9 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
     constexpr int SEG = kDSurv / 4;
     return i < s0 ? i : i < s1 ? SEG + (i - s0) : i < s2 ? 2 * SEG + (i - s1) : 3 * SEG + (i - s2);
   };
-  // one wave (J survivors per lane): K-th key, ties by lowest block, own block + local
-  // predecessors, and the ascending list from the bitmap -- no workgroup barrier until the list
-  // is done
+  // one wave (J survivors per lane): K-th key, ties by lowest block, then the ascending list of
+  // the taken blocks, own block and local predecessors -- no workgroup barrier until the list is
+  // done
   auto one_wave = [&](auto jc) {
     constexpr int J = decltype(jc)::value;
     if (wv == 0) {
@@ -776,36 +792,26 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
         for (int j = 0; j < J; ++j)
           takem |= (key[j] > T || (key[j] == T && tk[j] >= T2) ? 1u : 0u) << j;
       }
+      // The list: the taken blocks below the local range [lo, hi] (at most K <= 64 of them,
+      // distinct) sorted ascending in one register, then the local range (own block and its
+      // predecessors, the largest block indices of the row)
+      int64_t lo = own - f.local;
+      if (lo < 0) lo = 0;
+      const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
+      int at = 0;
 #pragma unroll
-      for (int j = 0; j < J; ++j)
-        if ((takem >> j) & 1u) atomicOr(&sel[blk[j] >> 5], 1u << (blk[j] & 31));
-      {
-        int64_t lo = own - f.local;
-        if (lo < 0) lo = 0;
-        const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
-        for (int64_t c = lo + lane; c <= hi; c += 64) atomicOr(&sel[c >> 5], 1u << (c & 31));
+      for (int j = 0; j < J; ++j) {
+        const bool t = ((takem >> j) & 1u) && (int64_t)blk[j] < lo;
+        const unsigned long long bt = __ballot(t);
+        if (t) hist[at + (int)__popcll(bt & lt)] = blk[j];
+        at += (int)__popcll(bt);
       }
       wave_lds_sync();
-      const int wpl = (nwords + 63) / 64, w0 = lane * wpl;
-      int cnt = 0;
-      for (int w = w0; w < w0 + wpl && w < nwords; ++w) cnt += __popc(sel[w]);
-      int incl = cnt;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int o = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += o;
-      }
-      int at = incl - cnt;
-      for (int w = w0; w < w0 + wpl && w < nwords; ++w) {
-        unsigned int m = sel[w];
-        while (m) {
-          const int bit = __ffs(m) - 1;
-          m &= m - 1;
-          if (at < f.W) list[at] = w * 32 + bit;
-          ++at;
-        }
-      }
-      if (lane == 63) sh_n = (unsigned int)incl;
+      const unsigned int v = wave_sort_asc(lane < at ? hist[lane] : 0xffffffffu);
+      if (lane < at && lane < f.W) list[lane] = (int32_t)v;
+      for (int64_t c = lane; c <= hi - lo; c += 64)
+        if (at + c < f.W) list[at + c] = (int32_t)(lo + c);
+      if (lane == 0) sh_n = (unsigned int)(at + (hi - lo + 1));
     }
     __syncthreads();
   };
