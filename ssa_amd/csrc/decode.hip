@@ -195,18 +195,18 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     }
   }
 
-  // FUSED (one wave of several per CU: registers to spare): the lane's K rows of such a block
-  // (keys lane, lane + 64) are loaded with the V rows, before the query row is staged
-  u32x4 kpre[2][8];
+  // FUSED (one wave of several per CU: registers to spare): the K rows of such a block are
+  // loaded with the V rows and in their layout (lane: chunk ch of key kg + 8t; a load instruction
+  // reads 8 whole 128-byte rows), before the query row is staged
+  u32x4 kpre[kPre];
   if constexpr (FUSED && DT != SSA_F32) {
     if (pre) {
+      const int chc = ch * 8 < d ? ch : d / 8 - 1;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int kk = lane + 64 * t < nk ? lane + 64 * t : nk - 1;
-        const unsigned short* kr = reinterpret_cast<const unsigned short*>(krow(key0 + kk));
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          kpre[t][e] = *reinterpret_cast<const u32x4*>(kr + (e * 8 < d ? e : d / 8 - 1) * 8);
+      for (int t = 0; t < kPre; ++t) {
+        const int kk = kg + 8 * t < nk ? kg + 8 * t : nk - 1;
+        kpre[t] = *reinterpret_cast<const u32x4*>(
+            reinterpret_cast<const unsigned short*>(krow(key0 + kk)) + chc * 8);
       }
     }
   }
@@ -221,29 +221,49 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   lds_sync();
 
   float mloc = -INFINITY;
+  // FUSED 16-bit blocks in the K / V layout above: lane (kg, ch) forms the 8-dim partial dots of
+  // its 16 keys kg + 8t, and three halving exchanges over the 8 lanes of its key group (xor 4, 2,
+  // 1) leave it the full dots of keys kg + 8t for t = 2 ch, 2 ch + 1; their exps go to ps
+  bool done = false;
+  float lsum = 0.0f;
   if constexpr (FUSED && DT != SSA_F32) {
     if (pre) {
+      float qv[8];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int kk = lane + 64 * t;
-        float s = 0.0f;
+      for (int u = 0; u < 8; ++u) qv[u] = ch * 8 < d ? qs[ch * 8 + u] : 0.0f;
+      float sc[kPre];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (e * 8 >= d) break;  // uniform
-          float kv[8];
-          unpack8(kpre[t][e], kv, DT == SSA_BF16);
+      for (int t = 0; t < kPre; ++t) {
+        float kv[8];
+        unpack8(kpre[t], kv, DT == SSA_BF16);
+        float a = 0.0f;
 #pragma unroll
-          for (int u = 0; u < 8; ++u) s = fmaf(qs[e * 8 + u], kv[u], s);
-        }
-        if (kk < nk) {
-          const float sl = s * p.scale_log2;
-          ps[kk] = sl;
-          mloc = fmaxf(mloc, sl);
+        for (int u = 0; u < 8; ++u) a = fmaf(qv[u], kv[u], a);
+        sc[t] = a;
+      }
+#pragma unroll
+      for (int w = 4; w >= 1; w >>= 1) {  // keep half of the values (t bit log2(2w) = ch bit)
+        const bool hi = (ch & w) != 0;
+#pragma unroll
+        for (int i = 0; i < 2 * w; ++i) {
+          const float keep = hi ? sc[i + 2 * w] : sc[i];
+          const float send = hi ? sc[i] : sc[i + 2 * w];
+          sc[i] = keep + lane_xor(send, w);
         }
       }
+      const int kk0 = kg + 16 * ch, kk1 = kk0 + 8;
+      const float s0 = sc[0] * p.scale_log2, s1 = sc[1] * p.scale_log2;
+      mloc = fmaxf(kk0 < nk ? s0 : -INFINITY, kk1 < nk ? s1 : -INFINITY);
+      const float m = wave_max(mloc);
+      const float p0 = kk0 < nk ? exp2f(s0 - m) : 0.0f, p1 = kk1 < nk ? exp2f(s1 - m) : 0.0f;
+      if (kk0 < nk) ps[kk0] = p0;
+      if (kk1 < nk) ps[kk1] = p1;
+      lsum = p0 + p1;
+      mloc = m;
+      done = true;
     }
   }
-  for (int kk = lane; kk < nk && !(FUSED && DT != SSA_F32 && pre); kk += 64) {
+  for (int kk = lane; kk < nk && !done; kk += 64) {
     const char* kr = krow(key0 + kk);
     float s = 0.0f;
     if constexpr (DT == SSA_F32) {
@@ -268,10 +288,10 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     ps[kk] = sl;
     mloc = fmaxf(mloc, sl);
   }
-  const float m = wave_max(mloc);
+  const float m = done ? mloc : wave_max(mloc);
   lds_sync();
-  float lloc = 0.0f;
-  for (int kk = lane; kk < nk; kk += 64) {
+  float lloc = lsum;
+  for (int kk = lane; kk < nk && !done; kk += 64) {
     const float pk = exp2f(ps[kk] - m);
     ps[kk] = pk;
     lloc += pk;
