@@ -126,28 +126,39 @@ __device__ inline void put_part(float* p, float x) {
   else *p = x;
 }
 
-// Partial softmax attention of query row (b, h, r) over key block c: (m, l, o[d]) into part,
-// computed by one wave (qs, ps: that wave's LDS). FUSED: the wave is one of several in its
-// workgroup (wave-local LDS ordering) and stores with put_part<true>.
-template <int DT, bool FUSED = false>
+// Partial softmax attention of query row (b, h, r) over key block c (keys [kofs, kofs + kcnt)
+// of the block; kcnt < 0: the whole block): (m, l, o[d]) into part, computed by one wave (qs,
+// ps: that wave's LDS); a range without keys at or before pos stores the empty partial
+// (m = -inf, l = 0, o = 0). FUSED: the wave is one of several in its workgroup (wave-local LDS
+// ordering) and stores with put_part<true>.
+template <int DT, bool FUSED = false, int KPRE = 16>
 __device__ inline void block_partial(const DecodeParams& p, float* part, float* qs, float* ps,
                                      int64_t b, int64_t h, int64_t kvh, int64_t r, int64_t pos,
-                                     int64_t c) {
+                                     int64_t c, int64_t kofs = 0, int64_t kcnt = -1) {
   const int lane = threadIdx.x & 63;
   auto lds_sync = []() {
     if constexpr (FUSED) wave_lds_sync();
     else __syncthreads();
   };
   const int d = (int)p.d;
-  const int64_t key0 = c * p.block;
-  int64_t key1 = key0 + p.block;
+  const int64_t key0 = c * p.block + kofs;
+  int64_t key1 = c * p.block + p.block;
+  if (kcnt >= 0 && key0 + kcnt < key1) key1 = key0 + kcnt;
   if (key1 > pos + 1) key1 = pos + 1;
   if (key1 > p.cap) key1 = p.cap;
   const int nk = (int)(key1 - key0);
+  if (nk <= 0) {
+    if (lane == 0) {
+      put_part<FUSED>(&part[0], -INFINITY);
+      put_part<FUSED>(&part[1], 0.0f);
+    }
+    for (int e = lane; e < d; e += 64) put_part<FUSED>(&part[2 + e], 0.0f);
+    return;
+  }
   // PV lane layout (16-bit): key group kg = lane / 8, 16-byte chunk ch = lane % 8 of the V row.
-  // Blocks of at most 8 * kPre keys with d <= 64 load their V rows up front, in flight while the
+  // Ranges of at most 8 * kPre keys with d <= 64 load their V rows up front, in flight while the
   // scores are computed.
-  constexpr int kPre = 16;
+  constexpr int kPre = KPRE;
   const int kg = lane >> 3, ch = lane & 7;
   const int64_t voff = b * p.vsb + kvh * p.vsh;
   const int64_t koff = b * p.ksb + kvh * p.ksh;
@@ -221,9 +232,10 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   lds_sync();
 
   float mloc = -INFINITY;
-  // FUSED 16-bit blocks in the K / V layout above: lane (kg, ch) forms the 8-dim partial dots of
-  // its 16 keys kg + 8t, and three halving exchanges over the 8 lanes of its key group (xor 4, 2,
-  // 1) leave it the full dots of keys kg + 8t for t = 2 ch, 2 ch + 1; their exps go to ps
+  // FUSED 16-bit ranges in the K / V layout above: lane (kg, ch) forms the 8-dim partial dots of
+  // its kPre keys kg + 8t, and three halving exchanges over the 8 lanes of its key group (xor 4,
+  // 2, 1) leave it the full dots of keys kg + 8t for t = V ch + i, i < V = kPre / 8; their exps
+  // go to ps
   bool done = false;
   float lsum = 0.0f;
   if constexpr (FUSED && DT != SSA_F32) {
@@ -241,24 +253,31 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
         for (int u = 0; u < 8; ++u) a = fmaf(qv[u], kv[u], a);
         sc[t] = a;
       }
+      constexpr int V = kPre / 8;  // full dots per lane at the end
 #pragma unroll
-      for (int w = 4; w >= 1; w >>= 1) {  // keep half of the values (t bit log2(2w) = ch bit)
+      for (int w = 4; w >= 1; w >>= 1) {  // keep the half of the values whose t bit = ch bit w
         const bool hi = (ch & w) != 0;
 #pragma unroll
-        for (int i = 0; i < 2 * w; ++i) {
-          const float keep = hi ? sc[i + 2 * w] : sc[i];
-          const float send = hi ? sc[i] : sc[i + 2 * w];
+        for (int i = 0; i < V * w; ++i) {
+          const float keep = hi ? sc[i + V * w] : sc[i];
+          const float send = hi ? sc[i] : sc[i + V * w];
           sc[i] = keep + lane_xor(send, w);
         }
       }
-      const int kk0 = kg + 16 * ch, kk1 = kk0 + 8;
-      const float s0 = sc[0] * p.scale_log2, s1 = sc[1] * p.scale_log2;
-      mloc = fmaxf(kk0 < nk ? s0 : -INFINITY, kk1 < nk ? s1 : -INFINITY);
+      float sl[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        sl[i] = sc[i] * p.scale_log2;
+        if (kg + 8 * (V * ch + i) < nk) mloc = fmaxf(mloc, sl[i]);
+      }
       const float m = wave_max(mloc);
-      const float p0 = kk0 < nk ? exp2f(s0 - m) : 0.0f, p1 = kk1 < nk ? exp2f(s1 - m) : 0.0f;
-      if (kk0 < nk) ps[kk0] = p0;
-      if (kk1 < nk) ps[kk1] = p1;
-      lsum = p0 + p1;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int kk = kg + 8 * (V * ch + i);
+        const float pk = kk < nk ? exp2f(sl[i] - m) : 0.0f;
+        if (kk < nk) ps[kk] = pk;
+        lsum += pk;
+      }
       mloc = m;
       done = true;
     }
@@ -495,15 +514,16 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
 //   chunk's K-th key. A chunk's top-K holds every candidate of the chunk that can be in the
 //   row's top-K (one it drops has K candidates of its chunk ranked above it). Workgroup (0, 0)
 //   also clears the arrival counters of the attend launch.
-// decode_attend_fused_kernel: grid (ceil(W / 4), B*Hq), 4 waves. Every workgroup of a row merges
-//   the row's chunk lists: T_lb = the largest chunk K-th key bounds the row's K-th key from
-//   below, so only entries >= T_lb (every member of the top-K) go to LDS; a block-wide bit search
-//   finds the K-th key T, keys > T are taken and ties at T by lowest block index (a tie bitmap
-//   scanned in order), the own block and its `local` predecessors are added, and the list is
-//   compacted ascending. Wave w then attends slot 4*blockIdx.x + w of the list (block_partial)
-//   and stores its partial with agent-scope stores; after each wave's stores have completed, an
-//   agent-scope arrival counter per row picks the row's last workgroup, which reads the partials
-//   with agent-scope loads, combines them, and writes the output row and (kv_num, kv_idx).
+// decode_attend_fused_kernel: grid (ceil(W / 4), B*Hq), 8 waves. Every workgroup of a row merges
+//   the row's chunk lists: T_lb, a lower bound of the row's K-th key from the chunks' sorted
+//   lists, keeps only entries >= T_lb (every member of the top-K) in LDS; one wave finds the
+//   K-th key T, takes keys > T and ties at T by lowest block index, and sorts the taken blocks
+//   below the local range ascending, followed by the own block and its `local` predecessors (a
+//   block-wide radix search and bitmaps above 512 survivors). Waves w and w + 4 then attend the
+//   two halves of slot 4*blockIdx.x + w of the list (block_partial) and store their partials
+//   with agent-scope stores; after each wave's stores have completed, an agent-scope arrival
+//   counter per row picks the row's last workgroup, which reads the partials with agent-scope
+//   loads, combines them, and writes the output row and (kv_num, kv_idx).
 // ---------------------------------------------------------------------------------------------
 constexpr int kDChunk = 256;     // largest chunk of candidate blocks per route workgroup
 constexpr int kDTop = 64;        // largest keep of the fused step
@@ -551,8 +571,9 @@ __device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
     }
 }
 
+// One route workgroup's work: chunk `chunk` of the candidate blocks of key head bk.
 template <int DT, int DQ, int NW>
-__global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
+__device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk_) {
   constexpr int NT = NW * 64, CH = NW * 16;  // threads, candidates per workgroup
   constexpr int NQ = kDMaxRows * kDMaxD / NT;  // query elements staged per thread
   __shared__ double qd[kDMaxRows][kDMaxD + 1];   // q as fp64 (rows padded: conflict-free reads)
@@ -560,13 +581,10 @@ __global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
   __shared__ unsigned int skey[kDMaxRows][CH];
   __shared__ unsigned int sbuf[NW][2][64];       // per wave: a row's kept entries
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t bk = blockIdx.y, b = bk / f.Hkv, kvh = bk % f.Hkv;
-  const int64_t c0 = (int64_t)blockIdx.x * CH;
+  const int64_t bk = bk_, b = bk / f.Hkv, kvh = bk % f.Hkv;
+  const int64_t c0 = chunk * CH;
   const int G = (int)f.G;
   constexpr int d = 4 * DQ;
-  if (blockIdx.x == 0 && blockIdx.y == 0)
-    for (int64_t t = tid; t < f.B * f.Hq; t += NT)
-      __hip_atomic_store(&f.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // the query element of this thread first (row tid / d, dim tid % d; 16 * d <= 2048 elements),
   // then the candidate operands, so that staging the query waits for the query load only
   float qx[NQ];
@@ -654,13 +672,22 @@ __global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
     unsigned int sk = lane < at ? sbuf[wv][0][lane] : 0u, sb = lane < at ? sbuf[wv][1][lane] : 0u;
     wave_lds_sync();
     wave_sort_desc(sk, sb);
-    const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + blockIdx.x;
+    const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + chunk;
     f.ckey[cb * kDTop + lane] = sk;
     f.cidx[cb * kDTop + lane] = sb;
     if (lane == 0) f.ckth[cb] = (unsigned int)at;  // entries kept
   }
 }
 
+template <int DT, int DQ, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
+  if (blockIdx.x == 0 && blockIdx.y == 0)
+    for (int64_t t = threadIdx.x; t < f.B * f.Hq; t += NW * 64)
+      __hip_atomic_store(&f.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  route_chunk<DT, DQ, NW>(f, blockIdx.x, blockIdx.y);
+}
+
+template <int NWA>
 __device__ inline unsigned int block_sum_u32(unsigned int x, unsigned int* red) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
@@ -668,7 +695,10 @@ __device__ inline unsigned int block_sum_u32(unsigned int x, unsigned int* red) 
   __syncthreads();
   if (lane == 0) red[wv] = x;
   __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
+  unsigned int t = 0u;
+#pragma unroll
+  for (int w = 0; w < NWA; ++w) t += red[w];
+  return t;
 }
 
 // Bitonic sort of one value per lane across the wave, ascending: lane j ends with the (j+1)-th
@@ -687,21 +717,25 @@ __device__ inline unsigned int wave_sort_asc(unsigned int v) {
   return v;
 }
 
-template <int DT>
-__global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, DecodeParams p) {
+// One attend workgroup's work (NWA waves): group `group` of the selected slots of query row
+// `row` (b*Hq + h), NWA / HALVES slots, each attended by HALVES waves (a wave per 1/HALVES of
+// the block's keys, each storing a partial of its own).
+template <int DT, int NWA, int HALVES>
+__device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, int64_t row,
+                                    int64_t group) {
+  constexpr int NT = NWA * 64, SPW = NWA / HALVES;
   __shared__ unsigned int skey[kDSurv], sidx[kDSurv];
   __shared__ unsigned int sel[kDBitWords], tie[kDBitWords];
   __shared__ int32_t list[kDMaxW];
-  __shared__ __attribute__((aligned(16))) float qs[4][kDMaxD];
-  __shared__ float ps[4][kDMaxBlock];
-  __shared__ float wgt[kDMaxW];
-  __shared__ unsigned int red[4], rand_[4], hist[256];  // (hist: also reduction scratch)
+  __shared__ __attribute__((aligned(16))) float qs[NWA][kDMaxD];
+  __shared__ float ps[NWA][kDMaxBlock];
+  __shared__ float wgt[kDMaxW * HALVES];
+  __shared__ unsigned int red[NWA], rand_[4], hist[256];  // (hist: also reduction scratch)
   __shared__ unsigned int sh_n, sh_last;
-  __shared__ int wsum[4];
+  __shared__ int wsum[NWA];
   __shared__ unsigned int rth[7][64];  // r-th key of every chunk, r = 1, 2, 4, ..., 64
   __shared__ unsigned int rbound[8];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t row = blockIdx.y;  // b*Hq + h
   const int64_t b = row / f.Hq, h = row % f.Hq, kvh = h / f.G;
   const int64_t pos = f.pos;
   const int64_t own = pos / f.block;
@@ -709,38 +743,38 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   const unsigned long long lt = (1ull << lane) - 1ull;
 
   // ---- merge the row's chunk lists ----
-  // Every entry of the row's chunk lists is loaded at once (kDSurv / 256 per thread; an index
+  // Every entry of the row's chunk lists is loaded at once (kDSurv / NT per thread; an index
   // past the lists reads entry 0 and is dropped): thread (wave w, lane l) holds entry l of chunks
-  // w + 4u, so a chunk's r-th key is lane r-1's value of one register.
+  // w + NWA u, so a chunk's r-th key is lane r-1's value of one register.
   // T_lb, a lower bound of the row's K-th key from the sorted chunk lists: for r = 1, 2, 4, ...,
   // 64, the ceil(K / r)-th largest of the chunks' r-th keys (that many chunks hold r keys at or
   // above it: at least K entries reach it), the largest of these bounds. Real keys are nonzero;
   // key 0 past a chunk's kept entries.
-  for (int w = tid; w < nwords; w += 256) {
+  for (int w = tid; w < nwords; w += NT) {
     sel[w] = 0u;
     tie[w] = 0u;
   }
   if (tid == 0) sh_n = 0u;
   const int64_t K = f.K;
   const int nch = f.nchunk;
-  constexpr int kE = kDSurv / 256;
+  constexpr int kE = kDSurv / NT;
   const int ne = nch * kDTop;
   unsigned int kk[kE], ci[kE];
 #pragma unroll
   for (int u = 0; u < kE; ++u) {
-    const int i = tid + 256 * u;
+    const int i = tid + NT * u;
     kk[u] = f.ckey[row * ne + (i < ne ? i : 0)];
     ci[u] = f.cidx[row * ne + (i < ne ? i : 0)];
   }
-  // the r-th keys to LDS (chunk c = wv + 4u is lane r-1's register u)
+  // the r-th keys to LDS (chunk c = wv + NWA u is lane r-1's register u)
 #pragma unroll
   for (int u = 0; u < kE; ++u) {
-    const int c = wv + 4 * u;  // wave-uniform
+    const int c = wv + NWA * u;  // wave-uniform
     const int lg = __popc(lane + 1) == 1 ? 31 - __clz(lane + 1) : -1;  // lane = r - 1, r = 2^lg
     if (c < 64 && lg >= 0) rth[lg][c] = c < nch ? kk[u] : 0u;
   }
   __syncthreads();
-  for (int lg = wv; lg < 7; lg += 4) {
+  for (int lg = wv; lg < 7; lg += NWA) {
     const unsigned int r = 1u << lg;
     const int64_t m = K > 0 ? (K + r - 1) / r : 0;  // chunks needed
     unsigned int v[1] = {rth[lg][lane]};
@@ -753,17 +787,18 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
 #pragma unroll
   for (int lg = 0; lg < 7; ++lg) tlb = rbound[lg] > tlb ? rbound[lg] : tlb;
   // Survivors (keys >= T_lb, real keys nonzero) go to their wave's own LDS segment
-  // [1024 w, 1024 w + n_w) in ballot order -- no atomics; survivor i of the row is entry
+  // [SEG w, SEG w + n_w) in ballot order -- no atomics; survivor i of the row is entry
   // phys(i) of the concatenated segments.
+  constexpr int SEG = kDSurv / NWA;
   {
     const unsigned int floor_ = tlb > 1u ? tlb : 1u;
     int at = 0;
 #pragma unroll
     for (int u = 0; u < kE; ++u) {
-      const bool take = tid + 256 * u < ne && kk[u] >= floor_;
+      const bool take = tid + NT * u < ne && kk[u] >= floor_;
       const unsigned long long bt = __ballot(take);
       if (take) {
-        const int sl = wv * (kDSurv / 4) + at + (int)__popcll(bt & lt);
+        const int sl = wv * SEG + at + (int)__popcll(bt & lt);
         skey[sl] = kk[u];
         sidx[sl] = ci[u];
       }
@@ -772,11 +807,21 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
     if (lane == 0) wsum[wv] = at;
   }
   __syncthreads();
-  const int s0 = wsum[0], s1 = s0 + wsum[1], s2 = s1 + wsum[2];
-  const int n = s2 + wsum[3];
+  int pre[NWA];  // survivors of the waves before wave w
+  int n = 0;
+#pragma unroll
+  for (int w = 0; w < NWA; ++w) {
+    pre[w] = n;
+    n += wsum[w];
+  }
   auto phys = [&](int i) -> int {  // survivor i -> its LDS entry
-    constexpr int SEG = kDSurv / 4;
-    return i < s0 ? i : i < s1 ? SEG + (i - s0) : i < s2 ? 2 * SEG + (i - s1) : 3 * SEG + (i - s2);
+    int w = 0;
+#pragma unroll
+    for (int v = 1; v < NWA; ++v) w += i >= pre[v] ? 1 : 0;
+    int base = 0;
+#pragma unroll
+    for (int v = 0; v < NWA; ++v) base = v == w ? pre[v] : base;
+    return w * SEG + (i - base);
   };
   // one wave (J survivors per lane): K-th key, ties by lowest block, then the ascending list of
   // the taken blocks, own block and local predecessors -- no workgroup barrier until the list is
@@ -847,9 +892,9 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
     if (K > 0) {
       unsigned int prefix = 0u, pmask = 0u, kk_ = (unsigned int)K;
       for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[tid] = 0u;
+        if (tid < 256) hist[tid] = 0u;
         __syncthreads();
-        for (int i = tid; i < n; i += 256) {
+        for (int i = tid; i < n; i += NT) {
           const unsigned int k = skey[phys(i)];
           if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
         }
@@ -889,7 +934,7 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
       }
       T = prefix;
       unsigned int above = 0u;
-      for (int i = tid; i < n; i += 256) {
+      for (int i = tid; i < n; i += NT) {
         const unsigned int k = skey[phys(i)], c = sidx[phys(i)];
         if (k > T) {
           atomicOr(&sel[c >> 5], 1u << (c & 31));
@@ -898,21 +943,21 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
           atomicOr(&tie[c >> 5], 1u << (c & 31));
         }
       }
-      above = block_sum_u32(above, red);
+      above = block_sum_u32<NWA>(above, red);
       // ties at T: the lowest block indices, in order over the tie bitmap
       const int need = (int)K - (int)above;
-      const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+      const int wpt = (nwords + NT - 1) / NT, w0 = tid * wpt;
       int tc = 0;
       for (int w = w0; w < w0 + wpt && w < nwords; ++w) tc += __popc(tie[w]);
       int tot;
-      int pre = block_exclusive_scan<256>(tc, wsum, &tot);
+      int tpre = block_exclusive_scan<NT>(tc, wsum, &tot);
       for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
         unsigned int m = tie[w];
         while (m) {
           const int bit = __ffs(m) - 1;
           m &= m - 1;
-          if (pre < need) atomicOr(&sel[w], 1u << bit);
-          ++pre;
+          if (tpre < need) atomicOr(&sel[w], 1u << bit);
+          ++tpre;
         }
       }
     }
@@ -922,15 +967,15 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
       int64_t lo = own - f.local;
       if (lo < 0) lo = 0;
       const int64_t hi = own < f.nbk - 1 ? own : f.nbk - 1;
-      for (int64_t c = lo + tid; c <= hi; c += 256) atomicOr(&sel[c >> 5], 1u << (c & 31));
+      for (int64_t c = lo + tid; c <= hi; c += NT) atomicOr(&sel[c >> 5], 1u << (c & 31));
     }
     __syncthreads();
     {
-      const int wpt = (nwords + 255) / 256, w0 = tid * wpt;
+      const int wpt = (nwords + NT - 1) / NT, w0 = tid * wpt;
       int cnt = 0;
       for (int w = w0; w < w0 + wpt && w < nwords; ++w) cnt += __popc(sel[w]);
       int total;
-      int at = block_exclusive_scan<256>(cnt, wsum, &total);
+      int at = block_exclusive_scan<NT>(cnt, wsum, &total);
       for (int w = w0; w < w0 + wpt && w < nwords; ++w) {
         unsigned int m = sel[w];
         while (m) {
@@ -946,16 +991,23 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   }
   const int num = (int)sh_n < f.W ? (int)sh_n : (int)f.W;
 
-  // ---- attend slot 4*blockIdx.x + w ----
-  const int64_t s = (int64_t)blockIdx.x * 4 + wv;
+  // ---- attend slot SPW*group + w % SPW: keys [half kh, half kh + kh) of its block ----
+  const int64_t s = group * SPW + wv % SPW;
+  const int half = wv / SPW;
   const int64_t stride = f.d + 2;
-  float* prow = p.part + row * f.W * stride;
+  float* prow = p.part + row * f.W * HALVES * stride;
   if (s < num) {
-    block_partial<DT, true>(p, prow + s * stride, qs[wv], ps[wv], b, h, kvh, 0, pos, list[s]);
+    if constexpr (HALVES == 1) {
+      block_partial<DT, true>(p, prow + s * stride, qs[wv], ps[wv], b, h, kvh, 0, pos, list[s]);
+    } else {
+      const int64_t kh = (f.block + HALVES - 1) / HALVES;
+      block_partial<DT, true, 16 / HALVES>(p, prow + (s * HALVES + half) * stride, qs[wv],
+                                           ps[wv], b, h, kvh, 0, pos, list[s], half * kh, kh);
+    }
   }
   // folded append: workgroup 0 of the first query head of each key head writes the new token
   // into the caches (every read of that row in this launch comes from k_new / v_new)
-  if (p.fused_append && blockIdx.x == 0 && h % f.G == 0 && wv == 0) {
+  if (p.fused_append && group == 0 && h % f.G == 0 && wv == 0) {
     for (int e = lane; e < f.d; e += 64) {
       store_elem<DT>(const_cast<char*>(p.k), b * p.ksb + kvh * p.ksh + pos * p.ksn + e,
                      load_elem<DT>(p.k_new, b * p.knb + kvh * p.knh + e));
@@ -977,15 +1029,16 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
   if (!sh_last) return;  // uniform
 
   // ---- the row's last workgroup: combine the partials ----
-  // (m_j, l_j) loaded by thread j together with the first batch of partials: partial j = w + 4u
+  // (m_j, l_j) loaded by thread j together with the first batch of partials: partial j = w + NWA u
   // (u < kB) of wave w, lane e owning head dims e, e + 64; loads are unconditional (indices past
   // the partials / head dims read the last one and get weight 0 / are not stored)
-  constexpr int kDE = kDMaxD / 64, kB = 17;
-  const int jc = tid < num ? tid : num - 1;
+  constexpr int kDE = kDMaxD / 64, kB = (68 * HALVES + NWA - 1) / NWA;
+  const int nump = num * HALVES;  // partials of the row
+  const int jc = tid < nump ? tid : nump - 1;
   const float mj0 = __hip_atomic_load(&prow[jc * stride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float lj0 = __hip_atomic_load(&prow[jc * stride + 1], __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
-  const int nb = (num - wv + 3) / 4;  // partials of this wave
+  const int nb = (nump - wv + NWA - 1) / NWA;  // partials of this wave
   float acc[kDE];
 #pragma unroll
   for (int t = 0; t < kDE; ++t) acc[t] = 0.0f;
@@ -994,7 +1047,7 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
     float x[kB][kDE];
 #pragma unroll
     for (int u = 0; u < kB; ++u) {
-      const int jw = wv + 4 * (u0 + u), j = jw < num ? jw : num - 1;  // num >= 1 (own block)
+      const int jw = wv + NWA * (u0 + u), j = jw < nump ? jw : nump - 1;  // nump >= 1 (own block)
 #pragma unroll
       for (int t = 0; t < kDE; ++t) {
         const int e = lane + 64 * t < f.d ? lane + 64 * t : (int)f.d - 1;
@@ -1003,21 +1056,25 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
       }
     }
     if (u0 == 0) {  // the weights, once the first batch is in flight
-      const float mj = tid < num ? mj0 : -INFINITY, lj = tid < num ? lj0 : 0.0f;
+      const float mj = tid < nump ? mj0 : -INFINITY, lj = tid < nump ? lj0 : 0.0f;
       M = wave_max(mj);
       if (lane == 0) ps[0][wv] = M;
       __syncthreads();
-      M = fmaxf(fmaxf(ps[0][0], ps[0][1]), fmaxf(ps[0][2], ps[0][3]));
+      M = ps[0][0];
+#pragma unroll
+      for (int w = 1; w < NWA; ++w) M = fmaxf(M, ps[0][w]);
       const float wj = mj == -INFINITY ? 0.0f : exp2f(mj - M);  // empty partials: weight 0
-      if (tid < num) wgt[tid] = wj;
+      if (tid < nump) wgt[tid] = wj;
       L = wave_sum(lj * wj);
       if (lane == 0) ps[1][wv] = L;
       __syncthreads();
-      L = ps[1][0] + ps[1][1] + ps[1][2] + ps[1][3];
+      L = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NWA; ++w) L += ps[1][w];
     }
 #pragma unroll
     for (int u = 0; u < kB; ++u) {
-      const float w = u0 + u < nb ? wgt[wv + 4 * (u0 + u)] : 0.0f;
+      const float w = u0 + u < nb ? wgt[wv + NWA * (u0 + u)] : 0.0f;
 #pragma unroll
       for (int t = 0; t < kDE; ++t) acc[t] = fmaf(x[u][t], w, acc[t]);
     }
@@ -1027,14 +1084,24 @@ __global__ __launch_bounds__(256) void decode_attend_fused_kernel(FusedStep f, D
     if (lane + 64 * t < f.d) qs[wv][lane + 64 * t] = acc[t];
   __syncthreads();
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  for (int e = tid; e < f.d; e += 256)
-    store_elem<DT>(p.o, b * p.osb + h * p.osh + e, (qs[0][e] + qs[1][e] + qs[2][e] + qs[3][e]) * inv);
+  for (int e = tid; e < f.d; e += NT) {
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWA; ++w) o += qs[w][e];
+    store_elem<DT>(p.o, b * p.osb + h * p.osh + e, o * inv);
+  }
   int32_t* out = f.kv_idx + row * f.W;
-  for (int j = tid; j < f.W; j += 256) out[j] = j < num ? list[j] : 0;
+  for (int j = tid; j < f.W; j += NT) out[j] = j < num ? list[j] : 0;
   if (tid == 0) {
     f.kv_num[row] = num;
     __hip_atomic_store(&f.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// 8 waves: 4 slots, each attended by 2 waves (half of the block's keys each)
+template <int DT>
+__global__ __launch_bounds__(512) void decode_attend_fused_kernel(FusedStep f, DecodeParams p) {
+  attend_group<DT, 8, 2>(f, p, blockIdx.y, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1266,7 +1333,8 @@ extern "C" size_t ssa_decode_step_workspace_size(int64_t B, int64_t Hq, int64_t 
   qf = (qf + 255) / 256 * 256;
   size_t keys = (size_t)B * Hq * nbk * 4u;
   keys = (keys + 255) / 256 * 256;
-  return qf + keys + ssa_decode_attend_workspace_size(B, Hq, 1, W, d);
+  // partials: two per selected block (the one-launch step attends a block with two waves)
+  return qf + keys + ssa_decode_attend_workspace_size(B, Hq, 2, W, d);
 }
 
 namespace {
@@ -1427,7 +1495,7 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   do {                                                                                            \
     if (chunk == kDChunk) SSA_FUSED_ROUTE(DT, 16);                                                \
     else SSA_FUSED_ROUTE(DT, 8);                                                                  \
-    decode_attend_fused_kernel<DT><<<g2, 256, 0, st>>>(f, p);                                     \
+    decode_attend_fused_kernel<DT><<<g2, 512, 0, st>>>(f, p);                                     \
   } while (0)
     switch (dtype) {
       case SSA_F32: SSA_FUSED_STEP(SSA_F32); break;
