@@ -530,7 +530,7 @@ constexpr int kDTop = 64;        // largest keep of the fused step
 constexpr int kDMaxRows = 16;    // query rows per key head (G)
 constexpr int kDMaxD = 128;      // head dim
 constexpr int kDMaxBlock = 512;  // keys per block
-constexpr int kDSurv = 4096;     // merged entries held in LDS (nchunk * K <= kDSurv)
+constexpr int kDSurv = 4608;     // merged entries held in LDS (nchunk * K <= kDSurv)
 constexpr int kDBitWords = 1024; // bitmap words: blocks <= own < 32768
 constexpr int kDMaxW = 128;
 
@@ -647,6 +647,7 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
   const unsigned long long lt = (1ull << lane) - 1ull;
   constexpr int J = CH / 64;
   for (int r = wv; r < G; r += NW) {
+    const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + chunk;
     unsigned int key[J], cm = 0u;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -672,7 +673,6 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
     unsigned int sk = lane < at ? sbuf[wv][0][lane] : 0u, sb = lane < at ? sbuf[wv][1][lane] : 0u;
     wave_lds_sync();
     wave_sort_desc(sk, sb);
-    const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + chunk;
     f.ckey[cb * kDTop + lane] = sk;
     f.cidx[cb * kDTop + lane] = sb;
     if (lane == 0) f.ckth[cb] = (unsigned int)at;  // entries kept
@@ -1326,13 +1326,26 @@ extern "C" int ssa_decode_attend(const void* q, const void* k, const void* v, vo
   return run_attend(dtype, p, static_cast<hipStream_t>(stream));
 }
 
+namespace ssa {
+namespace {
+// The router keys of the general step (B*Hq*nbk u32), large enough to also hold the fused step's
+// counters and chunk lists at 128-candidate chunks (with the query region before it).
+size_t step_key_bytes(int64_t B, int64_t Hq, int64_t nbk) {
+  const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t rows = (size_t)B * (size_t)Hq, nch = (size_t)(nbk + 127) / 128;
+  const size_t keys = r256(rows * (size_t)nbk * 4u);
+  const size_t lists = r256(rows * 4u) + r256(rows * nch * 4u) + 2 * r256(rows * nch * kDTop * 4u);
+  return keys > lists ? keys : lists;
+}
+}  // namespace
+}  // namespace ssa
+
 extern "C" size_t ssa_decode_step_workspace_size(int64_t B, int64_t Hq, int64_t cap, int64_t d,
                                                  int64_t block, int64_t W) {
   const int64_t nbk = block > 0 ? (cap + block - 1) / block : 0;
   size_t qf = (size_t)B * Hq * d * 4u;
   qf = (qf + 255) / 256 * 256;
-  size_t keys = (size_t)B * Hq * nbk * 4u;
-  keys = (keys + 255) / 256 * 256;
+  const size_t keys = ssa::step_key_bytes(B, Hq, nbk);
   // partials: two per selected block (the one-launch step attends a block with two waves)
   return qf + keys + ssa_decode_attend_workspace_size(B, Hq, 2, W, d);
 }
@@ -1362,7 +1375,7 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   const int es = dtype_size(dtype);
   char* ws = static_cast<char*>(workspace);
   const size_t qf_bytes = ((size_t)B * Hq * d * 4u + 255) / 256 * 256;
-  const size_t key_bytes = ((size_t)B * Hq * nbk * 4u + 255) / 256 * 256;
+  const size_t key_bytes = step_key_bytes(B, Hq, nbk);
   float* qf = reinterpret_cast<float*>(ws);
   void* keys = ws + qf_bytes;
   float* part = reinterpret_cast<float*>(ws + qf_bytes + key_bytes);
