@@ -130,8 +130,8 @@ __device__ inline void put_part(float* p, float x) {
 // of the block; kcnt < 0: the whole block): (m, l, o[d]) into part, computed by one wave (qs,
 // ps: that wave's LDS); a range without keys at or before pos stores the empty partial
 // (m = -inf, l = 0, o = 0). FUSED: the wave is one of several in its workgroup (wave-local LDS
-// ordering) and stores with put_part<true>.
-template <int DT, bool FUSED = false, int KPRE = 16>
+// ordering); COH: the partial is stored with put_part<true> (else plain stores, e.g. into LDS).
+template <int DT, bool FUSED = false, int KPRE = 16, bool COH = FUSED>
 __device__ inline void block_partial(const DecodeParams& p, float* part, float* qs, float* ps,
                                      int64_t b, int64_t h, int64_t kvh, int64_t r, int64_t pos,
                                      int64_t c, int64_t kofs = 0, int64_t kcnt = -1) {
@@ -149,10 +149,10 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
   const int nk = (int)(key1 - key0);
   if (nk <= 0) {
     if (lane == 0) {
-      put_part<FUSED>(&part[0], -INFINITY);
-      put_part<FUSED>(&part[1], 0.0f);
+      put_part<COH>(&part[0], -INFINITY);
+      put_part<COH>(&part[1], 0.0f);
     }
-    for (int e = lane; e < d; e += 64) put_part<FUSED>(&part[2 + e], 0.0f);
+    for (int e = lane; e < d; e += 64) put_part<COH>(&part[2 + e], 0.0f);
     return;
   }
   // PV lane layout (16-bit): key group kg = lane / 8, 16-byte chunk ch = lane % 8 of the V row.
@@ -322,7 +322,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
       float acc = 0.0f;
       for (int kk = 0; kk < nk; ++kk)
         acc = fmaf(ps[kk], load_elem<DT>(vrow(key0 + kk), e), acc);
-      put_part<FUSED>(&part[2 + e], acc);
+      put_part<COH>(&part[2 + e], acc);
     }
   } else if (pre) {  // the prefetched V rows; the 8 key groups summed with shuffles
     float acc[8];
@@ -349,7 +349,7 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
     }
     if (kg == 0 && ch * 8 < d)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) put_part<FUSED>(&part[2 + ch * 8 + t], acc[t]);
+      for (int t = 0; t < 8; ++t) put_part<COH>(&part[2 + ch * 8 + t], acc[t]);
   } else {
     // 8 keys per pass, 16-byte V row loads; the 8 key groups are summed with shuffles.
     for (int e0 = 0; e0 < d; e0 += 64) {
@@ -379,12 +379,12 @@ __device__ inline void block_partial(const DecodeParams& p, float* part, float* 
       }
       if (kg == 0 && on)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) put_part<FUSED>(&part[2 + e0 + ch * 8 + t], acc[t]);
+        for (int t = 0; t < 8; ++t) put_part<COH>(&part[2 + e0 + ch * 8 + t], acc[t]);
     }
   }
   if (lane == 0) {
-    put_part<FUSED>(&part[0], m);
-    put_part<FUSED>(&part[1], l);
+    put_part<COH>(&part[0], m);
+    put_part<COH>(&part[1], l);
   }
 }
 
@@ -729,7 +729,8 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   __shared__ int32_t list[kDMaxW];
   __shared__ __attribute__((aligned(16))) float qs[NWA][kDMaxD];
   __shared__ float ps[NWA][kDMaxBlock];
-  __shared__ float wgt[kDMaxW * HALVES];
+  __shared__ float wgt[kDMaxW];
+  __shared__ float wpart[NWA][kDMaxD + 2];  // the waves' partials, combined into the group's
   __shared__ unsigned int red[NWA], rand_[4], hist[256];  // (hist: also reduction scratch)
   __shared__ unsigned int sh_n, sh_last;
   __shared__ int wsum[NWA];
@@ -992,17 +993,44 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   const int num = (int)sh_n < f.W ? (int)sh_n : (int)f.W;
 
   // ---- attend slot SPW*group + w % SPW: keys [half kh, half kh + kh) of its block ----
+  // Each wave's partial goes to LDS; the group's waves are combined into one partial (partial
+  // `group` of the row), stored with agent-scope stores.
   const int64_t s = group * SPW + wv % SPW;
   const int half = wv / SPW;
   const int64_t stride = f.d + 2;
-  float* prow = p.part + row * f.W * HALVES * stride;
+  float* prow = p.part + row * f.ngroups * stride;
   if (s < num) {
-    if constexpr (HALVES == 1) {
-      block_partial<DT, true>(p, prow + s * stride, qs[wv], ps[wv], b, h, kvh, 0, pos, list[s]);
-    } else {
-      const int64_t kh = (f.block + HALVES - 1) / HALVES;
-      block_partial<DT, true, 16 / HALVES>(p, prow + (s * HALVES + half) * stride, qs[wv],
-                                           ps[wv], b, h, kvh, 0, pos, list[s], half * kh, kh);
+    const int64_t kh = (f.block + HALVES - 1) / HALVES;
+    block_partial<DT, true, 16 / HALVES, false>(p, wpart[wv], qs[wv], ps[wv], b, h, kvh, 0, pos,
+                                                list[s], half * kh, kh);
+  } else {
+    if (lane == 0) {
+      wpart[wv][0] = -INFINITY;
+      wpart[wv][1] = 0.0f;
+    }
+    for (int e = lane; e < f.d; e += 64) wpart[wv][2 + e] = 0.0f;
+  }
+  __syncthreads();
+  {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWA; ++w) M = fmaxf(M, wpart[w][0]);
+    float wt[NWA], L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWA; ++w) {
+      wt[w] = wpart[w][0] == -INFINITY ? 0.0f : exp2f(wpart[w][0] - M);  // empty: weight 0
+      L += wpart[w][1] * wt[w];
+    }
+    float* gp = prow + group * stride;
+    if (tid == 0) {
+      put_part<true>(&gp[0], M);
+      put_part<true>(&gp[1], L);
+    }
+    for (int e = tid; e < f.d; e += NT) {
+      float o = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NWA; ++w) o = fmaf(wpart[w][2 + e], wt[w], o);
+      put_part<true>(&gp[2 + e], o);
     }
   }
   // folded append: workgroup 0 of the first query head of each key head writes the new token
@@ -1032,8 +1060,8 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   // (m_j, l_j) loaded by thread j together with the first batch of partials: partial j = w + NWA u
   // (u < kB) of wave w, lane e owning head dims e, e + 64; loads are unconditional (indices past
   // the partials / head dims read the last one and get weight 0 / are not stored)
-  constexpr int kDE = kDMaxD / 64, kB = (68 * HALVES + NWA - 1) / NWA;
-  const int nump = num * HALVES;  // partials of the row
+  constexpr int kDE = kDMaxD / 64, kB = (kDMaxW / SPW + NWA - 1) / NWA;
+  const int nump = (int)f.ngroups;  // partials of the row (one per group)
   const int jc = tid < nump ? tid : nump - 1;
   const float mj0 = __hip_atomic_load(&prow[jc * stride], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float lj0 = __hip_atomic_load(&prow[jc * stride + 1], __ATOMIC_RELAXED,
