@@ -732,7 +732,7 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   __shared__ float wgt[kDMaxW];
   __shared__ float wpart[NWA][kDMaxD + 2];  // the waves' partials, combined into the group's
   __shared__ unsigned int red[NWA], rand_[4], hist[256];  // (hist: also reduction scratch)
-  __shared__ unsigned int sh_n, sh_last;
+  __shared__ unsigned int sh_n, sh_last, sh_ovf;
   __shared__ int wsum[NWA];
   __shared__ unsigned int rth[7][64];  // r-th key of every chunk, r = 1, 2, 4, ..., 64
   __shared__ unsigned int rbound[8];
@@ -744,59 +744,75 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   const unsigned long long lt = (1ull << lane) - 1ull;
 
   // ---- merge the row's chunk lists ----
-  // Every entry of the row's chunk lists is loaded at once (kDSurv / NT per thread; an index
-  // past the lists reads entry 0 and is dropped): thread (wave w, lane l) holds entry l of chunks
-  // w + NWA u, so a chunk's r-th key is lane r-1's value of one register.
   // T_lb, a lower bound of the row's K-th key from the sorted chunk lists: for r = 1, 2, 4, ...,
-  // 64, the ceil(K / r)-th largest of the chunks' r-th keys (that many chunks hold r keys at or
-  // above it: at least K entries reach it), the largest of these bounds. Real keys are nonzero;
-  // key 0 past a chunk's kept entries.
+  // the ceil(K / r)-th largest of the chunks' r-th keys (that many chunks hold r keys at or above
+  // it: at least K entries reach it), the largest of these bounds. Real keys are nonzero; key 0
+  // past a chunk's kept entries. A first pass loads the first P = 16 entries of every chunk list
+  // (bound from r <= 16): when no chunk's 16th entry reaches that bound, every entry >= T_lb is
+  // among them; otherwise a second pass loads the whole lists (bound from r <= 64). A pass's
+  // thread (wave w, lane l) holds entry l % P of chunk (w + NWA u) 64/P + l / P in register u.
   for (int w = tid; w < nwords; w += NT) {
     sel[w] = 0u;
     tie[w] = 0u;
   }
-  if (tid == 0) sh_n = 0u;
+  if (tid == 0) {
+    sh_n = 0u;
+    sh_ovf = 0u;
+  }
   const int64_t K = f.K;
   const int nch = f.nchunk;
-  constexpr int kE = kDSurv / NT;
   const int ne = nch * kDTop;
-  unsigned int kk[kE], ci[kE];
-#pragma unroll
-  for (int u = 0; u < kE; ++u) {
-    const int i = tid + NT * u;
-    kk[u] = f.ckey[row * ne + (i < ne ? i : 0)];
-    ci[u] = f.cidx[row * ne + (i < ne ? i : 0)];
-  }
-  // the r-th keys to LDS (chunk c = wv + NWA u is lane r-1's register u)
-#pragma unroll
-  for (int u = 0; u < kE; ++u) {
-    const int c = wv + NWA * u;  // wave-uniform
-    const int lg = __popc(lane + 1) == 1 ? 31 - __clz(lane + 1) : -1;  // lane = r - 1, r = 2^lg
-    if (c < 64 && lg >= 0) rth[lg][c] = c < nch ? kk[u] : 0u;
-  }
-  __syncthreads();
-  for (int lg = wv; lg < 7; lg += NWA) {
-    const unsigned int r = 1u << lg;
-    const int64_t m = K > 0 ? (K + r - 1) / r : 0;  // chunks needed
-    unsigned int v[1] = {rth[lg][lane]};
-    unsigned int bnd = 0u;
-    if (m > 0 && m <= 64) bnd = wave_kth_key<1>(v, m);  // 0 when fewer than m chunks hold r keys
-    if (lane == 0) rbound[lg] = bnd;
-  }
-  __syncthreads();
-  unsigned int tlb = 0u;
-#pragma unroll
-  for (int lg = 0; lg < 7; ++lg) tlb = rbound[lg] > tlb ? rbound[lg] : tlb;
-  // Survivors (keys >= T_lb, real keys nonzero) go to their wave's own LDS segment
-  // [SEG w, SEG w + n_w) in ballot order -- no atomics; survivor i of the row is entry
-  // phys(i) of the concatenated segments.
   constexpr int SEG = kDSurv / NWA;
-  {
+  auto merge_pass = [&](auto pc) -> bool {
+    constexpr int P = decltype(pc)::value, CPR = 64 / P;
+    constexpr int KR = (kDSurv / kDTop + NWA * CPR - 1) / (NWA * CPR);
+    constexpr int LG = P == 64 ? 6 : P == 32 ? 5 : P == 16 ? 4 : P == 8 ? 3 : -1;
+    static_assert(LG >= 0, "prefix length");
+    const int pos = lane % P;
+    unsigned int kk[KR], ci[KR];
+#pragma unroll
+    for (int u = 0; u < KR; ++u) {
+      const int c = (wv + NWA * u) * CPR + lane / P;
+      const int64_t i = row * ne + (c < nch ? c * kDTop + pos : 0);
+      kk[u] = f.ckey[i];
+      ci[u] = f.cidx[i];
+      if (c >= nch) kk[u] = 0u;
+    }
+    // the r-th keys to LDS (chunks past the lists: 0)
+    const int lgp = __popc(pos + 1) == 1 ? 31 - __clz(pos + 1) : -1;  // pos = r - 1, r = 2^lgp
+#pragma unroll
+    for (int u = 0; u < KR; ++u) {
+      const int c = (wv + NWA * u) * CPR + lane / P;
+      if (c < 64 && lgp >= 0) rth[lgp][c] = kk[u];
+    }
+    __syncthreads();
+    for (int lg = wv; lg <= LG; lg += NWA) {
+      const unsigned int r = 1u << lg;
+      const int64_t m = K > 0 ? (K + r - 1) / r : 0;  // chunks needed
+      unsigned int v[1] = {rth[lg][lane]};
+      unsigned int bnd = 0u;
+      if (m > 0 && m <= 64) bnd = wave_kth_key<1>(v, m);  // 0 when fewer than m chunks hold r keys
+      if (lane == 0) rbound[lg] = bnd;
+    }
+    __syncthreads();
+    unsigned int tlb = 0u;
+#pragma unroll
+    for (int lg = 0; lg <= LG; ++lg) tlb = rbound[lg] > tlb ? rbound[lg] : tlb;
     const unsigned int floor_ = tlb > 1u ? tlb : 1u;
+    if constexpr (P < kDTop) {  // a chunk whose P-th entry reaches the bound may hold more
+      bool ovf = false;
+#pragma unroll
+      for (int u = 0; u < KR; ++u) ovf = ovf || (pos == P - 1 && kk[u] >= floor_);
+      if (__ballot(ovf) != 0ull && lane == 0) sh_ovf = 1u;
+      __syncthreads();
+      if (sh_ovf) return true;  // uniform
+    }
+    // Survivors (keys >= T_lb) go to their wave's own LDS segment [SEG w, SEG w + n_w) in ballot
+    // order -- no atomics; survivor i of the row is entry phys(i) of the concatenated segments.
     int at = 0;
 #pragma unroll
-    for (int u = 0; u < kE; ++u) {
-      const bool take = tid + NT * u < ne && kk[u] >= floor_;
+    for (int u = 0; u < KR; ++u) {
+      const bool take = kk[u] >= floor_;
       const unsigned long long bt = __ballot(take);
       if (take) {
         const int sl = wv * SEG + at + (int)__popcll(bt & lt);
@@ -806,8 +822,10 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
       at += (int)__popcll(bt);
     }
     if (lane == 0) wsum[wv] = at;
-  }
-  __syncthreads();
+    __syncthreads();
+    return false;
+  };
+  if (merge_pass(std::integral_constant<int, 16>{})) merge_pass(std::integral_constant<int, 64>{});
   int pre[NWA];  // survivors of the waves before wave w
   int n = 0;
 #pragma unroll
