@@ -506,8 +506,8 @@ __global__ __launch_bounds__(64) void decode_partial_kernel(DecodeParams p) {
 // ---------------------------------------------------------------------------------------------
 // Fused decode step: two launches per step.
 // decode_route_kernel<DT, DQ, NW>: grid (ceil(ncand / (16 NW)), B*Hkv), NW waves of 16
-//   candidates. A workgroup scores a chunk of 16 NW candidate blocks (128 or 256: the smaller
-//   chunk spreads the scoring over twice the CUs, when the merge below can hold its lists) of one
+//   candidates. A workgroup scores a chunk of 16 NW candidate blocks (64, 128 or 256: the
+//   smallest whose lists the merge below can hold, spreading the scoring over the most CUs) of one
 //   key head for all G query rows of that head -- exact: fp64 sums over the head
 //   dim from the fp32 operands (q, fl32(q*q) broadcast from LDS), the fp32 score assembled as
 //   route_score_kernel does -- and keeps each row's chunk top-K by (key desc, block asc) with the
@@ -530,7 +530,8 @@ constexpr int kDTop = 64;        // largest keep of the fused step
 constexpr int kDMaxRows = 16;    // query rows per key head (G)
 constexpr int kDMaxD = 128;      // head dim
 constexpr int kDMaxBlock = 512;  // keys per block
-constexpr int kDSurv = 4608;     // merged entries held in LDS (nchunk * K <= kDSurv)
+constexpr int kDSurv = 8192;     // merged entries held in LDS (nchunk * K <= kDSurv)
+constexpr int kDMaxChunks = 128; // chunks whose r-th keys bound the row's K-th key
 constexpr int kDBitWords = 1024; // bitmap words: blocks <= own < 32768
 constexpr int kDMaxW = 128;
 
@@ -734,7 +735,7 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
   __shared__ unsigned int red[NWA], rand_[4], hist[256];  // (hist: also reduction scratch)
   __shared__ unsigned int sh_n, sh_last, sh_ovf;
   __shared__ int wsum[NWA];
-  __shared__ unsigned int rth[7][64];  // r-th key of every chunk, r = 1, 2, 4, ..., 64
+  __shared__ unsigned int rth[7][kDMaxChunks];  // r-th key of every chunk, r = 1, 2, 4, ..., 64
   __shared__ unsigned int rbound[8];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t b = row / f.Hq, h = row % f.Hq, kvh = h / f.G;
@@ -783,15 +784,18 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
 #pragma unroll
     for (int u = 0; u < KR; ++u) {
       const int c = (wv + NWA * u) * CPR + lane / P;
-      if (c < 64 && lgp >= 0) rth[lgp][c] = kk[u];
+      if (c < kDMaxChunks && lgp >= 0) rth[lgp][c] = kk[u];
     }
     __syncthreads();
     for (int lg = wv; lg <= LG; lg += NWA) {
       const unsigned int r = 1u << lg;
       const int64_t m = K > 0 ? (K + r - 1) / r : 0;  // chunks needed
-      unsigned int v[1] = {rth[lg][lane]};
+      unsigned int v[kDMaxChunks / 64];
+#pragma unroll
+      for (int j = 0; j < kDMaxChunks / 64; ++j) v[j] = rth[lg][lane + 64 * j];
       unsigned int bnd = 0u;
-      if (m > 0 && m <= 64) bnd = wave_kth_key<1>(v, m);  // 0 when fewer than m chunks hold r keys
+      if (m > 0 && m <= kDMaxChunks)  // 0 when fewer than m chunks hold r keys
+        bnd = wave_kth_key<kDMaxChunks / 64>(v, m);
       if (lane == 0) rbound[lg] = bnd;
     }
     __syncthreads();
@@ -1375,10 +1379,10 @@ extern "C" int ssa_decode_attend(const void* q, const void* k, const void* v, vo
 namespace ssa {
 namespace {
 // The router keys of the general step (B*Hq*nbk u32), large enough to also hold the fused step's
-// counters and chunk lists at 128-candidate chunks (with the query region before it).
+// counters and chunk lists at 64-candidate chunks (with the query region before it).
 size_t step_key_bytes(int64_t B, int64_t Hq, int64_t nbk) {
   const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t rows = (size_t)B * (size_t)Hq, nch = (size_t)(nbk + 127) / 128;
+  const size_t rows = (size_t)B * (size_t)Hq, nch = (size_t)(nbk + 63) / 64;
   const size_t keys = r256(rows * (size_t)nbk * 4u);
   const size_t lists = r256(rows * 4u) + r256(rows * nch * 4u) + 2 * r256(rows * nch * kDTop * 4u);
   return keys > lists ? keys : lists;
@@ -1451,17 +1455,18 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
   const int64_t own = pos / block;
   const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t rows = (size_t)(B * Hq);
-  // chunks of 128 candidates when the merge can hold their lists, else 256
+  // the smallest chunk (64, 128 or 256 candidates) whose lists the merge can hold: it loads
+  // kDTop entries per chunk (whatever K is) and bounds from at most kDMaxChunks chunks
   auto fused_fits = [&](int64_t chunk, int64_t* nch_out) {
     const int64_t nch = ncand > 0 ? (ncand + chunk - 1) / chunk : 1;
     const size_t fa = r256(rows * 4u), fk = r256(rows * nch * 4u), fl = r256(rows * nch * kDTop * 4u);
     *nch_out = nch;
-    return nch * Kf <= kDSurv && fa + fk + 2 * fl <= qf_bytes + key_bytes && nch < 65536;
+    return nch * kDTop <= kDSurv && nch <= kDMaxChunks && fa + fk + 2 * fl <= qf_bytes + key_bytes;
   };
-  int64_t nchunk = 1, chunk = kDChunk / 2;
+  int64_t nchunk = 1, chunk = kDChunk / 4;
   bool fits = fused_fits(chunk, &nchunk);
-  if (!fits) {
-    chunk = kDChunk;
+  while (!fits && chunk < kDChunk) {
+    chunk *= 2;
     fits = fused_fits(chunk, &nchunk);
   }
   const size_t f_arrive = r256(rows * 4u), f_kth = r256(rows * nchunk * 4u);
@@ -1553,6 +1558,7 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
 #define SSA_FUSED_STEP(DT)                                                                        \
   do {                                                                                            \
     if (chunk == kDChunk) SSA_FUSED_ROUTE(DT, 16);                                                \
+    else if (chunk == kDChunk / 4) SSA_FUSED_ROUTE(DT, 4);                                        \
     else SSA_FUSED_ROUTE(DT, 8);                                                                  \
     decode_attend_fused_kernel<DT><<<g2, 512, 0, st>>>(f, p);                                     \
   } while (0)
