@@ -857,20 +857,23 @@ def test_tiled_prefill_wide_head_dims_match_oracle(cuda, d, dtype, block):
     assert torch.equal(out, out2)
 
 
-@pytest.mark.parametrize("case", ["all_equal", "top_ties", "random"])
-def test_fused_decode_step_ties_match_oracle(cuda, case):
+@pytest.mark.parametrize("case,top_c,nblk", [("all_equal", 64, 3000), ("top_ties", 64, 3000),
+                                             ("random", 64, 3000), ("random", 4, 12000)])
+def test_fused_decode_step_ties_match_oracle(cuda, case, top_c, nblk):
     """The fused two-launch decode step on exact score ties (identical key blocks have identical
     summaries, so identical scores for any query): the lowest block indices win, as in the
-    oracle. all_equal: every complete block holds one pattern -- every chunk keeps K equal keys
-    and the row's survivors exceed what one wave holds (the workgroup-wide search runs);
-    top_ties: 100 identical copies of a block aligned with the key head's queries among random
-    blocks (ties straddle the K-th key); random: no ties. 3000 candidate blocks of 16 keys (24
-    route chunks), top_c 64 + local 1. Selections bit-exact against the oracle; outputs within
-    2e-2 of the oracle's decode_attend."""
+    oracle. all_equal: every complete block holds one pattern -- every chunk keeps K equal keys,
+    the 16-entry prefix pass hands over to the whole lists, and the row's survivors exceed what
+    one wave holds (the workgroup-wide search runs); top_ties: 100 identical copies of a block
+    aligned with the key head's queries among random blocks (ties straddle the K-th key);
+    random: no ties. 3000 candidate blocks of 16 keys (47 route chunks of 64), top_c 64 + local
+    1; and 12000 blocks at top_c 4 (94 chunks of 128: the merge must load every chunk list
+    although K is small). Selections bit-exact against the oracle; outputs within 2e-2 of the
+    oracle's decode_attend."""
     rng = np.random.default_rng(43)
-    hq, hkv, d, block, nblk, top_c = 4, 2, 64, 16, 3000, 64
+    hq, hkv, d, block = 4, 2, 64, 16
     G_ = hq // hkv
-    n0 = nblk * block + 5  # the step's position: 3000 complete blocks before it
+    n0 = nblk * block + 5  # the step's position: nblk complete blocks before it
     k = rng.standard_normal((1, hkv, n0 + 1, d)).astype(np.float32)
     v = rng.standard_normal((1, hkv, n0 + 1, d)).astype(np.float32)
     q = rng.standard_normal((1, hq, d)).astype(np.float32)
