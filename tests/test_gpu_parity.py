@@ -58,9 +58,11 @@ def test_block_summary_matches_oracle(cuda, dtype):
     assert ulp_diff(np_of(qb), O.qmean(x, 128)).max() <= 1
 
 
-@pytest.mark.parametrize("d", [24, 96, 200, 512])
+@pytest.mark.parametrize("d", [24, 96, 128, 200, 512])
 def test_block_summary_other_head_dims(cuda, d):
-    """Head dims whose 8-column groups do not divide the 256 threads (the last threads idle)."""
+    """Head dims other than 64: 128 takes the one-wave-per-block kernel with 4 row groups per
+    wave; the others the workgroup-per-block kernel, whose 8-column groups do not all divide the
+    256 threads (the last threads idle)."""
     rng = np.random.default_rng(8)
     x = WL.round_to(rng.standard_normal((1, 2, 700, d)).astype(np.float32) * 2 - 1, torch.bfloat16)
     xt = dev(x, torch.bfloat16, cuda)
