@@ -1050,6 +1050,48 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
 // the per-j ballots. Approximate keys (ca.on) are certified: candidates above the band are
 // taken, those below are not; when the band holds more candidates than places remain, they are
 // rescored exactly (a wave per candidate) and ranked by (exact key, lowest block).
+// wave_kth_key / wave_select_top over the first J of kSmallJ slots per lane (the slots past them
+// hold no candidate), J the smallest power of two >= jeff: a row with fewer candidates than the
+// kernel's slots searches only the slots that hold them (wave-uniform dispatch).
+template <int J, int kSmallJ>
+__device__ inline unsigned int kth_first(const unsigned int (&key)[kSmallJ], int64_t K) {
+  unsigned int k2[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) k2[j] = key[j];
+  return wave_kth_key<J>(k2, K);
+}
+template <int kSmallJ>
+__device__ inline unsigned int kth_slots(const unsigned int (&key)[kSmallJ], int64_t K, int jeff) {
+  if (kSmallJ >= 2 && jeff <= 1) return kth_first<1>(key, K);
+  if constexpr (kSmallJ >= 4)
+    if (jeff <= 2) return kth_first<2>(key, K);
+  if constexpr (kSmallJ >= 8)
+    if (jeff <= 4) return kth_first<4>(key, K);
+  if constexpr (kSmallJ >= 16)
+    if (jeff <= 8) return kth_first<8>(key, K);
+  return wave_kth_key<kSmallJ>(key, K);
+}
+template <int J, int kSmallJ>
+__device__ inline unsigned int select_first(const unsigned int (&key)[kSmallJ], unsigned int cm,
+                                            int64_t K, int64_t ncand) {
+  unsigned int k2[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) k2[j] = key[j];
+  return wave_select_top<J>(k2, cm, K, ncand);
+}
+template <int kSmallJ>
+__device__ inline unsigned int select_slots(const unsigned int (&key)[kSmallJ], unsigned int cm,
+                                            int64_t K, int64_t ncand, int jeff) {
+  if (kSmallJ >= 2 && jeff <= 1) return select_first<1>(key, cm, K, ncand);
+  if constexpr (kSmallJ >= 4)
+    if (jeff <= 2) return select_first<2>(key, cm, K, ncand);
+  if constexpr (kSmallJ >= 8)
+    if (jeff <= 4) return select_first<4>(key, cm, K, ncand);
+  if constexpr (kSmallJ >= 16)
+    if (jeff <= 8) return select_first<8>(key, cm, K, ncand);
+  return wave_select_top<kSmallJ>(key, cm, K, ncand);
+}
+
 template <int kSmallJ, int QR>
 __global__ __launch_bounds__(256) void route_select_small_kernel(
     const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
@@ -1081,9 +1123,10 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     key[j] = m;
   }
   unsigned int selm;
+  const int jeff = (int)((cmax + 63) / 64);  // slots holding candidates (wave-uniform)
   if (ca.on && K > 0 && K < cmax) {
     float M = cert_emag_max(ca, lrow, cmax * g.pool, lane, 64);
-    const unsigned int T = wave_kth_key<kSmallJ>(key, K);
+    const unsigned int T = kth_slots<kSmallJ>(key, K, jeff);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     unsigned int lo, hi;
@@ -1161,7 +1204,7 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     unsigned int cm = 0u;
 #pragma unroll
     for (int j = 0; j < kSmallJ; ++j) cm |= (lane + 64 * j < cmax ? 1u : 0u) << j;
-    selm = wave_select_top<kSmallJ>(key, cm, K, cmax);
+    selm = select_slots<kSmallJ>(key, cm, K, cmax, jeff);
   }
   const int64_t own = row_own(g, i);
   int64_t lo = own - g.local;
