@@ -106,6 +106,13 @@ __device__ inline double lane_xor(double x, int j) {
   return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 }
 
+// Orders one wave's LDS writes before its later LDS reads (other lanes' data).
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Order-preserving map of an fp32 score to uint32 (larger score -> larger key). -0 is folded
 // onto +0 so the two compare equal, as they do for torch.topk; NaN maps above +inf (torch.topk
 // treats NaN as the largest value).

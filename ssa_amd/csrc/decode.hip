@@ -110,12 +110,6 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// Orders one wave's LDS writes before its later LDS reads (other lanes' data).
-__device__ inline void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Stores of a partial result: plain, or (FUSED) relaxed agent-scope atomic stores, which are
 // performed at the device's coherence point, so a workgroup on another XCD can read them with

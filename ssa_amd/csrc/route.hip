@@ -673,6 +673,41 @@ __device__ inline unsigned int cert_exact_key(const CertArgs& ca, const float (&
   return best;
 }
 
+// Exact score key of candidate c (as cert_exact_key) computed by a group of 16 lanes: lane
+// (lane & 15) sums head dims (lane & 15) + 16 t, the group reduces with lane exchanges; qg holds
+// the query row at those dims. Every lane of the group returns the key.
+template <int QR>
+__device__ inline unsigned int group_exact_key(const CertArgs& ca, const float (&qg)[4 * QR],
+                                               int64_t cbase, int64_t c, int64_t pool) {
+  const int l16 = threadIdx.x & 15;
+  unsigned int best = 0u;
+  for (int64_t s = 0; s < pool; ++s) {
+    const int64_t off = cbase + (c * pool + s) * ca.d;
+    double e1 = 0.0, e2 = 0.0, e3 = 0.0;
+#pragma unroll
+    for (int t = 0; t < 4 * QR; ++t) {
+      const int k = l16 + 16 * t;
+      if (k < ca.d) {
+        const float q = qg[t], q2 = q * q;
+        e1 = fma((double)q, (double)ca.mu[off + k], e1);
+        if (ca.var) e2 = fma((double)q2, (double)ca.var[off + k], e2);
+        if (ca.m3) e3 = fma((double)(q2 * q), (double)ca.m3[off + k], e3);
+      }
+    }
+#pragma unroll
+    for (int w = 1; w < 16; w <<= 1) {
+      e1 += lane_xor(e1, w);
+      e2 += lane_xor(e2, w);
+      if (ca.m3) e3 += lane_xor(e3, w);
+    }
+    float sc = __fadd_rn((float)e1, __fmul_rn(ca.coef2, (float)e2));
+    if (ca.m3) sc = __fadd_rn(sc, __fmul_rn(ca.coef3, (float)e3));
+    const unsigned int k = score_key(sc);
+    best = k > best ? k : best;
+  }
+  return best;
+}
+
 constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
 
 // Top-K of one row of score keys (K = min(keep, cmax)), ties to the lowest block index, then the
@@ -1148,6 +1183,58 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
     const int m = (int)K - nin;
     if (nunc <= m) {  // the band fills the remaining places exactly
       selm |= uncm;
+    } else if (nunc <= 64) {
+      // the band (in block order) to LDS; its exact keys four at a time (a 16-lane group per
+      // candidate); candidate i is taken when fewer than m band candidates rank above it
+      // (larger exact key, or equal key and lower block)
+      __shared__ int band_c[4][64];
+      __shared__ unsigned int band_k[4][64];
+      __shared__ int band_t[4][64];
+      const int wv = threadIdx.x >> 6;
+      int bpos[kSmallJ];
+      int nb = 0;
+#pragma unroll
+      for (int j = 0; j < kSmallJ; ++j) {
+        const bool u = (uncm >> j) & 1u;
+        const unsigned long long bal = __ballot(u);
+        bpos[j] = nb + (int)__popcll(bal & lt);
+        if (u) band_c[wv][bpos[j]] = lane + 64 * j;
+        nb += (int)__popcll(bal);
+      }
+      const int64_t b = bh / g.Hq, h = bh % g.Hq;
+      const int64_t bk = b * g.Hkv + h / g.G;
+      const int64_t cbase = bk * g.nbk * g.pool * ca.d;
+      float qg[4 * QR];
+      {
+        const int64_t roff = ((b * g.Hq + h) * g.nbq + i) * ca.d;
+#pragma unroll
+        for (int t = 0; t < 4 * QR; ++t) {
+          const int k = (lane & 15) + 16 * t;
+          qg[t] = k < ca.d ? load_row(ca.rows, roff + k, g.rows_dt) : 0.0f;
+        }
+      }
+      wave_lds_sync();
+      for (int base = 0; base < nb; base += 4) {  // wave-uniform
+        const int bi = base + (lane >> 4);
+        const int cb = bi < nb ? band_c[wv][bi] : 0;
+        const unsigned int kx = group_exact_key<QR>(ca, qg, cbase, cb, g.pool);
+        if ((lane & 15) == 0 && bi < nb) band_k[wv][bi] = kx;
+      }
+      wave_lds_sync();
+      if (lane < nb) {
+        const unsigned int ki = band_k[wv][lane];
+        const int ci = band_c[wv][lane];
+        int above = 0;
+        for (int jj = 0; jj < nb; ++jj) {
+          const unsigned int kj = band_k[wv][jj];
+          above += (kj > ki || (kj == ki && band_c[wv][jj] < ci)) ? 1 : 0;
+        }
+        band_t[wv][lane] = above < m ? 1 : 0;
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < kSmallJ; ++j)
+        if (((uncm >> j) & 1u) && band_t[wv][bpos[j]]) selm |= 1u << j;
     } else {
       // rescore the band exactly, one candidate at a time in block order (a wave-uniform loop),
       // then take its best m by (exact key, lowest block)
