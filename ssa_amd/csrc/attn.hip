@@ -43,9 +43,9 @@ constexpr float kRescaleSlack = 8.0f;
 // type's range. fp16's largest finite value is 65504 < 2^16 and its smallest normal 2^-14: with
 // |s| < 15, P lies in (2^-15, 2^15), finite, and at worst one bit short of full precision at the
 // bottom. bf16 has fp32's exponent range; its bound is set by precision instead: the bounded path
-// pre-scales q by scale*log2e and rounds it to bf16 (relative error <= 2^-9 per element), which
-// moves a score by at most 2^-9 * |q| |k| scale log2e < 2^-9 * bound = 1/16 log2 unit at 32 (a
-// relative change of P of at most 4.4 %, typically ~0.5 % since the rounding errors of the 64
+// pre-scales q by scale*log2e and rounds it to bf16 (relative error <= 2^-8 per element), which
+// moves a score by at most 2^-8 * |q| |k| scale log2e < 2^-8 * bound = 1/8 log2 unit at 32 (a
+// relative change of P of at most 9 %, typically ~1 % since the rounding errors of the 64
 // elements have random signs) -- the size of the query's own bf16 rounding. Rows beyond the bound
 // take the exact running-max path, whose scores are the fp32 products.
 constexpr float kFastBoundBf16 = 32.0f;

@@ -943,6 +943,11 @@ def test_gemma_decode_equals_prefill_last_row(cuda):
 
 
 def test_gemma_flex_no_future_leak_and_sharing(cuda):
+    """ssa/tests/test_flex_swap.py:78-90 restated (outputs up to `cut` within 2e-2 when later
+    keys/values change), plus bit-equality for the query blocks wholly before cut's block: the
+    rows of cut's own block may take the other softmax path when the later keys of that block
+    change its key-norm bound (outputs equal to rounding). Then cross-layer sharing: the donor's
+    selection object is reused by the consumer layer."""
     torch.manual_seed(0)
     n, cut = 512, 256
     q = torch.randn(1, 2, n, 64, device=cuda, dtype=torch.float16)
@@ -954,7 +959,9 @@ def test_gemma_flex_no_future_leak_and_sharing(cuda):
     k2[:, :, cut + 1:] += 5.0 * torch.randn_like(k2[:, :, cut + 1:])
     v2[:, :, cut + 1:] += 5.0 * torch.randn_like(v2[:, :, cut + 1:])
     o2, _ = G.ssa_attention_forward(_mod(), q, k2, v2, scaling=1 / 8)
-    assert torch.equal(o1[:, :cut + 1], o2[:, :cut + 1])
+    whole = cut // 128 * 128
+    assert torch.equal(o1[:, :whole], o2[:, :whole])
+    assert (o1[:, :cut + 1].float() - o2[:, :cut + 1].float()).abs().max().item() < 2e-2
     # donor layer 0 stashes its selection; consumer layer 1 reuses the same object
     G.CFG = G.SSAConfig(block=128, budget_frac=0.25, impl="flex", share_route_from=0)
     G._SHARE["sig"] = None
