@@ -39,17 +39,19 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.0f;
 // Rows whose scores provably stay within +-fast_bound<DT>() (log2 units) take the softmax without
-// a running max: P = 2^s is packed into the MFMA input type, so the bound must keep P inside that
-// type's range. fp16's largest finite value is 65504 < 2^16 and its smallest normal 2^-14: with
-// |s| < 15, P lies in (2^-15, 2^15), finite, and at worst one bit short of full precision at the
-// bottom. bf16 has fp32's exponent range; its bound is set by precision instead: the bounded path
-// pre-scales q by scale*log2e and rounds it to bf16 (relative error <= 2^-8 per element), which
-// moves a score by at most 2^-8 * |q| |k| scale log2e < 2^-8 * bound = 1/8 log2 unit at 32 (a
-// relative change of P of at most 9 %, typically ~1 % since the rounding errors of the 64
-// elements have random signs) -- the size of the query's own bf16 rounding. Rows beyond the bound
-// take the exact running-max path, whose scores are the fp32 products.
+// a running max. The bound is set by precision: the bounded path pre-scales q by scale*log2e and
+// rounds it to the input type (relative error <= 2^-8 per element for bf16, 2^-11 for fp16),
+// which moves a score by at most that error times |q| |k| scale log2e < bound: 1/8 log2 unit at
+// 32 (bf16) and at 256 (fp16) -- a relative change of P of at most 9 %, typically ~1 % since the
+// rounding errors of the 64 elements have random signs, the size of the query's own rounding.
+// P = 2^s is packed into the MFMA input type. bf16 has fp32's exponent range. fp16's largest
+// finite value is 65504 < 2^16: an fp16 row takes P = 2^(s - m0), m0 the largest score of its
+// first sub-tile (a lower bound of its maximum: the row's largest P is >= 1, so P below 2^-24,
+// flushed to 0, is negligible beside it), which stays finite unless a later score exceeds
+// m0 + 16; a row whose sum l comes out non-finite sends its query block to the exact launch.
+// Rows beyond the bound take the exact running-max path, whose scores are the fp32 products.
 constexpr float kFastBoundBf16 = 32.0f;
-constexpr float kFastBoundF16 = 15.0f;
+constexpr float kFastBoundF16 = 256.0f;
 template <int DT>
 __device__ constexpr float fast_bound() {
   return DT == SSA_F16 ? kFastBoundF16 : kFastBoundBf16;
@@ -75,6 +77,9 @@ struct AttnParams {
   const float* tmax2;  // per-tile maxima of the squared key norms (NULL: exact path only)
   int64_t ntile;       // 64-key tiles per key head (n_pad / 64)
   int* unbounded;      // per (b, kv head): set by mode 1 when one of its workgroups is not bounded
+                       // (or, fp16, overflowed)
+  int* redo;           // per (b, kv head, query block): set by mode 1 (fp16) when a row of a
+                       // workgroup of it overflowed; the exact launch then redoes the query block
   int64_t qsub;   // query sub-tiles per query block
   int64_t total;  // logical workgroups
   int64_t group;  // logical workgroups placed together on one XCD
@@ -157,7 +162,7 @@ struct Mfma<SSA_F16> {
 
 // Key-norm bound of the attention call: the largest squared norm of key rows k0..k0+63 of one
 // key head (rows >= n count 0) into its tile's slot; the first tile's workgroup also clears the
-// head's unbounded flag for the mode-1 launch. 256 threads; lanes 8r..8r+7 of a pass read row
+// head's unbounded flag for the mode-1 launch, and the tile starting a query block its redo flag. 256 threads; lanes 8r..8r+7 of a pass read row
 // r's 8 16-byte chunks.
 struct KeyNorm {
   const unsigned short* k;  // NULL: no key norms
@@ -166,6 +171,8 @@ struct KeyNorm {
   float* tmax2;    // (B*Hkv, ntile)
   int* unbounded;  // (B*Hkv)
   int64_t ntile;
+  int* redo;       // (B*Hkv, nbq): cleared here, one entry per query block (block a multiple of 64)
+  int64_t block, nbq;
 };
 
 __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t kvh,
@@ -199,6 +206,7 @@ __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t k
     const int64_t bk = b * Hkv + kvh;
     kn.tmax2[bk * kn.ntile + k0 / 64] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     if (k0 == 0) kn.unbounded[bk] = 0;
+    if (kn.redo != nullptr && k0 % kn.block == 0) kn.redo[bk * kn.nbq + k0 / kn.block] = 0;
   }
 }
 
@@ -459,6 +467,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   // pre-scaled by scale log2e (rounded to the input type) and the softmax is exp2 of the raw
   // MFMA output; numerator and denominator share the implicit max 0.
   constexpr bool fast = MODE == 1;
+  constexpr bool OFS = fast && DT == SSA_F16;  // fp16 bounded rows: scores offset by m0 (above)
   if constexpr (MODE != 0) {
     __shared__ int wg_bounded;
     // largest squared key norm over the tiles this workgroup attends (its list's blocks, tiles
@@ -496,9 +505,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     if (!__all(ok) && lane == 0) wg_bounded = 0;
     __syncthreads();
     const bool bounded = wg_bounded != 0;
-    if (bounded != fast) {  // the other launch takes this workgroup
-      if (fast && tid == 0) p.unbounded[b * p.Hkv + kvh] = 1;
-      return;
+    if constexpr (fast) {
+      if (!bounded) {  // the exact launch takes this workgroup
+        if (tid == 0) p.unbounded[b * p.Hkv + kvh] = 1;
+        return;
+      }
+    } else if (bounded && (DT != SSA_F16 || p.redo[(b * p.Hkv + kvh) * p.nbq + i] == 0)) {
+      return;  // the bounded launch completed this workgroup
     }
     if constexpr (fast) {
 #pragma unroll
@@ -611,6 +624,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     m_run[c] = fast ? 0.0f : -INFINITY;
     l_part[c] = 0.0f;
   }
+  bool have_m0 = !OFS;  // OFS: m_run holds m0 once the first sub-tile set it
   const float c2 = p.scale_log2;
 
   auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0) {
@@ -628,7 +642,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[tt][c][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) sacc[tt][c][r] = OFS ? -m_run[c] : 0.0f;
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd)
           sacc[tt][c] = M::mma(M::from_bits(ka[tt][kd]), qf[c][kd], sacc[tt][c]);
@@ -658,6 +672,26 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       }
     }
     if constexpr (fast) {  // ---- bounded rows: P^T = 2^(S^T), O^T += V^T P^T ----
+      if constexpr (OFS) {
+        if (!have_m0) {  // first sub-tile: m0 = its largest score per row, subtracted here (the
+                         // later sub-tiles start their accumulators at -m0)
+#pragma unroll
+          for (int c = 0; c < CG; ++c) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][c][r]);
+            mx = pair_max(mx);
+            m_run[c] = mx == -INFINITY ? 0.0f : mx;
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) sacc[tt][c][r] -= m_run[c];
+          }
+          have_m0 = true;
+        }
+      }
 #pragma unroll
       for (int s = 0; s < SS; ++s) {
         if (s + 2 < SS) {
@@ -762,6 +796,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   }
 
   // ---- epilogue: O = O^T / l ----
+  if constexpr (OFS) {  // a row whose P overflowed fp16: its query block goes to the exact launch
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const float lt = pair_sum(l_part[c]);  // (every lane: a cross-lane sum)
+      if (qpos[c] < p.n && !(lt < INFINITY)) bad = true;
+    }
+    if (__any(bad) && lane == 0) {
+      p.redo[(b * p.Hkv + kvh) * p.nbq + i] = 1;
+      p.unbounded[b * p.Hkv + kvh] = 1;
+    }
+  }
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
     const float l_tot = pair_sum(l_part[c]);
@@ -828,9 +874,9 @@ extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t H
   if (dtype == SSA_F32 || block <= 0) return 0;
   const int64_t n_pad = (n + block - 1) / block * block;
   const size_t vt = ((size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u + 255) / 256 * 256;
-  // V^T, then the per-tile key-norm maxima (float) and one unbounded-workgroup flag (int) per
-  // key head
-  const size_t tail = (size_t)(B * Hkv * (n_pad / 64) + B * Hkv) * 4u;
+  // V^T, then the per-tile key-norm maxima (float), one unbounded-workgroup flag (int) per key
+  // head and one redo flag (int) per (key head, query block)
+  const size_t tail = (size_t)(B * Hkv * (n_pad / 64) + B * Hkv + B * Hkv * (n_pad / block)) * 4u;
   return vt + (tail + 255) / 256 * 256;
 }
 
@@ -911,6 +957,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   p.tmax2 = nullptr;
+  p.unbounded = nullptr;
+  p.redo = nullptr;
   p.ntile = p.n_pad / 64;
   if (dtype == SSA_F32) {
     p.vt = nullptr;
@@ -932,8 +980,9 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   const size_t vt_bytes = ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
   float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
   int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
+  int* redo = unbounded + B * Hkv;
   KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
-             unbounded, p.ntile};
+             unbounded, p.ntile, redo, block, p.nbq};
   if (d != 64) {  // exact path only: V^T (unless supplied), no key norms
     if (!(flags & SSA_ATTN_VT_READY)) {
       KeyNorm none{};
@@ -957,6 +1006,7 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   }
   p.tmax2 = tmax2;
   p.unbounded = unbounded;
+  p.redo = redo;
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, 64, st);
   return launch_mfma<SSA_F16>(p, 64, st);
 }
