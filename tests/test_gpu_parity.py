@@ -427,6 +427,49 @@ def test_rows_near_the_fast_path_bound(cuda, dtype, target, aligned):
     assert np.abs(np_of(out) - ref).max() < TOL[dtype]
 
 
+@pytest.mark.parametrize("block", [64, 128])
+def test_fp16_bounded_rows_overflow_redone_exactly(cuda, block):
+    """fp16 bounded rows take P = 2^(S - m0) with m0 the largest score of the row's first
+    sub-tile. Here every query leans on one direction u and a needle key along u sits in key
+    block 5, while the other keys are random: the rows' first sub-tiles (earlier blocks) score
+    far below the needle (about |q| |k|/8 against |q| |k|), so the needle's P overflows fp16 and
+    the query blocks that attend block 5 must be redone by the exact launch. Every row within
+    2e-2 of the float64 oracle, the output finite."""
+    rng = np.random.default_rng(41)
+    n, scale = 1024, 0.125
+    u = rng.standard_normal(64).astype(np.float32)
+    u /= np.linalg.norm(u)
+    q = (0.1 * rng.standard_normal((1, 2, n, 64)) + u).astype(np.float32)
+    k = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
+    k[0, 0, 5 * block + 3] = 20.0 * u  # the needle
+    c2 = scale * math.log2(math.e)
+    # |q| max|k| scale log2e ~ 100: inside the fp16 admission bound (256)
+    q *= 100.0 / (c2 * np.linalg.norm(q, axis=-1, keepdims=True) * 20.0)
+    q, k, v = (WL.round_to(x, torch.float16) for x in (q, k, v))
+    qt, kt, vt = (dev(x, torch.float16, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=3, local=1, beta=2.0,
+                                             compact=True)
+    idx, num = kv_idx.cpu().numpy(), kv_num.cpu().numpy()
+    # rows whose needle score exceeds their first sub-tile's largest score by more than 16
+    q64, k64 = q.astype(np.float64), k.astype(np.float64)
+    over = 0
+    for h in range(2):
+        for i in range(6, n // block):
+            sel = idx[0, h, i, :num[0, h, i]]
+            if 5 not in sel:
+                continue
+            k0 = sel[0] * block
+            rows = np.arange(i * block, (i + 1) * block)
+            m0 = (c2 * q64[0, h, rows] @ k64[0, 0, k0:k0 + 64].T).max(-1)
+            over += int((c2 * q64[0, h, rows] @ k64[0, 0, 5 * block + 3] - m0 > 16.5).sum())
+    assert over > 0  # the overflow path is exercised
+    out = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, scale=scale)
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), idx, block, scale=scale)
+    assert torch.isfinite(out).all()
+    assert np.abs(np_of(out) - ref).max() < TOL[torch.float16]
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("block", [64, 128, 256])
 def test_full_budget_matches_dense_sdpa(cuda, dtype, block):
