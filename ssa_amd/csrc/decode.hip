@@ -567,14 +567,17 @@ __device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
 }
 
 // One route workgroup's work: chunk `chunk` of the candidate blocks of key head bk.
-template <int DT, int DQ, int NW>
+// NW waves score (16 candidates each); all NWT >= NW waves take the rows' selections (one row
+// per wave and round).
+template <int DT, int DQ, int NW, int NWT = NW>
 __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk_) {
-  constexpr int NT = NW * 64, CH = NW * 16;  // threads, candidates per workgroup
+  static_assert(NWT >= NW, "selection waves include the scoring waves");
+  constexpr int NT = NWT * 64, CH = NW * 16;  // threads, candidates per workgroup
   constexpr int NQ = kDMaxRows * kDMaxD / NT;  // query elements staged per thread
   __shared__ double qd[kDMaxRows][kDMaxD + 1];   // q as fp64 (rows padded: conflict-free reads)
   __shared__ double q2d[kDMaxRows][kDMaxD + 1];  // fl32(q*q) as fp64
   __shared__ unsigned int skey[kDMaxRows][CH];
-  __shared__ unsigned int sbuf[NW][2][64];       // per wave: a row's kept entries
+  __shared__ unsigned int sbuf[NWT][2][64];      // per wave: a row's kept entries
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t bk = bk_, b = bk / f.Hkv, kvh = bk % f.Hkv;
   const int64_t c0 = chunk * CH;
@@ -596,7 +599,8 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
   // vectors (a candidate past the last one reads the last one; its score is discarded).
   // E1 = <q, mu> and E2 = <q*q, var> accumulate in fp64 in two chains.
   const int g = lane >> 4, n16 = lane & 15;
-  const int64_t c = c0 + wv * 16 + n16;
+  const int wsc = wv < NW ? wv : NW - 1;  // (waves past the scoring ones load wave NW-1's operands)
+  const int64_t c = c0 + wsc * 16 + n16;
   const bool cv = c < f.ncand;
   const int64_t cl = cv ? c : (f.ncand > 0 ? f.ncand - 1 : 0);
   float mm[DQ], vv[DQ];
@@ -625,15 +629,17 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
   __syncthreads();
   typedef double f64x4 __attribute__((ext_vector_type(4)));
   f64x4 a1 = {0.0, 0.0, 0.0, 0.0}, a2 = {0.0, 0.0, 0.0, 0.0};
+  if (NWT == NW || wv < NW) {  // wave-uniform: the selection-only waves skip the scoring
 #pragma unroll
-  for (int s = 0; s < DQ; ++s) {
-    a1 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[n16][g * DQ + s], (double)mm[s], a1, 0, 0, 0);
-    a2 = __builtin_amdgcn_mfma_f64_16x16x4f64(q2d[n16][g * DQ + s], (double)vv[s], a2, 0, 0, 0);
+    for (int s = 0; s < DQ; ++s) {
+      a1 = __builtin_amdgcn_mfma_f64_16x16x4f64(qd[n16][g * DQ + s], (double)mm[s], a1, 0, 0, 0);
+      a2 = __builtin_amdgcn_mfma_f64_16x16x4f64(q2d[n16][g * DQ + s], (double)vv[s], a2, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 4 * j + g;
-    if (r < G)
+    if (r < G && wv < NW)
       skey[r][wv * 16 + n16] =
           cv ? score_key(__fadd_rn((float)a1[j], __fmul_rn(f.coef2, (float)a2[j]))) : 0u;
   }
@@ -641,7 +647,7 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
   const int64_t nvalid = f.ncand - c0 < CH ? f.ncand - c0 : CH;
   const unsigned long long lt = (1ull << lane) - 1ull;
   constexpr int J = CH / 64;
-  for (int r = wv; r < G; r += NW) {
+  for (int r = wv; r < G; r += NWT) {
     const int64_t cb = (b * f.Hq + kvh * G + r) * f.nchunk + chunk;
     unsigned int key[J], cm = 0u;
 #pragma unroll
@@ -674,12 +680,12 @@ __device__ inline void route_chunk(const FusedStep& f, int64_t chunk, int64_t bk
   }
 }
 
-template <int DT, int DQ, int NW>
-__global__ __launch_bounds__(NW * 64) void decode_route_kernel(FusedStep f) {
+template <int DT, int DQ, int NW, int NWT = NW>
+__global__ __launch_bounds__(NWT * 64) void decode_route_kernel(FusedStep f) {
   if (blockIdx.x == 0 && blockIdx.y == 0)
-    for (int64_t t = threadIdx.x; t < f.B * f.Hq; t += NW * 64)
+    for (int64_t t = threadIdx.x; t < f.B * f.Hq; t += NWT * 64)
       __hip_atomic_store(&f.arrive[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  route_chunk<DT, DQ, NW>(f, blockIdx.x, blockIdx.y);
+  route_chunk<DT, DQ, NW, NWT>(f, blockIdx.x, blockIdx.y);
 }
 
 template <int NWA>
@@ -1543,17 +1549,17 @@ int decode_step_impl(const void* q, const void* k_new, const void* v_new, void* 
     f.kv_num = kv_num;
     f.kv_idx = kv_idx;
     const dim3 g1((unsigned)nchunk, (unsigned)(B * Hkv)), g2((unsigned)f.ngroups, (unsigned)(B * Hq));
-#define SSA_FUSED_ROUTE(DT, NW)                                                                   \
+#define SSA_FUSED_ROUTE(DT, NW, NWT)                                                              \
   do {                                                                                            \
-    if (d == 32) decode_route_kernel<DT, 8, NW><<<g1, NW * 64, 0, st>>>(f);                       \
-    else if (d == 64) decode_route_kernel<DT, 16, NW><<<g1, NW * 64, 0, st>>>(f);                 \
-    else decode_route_kernel<DT, 32, NW><<<g1, NW * 64, 0, st>>>(f);                              \
+    if (d == 32) decode_route_kernel<DT, 8, NW, NWT><<<g1, NWT * 64, 0, st>>>(f);                 \
+    else if (d == 64) decode_route_kernel<DT, 16, NW, NWT><<<g1, NWT * 64, 0, st>>>(f);           \
+    else decode_route_kernel<DT, 32, NW, NWT><<<g1, NWT * 64, 0, st>>>(f);                        \
   } while (0)
 #define SSA_FUSED_STEP(DT)                                                                        \
   do {                                                                                            \
-    if (chunk == kDChunk) SSA_FUSED_ROUTE(DT, 16);                                                \
-    else if (chunk == kDChunk / 4) SSA_FUSED_ROUTE(DT, 4);                                        \
-    else SSA_FUSED_ROUTE(DT, 8);                                                                  \
+    if (chunk == kDChunk) SSA_FUSED_ROUTE(DT, 16, 16);                                            \
+    else if (chunk == kDChunk / 4) SSA_FUSED_ROUTE(DT, 4, 8);                                     \
+    else SSA_FUSED_ROUTE(DT, 8, 8);                                                               \
     decode_attend_fused_kernel<DT><<<g2, 512, 0, st>>>(f, p);                                     \
   } while (0)
     switch (dtype) {
