@@ -437,9 +437,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, col = lane & 31;
   const int64_t qw0 = q0 + w * 32 * CG;  // first query row of this wave
-  int64_t qpos[CG];
+  int qpos[CG];  // 32-bit (the host checks n < 2^31)
 #pragma unroll
-  for (int c = 0; c < CG; ++c) qpos[c] = qw0 + 32 * c + col;
+  for (int c = 0; c < CG; ++c) qpos[c] = (int)qw0 + 32 * c + col;
+  // the same row, re-formed from the lane index where the tile loop and the epilogue use it: kept
+  // live across the loop it takes registers the fp16 bounded-row build does not have (it spilled)
+  auto qrow = [&](int c) -> int {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    return (int)qw0 + 32 * c + (ln & 31);
+  };
 
   const int64_t row = (b * p.Hq + h) * p.nbq + i;
   int cnt = p.kv_num[row];
@@ -577,10 +584,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     const unsigned short* kt = kbase + key0 * p.ksn;
     const unsigned short* vt = vtbase + key0;
     if (key0 + KT <= n32) {
+      // the lane's offsets are re-formed from the lane index on each call: hoisted out of the
+      // tile loop they stay live across it (and spilled in the fp16 bounded-row build)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int lrr = w * KR + ln / KC;
+      const uint32_t klr = (uint32_t)lrr * (uint32_t)p.ksn;
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        const int lcj = (lane % KC) ^ swz<KRB>(lr + j * KR * NW);
-        __builtin_amdgcn_global_load_lds(kt + j * kstep + (uint32_t)(lr * p.ksn + lcj * 8),
+        const int lcj = (ln % KC) ^ swz<KRB>(lrr + j * KR * NW);
+        __builtin_amdgcn_global_load_lds(kt + j * kstep + (klr + (uint32_t)(lcj * 8)),
                                          kdst + j * 1024 * NW + w * 1024, 16, 0, 0);
       }
     } else {  // ragged tail: rows >= n re-read row n-1 (their scores are masked)
@@ -659,7 +672,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     if (key0 + KT - 1 > (int)qw0 || key0 + KT > n32) {
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
-        const int lim_q = (int)qpos[c] - key0;
+        const int lim_q = qrow(c) - key0;
         const int lim_n = n32 - 1 - key0;
         const int lim = lim_q < lim_n ? lim_q : lim_n;
 #pragma unroll
@@ -801,7 +814,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
       const float lt = pair_sum(l_part[c]);  // (every lane: a cross-lane sum)
-      if (qpos[c] < p.n && !(lt < INFINITY)) bad = true;
+      if (qrow(c) < n32 && !(lt < INFINITY)) bad = true;
     }
     if (__any(bad) && lane == 0) {
       p.redo[(b * p.Hkv + kvh) * p.nbq + i] = 1;
@@ -812,9 +825,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   for (int c = 0; c < CG; ++c) {
     const float l_tot = pair_sum(l_part[c]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (qpos[c] < p.n) {
+    const int qr = qrow(c);
+    if (qr < n32) {
       unsigned short* op =
-          reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qpos[c] * p.osn;
+          reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh + qr * p.osn;
 #pragma unroll
       for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
@@ -826,7 +840,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
           *reinterpret_cast<uint2*>(op + d0) = wv;
         }
       if (p.lse != nullptr && half == 0)
-        p.lse[(b * p.Hq + h) * p.n + qpos[c]] =
+        p.lse[(b * p.Hq + h) * p.n + qr] =
             l_tot > 0.0f ? (m_run[c] + log2f(l_tot)) * kLn2 : -INFINITY;
     }
   }
