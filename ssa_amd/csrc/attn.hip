@@ -440,11 +440,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   int qpos[CG];  // 32-bit (the host checks n < 2^31)
 #pragma unroll
   for (int c = 0; c < CG; ++c) qpos[c] = (int)qw0 + 32 * c + col;
-  // the same row, re-formed from the lane index where the tile loop and the epilogue use it: kept
-  // live across the loop it takes registers the fp16 bounded-row build does not have (it spilled)
+  // REMAT: the fp16 bounded-row build (its m0 offset takes the last registers of the 128-VGPR
+  // budget) re-forms the lane's query row and K row offset from the lane index where the tile
+  // loop and the epilogue use them; kept live across the loop they spilled. The other builds
+  // keep them hoisted (re-forming costs ~11 VALU instructions per sub-tile).
+  constexpr bool REMAT = MODE == 1 && DT == SSA_F16;
   auto qrow = [&](int c) -> int {
     int ln = lane;
-    asm volatile("" : "+v"(ln));
+    if constexpr (REMAT) asm volatile("" : "+v"(ln));
     return (int)qw0 + 32 * c + (ln & 31);
   };
 
@@ -584,10 +587,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     const unsigned short* kt = kbase + key0 * p.ksn;
     const unsigned short* vt = vtbase + key0;
     if (key0 + KT <= n32) {
-      // the lane's offsets are re-formed from the lane index on each call: hoisted out of the
-      // tile loop they stay live across it (and spilled in the fp16 bounded-row build)
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
+      int ln = lane;  // (REMAT: re-formed on each call)
+      if constexpr (REMAT) asm volatile("" : "+v"(ln));
       const int lrr = w * KR + ln / KC;
       const uint32_t klr = (uint32_t)lrr * (uint32_t)p.ksn;
 #pragma unroll
