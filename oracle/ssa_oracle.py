@@ -56,23 +56,32 @@ def block_stats(x: np.ndarray, block: int, mode: str = "pop", n_real: int | None
     B, H, n, d = x.shape
     nb = -(-n // block)
     nr = n if n_real is None else min(n, int(n_real))
-    xp = np.zeros((B, H, nb * block, d), dtype=np.float64)
-    xp[:, :, :n] = x
-    valid = np.zeros((nb * block,), dtype=bool)
-    valid[:nr] = True
-    xb = xp.reshape(B, H, nb, block, d)
-    vb = valid.reshape(nb, block)[None, None, :, :, None]
-    cnt_rows = vb.sum(3)                                      # (1,1,nb,1)
-    cnt = np.maximum(cnt_rows, 1).astype(np.float64)
-    s1 = np.where(vb, xb, 0.0).sum(3)
-    mean = s1 / cnt
-    cen = np.where(vb, xb - mean[:, :, :, None, :], 0.0)
-    s2 = (cen * cen).sum(3)
-    s3 = (cen * cen * cen).sum(3)
-    vden = cnt - 1.0 if mode == "unbiased" else cnt
-    with np.errstate(divide="ignore", invalid="ignore"):
-        var = s2 / vden
-    return mean.astype(np.float32), var.astype(np.float32), (s3 / cnt).astype(np.float32)
+    outs = [np.empty((B, H, nb, d), dtype=np.float32) for _ in range(3)]
+    # blocks are independent: taken in chunks of whole blocks to bound the float64 temporaries
+    step = max(1, (1 << 22) // max(1, B * H * block * d))
+    for c0 in range(0, nb, step):
+        c1 = min(nb, c0 + step)
+        r0, r1 = c0 * block, min(n, c1 * block)
+        xp = np.zeros((B, H, (c1 - c0) * block, d), dtype=np.float64)
+        xp[:, :, :r1 - r0] = x[:, :, r0:r1]
+        valid = np.zeros(((c1 - c0) * block,), dtype=bool)
+        valid[:max(0, min(nr, r1) - r0)] = True
+        xb = xp.reshape(B, H, c1 - c0, block, d)
+        vb = valid.reshape(c1 - c0, block)[None, None, :, :, None]
+        cnt_rows = vb.sum(3)                                      # (1,1,nb,1)
+        cnt = np.maximum(cnt_rows, 1).astype(np.float64)
+        s1 = np.where(vb, xb, 0.0).sum(3)
+        mean = s1 / cnt
+        cen = np.where(vb, xb - mean[:, :, :, None, :], 0.0)
+        s2 = (cen * cen).sum(3)
+        s3 = (cen * cen * cen).sum(3)
+        vden = cnt - 1.0 if mode == "unbiased" else cnt
+        with np.errstate(divide="ignore", invalid="ignore"):
+            var = s2 / vden
+        outs[0][:, :, c0:c1] = mean
+        outs[1][:, :, c0:c1] = var
+        outs[2][:, :, c0:c1] = s3 / cnt
+    return outs[0], outs[1], outs[2]
 
 
 def qmean(q: np.ndarray, block: int) -> np.ndarray:
@@ -80,9 +89,15 @@ def qmean(q: np.ndarray, block: int) -> np.ndarray:
     (ssa/ssa_kernel.py:44,79; the caller pads with zeros at ssa/gemma_ssa.py:149)."""
     B, H, n, d = q.shape
     nb = -(-n // block)
-    qp = np.zeros((B, H, nb * block, d), dtype=np.float64)
-    qp[:, :, :n] = q
-    return (qp.reshape(B, H, nb, block, d).sum(3) / block).astype(np.float32)
+    out = np.empty((B, H, nb, d), dtype=np.float32)
+    step = max(1, (1 << 22) // max(1, B * H * block * d))  # whole blocks per chunk
+    for c0 in range(0, nb, step):
+        c1 = min(nb, c0 + step)
+        r0, r1 = c0 * block, min(n, c1 * block)
+        qp = np.zeros((B, H, (c1 - c0) * block, d), dtype=np.float64)
+        qp[:, :, :r1 - r0] = q[:, :, r0:r1]
+        out[:, :, c0:c1] = qp.reshape(B, H, c1 - c0, block, d).sum(3) / block
+    return out
 
 
 # ---------------------------------------------------------------------------------------------
