@@ -66,6 +66,77 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _event_ms(torch, fn, reps, warm=2):
+    """Mean HIP-event time of fn() over reps calls on the current stream (after warm calls)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def published_bench(torch, dev):
+    """The shapes of the reference's own published measurements, run here with seeded N(0,1)
+    inputs on the device. The reference's figures were taken on an RTX 4080 with FlexAttention /
+    faiss-gpu: the ratios compare whole systems on different hardware, not kernels.
+      flat-router SSA forward (ssa_flex: block_route + attention), B=1, H=8, d=64, fp16, block
+        128, top_c 8, local 1, against dense SDPA causal: paper/figures/kernel_speed_measured.json
+        :32-43 (13.25 / 203.9 ms at 131,072; 36.4 / 807 ms at 262,144);
+      IVF-routed forward (ssa_flex_ivf), H=1, fp16, block 128, top_c 8:
+        paper/figures/ivf_kernel_e2e.json:51-67,119-135 (16.1 ms at 1M, 139.5 ms at 12,582,912);
+      routed decode step over a 1,048,576-token cache, H=1, fp16, block 128, top_c 8, local 1,
+        mean of 128 steps: paper/figures/ivf_decode.json:17-31 (0.60 ms; dense 0.52 ms)."""
+    from ssa_amd import ivf_decode as D, ivf_kernel as IV, ssa_kernel as K
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def qkv(h, n):
+        return [torch.randn(1, h, n, 64, device=dev, dtype=torch.float16, generator=g)
+                for _ in range(3)]
+
+    out = {"note": "reference figures: RTX 4080 16 GB, FlexAttention/Triton and faiss-gpu "
+                   "(BASELINE.md section 1); here: MI355X, this build"}
+    for n, ref_ms, ref_dense in ((131072, 13.25, 203.9), (262144, 36.4, 807.0)):
+        q, k, v = qkv(8, n)
+        ms = _event_ms(torch, lambda: K.ssa_flex(q, k, v, 128, 8, 1), 5)
+        dms = _event_ms(torch, lambda: sdpa(q, k, v, is_causal=True), 3, warm=1)
+        out[f"flat_forward_h8_n{n}"] = {
+            "ms": ms, "dense_sdpa_ms": dms, "speedup_vs_dense": dms / ms,
+            "reference_ms": ref_ms, "reference_dense_ms": ref_dense,
+            "reference_speedup_vs_dense": ref_dense / ref_ms}
+        del q, k, v
+    for n, ref_ms in ((1 << 20, 16.1), (12582912, 139.5)):
+        q, k, v = qkv(1, n)
+        ms = _event_ms(torch, lambda: IV.ssa_flex_ivf(q, k, v, 128, 8, 1), 3, warm=1)
+        out[f"ivf_forward_h1_n{n}"] = {"ms": ms, "reference_ms": ref_ms}
+        del q, k, v
+    n, steps = 1 << 20, 128
+    q, k, v = qkv(1, n + steps)
+    dec = D.RoutedDecoder(1, 1, 1, 64, n + steps, block=128, top_c=8, local=1,
+                          dtype=torch.float16, device=dev)
+    dec.prefill(k[:, :, :n], v[:, :, :n])
+    o = torch.empty(1, 1, 64, device=dev, dtype=torch.float16)
+    for t in range(8):
+        dec.step(q[:, :, n + t], k[:, :, n + t], v[:, :, n + t], out=o)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(8, steps):
+        dec.step(q[:, :, n + t], k[:, :, n + t], v[:, :, n + t], out=o)
+    torch.cuda.synchronize()
+    dms = (time.perf_counter() - t0) / (steps - 8) * 1000.0
+    qd = q[:, :, n + steps - 1:n + steps]
+    dense = _event_ms(torch, lambda: sdpa(qd, k[:, :, :n + steps], v[:, :, :n + steps]), 10)
+    out["decode_h1_1m"] = {"ms_per_step": dms, "dense_sdpa_ms": dense, "reference_ms": 0.60,
+                           "reference_dense_ms": 0.52}
+    del q, k, v, dec
+    return out
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +152,8 @@ def parse():
                     help="skip the trainable swap (ssa_masked forward + backward)")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the whole-model prefill timing (Qwen2.5-0.5B architecture)")
+    ap.add_argument("--no-published", action="store_true",
+                    help="skip the reference's own published shapes (RTX 4080 numbers)")
     ap.add_argument("--swap-only", action="store_true",
                     help="run only the swap arm and print its JSON (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -566,6 +639,14 @@ def main():
             },
         }
         del q5, k5, v5, d5, vt5, idx5
+        torch.cuda.empty_cache()
+
+    if not args.no_published:
+        log("bench: the reference's published shapes")
+        try:
+            result["published_shapes"] = published_bench(torch, dev)
+        except Exception as e:  # reported, never fatal to the headline line
+            result["published_shapes"] = {"error": repr(e)}
         torch.cuda.empty_cache()
 
     if args.calibrate_copy:
