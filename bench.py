@@ -55,9 +55,7 @@ def router_fields(Hq, Hkv, nb, d, ms):
     s = ms / 1e3
     return {"ms": ms, "flops": flops, "mfma_flops": mfma, "tflops": flops / s / 1e12,
             "mfma_tflops": mfma / s / 1e12, "frac_bf16_mfma_peak": mfma / s / 1e12 / PEAK_BF16_TFLOPS,
-            "method": "bf16-split MFMA scores (3 products per fp32 product), certified: the "
-                      "candidates within the error bound of the keep-th score are ranked by the "
-                      "exact fp64-accumulated score"}
+            "method": "bf16-split MFMA scores, certified; band ranked by exact fp64 scores"}
 IVF_NPROBE = 4          # build_ivf's default (ssa/ivf_kernel.py:63)
 TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
 
@@ -99,8 +97,7 @@ def published_bench(torch, dev):
         return [torch.randn(1, h, n, 64, device=dev, dtype=torch.float16, generator=g)
                 for _ in range(3)]
 
-    out = {"note": "reference figures: RTX 4080 16 GB, FlexAttention/Triton and faiss-gpu "
-                   "(BASELINE.md section 1); here: MI355X, this build"}
+    out = {"note": "reference_*: RTX 4080 figures (BASELINE.md section 1)"}
     for n, ref_ms, ref_dense in ((131072, 13.25, 203.9), (262144, 36.4, 807.0)):
         q, k, v = qkv(8, n)
         ms = _event_ms(torch, lambda: K.ssa_flex(q, k, v, 128, 8, 1), 5)
@@ -287,12 +284,9 @@ def cpu_baseline(p, dec):
     t_total = t_route + t_attn
     out = {
         "value": cfg.n / t_total, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": (f"torch float32 on the host (oracle/cpu_path.py): the reference's "
-                   f"block_route_budget op sequence over all {cfg.Hq * nb} query-block rows "
-                   f"({t_route:.2f} s, median of 3) + block-sparse softmax for {len(pairs)} "
-                   f"(head, query-block) pairs ({sample_kv} of {total_kv} selected tiles = "
-                   f"{100.0 * sample_kv / total_kv:.2f} %, {t_sample:.2f} s) extrapolated by "
-                   f"sum(kv_num) to {t_attn:.1f} s: {t_total:.1f} s per layer"),
+        "sample": (f"torch fp32 host restatement (oracle/cpu_path.py): router over all "
+                   f"{cfg.Hq * nb} rows + softmax on {len(pairs)} (head, q-block) pairs "
+                   f"({100.0 * sample_kv / total_kv:.2f} % of tiles), scaled by sum(kv_num)"),
         "c3_router_s": t_route, "c3_attention_s_extrapolated": t_attn,
         "c3_attention_sample_fraction": sample_kv / total_kv,
     }
@@ -314,8 +308,7 @@ def cpu_baseline(p, dec):
                               c4.beta)
             runs.append((time.perf_counter() - t0) / 8)
         out["c4_decode_ms_per_step"] = sorted(runs)[1] * 1000.0
-        out["c4_sample"] = (f"{c4.Hq} query heads over the {n0}-token cache (resident block "
-                            f"summaries, as the GPU step), 8 steps per run, median of 3 runs")
+        out["c4_sample"] = f"{c4.Hq} heads, {n0}-token cache, median of 3 runs of 8 steps"
     return out
 
 
@@ -430,8 +423,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "sparse_attn_dma_kernel",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
-                     "traffic_source": f"committed rocprofv3 FETCH/WRITE_SIZE profile "
-                                       f"({TRAFFIC_FILE.name}), not measured in this run",
+                     "traffic_source": f"committed profile {TRAFFIC_FILE.name}",
                      "flops_per_launch": flops, "flops_causal_exact": flops_causal,
                      "sum_kv_num": sum_kv, "l2_hit_rate": l2_hit,
                      "gathered_kv_bytes": sum_kv * 2 * blk * cfg.d * 2},
@@ -461,8 +453,7 @@ def main():
                 2 * cfg.top_c)
     torch.cuda.synchronize()
     result["c3_ivf"] = {
-        "note": "approximate (sub-linear) IVF router timing, beside the exact router's; its "
-                "selections differ from the exact ones",
+        "note": "approximate IVF router timing; selections differ from the exact router's",
         "router": f"IVF over each key head's {nb3} block means: nlist {idx3.nlist}, nprobe "
                   f"{IVF_NPROBE}, search_k {2 * cfg.top_c}, top_c {cfg.top_c} + local {cfg.local}",
         "build_ms": ti.mean_ms("ivf_build"), "route_ms": ti.mean_ms("ivf_route"),
@@ -540,8 +531,7 @@ def main():
         torch.cuda.synchronize()
         dense_dms = (time.perf_counter() - t0) / 32 * 1000.0
         result["decode"] = {
-            "workload": "C4: routed decode step, bf16, 14q/2kv, d=64, KV cache 1,048,576 tokens "
-                        "(+ appended steps), block 128, top_c 64 + last 2 blocks, beta 2",
+            "workload": "C4: decode, bf16, 14q/2kv, d=64, 1M-token cache, block 128, top_c 64",
             "ms_per_step": dms, "steps": args.decode_steps,
             "bytes_per_step": dbytes, "achieved_gbs": dbytes / (dms / 1e3) / 1e9,
             "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
@@ -565,10 +555,8 @@ def main():
         try:
             from ssa_amd import longctx_swap as L
             res = L.run([32768, 131072], [1.0, 0.25, 0.12, 0.06], log=log)
-            res["workload"] = ("model(ids, logits_to_keep=1) of the 24-layer Qwen2.5-0.5B "
-                               "architecture in bf16 (random weights, random tokens; YaRN x4 "
-                               "for both arms), dense = torch SDPA, hip = install_ssa(impl='hip', "
-                               "block 128, beta 2, budget_frac); median of 3 after 2 warm-ups")
+            res["workload"] = ("24-layer Qwen2.5-0.5B architecture, bf16, random weights, "
+                               "YaRN x4; dense = SDPA, hip = install_ssa(impl='hip')")
             result["prefill"] = res
         except Exception as e:  # reported, never fatal to the headline line
             result["prefill"] = {"error": f"{type(e).__name__}: {e}"}
@@ -614,8 +602,7 @@ def main():
         attn = t5.mean_ms("transpose_v") + t5.mean_ms("attention")
         kv5 = int(kn5.sum().item())
         result["c5"] = {
-            "workload": "C5: single-head causal routed prefill, fp16, d=64, n=12,582,912, block 256 "
-                        "(49152 blocks), top_c 64 + local 1, beta 2; inputs seeded on the device",
+            "workload": "C5: 1 head, fp16, d=64, n=12,582,912, block 256, top_c 64 + local 1",
             "router_ms": router, "attention_ms": attn, "total_ms": router + attn,
             "tokens_per_s": c5.n / ((router + attn) / 1e3),
             "summaries_ms": t5.mean_ms("summaries") + t5.mean_ms("summaries_k"),
@@ -624,12 +611,8 @@ def main():
             "attention_tflops": 4.0 * c5.block * c5.block * c5.d * kv5 / (t5.mean_ms("attention") / 1e3) / 1e12,
             "sum_kv_num": kv5,
             "ivf": {
-                "note": "approximate (sub-linear) IVF router timing on C5's inputs, not a C5 "
-                        "result: its selections differ from the exact router's (Jaccard "
-                        "similarity below)",
-                "router": f"IVF over the 49152 key-block means: nlist {idx5.nlist} lists by "
-                          f"10 rounds of spherical k-means, nprobe {IVF_NPROBE}, search_k "
-                          f"{2 * c5.top_c}, top_c {c5.top_c} + local {c5.local}",
+                "note": "approximate IVF router timing, not a C5 result (Jaccard below)",
+                "router": f"nlist {idx5.nlist}, nprobe {IVF_NPROBE}, search_k {2 * c5.top_c}",
                 "build_ms": t5.mean_ms("ivf_build"), "route_ms": t5.mean_ms("ivf_route"),
                 "router_ms": ivf_router, "attention_kernel_ms": t5.mean_ms("ivf_attention"),
                 "total_ms": ivf_total, "tokens_per_s": c5.n / (ivf_total / 1e3),
@@ -667,7 +650,21 @@ def main():
         except Exception:
             pass
 
-    print(json.dumps(result), flush=True)
+    print(json.dumps(compact(result)), flush=True)
+
+
+def compact(result):
+    """The JSON line with the nested figures rounded to 5 significant digits (value and
+    ms_per_step in full), so that the line stays short."""
+    def rnd(o):
+        if isinstance(o, float):
+            return float(f"{o:.5g}") if math.isfinite(o) and o != 0.0 else o
+        if isinstance(o, dict):
+            return {k: rnd(v) for k, v in o.items()}
+        if isinstance(o, list):
+            return [rnd(v) for v in o]
+        return o
+    return {k: (v if k in ("value", "ms_per_step") else rnd(v)) for k, v in result.items()}
 
 
 if __name__ == "__main__":
