@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 5
+#define SSA_ABI_VERSION 6
 
 typedef void* ssa_stream_t; /* hipStream_t */
 

@@ -339,31 +339,40 @@ def sparse_attention(q, k, v, kv_num, kv_idx, block, scale=None, n=None, qblocks
     """o_t = softmax_j(scale * q_t.k_j) v_j over keys j <= t, j < n of the selected blocks of
     t's query block -- FlexAttention with BlockMask.from_kv_blocks + mask_mod kv<=q & kv<n
     (ssa/ssa_kernel.py:33-34,125-126; ssa/gemma_ssa.py:159-162,179), in float64.
-    Returns float64 (B, Hq, n, d); rows of query blocks not in `qblocks` (if given) are NaN."""
+    Returns float64 (B, Hq, n, d): rows of the `heads` (default all) whose query blocks are not in
+    `qblocks` (if given) are NaN; heads not in `heads` are zero. Only the rows and key heads used
+    are converted to float64 (the full-size conversions dominated the cost at 131K tokens)."""
     B, Hq, N, d = q.shape
     n = N if n is None else n
     Hkv = k.shape[1]
     G = Hq // Hkv
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     nb = -(-n // block)
-    out = np.full((B, Hq, n, d), np.nan)
-    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    hs = list(range(Hq)) if heads is None else [int(h) for h in heads]
+    out = np.zeros((B, Hq, n, d))
     for b in range(B):
-        for h in (range(Hq) if heads is None else heads):
+        for h in hs:
+            out[b, h] = np.nan
+    for b in range(B):
+        kv64 = {}
+        for h in hs:
             kh = h // G
+            if kh not in kv64:
+                kv64 = {kh: (k[b, kh, :n].astype(np.float64), v[b, kh, :n].astype(np.float64))}
+            k64, v64 = kv64[kh]
             for i in (range(nb) if qblocks is None else qblocks):
                 t0, t1 = i * block, min((i + 1) * block, n)
                 ids = [int(c) for c in kv_idx[b, h, i, :kv_num[b, h, i]]]
                 keys = np.concatenate([np.arange(c * block, min((c + 1) * block, n)) for c in ids]) \
                     if ids else np.zeros(0, dtype=np.int64)
-                s = scale * (q64[b, h, t0:t1] @ k64[b, kh, keys].T)
+                s = scale * (q[b, h, t0:t1].astype(np.float64) @ k64[keys].T)
                 allow = keys[None, :] <= np.arange(t0, t1)[:, None]
                 s = np.where(allow, s, -np.inf)
                 m = s.max(-1, keepdims=True)
                 m = np.where(np.isfinite(m), m, 0.0)
                 p = np.exp(s - m)
                 l = p.sum(-1, keepdims=True)
-                out[b, h, t0:t1] = np.where(l > 0, (p @ v64[b, kh, keys]) / np.where(l > 0, l, 1), 0.0)
+                out[b, h, t0:t1] = np.where(l > 0, (p @ v64[keys]) / np.where(l > 0, l, 1), 0.0)
     return out
 
 

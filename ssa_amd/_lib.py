@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2

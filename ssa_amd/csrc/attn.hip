@@ -39,19 +39,23 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleSlack = 8.0f;
 // Rows whose scores provably stay within +-fast_bound<DT>() (log2 units) take the softmax without
-// a running max. The bound is set by precision: the bounded path pre-scales q by scale*log2e and
-// rounds it to the input type (relative error <= 2^-8 per element for bf16, 2^-11 for fp16),
-// which moves a score by at most that error times |q| |k| scale log2e < bound: 1/8 log2 unit at
-// 32 (bf16) and at 256 (fp16) -- a relative change of P of at most 9 %, typically ~1 % since the
-// rounding errors of the 64 elements have random signs, the size of the query's own rounding.
-// P = 2^s is packed into the MFMA input type. bf16 has fp32's exponent range. fp16's largest
-// finite value is 65504 < 2^16: an fp16 row takes P = 2^(s - m0), m0 the largest score of its
-// first sub-tile (a lower bound of its maximum: the row's largest P is >= 1, so P below 2^-24,
-// flushed to 0, is negligible beside it), which stays finite unless a later score exceeds
-// m0 + 16; a row whose sum l comes out non-finite sends its query block to the exact launch.
-// Rows beyond the bound take the exact running-max path, whose scores are the fp32 products.
+// a running max. The bounded path pre-scales q by scale*log2e and rounds it to fp16 for the QK
+// product (bf16 inputs: against the fp16 copy of K written by the key-norm pass, exact for
+// |k| < 2^16), so a score moves by at most 2^-11 |q| |k| scale log2e < 2^-11 * bound = 1/64
+// log2 unit at the bound of 32 -- a change of at most 1.1 % in one P, 2.2 % in the ratio of two
+// (typically ~0.1 %: the 64 elements' rounding errors have random signs); the fp32-scaled
+// scores of the exact path and of FlexAttention carry no such error. A key-norm limit of 4096
+// keeps the fp16 rounding of tiny q elements (absolute 2^-25) and the fp16 copy's range out of
+// the error. P = 2^s is packed into the PV input type. bf16 has fp32's exponent range. fp16's
+// largest finite value is 65504 < 2^16: an fp16 row takes P = 2^(s - m0), m0 the largest score
+// of its first sub-tile (a lower bound of its maximum: the row's largest P is >= 1, so P below
+// 2^-24, flushed to 0, is negligible beside it), which stays finite unless a later score
+// exceeds m0 + 16; a row whose sum l comes out non-finite sends its query block to the exact
+// launch. Rows beyond the bound take the exact running-max path, whose scores are the fp32
+// products scaled in fp32.
 constexpr float kFastBoundBf16 = 32.0f;
-constexpr float kFastBoundF16 = 256.0f;
+constexpr float kFastBoundF16 = 32.0f;
+constexpr float kKeyNormLimit = 4096.0f;
 template <int DT>
 __device__ constexpr float fast_bound() {
   return DT == SSA_F16 ? kFastBoundF16 : kFastBoundBf16;
@@ -64,6 +68,7 @@ __device__ constexpr float fast_bound() {
 struct AttnParams {
   const char* q;
   const char* k;
+  const char* k16;  // fp16 copy of bf16 K (B, Hkv, n_pad, 64) in the workspace (bounded rows)
   const char* v;   // natural V (fp32 path)
   const char* vt;  // V^T workspace (B, Hkv, 64, n_pad) (16-bit path)
   char* o;
@@ -160,6 +165,12 @@ struct Mfma<SSA_F16> {
   }
 };
 
+__device__ inline unsigned int pack2_f16(float a, float b) {
+  const unsigned short lo = __builtin_bit_cast(unsigned short, (_Float16)a);
+  const unsigned short hi = __builtin_bit_cast(unsigned short, (_Float16)b);
+  return (unsigned int)lo | ((unsigned int)hi << 16);
+}
+
 // Key-norm bound of the attention call: the largest squared norm of key rows k0..k0+63 of one
 // key head (rows >= n count 0) into its tile's slot; the first tile's workgroup also clears the
 // head's unbounded flag for the mode-1 launch, and the tile starting a query block its redo flag. 256 threads; lanes 8r..8r+7 of a pass read row
@@ -173,6 +184,8 @@ struct KeyNorm {
   int64_t ntile;
   int* redo;       // (B*Hkv, nbq): cleared here, one entry per query block (block a multiple of 64)
   int64_t block, nbq;
+  unsigned short* k16;  // bf16 keys: their fp16 copy (B*Hkv, n_pad, 64), rows >= n zero (else NULL)
+  int64_t n_pad;
 };
 
 __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t kvh,
@@ -186,13 +199,21 @@ __device__ inline void key_tile_norm_max(const KeyNorm& kn, int64_t b, int64_t k
     const int q = tid + 256 * j;
     const int row = q >> 3, ch = q & 7;
     float acc = 0.0f;
+    u32x4 h = {0u, 0u, 0u, 0u};
     if (k0 + row < n) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(base + (k0 + row) * kn.ksn + ch * 8);
       float x[8];
       unpack8(w, x, kn.bf16);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = fmaf(x[e], x[e], acc);
+      // fp16 holds every bf16 value of magnitude in [2^-14, 2^16) exactly (8 significant bits
+      // in 11); smaller ones move by at most 2^-25, larger ones overflow -- tiles with such keys
+      // fail the bounded rows' key-norm limit, so the exact path (which reads k) takes them
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = pack2_f16(x[2 * e], x[2 * e + 1]);
     }
+    if (kn.k16 != nullptr)
+      *reinterpret_cast<u32x4*>(kn.k16 + ((b * Hkv + kvh) * kn.n_pad + k0 + row) * 64 + ch * 8) = h;
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
     acc += __shfl_xor(acc, 4, 64);
@@ -396,6 +417,10 @@ template <int DT, int NW, int CG, int WPE, int MODE, int D = 64, int KT = 64>
 __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
+  // bounded rows of bf16 inputs: S^T = K Q^T on fp16 operands (the fp16 copy of K, q scale log2e
+  // rounded to fp16); every other product in the input type
+  constexpr bool K16 = MODE == 1 && DT == SSA_BF16;
+  using MQ = Mfma<K16 ? SSA_F16 : DT>;
   static_assert(D % 64 == 0 && (KT == 32 || KT == 64), "head dim a multiple of 64, KT 32 or 64");
   static_assert(MODE == 0 || D == 64, "the bounded-row path is built for head dim 64");
   constexpr int TILE = KT * D * 2;    // bytes of one K or V^T sub-tile
@@ -508,7 +533,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         }
       qn2 = pair_sum(qn2);
       const float qn = sqrtf(qn2);
-      ok = ok && (p.scale_log2 * qn * sqrtf(km2) < fast_bound<DT>()) && (p.scale_log2 * qn < 1.0e4f);
+      ok = ok && (p.scale_log2 * qn * sqrtf(km2) < fast_bound<DT>()) &&
+           (sqrtf(km2) < kKeyNormLimit) && (p.scale_log2 * qn < 1.0e4f);
     }
     if (tid == 0) wg_bounded = 1;
     __syncthreads();
@@ -531,13 +557,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
           float x[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) x[j] = (float)qf[c][kd][j] * p.scale_log2;
-          qf[c][kd] = M::pack(x);
+          qf[c][kd] = __builtin_bit_cast(vec, MQ::pack(x));
         }
     }
   }
 
+  // K rows: the input, or (K16) its fp16 copy, contiguous rows of 64
+  const int64_t ksn = K16 ? 64 : p.ksn;
   const unsigned short* kbase =
-      reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
+      K16 ? reinterpret_cast<const unsigned short*>(p.k16) + (b * p.Hkv + kvh) * p.n_pad * 64
+          : reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb + kvh * p.ksh;
   const unsigned short* vtbase =
       reinterpret_cast<const unsigned short*>(p.vt) + (b * p.Hkv + kvh) * D * p.n_pad;
 
@@ -553,7 +582,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   static_assert((VR * NW) % 16 == 0, "V^T rows per load instruction keep the swizzle");
   const int vc = (lane % VC) ^ swz<VRB>(vr);
   const uint32_t vgo = (uint32_t)(vr * p.n_pad + vc * 8);
-  const int64_t kstep = KR * NW * p.ksn, vstep = VR * NW * p.n_pad;
+  const int64_t kstep = KR * NW * ksn, vstep = VR * NW * p.n_pad;
 
   // Tile cursor over the row's block list: entry ce, sub-tile cs (key0 = list[ce]*block + cs*KT).
   // The list is held 64 entries at a time in one VGPR (entry lbase + j in lane j), read with
@@ -584,13 +613,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
     }
   };
   auto issue = [&](unsigned char* kdst, unsigned char* vdst, int key0) {
-    const unsigned short* kt = kbase + key0 * p.ksn;
+    const unsigned short* kt = kbase + key0 * ksn;
     const unsigned short* vt = vtbase + key0;
     if (key0 + KT <= n32) {
       int ln = lane;  // (REMAT: re-formed on each call)
       if constexpr (REMAT) asm volatile("" : "+v"(ln));
       const int lrr = w * KR + ln / KC;
-      const uint32_t klr = (uint32_t)lrr * (uint32_t)p.ksn;
+      const uint32_t klr = (uint32_t)lrr * (uint32_t)ksn;
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
         const int lcj = (ln % KC) ^ swz<KRB>(lrr + j * KR * NW);
@@ -603,7 +632,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         int64_t r = key0 + j * KR * NW + lr;
         if (r > p.n - 1) r = p.n - 1;
         const int lcj = (lane % KC) ^ swz<KRB>(lr + j * KR * NW);
-        __builtin_amdgcn_global_load_lds(kbase + r * p.ksn + lcj * 8,
+        __builtin_amdgcn_global_load_lds(kbase + r * ksn + lcj * 8,
                                          kdst + j * 1024 * NW + w * 1024, 16, 0, 0);
       }
     }
@@ -659,7 +688,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         for (int r = 0; r < 16; ++r) sacc[tt][c][r] = OFS ? -m_run[c] : 0.0f;
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd)
-          sacc[tt][c] = M::mma(M::from_bits(ka[tt][kd]), qf[c][kd], sacc[tt][c]);
+          sacc[tt][c] = MQ::mma(MQ::from_bits(ka[tt][kd]),
+                                __builtin_bit_cast(typename MQ::vec, qf[c][kd]), sacc[tt][c]);
       }
     if constexpr (!fast) __builtin_amdgcn_s_setprio(0);
     // V^T fragments of the first two key steps, in flight during the softmax
@@ -884,15 +914,26 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
 }  // namespace
 }  // namespace ssa
 
+namespace ssa {
+namespace {
+// bytes of the fp16 key copy (bf16 inputs at head dim 64: the bounded rows' QK operand)
+size_t k16_bytes(int dtype, int64_t B, int64_t Hkv, int64_t n_pad, int64_t d) {
+  if (dtype != SSA_BF16 || d != 64) return 0;
+  return ((size_t)B * (size_t)Hkv * (size_t)n_pad * 64u * 2u + 255) / 256 * 256;
+}
+}  // namespace
+}  // namespace ssa
+
 extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n,
                                                  int64_t d, int64_t block) {
   if (dtype == SSA_F32 || block <= 0) return 0;
   const int64_t n_pad = (n + block - 1) / block * block;
   const size_t vt = ((size_t)B * (size_t)Hkv * (size_t)d * (size_t)n_pad * 2u + 255) / 256 * 256;
-  // V^T, then the per-tile key-norm maxima (float), one unbounded-workgroup flag (int) per key
-  // head and one redo flag (int) per (key head, query block)
+  // V^T, then (bf16, head dim 64) the fp16 copy of K, then the per-tile key-norm maxima
+  // (float), one unbounded-workgroup flag (int) per key head and one redo flag (int) per
+  // (key head, query block)
   const size_t tail = (size_t)(B * Hkv * (n_pad / 64) + B * Hkv + B * Hkv * (n_pad / block)) * 4u;
-  return vt + (tail + 255) / 256 * 256;
+  return vt + ssa::k16_bytes(dtype, B, Hkv, n_pad, d) + (tail + 255) / 256 * 256;
 }
 
 extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
@@ -974,6 +1015,7 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.tmax2 = nullptr;
   p.unbounded = nullptr;
   p.redo = nullptr;
+  p.k16 = nullptr;
   p.ntile = p.n_pad / 64;
   if (dtype == SSA_F32) {
     p.vt = nullptr;
@@ -990,14 +1032,17 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.vt = static_cast<const char*>(workspace);
   SSA_REQUIRE(B * Hkv < 65536 && p.n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "sparse_attn: grid too large");
-  // after V^T: the per-tile key-norm maxima, then mode 1's unbounded flags (both written by the
-  // key-norm pass below, every entry every call)
+  // after V^T: the fp16 copy of K (bf16, head dim 64), the per-tile key-norm maxima, then mode
+  // 1's unbounded flags (all written by the key-norm pass below, every entry every call)
   const size_t vt_bytes = ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
-  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes);
+  const size_t k16b = k16_bytes(dtype, B, Hkv, p.n_pad, d);
+  unsigned short* k16 =
+      k16b ? reinterpret_cast<unsigned short*>(static_cast<char*>(workspace) + vt_bytes) : nullptr;
+  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes + k16b);
   int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
   int* redo = unbounded + B * Hkv;
   KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
-             unbounded, p.ntile, redo, block, p.nbq};
+             unbounded, p.ntile, redo, block, p.nbq, k16, p.n_pad};
   if (d != 64) {  // exact path only: V^T (unless supplied), no key norms
     if (!(flags & SSA_ATTN_VT_READY)) {
       KeyNorm none{};
@@ -1022,6 +1067,7 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.tmax2 = tmax2;
   p.unbounded = unbounded;
   p.redo = redo;
+  p.k16 = reinterpret_cast<const char*>(k16);
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, 64, st);
   return launch_mfma<SSA_F16>(p, 64, st);
 }

@@ -112,10 +112,17 @@ def test_route_width():
 
 
 def test_workspace_queries():
-    # V^T (256-byte aligned), then the fp32 key-norm maximum of every 64-key tile (2 heads x 6
-    # tiles) and one flag per (b, kv head), rounded up to 256 bytes
+    # V^T (256-byte aligned), the fp16 copy of the bf16 keys (2 heads x 384 rows x 64), then the
+    # fp32 key-norm maximum of every 64-key tile (2 heads x 6 tiles) and the per-(b, kv head) and
+    # per-query-block flags, rounded up to 256 bytes
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.BF16, 1, 2, 300, 64, 128) == \
+        2 * 64 * 384 * 2 + 2 * 384 * 64 * 2 + 256
+    # fp16 keys are read directly: no copy
+    assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F16, 1, 2, 300, 64, 128) == \
         2 * 64 * 384 * 2 + 256
+    # head dim 128 (exact path only): V^T and the flags
+    assert _lib.query("ssa_sparse_attn_workspace_size", _lib.BF16, 1, 2, 300, 128, 128) == \
+        2 * 128 * 384 * 2 + 256
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F32, 1, 2, 300, 64, 128) == 0
     # per routed row: the score keys, then the certified scoring's error magnitude and largest
     # key per 64-candidate tile

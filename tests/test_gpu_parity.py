@@ -4,6 +4,7 @@ CPU oracle and the reference's golden outputs, on the seeded configurations and 
 Bars: selections bit-exact against the oracle and equal to the reference's float32 selections
 except on certified float32 near-ties; summaries within 1 ulp of the oracle; attention outputs
 within 2e-2 (bf16/fp16) or 1e-5 (fp32) max-abs of the oracle's float64 masked softmax."""
+import functools
 import math
 
 import numpy as np
@@ -336,11 +337,17 @@ def test_ssa_flex_c1_fp32_matches_reference_flexattention(cuda):
     assert err < 1e-5, err
 
 
+@functools.lru_cache(maxsize=1)
+def c3_inputs():
+    """The C3 bench input (host arrays), generated once per test session."""
+    return WL.make("C3")
+
+
 @pytest.mark.parametrize("cfg_name,n,qblocks", [("C2", 8192, [0, 1, 5, 63, 127]),
                                                 ("C2", 32768, [0, 2, 100, 311, 511]),
                                                 ("C3", 131072, [0, 3, 64, 511, 1023])])
 def test_sparse_attention_matches_oracle(cuda, cfg_name, n, qblocks):
-    p = WL.make(cfg_name, n=n)
+    p = c3_inputs() if cfg_name == "C3" else WL.make(cfg_name, n=n)
     cfg = p["cfg"]
     q, k, v = (dev(p[x], cfg.dtype, cuda) for x in ("q", "k", "v"))
     kv_num, kv_idx, _ = K.block_route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
@@ -356,6 +363,120 @@ def test_sparse_attention_matches_oracle(cuda, cfg_name, n, qblocks):
             err = np.abs(o[0, h, sl] - ref[0, h, sl]).max()
             assert err < TOL[cfg.dtype], (h, i, err)
     assert torch.isfinite(out).all()
+
+
+def test_c3_attention_whole_heads_match_oracle(cuda):
+    """Every query block (all 1,024) of query heads 0 and 13 -- one per key head -- of the C3
+    bench input against the float64 oracle (every C3 workgroup takes the bounded-row path)."""
+    p = c3_inputs()
+    cfg = p["cfg"]
+    q, k, v = (dev(p[x], cfg.dtype, cuda) for x in ("q", "k", "v"))
+    kv_num, kv_idx, _ = K.block_route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                             beta=cfg.beta, compact=True)
+    out = np_of(K.sparse_attention(q, k, v, kv_num, kv_idx, cfg.block))
+    heads = [0, 13]
+    ref = O.sparse_attention(p["q"], p["k"], p["v"], kv_num.cpu().numpy(), kv_idx.cpu().numpy(),
+                             cfg.block, heads=heads)
+    err = max(float(np.abs(out[0, h] - ref[0, h]).max()) for h in heads)
+    print(f"C3 heads {heads}, all {cfg.n // cfg.block} query blocks: max |err| {err:.3g}")
+    assert err < TOL[cfg.dtype], err
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_c3_shape_rows_near_the_bound(cuda, seed):
+    """C3-shaped inputs (14q/2kv, d 64, block 128, top_c 64 + local 2, beta 2, keys from the
+    segmented Gaussian mixture, n = 32,768) with every query row rescaled so that
+    scale*log2e*|q|*max|k| (max over the key head) lies in [0.9, 0.995] of the bf16 admission
+    bound: every workgroup takes the bounded-row path with rows at its edge. 48 query blocks of
+    4 heads against the float64 oracle."""
+    cfg = WL.C3
+    n, c = 32768, math.log2(math.e) / 8.0
+    rng = np.random.default_rng(1000 + seed)
+    q = rng.standard_normal((1, cfg.Hq, n, cfg.d), dtype=np.float32)
+    k = WL.round_to(WL._gmm_keys(rng, cfg.Hkv, n, cfg.d), cfg.dtype)
+    v = WL.round_to(rng.standard_normal((1, cfg.Hkv, n, cfg.d), dtype=np.float32), cfg.dtype)
+    kmax = np.sqrt((k.astype(np.float64) ** 2).sum(-1)).max(-1)  # (1, Hkv)
+    G = cfg.Hq // cfg.Hkv
+    u = rng.uniform(0.9, 0.995, size=(1, cfg.Hq, n, 1))
+    target = u * FAST_BOUND[cfg.dtype] / (c * np.repeat(kmax, G, axis=1)[:, :, None, None])
+    q = q / np.linalg.norm(q, axis=-1, keepdims=True) * target
+    q = WL.round_to(q.astype(np.float32), cfg.dtype)
+    qmax = np.linalg.norm(q.astype(np.float64), axis=-1).max(-1)  # (1, Hq)
+    bound = float((c * qmax * np.repeat(kmax, G, axis=1)).max())
+    assert 0.95 * FAST_BOUND[cfg.dtype] < bound < FAST_BOUND[cfg.dtype], bound
+    qt, kt, vt = (dev(x, cfg.dtype, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                             beta=cfg.beta, compact=True)
+    out = np_of(K.sparse_attention(qt, kt, vt, kv_num, kv_idx, cfg.block))
+    qblocks = sorted(set(rng.choice(n // cfg.block, 47, replace=False).tolist()) | {n // cfg.block - 1})
+    heads = [0, 6, 7, 13]
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), cfg.block,
+                             qblocks=qblocks, heads=heads)
+    err = max(float(np.abs(out[0, h, i * cfg.block:(i + 1) * cfg.block] -
+                        ref[0, h, i * cfg.block:(i + 1) * cfg.block]).max())
+              for h in heads for i in qblocks)
+    print(f"seed {seed}: max bound {bound:.2f}, max |err| {err:.3g}")
+    assert err < TOL[cfg.dtype], err
+
+
+def two_key_case(dtype, target, rounding, seed=0, n=2048, block=128, amp=1.0, scale=0.125):
+    """A case built against the bounded-row path's one approximation, the rounding of
+    q*scale*log2e before the QK product. Query block i (i >= 1) repeats one query row q_i with
+    scale*log2e*|q_i|*8 = target; key block i-1 starts with two keys k+- = a*qh +- b*w (|k+-| =
+    8, a = 4, qh = q_i/|q_i|) whose exact scores are equal, w being the part orthogonal to qh of
+    the rounding error of q_i*scale*log2e in `rounding` (float16: what the kernel rounds to;
+    bfloat16: what it rounded to before) -- so that rounding moves the two scores in opposite
+    directions by the largest amount its error allows. Their values are +-amp*e_(i mod 64): the
+    exact output there is 0 and a score difference of x log2 units shows as amp*tanh(x ln2/2).
+    The other keys: random directions of norm 2.4, values ~0.1 N(0,1). Lists: [i-1, i]."""
+    rng = np.random.default_rng(seed)
+    d, c, kn = 64, scale * math.log2(math.e), 8.0
+    nb = n // block
+    q = np.zeros((1, 1, n, d), np.float32)
+    for i in range(nb):
+        x = rng.standard_normal(d)
+        q[0, 0, i * block:(i + 1) * block] = x / np.linalg.norm(x) * (target / (c * kn))
+    q = WL.round_to(q, dtype)
+    r = rng.standard_normal((1, 1, n, d))
+    k = (r / np.linalg.norm(r, axis=-1, keepdims=True) * 0.3 * kn).astype(np.float32)
+    v = (0.1 * rng.standard_normal((1, 1, n, d))).astype(np.float32)
+    a = 0.5 * kn
+    b = math.sqrt(kn * kn - a * a) * 0.999
+    for i in range(1, nb):
+        x = q[0, 0, i * block].astype(np.float64)
+        qc = x * c
+        delta = WL.round_to(qc.astype(np.float32), rounding).astype(np.float64) - qc
+        qh = x / np.linalg.norm(x)
+        w = delta - (delta @ qh) * qh
+        w /= np.linalg.norm(w)
+        p0 = (i - 1) * block
+        k[0, 0, p0], k[0, 0, p0 + 1] = a * qh + b * w, a * qh - b * w
+        v[0, 0, p0:p0 + 2] = 0.0
+        v[0, 0, p0, i % d], v[0, 0, p0 + 1, i % d] = amp, -amp
+    k, v = WL.round_to(k, dtype), WL.round_to(v, dtype)
+    kv_num = np.full((1, 1, nb), 2, np.int32)
+    kv_num[0, 0, 0] = 1
+    kv_idx = np.array([[[[max(i - 1, 0), i] for i in range(nb)]]], np.int32)
+    return q, k, v, kv_num, kv_idx, block, scale
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("target", [16.0, 31.0, 40.0])
+@pytest.mark.parametrize("rounding", [torch.float16, torch.bfloat16])
+def test_bounded_rows_constructive_rounding(cuda, dtype, target, rounding):
+    """two_key_case: rounding errors of q*scale*log2e added constructively along k. Just under
+    the admission bound (31) the bounded path rounds q*scale*log2e to fp16 and stays well within
+    2e-2 (the earlier bf16 rounding gave 0.040 here); above it (40) the exact path, whose scores
+    are scaled in fp32, shows only the rounding of P."""
+    q, k, v, num, idx, block, scale = two_key_case(dtype, target, rounding)
+    ref = O.sparse_attention(q, k, v, num, idx, block, scale=scale)
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    out = np_of(K.sparse_attention(qt, kt, vt, torch.from_numpy(num).to(cuda),
+                                   torch.from_numpy(idx).to(cuda), block, scale=scale))
+    err = float(np.abs(out - ref).max())
+    print(f"{dtype} target {target} rounding {rounding}: max |err| {err:.3g}")
+    assert np.isfinite(out).all()
+    assert err < 1e-2, err
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -382,23 +503,24 @@ def test_unbounded_rows_take_the_exact_path(cuda, dtype, block):
 
 
 # admission bounds of the bounded-row path (log2 units of scale * q.k): attn.hip fast_bound<DT>
-FAST_BOUND = {torch.float16: 256.0, torch.bfloat16: 32.0}
+FAST_BOUND = {torch.float16: 32.0, torch.bfloat16: 32.0}
 
 
 @pytest.mark.parametrize("dtype,target,aligned", [
-    (torch.float16, 14.0, True), (torch.float16, 22.0, True), (torch.float16, 60.0, True),
-    (torch.float16, 250.0, True), (torch.float16, 270.0, True), (torch.float16, 60.0, False),
-    (torch.float16, 250.0, False), (torch.bfloat16, 31.0, True), (torch.bfloat16, 60.0, True)])
+    (torch.float16, 14.0, True), (torch.float16, 22.0, True), (torch.float16, 31.0, True),
+    (torch.float16, 33.0, True), (torch.float16, 250.0, True), (torch.float16, 31.0, False),
+    (torch.float16, 250.0, False), (torch.bfloat16, 14.0, True), (torch.bfloat16, 31.0, True),
+    (torch.bfloat16, 33.0, True), (torch.bfloat16, 60.0, True)])
 def test_rows_near_the_fast_path_bound(cuda, dtype, target, aligned):
     """Every row's |q| is set so that the key-norm bound scale*log2e*|q|*max|k| equals `target`:
-    just under the dtype's admission bound the rows take the bounded path (bf16 and fp16: the
-    pre-scaled q's rounding must stay within tolerance; fp16: P = 2^(S - m0), m0 the largest
-    score of the row's first sub-tile, overflows when a later score exceeds m0 + 16, and the
-    query block is then redone exactly), just over it the exact path. aligned: keys lean on the
-    queries' direction so that scores reach the bound (largest scores near `target`, a peaked
-    softmax); not aligned: random keys, scores far below the bound, so at fp16 250 the scores
-    of later sub-tiles can exceed m0 + 16 (overflow and redo). The output must be finite and
-    within 2e-2 of the float64 oracle either way."""
+    just under the admission bound (32) the rows take the bounded path (q*scale*log2e rounded to
+    fp16 must stay within tolerance; fp16: P = 2^(S - m0), m0 the largest score of the row's
+    first sub-tile, overflows when a later score exceeds m0 + 16, and the query block is then
+    redone exactly), just over it the exact path. aligned: keys lean on the queries' direction so
+    that scores reach the bound (largest scores near `target`, a peaked softmax); not aligned:
+    random keys, scores far below the bound, so at fp16 31 the scores of later sub-tiles can
+    exceed m0 + 16 (overflow and redo). The output must be finite and within 2e-2 of the float64
+    oracle either way."""
     rng = np.random.default_rng(21)
     n, block, scale = 1024, 128, 0.125
     q = rng.standard_normal((1, 2, n, 64)).astype(np.float32)
@@ -444,8 +566,8 @@ def test_fp16_bounded_rows_overflow_redone_exactly(cuda, block):
     v = rng.standard_normal((1, 1, n, 64)).astype(np.float32)
     k[0, 0, 5 * block + 3] = 20.0 * u  # the needle
     c2 = scale * math.log2(math.e)
-    # |q| max|k| scale log2e ~ 100: inside the fp16 admission bound (256)
-    q *= 100.0 / (c2 * np.linalg.norm(q, axis=-1, keepdims=True) * 20.0)
+    # |q| max|k| scale log2e ~ 31: inside the admission bound (32)
+    q *= 31.0 / (c2 * np.linalg.norm(q, axis=-1, keepdims=True) * 20.0)
     q, k, v = (WL.round_to(x, torch.float16) for x in (q, k, v))
     qt, kt, vt = (dev(x, torch.float16, cuda) for x in (q, k, v))
     kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=3, local=1, beta=2.0,
