@@ -54,9 +54,17 @@ def router_fields(Hq, Hkv, nb, d, ms):
     mfma = 3.0 * 2.0 * (2 * d) * 64 * 64 * tiles * Hkv
     s = ms / 1e3
     return {"ms": ms, "flops": flops, "mfma_flops": mfma, "tflops": flops / s / 1e12,
-            "mfma_tflops": mfma / s / 1e12, "frac_bf16_mfma_peak": mfma / s / 1e12 / PEAK_BF16_TFLOPS,
+            "mfma_tflops": mfma / s / 1e12,
+            # the reference einsum's FLOPs over the route time (the fraction of the bf16 peak the
+            # router's algorithmic work reaches), and the issued bf16-split MFMA work's fraction
+            "frac_bf16_peak_algorithmic": flops / s / 1e12 / PEAK_BF16_TFLOPS,
+            "frac_bf16_mfma_peak": mfma / s / 1e12 / PEAK_BF16_TFLOPS,
             "method": "bf16-split MFMA scores, certified; band ranked by exact fp64 scores"}
 IVF_NPROBE = 4          # build_ivf's default (ssa/ivf_kernel.py:63)
+# the timed attention calls walk each workgroup's key blocks from a clock-derived position
+# (sparse_attention(rotate=True): workgroups resident together share the key blocks they read
+# in L2); outputs differ from the default list-order walk by fp32 rounding only
+ROTATE = True
 TRAFFIC_FILE = ROOT / "profiles" / "sparse_attn_c3_traffic.txt"
 
 
@@ -381,19 +389,20 @@ def main():
         kv_num, kv_idx = timer.run("route", K.route, qbar, mu, var, None, "budget", cfg.top_c,
                                    0.0, cfg.local, 0.5 * cfg.beta)
         vt = timer.run("transpose_v", K.transpose_v, v, blk)
-        out = timer.run("attention", K.sparse_attention, q, k, v, kv_num, kv_idx, blk, vt=vt)
-        return out, kv_num
+        out = timer.run("attention", K.sparse_attention, q, k, v, kv_num, kv_idx, blk, vt=vt,
+                        rotate=ROTATE)
+        return out, kv_num, vt
 
     log(f"bench: warmup {args.warmup}")
     for _ in range(args.warmup):
-        out, kv_num = step(tm)
+        out, kv_num, vt = step(tm)
     torch.cuda.synchronize()
     tm.reset()
     log(f"bench: timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out, kv_num = step(tm)
+        out, kv_num, vt = step(tm)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1000.0
@@ -407,6 +416,18 @@ def main():
     flops_causal = 4.0 * cfg.d * (blk * blk * (sum_kv - diag) + diag * blk * (blk + 1) / 2)
     summary_bytes = (cfg.Hkv + cfg.Hq) * n * cfg.d * 2 + (2 * cfg.Hkv + cfg.Hq) * cfg.nb * cfg.d * 4
     log(f"bench: {ms_step:.3f} ms/step; parts {parts}; sum kv_num {sum_kv}")
+    # the same attention call with every workgroup on the exact path (fp32-scaled scores, running
+    # max): what rows beyond the bounded path's +-32 log2-unit admission bound run at
+    te = Timer(torch)
+    qbar = K.block_summary(q, blk, "qmean")
+    mu, var, _ = K.block_summary(k, blk, "pop")
+    enum_, eidx = K.route(qbar, mu, var, None, "budget", cfg.top_c, 0.0, cfg.local, 0.5 * cfg.beta)
+    for i in range(12):
+        te.run("exact" if i >= 2 else "warm", K.sparse_attention, q, k, v, enum_, eidx, blk, vt=vt,
+               exact=True)
+    torch.cuda.synchronize()
+    exact_ms = te.mean_ms("exact")
+    del qbar, mu, var, enum_, eidx
 
     result = {
         "metric": METRIC, "value": n / (ms_step / 1e3), "unit": "tokens/s", "n_gpus": 1,
@@ -423,11 +444,18 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "sparse_attn_dma_kernel",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     # the same time with the masked upper halves of the diagonal tiles not
+                     # counted (the causal-exact FLOPs)
+                     "frac_causal_exact": flops_causal / t_attn / 1e12 / PEAK_BF16_TFLOPS,
+                     "attention_walk": "clock-rotated" if ROTATE else "list order",
                      "traffic_source": f"committed profile {TRAFFIC_FILE.name}",
                      "flops_per_launch": flops, "flops_causal_exact": flops_causal,
                      "sum_kv_num": sum_kv, "l2_hit_rate": l2_hit,
                      "gathered_kv_bytes": sum_kv * 2 * blk * cfg.d * 2},
         "breakdown_ms": parts,
+        "exact_path": {"attention_ms": exact_ms, "tflops": flops / (exact_ms / 1e3) / 1e12,
+                       "frac": flops / (exact_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS,
+                       "note": "sparse_attention(exact=True): every workgroup on the exact path"},
         "summaries_gbs": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3) / 1e9,
         "summaries": {"bytes": summary_bytes, "ms": parts["qmean"] + parts["kstats"],
                       "hbm_frac": summary_bytes / ((parts["qmean"] + parts["kstats"]) / 1e3)
@@ -473,7 +501,8 @@ def main():
         fnum, fidx = K.route(qbar, mu, var, None, "budget", None, 1.0, cfg.local, 0.5 * cfg.beta)
         vt = K.transpose_v(v, blk)
         for i in range(3):
-            sd.run("own_full" if i else "warm", K.sparse_attention, q, k, v, fnum, fidx, blk, vt=vt)
+            sd.run("own_full" if i else "warm", K.sparse_attention, q, k, v, fnum, fidx, blk, vt=vt,
+                   rotate=ROTATE)
         torch.cuda.synchronize()
         dense_ms = sd.mean_ms("sdpa")
         own_full = sd.mean_ms("own_full")
@@ -578,14 +607,16 @@ def main():
             kn5, ki5 = tmr.run("route", K.route, qb5, mu5, var5, None, "budget", c5.top_c, 0.0,
                                c5.local, 0.5 * c5.beta)
             vt5 = tmr.run("transpose_v", K.transpose_v, v5, c5.block)
-            tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block, vt=vt5)
+            tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block, vt=vt5,
+                    rotate=ROTATE)
             # the IVF router (sub-linear, approximate) on the same summaries, and the attention
             # over its lists
             idx5 = tmr.run("ivf_build", IV.build_ivf, mu5.view(1, nb5, c5.d), None, IVF_NPROBE)
             ivn, ivi = tmr.run("ivf_route", IV.search, idx5, qb5.view(1, nb5, c5.d), c5.top_c,
                                c5.local, IVF_NPROBE, 2 * c5.top_c)
             ivn4, ivi4 = ivn.view(1, 1, nb5), ivi.view(1, 1, nb5, -1)
-            tmr.run("ivf_attention", K.sparse_attention, q5, k5, v5, ivn4, ivi4, c5.block, vt=vt5)
+            tmr.run("ivf_attention", K.sparse_attention, q5, k5, v5, ivn4, ivi4, c5.block, vt=vt5,
+                    rotate=ROTATE)
         torch.cuda.synchronize()
         rows5 = np.linspace(c5.top_c, nb5 - 1, 256).astype(np.int64)
         kn_h, ki_h = kn5[0, 0].cpu().numpy(), ki5[0, 0].cpu().numpy()

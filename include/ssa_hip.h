@@ -206,11 +206,20 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
  * the workspace (ssa_sparse_attn_workspace_size() bytes). flags = 0: the call first writes V^T
  * there itself; flags = SSA_ATTN_VT_READY: the workspace already holds V^T of this v (from
  * ssa_transpose_v), e.g. kept resident across calls. After V^T the workspace holds per-call state
- * (d = 64: the largest squared key norm of every 64-key tile, one flag per (b, kv head)),
- * rewritten by every call, so calls sharing one workspace must not overlap. The fp32 path needs
- * no workspace.
+ * (d = 64: for bf16 an fp16 copy of K, the largest squared key norm of every 64-key tile, one
+ * flag per (b, kv head) and per (b, kv head, query block)), rewritten by every call, so calls
+ * sharing one workspace must not overlap. The fp32 path needs no workspace.
+ * Summation order: every query block walks its key blocks in list order (bit-reproducible
+ * output). flags |= SSA_ATTN_ROTATE (16-bit, d = 64, lists of at most 128 entries): each
+ * workgroup starts its walk at a position taken from the GPU clock, so workgroups resident
+ * together read the same key blocks at the same time (more L2 hits); outputs then differ between
+ * calls by the rounding of the fp32 accumulation.
+ * Softmax path (16-bit, d = 64): workgroups whose rows provably keep every score within +-32
+ * (log2 units) take the bounded-row path (no running max; q*scale*log2e rounded to fp16 for the
+ * QK product), the others the exact path (fp32 scores scaled in fp32, running max).
+ * flags |= SSA_ATTN_EXACT sends every workgroup to the exact path.
  */
-enum { SSA_ATTN_VT_READY = 1 };
+enum { SSA_ATTN_VT_READY = 1, SSA_ATTN_ROTATE = 2, SSA_ATTN_EXACT = 4 };
 size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,
                                       int64_t block);
 int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,

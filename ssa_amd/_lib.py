@@ -21,6 +21,8 @@ F32, F16, BF16 = 0, 1, 2
 STATS_POP, STATS_UNBIASED, STATS_QMEAN = 0, 1, 2
 ROUTE_BUDGET, ROUTE_FLAT, ROUTE_QUERY, ROUTE_STARTED = 0, 1, 2, 3
 ATTN_VT_READY = 1
+ATTN_ROTATE = 2
+ATTN_EXACT = 4
 MASKED_MASKS_READY = 1
 DECODE_STATIC_SCRATCH_BYTES = 16 << 20  # SSA_DECODE_STATIC_SCRATCH_BYTES
 

@@ -56,6 +56,12 @@ constexpr float kRescaleSlack = 8.0f;
 constexpr float kFastBoundBf16 = 32.0f;
 constexpr float kFastBoundF16 = 32.0f;
 constexpr float kKeyNormLimit = 4096.0f;
+// Step of the clock-rotated list walk (bounded launch, lists of <= 128 entries): roughly the time
+// a workgroup spends on one K / V^T sub-tile with the device full, measured at C3 (4 waves x 32
+// rows, 128-row workgroups: best at 1.5-2 us) and C5 (8 waves x 32 rows: 2-3 us); in
+// s_memrealtime ticks (100 MHz).
+constexpr int64_t kRotTicks128 = 200;
+constexpr int64_t kRotTicks256 = 250;
 template <int DT>
 __device__ constexpr float fast_bound() {
   return DT == SSA_F16 ? kFastBoundF16 : kFastBoundBf16;
@@ -83,8 +89,12 @@ struct AttnParams {
   int64_t ntile;       // 64-key tiles per key head (n_pad / 64)
   int* unbounded;      // per (b, kv head): set by mode 1 when one of its workgroups is not bounded
                        // (or, fp16, overflowed)
-  int* redo;           // per (b, kv head, query block): set by mode 1 (fp16) when a row of a
-                       // workgroup of it overflowed; the exact launch then redoes the query block
+  int64_t rot_ticks;   // bounded launch, lists of <= 128 entries: s_memrealtime ticks per sub-tile
+                       // step of the clock-rotated list walk (0: every walk starts at entry 0)
+  bool rotate;         // host: rotate the walks (SSA_ATTN_ROTATE)
+  int* redo;           // per (b, kv head, query block): set by mode 1 when a workgroup of the
+                       // query block is not bounded or (fp16) a row of it overflowed; the exact
+                       // launch then redoes the query block for every query head of the key head
   int64_t qsub;   // query sub-tiles per query block
   int64_t total;  // logical workgroups
   int64_t group;  // logical workgroups placed together on one XCD
@@ -281,6 +291,15 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const char* __restrict
   }
 }
 
+// Workgroup barrier once this wave's LDS DMA (global_load_lds) has landed. __syncthreads() is not
+// enough: its workgroup-scope release fence waits for LDS and store traffic (lgkmcnt) only, not
+// for the loads that write LDS asynchronously (vmcnt) -- the compiler's own tracking of them
+// inserted the vmcnt(0) in some builds of the tile loop and not in others. The "memory" clobber
+// keeps the compiler from moving LDS or global accesses across it.
+__device__ inline void dma_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Max / sum of a value with its partner lane (lane ^ 32) without an LDS round trip:
 // permlane32_swap(x, x) returns {x of lanes 0-31 (both halves), x of lanes 32-63 (both halves)}.
 __device__ inline float pair_max(float x) {
@@ -413,7 +432,7 @@ __device__ inline int swz(int r) {
 // MODE 0: every workgroup, exact online softmax. MODE 1: only workgroups whose rows are all
 // bounded (P = 2^S without a running max). MODE 2: only the others, exact. Modes 1 and 2 are
 // launched back to back and together cover every workgroup (head dim 64 only).
-template <int DT, int NW, int CG, int WPE, int MODE, int D = 64, int KT = 64>
+template <int DT, int NW, int CG, int WPE, int MODE, int D = 64, int KT = 64, bool REG = false>
 __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParams p) {
   using M = Mfma<DT>;
   typedef typename M::vec vec;
@@ -451,8 +470,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   L /= p.B;
   const int64_t i = p.nbq - 1 - L;
   const int64_t h = kvh * p.G + hg;
-  if constexpr (MODE == 2)
-    if (p.unbounded[b * p.Hkv + kvh] == 0) return;  // mode 1 ran every workgroup of this head
+  if constexpr (MODE == 2) {
+    // mode 1 completed every query block of this head, or this one
+    if (p.unbounded[b * p.Hkv + kvh] == 0) return;
+    if (p.redo[(b * p.Hkv + kvh) * p.nbq + i] == 0) return;
+  }
 
   const int64_t q0 = i * p.block + qs * ROWS;
   if (q0 >= p.n) return;
@@ -503,8 +525,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   // MFMA output; numerator and denominator share the implicit max 0.
   constexpr bool fast = MODE == 1;
   constexpr bool OFS = fast && DT == SSA_F16;  // fp16 bounded rows: scores offset by m0 (above)
-  if constexpr (MODE != 0) {
-    __shared__ int wg_bounded;
+  int e0 = 0;  // first list entry walked (REG: rotated by the clock, below)
+  if constexpr (MODE == 1) {
+    __shared__ int wg_bounded, wg_e0;
     // largest squared key norm over the tiles this workgroup attends (its list's blocks, tiles
     // starting at or before its last query row)
     float km2 = 0.0f;
@@ -536,20 +559,31 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       ok = ok && (p.scale_log2 * qn * sqrtf(km2) < fast_bound<DT>()) &&
            (sqrtf(km2) < kKeyNormLimit) && (p.scale_log2 * qn < 1.0e4f);
     }
-    if (tid == 0) wg_bounded = 1;
+    if (tid == 0) {
+      wg_bounded = 1;
+      int e = 0;
+      if (REG && p.rot_ticks > 0 && cnt > 0) {
+        // the walk starts at the list position the clock points to: with a period of cnt*S*rot
+        // ticks (rot ~ one sub-tile step), workgroups resident together read the same part of
+        // their (ascending) lists at the same time, wherever they started, so the key blocks
+        // they share are fetched once into L2 / MALL for all of them
+        const uint64_t per = (uint64_t)cnt * (uint64_t)S * (uint64_t)p.rot_ticks;
+        e = (int)((__builtin_amdgcn_s_memrealtime() % per) / ((uint64_t)S * (uint64_t)p.rot_ticks));
+      }
+      wg_e0 = e;
+    }
     __syncthreads();
     if (!__all(ok) && lane == 0) wg_bounded = 0;
     __syncthreads();
-    const bool bounded = wg_bounded != 0;
-    if constexpr (fast) {
-      if (!bounded) {  // the exact launch takes this workgroup
-        if (tid == 0) p.unbounded[b * p.Hkv + kvh] = 1;
-        return;
+    e0 = wg_e0;
+    if (wg_bounded == 0) {  // the exact launch takes this query block
+      if (tid == 0) {
+        p.redo[(b * p.Hkv + kvh) * p.nbq + i] = 1;
+        p.unbounded[b * p.Hkv + kvh] = 1;
       }
-    } else if (bounded && (DT != SSA_F16 || p.redo[(b * p.Hkv + kvh) * p.nbq + i] == 0)) {
-      return;  // the bounded launch completed this workgroup
+      return;
     }
-    if constexpr (fast) {
+    {
 #pragma unroll
       for (int c = 0; c < CG; ++c)
 #pragma unroll
@@ -590,21 +624,36 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   const int n32 = (int)p.n, blk32 = (int)p.block, nbq32 = (int)p.nbq, qmax32 = (int)qmax;
   int lbase = 0;
   int32_t lreg = lane < cnt ? list[lane] : -1;
-  int ce = 0, cs = -1;
+  // REG (the host launches it for lists of at most 128 entries): entries 64..127 in a second
+  // register, no reload, so the walk can start anywhere in the list and wrap around
+  int32_t lreg1 = -1;
+  if constexpr (REG) lreg1 = 64 + lane < cnt ? list[64 + lane] : -1;
+  int ce = e0, cs = -1, kk = 0;  // kk: entries walked (REG: entry ce = e0 + kk mod cnt)
   // advances the cursor to the next tile that starts at or before the last query row and before
   // n; returns its first key, or -1 past the list
   auto next_tile = [&]() -> int {
     while (true) {
-      if (++cs == S) {
-        cs = 0;
-        ++ce;
+      int c;
+      if constexpr (REG) {
+        if (++cs == S) {
+          cs = 0;
+          ++kk;
+          if (++ce == cnt) ce = 0;
+        }
+        if (kk >= cnt) return -1;
+        c = ce < 64 ? __builtin_amdgcn_readlane(lreg, ce) : __builtin_amdgcn_readlane(lreg1, ce - 64);
+      } else {
+        if (++cs == S) {
+          cs = 0;
+          ++ce;
+        }
+        if (ce >= cnt) return -1;
+        if (ce - lbase >= 64) {  // wave-uniform; once per 64 list entries
+          lbase = ce;
+          lreg = ce + lane < cnt ? list[ce + lane] : -1;
+        }
+        c = __builtin_amdgcn_readlane(lreg, ce - lbase);
       }
-      if (ce >= cnt) return -1;
-      if (ce - lbase >= 64) {  // wave-uniform; once per 64 list entries
-        lbase = ce;
-        lreg = ce + lane < cnt ? list[ce + lane] : -1;
-      }
-      const int c = __builtin_amdgcn_readlane(lreg, ce - lbase);
       if (c >= 0 && c < nbq32) {
         const int k0 = c * blk32 + cs * KT;
         if (k0 <= qmax32 && k0 < n32) return k0;
@@ -827,13 +876,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   if (key0 >= 0) issue(kst0, vst0, key0);
   while (key0 >= 0) {
     int key0n = next_tile();
-    __syncthreads();  // stage 0 landed for all waves; stage 1 no longer read
+    dma_barrier();  // stage 0 landed for all waves; stage 1 no longer read
     if (key0n >= 0) issue(kst1, vst1, key0n);
     if (key0 <= wlast) compute(kst0, vst0, key0);
     key0 = key0n;
     if (key0 < 0) break;
     key0n = next_tile();
-    __syncthreads();  // stage 1 landed; stage 0 no longer read
+    dma_barrier();  // stage 1 landed; stage 0 no longer read
     if (key0n >= 0) issue(kst0, vst0, key0n);
     if (key0 <= wlast) compute(kst1, vst1, key0);
     key0 = key0n;
@@ -877,16 +926,25 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   }
 }
 
-template <int DT>
-int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
-  // head dim 64: 2 waves x 32 rows per workgroup for block 64 (one query block), otherwise
-  // 128-row workgroups (bounded rows 4 waves x 32, exact 2 waves x 64); head dims 128 / 256
-  // (exact path): 2 or 4 waves x 32 rows
-  const bool b64 = p.block == 64;
-  p.qsub = b64 ? 1 : p.block / 128;
+// Logical work items of a launch whose workgroups own `rows` query rows (a divisor of the block,
+// or the whole block 64): query sub-tiles per query block, the run of items placed together on
+// one XCD (the query heads of a key head for one query block), and the grid (a multiple of 8
+// runs, so every XCD receives whole runs).
+inline int64_t set_rows(AttnParams& p, int64_t rows) {
+  p.qsub = p.block == 64 ? 1 : p.block / rows;
   p.group = p.G * p.qsub;
   p.total = p.nbq * p.B * p.Hkv * p.G * p.qsub;
-  const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+  return (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+}
+
+template <int DT>
+int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
+  // head dim 64: 2 waves x 32 rows per workgroup for block 64 (one query block); otherwise the
+  // bounded launch runs 4 waves x 32 rows (block 128) or 8 waves x 32 rows (a multiple of 256:
+  // a whole 256-row query block, so each K / V^T sub-tile is read once per query block) and the
+  // exact launch 2 waves x 64 rows; head dims 128 / 256 (exact path): 2 or 4 waves x 32 rows
+  const bool b64 = p.block == 64;
+  int64_t grid = set_rows(p, 128);
   SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
   if (d == 128) {
     if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0, 128, 64><<<(unsigned)grid, 128, 0, stream>>>(p);
@@ -901,11 +959,24 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
     sparse_attn_dma_kernel<DT, 2, 1, 2, 1><<<(unsigned)grid, 128, 0, stream>>>(p);
     sparse_attn_dma_kernel<DT, 2, 1, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
   } else {
-    // bounded rows: 4 waves x 32 rows, 4 waves per SIMD (one score-fragment set per wave in 128
-    // VGPRs: 4-6 % faster at C3 than 2 waves x 64 rows, the same at C5); the exact path keeps 2
-    // waves x 64 rows (1 % faster there; same 128-row workgroups, so the two launches partition
-    // the same logical items)
-    sparse_attn_dma_kernel<DT, 4, 1, 4, 1><<<(unsigned)grid, 256, 0, stream>>>(p);
+    // bounded rows: 32 rows per wave, 4 waves per SIMD (one score-fragment set per wave in 128
+    // VGPRs: 4-6 % faster at C3 than 2 waves x 64 rows); the exact launch keeps 2 waves x 64
+    // rows (1 % faster there) and redoes the query blocks the bounded launch flagged
+    if (p.block % 256 == 0) {
+      const int64_t g1 = set_rows(p, 256);
+      SSA_REQUIRE(g1 < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+      p.rot_ticks = p.rotate ? kRotTicks256 : 0;
+      if (p.W <= 128)
+        sparse_attn_dma_kernel<DT, 8, 1, 4, 1, 64, 64, true><<<(unsigned)g1, 512, 0, stream>>>(p);
+      else
+        sparse_attn_dma_kernel<DT, 8, 1, 4, 1><<<(unsigned)g1, 512, 0, stream>>>(p);
+    } else if (p.W <= 128) {
+      p.rot_ticks = p.rotate ? kRotTicks128 : 0;
+      sparse_attn_dma_kernel<DT, 4, 1, 4, 1, 64, 64, true><<<(unsigned)grid, 256, 0, stream>>>(p);
+    } else {
+      sparse_attn_dma_kernel<DT, 4, 1, 4, 1><<<(unsigned)grid, 256, 0, stream>>>(p);
+    }
+    grid = set_rows(p, 128);
     sparse_attn_dma_kernel<DT, 2, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
   }
   return launch_status("sparse_attn_dma_kernel");
@@ -985,7 +1056,9 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(B * Hq < (1ll << 24), SSA_ERR_UNSUPPORTED, "sparse_attn: too many heads");
   SSA_REQUIRE(n + block < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "sparse_attn: n = %lld too large (key positions are 32-bit)", (long long)n);
-  SSA_REQUIRE((flags & ~SSA_ATTN_VT_READY) == 0, SSA_ERR_INVALID, "sparse_attn: unknown flags");
+  SSA_REQUIRE((flags & ~(SSA_ATTN_VT_READY | SSA_ATTN_ROTATE | SSA_ATTN_EXACT)) == 0,
+              SSA_ERR_INVALID,
+              "sparse_attn: unknown flags");
   const int64_t vec = dtype == SSA_F32 ? 4 : 8;
   for (int s = 0; s < 12; ++s)
     SSA_REQUIRE(strides[s] % vec == 0, SSA_ERR_UNSUPPORTED,
@@ -1016,6 +1089,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   p.unbounded = nullptr;
   p.redo = nullptr;
   p.k16 = nullptr;
+  p.rot_ticks = 0;
+  p.rotate = (flags & SSA_ATTN_ROTATE) != 0;
   p.ntile = p.n_pad / 64;
   if (dtype == SSA_F32) {
     p.vt = nullptr;
@@ -1043,7 +1118,7 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   int* redo = unbounded + B * Hkv;
   KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
              unbounded, p.ntile, redo, block, p.nbq, k16, p.n_pad};
-  if (d != 64) {  // exact path only: V^T (unless supplied), no key norms
+  if (d != 64 || (flags & SSA_ATTN_EXACT)) {  // exact path only: V^T (unless supplied), no key norms
     if (!(flags & SSA_ATTN_VT_READY)) {
       KeyNorm none{};
       const dim3 tz((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv), (unsigned)(d / 64));

@@ -198,7 +198,7 @@ def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
 def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: torch.Tensor,
                      kv_idx: torch.Tensor, block: int, scale: float | None = None,
                      out: torch.Tensor | None = None, return_lse: bool = False,
-                     vt: torch.Tensor | None = None):
+                     vt: torch.Tensor | None = None, rotate: bool = False, exact: bool = False):
     """Block-sparse causal attention on the compact contract (replaces FlexAttention with
     BlockMask.from_kv_blocks + mask_mod kv<=q & kv<n; ssa/ssa_kernel.py:125-126,
     ssa/gemma_ssa.py:159-162,179).
@@ -206,6 +206,14 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
     q (B, Hq, n, d); k, v (B, Hkv, n, d); kv_num (B, Hq, nb); kv_idx (B, Hq, nb, W).
     `out` may be any (B, Hq, n, d) view with a contiguous last dim (e.g. a transpose of a
     (B, n, Hq, d) buffer). `vt` is an optional V^T from transpose_v(v, block).
+    Every query block walks its key blocks in list order (bit-identical outputs across calls).
+    `rotate` (16-bit, head dim 64, lists of <= 128 entries; ignored under
+    torch.use_deterministic_algorithms(True)): each workgroup starts its walk at a position taken
+    from the GPU clock, so workgroups resident together read the same key blocks at the same
+    time -- more L2 hits, outputs that vary between calls by fp32 rounding.
+    `exact`: every row takes the exact running-max softmax on fp32-scaled scores (by default rows
+    whose scores provably stay within +-32 log2 units take the bounded-row path, which rounds
+    q*scale*log2e to fp16 for the QK product).
     Returns out (and lse (B, Hq, n) fp32 if requested).
     """
     if torch.compiler.is_compiling():  # V^T is rebuilt inside the op (vt is a cache only)
@@ -219,11 +227,12 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
             out.copy_(o)
             o = out
         return (o, lse) if return_lse else o
-    return _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale, out, return_lse, vt)
+    return _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale, out, return_lse, vt,
+                                  rotate, exact)
 
 
 def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
-                           return_lse=False, vt=None):
+                           return_lse=False, vt=None, rotate=False, exact=False):
     _lib.require_device(q, k, v, kv_num, kv_idx)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share a dtype")
@@ -262,6 +271,10 @@ def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
         ws, flags = vt, _lib.ATTN_VT_READY
     else:
         ws = torch.empty(max(ws_bytes, 16), device=q.device, dtype=torch.uint8)
+    if rotate and not torch.are_deterministic_algorithms_enabled():
+        flags |= _lib.ATTN_ROTATE
+    if exact:
+        flags |= _lib.ATTN_EXACT
     strides = _lib.i64_array([*_bhn_strides(q), *_bhn_strides(k), *_bhn_strides(v),
                               *_bhn_strides(out)])
     _lib.call("ssa_sparse_attn_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt,

@@ -419,6 +419,47 @@ def test_c3_shape_rows_near_the_bound(cuda, seed):
     assert err < TOL[cfg.dtype], err
 
 
+@pytest.mark.parametrize("dtype,block", [(torch.bfloat16, 128), (torch.float16, 256)])
+def test_rotated_walk_and_exact_flag(cuda, dtype, block):
+    """rotate=True: each bounded-row workgroup starts its walk over its key blocks at a position
+    taken from the GPU clock (lists of <= 128 entries), so the summation order, and the output's
+    last bits, vary between calls; the default walks in list order and repeats bit for bit, as
+    does rotate=True under torch.use_deterministic_algorithms(True). Every output -- and that of
+    exact=True, which sends every workgroup to the exact path -- within 2e-2 of the oracle on
+    sampled blocks, rotated within 4e-3 of the list-order output."""
+    rng = np.random.default_rng(77)
+    n, hq, hkv = 16384, 4, 2
+    q, k, v = (WL.round_to(rng.standard_normal((1, h_, n, 64)).astype(np.float32), dtype)
+               for h_ in (hq, hkv, hkv))
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    kv_num, kv_idx, _ = K.block_route_budget(qt, kt, block, top_c=32, local=1, beta=2.0,
+                                             compact=True)
+    det = [K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block) for _ in range(2)]
+    rot = [K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, rotate=True) for _ in range(3)]
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        det.append(K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, rotate=True))
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    assert torch.equal(det[0], det[1]) and torch.equal(det[0], det[2])
+    spread = max(float((r.float() - det[0].float()).abs().max()) for r in rot)
+    print(f"{dtype} block {block}: rotated vs list-order walk max |diff| {spread:.3g}")
+    assert spread < 4e-3, spread
+    # exact=True: every workgroup on the exact (running-max, fp32-scaled) path
+    ex = K.sparse_attention(qt, kt, vt, kv_num, kv_idx, block, exact=True)
+    rot.append(ex)
+    qblocks = [0, 1, n // block // 2, n // block - 1]
+    ref = O.sparse_attention(q, k, v, kv_num.cpu().numpy(), kv_idx.cpu().numpy(), block,
+                             qblocks=qblocks, heads=[0, 3])
+    for o in det[:1] + rot:
+        oo = np_of(o)
+        for h in (0, 3):
+            for i in qblocks:
+                sl = slice(i * block, (i + 1) * block)
+                assert np.abs(oo[0, h, sl] - ref[0, h, sl]).max() < TOL[dtype]
+
+
 def two_key_case(dtype, target, rounding, seed=0, n=2048, block=128, amp=1.0, scale=0.125):
     """A case built against the bounded-row path's one approximation, the rounding of
     q*scale*log2e before the QK product. Query block i (i >= 1) repeats one query row q_i with
@@ -480,7 +521,7 @@ def test_bounded_rows_constructive_rounding(cuda, dtype, target, rounding):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("block", [64, 128])
+@pytest.mark.parametrize("block", [64, 128, 256])
 def test_unbounded_rows_take_the_exact_path(cuda, dtype, block):
     """Query blocks whose |q| max|k| bound exceeds the fp32-safe range (every other block scaled
     by 40: scaled logits up to ~500) run the exact running-max softmax, the others the bounded
@@ -549,7 +590,7 @@ def test_rows_near_the_fast_path_bound(cuda, dtype, target, aligned):
     assert np.abs(np_of(out) - ref).max() < TOL[dtype]
 
 
-@pytest.mark.parametrize("block", [64, 128])
+@pytest.mark.parametrize("block", [64, 128, 256])
 def test_fp16_bounded_rows_overflow_redone_exactly(cuda, block):
     """fp16 bounded rows take P = 2^(S - m0) with m0 the largest score of the row's first
     sub-tile. Here every query leans on one direction u and a needle key along u sits in key
@@ -558,7 +599,7 @@ def test_fp16_bounded_rows_overflow_redone_exactly(cuda, block):
     the query blocks that attend block 5 must be redone by the exact launch. Every row within
     2e-2 of the float64 oracle, the output finite."""
     rng = np.random.default_rng(41)
-    n, scale = 1024, 0.125
+    n, scale = max(1024, 8 * block), 0.125
     u = rng.standard_normal(64).astype(np.float32)
     u /= np.linalg.norm(u)
     q = (0.1 * rng.standard_normal((1, 2, n, 64)) + u).astype(np.float32)
