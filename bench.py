@@ -259,45 +259,92 @@ def cpu_threads(torch):
     return torch.get_num_threads()
 
 
-def cpu_baseline(p, dec):
+def _runs(fn, runs):
+    """Wall-clock seconds of `runs` calls of fn."""
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return ts
+
+
+def _med_iqr(ts):
+    """{median_s, iqr_s, runs} of a list of run times."""
+    import numpy as np
+    q1, med, q3 = np.percentile(np.asarray(ts, dtype=np.float64), [25, 50, 75])
+    return {"median_s": float(med), "iqr_s": float(q3 - q1), "runs": len(ts)}
+
+
+def _cpu_prefill_full(C, torch, p, runs):
+    """Router + block-sparse softmax of every (head, query block) pair of a config, on the host.
+    Returns (run times, kv_num)."""
+    cfg = p["cfg"]
+    dt = torch.float32 if cfg.dtype == torch.float32 else torch.bfloat16
+    q, k, v = (torch.from_numpy(p[x]).to(dt) for x in ("q", "k", "v"))
+    pairs = [(h, i) for h in range(cfg.Hq) for i in range(cfg.nb)]
+    res = {}
+
+    def once():
+        kv_num, kv_idx, _ = C.route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
+                                           beta=cfg.beta)
+        C.attend_blocks(q, k, v, kv_num, kv_idx, cfg.block, pairs)
+        res["kv_num"] = kv_num
+    return _runs(once, runs), res["kv_num"]
+
+
+def cpu_baseline(p, dec, c5=None):
     """The reference's path restated in torch float32 on this host's cores (oracle/cpu_path.py;
     ssa/ssa_kernel.py:61-119 and the FlexAttention softmax, ssa/ivf_decode.py:49-62 with the
-    router of ssa/gemma_ssa.py:99-131): the C3 router in full (median of 3 runs), attention over a
-    stratified sample of (query head, query block) pairs extrapolated by sum(kv_num), and C4
-    decode steps over the full 1,048,576-token cache (median step time of 3 runs of 8 steps)."""
+    router of ssa/gemma_ssa.py:99-131), each part as the median and inter-quartile range of
+    repeated runs:
+      c1, c2  router + attention in full (5 and 3 runs);
+      c3      the router in full and attention over a stratified sample of (query head, query
+              block) pairs (every query block once, heads in turn), extrapolated by sum(kv_num)
+              (3 runs each) -- the headline `value`;
+      c4      decode steps over the full 1,048,576-token cache (3 runs of 8 steps);
+      c5      (from the C5 arm) the router over a prefix of the query blocks, extrapolated by the
+              square of the block count (its score matrix and top-k grow with nb^2), and
+              attention over 32 evenly spaced query blocks, extrapolated by sum(kv_num)."""
     import torch
 
     from oracle import cpu_path as C
+    from ssa_amd import workloads as WL
     threads = cpu_threads(torch)
     cfg = p["cfg"]
     q, k, v = (torch.from_numpy(p[x]).to(torch.bfloat16) for x in ("q", "k", "v"))
-    routes = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        kv_num, kv_idx, _ = C.route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local,
-                                           beta=cfg.beta)
-        routes.append(time.perf_counter() - t0)
-    t_route = sorted(routes)[1]
+    res = {}
+
+    def route():
+        res["r"] = C.route_budget(q, k, cfg.block, top_c=cfg.top_c, local=cfg.local, beta=cfg.beta)
+    t_route = _runs(route, 3)
+    kv_num, kv_idx, _ = res["r"]
     nb = cfg.nb
     pairs = [(i % cfg.Hq, i) for i in range(nb)]  # every query block once, heads in turn
     sample_kv = sum(int(kv_num[0, h, i]) for h, i in pairs)
     total_kv = int(kv_num.sum())
-    samples = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        C.attend_blocks(q, k, v, kv_num, kv_idx, cfg.block, pairs)
-        samples.append(time.perf_counter() - t0)
-    t_sample = sorted(samples)[1]
-    t_attn = t_sample * total_kv / sample_kv
-    t_total = t_route + t_attn
+    t_sample = _runs(lambda: C.attend_blocks(q, k, v, kv_num, kv_idx, cfg.block, pairs), 3)
+    route_s, sample_s = _med_iqr(t_route), _med_iqr(t_sample)
+    t_attn = sample_s["median_s"] * total_kv / sample_kv
+    t_total = route_s["median_s"] + t_attn
     out = {
         "value": cfg.n / t_total, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": (f"torch fp32 host restatement (oracle/cpu_path.py): router over all "
+        "sample": (f"C3: torch fp32 host restatement (oracle/cpu_path.py): router over all "
                    f"{cfg.Hq * nb} rows + softmax on {len(pairs)} (head, q-block) pairs "
-                   f"({100.0 * sample_kv / total_kv:.2f} % of tiles), scaled by sum(kv_num)"),
-        "c3_router_s": t_route, "c3_attention_s_extrapolated": t_attn,
-        "c3_attention_sample_fraction": sample_kv / total_kv,
+                   f"({100.0 * sample_kv / total_kv:.2f} % of tiles), scaled by sum(kv_num); "
+                   f"medians of 3 runs"),
+        "c3": {"router": route_s, "attention_sample": sample_s,
+               "attention_s_extrapolated": t_attn, "sample_fraction": sample_kv / total_kv,
+               "tokens_per_s": cfg.n / t_total},
     }
+    del q, k, v, res
+    for name, runs in (("C1", 5), ("C2", 3)):
+        pc = WL.make(name)
+        ts, _ = _cpu_prefill_full(C, torch, pc, runs)
+        st = _med_iqr(ts)
+        out[name.lower()] = dict(st, workload=f"{name} router + attention in full",
+                                 tokens_per_s=pc["cfg"].n / st["median_s"])
+        del pc
     if dec is not None:
         c4 = dec["cfg"]
         n0 = dec["n_cache"]
@@ -308,16 +355,52 @@ def cpu_baseline(p, dec):
         kb = kc[:, :ncomp * c4.block].float().reshape(c4.Hkv, ncomp, c4.block, c4.d)
         mu, var = kb.mean(2), kb.var(2, unbiased=False)  # resident summaries (not timed)
         del kb
-        runs = []
-        for _ in range(3):
-            t0 = time.perf_counter()
+
+        def steps8():
             for t in range(8):
                 C.decode_step(qd[:, t], kc, vc, mu, var, n0 + t, c4.block, c4.top_c, c4.local,
                               c4.beta)
-            runs.append((time.perf_counter() - t0) / 8)
-        out["c4_decode_ms_per_step"] = sorted(runs)[1] * 1000.0
-        out["c4_sample"] = f"{c4.Hq} heads, {n0}-token cache, median of 3 runs of 8 steps"
+        st = _med_iqr([x / 8 for x in _runs(steps8, 3)])
+        out["c4"] = {"ms_per_step": st["median_s"] * 1e3, "iqr_ms": st["iqr_s"] * 1e3,
+                     "runs": st["runs"],
+                     "workload": f"{c4.Hq} heads, {n0}-token cache, 3 runs of 8 steps"}
+    if c5 is not None:
+        out["c5"] = c5
     return out
+
+
+def cpu_baseline_c5(torch, c5, q5, k5, v5, kn5, ki5, prefix_blocks=4096, sample_blocks=32):
+    """C5 on the host (see cpu_baseline): router over the first `prefix_blocks` query blocks
+    (their causal past is inside the prefix) and attention over `sample_blocks` evenly spaced
+    query blocks with the device router's lists, each extrapolated and labelled so."""
+    import numpy as np
+
+    from oracle import cpu_path as C
+    cpu_threads(torch)
+    nb = c5.n // c5.block
+    npre = prefix_blocks * c5.block
+    qp = q5[:, :, :npre].cpu()
+    kp = k5[:, :, :npre].cpu()
+    t_route = _med_iqr(_runs(lambda: C.route_budget(qp, kp, c5.block, top_c=c5.top_c,
+                                                    local=c5.local, beta=c5.beta), 3))
+    del qp, kp
+    qh, kh, vh = q5.cpu(), k5.cpu(), v5.cpu()
+    num, idx = kn5.cpu(), ki5.cpu()
+    rows = np.linspace(0, nb - 1, sample_blocks).astype(np.int64).tolist()
+    pairs = [(0, i) for i in rows]
+    sample_kv = sum(int(num[0, 0, i]) for i in rows)
+    total_kv = int(num.sum())
+    t_attn = _med_iqr(_runs(lambda: C.attend_blocks(qh, kh, vh, num, idx, c5.block, pairs), 3))
+    del qh, kh, vh
+    route_x = t_route["median_s"] * (nb / prefix_blocks) ** 2
+    attn_x = t_attn["median_s"] * total_kv / sample_kv
+    return {"router_prefix": t_route, "router_s_extrapolated": route_x,
+            "attention_sample": t_attn, "attention_s_extrapolated": attn_x,
+            "tokens_per_s": c5.n / (route_x + attn_x),
+            "sample": (f"router over the first {prefix_blocks} of {nb} query blocks, scaled by "
+                       f"({nb}/{prefix_blocks})^2; attention over {sample_blocks} evenly spaced "
+                       f"query blocks ({100.0 * sample_kv / total_kv:.3f} % of tiles), scaled by "
+                       f"sum(kv_num); medians of 3 runs")}
 
 
 def swap_bench(torch, dev):
@@ -519,6 +602,7 @@ def main():
         del kr, vr
 
     dec_host = None
+    c5_cpu = None
     if not args.no_decode:
         log("bench: C4 decode")
         ds = WL.make_decode(steps=args.decode_steps + 8)
@@ -652,6 +736,9 @@ def main():
                 "jaccard_vs_flat_256_rows": float(np.mean(jac5)),
             },
         }
+        if not args.no_cpu:
+            log("bench: C5 CPU baseline (router prefix, attention sample)")
+            c5_cpu = cpu_baseline_c5(torch, c5, q5, k5, v5, kn5, ki5)
         del q5, k5, v5, d5, vt5, idx5
         torch.cuda.empty_cache()
 
@@ -673,7 +760,7 @@ def main():
 
     if not args.no_cpu:
         log("bench: CPU baseline (torch float32 restatement of the reference path)")
-        result["cpu_baseline"] = cpu_baseline(p, dec_host)
+        result["cpu_baseline"] = cpu_baseline(p, dec_host, c5_cpu)
         try:
             model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
                          if l.startswith("model name"))

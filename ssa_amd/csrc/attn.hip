@@ -942,7 +942,7 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
   // head dim 64: 2 waves x 32 rows per workgroup for block 64 (one query block); otherwise the
   // bounded launch runs 4 waves x 32 rows (block 128) or 8 waves x 32 rows (a multiple of 256:
   // a whole 256-row query block, so each K / V^T sub-tile is read once per query block) and the
-  // exact launch 2 waves x 64 rows; head dims 128 / 256 (exact path): 2 or 4 waves x 32 rows
+  // exact launch 4 waves x 32 rows; head dims 128 / 256 (exact path): 2 or 4 waves x 32 rows
   const bool b64 = p.block == 64;
   int64_t grid = set_rows(p, 128);
   SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
@@ -954,14 +954,14 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
     else sparse_attn_dma_kernel<DT, 4, 1, 1, 0, 256, 32><<<(unsigned)grid, 256, 0, stream>>>(p);
   } else if (p.tmax2 == nullptr) {
     if (b64) sparse_attn_dma_kernel<DT, 2, 1, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
-    else sparse_attn_dma_kernel<DT, 2, 2, 2, 0><<<(unsigned)grid, 128, 0, stream>>>(p);
+    else sparse_attn_dma_kernel<DT, 4, 1, 4, 0><<<(unsigned)grid, 256, 0, stream>>>(p);
   } else if (b64) {
     sparse_attn_dma_kernel<DT, 2, 1, 2, 1><<<(unsigned)grid, 128, 0, stream>>>(p);
     sparse_attn_dma_kernel<DT, 2, 1, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
   } else {
-    // bounded rows: 32 rows per wave, 4 waves per SIMD (one score-fragment set per wave in 128
-    // VGPRs: 4-6 % faster at C3 than 2 waves x 64 rows); the exact launch keeps 2 waves x 64
-    // rows (1 % faster there) and redoes the query blocks the bounded launch flagged
+    // 32 rows per wave, 4 waves per SIMD (one score-fragment set per wave in 128 VGPRs: at C3
+    // 4-6 % faster than 2 waves x 64 rows for the bounded rows, 2-3 % for the exact path); the
+    // exact launch redoes the query blocks the bounded launch flagged
     if (p.block % 256 == 0) {
       const int64_t g1 = set_rows(p, 256);
       SSA_REQUIRE(g1 < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
@@ -977,7 +977,7 @@ int launch_mfma(AttnParams& p, int64_t d, hipStream_t stream) {
       sparse_attn_dma_kernel<DT, 4, 1, 4, 1><<<(unsigned)grid, 256, 0, stream>>>(p);
     }
     grid = set_rows(p, 128);
-    sparse_attn_dma_kernel<DT, 2, 2, 2, 2><<<(unsigned)grid, 128, 0, stream>>>(p);
+    sparse_attn_dma_kernel<DT, 4, 1, 4, 2><<<(unsigned)grid, 256, 0, stream>>>(p);
   }
   return launch_status("sparse_attn_dma_kernel");
 }

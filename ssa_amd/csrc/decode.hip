@@ -1065,14 +1065,14 @@ __device__ inline void attend_group(const FusedStep& f, const DecodeParams& p, i
                      load_elem<DT>(p.v_new, b * p.vnb + kvh * p.vnh + e));
     }
   }
-  // every wave's stores complete before the workgroup arrives
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // The workgroup's partial stores happen before its arrival (the barrier), and the arrival
+  // releases them at agent scope; the row's last workgroup acquires every other workgroup's
+  // released stores with its own arrival (acq_rel: release and acquire edges of the HIP memory
+  // model, not an ordering of this ISA's memory pipeline).
   __syncthreads();
   if (tid == 0) {
     const unsigned int old =
-        __hip_atomic_fetch_add(&f.arrive[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&f.arrive[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     sh_last = old == (unsigned int)(f.ngroups - 1) ? 1u : 0u;
   }
   __syncthreads();

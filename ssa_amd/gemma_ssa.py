@@ -56,6 +56,18 @@ ROUTE_MS = 0.0
 # When True, route time is accumulated into ROUTE_MS (costs two device synchronisations per
 # routed call, like the reference's timing at ssa/gemma_ssa.py:151-165).
 TIME_ROUTE = False
+# Per-layer key-block summaries of the per-query (decode) path, kept resident between calls:
+# layer -> {"sig", "kv_len", "nc" (complete blocks summarised), "mu", "var", "m3" (capacity
+# blocks)}. A call that continues the previous one (kv_len = previous kv_len + q_len, queries
+# starting at the previous kv_len) summarises only the blocks it completes.
+_DECODE = {}
+
+
+def reset_decode_state():
+    """Forgets the resident decode summaries of every layer. Needed only when a cache is edited
+    in place at unchanged lengths (e.g. beam search reordering its batch): prefills, shorter or
+    cropped caches and shape changes are detected and reset a layer's summaries by themselves."""
+    _DECODE.clear()
 
 
 def repeat_kv(x: torch.Tensor, n: int) -> torch.Tensor:
@@ -177,6 +189,8 @@ def ssa_attention_forward(module, query, key, value, attention_mask=None, scalin
 
     if cfg.impl in ("flex", "hip") and q_len == kv_len and q_len > cfg.block:
         li = getattr(module, "layer_idx", None)
+        # a prefill starts a sequence: the layer's resident decode summaries no longer apply
+        _DECODE.pop(("layer", li) if li is not None else ("module", id(module)), None)
         donor = cfg.share_route_from
         lists = None
         if donor is not None and li is not None:
@@ -209,7 +223,7 @@ def ssa_attention_forward(module, query, key, value, attention_mask=None, scalin
     # the edgeworth (third-cumulant) term joins the score as in ssa/gemma_ssa.py:101-102; a
     # dense call selects every causal block, so it needs no score terms beyond the first
     edge = cfg.edgeworth and not is_dense
-    mu, var, m3 = block_summary(key, cfg.block, "pop", n_real=kv_len, with_m3=edge)
+    mu, var, m3 = _query_path_summaries(module, key, q_len, pos0, edge, cfg.block)
     rows = _router_rows(query)
     if is_dense:
         top_c, frac = nb_layer, 0.0
@@ -223,6 +237,48 @@ def ssa_attention_forward(module, query, key, value, attention_mask=None, scalin
     return out, None
 
 
+def _query_path_summaries(module, key, q_len, pos0, with_m3, block):
+    """mu, var, m3 (b, hkv, ceil(kv_len/block), d) fp32 for the per-query router. The router's
+    candidates are the blocks complete at each query's position (ssa/gemma_ssa.py:109-110), all
+    complete at kv_len, so only those entries are read: they are the population statistics of
+    their rows (ssa/gemma_ssa.py:65-82), bit for bit the values block_summary gives over the
+    whole key; the tail block's entry is not used. Decode steps continue the previous call, so a
+    step summarises at most the one block it completes instead of the whole cache."""
+    b, hkv, kv_len, d = key.shape
+    nb = -(-kv_len // block)
+    if torch.compiler.is_compiling():  # no Python-side state under tracing
+        return block_summary(key, block, "pop", n_real=kv_len, with_m3=with_m3)
+    li = getattr(module, "layer_idx", None)
+    lk = ("layer", li) if li is not None else ("module", id(module))
+    sig = (b, hkv, d, key.dtype, str(key.device), block, bool(with_m3))
+    st = _DECODE.get(lk)
+    if st is None or st["sig"] != sig or pos0 != st["kv_len"] or kv_len != st["kv_len"] + q_len:
+        st = {"sig": sig, "kv_len": 0, "nc": 0, "mu": None, "var": None, "m3": None}
+        _DECODE[lk] = st
+    if st["mu"] is None or st["mu"].shape[2] < nb:  # capacity doubles, contents kept
+        cap = max(nb, 2 * (0 if st["mu"] is None else st["mu"].shape[2]), 64)
+        for name in ("mu", "var", "m3"):
+            if name == "m3" and not with_m3:
+                continue
+            buf = torch.zeros(b, hkv, cap, d, device=key.device, dtype=torch.float32)
+            if st[name] is not None:
+                buf[:, :, :st["nc"]].copy_(st[name][:, :, :st["nc"]])
+            st[name] = buf
+    nc = kv_len // block
+    if nc > st["nc"]:
+        a = st["nc"]
+        mu, var, m3 = block_summary(key[:, :, a * block:nc * block], block, "pop",
+                                    with_m3=with_m3)
+        st["mu"][:, :, a:nc].copy_(mu)
+        st["var"][:, :, a:nc].copy_(var)
+        if with_m3:
+            st["m3"][:, :, a:nc].copy_(m3)
+        st["nc"] = nc
+    st["kv_len"] = kv_len
+    return (st["mu"][:, :, :nb], st["var"][:, :, :nb],
+            st["m3"][:, :, :nb] if with_m3 else None)
+
+
 def install_ssa(model, **cfg_kwargs):
     """Registers ssa_attention_forward as the model's attention implementation, resetting every
     SSAConfig field not passed here to its default (ssa/gemma_ssa.py:244-279)."""
@@ -234,6 +290,7 @@ def install_ssa(model, **cfg_kwargs):
         setattr(CFG, k, val)
     _SHARE["sig"] = None
     _SHARE["bm"] = None
+    _DECODE.clear()
     _PROJ = None
     if CFG.proj_path:
         _PROJ = load_projection(CFG.proj_path)

@@ -1153,6 +1153,56 @@ def test_gemma_decode_equals_prefill_last_row(cuda):
         assert (inc[:, 0] - full[:, -1]).abs().max().item() < 1e-5
 
 
+@pytest.mark.parametrize("edgeworth", [False, True])
+def test_gemma_decode_resident_summaries(cuda, monkeypatch, edgeworth):
+    """Decode steps through ssa_attention_forward keep the key-block summaries resident and
+    summarise only the block a step completes (ssa/ivf_decode.py:133-135 grows its index the same
+    way): over 150 steps crossing two block boundaries every output equals, bit for bit, the same
+    call with the summaries recomputed from the whole cache; a prefill, a shorter cache and a
+    non-consecutive position each start over."""
+    torch.manual_seed(5)
+    n0, steps, block = 1000, 150, 128
+    q = torch.randn(1, 4, n0 + steps, 64, device=cuda, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, n0 + steps, 64, device=cuda, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    G.CFG = G.SSAConfig(block=block, budget_frac=0.3, impl="hip", edgeworth=edgeworth)
+    G.reset_decode_state()
+    lens = []
+    real = G.block_summary
+
+    def recording(x, *a, **kw):
+        lens.append(x.shape[2])
+        return real(x, *a, **kw)
+    mod = _mod(groups=2, layer_idx=3)
+    for t in range(n0, n0 + steps):
+        args = (q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1])
+        monkeypatch.setattr(G, "block_summary", recording)
+        inc, _ = G.ssa_attention_forward(mod, *args, scaling=0.125,
+                                         cache_position=torch.tensor([t], device=cuda))
+        monkeypatch.setattr(G, "block_summary", real)
+        saved = dict(G._DECODE)
+        G.reset_decode_state()
+        ref, _ = G.ssa_attention_forward(mod, *args, scaling=0.125)
+        G._DECODE.clear()
+        G._DECODE.update(saved)
+        assert torch.equal(inc, ref), t
+    # the first step summarised the prefix's complete blocks, later ones only completed blocks
+    assert lens[0] == (n0 + 1) // block * block and all(x == block for x in lens[1:]), lens
+    assert len(lens) == 1 + (n0 + steps) // block - (n0 + 1) // block
+    st = G._DECODE[("layer", 3)]
+    assert st["kv_len"] == n0 + steps and st["nc"] == (n0 + steps) // block
+    # a shorter cache (a new sequence) and a position gap each start over
+    G.ssa_attention_forward(mod, q[:, :, 499:500], k[:, :, :500], v[:, :, :500], scaling=0.125)
+    assert G._DECODE[("layer", 3)]["kv_len"] == 500
+    G.ssa_attention_forward(mod, q[:, :, 600:601], k[:, :, :601], v[:, :, :601], scaling=0.125)
+    assert G._DECODE[("layer", 3)]["kv_len"] == 601 and G._DECODE[("layer", 3)]["nc"] == 4
+    # a prefill drops the layer's decode summaries
+    G.CFG = G.SSAConfig(block=block, budget_frac=0.3, impl="hip")
+    G.ssa_attention_forward(mod, q[:, :, :512], k[:, :, :512], v[:, :, :512], scaling=0.125)
+    assert ("layer", 3) not in G._DECODE
+    G.reset_decode_state()
+
+
 def test_gemma_flex_no_future_leak_and_sharing(cuda):
     """ssa/tests/test_flex_swap.py:78-90 restated (outputs up to `cut` within 2e-2 when later
     keys/values change), plus bit-equality for the query blocks wholly before cut's block: the
