@@ -114,11 +114,19 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
  * ssa_route_workspace_size() gives the size that routes every row in one pass, and any size
  * >= ssa_route_workspace_size(B, Hq, 1, nbk) works. With at least B*Hq*nbk*4 bytes but less
  * than ssa_route_workspace_size(B, Hq, 1, nbk) the scores are computed exactly in fp64 instead
- * of by the certified MFMA contraction (the selection is the same either way).
+ * of by the certified MFMA contraction (the selection is the same either way). A workspace that
+ * also holds the MFMA operands split into bf16 parts -- ssa_route_workspace_size_split() bytes
+ * for every row in one pass (nterms: 1 + (var != NULL) + (m3 != NULL); nbk: summaries per key
+ * head, nbk*pool for ssa_route_pooled) -- lets the router split them once per call instead of in
+ * every score tile (used when nbk > 1024; with fewer key summaries one score tile per row makes
+ * the split a single pass anyway); with less, rows are routed in chunks that fit, the split
+ * operands included when at least one row's do.
  */
 int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c, float budget_frac,
                         int64_t local, int64_t query_pos, int64_t block);
 size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk);
+size_t ssa_route_workspace_size_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq,
+                                      int64_t nbk, int64_t d, int64_t nterms);
 int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,
               const float* m3, int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq, int64_t nbk, int64_t d, int mode,
               int64_t top_c, float budget_frac, int64_t local, float coef2, float coef3,
@@ -200,8 +208,9 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
  * the keys j <= t, j < n, of the blocks kv_idx[b,h,i,:kv_num[b,h,i]] with
  * softmax(scale * q.k) in fp32; out has q's dtype. strides[12] = q(b,h,n), k(b,h,n), v(b,h,n),
  * out(b,h,n) in elements. lse (B, Hq, n) fp32 natural-log sum-exp, may be NULL.
- * dtype: SSA_BF16 / SSA_F16 (MFMA, d = 64, 128 or 256) or SSA_F32 (d = 64). block: 64 or a
- * multiple of 128.
+ * dtype: SSA_BF16 / SSA_F16 (MFMA, d = 64, 128, 256 or 512) or SSA_F32 (d = 64). block: 64 or a
+ * multiple of 128. At d = 512 the four waves of a workgroup split the head dim over 32 query
+ * rows and sum their partial scores in wave order (the same order for every row).
  * The 16-bit paths read V transposed, (B, Hkv, d, n_pad) with n_pad = ceil(n/block)*block, from
  * the workspace (ssa_sparse_attn_workspace_size() bytes). flags = 0: the call first writes V^T
  * there itself; flags = SSA_ATTN_VT_READY: the workspace already holds V^T of this v (from

@@ -43,6 +43,7 @@ _SIGNATURES = {
                                    _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p]),
     "ssa_route_width": (_c_i64, [_c_int, _c_i64, _c_i64, _c_i64, _c_f, _c_i64, _c_i64, _c_i64]),
     "ssa_route_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ssa_route_workspace_size_split": (_c_sz, [_c_i64] * 7),
     "ssa_route": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_p] + [_c_i64] * 6 +
                   [_c_int, _c_i64, _c_f, _c_i64, _c_f, _c_f, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
                    _c_p, _c_sz, _c_p]),

@@ -926,6 +926,199 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   }
 }
 
+// Wide head dims (d = 128 NW, e.g. 512): a 32-key sub-tile of K and V^T is 64 KB at d = 512, so
+// an LDS ring of them would leave one workgroup per CU. Here the head dim is split across the NW
+// waves of a workgroup instead -- wave w owns dims [128 w, 128 w + 128) of one 32-row query group
+// -- and each wave loads its K and V^T fragments from global memory straight into registers
+// (their reuse across query groups and the query heads of a key head is L2's). Each wave
+// contracts its dims into a partial S^T = K Q^T (32 keys x 32 rows, the K rows permuted as in
+// sparse_attn_dma_kernel so P^T never leaves registers); the NW partials are summed through LDS
+// in wave order, so every wave holds the same fp32 scores, runs the same online softmax (exact
+// path: running max, fp32-scaled scores) and multiplies the same P into its dims of O.
+template <int DT, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void sparse_attn_wide_kernel(AttnParams p) {
+  using M = Mfma<DT>;
+  typedef typename M::vec vec;
+  constexpr int D = 128 * NW;
+  constexpr int KD = 8;   // 16-dim k-steps of a wave's 128 dims
+  constexpr int DTN = 4;  // 32-dim output tiles of a wave's 128 dims
+  constexpr int KT = 32;  // keys per sub-tile
+  __shared__ float sx[2][NW][16][64];  // partial scores [parity][wave][accumulator][lane]
+
+  const int64_t L0 = logical_id(blockIdx.x, p.group);
+  if (L0 >= p.total) return;
+  int64_t L = L0;
+  const int64_t qs = L % p.qsub;
+  L /= p.qsub;
+  const int64_t hg = L % p.G;
+  L /= p.G;
+  const int64_t kvh = L % p.Hkv;
+  L /= p.Hkv;
+  const int64_t b = L % p.B;
+  L /= p.B;
+  const int64_t i = p.nbq - 1 - L;
+  const int64_t h = kvh * p.G + hg;
+  const int64_t q0 = i * p.block + qs * 32;
+  if (q0 >= p.n) return;
+  const int64_t qmax = q0 + 31 < p.n - 1 ? q0 + 31 : p.n - 1;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, col = lane & 31;
+  const int qpos = (int)q0 + col;  // 32-bit (the host checks n < 2^31)
+  const int d0 = 128 * w;          // this wave's first head dim
+  const int64_t row = (b * p.Hq + h) * p.nbq + i;
+  int cnt = p.kv_num[row];
+  if (cnt > p.W) cnt = (int)p.W;
+  if (cnt < 0) cnt = 0;
+  const int32_t* list = p.kv_idx + row * p.W;
+  const int S = (int)(p.block / KT);
+
+  // Q fragments of this wave's dims (B operands of S^T = K Q^T)
+  vec qf[KD];
+  {
+    const unsigned short* src = reinterpret_cast<const unsigned short*>(p.q) + b * p.qsb +
+                                h * p.qsh + (int64_t)qpos * p.qsn + d0 + half * 8;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      u32x4 wv = {0u, 0u, 0u, 0u};
+      if (qpos < p.n) wv = *reinterpret_cast<const u32x4*>(src + kd * 16);
+      qf[kd] = M::from_bits(wv);
+    }
+  }
+  const unsigned short* kbase = reinterpret_cast<const unsigned short*>(p.k) + b * p.ksb +
+                                kvh * p.ksh + d0 + half * 8;
+  const unsigned short* vtbase = reinterpret_cast<const unsigned short*>(p.vt) +
+                                 (b * p.Hkv + kvh) * (int64_t)D * p.n_pad +
+                                 (int64_t)(d0 + col) * p.n_pad + half * 8;
+  const int krow = sigma32(col);
+
+  const int n32 = (int)p.n, blk32 = (int)p.block, nbq32 = (int)p.nbq, qmax32 = (int)qmax;
+  int lbase = 0;
+  int32_t lreg = lane < cnt ? list[lane] : -1;
+  int ce = 0, cs = -1;
+  auto next_tile = [&]() -> int {
+    while (true) {
+      if (++cs == S) {
+        cs = 0;
+        ++ce;
+      }
+      if (ce >= cnt) return -1;
+      if (ce - lbase >= 64) {  // wave-uniform; once per 64 list entries
+        lbase = ce;
+        lreg = ce + lane < cnt ? list[ce + lane] : -1;
+      }
+      const int c = __builtin_amdgcn_readlane(lreg, ce - lbase);
+      if (c >= 0 && c < nbq32) {
+        const int k0 = c * blk32 + cs * KT;
+        if (k0 <= qmax32 && k0 < n32) return k0;
+      }
+      cs = S - 1;
+    }
+  };
+
+  f32x16 oacc[DTN];
+#pragma unroll
+  for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.0f;
+  float m_run = -INFINITY, l_part = 0.0f;
+  const float c2 = p.scale_log2;
+  int par = 0;
+  for (int key0 = next_tile(); key0 >= 0; key0 = next_tile()) {
+    // ---- partial S^T over this wave's dims ----
+    int kr = key0 + krow;
+    if (kr > n32 - 1) kr = n32 - 1;  // ragged tail: re-read row n-1 (masked below)
+    const unsigned short* kp = kbase + (int64_t)kr * p.ksn;
+    u32x4 ka[KD];
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) ka[kd] = *reinterpret_cast<const u32x4*>(kp + kd * 16);
+    u32x4 va[2][DTN];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+        va[st][dt] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)dt * 32 * p.n_pad + key0 +
+                                                     st * 16);
+    f32x16 sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) sacc = M::mma(M::from_bits(ka[kd]), qf[kd], sacc);
+    // ---- the NW partials summed in wave order (identical in every wave) ----
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sx[par][w][r][lane] = sacc[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = sx[par][0][r][lane];
+#pragma unroll
+      for (int u = 1; u < NW; ++u) x += sx[par][u][r][lane];
+      sacc[r] = x;
+    }
+    par ^= 1;  // the next tile writes the other buffer (a wave reaches it only after every wave
+               // has passed this tile's barrier, i.e. finished reading the buffer it overwrites
+               // two tiles later)
+    // ---- mask (diagonal / ragged tail sub-tiles) ----
+    if (key0 + KT - 1 > (int)q0 || key0 + KT > n32) {
+      const int lim_q = qpos - key0, lim_n = n32 - 1 - key0;
+      const int lim = lim_q < lim_n ? lim_q : lim_n;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = (r >> 3) * 16 + half * 8 + (r & 7);
+        if (key > lim) sacc[r] = -INFINITY;
+      }
+    }
+    // ---- online softmax (lazy rescale) ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+    mx = pair_max(mx);
+    const float m_cand = mx * c2;
+    if (m_cand > m_run + kRescaleSlack) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+      l_part *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      m_run = m_cand;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // ---- P^T (registers) and O^T += V^T P^T over this wave's dims ----
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[8 * st + j], c2, -m_use));
+      const vec pb = M::pack(pv);
+      l_part = M::rowsum(pb, l_part);
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt) oacc[dt] = M::mma(M::from_bits(va[st][dt]), pb, oacc[dt]);
+    }
+  }
+
+  // ---- epilogue: this wave's dims of O = O^T / l ----
+  const float l_tot = pair_sum(l_part);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (qpos < n32) {
+    unsigned short* op = reinterpret_cast<unsigned short*>(p.o) + b * p.osb + h * p.osh +
+                         (int64_t)qpos * p.osn + d0;
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int e0 = dt * 32 + rg * 8 + half * 4;
+        uint2 wv;
+        wv.x = M::pack2(oacc[dt][4 * rg] * inv, oacc[dt][4 * rg + 1] * inv);
+        wv.y = M::pack2(oacc[dt][4 * rg + 2] * inv, oacc[dt][4 * rg + 3] * inv);
+        *reinterpret_cast<uint2*>(op + e0) = wv;
+      }
+    if (p.lse != nullptr && w == 0 && half == 0)
+      p.lse[(b * p.Hq + h) * p.n + qpos] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+  }
+}
+
 // Logical work items of a launch whose workgroups own `rows` query rows (a divisor of the block,
 // or the whole block 64): query sub-tiles per query block, the run of items placed together on
 // one XCD (the query heads of a key head for one query block), and the grid (a multiple of 8
@@ -1015,8 +1208,8 @@ extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv,
   SSA_REQUIRE(dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
               "transpose_v: 16-bit dtypes only");
   SSA_REQUIRE(B > 0 && Hkv > 0 && n > 0 && block > 0, SSA_ERR_INVALID, "transpose_v: bad sizes");
-  SSA_REQUIRE(d == 64 || d == 128 || d == 256, SSA_ERR_UNSUPPORTED,
-              "transpose_v: head_dim must be 64, 128 or 256");
+  SSA_REQUIRE(d == 64 || d == 128 || d == 256 || d == 512, SSA_ERR_UNSUPPORTED,
+              "transpose_v: head_dim must be 64, 128, 256 or 512");
   SSA_REQUIRE(block % 64 == 0, SSA_ERR_UNSUPPORTED, "transpose_v: block must be a multiple of 64");
   SSA_REQUIRE(aligned16(v) && aligned16(vt) && stride_b % 8 == 0 && stride_h % 8 == 0 &&
                   stride_n % 8 == 0,
@@ -1048,8 +1241,9 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && n > 0 && W > 0, SSA_ERR_INVALID,
               "sparse_attn: sizes must be positive");
   SSA_REQUIRE(Hq % Hkv == 0, SSA_ERR_INVALID, "sparse_attn: Hq not a multiple of Hkv");
-  SSA_REQUIRE(d == 64 || ((d == 128 || d == 256) && dtype != SSA_F32), SSA_ERR_UNSUPPORTED,
-              "sparse_attn: head_dim %lld unsupported (64; 128 and 256 for 16-bit inputs)",
+  SSA_REQUIRE(d == 64 || ((d == 128 || d == 256 || d == 512) && dtype != SSA_F32),
+              SSA_ERR_UNSUPPORTED,
+              "sparse_attn: head_dim %lld unsupported (64; 128, 256 and 512 for 16-bit inputs)",
               (long long)d);
   SSA_REQUIRE(block == 64 || (block > 0 && block % 128 == 0), SSA_ERR_UNSUPPORTED,
               "sparse_attn: block %lld unsupported (64 or a multiple of 128)", (long long)block);
@@ -1126,6 +1320,16 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
                                              static_cast<char*>(workspace), Hkv, n, p.n_pad,
                                              p.vsb, p.vsh, p.vsn, d, none);
       SSA_TRY(launch_status("transpose_v_kernel"));
+    }
+    if (d == 512) {  // head dim split across 4 waves, 32 query rows per workgroup
+      p.qsub = block / 32;
+      p.group = p.G * p.qsub;
+      p.total = p.nbq * B * Hkv * p.G * p.qsub;
+      const int64_t grid = (p.total + 8 * p.group - 1) / (8 * p.group) * (8 * p.group);
+      SSA_REQUIRE(grid < (1ll << 31), SSA_ERR_UNSUPPORTED, "sparse_attn: grid too large");
+      if (dtype == SSA_BF16) sparse_attn_wide_kernel<SSA_BF16, 4><<<(unsigned)grid, 256, 0, st>>>(p);
+      else sparse_attn_wide_kernel<SSA_F16, 4><<<(unsigned)grid, 256, 0, st>>>(p);
+      return launch_status("sparse_attn_wide_kernel");
     }
     if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, d, st);
     return launch_mfma<SSA_F16>(p, d, st);

@@ -580,6 +580,240 @@ __global__ __launch_bounds__(256) void route_score_mfma_kernel(
 }
 
 
+// ---- operands split once per call ---------------------------------------------------------
+// route_score_split_kernel reads the certified scoring's operands already split: for each query
+// row of the chunk A = [q | c2 fl32(q*q) | c3 fl32(q*q*q)] and for each candidate of a key head
+// B = [mu | var | m3] (the present terms, nt of them, concatenated: nk = nt*d values), as bf16 hi
+// and lo parts (split_bf16x8, the same values route_score_mfma_kernel forms in every tile), with
+// the fp32 squared norm of every term. route_split_kernel writes them, one wave per item, lane l
+// taking 8 consecutive values at a time.
+struct SplitOut {
+  unsigned short* hi;  // (items, nk)
+  unsigned short* lo;  // (items, nk)
+  float* sq;           // (items, 3): squared norm of term slot t (absent slots 0)
+};
+
+// QROWS: items are the chunk's query rows (item lr = (b*Hq + h)*ni + il, read from `src` of type
+// g.rows_dt and transformed per term); else the candidates of every key head (item bk*nbs + c,
+// term t read from terms[t] as is).
+template <bool QROWS>
+__global__ __launch_bounds__(256) void route_split_kernel(const void* __restrict__ src,
+                                                          const float* __restrict__ t0,
+                                                          const float* __restrict__ t1,
+                                                          const float* __restrict__ t2, RouteGeom g,
+                                                          int d, int nt, float coef2, float coef3,
+                                                          int64_t items, SplitOut o) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const int nk = nt * d;
+  int64_t off;  // element offset of the item's values
+  if constexpr (QROWS) {
+    const int64_t bh = item / g.ni, il = item % g.ni;  // bh = b*Hq + h
+    off = (bh * g.nbq + g.i0 + il) * d;
+  } else {
+    off = item * d;
+  }
+  // term slot s -> operand: slot 0 q / mu, then var (if present), then m3 (if present)
+  const float* terms[3] = {t0, t1, t2};
+  float sq[3] = {0.0f, 0.0f, 0.0f};
+  for (int j = lane * 8; j < nk; j += 64 * 8) {
+    const int s = j / d, e0 = j % d;
+    float x[8];
+    if constexpr (QROWS) {
+      float q[8];
+      if (g.rows_dt == SSA_F32) {
+        const f32x4* pq = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + off + e0);
+        const f32x4 a0 = pq[0], a1 = pq[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          q[e] = a0[e];
+          q[4 + e] = a1[e];
+        }
+      } else {
+        const u32x4 wq =
+            *reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(src) + off + e0);
+        unpack8(wq, q, g.rows_dt == SSA_BF16);
+      }
+      const int term = s == 0 ? 0 : (t1 != nullptr && s == 1 ? 1 : 2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = q[e];
+        if (term == 1) x[e] = coef2 * (q[e] * q[e]);
+        else if (term == 2) x[e] = coef3 * ((q[e] * q[e]) * q[e]);
+      }
+    } else {
+      const f32x4* pb = reinterpret_cast<const f32x4*>(terms[s] + off + e0);
+      const f32x4 b0 = pb[0], b1 = pb[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = b0[e];
+        x[4 + e] = b1[e];
+      }
+    }
+    float a2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a2 = fmaf(x[e], x[e], a2);
+    sq[s] += a2;
+    u32x4 hi, lo;
+    split_bf16x8(x, hi, lo);
+    *reinterpret_cast<u32x4*>(o.hi + item * nk + j) = hi;
+    *reinterpret_cast<u32x4*>(o.lo + item * nk + j) = lo;
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sq[t] += __shfl_xor(sq[t], m, 64);
+  if (lane < 3) o.sq[item * 3 + lane] = lane == 0 ? sq[0] : lane == 1 ? sq[1] : sq[2];
+}
+
+// route_score_mfma_kernel on pre-split operands (route_split_kernel): the same tiles, products,
+// keys, emag and tile maxima; the staging copies 16-byte runs of the bf16 parts (the
+// concatenated terms as one contraction of nk values) instead of forming and splitting them.
+template <bool TMAX>
+__global__ __launch_bounds__(256) void route_score_split_kernel(
+    SplitOut A, SplitOut Bs, RouteGeom g, int nk, unsigned int* __restrict__ keys,
+    float* __restrict__ emag, unsigned int* __restrict__ tmax, int64_t ntile, int64_t row_tiles,
+    int64_t cand_tiles) {
+  constexpr int KC = 32;
+  static_assert(4 * kTile * kStageLd * 2 >= kTile * (kTile + 1) * 4, "stage too small");
+  __shared__ __attribute__((aligned(16))) unsigned short stage[4][kTile][kStageLd];
+  __shared__ int64_t row_key[kTile];  // chunk row index (b*Hq + h)*ni + il of the tile's rows (-1: none)
+  __shared__ int64_t row_cm[kTile];   // scored candidates of the tile's rows (0: none)
+  __shared__ float sqa[3][kTile], sqb[3][kTile];  // squared norms per term: rows, candidates
+  __shared__ unsigned int smax[kTile];
+
+  const int64_t bk = blockIdx.y;  // b * Hkv + kvh
+  const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
+  const int64_t rt = blockIdx.x / cand_tiles, ct = blockIdx.x % cand_tiles;
+  const int64_t R = g.G * g.ni;
+  const int64_t r0 = rt * kTile;
+  const int64_t c0 = ct * kTile;
+  if (r0 >= R) return;
+  const int64_t r_last = r0 + kTile - 1 < R ? r0 + kTile - 1 : R - 1;
+  const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
+  if (c0 >= row_cmax_s(g, imax)) return;  // uniform: no row of the tile has these candidates
+  const int64_t nbs = g.nbk * g.pool;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wr = w & 1, wc = w >> 1;
+  if (tid < kTile) {  // per-row geometry, once per tile (64-bit divisions)
+    const int64_t r = r0 + tid;
+    int64_t lr = -1, cm = 0;
+    if (r < R) {
+      const int64_t h = kvh * g.G + r / g.ni;
+      const int64_t il = r % g.ni;
+      lr = (b * g.Hq + h) * g.ni + il;
+      cm = row_cmax_s(g, g.i0 + il);
+    }
+    row_key[tid] = lr;
+    row_cm[tid] = cm;
+  } else if (tid < 2 * kTile) {  // the norms, from the split pass
+    const int t = tid - kTile;
+    const int64_t r = r0 + t;
+    int64_t lr = -1;
+    if (r < R) lr = (b * g.Hq + kvh * g.G + r / g.ni) * g.ni + r % g.ni;
+    const int64_t c = c0 + t;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      sqa[s][t] = lr >= 0 ? A.sq[lr * 3 + s] : 0.0f;
+      sqb[s][t] = c < nbs ? Bs.sq[(bk * nbs + c) * 3 + s] : 0.0f;
+    }
+  }
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  const int rr = tid >> 2, k8 = (tid & 3) * 8;  // staging: row / candidate rr, values k8..k8+7
+  const int64_t cand_s = c0 + rr;
+  for (int k0 = 0; k0 < nk; k0 += KC) {
+    __syncthreads();
+    const int64_t lr = row_key[rr];
+    u32x4 ah = {0u, 0u, 0u, 0u}, al = ah, bh = ah, bl = ah;
+    if (k0 + k8 < nk) {
+      if (lr >= 0) {
+        ah = *reinterpret_cast<const u32x4*>(A.hi + lr * nk + k0 + k8);
+        al = *reinterpret_cast<const u32x4*>(A.lo + lr * nk + k0 + k8);
+      }
+      if (cand_s < nbs) {
+        bh = *reinterpret_cast<const u32x4*>(Bs.hi + (bk * nbs + cand_s) * nk + k0 + k8);
+        bl = *reinterpret_cast<const u32x4*>(Bs.lo + (bk * nbs + cand_s) * nk + k0 + k8);
+      }
+    }
+    *reinterpret_cast<u32x4*>(&stage[0][rr][k8]) = ah;
+    *reinterpret_cast<u32x4*>(&stage[1][rr][k8]) = al;
+    *reinterpret_cast<u32x4*>(&stage[2][rr][k8]) = bh;
+    *reinterpret_cast<u32x4*>(&stage[3][rr][k8]) = bl;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < KC / 16; ++s) {
+      const int kk = s * 16 + (lane >> 5) * 8;
+      const int ra = wr * 32 + (lane & 31), rb = wc * 32 + (lane & 31);
+      const bf16x8 xah = *reinterpret_cast<const bf16x8*>(&stage[0][ra][kk]);
+      const bf16x8 xal = *reinterpret_cast<const bf16x8*>(&stage[1][ra][kk]);
+      const bf16x8 xbh = *reinterpret_cast<const bf16x8*>(&stage[2][rb][kk]);
+      const bf16x8 xbl = *reinterpret_cast<const bf16x8*>(&stage[3][rb][kk]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xah, xbh, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xah, xbl, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xal, xbh, acc, 0, 0, 0);
+    }
+  }
+  const int64_t cand = c0 + wc * 32 + (lane & 31);
+  unsigned int mk[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int rl = wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+    mk[j] = 0u;
+    if (cand >= row_cm[rl]) continue;  // past the row's candidates (or no row: 0)
+    const unsigned int k = score_key(acc[j]);
+    keys[row_key[rl] * nbs + cand] = k;
+    mk[j] = k;
+  }
+  if constexpr (TMAX) {
+    // row maxima: the tile's keys go to LDS as [row][candidate], 4 threads reduce each row
+    unsigned int* red = reinterpret_cast<unsigned int*>(&stage[0][0][0]);
+    __syncthreads();  // every wave is past its last contraction
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      red[(wr * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3)) * (kTile + 1) + wc * 32 +
+          (lane & 31)] = mk[j];
+    __syncthreads();
+    const unsigned int* pr = red + (tid >> 2) * (kTile + 1) + (tid & 3) * 16;
+    unsigned int mx = 0u;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = pr[e] > mx ? pr[e] : mx;
+    unsigned int o = __shfl_xor(mx, 1, 64);
+    mx = o > mx ? o : mx;
+    o = __shfl_xor(mx, 2, 64);
+    mx = o > mx ? o : mx;
+    if ((tid & 3) == 0) smax[tid >> 2] = mx;
+  }
+  __syncthreads();
+  if (w == 0) {
+    float M[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      M[t] = sqb[t][lane];  // zero for candidates past nbs
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) M[t] = fmaxf(M[t], __shfl_xor(M[t], off, 64));
+    }
+    if (c0 < row_cm[lane]) {
+      double mag = 0.0, nsum = 0.0;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const double a = sqrt((double)sqa[t][lane]), bb = sqrt((double)M[t]);
+        mag += a * bb;
+        nsum += a + bb;
+      }
+      mag += 0x1p-56 * nsum;
+      float f = (float)mag;
+      if ((double)f < mag) f = __uint_as_float(__float_as_uint(f) + 1u);  // round up (f >= 0)
+      const int64_t lrow = row_key[lane];
+      emag[lrow * ntile + ct] = f;
+      if constexpr (TMAX) tmax[lrow * ntile + ct] = smax[lane];
+    }
+  }
+}
+
 // Inverse of score_key.
 __device__ inline float key_value(unsigned int k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
@@ -1538,11 +1772,52 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                        workspace_bytes >= route_row_bytes(nbs) * rows_per_i;
   const size_t per_row = mfma_ok ? route_row_bytes(nbs) : row_bytes;
   int64_t chunk = (int64_t)(workspace_bytes / (per_row * rows_per_i));
+  // Operands split once (route_split_kernel) when the workspace holds them beside the keys: the
+  // candidates of every key head, then per chunk its query rows (bf16 hi + lo, 4 bytes per
+  // value, and 3 norms per item), after the chunk's keys, emag and tile maxima.
+  const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const int nt = 1 + (var ? 1 : 0) + (m3 ? 1 : 0);
+  const int64_t nk = nt * d;
+  const size_t ncand_all = (size_t)(B * Hkv) * (size_t)nbs;
+  const size_t cand_split = 2 * r256(ncand_all * nk * 2) + r256(ncand_all * 12);
+  // (it pays only for long rows: at 1,024 candidates the two split launches cost what the
+  // score kernel saves)
+  bool presplit = false;
+  if (mfma_ok && nbk > kSmallNbk && workspace_bytes > cand_split + 8 * 256) {
+    const size_t per_split_row = route_row_bytes(nbs) + (size_t)nk * 4 + 12;
+    const int64_t ch =
+        (int64_t)((workspace_bytes - cand_split - 8 * 256) / (per_split_row * rows_per_i));
+    if (ch >= 1) {
+      presplit = true;
+      chunk = ch;
+    }
+  }
   if (chunk > nbq) chunk = nbq;
   unsigned int* keys = static_cast<unsigned int*>(workspace);
   float* emag = reinterpret_cast<float*>(keys + (size_t)chunk * rows_per_i * (size_t)nbs);
   unsigned int* tmaxp =
       reinterpret_cast<unsigned int*>(emag + (size_t)chunk * rows_per_i * (size_t)ntile);
+  SplitOut As{}, Bs{};
+  if (presplit) {
+    const size_t nrow = (size_t)chunk * rows_per_i;
+    char* sp = static_cast<char*>(workspace) +
+               r256(nrow * ((size_t)nbs * 4 + (size_t)ntile * 8));
+    As.hi = reinterpret_cast<unsigned short*>(sp);
+    sp += r256(nrow * nk * 2);
+    As.lo = reinterpret_cast<unsigned short*>(sp);
+    sp += r256(nrow * nk * 2);
+    As.sq = reinterpret_cast<float*>(sp);
+    sp += r256(nrow * 12);
+    Bs.hi = reinterpret_cast<unsigned short*>(sp);
+    sp += r256(ncand_all * nk * 2);
+    Bs.lo = reinterpret_cast<unsigned short*>(sp);
+    sp += r256(ncand_all * nk * 2);
+    Bs.sq = reinterpret_cast<float*>(sp);
+    sp += r256(ncand_all * 12);
+    SSA_REQUIRE(sp <= static_cast<char*>(workspace) + workspace_bytes, SSA_ERR_WORKSPACE,
+                "route: split operands overflow the workspace");
+  }
+  bool cands_split = false;
 
   RouteGeom g;
   g.mode = mode;
@@ -1625,6 +1900,29 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
       ca.coef2 = coef2;
       ca.coef3 = coef3;
       dim3 grid((unsigned)(row_tiles * cand_tiles), (unsigned)(B * Hkv));
+      if (presplit) {
+        if (!cands_split) {
+          SSA_REQUIRE(ncand_all < (1ull << 33), SSA_ERR_UNSUPPORTED, "route: too many candidates");
+          // candidates: the present terms in slot order (mu, then var, then m3)
+          const float* ct1 = var ? var : m3;
+          const float* ct2 = var ? m3 : nullptr;
+          route_split_kernel<false><<<(unsigned)((ncand_all + 3) / 4), 256, 0, stream>>>(
+              nullptr, mu, ct1, ct2, g, (int)d, nt, coef2, coef3, (int64_t)ncand_all, Bs);
+          SSA_TRY(launch_status("route_split_kernel"));
+          cands_split = true;
+        }
+        const int64_t nrow = (int64_t)rows_per_i * g.ni;
+        route_split_kernel<true><<<(unsigned)((nrow + 3) / 4), 256, 0, stream>>>(
+            rows, nullptr, var, m3, g, (int)d, nt, coef2, coef3, nrow, As);
+        SSA_TRY(launch_status("route_split_kernel"));
+        if (tm)
+          route_score_split_kernel<true><<<grid, 256, 0, stream>>>(
+              As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
+        else
+          route_score_split_kernel<false><<<grid, 256, 0, stream>>>(
+              As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
+        SSA_TRY(launch_status("route_score_split_kernel"));
+      } else {
 #define SSA_SCORE_MFMA(E, T)                                                                       \
   route_score_mfma_kernel<E, T><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,    \
                                                           coef3, keys, emag, tmaxp, ntile,         \
@@ -1638,6 +1936,7 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
       }
 #undef SSA_SCORE_MFMA
       SSA_TRY(launch_status("route_score_mfma_kernel"));
+      }
     } else if (cand_tiles > 0) {
       SSA_REQUIRE(row_tiles * cand_tiles < (1ll << 31) && B * Hkv < 65536, SSA_ERR_UNSUPPORTED,
                   "route: score grid too large");
@@ -1707,6 +2006,18 @@ extern "C" int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t t
     if (cnt > w) w = cnt;
   }
   return w < nbk ? w : nbk;
+}
+
+extern "C" size_t ssa_route_workspace_size_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t nbq,
+                                                 int64_t nbk, int64_t d, int64_t nterms) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || nbq <= 0 || nbk <= 0 || d <= 0 || nterms < 1 ||
+      nterms > 3)
+    return 0;
+  const auto r256 = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t nk = (size_t)(nterms * d), rows = (size_t)(B * Hq * nbq);
+  const size_t cands = (size_t)(B * Hkv) * (size_t)nbk;
+  const size_t cand_split = 2 * r256(cands * nk * 2) + r256(cands * 12);
+  return rows * (ssa::route_row_bytes(nbk) + nk * 4 + 12) + cand_split + 8 * 256;
 }
 
 extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk) {

@@ -133,9 +133,12 @@ def _route_impl(rows, mu, var, m3, mode, top_c, budget_frac, local, coef2, coef3
     dev = rows.device
     kv_num = torch.empty(B, Hq, nbq, device=dev, dtype=torch.int32)
     kv_idx = torch.empty(B, Hq, nbq, W, device=dev, dtype=torch.int32)
-    full = int(_lib.query("ssa_route_workspace_size", B, Hq, nbq, nbs))
+    # every row in one pass with the operands split once (ssa_route_workspace_size_split) when it
+    # fits the limit, else the limit (rows routed in chunks), at least one row's keys
+    nterms = 1 + (var is not None) + (m3 is not None)
+    full = int(_lib.query("ssa_route_workspace_size_split", B, Hq, Hkv, nbq, nbs, d, nterms))
     per_i = int(_lib.query("ssa_route_workspace_size", B, Hq, 1, nbs))
-    ws_bytes = max(per_i, min(full, workspace_limit // per_i * per_i))
+    ws_bytes = max(per_i, min(full, workspace_limit))
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     _lib.call("ssa_route_pooled", rows.data_ptr(), _lib.dtype_code(rows.dtype), mu.data_ptr(),
               _lib.ptr(var), _lib.ptr(m3), B,
@@ -177,7 +180,7 @@ def expand_selection(kv_num: torch.Tensor, kv_idx: torch.Tensor, nbk: int):
 
 
 def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
-    """V (B, Hkv, n, d) 16-bit, d in 64 / 128 / 256 -> the V^T workspace (B, Hkv, d,
+    """V (B, Hkv, n, d) 16-bit, d in 64 / 128 / 256 / 512 -> the V^T workspace (B, Hkv, d,
     ceil(n/block)*block) that the 16-bit attention kernels read (keys >= n zero-filled). Pass it
     to sparse_attention(vt=...) to skip the per-call transpose."""
     _lib.require_device(v)
@@ -286,7 +289,7 @@ def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
 
 # head dims the tiled prefill kernels serve (with block 64 or a multiple of 128): the MFMA
 # kernel (bf16 / fp16) and the fp32 kernel; other head dims and blocks take the per-row kernel
-TILED_HEAD_DIMS = (64, 128, 256)
+TILED_HEAD_DIMS = (64, 128, 256, 512)
 TILED_HEAD_DIMS_F32 = (64,)
 _ROWS_WORKSPACE_LIMIT = 1 << 28
 
