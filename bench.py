@@ -245,6 +245,24 @@ def device_info(torch, dev):
     info["hbm_copy_gbs"] = gbs
     info["hbm_copy_frac_of_8tbs"] = gbs / PEAK_HBM_GBS
     del src, dst
+    # the MFMA rate a plain library GEMM sustains on this box (hipBLASLt through torch.matmul,
+    # bf16 8192^3): the practical ceiling the attention kernels' roofline fraction compares with
+    a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    c = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    tf = 2.0 * 8192 ** 3 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    info["gemm_bf16_8192_tflops"] = tf
+    info["gemm_bf16_frac_of_peak"] = tf / PEAK_BF16_TFLOPS
+    del a, b, c
     return info
 
 
