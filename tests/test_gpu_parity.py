@@ -831,6 +831,41 @@ def test_decoder_folded_append_equals_separate_append(cuda):
     assert torch.equal(decs[0].kcache[:, :, :n0 + steps], kt)
 
 
+def test_routed_decoder_step_under_torch_compile(cuda):
+    """RoutedDecoder.step compiled (dynamo + aot_eager: the ssa_amd::decode_step op's in-place
+    writes to the caches, summaries and selection are functionalised and written back): 8 steps
+    crossing a block completion give outputs, selections, caches and summaries bit-identical to
+    an eager decoder's, and the advancing position (self.pos, read inside the compiled step)
+    costs at most one recompilation: after the first change dynamo makes it a symbolic int."""
+    import torch._dynamo.testing as DT
+    torch._dynamo.reset()
+    Hq, Hkv, d, block, prefix, steps = 14, 2, 64, 128, 1020, 8
+    rng = np.random.default_rng(17)
+    total = prefix + steps
+    k = WL.round_to(rng.standard_normal((1, Hkv, total, d)).astype(np.float32), torch.bfloat16)
+    v = WL.round_to(rng.standard_normal((1, Hkv, total, d)).astype(np.float32), torch.bfloat16)
+    q = WL.round_to(rng.standard_normal((steps, 1, Hq, d)).astype(np.float32), torch.bfloat16)
+    kd, vd, qd = (dev(x, torch.bfloat16, cuda) for x in (k, v, q))
+    eager, comp = (D.RoutedDecoder(1, Hq, Hkv, d, total, block=block, top_c=8, local=1,
+                                   dtype=torch.bfloat16, device=cuda) for _ in range(2))
+    for dec in (eager, comp):
+        dec.prefill(kd[:, :, :prefix], vd[:, :, :prefix])
+    cnt = DT.CompileCounterWithBackend("aot_eager")
+    step_c = torch.compile(lambda q_, k_, v_: comp.step(q_, k_, v_), backend=cnt)
+    for t in range(steps):
+        pos = prefix + t
+        k_new, v_new = kd[:, :, pos].contiguous(), vd[:, :, pos].contiguous()
+        out_e = eager.step(qd[t], k_new, v_new)
+        out_c = step_c(qd[t], k_new, v_new)
+        assert torch.equal(out_e, out_c), t
+        assert torch.equal(eager.kv_num, comp.kv_num) and torch.equal(eager.kv_idx, comp.kv_idx), t
+    print(f"compiled decode steps: {cnt.frame_count} compilation(s) over {steps} steps", flush=True)
+    assert comp.pos == eager.pos == total
+    assert torch.equal(eager.kcache, comp.kcache) and torch.equal(eager.vcache, comp.vcache)
+    assert torch.equal(eager.mu, comp.mu) and torch.equal(eager.var, comp.var)
+    assert 1 <= cnt.frame_count <= 2, cnt.frame_count
+
+
 def test_routed_decoder_matches_reference_router_and_oracle(cuda):
     """RoutedDecoder on a C4-shaped cache: the selection at each fixture position equals the
     reference _selection_mask (float32) and the oracle; the output matches the oracle row."""
