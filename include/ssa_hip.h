@@ -120,7 +120,10 @@ int ssa_block_summary(const void* x, int dtype, int64_t B, int64_t H, int64_t n,
  * head, nbk*pool for ssa_route_pooled) -- lets the router split them once per call instead of in
  * every score tile (used when nbk > 1024; with fewer key summaries one score tile per row makes
  * the split a single pass anyway); with less, rows are routed in chunks that fit, the split
- * operands included when at least one row's do.
+ * operands included when at least one row's do. Both sizes include 4 bytes per routed row and
+ * 512 bytes at the end of the workspace for the long-row select (more than 1024 candidates,
+ * keep <= 64, W <= 128: one wave per row from the per-tile key maxima; the rows it cannot take
+ * -- ties or bands too wide for a wave -- go to the workgroup select).
  */
 int64_t ssa_route_width(int mode, int64_t nbq, int64_t nbk, int64_t top_c, float budget_frac,
                         int64_t local, int64_t query_pos, int64_t block);

@@ -362,6 +362,11 @@ constexpr int kMaxTiles = kMaxNbk / kNormTile;  // tile maxima of a row staged b
 inline size_t route_row_bytes(int64_t nbs) {
   return (size_t)nbs * 4u + (size_t)((nbs + kNormTile - 1) / kNormTile) * 8u;
 }
+// The wave select's bookkeeping at the end of the workspace: its deferred-row list (4 bytes per
+// routed row of a chunk) below kRouteTail bytes that hold one counter per chunk (the first
+// kRouteCounters chunks; alignment slack included).
+constexpr size_t kRouteTail = 512;
+constexpr int kRouteCounters = 64;
 
 // Approximate scores for the certified router: one MFMA contraction of the query rows
 // A = [q | c2 fl32(q*q) | c3 fl32(q*q*q)] against the candidates' B = [mu | var | m3] (n = 2d, 3d
@@ -959,7 +964,8 @@ constexpr int kSmallNbk = 1024;  // one wave, J = 16 entries per lane
 template <int NT, int QR>
 __global__ __launch_bounds__(NT) void route_select_kernel(
     unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int64_t W, CertArgs ca) {
+    int32_t* __restrict__ kv_idx, int64_t W, CertArgs ca,
+    const unsigned int* __restrict__ rowlist, const unsigned int* __restrict__ nlist) {
   __shared__ unsigned int bits[kMaxNbk / 32];
   __shared__ unsigned int cache[kCacheKeys];  // the row's keys, or the filtered candidates
   __shared__ unsigned int cidx[kCand];        // candidate block indices (filtered rows)
@@ -970,7 +976,11 @@ __global__ __launch_bounds__(NT) void route_select_kernel(
   __shared__ float sh_norm[NT / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
+  int64_t lrow = blockIdx.x;  // (b*Hq + h) * ni + il
+  if (rowlist != nullptr) {  // the rows route_select_wave_kernel deferred (workgroup-uniform)
+    if (blockIdx.x >= *nlist) return;
+    lrow = rowlist[blockIdx.x];
+  }
   const int64_t bh = lrow / g.ni, il = lrow % g.ni;
   const int64_t i = g.i0 + il;
   const int64_t cmax = row_cmax(g, i);
@@ -1547,6 +1557,227 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
   if (lane == 0) kv_num[bh * g.nbq + i] = (int32_t)num;
 }
 
+// Long rows with certified keys and per-tile maxima (pool 1, keep <= kWaveK): one wave per row,
+// no workgroup barriers, 4 rows per workgroup. T0, the K-th largest tile maximum (K distinct
+// tiles hold a key >= T0), bounds the K-th largest key from below, so every key >= T0 lies in a
+// tile whose maximum reaches T0: those tiles are read (8 in flight per lane) and their keys
+// >= T0 kept in the wave's LDS list. T, the K-th largest of the list, is the row's K-th largest
+// key (or a prefix with exactly K list keys >= it, in which case exactly K keys of the row are
+// >= T0 and T0 serves as the threshold). The certificate band [lo, hi] around it is classified
+// from the list when lo >= T0, else from the tiles whose maximum reaches lo; keys above hi are
+// taken, and when the band holds more candidates than places remain they are rescored exactly
+// (16 lanes per candidate) and ranked by (exact key, lowest block). The taken blocks and the
+// local window are written in ascending order. A row this kernel does not take (keep > kWaveK,
+// too few tiles, more than kWaveCap keys >= T0, a band of more than kWaveBand) is appended to
+// `defer` for route_select_kernel; no output of that row is written here.
+constexpr int kWaveK = 64;       // largest keep of the wave select
+constexpr int kWaveCap = 512;    // keys >= T0 one wave holds
+constexpr int kWaveBand = 128;   // band candidates one wave ranks exactly
+constexpr int kWaveSel = 128;    // taken blocks + local window (W <= kWaveSel)
+constexpr int kWaveSlots = kMaxTiles / 64;  // tile maxima per lane
+
+template <int QR>
+__global__ __launch_bounds__(256) void route_select_wave_kernel(
+    const unsigned int* __restrict__ keys, RouteGeom g, int32_t* __restrict__ kv_num,
+    int32_t* __restrict__ kv_idx, int64_t W, int64_t nrows, CertArgs ca,
+    unsigned int* __restrict__ defer, unsigned int* __restrict__ ndefer) {
+  __shared__ unsigned int skey[4][kWaveCap], sidx[4][kWaveCap];
+  __shared__ unsigned int bkey[4][kWaveBand], bidx[4][kWaveBand];
+  __shared__ unsigned int sel[4][kWaveSel];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t lrow = (int64_t)blockIdx.x * 4 + wv;
+  if (lrow >= nrows) return;  // whole wave
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int64_t bh = lrow / g.ni, il = lrow % g.ni;
+  const int64_t i = g.i0 + il;
+  const int64_t cmax = row_cmax(g, i);
+  const int64_t keep = row_keep(g, cmax);
+  const int64_t K = keep < cmax ? keep : cmax;
+  const int64_t nt = (cmax + kNormTile - 1) / kNormTile;
+  auto defer_row = [&]() {
+    if (lane == 0) defer[atomicAdd(ndefer, 1u)] = (unsigned int)lrow;
+  };
+  if (!(K > 0 && K < cmax && K <= kWaveK && nt > K && nt <= kMaxTiles)) {
+    defer_row();
+    return;
+  }
+  const unsigned int* kraw = keys + lrow * g.nbk;
+  const unsigned int* tm = ca.tmax + lrow * ca.ntile;
+  unsigned int tk[kWaveSlots];
+#pragma unroll
+  for (int j = 0; j < kWaveSlots; ++j) {
+    const int64_t t = lane + 64 * j;
+    tk[j] = t < nt ? tm[t] : 0u;
+  }
+  const unsigned int T0 = wave_kth_key<kWaveSlots>(tk, K);
+  if (T0 == 0u) {  // fewer than K nonzero tile maxima
+    defer_row();
+    return;
+  }
+  // each tile of the lanes' mask m of slot j whose maximum reaches `th`: fn(key, block, valid)
+  // for its 64 candidates (lane l: candidate 64 t + l), 8 tiles in flight
+  auto for_tiles = [&](unsigned int th, auto fn) {
+#pragma unroll
+    for (int j = 0; j < kWaveSlots; ++j) {
+      unsigned long long m = __ballot(lane + 64 * j < nt && tk[j] >= th);
+      while (m) {  // wave-uniform
+        int64_t cq[8];
+        unsigned int kq[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          int64_t c = cmax;
+          if (m) {
+            const int b = __ffsll((long long)m) - 1;
+            m &= m - 1;
+            c = (int64_t)(b + 64 * j) * kNormTile + lane;
+          }
+          cq[u] = c;
+          kq[u] = c < cmax ? kraw[c] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fn(kq[u], (unsigned int)cq[u], cq[u] < cmax);
+      }
+    }
+  };
+  // the keys >= T0 (and their blocks) to the wave's list
+  int ns = 0;
+  for_tiles(T0, [&](unsigned int key, unsigned int blk, bool valid) {
+    const bool take = valid && key >= T0;
+    const unsigned long long bm = __ballot(take);
+    const int slot = ns + (int)__popcll(bm & lt);
+    if (take && slot < kWaveCap) {
+      skey[wv][slot] = key;
+      sidx[wv][slot] = blk;
+    }
+    ns += (int)__popcll(bm);
+  });
+  if (ns > kWaveCap) {
+    defer_row();
+    return;
+  }
+  wave_lds_sync();
+  constexpr int SJ = kWaveCap / 64;
+  unsigned int sk[SJ];
+#pragma unroll
+  for (int j = 0; j < SJ; ++j) sk[j] = lane + 64 * j < ns ? skey[wv][lane + 64 * j] : 0u;
+  const unsigned int T = wave_kth_key<SJ>(sk, K);
+  float M = cert_emag_max(ca, lrow, cmax, lane, 64);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  const unsigned int Tc = T < T0 ? T0 : T;
+  unsigned int lo, hi;
+  cert_band(ca, Tc, M, &lo, &hi);
+  // classify: above the band -> taken (to sel); in the band -> listed for exact ranking
+  int nin = 0, nunc = 0;
+  auto classify = [&](unsigned int key, unsigned int blk, bool valid) {
+    const bool s = valid && key > hi;
+    const bool u = valid && !s && key >= lo;
+    const unsigned long long bs = __ballot(s), bu = __ballot(u);
+    const int ps = nin + (int)__popcll(bs & lt), pu = nunc + (int)__popcll(bu & lt);
+    if (s && ps < kWaveSel) sel[wv][ps] = blk;
+    if (u && pu < kWaveBand) {
+      bidx[wv][pu] = blk;
+      bkey[wv][pu] = key;
+    }
+    nin += (int)__popcll(bs);
+    nunc += (int)__popcll(bu);
+  };
+  if (lo >= T0) {
+#pragma unroll
+    for (int j = 0; j < SJ; ++j) {
+      const int e = lane + 64 * j;
+      classify(sk[j], e < ns ? sidx[wv][e] : 0u, e < ns);
+    }
+  } else {
+    for_tiles(lo, classify);
+  }
+  const int m = (int)K - nin;  // places left for the band
+  if (nin > (int)K || nunc > kWaveBand) {
+    defer_row();
+    return;
+  }
+  wave_lds_sync();
+  int n = nin;
+  if (nunc <= m) {  // the band fills them exactly
+    for (int e = lane; e < nunc; e += 64) sel[wv][nin + e] = bidx[wv][e];
+    n = nin + nunc;
+  } else {
+    // exact keys of the band, four candidates at a time (a 16-lane group each)
+    const int64_t b = bh / g.Hq, h = bh % g.Hq;
+    const int64_t bk = b * g.Hkv + h / g.G;
+    const int64_t cbase = bk * g.nbk * ca.d;
+    float qg[4 * QR];
+    {
+      const int64_t roff = ((b * g.Hq + h) * g.nbq + i) * ca.d;
+#pragma unroll
+      for (int t = 0; t < 4 * QR; ++t) {
+        const int k = (lane & 15) + 16 * t;
+        qg[t] = k < ca.d ? load_row(ca.rows, roff + k, g.rows_dt) : 0.0f;
+      }
+    }
+    for (int base = 0; base < nunc; base += 4) {  // wave-uniform
+      const int bi = base + (lane >> 4);
+      const unsigned int cb = bi < nunc ? bidx[wv][bi] : 0u;
+      const unsigned int kx = group_exact_key<QR>(ca, qg, cbase, (int64_t)cb, 1);
+      if ((lane & 15) == 0 && bi < nunc) bkey[wv][bi] = kx;
+    }
+    wave_lds_sync();
+    // band candidate e is taken when fewer than m rank above it (larger exact key, or equal key
+    // and lower block); exactly m are taken
+    int took = 0;
+    for (int e0 = 0; e0 < nunc; e0 += 64) {  // wave-uniform
+      const int e = e0 + lane;
+      bool take = false;
+      unsigned int ce = 0u;
+      if (e < nunc) {
+        const unsigned int ke = bkey[wv][e];
+        ce = bidx[wv][e];
+        int above = 0;
+        for (int f = 0; f < nunc; ++f) {
+          const unsigned int kf = bkey[wv][f];
+          above += (kf > ke || (kf == ke && bidx[wv][f] < ce)) ? 1 : 0;
+        }
+        take = above < m;
+      }
+      const unsigned long long bt = __ballot(take);
+      if (take) sel[wv][nin + took + (int)__popcll(bt & lt)] = ce;
+      took += (int)__popcll(bt);
+    }
+    n = nin + took;
+  }
+  wave_lds_sync();
+  // the own block and its `local` predecessors, clipped to [0, own] and to existing blocks,
+  // unless taken already
+  const int64_t own = row_own(g, i);
+  int64_t llo = own - g.local;
+  if (llo < 0) llo = 0;
+  const int64_t lhi = own < g.nbk - 1 ? own : g.nbk - 1;
+  for (int64_t c = llo; c <= lhi; ++c) {  // wave-uniform
+    bool hit = false;
+    for (int e = lane; e < n; e += 64) hit = hit || sel[wv][e] == (unsigned int)c;
+    if (!__any(hit)) {
+      if (lane == 0 && n < kWaveSel) sel[wv][n] = (unsigned int)c;
+      ++n;
+    }
+    wave_lds_sync();
+  }
+  // ascending order: entry e goes to its rank among the (distinct) entries
+  int32_t* out = kv_idx + (bh * g.nbq + i) * W;
+  const int nw = n < (int)W ? n : (int)W;
+  for (int e = lane; e < n; e += 64) {
+    const unsigned int ce = sel[wv][e];
+    int r = 0;
+    for (int f = 0; f < n; ++f) r += sel[wv][f] < ce ? 1 : 0;
+    if (r < (int)W) out[r] = (int32_t)ce;
+  }
+  for (int64_t p = nw + lane; p < W; p += 64) out[p] = 0;
+  if (lane == 0) kv_num[bh * g.nbq + i] = (int32_t)nw;
+}
+
+__global__ void route_clear_kernel(unsigned int* __restrict__ p, int n) {
+  for (int t = threadIdx.x; t < n; t += blockDim.x) p[t] = 0u;
+}
+
 // Rows of at most 64 key blocks without pooling or m3: a workgroup of kFusedRows waves takes
 // rows of one query head and stages the key head's mu / var rows in LDS as fp64 (row stride
 // d + 1 doubles); each wave scores and selects 2^r_log2 rows at once, 64 >> r_log2 lanes per row, no
@@ -1770,8 +2001,13 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                    (m3 == nullptr || a16(m3));
   const bool mfma_ok = vec && d <= 64 * kMaxQReg &&
                        workspace_bytes >= route_row_bytes(nbs) * rows_per_i;
-  const size_t per_row = mfma_ok ? route_row_bytes(nbs) : row_bytes;
-  int64_t chunk = (int64_t)(workspace_bytes / (per_row * rows_per_i));
+  // rows of more than kSmallNbk candidates take the wave select (route_select_wave_kernel) when
+  // the workspace also holds its deferred-row list and counters
+  const bool wave_sel = mfma_ok && nbk > kSmallNbk && pool == 1 && W <= kWaveSel &&
+                        workspace_bytes >= (route_row_bytes(nbs) + 4) * rows_per_i + kRouteTail;
+  const size_t ws_eff = wave_sel ? workspace_bytes - kRouteTail : workspace_bytes;
+  const size_t per_row = mfma_ok ? route_row_bytes(nbs) + (wave_sel ? 4 : 0) : row_bytes;
+  int64_t chunk = (int64_t)(ws_eff / (per_row * rows_per_i));
   // Operands split once (route_split_kernel) when the workspace holds them beside the keys: the
   // candidates of every key head, then per chunk its query rows (bf16 hi + lo, 4 bytes per
   // value, and 3 norms per item), after the chunk's keys, emag and tile maxima.
@@ -1783,10 +2019,10 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
   // (it pays only for long rows: at 1,024 candidates the two split launches cost what the
   // score kernel saves)
   bool presplit = false;
-  if (mfma_ok && nbk > kSmallNbk && workspace_bytes > cand_split + 8 * 256) {
-    const size_t per_split_row = route_row_bytes(nbs) + (size_t)nk * 4 + 12;
+  if (mfma_ok && nbk > kSmallNbk && ws_eff > cand_split + 8 * 256) {
+    const size_t per_split_row = route_row_bytes(nbs) + (size_t)nk * 4 + 12 + (wave_sel ? 4 : 0);
     const int64_t ch =
-        (int64_t)((workspace_bytes - cand_split - 8 * 256) / (per_split_row * rows_per_i));
+        (int64_t)((ws_eff - cand_split - 8 * 256) / (per_split_row * rows_per_i));
     if (ch >= 1) {
       presplit = true;
       chunk = ch;
@@ -1798,6 +2034,8 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
   unsigned int* tmaxp =
       reinterpret_cast<unsigned int*>(emag + (size_t)chunk * rows_per_i * (size_t)ntile);
   SplitOut As{}, Bs{};
+  // end of the keys, tile bounds / maxima (and split operands) of a chunk
+  char* used_end = static_cast<char*>(workspace) + (size_t)chunk * rows_per_i * route_row_bytes(nbs);
   if (presplit) {
     const size_t nrow = (size_t)chunk * rows_per_i;
     char* sp = static_cast<char*>(workspace) +
@@ -1814,10 +2052,26 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     sp += r256(ncand_all * nk * 2);
     Bs.sq = reinterpret_cast<float*>(sp);
     sp += r256(ncand_all * 12);
-    SSA_REQUIRE(sp <= static_cast<char*>(workspace) + workspace_bytes, SSA_ERR_WORKSPACE,
+    SSA_REQUIRE(sp <= static_cast<char*>(workspace) + ws_eff, SSA_ERR_WORKSPACE,
                 "route: split operands overflow the workspace");
+    used_end = sp;
   }
   bool cands_split = false;
+  // the wave select's deferred-row list (chunk rows) and per-chunk counters, cleared once here
+  unsigned int* defer = nullptr;
+  unsigned int* ndef = nullptr;
+  if (wave_sel) {
+    const uintptr_t end = reinterpret_cast<uintptr_t>(workspace) + workspace_bytes;
+    ndef = reinterpret_cast<unsigned int*>((end - 256) & ~(uintptr_t)15);
+    defer = reinterpret_cast<unsigned int*>(
+        (end - kRouteTail - (uintptr_t)chunk * rows_per_i * 4 + 15) & ~(uintptr_t)15);
+    SSA_REQUIRE(used_end <= reinterpret_cast<char*>(defer), SSA_ERR_WORKSPACE,
+                "route: the deferred-row list overlaps the score workspace");
+    const int64_t nchunks = (nbq + chunk - 1) / chunk;
+    route_clear_kernel<<<1, 64, 0, stream>>>(
+        ndef, nchunks < kRouteCounters ? (int)nchunks : kRouteCounters);
+    SSA_TRY(launch_status("route_clear_kernel"));
+  }
 
   RouteGeom g;
   g.mode = mode;
@@ -1955,6 +2209,8 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     const int64_t nrows = B * Hq * g.ni;
     SSA_REQUIRE(nrows < (1ll << 31), SSA_ERR_UNSUPPORTED, "route: too many rows");
     const int qr = d <= 64 ? 1 : d <= 128 ? 2 : d <= 256 ? 4 : 8;  // (cert rows: d <= 512)
+    const int64_t ci = i0 / chunk;  // chunk index: its wave-select counter
+    const bool wave = wave_sel && ca.on && ca.tmax != nullptr && ci < kRouteCounters;
 #define SSA_SELECT(QR)                                                                             \
   do {                                                                                             \
     if (nbk <= 256) /* few candidates: a wave per row */                                           \
@@ -1963,12 +2219,18 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
     else if (nbk <= kSmallNbk)                                                                     \
       route_select_small_kernel<16, QR><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(         \
           keys, g, kv_num, kv_idx, W, nrows, ca);                                                  \
-    else if (nrows < 1024) /* few rows (e.g. a decode step): more threads per row */               \
+    else if (wave) { /* long certified rows: a wave per row, the rows it defers next */          \
+      route_select_wave_kernel<QR><<<(unsigned)((nrows + 3) / 4), 256, 0, stream>>>(             \
+          keys, g, kv_num, kv_idx, W, nrows, ca, defer, ndef + ci);                                \
+      SSA_TRY(launch_status("route_select_wave_kernel"));                                          \
+      route_select_kernel<kSelThreads, QR><<<(unsigned)nrows, kSelThreads, 0, stream>>>(          \
+          keys, g, kv_num, kv_idx, W, ca, defer, ndef + ci);                                       \
+    } else if (nrows < 1024) /* few rows (e.g. a decode step): more threads per row */             \
       route_select_kernel<1024, QR><<<(unsigned)nrows, 1024, 0, stream>>>(keys, g, kv_num, kv_idx, \
-                                                                           W, ca);                 \
+                                                                           W, ca, nullptr, nullptr); \
     else                                                                                           \
       route_select_kernel<kSelThreads, QR><<<(unsigned)nrows, kSelThreads, 0, stream>>>(          \
-          keys, g, kv_num, kv_idx, W, ca);                                                         \
+          keys, g, kv_num, kv_idx, W, ca, nullptr, nullptr);                                       \
   } while (0)
     if (!ca.on || qr == 1) SSA_SELECT(1);
     else if (qr == 2) SSA_SELECT(2);
@@ -2017,11 +2279,14 @@ extern "C" size_t ssa_route_workspace_size_split(int64_t B, int64_t Hq, int64_t 
   const size_t nk = (size_t)(nterms * d), rows = (size_t)(B * Hq * nbq);
   const size_t cands = (size_t)(B * Hkv) * (size_t)nbk;
   const size_t cand_split = 2 * r256(cands * nk * 2) + r256(cands * 12);
-  return rows * (ssa::route_row_bytes(nbk) + nk * 4 + 12) + cand_split + 8 * 256;
+  return rows * (ssa::route_row_bytes(nbk) + 4 + nk * 4 + 12) + cand_split + 8 * 256 +
+         ssa::kRouteTail;
 }
 
 extern "C" size_t ssa_route_workspace_size(int64_t B, int64_t Hq, int64_t nbq, int64_t nbk) {
-  return (size_t)B * (size_t)Hq * (size_t)nbq * ssa::route_row_bytes(nbk);
+  // keys, tile bounds and maxima, and the wave select's deferred-row slot per row; its counters
+  return (size_t)B * (size_t)Hq * (size_t)nbq * (ssa::route_row_bytes(nbk) + 4) +
+         ssa::kRouteTail;
 }
 
 extern "C" int ssa_route(const void* rows, int rows_dtype, const float* mu, const float* var,

@@ -95,10 +95,16 @@ def route_width(mode: str, nbq: int, nbk: int, top_c: int | None, budget_frac: f
                           int(query_pos), int(block)))
 
 
+# Largest router workspace the wrappers allocate (score keys, tile bounds, split operands): rows
+# beyond it are routed in chunks. 4 GiB (1.4 % of an MI355X's HBM) routes a 12.6 M-token head
+# (49,152 blocks) in 3 chunks; at 1 GiB it takes 10 and ~7 % longer.
+ROUTE_WORKSPACE_LIMIT = 4 << 30
+
+
 def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: torch.Tensor | None,
           mode: str, top_c: int | None, budget_frac: float, local: int, coef2: float,
           coef3: float = 0.0, query_pos: int = 0, block: int = 1,
-          workspace_limit: int = 1 << 30, pool: int = 1):
+          workspace_limit: int = ROUTE_WORKSPACE_LIMIT, pool: int = 1):
     """Cumulant router over precomputed summaries -> compact (kv_num, kv_idx).
 
     rows (B, Hq, nbq, d) fp32, fp16 or bf16 (16-bit rows are read as their exact fp32 values, so
@@ -119,7 +125,7 @@ def route(rows: torch.Tensor, mu: torch.Tensor, var: torch.Tensor | None, m3: to
 
 
 def _route_impl(rows, mu, var, m3, mode, top_c, budget_frac, local, coef2, coef3, query_pos,
-                block, workspace_limit=1 << 30, pool=1):
+                block, workspace_limit=ROUTE_WORKSPACE_LIMIT, pool=1):
     _lib.require_device(rows, mu, var, m3)
     B, Hq, nbq, d = rows.shape
     Hkv, nbs = mu.shape[1], mu.shape[2]

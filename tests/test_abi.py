@@ -125,9 +125,9 @@ def test_workspace_queries():
         2 * 128 * 384 * 2 + 256
     assert _lib.query("ssa_sparse_attn_workspace_size", _lib.F32, 1, 2, 300, 64, 128) == 0
     # per routed row: the score keys, then the certified scoring's error magnitude and largest
-    # key per 64-candidate tile
+    # key per 64-candidate tile, and a deferred-row slot of the wave select; then its counters
     assert _lib.query("ssa_route_workspace_size", 1, 14, 1024, 1024) == \
-        14 * 1024 * (1024 * 4 + 16 * 8)
+        14 * 1024 * (1024 * 4 + 16 * 8 + 4) + 512
     assert _lib.query("ssa_decode_attend_workspace_size", 1, 14, 1, 66, 64) == 14 * 66 * 66 * 4
 
 
