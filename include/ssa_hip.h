@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define SSA_ABI_VERSION 6
+#define SSA_ABI_VERSION 7
 
 typedef void* ssa_stream_t; /* hipStream_t */
 
@@ -230,10 +230,21 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
  * (log2 units) take the bounded-row path (no running max; q*scale*log2e rounded to fp16 for the
  * QK product), the others the exact path (fp32 scores scaled in fp32, running max).
  * flags |= SSA_ATTN_EXACT sends every workgroup to the exact path.
+ * flags = SSA_ATTN_PREPARED: ssa_sparse_attn_prepare already wrote this call's per-(k, v) part
+ * of the workspace (V^T and, at d = 64, the key-norm pass), e.g. on another stream while the
+ * router runs; it serves one call (the call consumes the flags it leaves).
  */
-enum { SSA_ATTN_VT_READY = 1, SSA_ATTN_ROTATE = 2, SSA_ATTN_EXACT = 4 };
+enum { SSA_ATTN_VT_READY = 1, SSA_ATTN_ROTATE = 2, SSA_ATTN_EXACT = 4, SSA_ATTN_PREPARED = 8 };
 size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,
                                       int64_t block);
+/* ssa_sparse_attn_prepare: the part of ssa_sparse_attn_fwd that depends on k and v only, into
+ * its workspace (ssa_sparse_attn_workspace_size bytes): V^T, and at head dim 64 the fp16 copy of
+ * K (bf16), the per-tile key-norm maxima and cleared flags, in one pass. strides[6] = k(b,h,n),
+ * v(b,h,n). No counterpart in the reference (FlexAttention builds nothing per (k, v)); it lets a
+ * caller overlap this pass with the routing that needs only q and the key summaries. */
+int ssa_sparse_attn_prepare(const void* k, const void* v, int dtype, int64_t B, int64_t Hkv,
+                            int64_t n, int64_t d, int64_t block, const int64_t* strides,
+                            void* workspace, size_t workspace_bytes, ssa_stream_t stream);
 int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n, int64_t d,
                     int64_t block, int64_t stride_b, int64_t stride_h, int64_t stride_n,
                     void* vt, size_t vt_bytes, ssa_stream_t stream);

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libssa_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 SSA_OK, SSA_ERR_INVALID, SSA_ERR_UNSUPPORTED, SSA_ERR_HIP, SSA_ERR_WORKSPACE = 0, -1, -2, -3, -4
 F32, F16, BF16 = 0, 1, 2
@@ -23,6 +23,7 @@ ROUTE_BUDGET, ROUTE_FLAT, ROUTE_QUERY, ROUTE_STARTED = 0, 1, 2, 3
 ATTN_VT_READY = 1
 ATTN_ROTATE = 2
 ATTN_EXACT = 4
+ATTN_PREPARED = 8
 MASKED_MASKS_READY = 1
 DECODE_STATIC_SCRATCH_BYTES = 16 << 20  # SSA_DECODE_STATIC_SCRATCH_BYTES
 
@@ -61,6 +62,8 @@ _SIGNATURES = {
     "ssa_masked_attn_bwd": (_c_int, [_c_p] * 9 + [_c_int, _c_int, _c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),
     "ssa_sparse_attn_workspace_size": (_c_sz, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "ssa_sparse_attn_prepare": (_c_int, [_c_p, _c_p, _c_int] + [_c_i64] * 5 + [_c_p, _c_p, _c_sz,
+                                                                            _c_p]),
     "ssa_transpose_v": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                  _c_i64, _c_i64, _c_p, _c_sz, _c_p]),
     "ssa_sparse_attn_fwd": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_i64, _c_i64, _c_i64,

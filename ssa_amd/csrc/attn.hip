@@ -1188,6 +1188,49 @@ size_t k16_bytes(int dtype, int64_t B, int64_t Hkv, int64_t n_pad, int64_t d) {
 }  // namespace
 }  // namespace ssa
 
+namespace ssa {
+namespace {
+// The per-(k, v) part of an attention call, into its workspace: V^T (unless vt_ready) and, with
+// `norms` (16-bit, head dim 64), the key-norm pass -- the fp16 copy of K (bf16), the per-tile
+// key-norm maxima and the cleared unbounded / redo flags -- fused with the transpose when both run.
+int attn_prepare(const void* k, const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
+                 int64_t d, int64_t block, int64_t ksb, int64_t ksh, int64_t ksn, int64_t vsb,
+                 int64_t vsh, int64_t vsn, void* workspace, bool vt_ready, bool norms,
+                 hipStream_t st) {
+  const int64_t nbq = (n + block - 1) / block, n_pad = nbq * block, ntile = n_pad / 64;
+  const size_t vt_bytes = ((size_t)B * Hkv * d * n_pad * 2u + 255) / 256 * 256;
+  const size_t k16b = k16_bytes(dtype, B, Hkv, n_pad, d);
+  if (!norms) {
+    if (!vt_ready) {
+      KeyNorm none{};
+      const dim3 tz((unsigned)(n_pad / 64), (unsigned)(B * Hkv), (unsigned)(d / 64));
+      transpose_v_kernel<<<tz, 256, 0, st>>>(static_cast<const char*>(v),
+                                             static_cast<char*>(workspace), Hkv, n, n_pad, vsb,
+                                             vsh, vsn, d, none);
+      return launch_status("transpose_v_kernel");
+    }
+    return SSA_OK;
+  }
+  unsigned short* k16 =
+      k16b ? reinterpret_cast<unsigned short*>(static_cast<char*>(workspace) + vt_bytes) : nullptr;
+  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes + k16b);
+  int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * ntile);
+  int* redo = unbounded + B * Hkv;
+  KeyNorm kn{static_cast<const unsigned short*>(k), ksb, ksh, ksn, dtype == SSA_BF16, tmax2,
+             unbounded, ntile, redo, block, nbq, k16, n_pad};
+  const dim3 tg((unsigned)(n_pad / 64), (unsigned)(B * Hkv));
+  if (vt_ready) {
+    key_norm_max_kernel<<<tg, 256, 0, st>>>(kn, Hkv, n);
+    return launch_status("key_norm_max_kernel");
+  }
+  // V^T and the key norms in one pass
+  transpose_v_kernel<<<tg, 256, 0, st>>>(static_cast<const char*>(v), static_cast<char*>(workspace),
+                                         Hkv, n, n_pad, vsb, vsh, vsn, 64, kn);
+  return launch_status("transpose_v_kernel");
+}
+}  // namespace
+}  // namespace ssa
+
 extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t Hkv, int64_t n,
                                                  int64_t d, int64_t block) {
   if (dtype == SSA_F32 || block <= 0) return 0;
@@ -1198,6 +1241,38 @@ extern "C" size_t ssa_sparse_attn_workspace_size(int dtype, int64_t B, int64_t H
   // (key head, query block)
   const size_t tail = (size_t)(B * Hkv * (n_pad / 64) + B * Hkv + B * Hkv * (n_pad / block)) * 4u;
   return vt + ssa::k16_bytes(dtype, B, Hkv, n_pad, d) + (tail + 255) / 256 * 256;
+}
+
+extern "C" int ssa_sparse_attn_prepare(const void* k, const void* v, int dtype, int64_t B,
+                                       int64_t Hkv, int64_t n, int64_t d, int64_t block,
+                                       const int64_t* strides, void* workspace,
+                                       size_t workspace_bytes, ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(k && v && strides && workspace, SSA_ERR_INVALID,
+              "attn_prepare: NULL pointer argument");
+  SSA_REQUIRE(dtype == SSA_F16 || dtype == SSA_BF16, SSA_ERR_UNSUPPORTED,
+              "attn_prepare: 16-bit dtypes only");
+  SSA_REQUIRE(B > 0 && Hkv > 0 && n > 0, SSA_ERR_INVALID, "attn_prepare: sizes must be positive");
+  SSA_REQUIRE(d == 64 || d == 128 || d == 256 || d == 512, SSA_ERR_UNSUPPORTED,
+              "attn_prepare: head_dim must be 64, 128, 256 or 512");
+  SSA_REQUIRE(block == 64 || (block > 0 && block % 128 == 0), SSA_ERR_UNSUPPORTED,
+              "attn_prepare: block %lld unsupported (64 or a multiple of 128)", (long long)block);
+  SSA_REQUIRE(n + block < (1ll << 31), SSA_ERR_UNSUPPORTED, "attn_prepare: n too large");
+  for (int s = 0; s < 6; ++s)
+    SSA_REQUIRE(strides[s] % 8 == 0, SSA_ERR_UNSUPPORTED,
+                "attn_prepare: stride %d (%lld) not a multiple of 16 bytes", s,
+                (long long)strides[s]);
+  SSA_REQUIRE(aligned16(k) && aligned16(v) && aligned16(workspace), SSA_ERR_UNSUPPORTED,
+              "attn_prepare: tensors must be 16-byte aligned");
+  const size_t need = ssa_sparse_attn_workspace_size(dtype, B, Hkv, n, d, block);
+  SSA_REQUIRE(workspace_bytes >= need, SSA_ERR_WORKSPACE,
+              "attn_prepare: workspace needs %zu bytes", need);
+  const int64_t n_pad = (n + block - 1) / block * block;
+  SSA_REQUIRE(B * Hkv < 65536 && n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
+              "attn_prepare: grid too large");
+  return attn_prepare(k, v, dtype, B, Hkv, n, d, block, strides[0], strides[1], strides[2],
+                      strides[3], strides[4], strides[5], workspace, false, d == 64,
+                      static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ssa_transpose_v(const void* v, int dtype, int64_t B, int64_t Hkv, int64_t n,
@@ -1250,7 +1325,8 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(B * Hq < (1ll << 24), SSA_ERR_UNSUPPORTED, "sparse_attn: too many heads");
   SSA_REQUIRE(n + block < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "sparse_attn: n = %lld too large (key positions are 32-bit)", (long long)n);
-  SSA_REQUIRE((flags & ~(SSA_ATTN_VT_READY | SSA_ATTN_ROTATE | SSA_ATTN_EXACT)) == 0,
+  SSA_REQUIRE((flags & ~(SSA_ATTN_VT_READY | SSA_ATTN_ROTATE | SSA_ATTN_EXACT |
+                          SSA_ATTN_PREPARED)) == 0,
               SSA_ERR_INVALID,
               "sparse_attn: unknown flags");
   const int64_t vec = dtype == SSA_F32 ? 4 : 8;
@@ -1302,25 +1378,15 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
   SSA_REQUIRE(B * Hkv < 65536 && p.n_pad / 64 < (1ll << 31), SSA_ERR_UNSUPPORTED,
               "sparse_attn: grid too large");
   // after V^T: the fp16 copy of K (bf16, head dim 64), the per-tile key-norm maxima, then mode
-  // 1's unbounded flags (all written by the key-norm pass below, every entry every call)
+  // 1's unbounded flags (all written by the key-norm pass, every entry; by ssa_sparse_attn_prepare
+  // for a SSA_ATTN_PREPARED call)
   const size_t vt_bytes = ((size_t)B * Hkv * d * p.n_pad * 2u + 255) / 256 * 256;
   const size_t k16b = k16_bytes(dtype, B, Hkv, p.n_pad, d);
-  unsigned short* k16 =
-      k16b ? reinterpret_cast<unsigned short*>(static_cast<char*>(workspace) + vt_bytes) : nullptr;
-  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes + k16b);
-  int* unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
-  int* redo = unbounded + B * Hkv;
-  KeyNorm kn{static_cast<const unsigned short*>(k), p.ksb, p.ksh, p.ksn, dtype == SSA_BF16, tmax2,
-             unbounded, p.ntile, redo, block, p.nbq, k16, p.n_pad};
-  if (d != 64 || (flags & SSA_ATTN_EXACT)) {  // exact path only: V^T (unless supplied), no key norms
-    if (!(flags & SSA_ATTN_VT_READY)) {
-      KeyNorm none{};
-      const dim3 tz((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv), (unsigned)(d / 64));
-      transpose_v_kernel<<<tz, 256, 0, st>>>(static_cast<const char*>(v),
-                                             static_cast<char*>(workspace), Hkv, n, p.n_pad,
-                                             p.vsb, p.vsh, p.vsn, d, none);
-      SSA_TRY(launch_status("transpose_v_kernel"));
-    }
+  const bool norms = d == 64 && !(flags & SSA_ATTN_EXACT);
+  if (!(flags & SSA_ATTN_PREPARED))
+    SSA_TRY(attn_prepare(k, v, dtype, B, Hkv, n, d, block, p.ksb, p.ksh, p.ksn, p.vsb, p.vsh,
+                         p.vsn, workspace, (flags & SSA_ATTN_VT_READY) != 0, norms, st));
+  if (!norms) {  // exact path only
     if (d == 512) {  // head dim split across 4 waves, 32 query rows per workgroup
       p.qsub = block / 32;
       p.group = p.G * p.qsub;
@@ -1334,19 +1400,11 @@ extern "C" int ssa_sparse_attn_fwd(const void* q, const void* k, const void* v, 
     if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, d, st);
     return launch_mfma<SSA_F16>(p, d, st);
   }
-  const dim3 tg((unsigned)(p.n_pad / 64), (unsigned)(B * Hkv));
-  if (flags & SSA_ATTN_VT_READY) {
-    key_norm_max_kernel<<<tg, 256, 0, st>>>(kn, Hkv, n);
-    SSA_TRY(launch_status("key_norm_max_kernel"));
-  } else {  // V^T and the key norms in one pass
-    transpose_v_kernel<<<tg, 256, 0, st>>>(static_cast<const char*>(v), static_cast<char*>(workspace),
-                                           Hkv, n, p.n_pad, p.vsb, p.vsh, p.vsn, 64, kn);
-    SSA_TRY(launch_status("transpose_v_kernel"));
-  }
+  float* tmax2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vt_bytes + k16b);
   p.tmax2 = tmax2;
-  p.unbounded = unbounded;
-  p.redo = redo;
-  p.k16 = reinterpret_cast<const char*>(k16);
+  p.unbounded = reinterpret_cast<int*>(tmax2 + B * Hkv * p.ntile);
+  p.redo = p.unbounded + B * Hkv;
+  p.k16 = k16b ? static_cast<const char*>(workspace) + vt_bytes : nullptr;
   if (dtype == SSA_BF16) return launch_mfma<SSA_BF16>(p, 64, st);
   return launch_mfma<SSA_F16>(p, 64, st);
 }

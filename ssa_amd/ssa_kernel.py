@@ -204,10 +204,51 @@ def transpose_v(v: torch.Tensor, block: int) -> torch.Tensor:
     return vt
 
 
+class PreparedKV:
+    """The per-(k, v) part of one sparse_attention call (ssa_sparse_attn_prepare): V^T and, at
+    head dim 64, the fp16 key copy, per-tile key-norm maxima and cleared flags, in the call's
+    workspace. Built by prepare_attention, consumed by one sparse_attention(prepared=...) call."""
+
+    def __init__(self, ws, shape, dtype, block, device):
+        self.ws, self.shape, self.dtype, self.block, self.device = ws, shape, dtype, block, device
+        self.used = False
+
+
+def prepare_attention(k: torch.Tensor, v: torch.Tensor, block: int,
+                      workspace: torch.Tensor | None = None) -> PreparedKV:
+    """k, v (B, Hkv, n, d) 16-bit -> the PreparedKV of one sparse_attention call on them, written
+    on the current stream. It depends on k and v only, so it can run on a second stream while the
+    router (which needs q and the key summaries) runs on the first; the attention call then skips
+    that pass. Head dims 64 / 128 / 256 / 512, block 64 or a multiple of 128.
+    `workspace`: a uint8 device buffer of at least ssa_sparse_attn_workspace_size bytes to write
+    into (e.g. one buffer reused step after step, no allocation per call); the caller orders this
+    call after the previous attention call that read it."""
+    _lib.require_device(k, v)
+    if k.dtype != v.dtype or k.shape != v.shape or k.dim() != 4:
+        raise ValueError("prepare_attention: k and v must be (B, Hkv, n, d) of one dtype")
+    k, v = _aligned(k), _aligned(v)
+    B, Hkv, n, d = k.shape
+    dt = _lib.dtype_code(k.dtype)
+    nbytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
+    if workspace is None:
+        ws = torch.empty(max(nbytes, 16), device=k.device, dtype=torch.uint8)
+    else:
+        if (workspace.dtype != torch.uint8 or workspace.device != k.device
+                or not workspace.is_contiguous() or workspace.numel() < nbytes):
+            raise ValueError(f"prepare_attention: workspace must be a contiguous uint8 tensor of "
+                             f">= {nbytes} bytes on {k.device}")
+        ws = workspace
+    strides = _lib.i64_array([*_bhn_strides(k), *_bhn_strides(v)])
+    _lib.call("ssa_sparse_attn_prepare", k.data_ptr(), v.data_ptr(), dt, B, Hkv, n, d, block,
+              strides, ws.data_ptr(), nbytes, _lib.stream_of(k))
+    return PreparedKV(ws, (B, Hkv, n, d), k.dtype, block, k.device)
+
+
 def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: torch.Tensor,
                      kv_idx: torch.Tensor, block: int, scale: float | None = None,
                      out: torch.Tensor | None = None, return_lse: bool = False,
-                     vt: torch.Tensor | None = None, rotate: bool = False, exact: bool = False):
+                     vt: torch.Tensor | None = None, rotate: bool = False, exact: bool = False,
+                     prepared: PreparedKV | None = None):
     """Block-sparse causal attention on the compact contract (replaces FlexAttention with
     BlockMask.from_kv_blocks + mask_mod kv<=q & kv<n; ssa/ssa_kernel.py:125-126,
     ssa/gemma_ssa.py:159-162,179).
@@ -223,6 +264,8 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
     `exact`: every row takes the exact running-max softmax on fp32-scaled scores (by default rows
     whose scores provably stay within +-32 log2 units take the bounded-row path, which rounds
     q*scale*log2e to fp16 for the QK product).
+    `prepared`: prepare_attention(k, v, block) of these k and v (not yet used by another call);
+    the call then skips its V^T / key-norm pass.
     Returns out (and lse (B, Hq, n) fp32 if requested).
     """
     if torch.compiler.is_compiling():  # V^T is rebuilt inside the op (vt is a cache only)
@@ -237,11 +280,11 @@ def sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_num: 
             o = out
         return (o, lse) if return_lse else o
     return _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale, out, return_lse, vt,
-                                  rotate, exact)
+                                  rotate, exact, prepared)
 
 
 def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
-                           return_lse=False, vt=None, rotate=False, exact=False):
+                           return_lse=False, vt=None, rotate=False, exact=False, prepared=None):
     _lib.require_device(q, k, v, kv_num, kv_idx)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share a dtype")
@@ -270,7 +313,19 @@ def _sparse_attention_impl(q, k, v, kv_num, kv_idx, block, scale=None, out=None,
     dt = _lib.dtype_code(q.dtype)
     ws_bytes = int(_lib.query("ssa_sparse_attn_workspace_size", dt, B, Hkv, n, d, block))
     flags = 0
-    if vt is not None and dt != _lib.F32:
+    if prepared is not None:
+        if vt is not None:
+            raise ValueError("sparse_attention: pass vt or prepared, not both")
+        if (prepared.shape != (B, Hkv, n, d) or prepared.dtype != v.dtype
+                or prepared.block != block or prepared.device != q.device or dt == _lib.F32):
+            raise ValueError("sparse_attention: `prepared` was built for other k / v / block")
+        if prepared.used:
+            raise ValueError("sparse_attention: a PreparedKV serves one call")
+        prepared.used = True
+        # (built on another stream, perhaps: keep its memory until this stream's work is done)
+        prepared.ws.record_stream(torch.cuda.current_stream(q.device))
+        ws, flags = prepared.ws, _lib.ATTN_PREPARED
+    elif vt is not None and dt != _lib.F32:
         n_pad = -(-n // block) * block
         room = vt.untyped_storage().nbytes() - vt.storage_offset() * vt.element_size()
         if (tuple(vt.shape) != (B, Hkv, d, n_pad) or vt.dtype != v.dtype or room < ws_bytes

@@ -220,6 +220,36 @@ def test_certified_router_band_cases(cuda, nbk, case):
             assert gi[0, h, r, :gn[0, h, r]].tolist() == sel, (case, nbk, h, r)
 
 
+@pytest.mark.parametrize("d, terms, pool, limit", [
+    (64, "mu", 1, None), (64, "mu_var", 1, None), (64, "mu_var_m3", 1, None),
+    (128, "mu_var", 1, None), (32, "mu_var", 1, 6 << 20), (64, "mu_var", 2, None)])
+def test_route_strip_scoring_matches_oracle(cuda, d, terms, pool, limit):
+    """Rows of more than 1024 candidates score with the row operands held in registers, a strip
+    of 128 rows per workgroup (contractions of 64, 128, 192 and 256 values: d x terms). Budget
+    mode over 1300 blocks with 2 query heads per key head: 2600 rows in 21 strips (the last one
+    partial, one straddling the heads), rows of 0 to 1299 candidates (21 tiles, two segments);
+    one case routes in row chunks (a 6 MiB workspace), one max-pools 2 sub-blocks per block (no
+    tile maxima). Every row against the oracle's selection."""
+    rng = np.random.default_rng(47)
+    nb, hq, keep = 1300, 2, 64
+    rows = rng.standard_normal((1, hq, nb, d)).astype(np.float32)
+    mu = (rng.standard_normal((1, 1, nb * pool, d)) * 0.3).astype(np.float32)
+    var = rng.uniform(0.5, 1.5, (1, 1, nb * pool, d)).astype(np.float32) if "var" in terms else None
+    m3 = (rng.standard_normal((1, 1, nb * pool, d)) * 0.2).astype(np.float32) \
+        if "m3" in terms else None
+    coef2, coef3 = (1.0 if var is not None else 0.0), (0.25 if m3 is not None else 0.0)
+    t = lambda x: None if x is None else dev(x, torch.float32, cuda)
+    kw = {} if limit is None else {"workspace_limit": limit}
+    kv_num, kv_idx = K.route(t(rows), t(mu), t(var), t(m3), "budget", keep, 0.0, 1, coef2,
+                             coef3, pool=pool, **kw)
+    gn, gi = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    keys = O.score_keys(O.pool_max(O.scores(rows, mu, var, coef2, m3, coef3), pool))
+    for h in range(hq):
+        for i in range(nb):
+            sel = O.select_row(keys[0, h, i], i, "budget", keep, 0.0, 1)
+            assert gi[0, h, i, :gn[0, h, i]].tolist() == sel, (d, terms, pool, h, i)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(4, 1, 3, 40, "started"), (2, 1, 1, 500, "query"),
                                    (4, 2, 24, 300, "query"), (1, 1, 200, 200, "budget")])
@@ -1106,6 +1136,41 @@ def test_tiled_prefill_wide_head_dims_match_oracle(cuda, d, dtype, block):
     vtr = K.transpose_v(vt_, block)
     out2 = K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, vt=vtr)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype,d,block,exact", [(torch.bfloat16, 64, 128, False),
+                                                (torch.float16, 64, 256, False),
+                                                (torch.bfloat16, 64, 128, True),
+                                                (torch.bfloat16, 128, 128, False),
+                                                (torch.float16, 512, 64, False)])
+def test_prepared_attention_matches_unprepared(cuda, dtype, d, block, exact):
+    """prepare_attention on a second stream (V^T and the key-norm pass, overlapping nothing here
+    but ordered by an event) + sparse_attention(prepared=...) gives the same output, bit for bit,
+    as the call that prepares for itself; a PreparedKV serves one call and must match k, v and
+    the block."""
+    rng = np.random.default_rng(d + block)
+    n, hq, hkv = 1100, 4, 2
+    q, k, v = (WL.round_to(rng.standard_normal((1, h_, n, d)).astype(np.float32), dtype)
+               for h_ in (hq, hkv, hkv))
+    kv_num, kv_idx = O.route_budget(q, k, block, budget_frac=0.4, local=1, beta=2.0, n_real=n)
+    qt, kt, vt_ = (dev(x, dtype, cuda) for x in (q, k, v))
+    num_t, idx_t = torch.from_numpy(kv_num).to(cuda), torch.from_numpy(kv_idx).to(cuda)
+    ref = K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, exact=exact)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        prep = K.prepare_attention(kt, vt_, block)
+        done = torch.cuda.Event()
+        done.record(side)
+    torch.cuda.current_stream().wait_event(done)
+    out = K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, exact=exact, prepared=prep)
+    assert torch.equal(out, ref)
+    with pytest.raises(ValueError):
+        K.sparse_attention(qt, kt, vt_, num_t, idx_t, block, prepared=prep)
+    if d == 64 and block == 128:
+        with pytest.raises(ValueError):
+            K.sparse_attention(qt, kt, vt_, num_t, idx_t, 256, prepared=K.prepare_attention(
+                kt, vt_, block))
 
 
 def test_d512_tiled_prefill_gemma_shape_beats_per_row_path(cuda):
