@@ -18,6 +18,8 @@
 // ssa/gemma_ssa.py:99-131 (_selection_mask).
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "select.h"
 
@@ -815,6 +817,212 @@ __global__ __launch_bounds__(256) void route_score_split_kernel(
       const int64_t lrow = row_key[lane];
       emag[lrow * ntile + ct] = f;
       if constexpr (TMAX) tmax[lrow * ntile + ct] = smax[lane];
+    }
+  }
+}
+
+// route_score_split_kernel's products for long rows with the row operands held in registers: a
+// workgroup takes a strip of kStripRows chunk rows (wave w: rows 32w .. 32w+31, lane l holding
+// A[row 32w + l%32][16 ks + 8 (l/32) .. +8] for every 16-value step ks of the contraction, hi and
+// lo parts) and walks a segment of kStripSeg candidate tiles, staging each tile's 64 candidates
+// (hi and lo rows of NK values, padded to NK + 8: a ds_read_b128 phase of 16 lanes covers the 64
+// banks once) in LDS, the next tile's loads in flight in registers meanwhile; per tile every
+// wave forms its 32 x 64 block as two 32 x 32 MFMA blocks with the same operands and the same
+// product order as route_score_split_kernel, so the keys, emag and tile maxima are the same bits.
+// The key operands are then read once per 128-row strip instead of once per 64-row tile (C5: 1.2
+// instead of 8.9 GB per route), leaving the kernel bound by the keys it writes. Grid:
+// segment-major (block x = segment * nstrips + strip): the strips running together share the
+// segment's candidate tiles in L2.
+constexpr int kStripRows = 128;
+constexpr int kStripSeg = 16;
+
+template <int NKS, bool TMAX>
+__global__ __launch_bounds__(256) void route_score_strip_kernel(
+    SplitOut A, SplitOut Bs, RouteGeom g, unsigned int* __restrict__ keys,
+    float* __restrict__ emag, unsigned int* __restrict__ tmax, int64_t ntile, int64_t nstrips) {
+  constexpr int NK = NKS * 16;
+  constexpr int LD = NK + 8;
+  constexpr int kPieces = kTile * NK / 8;  // 16-byte pieces per part of a staged tile
+  __shared__ __attribute__((aligned(16))) unsigned short sb[2][kTile][LD];
+  __shared__ int64_t row_key[kStripRows];  // chunk row index of the strip's rows (-1: none)
+  __shared__ int64_t row_cm[kStripRows];   // scored candidates of the strip's rows (0: none)
+
+  const int64_t bk = blockIdx.y;  // b * Hkv + kvh
+  const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
+  const int64_t seg = blockIdx.x / nstrips, st = blockIdx.x % nstrips;
+  const int64_t R = g.G * g.ni;
+  const int64_t r0 = st * kStripRows;
+  if (r0 >= R) return;
+  const int64_t r_last = r0 + kStripRows - 1 < R ? r0 + kStripRows - 1 : R - 1;
+  const int64_t imax = (r0 / g.ni != r_last / g.ni) ? g.i0 + g.ni - 1 : g.i0 + r_last % g.ni;
+  const int64_t cmax = row_cmax_s(g, imax);
+  const int64_t ct0 = seg * kStripSeg;
+  if (ct0 * kTile >= cmax) return;  // uniform: no row of the strip has these candidates
+  const int64_t ct_end = (cmax + kTile - 1) / kTile;
+  const int64_t ct1 = ct0 + kStripSeg < ct_end ? ct0 + kStripSeg : ct_end;
+  const int64_t nbs = g.nbk * g.pool;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid < kStripRows) {
+    const int64_t r = r0 + tid;
+    int64_t lr = -1, cm = 0;
+    if (r < R) {
+      const int64_t h = kvh * g.G + r / g.ni;
+      const int64_t il = r % g.ni;
+      lr = (b * g.Hq + h) * g.ni + il;
+      cm = row_cmax_s(g, g.i0 + il);
+    }
+    row_key[tid] = lr;
+    row_cm[tid] = cm;
+  }
+  __syncthreads();
+  const int ra = w * 32 + (lane & 31);
+  const int64_t lra = row_key[ra];
+  const int64_t cma = row_cm[ra];
+  bf16x8 ah[NKS], al[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    u32x4 h = {0u, 0u, 0u, 0u}, l = h;
+    if (lra >= 0) {
+      const int64_t off = lra * NK + ks * 16 + (lane >> 5) * 8;
+      h = *reinterpret_cast<const u32x4*>(A.hi + off);
+      l = *reinterpret_cast<const u32x4*>(A.lo + off);
+    }
+    ah[ks] = __builtin_bit_cast(bf16x8, h);
+    al[ks] = __builtin_bit_cast(bf16x8, l);
+  }
+  double sa[3];  // square roots of the row's term norms (emag)
+#pragma unroll
+  for (int t = 0; t < 3; ++t) sa[t] = sqrt((double)(lra >= 0 ? A.sq[lra * 3 + t] : 0.0f));
+  // rows of this lane's accumulator entries j: 32w + (j/4)*8 + (l/32)*4 + j%4
+  const int rbase = w * 32 + (lane >> 5) * 4;
+
+  // the next tile's pieces and candidate norms (lane = candidate) are loaded into registers
+  // while the current tile is multiplied
+  constexpr int kPer = 2 * kPieces / 256;
+  u32x4 pf[kPer];
+  float pn[3];
+  const auto fetch = [&](int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + 256 * i;
+      const int part = p / kPieces, rem = p % kPieces;
+      const int64_t c = c0 + rem / (NK / 8);
+      pf[i] = u32x4{0u, 0u, 0u, 0u};
+      if (c < nbs)
+        pf[i] = *reinterpret_cast<const u32x4*>((part ? Bs.lo : Bs.hi) + (bk * nbs + c) * NK +
+                                                (rem % (NK / 8)) * 8);
+    }
+    const int64_t cl = c0 + lane;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) pn[t] = cl < nbs ? Bs.sq[(bk * nbs + cl) * 3 + t] : 0.0f;
+  };
+  fetch(ct0 * kTile);
+  for (int64_t ct = ct0; ct < ct1; ++ct) {
+    const int64_t c0 = ct * kTile;
+    __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + 256 * i;
+      const int part = p / kPieces, rem = p % kPieces;
+      *reinterpret_cast<u32x4*>(&sb[part][rem / (NK / 8)][(rem % (NK / 8)) * 8]) = pf[i];
+    }
+    float M[3] = {pn[0], pn[1], pn[2]};
+    __syncthreads();
+    if (ct + 1 < ct1) fetch(c0 + kTile);
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      acc0[j] = 0.0f;
+      acc1[j] = 0.0f;
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int kk = ks * 16 + (lane >> 5) * 8;
+      const bf16x8 bh0 = *reinterpret_cast<const bf16x8*>(&sb[0][lane & 31][kk]);
+      const bf16x8 bl0 = *reinterpret_cast<const bf16x8*>(&sb[1][lane & 31][kk]);
+      const bf16x8 bh1 = *reinterpret_cast<const bf16x8*>(&sb[0][32 + (lane & 31)][kk]);
+      const bf16x8 bl1 = *reinterpret_cast<const bf16x8*>(&sb[1][32 + (lane & 31)][kk]);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks], bh0, acc0, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks], bl0, acc0, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks], bh0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks], bh1, acc1, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks], bl1, acc1, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks], bh1, acc1, 0, 0, 0);
+    }
+    const int64_t cA = c0 + (lane & 31), cB = cA + 32;
+    unsigned int m[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int rl = rbase + (j >> 2) * 8 + (j & 3);
+      const int64_t cm = row_cm[rl];
+      unsigned int* kr = keys + row_key[rl] * nbs;
+      unsigned int k0 = 0u, k1 = 0u;
+      if (cA < cm) {
+        k0 = score_key(acc0[j]);
+        kr[cA] = k0;
+      }
+      if (cB < cm) {
+        k1 = score_key(acc1[j]);
+        kr[cB] = k1;
+      }
+      m[j] = k0 > k1 ? k0 : k1;
+    }
+    if constexpr (TMAX) {
+      // row maxima over the 32 lanes of each half-wave: a transposing butterfly (at the step of
+      // xor mask s a lane keeps the half of its values that its bit s selects and takes the other
+      // half's maxima from its partner), 8 + 4 + 2 + 1 + 1 shuffles for 16 rows
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool up = lane & 16;
+        const unsigned int keep = up ? m[i + 8] : m[i], send = up ? m[i] : m[i + 8];
+        const unsigned int o = __shfl_xor(send, 16, 64);
+        m[i] = keep > o ? keep : o;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool up = lane & 8;
+        const unsigned int keep = up ? m[i + 4] : m[i], send = up ? m[i] : m[i + 4];
+        const unsigned int o = __shfl_xor(send, 8, 64);
+        m[i] = keep > o ? keep : o;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const bool up = lane & 4;
+        const unsigned int keep = up ? m[i + 2] : m[i], send = up ? m[i] : m[i + 2];
+        const unsigned int o = __shfl_xor(send, 4, 64);
+        m[i] = keep > o ? keep : o;
+      }
+      {
+        const bool up = lane & 2;
+        const unsigned int keep = up ? m[1] : m[0], send = up ? m[0] : m[1];
+        const unsigned int o = __shfl_xor(send, 2, 64);
+        m[0] = keep > o ? keep : o;
+      }
+      const unsigned int o = __shfl_xor(m[0], 1, 64);
+      const unsigned int mx = m[0] > o ? m[0] : o;
+      // lane l now holds the maximum of entry j = (l % 32) / 2
+      const int j = (lane & 31) >> 1;
+      const int rl = rbase + (j >> 2) * 8 + (j & 3);
+      if ((lane & 1) == 0 && c0 < row_cm[rl]) tmax[row_key[rl] * ntile + ct] = mx;
+    }
+    // emag of the strip's rows: sqrt of the tile's largest candidate norms per term
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) M[t] = fmaxf(M[t], __shfl_xor(M[t], off, 64));
+    if (lane < 32 && c0 < cma) {
+      double mag = 0.0, nsum = 0.0;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const double a = sa[t], bb = sqrt((double)M[t]);
+        mag += a * bb;
+        nsum += a + bb;
+      }
+      mag += 0x1p-56 * nsum;
+      float f = (float)mag;
+      if ((double)f < mag) f = __uint_as_float(__float_as_uint(f) + 1u);  // round up (f >= 0)
+      emag[lra * ntile + ct] = f;
     }
   }
 }
@@ -2169,13 +2377,36 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
         route_split_kernel<true><<<(unsigned)((nrow + 3) / 4), 256, 0, stream>>>(
             rows, nullptr, var, m3, g, (int)d, nt, coef2, coef3, nrow, As);
         SSA_TRY(launch_status("route_split_kernel"));
-        if (tm)
-          route_score_split_kernel<true><<<grid, 256, 0, stream>>>(
-              As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
-        else
-          route_score_split_kernel<false><<<grid, 256, 0, stream>>>(
-              As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
-        SSA_TRY(launch_status("route_score_split_kernel"));
+        if (nk == 64 || nk == 128 || nk == 192 || nk == 256) {
+          // the row operands in registers, a strip of rows per workgroup
+          const int64_t nstrips = (R + kStripRows - 1) / kStripRows;
+          const int64_t nseg = (cand_tiles + kStripSeg - 1) / kStripSeg;
+          SSA_REQUIRE(nstrips * nseg < (1ll << 31), SSA_ERR_UNSUPPORTED,
+                      "route: score grid too large");
+          const dim3 sgrid((unsigned)(nstrips * nseg), (unsigned)(B * Hkv));
+          const auto strip = [&](auto nks) {
+            constexpr int N = decltype(nks)::value;
+            if (tm)
+              route_score_strip_kernel<N, true><<<sgrid, 256, 0, stream>>>(
+                  As, Bs, g, keys, emag, tmaxp, ntile, nstrips);
+            else
+              route_score_strip_kernel<N, false><<<sgrid, 256, 0, stream>>>(
+                  As, Bs, g, keys, emag, tmaxp, ntile, nstrips);
+          };
+          if (nk == 64) strip(std::integral_constant<int, 4>{});
+          else if (nk == 128) strip(std::integral_constant<int, 8>{});
+          else if (nk == 192) strip(std::integral_constant<int, 12>{});
+          else strip(std::integral_constant<int, 16>{});
+          SSA_TRY(launch_status("route_score_strip_kernel"));
+        } else {
+          if (tm)
+            route_score_split_kernel<true><<<grid, 256, 0, stream>>>(
+                As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
+          else
+            route_score_split_kernel<false><<<grid, 256, 0, stream>>>(
+                As, Bs, g, (int)nk, keys, emag, tmaxp, ntile, row_tiles, cand_tiles);
+          SSA_TRY(launch_status("route_score_split_kernel"));
+        }
       } else {
 #define SSA_SCORE_MFMA(E, T)                                                                       \
   route_score_mfma_kernel<E, T><<<grid, 256, 0, stream>>>(rows, mu, var, m3, g, (int)d, coef2,    \
