@@ -1566,6 +1566,90 @@ __device__ inline unsigned int select_first(const unsigned int (&key)[kSmallJ], 
   for (int j = 0; j < J; ++j) k2[j] = key[j];
   return wave_select_top<J>(k2, cm, K, ncand);
 }
+// wave_kth_key over J slots, except that the search stops early (at a value with exactly K keys
+// at or above it) only at trial values >= floor_: the slots hold only the keys >= floor_.
+template <int J>
+__device__ inline unsigned int wave_kth_key_above(const unsigned int (&key)[J], int64_t K,
+                                                  unsigned int floor_) {
+  unsigned int all = 0xffffffffu, any = 0u;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    all &= key[j] ? key[j] : 0xffffffffu;
+    any |= key[j];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    all &= lane_xor(all, off);
+    any |= lane_xor(any, off);
+  }
+  const unsigned int diff = all ^ any;
+  if (diff == 0u) return all;
+  const int top = 31 - __clz(diff);
+  unsigned int T = top == 31 ? 0u : all & ~((2u << top) - 1u);
+  for (int bit = top; bit >= 0; --bit) {
+    const unsigned int t = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) cnt += __popcll(__ballot(key[j] >= t));
+    if (cnt >= K) {
+      T = t;
+      if (cnt == K && t >= floor_) break;  // wave-uniform
+    }
+  }
+  return T;
+}
+
+// kth_slots on fewer slots: T0, the K-th largest of the lanes' maxima (K <= 64), is at most the
+// K-th largest key (K lanes hold a key >= T0), so the search runs over the keys >= T0 alone,
+// compacted through the wave's LDS buffer `buf` (64 kSmallJ entries) into 2, 4 or 8 slots. It
+// returns the K-th largest key or a value with exactly K keys at or above it, as kth_slots does
+// (not always the same value: the certified selection is the same for either).
+template <int kSmallJ>
+__device__ inline unsigned int kth_filtered(const unsigned int (&key)[kSmallJ], int64_t K,
+                                            int jeff, unsigned int* buf) {
+  if (jeff <= 2 || K <= 0 || K > 64) return kth_slots<kSmallJ>(key, K, jeff);
+  const int lane = threadIdx.x & 63;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  unsigned int mx = 0u;
+#pragma unroll
+  for (int j = 0; j < kSmallJ; ++j) mx = key[j] > mx ? key[j] : mx;
+  unsigned int t0;
+  if (K == 64) {  // the smallest lane maximum (0 when a lane holds no candidate)
+    t0 = mx;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const unsigned int o = lane_xor(t0, off);
+      t0 = o < t0 ? o : t0;
+    }
+  } else {
+    const unsigned int m1[1] = {mx};
+    t0 = wave_kth_key<1>(m1, K);  // 0 when fewer than K lanes hold a candidate
+  }
+  if (t0 == 0u) return kth_slots<kSmallJ>(key, K, jeff);
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < kSmallJ; ++j) {
+    const bool take = key[j] >= t0;
+    const unsigned long long bt = __ballot(take);
+    if (take) buf[n + (int)__popcll(bt & lt)] = key[j];
+    n += (int)__popcll(bt);
+  }
+  wave_lds_sync();
+  const auto search = [&](auto jc) -> unsigned int {
+    constexpr int J = decltype(jc)::value;
+    unsigned int s[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) s[j] = lane + 64 * j < n ? buf[lane + 64 * j] : 0u;
+    wave_lds_sync();  // the buffer is free for the wave's next use
+    return wave_kth_key_above<J>(s, K, t0);
+  };
+  if (n <= 128) return search(std::integral_constant<int, 2>{});
+  if (n <= 256) return search(std::integral_constant<int, 4>{});
+  if constexpr (kSmallJ >= 8)
+    if (n <= 512) return search(std::integral_constant<int, 8>{});
+  return kth_slots<kSmallJ>(key, K, jeff);
+}
+
 template <int kSmallJ>
 __device__ inline unsigned int select_slots(const unsigned int (&key)[kSmallJ], unsigned int cm,
                                             int64_t K, int64_t ncand, int jeff) {
@@ -1613,7 +1697,8 @@ __global__ __launch_bounds__(256) void route_select_small_kernel(
   const int jeff = (int)((cmax + 63) / 64);  // slots holding candidates (wave-uniform)
   if (ca.on && K > 0 && K < cmax) {
     float M = cert_emag_max(ca, lrow, cmax * g.pool, lane, 64);
-    const unsigned int T = kth_slots<kSmallJ>(key, K, jeff);
+    __shared__ unsigned int kbuf[4][64 * kSmallJ];
+    const unsigned int T = kth_filtered<kSmallJ>(key, K, jeff, kbuf[threadIdx.x >> 6]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     unsigned int lo, hi;
