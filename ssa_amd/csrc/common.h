@@ -117,10 +117,11 @@ __device__ inline void wave_lds_sync() {
 // onto +0 so the two compare equal, as they do for torch.topk; NaN maps above +inf (torch.topk
 // treats NaN as the largest value).
 __device__ inline unsigned int score_key(float r) {
-  if (r != r) return 0xffffffffu;
-  if (r == 0.0f) r = 0.0f;
   unsigned int u = __float_as_uint(r);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  u = u == 0x80000000u ? 0u : u;  // -0 -> +0
+  // negative: all bits flipped; otherwise the sign bit set
+  const unsigned int k = u ^ ((unsigned int)((int)u >> 31) | 0x80000000u);
+  return r != r ? 0xffffffffu : k;
 }
 
 }  // namespace ssa

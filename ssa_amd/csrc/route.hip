@@ -830,14 +830,14 @@ __global__ __launch_bounds__(256) void route_score_split_kernel(
 // wave forms its 32 x 64 block as two 32 x 32 MFMA blocks with the same operands and the same
 // product order as route_score_split_kernel, so the keys, emag and tile maxima are the same bits.
 // The key operands are then read once per 128-row strip instead of once per 64-row tile (C5: 1.2
-// instead of 8.9 GB per route), leaving the kernel bound by the keys it writes. Grid:
-// segment-major (block x = segment * nstrips + strip): the strips running together share the
-// segment's candidate tiles in L2.
+// instead of 8.9 GB per route). Contractions of 64 or 128 values (NKS 4, 8: the row fragments
+// and two waves per SIMD fit the registers). Grid: segment-major (block x = segment * nstrips +
+// strip): the strips running together share the segment's candidate tiles in L2.
 constexpr int kStripRows = 128;
 constexpr int kStripSeg = 16;
 
 template <int NKS, bool TMAX>
-__global__ __launch_bounds__(256) void route_score_strip_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void route_score_strip_kernel(
     SplitOut A, SplitOut Bs, RouteGeom g, unsigned int* __restrict__ keys,
     float* __restrict__ emag, unsigned int* __restrict__ tmax, int64_t ntile, int64_t nstrips) {
   constexpr int NK = NKS * 16;
@@ -846,6 +846,7 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
   __shared__ __attribute__((aligned(16))) unsigned short sb[2][kTile][LD];
   __shared__ int64_t row_key[kStripRows];  // chunk row index of the strip's rows (-1: none)
   __shared__ int64_t row_cm[kStripRows];   // scored candidates of the strip's rows (0: none)
+  __shared__ double sroot[3];              // the tile's sqrt(largest candidate norm) per term
 
   const int64_t bk = blockIdx.y;  // b * Hkv + kvh
   const int64_t b = bk / g.Hkv, kvh = bk % g.Hkv;
@@ -896,6 +897,13 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
   for (int t = 0; t < 3; ++t) sa[t] = sqrt((double)(lra >= 0 ? A.sq[lra * 3 + t] : 0.0f));
   // rows of this lane's accumulator entries j: 32w + (j/4)*8 + (l/32)*4 + j%4
   const int rbase = w * 32 + (lane >> 5) * 4;
+  // Full tiles: a whole strip of one head has consecutive chunk rows lr0 + rl, and a tile whose
+  // candidates all lie below the strip's first row's candidate count (the counts grow along the
+  // rows) holds every candidate for every row: its key rows are addressed from lr0 alone and
+  // need no bounds checks.
+  const bool contig = r0 + kStripRows <= R && r0 / g.ni == (r0 + kStripRows - 1) / g.ni;
+  const int64_t lr0 = (b * g.Hq + kvh * g.G + r0 / g.ni) * g.ni + r0 % g.ni;
+  const int64_t cm_first = contig ? row_cmax_s(g, g.i0 + r0 % g.ni) : 0;
 
   // the next tile's pieces and candidate norms (lane = candidate) are loaded into registers
   // while the current tile is multiplied
@@ -903,15 +911,25 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
   u32x4 pf[kPer];
   float pn[3];
   const auto fetch = [&](int64_t c0) {
+    if (c0 + kTile <= nbs) {  // the tile's hi and lo rows: two contiguous 64 x NK blocks
+      const unsigned short* ph = Bs.hi + (bk * nbs + c0) * NK;
+      const unsigned short* pl = Bs.lo + (bk * nbs + c0) * NK;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int p = tid + 256 * i;
-      const int part = p / kPieces, rem = p % kPieces;
-      const int64_t c = c0 + rem / (NK / 8);
-      pf[i] = u32x4{0u, 0u, 0u, 0u};
-      if (c < nbs)
-        pf[i] = *reinterpret_cast<const u32x4*>((part ? Bs.lo : Bs.hi) + (bk * nbs + c) * NK +
-                                                (rem % (NK / 8)) * 8);
+      for (int i = 0; i < kPer; ++i) {
+        const int p = tid + 256 * i;
+        pf[i] = *reinterpret_cast<const u32x4*>((p < kPieces ? ph : pl) + (p % kPieces) * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int p = tid + 256 * i;
+        const int part = p / kPieces, rem = p % kPieces;
+        const int64_t c = c0 + rem / (NK / 8);
+        pf[i] = u32x4{0u, 0u, 0u, 0u};
+        if (c < nbs)
+          pf[i] = *reinterpret_cast<const u32x4*>((part ? Bs.lo : Bs.hi) + (bk * nbs + c) * NK +
+                                                  (rem % (NK / 8)) * 8);
+      }
     }
     const int64_t cl = c0 + lane;
 #pragma unroll
@@ -927,8 +945,14 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
       const int part = p / kPieces, rem = p % kPieces;
       *reinterpret_cast<u32x4*>(&sb[part][rem / (NK / 8)][(rem % (NK / 8)) * 8]) = pf[i];
     }
-    float M[3] = {pn[0], pn[1], pn[2]};
-    __syncthreads();
+    // sqrt of the tile's largest candidate norm per term, for emag: wave t (< 3) reduces term t
+    if (w < 3) {
+      float mt = w == 0 ? pn[0] : w == 1 ? pn[1] : pn[2];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+      if (lane == 0) sroot[w] = sqrt((double)mt);
+    }
+    __syncthreads();  // the tile and its roots are staged
     if (ct + 1 < ct1) fetch(c0 + kTile);
     f32x16 acc0, acc1;
 #pragma unroll
@@ -951,22 +975,37 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
       acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks], bh1, acc1, 0, 0, 0);
     }
     const int64_t cA = c0 + (lane & 31), cB = cA + 32;
+    const bool full = contig && c0 + kTile <= cm_first;  // wave-uniform
     unsigned int m[16];
+    if (full) {
+      // key row of entry j: lr0 + rbase + (j/4)*8 + j%4, a wave-uniform base plus a 32-bit
+      // per-lane offset
+      const unsigned int vb = (unsigned int)(rbase * nbs + cA) * 4u;  // byte offset
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int rl = rbase + (j >> 2) * 8 + (j & 3);
-      const int64_t cm = row_cm[rl];
-      unsigned int* kr = keys + row_key[rl] * nbs;
-      unsigned int k0 = 0u, k1 = 0u;
-      if (cA < cm) {
-        k0 = score_key(acc0[j]);
-        kr[cA] = k0;
+      for (int j = 0; j < 16; ++j) {
+        char* kj = reinterpret_cast<char*>(keys + (lr0 + (j >> 2) * 8 + (j & 3)) * nbs);
+        const unsigned int k0 = score_key(acc0[j]), k1 = score_key(acc1[j]);
+        *reinterpret_cast<unsigned int*>(kj + vb) = k0;
+        *reinterpret_cast<unsigned int*>(kj + vb + 128u) = k1;
+        m[j] = k0 > k1 ? k0 : k1;
       }
-      if (cB < cm) {
-        k1 = score_key(acc1[j]);
-        kr[cB] = k1;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int rl = rbase + (j >> 2) * 8 + (j & 3);
+        const int64_t cm = row_cm[rl];
+        unsigned int* kr = keys + row_key[rl] * nbs;
+        unsigned int k0 = 0u, k1 = 0u;
+        if (cA < cm) {
+          k0 = score_key(acc0[j]);
+          kr[cA] = k0;
+        }
+        if (cB < cm) {
+          k1 = score_key(acc1[j]);
+          kr[cB] = k1;
+        }
+        m[j] = k0 > k1 ? k0 : k1;
       }
-      m[j] = k0 > k1 ? k0 : k1;
     }
     if constexpr (TMAX) {
       // row maxima over the 32 lanes of each half-wave: a transposing butterfly (at the step of
@@ -1004,18 +1043,18 @@ __global__ __launch_bounds__(256) void route_score_strip_kernel(
       // lane l now holds the maximum of entry j = (l % 32) / 2
       const int j = (lane & 31) >> 1;
       const int rl = rbase + (j >> 2) * 8 + (j & 3);
-      if ((lane & 1) == 0 && c0 < row_cm[rl]) tmax[row_key[rl] * ntile + ct] = mx;
+      if (full) {
+        if ((lane & 1) == 0) tmax[(lr0 + rl) * ntile + ct] = mx;
+      } else if ((lane & 1) == 0 && c0 < row_cm[rl]) {
+        tmax[row_key[rl] * ntile + ct] = mx;
+      }
     }
-    // emag of the strip's rows: sqrt of the tile's largest candidate norms per term
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) M[t] = fmaxf(M[t], __shfl_xor(M[t], off, 64));
+    // emag of the strip's rows
     if (lane < 32 && c0 < cma) {
       double mag = 0.0, nsum = 0.0;
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        const double a = sa[t], bb = sqrt((double)M[t]);
+        const double a = sa[t], bb = sroot[t];
         mag += a * bb;
         nsum += a + bb;
       }
@@ -2462,7 +2501,7 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
         route_split_kernel<true><<<(unsigned)((nrow + 3) / 4), 256, 0, stream>>>(
             rows, nullptr, var, m3, g, (int)d, nt, coef2, coef3, nrow, As);
         SSA_TRY(launch_status("route_split_kernel"));
-        if (nk == 64 || nk == 128 || nk == 192 || nk == 256) {
+        if ((nk == 64 || nk == 128) && nbs < (1ll << 24)) {
           // the row operands in registers, a strip of rows per workgroup
           const int64_t nstrips = (R + kStripRows - 1) / kStripRows;
           const int64_t nseg = (cand_tiles + kStripSeg - 1) / kStripSeg;
@@ -2479,9 +2518,7 @@ int route_impl(const void* rows, int rows_dt, const float* mu, const float* var,
                   As, Bs, g, keys, emag, tmaxp, ntile, nstrips);
           };
           if (nk == 64) strip(std::integral_constant<int, 4>{});
-          else if (nk == 128) strip(std::integral_constant<int, 8>{});
-          else if (nk == 192) strip(std::integral_constant<int, 12>{});
-          else strip(std::integral_constant<int, 16>{});
+          else strip(std::integral_constant<int, 8>{});
           SSA_TRY(launch_status("route_score_strip_kernel"));
         } else {
           if (tm)
