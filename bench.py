@@ -214,7 +214,7 @@ def read_traffic():
 
 def device_info(torch, dev):
     """The box's own figures: CU count and clock (rocminfo) -> derived bf16 MFMA peak, and the
-    achievable HBM rate of a plain 2 GiB device copy."""
+    achievable HBM rates of a plain 2 GiB device copy and of a plain 2 GiB fill (write only)."""
     props = torch.cuda.get_device_properties(dev)
     info = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
             "cus": props.multi_processor_count}
@@ -244,6 +244,15 @@ def device_info(torch, dev):
     gbs = 2 * src.numel() * 5 / (time.perf_counter() - t0) / 1e9
     info["hbm_copy_gbs"] = gbs
     info["hbm_copy_frac_of_8tbs"] = gbs / PEAK_HBM_GBS
+    # write-only rate (a plain fill of the same 2 GiB): what a kernel that mostly stores can reach
+    for _ in range(2):
+        dst.fill_(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        dst.fill_(1)
+    torch.cuda.synchronize()
+    info["hbm_fill_gbs"] = src.numel() * 5 / (time.perf_counter() - t0) / 1e9
     del src, dst
     # the MFMA rate a plain library GEMM sustains on this box (hipBLASLt through torch.matmul,
     # bf16 8192^3): the practical ceiling the attention kernels' roofline fraction compares with
