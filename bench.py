@@ -476,6 +476,7 @@ def main():
     import numpy as np
     import torch
 
+    from ssa_amd import _lib
     from ssa_amd import ivf_decode as D
     from ssa_amd import ivf_kernel as IV
     from ssa_amd import ssa_kernel as K
@@ -493,30 +494,35 @@ def main():
     n, blk = cfg.n, cfg.block
     tm = Timer(torch)
 
+    # the attention call's workspace, reused step after step: prepare_attention writes V^T, the
+    # fp16 key copy and the per-tile key-norm maxima into it in one pass over K and V
+    ws_attn = torch.empty(int(_lib.query("ssa_sparse_attn_workspace_size", _lib.dtype_code(v.dtype),
+                                         1, cfg.Hkv, n, cfg.d, blk)), device=dev, dtype=torch.uint8)
+
     def step(timer):
         qbar = timer.run("qmean", K.block_summary, q, blk, "qmean")
         mu, var, _ = timer.run("kstats", K.block_summary, k, blk, "pop")
         kv_num, kv_idx = timer.run("route", K.route, qbar, mu, var, None, "budget", cfg.top_c,
                                    0.0, cfg.local, 0.5 * cfg.beta)
-        vt = timer.run("transpose_v", K.transpose_v, v, blk)
-        out = timer.run("attention", K.sparse_attention, q, k, v, kv_num, kv_idx, blk, vt=vt,
-                        rotate=ROTATE)
-        return out, kv_num, vt
+        prep = timer.run("prepare_kv", K.prepare_attention, k, v, blk, ws_attn)
+        out = timer.run("attention", K.sparse_attention, q, k, v, kv_num, kv_idx, blk,
+                        prepared=prep, rotate=ROTATE)
+        return out, kv_num
 
     log(f"bench: warmup {args.warmup}")
     for _ in range(args.warmup):
-        out, kv_num, vt = step(tm)
+        out, kv_num = step(tm)
     torch.cuda.synchronize()
     tm.reset()
     log(f"bench: timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out, kv_num, vt = step(tm)
+        out, kv_num = step(tm)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1000.0
-    parts = {nm: tm.mean_ms(nm) for nm in ("qmean", "kstats", "route", "transpose_v", "attention")}
+    parts = {nm: tm.mean_ms(nm) for nm in ("qmean", "kstats", "route", "prepare_kv", "attention")}
     sum_kv = int(kv_num.sum().item())
     flops = 4.0 * blk * blk * cfg.d * sum_kv
     t_attn = parts["attention"] / 1e3
@@ -533,8 +539,9 @@ def main():
     mu, var, _ = K.block_summary(k, blk, "pop")
     enum_, eidx = K.route(qbar, mu, var, None, "budget", cfg.top_c, 0.0, cfg.local, 0.5 * cfg.beta)
     for i in range(12):
-        te.run("exact" if i >= 2 else "warm", K.sparse_attention, q, k, v, enum_, eidx, blk, vt=vt,
-               exact=True)
+        prep = K.prepare_attention(k, v, blk, ws_attn)
+        te.run("exact" if i >= 2 else "warm", K.sparse_attention, q, k, v, enum_, eidx, blk,
+               prepared=prep, exact=True)
     torch.cuda.synchronize()
     exact_ms = te.mean_ms("exact")
     del qbar, mu, var, enum_, eidx
@@ -609,10 +616,10 @@ def main():
         qbar = K.block_summary(q, blk, "qmean")
         mu, var, _ = K.block_summary(k, blk, "pop")
         fnum, fidx = K.route(qbar, mu, var, None, "budget", None, 1.0, cfg.local, 0.5 * cfg.beta)
-        vt = K.transpose_v(v, blk)
         for i in range(3):
-            sd.run("own_full" if i else "warm", K.sparse_attention, q, k, v, fnum, fidx, blk, vt=vt,
-                   rotate=ROTATE)
+            prep = K.prepare_attention(k, v, blk, ws_attn)
+            sd.run("own_full" if i else "warm", K.sparse_attention, q, k, v, fnum, fidx, blk,
+                   prepared=prep, rotate=ROTATE)
         torch.cuda.synchronize()
         dense_ms = sd.mean_ms("sdpa")
         own_full = sd.mean_ms("own_full")
@@ -710,6 +717,9 @@ def main():
         c5 = d5["cfg"]
         q5, k5, v5 = d5["q"], d5["k"], d5["v"]
         nb5 = c5.n // c5.block
+        ws5 = torch.empty(int(_lib.query("ssa_sparse_attn_workspace_size",
+                                         _lib.dtype_code(v5.dtype), 1, 1, c5.n, c5.d, c5.block)),
+                          device=dev, dtype=torch.uint8)
         t5 = Timer(torch)
         layer_ev = []
         for rep in range(4):
@@ -721,9 +731,10 @@ def main():
             mu5, var5, _ = tmr.run("summaries_k", K.block_summary, k5, c5.block, "pop")
             kn5, ki5 = tmr.run("route", K.route, qb5, mu5, var5, None, "budget", c5.top_c, 0.0,
                                c5.local, 0.5 * c5.beta)
-            vt5 = tmr.run("transpose_v", K.transpose_v, v5, c5.block)
-            tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block, vt=vt5,
-                    rotate=ROTATE)
+            prep5 = tmr.run("prepare_kv", K.prepare_attention, k5, v5, c5.block, ws5)
+            tmr.run("attention", K.sparse_attention, q5, k5, v5, kn5, ki5, c5.block,
+                    prepared=prep5, rotate=ROTATE)
+            vt5 = prep5.ws[:v5.numel() * 2].view(v5.dtype).view(1, 1, c5.d, nb5 * c5.block)
             l1.record()
             if rep:
                 layer_ev.append((l0, l1))
@@ -746,9 +757,9 @@ def main():
             jac5.append(len(a & b) / max(1, len(a | b)))
         ivf_router = (t5.mean_ms("summaries") + t5.mean_ms("summaries_k") +
                       t5.mean_ms("ivf_build") + t5.mean_ms("ivf_route"))
-        ivf_total = ivf_router + t5.mean_ms("transpose_v") + t5.mean_ms("ivf_attention")
+        ivf_total = ivf_router + t5.mean_ms("prepare_kv") + t5.mean_ms("ivf_attention")
         router = t5.mean_ms("summaries") + t5.mean_ms("summaries_k") + t5.mean_ms("route")
-        attn = t5.mean_ms("transpose_v") + t5.mean_ms("attention")
+        attn = t5.mean_ms("prepare_kv") + t5.mean_ms("attention")
         layer = sum(a.elapsed_time(b) for a, b in layer_ev) / len(layer_ev)
         kv5 = int(kn5.sum().item())
         result["c5"] = {
