@@ -29,6 +29,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -718,8 +719,16 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   }
   bool have_m0 = !OFS;  // OFS: m_run holds m0 once the first sub-tile set it
   const float c2 = p.scale_log2;
+  // Exact path, bf16 (XO): the running max is taken on a wave's first sub-tile only; later
+  // sub-tiles reuse it as the offset of P = 2^(s - m) (bf16 P has fp32's exponent range, so a
+  // later score may exceed m by up to ~100 log2 units before anything overflows). A workgroup
+  // with a row whose sum or output left that range walks its list again with the per-sub-tile
+  // running max (xo_pass false).
+  constexpr bool XO = !fast && DT == SSA_BF16;
 
-  auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0) {
+  // SKIPC (std::true_type): the running max is not taken for this sub-tile (XO)
+  auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0, auto skipc) {
+    constexpr bool SKIP = decltype(skipc)::value;
     // ---- S^T = K Q^T ----
     u32x4 ka[TT][KD];
 #pragma unroll
@@ -810,32 +819,35 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       }
       return;
     }
-    // ---- online softmax (lazy rescale) ----
-    float m_use[CG], m_cand[CG];
-    bool grew[CG];
-    bool any_grew = false;
-#pragma unroll
-    for (int c = 0; c < CG; ++c) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][c][r]);
-      mx = pair_max(mx);
-      m_cand[c] = mx * c2;
-      grew[c] = m_cand[c] > m_run[c] + kRescaleSlack;
-      any_grew = any_grew || grew[c];
-    }
-    if (__any(any_grew)) {
+    // ---- online softmax (lazy rescale; XO: on a wave's first sub-tile only) ----
+    float m_use[CG];
+    if constexpr (!SKIP) {
+      float m_cand[CG];
+      bool grew[CG];
+      bool any_grew = false;
 #pragma unroll
       for (int c = 0; c < CG; ++c) {
-        const float alpha = grew[c] ? __builtin_amdgcn_exp2f(m_run[c] - m_cand[c]) : 1.0f;
-        l_part[c] *= alpha;
+        float mx = -INFINITY;
 #pragma unroll
-        for (int dt = 0; dt < DTN; ++dt)
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[dt][c][r] *= alpha;
-        m_run[c] = grew[c] ? m_cand[c] : m_run[c];
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[tt][c][r]);
+        mx = pair_max(mx);
+        m_cand[c] = mx * c2;
+        grew[c] = m_cand[c] > m_run[c] + kRescaleSlack;
+        any_grew = any_grew || grew[c];
+      }
+      if (__any(any_grew)) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          const float alpha = grew[c] ? __builtin_amdgcn_exp2f(m_run[c] - m_cand[c]) : 1.0f;
+          l_part[c] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][c][r] *= alpha;
+          m_run[c] = grew[c] ? m_cand[c] : m_run[c];
+        }
       }
     }
 #pragma unroll
@@ -872,20 +884,110 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   // (the cursor advances before each barrier: scalar work off the path from the barrier to
   // the next tile's loads)
   const int wlast = (int)qw0 + 32 * CG - 1;  // this wave's last query row
-  int key0 = next_tile();
-  if (key0 >= 0) issue(kst0, vst0, key0);
-  while (key0 >= 0) {
+  const std::false_type take_max;
+  // the whole walk with the running max of every sub-tile (XO: the second walk)
+  [[maybe_unused]] auto walk = [&]() {
+    int key0 = next_tile();
+    if (key0 >= 0) issue(kst0, vst0, key0);
+    while (key0 >= 0) {
+      int key0n = next_tile();
+      dma_barrier();  // stage 0 landed for all waves; stage 1 no longer read
+      if (key0n >= 0) issue(kst1, vst1, key0n);
+      if (key0 <= wlast) compute(kst0, vst0, key0, take_max);
+      key0 = key0n;
+      if (key0 < 0) break;
+      key0n = next_tile();
+      dma_barrier();  // stage 1 landed; stage 0 no longer read
+      if (key0n >= 0) issue(kst0, vst0, key0n);
+      if (key0 <= wlast) compute(kst1, vst1, key0, take_max);
+      key0 = key0n;
+    }
+  };
+  // XO: the running max of the walk's first sub-tile only (in list order every wave computes
+  // it: its key blocks start at or before the query block's first row; a wave that does not
+  // keeps m = -inf, offsets by 0, and overflows into the second walk if its scores are large)
+  [[maybe_unused]] auto walk_xo = [&]() {
+    const std::true_type skip_max;
+    int key0 = next_tile();
+    if (key0 < 0) return;
+    issue(kst0, vst0, key0);
     int key0n = next_tile();
-    dma_barrier();  // stage 0 landed for all waves; stage 1 no longer read
+    dma_barrier();
     if (key0n >= 0) issue(kst1, vst1, key0n);
-    if (key0 <= wlast) compute(kst0, vst0, key0);
+    if (key0 <= wlast) compute(kst0, vst0, key0, take_max);
     key0 = key0n;
-    if (key0 < 0) break;
-    key0n = next_tile();
-    dma_barrier();  // stage 1 landed; stage 0 no longer read
-    if (key0n >= 0) issue(kst0, vst0, key0n);
-    if (key0 <= wlast) compute(kst1, vst1, key0);
-    key0 = key0n;
+    while (key0 >= 0) {
+      key0n = next_tile();
+      dma_barrier();  // stage 1 landed; stage 0 no longer read
+      if (key0n >= 0) issue(kst0, vst0, key0n);
+      if (key0 <= wlast) compute(kst1, vst1, key0, skip_max);
+      key0 = key0n;
+      if (key0 < 0) break;
+      key0n = next_tile();
+      dma_barrier();  // stage 0 landed; stage 1 no longer read
+      if (key0n >= 0) issue(kst1, vst1, key0n);
+      if (key0 <= wlast) compute(kst0, vst0, key0, skip_max);
+      key0 = key0n;
+    }
+  };
+  if constexpr (XO) {
+    __shared__ int wg_ovf;
+    if (tid == 0) wg_ovf = 0;
+    walk_xo();
+    // a row whose sum reached 2^100 (a later score ~100 log2 units above its first sub-tile's
+    // maximum) or whose output accumulators overflowed: the workgroup walks again with the
+    // per-sub-tile running max
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const float lt = pair_sum(l_part[c]);
+      bool ok = lt < 0x1p100f;
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ok = ok && fabsf(oacc[dt][c][r]) < INFINITY;
+      if (qrow(c) < n32 && !ok) bad = true;
+    }
+    __syncthreads();  // (orders the flag's clear before the writes below)
+    if (__any(bad) && lane == 0) wg_ovf = 1;
+    __syncthreads();  // every wave is also past its last LDS read of the walk
+    if (wg_ovf) {     // workgroup-uniform
+      ce = e0;
+      cs = -1;
+      kk = 0;
+      if (lbase != 0) {
+        lbase = 0;
+        lreg = lane < cnt ? list[lane] : -1;
+      }
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+        for (int c = 0; c < CG; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][c][r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        m_run[c] = -INFINITY;
+        l_part[c] = 0.0f;
+      }
+      walk();
+    }
+  } else {
+    int key0 = next_tile();
+    if (key0 >= 0) issue(kst0, vst0, key0);
+    while (key0 >= 0) {
+      int key0n = next_tile();
+      dma_barrier();  // stage 0 landed for all waves; stage 1 no longer read
+      if (key0n >= 0) issue(kst1, vst1, key0n);
+      if (key0 <= wlast) compute(kst0, vst0, key0, take_max);
+      key0 = key0n;
+      if (key0 < 0) break;
+      key0n = next_tile();
+      dma_barrier();  // stage 1 landed; stage 0 no longer read
+      if (key0n >= 0) issue(kst0, vst0, key0n);
+      if (key0 <= wlast) compute(kst1, vst1, key0, take_max);
+      key0 = key0n;
+    }
   }
 
   // ---- epilogue: O = O^T / l ----

@@ -573,6 +573,61 @@ def test_unbounded_rows_take_the_exact_path(cuda, dtype, block):
     assert np.abs(np_of(out) - ref).max() < TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("jump", [40.0, 90.0, 220.0])
+@pytest.mark.parametrize("exact", [False, True])
+def test_exact_path_score_jump_after_the_first_sub_tile(cuda, dtype, jump, exact):
+    """The exact path (bf16) takes the running max on a wave's first sub-tile only and offsets the
+    later sub-tiles' P = 2^(s - m) by it; a row whose sum then reaches 2^100 sends its workgroup
+    through its list again with the running max of every sub-tile (fp16 inputs always take the
+    running max of every sub-tile). Query block i (i >= 2) repeats one direction q_i with |q_i| =
+    40 and walks [0, i - 1, i]: block 0 holds short random keys (its scores, the first sub-tile's
+    max, a few log2 units), block i - 1 starts with a needle along q_i whose score lies `jump`
+    log2 units above them, value e_(i mod 64). jump 40 / 90: the offset pass keeps every sum
+    finite; 220: it overflows and the second walk runs. Both the exact launch of unbounded rows
+    (exact=False: |q| max|k| is far over the bounded path's limit) and exact=True. Every row within
+    2e-2 of the float64 oracle."""
+    rng = np.random.default_rng(31)
+    n, block, d, scale = 1024, 128, 64, 0.125
+    c = scale * math.log2(math.e)
+    nb = n // block
+    qn = 40.0
+    q = np.zeros((1, 1, n, d), np.float32)
+    k = (0.05 * rng.standard_normal((1, 1, n, d))).astype(np.float32)
+    v = (0.1 * rng.standard_normal((1, 1, n, d))).astype(np.float32)
+    kv_num = np.full((1, 1, nb), 3, np.int32)
+    kv_idx = np.zeros((1, 1, nb, 3), np.int32)
+    kv_num[0, 0, 0], kv_num[0, 0, 1] = 1, 2
+    kv_idx[0, 0, 0, 0] = 0
+    kv_idx[0, 0, 1, :2] = [0, 1]
+    for i in range(nb):
+        x = rng.standard_normal(d)
+        qh = x / np.linalg.norm(x)
+        q[0, 0, i * block:(i + 1) * block] = qh * qn
+        if i >= 2:
+            p0 = (i - 1) * block
+            k[0, 0, p0] = qh * (jump / (c * qn))  # score c * |q| * |k| = jump log2 units
+            v[0, 0, p0] = 0.0
+            v[0, 0, p0, i % d] = 1.0
+            kv_idx[0, 0, i] = [0, i - 1, i]
+    q, k, v = (WL.round_to(x, dtype) for x in (q, k, v))
+    # block 0's scores: the first sub-tile's row maxima lie far below the needle
+    s0 = c * (q[0, 0, 2 * block:].astype(np.float64) @ k[0, 0, :block].astype(np.float64).T)
+    assert s0.max() < 10.0, s0.max()
+    ref = O.sparse_attention(q, k, v, kv_num, kv_idx, block, scale=scale)
+    qt, kt, vt = (dev(x, dtype, cuda) for x in (q, k, v))
+    out = K.sparse_attention(qt, kt, vt, torch.from_numpy(kv_num).to(cuda),
+                             torch.from_numpy(kv_idx).to(cuda), block, scale=scale, exact=exact)
+    o = np_of(out)
+    err = float(np.abs(o - ref).max())
+    print(f"{dtype} jump {jump} exact={exact}: max |err| {err:.3g}")
+    assert np.isfinite(o).all()
+    assert err < TOL[dtype], err
+    # the needle dominates its rows
+    i = nb - 1
+    assert abs(o[0, 0, i * block + 5, i % d] - ref[0, 0, i * block + 5, i % d]) < TOL[dtype]
+
+
 # admission bounds of the bounded-row path (log2 units of scale * q.k): attn.hip fast_bound<DT>
 FAST_BOUND = {torch.float16: 32.0, torch.bfloat16: 32.0}
 
