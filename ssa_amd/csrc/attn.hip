@@ -725,6 +725,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
   // with a row whose sum or output left that range walks its list again with the per-sub-tile
   // running max (xo_pass false).
   constexpr bool XO = !fast && DT == SSA_BF16;
+  // raised wave priority around the exact path's MFMA phases: kept for head dims 128 / 256; at 64
+  // the default priority is 1.5-2 % faster since the max is no longer taken every sub-tile
+  constexpr bool PRIO = !fast && D != 64;
 
   // SKIPC (std::true_type): the running max is not taken for this sub-tile (XO)
   auto compute = [&](const unsigned char* ks, const unsigned char* vs, int key0, auto skipc) {
@@ -737,7 +740,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
       for (int kd = 0; kd < KD; ++kd)
         ka[tt][kd] = *reinterpret_cast<const u32x4*>(ks + koff[kd] + tt * (32 * KRB));
     f32x16 sacc[TT][CG];  // [tt][c]
-    if constexpr (!fast) __builtin_amdgcn_s_setprio(1);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
@@ -749,7 +752,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
           sacc[tt][c] = MQ::mma(MQ::from_bits(ka[tt][kd]),
                                 __builtin_bit_cast(typename MQ::vec, qf[c][kd]), sacc[tt][c]);
       }
-    if constexpr (!fast) __builtin_amdgcn_s_setprio(0);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     // V^T fragments of the first two key steps, in flight during the softmax
     u32x4 va[SS][DTN];
 #pragma unroll
@@ -853,7 +856,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
 #pragma unroll
     for (int c = 0; c < CG; ++c) m_use[c] = m_run[c] == -INFINITY ? 0.0f : m_run[c];
     // ---- P^T (registers) and O^T += V^T P^T ----
-    __builtin_amdgcn_s_setprio(1);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < SS; ++s) {
       if (s + 2 < SS) {
@@ -877,7 +880,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void sparse_attn_dma_kernel(AttnParam
         for (int c = 0; c < CG; ++c)
           oacc[dt][c] = M::mma(M::from_bits(va[s][dt]), pb[c], oacc[dt][c]);
     }
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
   // 2-stage ring, statically unrolled by two so each LDS access names its stage's array.
