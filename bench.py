@@ -96,8 +96,12 @@ def published_bench(torch, dev):
       IVF-routed forward (ssa_flex_ivf), H=1, fp16, block 128, top_c 8:
         paper/figures/ivf_kernel_e2e.json:51-67,119-135 (16.1 ms at 1M, 139.5 ms at 12,582,912);
       routed decode step over a 1,048,576-token cache, H=1, fp16, block 128, top_c 8, local 1,
-        mean of 128 steps: paper/figures/ivf_decode.json:17-31 (0.60 ms; dense 0.52 ms)."""
-    from ssa_amd import ivf_decode as D, ivf_kernel as IV, ssa_kernel as K
+        mean of 128 steps: paper/figures/ivf_decode.json:17-31 (0.60 ms; dense 0.52 ms);
+      treecode router (ssa/treecode_bench.py: build_tree over fp16 keys, H=8, d=64, block 128, F 8,
+        then the Q-tiled descend_beam of nb random query rows per head, W 16, top_c 8):
+        paper/figures/treecode_router_measured.json:18-33 (build 23.8 / descend 63.3 ms at
+        1,048,576; 56.6 / 115.4 ms at 2,097,152)."""
+    from ssa_amd import ivf_decode as D, ivf_kernel as IV, ssa_kernel as K, treecode as TC
     sdpa = torch.nn.functional.scaled_dot_product_attention
     g = torch.Generator(device=dev).manual_seed(11)
 
@@ -120,6 +124,17 @@ def published_bench(torch, dev):
         ms = _event_ms(torch, lambda: IV.ssa_flex_ivf(q, k, v, 128, 8, 1), 3, warm=1)
         out[f"ivf_forward_h1_n{n}"] = {"ms": ms, "reference_ms": ref_ms}
         del q, k, v
+    for n, ref_build, ref_desc in ((1 << 20, 23.832, 63.286), (1 << 21, 56.604, 115.384)):
+        k = torch.randn(1, 8, n, 64, device=dev, dtype=torch.float16, generator=g)
+        nb = n // 128
+        qb = torch.randn(8, nb, 64, device=dev, generator=g)
+        bms = _event_ms(torch, lambda: TC.build_tree(k, 128, 8), 3, warm=1)
+        levels, F = TC.build_tree(k, 128, 8)
+        dms_t = _event_ms(torch, lambda: TC.tree_router(levels, F, qb, 16, 8), 3, warm=1)
+        out[f"treecode_h8_n{n}"] = {"build_ms": bms, "descend_ms": dms_t,
+                                    "reference_build_ms": ref_build,
+                                    "reference_descend_ms": ref_desc}
+        del k, qb, levels
     n, steps = 1 << 20, 128
     q, k, v = qkv(1, n + steps)
     dec = D.RoutedDecoder(1, 1, 1, 64, n + steps, block=128, top_c=8, local=1,

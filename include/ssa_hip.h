@@ -204,6 +204,39 @@ int ssa_ivf_route(const void* index, const float* qb, int64_t BH, int64_t G, int
                   ssa_stream_t stream);
 
 /*
+ * Treecode router: the bounded-candidate sub-linear selector of ssa/treecode.py (build_tree
+ * :34-86, descend_beam :89-137), the other f4 candidate beside the IVF router.
+ *
+ * ssa_tree_build (build_tree): k (B, H, n, d) fp32 / fp16 / bf16, strides[3] = k(b,h,n)
+ *   elements, d a multiple of 4 up to 512; nb = n / block whole blocks (a partial tail block is
+ *   dropped, as the reference's n // block does); 2 <= F <= 16, 1 <= top_cap <= 64. Level 0 holds
+ *   the nb leaf blocks of each of the BH = B H heads: mean, population variance (E[k^2] - mean^2)
+ *   and R = max over the block's keys of |k - mean|; each level above groups F consecutive nodes
+ *   (the last group may be short): mean of the children's means, variance mean(var + mean_c^2) -
+ *   mean^2, R = max over children of |mean_c - mean| + R_c, lo = the smallest child lo (level 0:
+ *   block * block index); levels are added while the last holds more than top_cap nodes. Sums in
+ *   fp64 from the stored fp32 values, each stored value rounded once. The tree buffer takes
+ *   ssa_tree_size bytes (16-byte aligned): per level from the leaves up, each region 256-byte
+ *   aligned, mean (BH, n_l, d) fp32, var (BH, n_l, d) fp32, R (BH, n_l) fp32, lo (n_l) int64.
+ * ssa_tree_descend (descend_beam): q (BH, Q, d) fp32 contiguous, q_pos (BH, Q) int64 or NULL (no
+ *   causal mask); a node is scored by <q, mean> + |q| R + beta/2 <q*q, var> (fp64, rounded to
+ *   fp32) and masked when its lo exceeds q_pos; the top level is scanned whole and its best W
+ *   valid nodes start the frontier; per level below, the children of the frontier are scored and
+ *   the best W valid ones kept (1 <= W <= 64, W F <= 1024); sel (BH, Q, min(top_c, W)) int32 holds
+ *   the best leaves of the last frontier in (score desc, leaf asc) order, -1 past the valid ones.
+ *   Ties rank by the lower node index at every level.
+ */
+size_t ssa_tree_size(int64_t BH, int64_t nb, int64_t d, int64_t F, int64_t top_cap);
+
+int ssa_tree_build(const void* k, int dtype, int64_t B, int64_t H, int64_t n, int64_t d,
+                   int64_t block, const int64_t* strides, int64_t F, int64_t top_cap, void* tree,
+                   size_t tree_bytes, ssa_stream_t stream);
+
+int ssa_tree_descend(const void* tree, const float* q, const int64_t* q_pos, int64_t BH, int64_t Q,
+                     int64_t nb, int64_t d, int64_t F, int64_t top_cap, int64_t W, int64_t top_c,
+                     float beta, int32_t* sel, ssa_stream_t stream);
+
+/*
  * Block-sparse causal attention forward (replaces FlexAttention with
  * BlockMask.from_kv_blocks(kv_num, kv_idx, block, mask_mod = kv<=q & kv<n):
  * ssa/ssa_kernel.py:30-34,125-126, ssa/gemma_ssa.py:159-162,179, ssa/ivf_kernel.py:122-127).

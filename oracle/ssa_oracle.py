@@ -34,6 +34,13 @@ Pinning (what checks each function; details in tests/test_oracle.py):
                          clusters are recovered exactly; the final lists partition the blocks,
                          ascending, each member at its argmax centroid; Jaccard >= 0.6 against
                          the flat router on the clustered geometry of the reference's own test.
+  tree_build /           (the reference has no tests or fixtures for ssa/treecode.py.) The
+  tree_descend           admissible invariant of its own validation (treecode.py:141-157: every
+                         node's bound >= the largest key score below it) on random and clustered
+                         keys; brute-force leaf statistics; a beam wide enough to hold every node
+                         reduces the descent to the flat top_c of the leaf bounds; recall climbs
+                         with W to the flat ceiling (treecode.py:160-200); the causal mask keeps
+                         every selected leaf at or before q_pos.
 """
 from __future__ import annotations
 
@@ -599,3 +606,93 @@ def ivf_route(qb: np.ndarray, mu: np.ndarray, top_c=8, local=1, nprobe=4, search
                                              top_c, local)):
                 sel[b, h, i] = s
     return sel, cents, inv
+
+
+# ---------------------------------------------------------------------------------------------
+# f4 (treecode): the bounded-candidate tree router of ssa/treecode.py
+# ---------------------------------------------------------------------------------------------
+
+
+def tree_build(k: np.ndarray, block: int, F: int = 8, top_cap: int = 8):
+    """build_tree (ssa/treecode.py:34-86): k (B, H, n, d) -> list of levels from the leaves up,
+    each a dict mu (BH, n_l, d) f32, var (BH, n_l, d) f32, R (BH, n_l) f32, lo (n_l,) int64.
+    Leaves (:40-52): per block the mean, the population variance E[k^2] - mean^2 and R = max
+    |k - fl32(mean)|; parents (:55-76): groups of F consecutive nodes (a short last group), mean
+    of the child means, var mean(var_c + mu_c^2) - mean^2, R = max(|mu_c - fl32(mean)| + R_c),
+    lo = min child lo; until a level holds at most top_cap nodes. Sums in float64 from the
+    stored float32 values, each stored value rounded once."""
+    B, H, n, d = k.shape
+    BH, nb = B * H, n // block
+    kb = k[:, :, :nb * block].astype(np.float64).reshape(BH, nb, block, d)
+    m64 = kb.mean(axis=2)
+    mu = m64.astype(np.float32)
+    var = ((kb * kb).mean(axis=2) - m64 * m64).astype(np.float32)
+    dev = kb - mu.astype(np.float64)[:, :, None, :]
+    R = np.sqrt((dev * dev).sum(-1).max(-1)).astype(np.float32)
+    levels = [dict(mu=mu, var=var, R=R, lo=np.arange(nb, dtype=np.int64) * block)]
+    while levels[-1]["mu"].shape[1] > top_cap:
+        ch = levels[-1]
+        nc = ch["mu"].shape[1]
+        npar = -(-nc // F)
+        pm = np.zeros((BH, npar, d), np.float32)
+        pv = np.zeros((BH, npar, d), np.float32)
+        pr = np.zeros((BH, npar), np.float32)
+        pl = np.zeros(npar, np.int64)
+        for p in range(npar):
+            c0, c1 = p * F, min(nc, p * F + F)
+            cm = ch["mu"][:, c0:c1].astype(np.float64)
+            m = cm.mean(axis=1)
+            pm[:, p] = m.astype(np.float32)
+            pv[:, p] = ((ch["var"][:, c0:c1].astype(np.float64) + cm * cm).mean(axis=1)
+                        - m * m).astype(np.float32)
+            dist = np.sqrt(((cm - pm[:, p].astype(np.float64)[:, None, :]) ** 2).sum(-1))
+            pr[:, p] = (dist + ch["R"][:, c0:c1].astype(np.float64)).max(axis=1).astype(np.float32)
+            pl[p] = ch["lo"][c0:c1].min()
+        levels.append(dict(mu=pm, var=pv, R=pr, lo=pl))
+    return levels
+
+
+def _tree_scores(lvl, bh, nodes, q64, qn, beta):
+    """Admissible bound <q, mu> + |q| R (+ beta/2 <q*q, var>) of `nodes` of head bh
+    (ssa/treecode.py:98-102), float64 rounded to float32."""
+    mu = lvl["mu"][bh, nodes].astype(np.float64)
+    s = mu @ q64 + qn * lvl["R"][bh, nodes].astype(np.float64)
+    if beta:
+        s = s + 0.5 * beta * (lvl["var"][bh, nodes].astype(np.float64) @ (q64 * q64))
+    return s.astype(np.float32)
+
+
+def _tree_best(nodes, s32, valid, W):
+    """The W best valid (node, score) pairs by (score desc, node asc), ascending by node."""
+    nodes, s32 = nodes[valid], s32[valid]
+    order = np.lexsort((nodes, -score_keys(s32).astype(np.int64)))[:W]
+    keep = order[np.argsort(nodes[order], kind="stable")]
+    return nodes[keep], s32[keep]
+
+
+def tree_descend(levels, F, q: np.ndarray, W: int, top_c: int, q_pos=None, beta: float = 0.0):
+    """descend_beam (ssa/treecode.py:89-137): q (BH, Q, d) -> (BH, Q, min(top_c, W)) int64 leaf
+    indices, best first, -1 past the valid ones. The top level is scanned whole (:104-117), then
+    each level keeps the W best valid children of the frontier (:119-133); a node whose lo
+    exceeds q_pos is masked (:110-111, :130-131); ties rank by the lower node index."""
+    BH, Q, d = q.shape
+    tc = min(top_c, W)
+    out = np.full((BH, Q, tc), -1, np.int64)
+    top = len(levels) - 1
+    for bh in range(BH):
+        for qi in range(Q):
+            q64 = q[bh, qi].astype(np.float64)
+            qn = math.sqrt(float(q64 @ q64))
+            qp = np.iinfo(np.int64).max if q_pos is None else int(q_pos[bh, qi])
+            nodes = np.arange(levels[top]["mu"].shape[1], dtype=np.int64)
+            s32 = _tree_scores(levels[top], bh, nodes, q64, qn, beta)
+            fr, fs = _tree_best(nodes, s32, levels[top]["lo"][nodes] <= qp, W)
+            for l in range(top - 1, -1, -1):
+                nl = levels[l]["mu"].shape[1]
+                ch = (fr[:, None] * F + np.arange(F)[None, :]).reshape(-1)
+                ch = ch[ch < nl]
+                s32 = _tree_scores(levels[l], bh, ch, q64, qn, beta)
+                fr, fs = _tree_best(ch, s32, levels[l]["lo"][ch] <= qp, W)
+            order = np.lexsort((fr, -score_keys(fs).astype(np.int64)))[:tc]
+            out[bh, qi, :len(order)] = fr[order]
+    return out

@@ -20,7 +20,8 @@ INCLUDE = ROOT / "include"
 LIB = PKG / "libssa_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "summary.hip", "route.hip", "attn.hip", "decode.hip", "swap.hip", "ivf.hip"]
+SOURCES = ["abi.hip", "summary.hip", "route.hip", "attn.hip", "decode.hip", "swap.hip", "ivf.hip",
+           "tree.hip"]
 
 
 def hipcc() -> str:

@@ -545,27 +545,6 @@ struct FusedStep {
   int32_t* kv_idx;       // (B*Hq, W)
 };
 
-// Bitonic sort of one (key, block) pair per lane across the wave: descending keys, ties by
-// ascending block (the router's order); lane j ends with the (j+1)-th.
-__device__ inline void wave_sort_desc(unsigned int& key, unsigned int& blk) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-    for (int j = k >> 1; j >= 1; j >>= 1) {
-      const unsigned int ok = lane_xor(key, j), ob = lane_xor(blk, j);
-      // does the partner rank before this lane's pair?
-      const bool before = ok > key || (ok == key && ob < blk);
-      const bool lower = (lane & j) == 0, desc = (lane & k) == 0;
-      // the lower lane of a descending pair keeps the better pair, and so on
-      const bool take = (lower == desc) ? before : !before;
-      if (take) {
-        key = ok;
-        blk = ob;
-      }
-    }
-}
-
 // One route workgroup's work: chunk `chunk` of the candidate blocks of key head bk.
 // NW waves score (16 candidates each); all NWT >= NW waves take the rows' selections (one row
 // per wave and round).
