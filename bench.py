@@ -685,6 +685,35 @@ def main():
             dec.step(qd[t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
         torch.cuda.synchronize()
         dms = (time.perf_counter() - t0) / args.decode_steps * 1000.0
+        # the same steps captured in a HIP graph through the allocation-free entry point
+        # (ssa_decode_step_static): 32 consecutive steps per graph (each with its position baked
+        # in; a replay appends the same tokens again), replayed back to back
+        decs = D.RoutedDecoder(1, c4.Hq, c4.Hkv, c4.d, ncache + args.decode_steps + 8,
+                               block=c4.block, top_c=c4.top_c, local=c4.local, beta=c4.beta,
+                               dtype=c4.dtype, device=dev, static_scratch=True)
+        decs.prefill(kd[:, :, :ncache], vd[:, :, :ncache])
+        for t in range(8):
+            decs.step(qd[t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+        gs = torch.cuda.Stream()
+        gs.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        ng = 32
+        with torch.cuda.stream(gs):
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=gs):
+                for t in range(8, 8 + ng):
+                    decs.step(qd[t], kd[:, :, ncache + t], vd[:, :, ncache + t], out=out_d)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        reps = max(1, args.decode_steps // ng)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        gms = (time.perf_counter() - t0) / (reps * ng) * 1000.0
+        del graph, decs
         kvn = int(dec.kv_num.sum().item())
         nbk = dec.pos // c4.block
         dbytes = c4.Hkv * nbk * 2 * c4.d * 4 + kvn * c4.block * c4.d * 2 * 2
@@ -707,6 +736,8 @@ def main():
         result["decode"] = {
             "workload": "C4: decode, bf16, 14q/2kv, d=64, 1M-token cache, block 128, top_c 64",
             "ms_per_step": dms, "steps": args.decode_steps,
+            "graph_ms_per_step": gms,
+            "graph": f"{ng} steps per HIP graph through ssa_decode_step_static, replayed {reps}x",
             "bytes_per_step": dbytes, "achieved_gbs": dbytes / (dms / 1e3) / 1e9,
             "hbm_frac": dbytes / (dms / 1e3) / 1e9 / PEAK_HBM_GBS,
             # torch SDPA has no split-KV decode path on ROCm: its grid is (query tiles x
