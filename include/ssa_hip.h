@@ -237,6 +237,73 @@ int ssa_tree_descend(const void* tree, const float* q, const int64_t* q_pos, int
                      float beta, int32_t* sel, ssa_stream_t stream);
 
 /*
+ * Certified causal cascade (CCC): the streaming chunked-causal sub-block selector of
+ * ssa/cascade_router.py:66-442 (CausalCascade, ccc_prefill), faiss-free. One head; the caller
+ * holds the state: the routing-space sub-block means (n_sub, d) fp32 row-major, the first
+ * `committed` of them indexed (or scanned flat before the index exists), the outlier keys, and
+ * one index buffer of ssa_ccc_index_size(n_cap, nlist, d) bytes (256-byte aligned). d: a multiple
+ * of 32 up to 256 for the means, the index and the route. Inner products accumulate in fp64 in
+ * dimension order and round once to fp32; rankings break ties by the lower index.
+ *
+ * ssa_ccc_stage (sub_block_means + _extract_outliers, :46-48,:214-231): means[g] of x's rows
+ *   g*group .. g*group+group-1 (x (m, d) of `dtype`, row_stride elements; fp64 sums in row
+ *   order / group, rounded once; m / group groups). quota > 0 (at most 2048, m a multiple of
+ *   group): the min(quota, m) rows of largest fl32(||x_row - mean||^2) (fp64, dimension order;
+ *   ties to the lower row) are written, largest first, to out_vec (fp32, d each), out_parent =
+ *   (base_tok + row) / block, out_pos = base_tok + row; ws holds 8 m bytes.
+ * ssa_ccc_kmeans (_kmeans, :149-161): iters inner-product Lloyd rounds over x (n, d): every row
+ *   joins the centroid of largest <x, c>, each centroid with members becomes fl32 of their fp64
+ *   mean (ascending member order). warm = 0 starts centroid c at x[c * n / nlist]; otherwise cent
+ *   holds the start. ws: ssa_ccc_index_size(n, nlist, d) bytes.
+ * ssa_ccc_assign (_assign, :139-147): assign[j] = the centroid of largest <x_j, c>; same ws.
+ * ssa_ccc_index_build (_build_index, :163-190): the index over x[0..n) with the centroids cent:
+ *   the lists of the assignment (members ascending) and exact radii max ||x - c|| (fp64, rounded).
+ * ssa_ccc_index_add (_commit with an index + _update_radii, :140-147,:192-194): x[n_old..n)
+ *   join their best centroid's list; radii rise to cover them.
+ * ssa_ccc_route (route, :282-331; _search_committed :233-255, _search_staged :257-280,
+ *   _select_topc :333-347, _outlier_parents :349-366, _pack :374-383, _certify :385-403): one
+ *   workgroup per query block i (global block q = qb_start + i) of qr (nbq, d) fp32: the staged
+ *   means committed..n_sub-1 whose parent (index / spb) is < q, best search_k_staged; the
+ *   committed ones, best min(search_k, committed), flat when index is NULL, else over the
+ *   min(nprobe, nlist) lists of largest <qr, c>; each parent's best sub-block, the best top_c
+ *   parents (tau = the smallest kept score); the outlier keys of parents < q scoring above tau,
+ *   best outlier_cap; OR blocks q - local .. q; ascending in kv_idx (W >= min(top_c + local + 1 +
+ *   outlier_cap, qb_start + nbq), pad 0), counted in kv_num. certify: cert = the kept budget is
+ *   full (min(top_c, q)) and above -inf and, with an index, no unprobed cell's bound <qr, c> +
+ *   |qr| R_c and no filled search's last score reaches tau - cert_margin (flat: full budget and
+ *   tau above -inf or q = 0); an uncertified block with an index is searched again with nprobe *
+ *   escalate_factor lists and twice the search_k (at most max_escalations times); rounds = the
+ *   last round run. search_k values up to 1024.
+ */
+size_t ssa_ccc_index_size(int64_t n_cap, int64_t nlist, int64_t d);
+
+int ssa_ccc_stage(const void* x, int dtype, int64_t m, int64_t d, int64_t row_stride,
+                  int64_t group, float* means, int64_t quota, int64_t base_tok, int64_t block,
+                  float* out_vec, int64_t* out_parent, int64_t* out_pos, void* ws,
+                  size_t ws_bytes, ssa_stream_t stream);
+
+int ssa_ccc_kmeans(const float* x, int64_t n, int64_t d, int64_t nlist, int64_t iters, int warm,
+                   float* cent, void* ws, size_t ws_bytes, ssa_stream_t stream);
+
+int ssa_ccc_assign(const float* x, int64_t n, int64_t d, const float* cent, int64_t nlist,
+                   int32_t* assign, void* ws, size_t ws_bytes, ssa_stream_t stream);
+
+int ssa_ccc_index_build(const float* x, int64_t n, int64_t d, int64_t nlist, const float* cent,
+                        void* index, int64_t n_cap, size_t index_bytes, ssa_stream_t stream);
+
+int ssa_ccc_index_add(const float* x, int64_t n_old, int64_t n, int64_t d, int64_t nlist,
+                      void* index, int64_t n_cap, size_t index_bytes, ssa_stream_t stream);
+
+int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int64_t d, const float* means,
+                  int64_t committed, int64_t n_sub, int64_t spb, const void* index, int64_t n_cap,
+                  int64_t nlist, const float* out_vec, const int64_t* out_parent, int64_t n_out,
+                  int64_t top_c, int64_t local, int64_t outlier_cap, int64_t search_k_staged,
+                  int64_t search_k, int64_t nprobe, int64_t escalate_factor,
+                  int64_t max_escalations, int certify, float cert_margin, int32_t* kv_num,
+                  int32_t* kv_idx, int64_t W, uint8_t* cert, int32_t* rounds,
+                  ssa_stream_t stream);
+
+/*
  * Block-sparse causal attention forward (replaces FlexAttention with
  * BlockMask.from_kv_blocks(kv_num, kv_idx, block, mask_mod = kv<=q & kv<n):
  * ssa/ssa_kernel.py:30-34,125-126, ssa/gemma_ssa.py:159-162,179, ssa/ivf_kernel.py:122-127).

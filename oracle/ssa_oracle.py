@@ -696,3 +696,259 @@ def tree_descend(levels, F, q: np.ndarray, W: int, top_c: int, q_pos=None, beta:
             order = np.lexsort((fr, -score_keys(fs).astype(np.int64)))[:tc]
             out[bh, qi, :len(order)] = fr[order]
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# f4 (cascade): the certified causal cascade of ssa/cascade_router.py, faiss-free
+# ---------------------------------------------------------------------------------------------
+
+
+def _seq_sum(x64: np.ndarray, axis: int) -> np.ndarray:
+    """Sum along `axis` in index order (each step rounds once, as the kernels' adds do)."""
+    return np.add.accumulate(x64, axis=axis).take(-1, axis=axis)
+
+
+def ccc_group_means(x: np.ndarray, group: int) -> np.ndarray:
+    """(m, d) -> (m // group, d) float32: fp64 sums of each group's rows in row order, divided
+    by group and rounded once (sub_block_means / block_means, ssa/cascade_router.py:46-48,
+    ssa/ivf_kernel.py:50-60)."""
+    m, d = x.shape
+    ng = m // group
+    x64 = x[:ng * group].astype(np.float32).astype(np.float64).reshape(ng, group, d)
+    return (_seq_sum(x64, 1) / group).astype(np.float32)
+
+
+def _sq_dist(x: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Row-wise sum over dimensions (in order) of (x - c)^2 in float64: x, c float32 (R, d)."""
+    df = x.astype(np.float64) - c.astype(np.float64)
+    return _seq_sum(df * df, 1)
+
+
+def ccc_outliers(x: np.ndarray, means: np.ndarray, group: int, quota: int, base: int, block: int):
+    """_extract_outliers (ssa/cascade_router.py:214-231): the min(quota, m) rows of largest
+    fl32(||x_row - mean of its group||^2) (ties to the lower row), largest first ->
+    (vectors float32, parent blocks, positions)."""
+    m = x.shape[0]
+    x32 = x.astype(np.float32)
+    ss = _sq_dist(x32, means[np.arange(m) // group]).astype(np.float32)
+    keys = ivf_keys(ss, np.arange(m))
+    top = np.argsort(keys)[::-1][:min(quota, m)]
+    return x32[top], (base + top) // block, base + top
+
+
+def ccc_assign(X: np.ndarray, C: np.ndarray) -> np.ndarray:
+    """_assign (:139-147): argmax <x, c> (fp64 dimension order, rounded), ties to the lower c."""
+    return ivf_keys(_dot_seq(X, C), np.arange(C.shape[0])[None, :]).argmax(1)
+
+
+def ccc_kmeans(X: np.ndarray, nlist: int, iters: int = 6, C0: np.ndarray | None = None):
+    """_kmeans (:149-161): inner-product Lloyd rounds from C0 (warm) or from the evenly spaced
+    rows X[c * n // nlist] (cold; the reference draws a seeded random sample); a centroid with
+    members becomes fl32 of the fp64 mean of its members in ascending order."""
+    n = X.shape[0]
+    C = (X[[(c * n) // nlist for c in range(nlist)]] if C0 is None else C0).astype(np.float32).copy()
+    X64 = X.astype(np.float64)
+    for _ in range(iters):
+        a = ccc_assign(X, C)
+        for c in range(nlist):
+            mem = np.nonzero(a == c)[0]
+            if len(mem):
+                C[c] = (_seq_sum(X64[mem], 0) / len(mem)).astype(np.float32)
+    return C
+
+
+def ccc_radii(X: np.ndarray, C: np.ndarray, a: np.ndarray, R: np.ndarray) -> np.ndarray:
+    """_update_radii (:192-194): R[c] = max(R[c], fl32(||x - c||)) over the rows assigned to c."""
+    r = np.sqrt(_sq_dist(X, C[a])).astype(np.float32)
+    R = R.copy()
+    np.maximum.at(R, a, r)
+    return R
+
+
+class CascadeOracle:
+    """CausalCascade (ssa/cascade_router.py:66-415) on the CPU, proj = None: the state machine
+    (staging, commit, first build, incremental add, rebuild), the routing metric, the
+    escalation and the certificate, with the deterministic choices of the library's kernels
+    (ccc_kmeans' cold start, fp64 inner products rounded once, ties to the lower index)."""
+
+    def __init__(self, d, block=128, sub=32, top_c=8, local=1, nprobe=4, chunk_blocks=2048,
+                 retrain_every=None, n_hint=None, outlier_rate=1e-3, outlier_cap=4,
+                 cert_margin=0.0, max_escalations=2, escalate_factor=4, search_k=None,
+                 nlist=None, kmeans=None):
+        self.d, self.block, self.sub, self.spb = d, block, sub, block // sub
+        self.top_c, self.local, self.nprobe = top_c, local, nprobe
+        self.chunk_blocks, self.retrain_every = chunk_blocks, retrain_every
+        self.outlier_rate, self.outlier_cap = outlier_rate, outlier_cap
+        self.cert_margin, self.max_escalations = cert_margin, max_escalations
+        self.escalate_factor = escalate_factor
+        self.search_k = search_k or 4 * top_c
+        if nlist is not None:
+            self.nlist = nlist
+        elif n_hint is not None:
+            self.nlist = max(4, int((n_hint / sub) ** 0.5))
+        else:
+            self.nlist = None
+        self.build_threshold = max(4 * (self.nlist or 4), 16384)
+        self.kmeans = kmeans            # a replacement for ccc_kmeans (fixed centroids), or None
+        self.means = np.zeros((0, d), np.float32)
+        self.committed = 0
+        self.C = None                   # centroids once the index exists
+        self.Rc = None
+        self.assign = None              # cell of every committed sub-mean
+        self.committed_at_rebuild = 0
+        self.chunks_since_rebuild = 0
+        self.O = np.zeros((0, d), np.float32)
+        self.O_parent = np.zeros(0, np.int64)
+        self.O_pos = np.zeros(0, np.int64)
+
+    @property
+    def n_sub(self):
+        return self.means.shape[0]
+
+    def append(self, k_chunk):
+        """:120-128 (commit, summarise, stage) and :214-231 (outliers)."""
+        self._commit()
+        k32 = np.asarray(k_chunk, np.float32)
+        m = k32.shape[0]
+        assert m % self.sub == 0
+        mu = ccc_group_means(k32, self.sub)
+        quota = max(1, int(self.outlier_rate * m))
+        v, p, s = ccc_outliers(k32, mu, self.sub, quota, self.n_sub * self.sub, self.block)
+        self.means = np.concatenate([self.means, mu])
+        self.O = np.concatenate([self.O, v])
+        self.O_parent = np.concatenate([self.O_parent, p])
+        self.O_pos = np.concatenate([self.O_pos, s])
+
+    def _commit(self):
+        """:130-147."""
+        if self.n_sub <= self.committed:
+            return
+        if self.C is None:
+            self.committed = self.n_sub
+            if self.n_sub >= self.build_threshold:
+                self._build_index()
+            return
+        X = self.means[self.committed:]
+        a = ccc_assign(X, self.C)
+        self.assign = np.concatenate([self.assign, a])
+        self.Rc = ccc_radii(X, self.C, a, self.Rc)
+        self.committed = self.n_sub
+        self.chunks_since_rebuild += 1
+        due = (self.chunks_since_rebuild >= self.retrain_every) if self.retrain_every \
+            else (self.committed >= 2 * max(1, self.committed_at_rebuild))
+        if due:
+            self._build_index()
+
+    def _build_index(self, iters=6):
+        """:163-190 (first build and warm rebuilds)."""
+        X = self.means[:self.committed]
+        if self.nlist is None:
+            self.nlist = max(4, int(self.committed ** 0.5))
+        if self.kmeans is not None:
+            C = np.asarray(self.kmeans(X, iters), np.float32)
+        else:
+            warm = self.C is not None and self.C.shape[0] == self.nlist
+            C = ccc_kmeans(X, self.nlist, iters, self.C if warm else None)
+        self.C = C
+        self.assign = ccc_assign(X, C)
+        self.Rc = ccc_radii(X, C, self.assign, np.zeros(self.nlist, np.float32))
+        self.committed_at_rebuild = self.committed
+        self.chunks_since_rebuild = 0
+
+    def lists(self):
+        return [np.nonzero(self.assign == c)[0] for c in range(self.nlist)]
+
+    def route(self, q_chunk, qpos, certify=False, search_k=None):
+        """:282-331 -> (kv_num (nbq,), kv_idx list of ascending block lists, cert (nbq,) bool,
+        rounds (nbq,))."""
+        qr = ccc_group_means(np.asarray(q_chunk, np.float32), self.block)
+        return self.route_rows(qr, qpos // self.block, certify, search_k)
+
+    def route_rows(self, qr, qb_start, certify=False, search_k=None):
+        nbq = qr.shape[0]
+        sk0 = search_k or self.search_k
+        comm = self.committed
+        ns = self.n_sub - comm
+        sj = np.arange(comm, self.n_sub)
+        st_scores = _dot_seq(qr, self.means[comm:]) if ns else np.zeros((nbq, 0), np.float32)
+        cm_scores = _dot_seq(qr, self.means[:comm]) if comm else np.zeros((nbq, 0), np.float32)
+        o_scores = _dot_seq(qr, self.O) if len(self.O) else np.zeros((nbq, 0), np.float32)
+        if self.C is not None:
+            cs = _dot_seq(qr, self.C)
+            lists = self.lists()
+        kv, cert = [], np.zeros(nbq, bool)
+        rounds = np.zeros(nbq, np.int32)
+        for i in range(nbq):
+            qblk = qb_start + i
+            q64 = qr[i].astype(np.float64)
+            qn = np.float32(np.sqrt(_seq_sum(q64 * q64, 0)))
+            ok_st = sj // self.spb < qblk
+            stk = ivf_keys(st_scores[i][ok_st], sj[ok_st])
+            stk = np.sort(stk)[::-1][:min(self.search_k, ns)]
+            nprobe = min(self.nprobe, self.nlist) if self.C is not None else self.nprobe
+            sk = sk0
+            for rnd in range(self.max_escalations + 1):
+                kc = min(sk, comm)
+                dlast = np.float32(-np.inf)
+                cmk = np.zeros(0, np.uint64)
+                probed = None
+                if comm and kc:
+                    if self.C is None:
+                        cmk = np.sort(ivf_keys(cm_scores[i], np.arange(comm)))[::-1][:kc]
+                    else:
+                        ck = ivf_keys(cs[i], np.arange(self.nlist))
+                        probed = np.argsort(ck)[::-1][:nprobe]
+                        mem = np.concatenate([lists[c] for c in probed]).astype(np.int64)
+                        cmk = np.sort(ivf_keys(cm_scores[i][mem], mem))[::-1][:kc]
+                        if len(mem) >= kc:
+                            dlast = _key_score(cmk[-1])
+                cand = np.concatenate([cmk, stk])
+                best = {}
+                for key in sorted(cand.tolist(), reverse=True):         # score desc, sub asc
+                    p = _key_index(key) // self.spb
+                    if p not in best:
+                        best[p] = key
+                kept = sorted(best.items(), key=lambda t: -t[1])[:self.top_c]
+                tau = _key_score(min(k for _, k in kept)) if kept else np.float32(-np.inf)
+                opar = []
+                cap = min(self.outlier_cap, len(self.O))
+                if cap:
+                    hit = np.nonzero((self.O_parent < qblk) & (o_scores[i] > tau))[0]
+                    ok = np.sort(ivf_keys(o_scores[i][hit], hit))[::-1][:cap]
+                    opar = [int(self.O_parent[_key_index(k)]) for k in ok.tolist()]
+                loc = [qblk - L for L in range(self.local + 1) if qblk - L >= 0]
+                kv_i = sorted(set([p for p, _ in kept]) | set(opar) | set(loc))
+                ok_cert = False
+                if certify:
+                    full = len(kept) >= min(self.top_c, qblk)
+                    has_tau = tau > -np.inf
+                    if self.C is None:
+                        ok_cert = full and (has_tau or qblk == 0)
+                    else:
+                        lim = np.float32(tau) - np.float32(self.cert_margin)
+                        ub = cs[i] + qn * self.Rc                          # float32 ops
+                        unp = np.ones(self.nlist, bool)
+                        unp[probed] = False
+                        mx = ub[unp].max() if unp.any() else np.float32(-np.inf)
+                        ok_cert = bool(full and has_tau and mx < lim and dlast < lim)
+                    rounds[i] = rnd
+                if not certify or ok_cert or self.C is None:
+                    break
+                if rnd == self.max_escalations:
+                    break
+                nprobe = min(nprobe * self.escalate_factor, self.nlist)
+                sk = min(sk * 2, comm)
+            cert[i] = ok_cert
+            kv.append(kv_i)
+        return np.array([len(x) for x in kv], np.int32), kv, cert, rounds
+
+
+def _key_index(key) -> int:
+    return 0xFFFFFFFF - (int(key) & 0xFFFFFFFF)
+
+
+def _key_score(key) -> np.float32:
+    """The float32 score an ivf_keys key came from."""
+    k = (int(key) >> 32) & 0xFFFFFFFF
+    u = (k ^ 0x80000000) if k & 0x80000000 else (~k & 0xFFFFFFFF)
+    return np.array([u], np.uint32).view(np.float32)[0]

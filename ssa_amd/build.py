@@ -21,7 +21,7 @@ LIB = PKG / "libssa_hip.so"
 ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "summary.hip", "route.hip", "attn.hip", "decode.hip", "swap.hip", "ivf.hip",
-           "tree.hip"]
+           "tree.hip", "ccc.hip"]
 
 
 def hipcc() -> str:
