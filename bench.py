@@ -86,6 +86,72 @@ def _event_ms(torch, fn, reps, warm=2):
     return s.elapsed_time(e) / reps
 
 
+# paper/figures/ccc_kernel.json rows (RTX 4080): append / route / attention ms, certified rate
+CCC_REFERENCE = {
+    262144: {"append_ms": 2.717, "route_ms": 4.805, "attention_ms": 1.15, "cert_rate": 1.0},
+    1048576: {"append_ms": 192.061, "route_ms": 60.818, "attention_ms": 5.128,
+              "cert_rate": 0.968},
+    4194304: {"append_ms": 132.086, "route_ms": 144.412, "attention_ms": 20.35,
+              "cert_rate": 0.856},
+    12582912: {"append_ms": 393.929, "route_ms": 519.643, "attention_ms": 66.802,
+               "cert_rate": 0.737}}
+
+
+def ccc_decompose(torch, dev, n, g, chunk_blocks=1024):
+    """The reference's selector-share decomposition (ssa/cascade_router.py:459-503,
+    decompose_ccc): clustered single-head keys and queries as its _gen (:459-473), one streaming
+    pass of append (summaries, outliers, index upkeep) and route (search, certificate,
+    escalation) per chunk of 1024 blocks, each timed between device synchronisations as the
+    reference times them, then the block-sparse attention over the assembled lists."""
+    from ssa_amd import cascade_router as CR, ssa_kernel as K
+    d, blk = 64, 128
+    nb4 = n // 32
+    nc = max(8, int(nb4 ** 0.5))
+    ctr = torch.randn(nc, d, generator=g, device=dev)
+    a = torch.randint(0, nc, (nb4,), generator=g, device=dev)
+    k = (ctr[a].repeat_interleave(32, 0) + 0.1 * torch.randn(n, d, generator=g, device=dev)).half()
+    nbq = n // blk
+    qc = ctr[torch.randint(0, nc, (nbq,), generator=g, device=dev)]
+    q = (qc.repeat_interleave(blk, 0) + 0.2 * torch.randn(n, d, generator=g, device=dev)).half()
+    v = torch.randn(n, d, generator=g, device=dev, dtype=torch.float16)
+    del ctr, a, qc
+    cc = CR.CausalCascade(d, block=blk, n_hint=n, chunk_blocks=chunk_blocks)
+    W = min(cc.top_c + cc.local + 1 + cc.outlier_cap, nbq)
+    kv_num = torch.empty(1, 1, nbq, dtype=torch.int32, device=dev)
+    kv_idx = torch.zeros(1, 1, nbq, W, dtype=torch.int32, device=dev)
+    cb = chunk_blocks * blk
+    app = rte = 0.0
+    certs, rounds, rebuilds = [], [], 0
+    torch.cuda.synchronize()
+    for t in range(0, n, cb):
+        e = min(n, t + cb)
+        before = cc.committed_at_rebuild
+        t0 = time.perf_counter()
+        cc.append(k[t:e])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        kn, ki, cert, st = cc.route(q[t:e], t, certify=True)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        app += t1 - t0
+        rte += t2 - t1
+        rebuilds += cc.committed_at_rebuild != before and t > 0
+        kv_num[0, 0, t // blk:e // blk] = kn
+        kv_idx[0, 0, t // blk:e // blk, :ki.shape[1]] = ki
+        certs.append(cert.float().mean().item())
+        rounds.append(st["rounds"].float().mean().item())
+    q4, k4, v4 = (x.view(1, 1, n, d) for x in (q, k, v))
+    att = _event_ms(torch, lambda: K.sparse_attention(q4, k4, v4, kv_num, kv_idx, blk), 3, warm=1)
+    sel = (app + rte) * 1000.0
+    res = {"append_ms": app * 1000.0, "route_ms": rte * 1000.0, "attention_ms": att,
+           "selector_share": sel / (sel + att), "rebuilds": rebuilds,
+           "cert_rate": sum(certs) / len(certs), "mean_rounds": sum(rounds) / len(rounds),
+           "sum_kv_num": int(kv_num.sum())}
+    del q, k, v, q4, k4, v4, cc, kv_num, kv_idx
+    torch.cuda.empty_cache()
+    return res
+
+
 def published_bench(torch, dev):
     """The shapes of the reference's own published measurements, run here with seeded N(0,1)
     inputs on the device. The reference's figures were taken on an RTX 4080 with FlexAttention /
@@ -100,7 +166,9 @@ def published_bench(torch, dev):
       treecode router (ssa/treecode_bench.py: build_tree over fp16 keys, H=8, d=64, block 128, F 8,
         then the Q-tiled descend_beam of nb random query rows per head, W 16, top_c 8):
         paper/figures/treecode_router_measured.json:18-33 (build 23.8 / descend 63.3 ms at
-        1,048,576; 56.6 / 115.4 ms at 2,097,152)."""
+        1,048,576; 56.6 / 115.4 ms at 2,097,152);
+      certified causal cascade (ccc_decompose below), H=1, d=64, clustered keys, certify,
+        chunk_blocks 1024: paper/figures/ccc_kernel.json rows (append / route / attention)."""
     from ssa_amd import ivf_decode as D, ivf_kernel as IV, ssa_kernel as K, treecode as TC
     sdpa = torch.nn.functional.scaled_dot_product_attention
     g = torch.Generator(device=dev).manual_seed(11)
@@ -135,6 +203,8 @@ def published_bench(torch, dev):
                                     "reference_build_ms": ref_build,
                                     "reference_descend_ms": ref_desc}
         del k, qb, levels
+    for n, ref in CCC_REFERENCE.items():
+        out[f"ccc_h1_n{n}"] = dict(ccc_decompose(torch, dev, n, g), reference=ref)
     n, steps = 1 << 20, 128
     q, k, v = qkv(1, n + steps)
     dec = D.RoutedDecoder(1, 1, 1, 64, n + steps, block=128, top_c=8, local=1,

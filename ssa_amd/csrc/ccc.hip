@@ -440,6 +440,7 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
           }
           nprobed = running;
         }
+        __syncthreads();  // the probed lists (written by any wave) before their sizes are read
         {
           int running = 0;
           for (int p0 = 0; p0 < nprobed; p0 += 256) {

@@ -138,6 +138,17 @@ def test_stream_index_regime(cuda, geom, nprobe, extra):
         assert s["rounds"] >= 1
 
 
+@pytest.mark.parametrize("nlist,geom", [(181, "clustered"), (150, "random")])
+def test_stream_many_cells(cuda, nlist, geom):
+    """More than 64 cells: the probed lists are found by threads of several waves (a missing
+    workgroup barrier between writing them and reading their sizes once let a route read stale
+    list ids at 1M tokens)."""
+    n = 400 * BLOCK
+    q, k = _clustered(n, seed=6) if geom == "clustered" else _random(n, seed=6)
+    s = _stream(cuda, q, k, 16, True, force_build=512, nlist=nlist, top_c=8, nprobe=4)
+    assert s["built"]
+
+
 def test_stream_long_scans(cuda):
     """More than 2048 candidates per search (several passes of the streaming top-k): a flat scan
     over 2304 committed sub-means, then a 4-list index whose probed lists hold ~3000."""
