@@ -41,6 +41,18 @@ Pinning (what checks each function; details in tests/test_oracle.py):
                          reduces the descent to the flat top_c of the leaf bounds; recall climbs
                          with W to the flat ceiling (treecode.py:160-200); the causal mask keeps
                          every selected leaf at or before q_pos.
+  CascadeOracle /        (faiss is absent and the reference holds no fixtures for
+  ccc_* (cascade)        ssa/cascade_router.py; tests/test_oracle_ccc.py.) Its own mechanics and
+                         soundness tests restated: exhaustive search equals the brute-force
+                         sub-block max-pool (float64); one chunk or 2-block chunks select alike;
+                         causal / own-block / unique lists; every certified row holds the exact
+                         top-k routing blocks with a built index (clustered and random keys),
+                         and dropping the radii from the bound breaks that; incremental radii
+                         bound every member and are exact after a rebuild; escalation never
+                         lowers the certified rate and raises it on random keys; the outlier
+                         channel catches a hidden 12 u key the sub-block routing misses; a
+                         starved probe fails closed. Closed forms: group means, outlier order,
+                         Lloyd update of two separated clusters.
 """
 from __future__ import annotations
 
