@@ -250,7 +250,8 @@ int ssa_tree_descend(const void* tree, const float* q, const int64_t* q_pos, int
  *   order / group, rounded once; m / group groups). quota > 0 (at most 2048, m a multiple of
  *   group): the min(quota, m) rows of largest fl32(||x_row - mean||^2) (fp64, dimension order;
  *   ties to the lower row) are written, largest first, to out_vec (fp32, d each), out_parent =
- *   (base_tok + row) / block, out_pos = base_tok + row; ws holds 8 m bytes.
+ *   (base_tok + row) / block, out_pos = base_tok + row; ws holds
+ *   8 m + 8 min(quota, m) ceil(m / 2048) bytes.
  * ssa_ccc_kmeans (_kmeans, :149-161): iters inner-product Lloyd rounds over x (n, d): every row
  *   joins the centroid of largest <x, c>, each centroid with members becomes fl32 of their fp64
  *   mean (ascending member order). warm = 0 starts centroid c at x[c * n / nlist]; otherwise cent

@@ -187,7 +187,7 @@ class CausalCascade:
             raise ValueError(f"append: outlier quota {quota} exceeds {MAX_QUOTA}")
         self._ensure_means(m4)
         self._ensure_outliers(quota)
-        ws = self._scratch(8 * m_tok)
+        ws = self._scratch(8 * m_tok + 8 * quota * (-(-m_tok // 2048)))
         _lib.call("ssa_ccc_stage", kr.data_ptr(), _lib.dtype_code(kr.dtype), m_tok, self.dr,
                   kr.stride(0), self.sub, self.means[self.n_sub].data_ptr(), quota,
                   self.n_sub * self.sub, self.block, self.O[self.n_out].data_ptr(),

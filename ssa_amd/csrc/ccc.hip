@@ -9,7 +9,8 @@
 // ssa_ccc_stage (append + _extract_outliers, :120-128,:214-231): means of `group` consecutive
 //   rows, fp64 sums in row order rounded once; with quota > 0, every row's squared distance to its
 //   group mean (fp64, dimension order) and the quota rows of largest distance (ties to the lower
-//   row), copied out as outlier keys, largest first.
+//   row; each tile of 2048 rows keeps its own quota best first), copied out as outlier keys,
+//   largest first.
 // ssa_ccc_kmeans / ssa_ccc_index_build / ssa_ccc_index_add (_kmeans, _build_index, _commit,
 //   _update_radii, :131-198): inner-product Lloyd rounds (each mean joins the centroid of largest
 //   inner product, ties to the lower centroid; a centroid with members becomes their mean), the
@@ -42,6 +43,26 @@ __device__ inline float key_score(unsigned long long key) {
   const unsigned int k = (unsigned int)(key >> 32);
   const unsigned int u = (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k;
   return __uint_as_float(u);
+}
+
+// <q, row> for a row-major fp32 row (16-byte aligned, d a multiple of 32): the same fp64 chain in
+// dimension order as dot_strided, the row read with 16-byte loads.
+__device__ inline float dot_row(const float* q, const float* row, int64_t d) {
+  double acc = 0.0;
+  for (int64_t t0 = 0; t0 < d; t0 += 32) {
+    float4 x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const float4*>(row + t0 + 4 * u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 qq = *reinterpret_cast<const float4*>(q + t0 + 4 * u);
+      acc = fma((double)qq.x, (double)x[u].x, acc);
+      acc = fma((double)qq.y, (double)x[u].y, acc);
+      acc = fma((double)qq.z, (double)x[u].z, acc);
+      acc = fma((double)qq.w, (double)x[u].w, acc);
+    }
+  }
+  return (float)acc;
 }
 
 // Smallest of v[0..n) (LDS) over a 256-thread workgroup; slot holds 4 values.
@@ -77,16 +98,22 @@ __device__ inline float block_max_f32(float x, float* slot) {
 }
 
 // Streams M candidates through buf (LDS, kIvfCap keys), keeping the K largest (K <= kIvfMaxSearch,
-// keys unique); keyof(m) is candidate m's key, or 0 to skip it. Returns how many are kept (in
+// keys unique); keyof(m) is candidate m's key, or 0 to skip it. Once K keys are kept, a candidate
+// below the threshold that kept them (K keys above it already) cannot enter the K largest and is
+// dropped on arrival, so later batches fill the buffer slowly. Returns how many are kept (in
 // buf[0..), any order). 256 threads.
 template <typename F>
 __device__ int stream_top(unsigned long long* buf, int64_t M, int K, F keyof, unsigned int* hist,
                           unsigned int* shv, int* ws) {
   int nk = 0;
+  unsigned long long floor_key = 1ull;  // every real key is at least 1
   for (int64_t m0 = 0; m0 < M;) {
     const int room = kIvfCap - nk;
     const int batch = (int)(M - m0 < room ? M - m0 : room);
-    for (int e = threadIdx.x; e < batch; e += 256) buf[nk + e] = keyof(m0 + e);
+    for (int e = threadIdx.x; e < batch; e += 256) {
+      const unsigned long long k = keyof(m0 + e);
+      buf[nk + e] = k >= floor_key ? k : 0ull;
+    }
     __syncthreads();
     int tot = block_compact<unsigned long long>(buf, nk + batch, buf, ws,
                                                 [](unsigned long long k) { return k != 0ull; });
@@ -94,6 +121,7 @@ __device__ int stream_top(unsigned long long* buf, int64_t M, int K, F keyof, un
       const unsigned long long T = block_kth_largest(buf, tot, K, hist, shv);
       tot = block_compact<unsigned long long>(buf, tot, buf, ws,
                                               [T](unsigned long long k) { return k >= T; });
+      floor_key = T;
     }
     nk = tot;
     m0 += batch;
@@ -143,8 +171,33 @@ __global__ __launch_bounds__(64) void ccc_means_kernel(const void* __restrict__ 
   }
 }
 
-// One workgroup: the K largest of the m row keys, largest first, copied out as outlier keys
-// (fp32 vector, parent block (base + row) / block, position base + row).
+// One workgroup per tile of kIvfCap row keys: the tile's K largest (every key of a tile holding
+// at most K), written to cand[tile * K ..] and padded with 0 (no key). The K largest of all rows
+// are among them.
+__global__ __launch_bounds__(256) void ccc_tile_top_kernel(
+    const unsigned long long* __restrict__ keys, int64_t m, int K,
+    unsigned long long* __restrict__ cand) {
+  __shared__ unsigned long long buf[kIvfCap];
+  __shared__ unsigned int hist[256];
+  __shared__ unsigned int shv[3];
+  __shared__ int ws[4];
+  const int64_t t0 = (int64_t)blockIdx.x * kIvfCap;
+  const int n = (int)(m - t0 < kIvfCap ? m - t0 : kIvfCap);
+  for (int e = threadIdx.x; e < n; e += 256) buf[e] = keys[t0 + e];
+  __syncthreads();
+  int keep = n;
+  if (n > K) {
+    const unsigned long long T = block_kth_largest(buf, n, K, hist, shv);
+    keep = block_compact<unsigned long long>(buf, n, buf, ws,
+                                             [T](unsigned long long k) { return k >= T; });
+  }
+  unsigned long long* out = cand + (int64_t)blockIdx.x * K;
+  for (int e = threadIdx.x; e < K; e += 256) out[e] = e < keep ? buf[e] : 0ull;
+}
+
+// One workgroup: the K largest of the m candidate keys (at least K of them real, the rest 0),
+// largest first, copied out as outlier keys (fp32 vector of the key's row, parent block
+// (base + row) / block, position base + row).
 template <int DT>
 __global__ __launch_bounds__(256) void ccc_outlier_kernel(
     const unsigned long long* __restrict__ keys, int64_t m, int K, const void* __restrict__ x,
@@ -320,11 +373,10 @@ int ccc_lists(const float* x, int64_t n, int64_t d, int64_t nlist, const CccLayo
   int32_t* tcount = reinterpret_cast<int32_t*>(base + L.tcount);
   ccc_rank_kernel<<<(unsigned)ntiles, kTile, 0, s>>>(assign, n, nlist, rank, tcount);
   SSA_TRY(launch_status("ccc_rank_kernel"));
-  ivf_scatter_kernel<<<dim3((unsigned)ntiles, 1), 256, 0, s>>>(
-      assign, rank, tcount, n, nlist, ntiles, reinterpret_cast<int32_t*>(base + L.count),
-      reinterpret_cast<int32_t*>(base + L.off), reinterpret_cast<int32_t*>(base + L.ids), x, d,
-      with_means ? reinterpret_cast<float*>(base + L.muL) : nullptr);
-  return launch_status("ivf_scatter_kernel");
+  return ivf_lists(assign, rank, tcount, 1, n, nlist, ntiles,
+                   reinterpret_cast<int32_t*>(base + L.count), reinterpret_cast<int32_t*>(base + L.off),
+                   reinterpret_cast<int32_t*>(base + L.ids), x, d,
+                   with_means ? reinterpret_cast<float*>(base + L.muL) : nullptr, s);
 }
 
 // ---- route ----------------------------------------------------------------------------------------
@@ -397,7 +449,7 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
         [&](int64_t m) -> unsigned long long {
           const int64_t j = committed + m;
           if (j / spb >= qblk) return 0ull;
-          return ivf_key(dot_strided(qs, means + j * d, 1, d), j);
+          return ivf_key(dot_row(qs, means + j * d, d), j);
         },
         hist, shv, ws);
     for (int e = tid; e < nst; e += 256) stg[e] = buf[e];
@@ -421,7 +473,7 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
         ncm = stream_top(
             buf, committed, (int)kc,
             [&](int64_t m) -> unsigned long long {
-              return ivf_key(dot_strided(qs, means + m * d, 1, d), m);
+              return ivf_key(dot_row(qs, means + m * d, d), m);
             },
             hist, shv, ws);
       } else {
@@ -528,7 +580,7 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
           buf, a.n_out, cap,
           [&](int64_t r) -> unsigned long long {
             if (op[r] >= qblk) return 0ull;
-            const float s = dot_strided(qs, ov + r * d, 1, d);
+            const float s = dot_row(qs, ov + r * d, d);
             return s > tau ? ivf_key(s, r) : 0ull;
           },
           hist, shv, ws);
@@ -654,8 +706,12 @@ int ccc_stage_impl(const void* x, int64_t m, int64_t d, int64_t rs, int64_t grou
     ssa::ccc_means_kernel<DT, true><<<(unsigned)ng, 64, 0, s>>>(x, rs, d, group, means, keys);
     SSA_TRY(ssa::launch_status("ccc_means_kernel"));
     const int K = (int)(quota < m ? quota : m);
-    ssa::ccc_outlier_kernel<DT><<<1, 256, 0, s>>>(keys, m, K, x, rs, d, base, block, ovec, opar,
-                                                  opos);
+    const int64_t ntiles = (m + ssa::kIvfCap - 1) / ssa::kIvfCap;
+    unsigned long long* cand = keys + m;
+    ssa::ccc_tile_top_kernel<<<(unsigned)ntiles, 256, 0, s>>>(keys, m, K, cand);
+    SSA_TRY(ssa::launch_status("ccc_tile_top_kernel"));
+    ssa::ccc_outlier_kernel<DT><<<1, 256, 0, s>>>(cand, ntiles * K, K, x, rs, d, base, block,
+                                                  ovec, opar, opos);
     return ssa::launch_status("ccc_outlier_kernel");
   }
   if (ng == 0) return SSA_OK;
@@ -684,7 +740,9 @@ extern "C" int ssa_ccc_stage(const void* x, int dtype, int64_t m, int64_t d, int
                 (long long)group);
     SSA_REQUIRE(out_vec != nullptr && out_parent != nullptr && out_pos != nullptr && block > 0,
                 SSA_ERR_INVALID, "ccc_stage: outlier outputs are NULL or block <= 0");
-    SSA_TRY(check_ccc_buffer("ccc_stage", ws, ws_bytes, size_t(m) * 8));
+    const int64_t K = quota < m ? quota : m;
+    SSA_TRY(check_ccc_buffer("ccc_stage", ws, ws_bytes,
+                             size_t(m) * 8 + size_t(K) * 8 * ((m + ssa::kIvfCap - 1) / ssa::kIvfCap)));
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   unsigned long long* keys = static_cast<unsigned long long*>(ws);

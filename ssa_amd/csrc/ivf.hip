@@ -299,9 +299,8 @@ extern "C" int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d,
     ssa::ivf_rank_kernel<<<gt, ssa::kTile, 0, s>>>(pbest, nb, nlist, L.ntiles, L.groups, assign,
                                                     rank, tcount);
     SSA_TRY(ssa::launch_status("ivf_rank_kernel"));
-    ssa::ivf_scatter_kernel<<<gt, 256, 0, s>>>(assign, rank, tcount, nb, nlist, L.ntiles, count,
-                                               off, ids, mu, d, last ? muL : nullptr);
-    SSA_TRY(ssa::launch_status("ivf_scatter_kernel"));
+    SSA_TRY(ssa::ivf_lists(assign, rank, tcount, BH, nb, nlist, L.ntiles, count, off, ids, mu, d,
+                           last ? muL : nullptr, s));
     if (last) break;
     switch ((d + 63) / 64) {
       case 1: ssa::ivf_update_kernel<1><<<gc, 64, 0, s>>>(mu, count, off, ids, nb, d, nlist, cent); break;

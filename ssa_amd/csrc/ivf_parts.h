@@ -247,61 +247,84 @@ __global__ __launch_bounds__(256) void ivf_rank_kernel(
   }
 }
 
-// One workgroup per tile: list sizes (count), list offsets (off, nlist + 1 per head) and, for the
-// tile's block means, their slots in ids: offset of the list + members in earlier tiles + rank.
-// Every workgroup derives the offsets from tcount; tile 0 writes count and off. With muL set
-// (the last assignment), each block mean is also copied to its list's transposed storage:
-// element t of member k of list p at d * off[p] + t * size[p] + k.
-__global__ __launch_bounds__(256) void ivf_scatter_kernel(
-    const int32_t* __restrict__ assign, const int32_t* __restrict__ rank,
-    const int32_t* __restrict__ tcount, int64_t nb, int64_t nlist, int64_t ntiles,
-    int32_t* __restrict__ count, int32_t* __restrict__ off, int32_t* __restrict__ ids,
-    const float* __restrict__ mu, int64_t d, float* __restrict__ muL) {
-  __shared__ int base[kIvfCap];
-  __shared__ int offl[kIvfCap];
-  __shared__ int cntl[kIvfCap];
+// One workgroup per (centroid, head): tcount[t] <- the centroid's members in the tiles before t
+// (an exclusive prefix over the tiles, in place, 256 tiles per pass) and count = its members in
+// all tiles. Work O(tiles x centroids).
+__global__ __launch_bounds__(256) void ivf_tile_prefix_kernel(int32_t* __restrict__ tcount,
+                                                               int64_t ntiles, int64_t nlist,
+                                                               int32_t* __restrict__ count) {
   __shared__ int ws[4];
+  const int64_t bh = blockIdx.y, c = blockIdx.x;
+  int32_t* col = tcount + bh * ntiles * nlist + c;
+  int running = 0;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 256) {
+    const int64_t t = t0 + threadIdx.x;
+    const int v = t < ntiles ? col[t * nlist] : 0;
+    int tot;
+    const int ex = ivf_block_scan(v, ws, &tot);
+    if (t < ntiles) col[t * nlist] = running + ex;
+    running += tot;
+  }
+  if (threadIdx.x == 0) count[bh * nlist + c] = running;
+}
+
+// One workgroup per head: off[c] = the members of the centroids before c, off[nlist] = all.
+__global__ __launch_bounds__(256) void ivf_offsets_kernel(const int32_t* __restrict__ count,
+                                                           int64_t nlist,
+                                                           int32_t* __restrict__ off) {
+  __shared__ int ws[4];
+  const int64_t bh = blockIdx.x;
   const int tid = threadIdx.x;
-  const int64_t bh = blockIdx.y, tile = blockIdx.x;
   int running = 0;
   for (int64_t c0 = 0; c0 < nlist; c0 += 256) {
     const int64_t c = c0 + tid;
-    int tot = 0, bef = 0;
-    if (c < nlist) {
-      const int32_t* col = tcount + bh * ntiles * nlist + c;
-#pragma unroll 8
-      for (int64_t t = 0; t < ntiles; ++t) {
-        const int x = col[t * nlist];
-        tot += x;
-        bef += t < tile ? x : 0;
-      }
-    }
-    int all;
-    const int ex = ivf_block_scan(tot, ws, &all);
-    if (c < nlist) {
-      base[c] = running + ex + bef;
-      offl[c] = running + ex;
-      cntl[c] = tot;
-      if (tile == 0) {
-        count[bh * nlist + c] = tot;
-        off[bh * (nlist + 1) + c] = running + ex;
-      }
-    }
-    running += all;
+    const int v = c < nlist ? count[bh * nlist + c] : 0;
+    int tot;
+    const int ex = ivf_block_scan(v, ws, &tot);
+    if (c < nlist) off[bh * (nlist + 1) + c] = running + ex;
+    running += tot;
   }
-  if (tile == 0 && tid == 0) off[bh * (nlist + 1) + nlist] = running;
-  __syncthreads();
-  const int64_t j = tile * kTile + tid;
-  if (j < nb) {
-    const int a = assign[bh * nb + j];
-    const int pos = base[a] + rank[bh * nb + j];
-    ids[bh * nb + pos] = (int32_t)j;
-    if (muL != nullptr) {
-      const float* src = mu + (bh * nb + j) * d;
-      float* dst = muL + bh * nb * d + d * (int64_t)offl[a] + (pos - offl[a]);
-      for (int64_t t = 0; t < d; ++t) dst[t * cntl[a]] = src[t];
-    }
+  if (tid == 0) off[bh * (nlist + 1) + nlist] = running;
+}
+
+// One thread per block mean: its slot in ids = offset of its list + members of the list in
+// earlier tiles (tbase, the prefix of ivf_tile_prefix_kernel) + its rank in its tile. With muL set
+// (the last assignment), the mean is also copied to its list's transposed storage: element t of
+// member k of list p at d * off[p] + t * size[p] + k.
+__global__ __launch_bounds__(256) void ivf_scatter_kernel(
+    const int32_t* __restrict__ assign, const int32_t* __restrict__ rank,
+    const int32_t* __restrict__ tbase, int64_t nb, int64_t nlist, int64_t ntiles,
+    const int32_t* __restrict__ count, const int32_t* __restrict__ off, int32_t* __restrict__ ids,
+    const float* __restrict__ mu, int64_t d, float* __restrict__ muL) {
+  const int64_t bh = blockIdx.y, tile = blockIdx.x;
+  const int64_t j = tile * kTile + threadIdx.x;
+  if (j >= nb) return;
+  const int a = assign[bh * nb + j];
+  const int o = off[bh * (nlist + 1) + a];
+  const int pos = o + tbase[(bh * ntiles + tile) * nlist + a] + rank[bh * nb + j];
+  ids[bh * nb + pos] = (int32_t)j;
+  if (muL != nullptr) {
+    const int64_t L = count[bh * nlist + a];
+    const float* src = mu + (bh * nb + j) * d;
+    float* dst = muL + bh * nb * d + d * (int64_t)o + (pos - o);
+    for (int64_t t = 0; t < d; ++t) dst[t * L] = src[t];
   }
+}
+
+// The lists of an assignment whose per-tile ranks and counts (tcount) are set: sizes, offsets,
+// member ids in ascending order and, with muL, the transposed member storage. tcount is
+// overwritten with its prefix over the tiles.
+inline int ivf_lists(const int32_t* assign, const int32_t* rank, int32_t* tcount, int64_t BH,
+                     int64_t nb, int64_t nlist, int64_t ntiles, int32_t* count, int32_t* off,
+                     int32_t* ids, const float* mu, int64_t d, float* muL, hipStream_t s) {
+  ivf_tile_prefix_kernel<<<dim3((unsigned)nlist, (unsigned)BH), 256, 0, s>>>(tcount, ntiles,
+                                                                             nlist, count);
+  SSA_TRY(launch_status("ivf_tile_prefix_kernel"));
+  ivf_offsets_kernel<<<(unsigned)BH, 256, 0, s>>>(count, nlist, off);
+  SSA_TRY(launch_status("ivf_offsets_kernel"));
+  ivf_scatter_kernel<<<dim3((unsigned)ntiles, (unsigned)BH), 256, 0, s>>>(
+      assign, rank, tcount, nb, nlist, ntiles, count, off, ids, mu, d, muL);
+  return launch_status("ivf_scatter_kernel");
 }
 
 // centT (BH, d, nlist) = the centroids transposed.
