@@ -159,6 +159,35 @@ def test_stream_long_scans(cuda):
             max_escalations=1)
 
 
+def test_stream_with_projection(cuda):
+    """proj = a (d, d_r) matrix (ssa/cascade_router.py:51-61): keys and query-block means routed in
+    the d_r-dimensional space. The oracle gets the projected keys and query summaries the class
+    forms (the same per-chunk GEMMs), so every selection, certificate and round must agree."""
+    n, d_r, cb_blocks = 64 * BLOCK, 32, 8
+    q, k = _clustered(n, seed=12)
+    rng = np.random.default_rng(12)
+    Wp = torch.from_numpy((rng.standard_normal((64, d_r)) / 8).astype(np.float32)).to(cuda)
+    gpu = C.CausalCascade(64, proj=Wp, chunk_blocks=cb_blocks, n_hint=n, top_c=6, nprobe=2)
+    ora = O.CascadeOracle(d_r, chunk_blocks=cb_blocks, n_hint=n, top_c=6, nprobe=2)
+    assert gpu.dr == d_r and gpu.nlist == ora.nlist
+    gpu.build_threshold = ora.build_threshold = 48
+    qt, kt = dev16(q, cuda), dev16(k, cuda)
+    cb = cb_blocks * BLOCK
+    for t in range(0, n, cb):
+        gpu.append(kt[t:t + cb])
+        ora.append((kt[t:t + cb].float() @ Wp).cpu().numpy())
+        kn, ki, cert, st = gpu.route(qt[t:t + cb], t, certify=True)
+        qr = (C._group_means(qt[t:t + cb], BLOCK) @ Wp).cpu().numpy()
+        okn, okv, ocert, orounds = ora.route_rows(qr, t // BLOCK, True)
+        kn, ki = kn.cpu().numpy(), ki.cpu().numpy()
+        np.testing.assert_array_equal(kn, okn, err_msg=f"chunk at {t}")
+        for j in range(len(kn)):
+            assert ki[j, :kn[j]].tolist() == okv[j], (t, j)
+        np.testing.assert_array_equal(cert.cpu().numpy(), ocert)
+        np.testing.assert_array_equal(st["rounds"].cpu().numpy(), orounds)
+    assert ora.C is not None
+
+
 def test_ccc_full_budget_matches_dense(cuda):
     """test_cascade_router.py:42-55."""
     from ssa_amd.ssa_kernel import dense
