@@ -84,11 +84,12 @@ def test_kmeans_and_index_build(cuda, nlist):
     np.testing.assert_array_equal(cc.centroids.cpu().numpy(), Cw)
 
 
-def _stream(cuda, q, k, chunk_blocks, certify, force_build=None, **cfg):
+def _stream(cuda, q, k, chunk_blocks, certify, force_build=None, hint=True, **cfg):
     """The GPU cascade and the oracle side by side over the chunks; every route compared."""
     n = k.shape[0]
-    gpu = C.CausalCascade(64, chunk_blocks=chunk_blocks, n_hint=n, **cfg)
-    ora = O.CascadeOracle(64, chunk_blocks=chunk_blocks, n_hint=n, **cfg)
+    nh = n if hint else None
+    gpu = C.CausalCascade(64, chunk_blocks=chunk_blocks, n_hint=nh, **cfg)
+    ora = O.CascadeOracle(64, chunk_blocks=chunk_blocks, n_hint=nh, **cfg)
     if force_build is not None:
         gpu.build_threshold = ora.build_threshold = force_build
     qt, kt = dev16(q, cuda), dev16(k, cuda)
@@ -146,6 +147,17 @@ def test_stream_many_cells(cuda, nlist, geom):
     n = 400 * BLOCK
     q, k = _clustered(n, seed=6) if geom == "clustered" else _random(n, seed=6)
     s = _stream(cuda, q, k, 16, True, force_build=512, nlist=nlist, top_c=8, nprobe=4)
+    assert s["built"]
+
+
+def test_stream_without_size_hint(cuda):
+    """No n_hint (as the reference's own tests construct it): the sub-mean, outlier and index
+    buffers grow as chunks arrive (the index is rebuilt larger with the same centroids and the
+    incremental radii carried over), and nlist is fixed at the first build from the committed
+    count."""
+    n = 200 * BLOCK
+    q, k = _clustered(n, seed=13)
+    s = _stream(cuda, q, k, 8, True, force_build=96, hint=False, top_c=6, nprobe=3)
     assert s["built"]
 
 
