@@ -237,6 +237,16 @@ int ssa_tree_descend(const void* tree, const float* q, const int64_t* q_pos, int
                      float beta, int32_t* sel, ssa_stream_t stream);
 
 /*
+ * ssa_tree_pack (the compact contract for causal query-block routing through the tree; no
+ * reference function -- ssa_amd.treecode.tree_route's packing): rows = B Hq nb rows (b, h, i),
+ * i = row % nb; sel (rows, tc) int32 the descent's leaves (-1 = none) of query block i; the row's
+ * list is those leaves OR blocks i - local .. i, distinct and ascending in kv_idx (rows, W) int32
+ * (pad 0), counted in kv_num (rows). tc + min(local, nb - 1) + 1 <= min(W, 256).
+ */
+int ssa_tree_pack(const int32_t* sel, int64_t rows, int64_t nb, int64_t tc, int64_t local,
+                  int32_t* kv_num, int32_t* kv_idx, int64_t W, ssa_stream_t stream);
+
+/*
  * Certified causal cascade (CCC): the streaming chunked-causal sub-block selector of
  * ssa/cascade_router.py:66-442 (CausalCascade, ccc_prefill), faiss-free. One head; the caller
  * holds the state: the routing-space sub-block means (n_sub, d) fp32 row-major, the first

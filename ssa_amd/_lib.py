@@ -60,6 +60,7 @@ _SIGNATURES = {
     "ssa_tree_build": (_c_int, [_c_p, _c_int] + [_c_i64] * 5 + [_c_p, _c_i64, _c_i64, _c_p, _c_sz,
                                                                 _c_p]),
     "ssa_tree_descend": (_c_int, [_c_p, _c_p, _c_p] + [_c_i64] * 8 + [_c_f, _c_p, _c_p]),
+    "ssa_tree_pack": (_c_int, [_c_p] + [_c_i64] * 4 + [_c_p, _c_p, _c_i64, _c_p]),
     "ssa_ccc_index_size": (_c_sz, [_c_i64] * 3),
     "ssa_ccc_stage": (_c_int, [_c_p, _c_int] + [_c_i64] * 4 + [_c_p] + [_c_i64] * 3 +
                       [_c_p] * 4 + [_c_sz, _c_p]),

@@ -441,6 +441,52 @@ __global__ __launch_bounds__(64) void tree_descend_kernel(TreeArgs a) {
     a.sel[(bh * a.Q + qi) * a.tc + lane] = lane < nf ? (int32_t)c : -1;
 }
 
+
+constexpr int kTreePackMax = 256;  // candidates of a packed row: leaves + local window
+
+// One wave per row r of (b, h, i) rows, i = r % nb: the descent's leaves of the row (sel[r, 0..tc),
+// -1 = none) OR blocks i - local .. i, distinct and ascending in kv_idx[r] (pad 0), counted in
+// kv_num[r]. A value is kept at its first occurrence; its slot is the number of kept values
+// below it.
+__global__ __launch_bounds__(64) void tree_pack_kernel(const int32_t* __restrict__ sel, int64_t nb,
+                                                        int tc, int64_t local,
+                                                        int32_t* __restrict__ kv_num,
+                                                        int32_t* __restrict__ kv_idx, int64_t W) {
+  __shared__ int c[kTreePackMax];
+  __shared__ int first[kTreePackMax];
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t i = r % nb;
+  const int nloc = (int)((local < i ? local : i) + 1);
+  const int n = tc + nloc;
+  for (int e = lane; e < n; e += 64) {
+    int v = e < tc ? sel[r * tc + e] : (int)(i - (e - tc));
+    c[e] = v < 0 ? 0x7fffffff : v;
+  }
+  __syncthreads();
+  for (int e = lane; e < n; e += 64) {
+    const int v = c[e];
+    bool f = v != 0x7fffffff;
+    for (int g = 0; g < e && f; ++g) f = c[g] != v;
+    first[e] = f ? 1 : 0;
+  }
+  __syncthreads();
+  int mine = 0;
+  for (int e = lane; e < n; e += 64) mine += first[e];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
+  int32_t* out = kv_idx + r * W;
+  for (int e = lane; e < n; e += 64) {
+    if (!first[e]) continue;
+    const int v = c[e];
+    int rank = 0;
+    for (int g = 0; g < n; ++g) rank += (first[g] && c[g] < v) ? 1 : 0;
+    out[rank] = v;
+  }
+  for (int64_t s = mine + lane; s < W; s += 64) out[s] = 0;
+  if (lane == 0) kv_num[r] = mine;
+}
+
 }  // namespace
 }  // namespace ssa
 
@@ -577,4 +623,25 @@ extern "C" int ssa_tree_descend(const void* tree, const float* q, const int64_t*
   else if (c <= 512) tree_descend_kernel<8><<<g, 64, 0, st>>>(a);
   else tree_descend_kernel<16><<<g, 64, 0, st>>>(a);
   return launch_status("tree_descend_kernel");
+}
+
+extern "C" int ssa_tree_pack(const int32_t* sel, int64_t rows, int64_t nb, int64_t tc,
+                             int64_t local, int32_t* kv_num, int32_t* kv_idx, int64_t W,
+                             ssa_stream_t stream) {
+  using namespace ssa;
+  SSA_REQUIRE(rows >= 0 && rows <= 0x7fffffff && nb >= 1 && rows % nb == 0, SSA_ERR_INVALID,
+              "tree_pack: rows=%lld must be a multiple of nb=%lld", (long long)rows, (long long)nb);
+  SSA_REQUIRE(tc >= 0 && local >= 0, SSA_ERR_INVALID, "tree_pack: tc and local must be >= 0");
+  const int64_t win = (local < nb - 1 ? local : nb - 1) + 1;
+  SSA_REQUIRE(tc + win <= kTreePackMax, SSA_ERR_UNSUPPORTED,
+              "tree_pack: tc + min(local, nb - 1) + 1 = %lld exceeds %d", (long long)(tc + win),
+              kTreePackMax);
+  SSA_REQUIRE(W >= tc + win, SSA_ERR_INVALID, "tree_pack: W=%lld < tc + min(local, nb - 1) + 1",
+              (long long)W);
+  if (rows == 0) return SSA_OK;
+  SSA_REQUIRE(kv_num != nullptr && kv_idx != nullptr && (tc == 0 || sel != nullptr),
+              SSA_ERR_INVALID, "tree_pack: NULL pointer argument");
+  tree_pack_kernel<<<(unsigned)rows, 64, 0, static_cast<hipStream_t>(stream)>>>(
+      sel, nb, (int)tc, local, kv_num, kv_idx, W);
+  return launch_status("tree_pack_kernel");
 }

@@ -97,10 +97,8 @@ def build_tree(k: torch.Tensor, block: int = BLOCK, F: int = 8, top_cap: int = 8
     return TreeLevels(levels, buf, BH, nb, d, F, top_cap), F
 
 
-@torch.no_grad()
-def descend_beam(levels, F, q, W, top_c, q_pos=None, beta=0.0):
-    """q: (BH, Q, d). Returns (BH, Q, min(top_c, W)) leaf-block indices (-1 = empty), best first;
-    fixed beam width W (ssa/treecode.py:89-137)."""
+def _descend(levels, F, q, W, top_c, q_pos=None, beta=0.0):
+    """descend_beam's selections as the kernel writes them: int32, -1 = empty."""
     if not isinstance(levels, TreeLevels):
         raise TypeError("descend_beam: levels must come from ssa_amd.treecode.build_tree")
     if F != levels.F:
@@ -122,7 +120,14 @@ def descend_beam(levels, F, q, W, top_c, q_pos=None, beta=0.0):
     _lib.call("ssa_tree_descend", levels.buf.data_ptr(), qf.data_ptr(),
               0 if qp is None else qp.data_ptr(), BH, Q, levels.nb, d, F, levels.top_cap, W,
               top_c, float(beta), sel.data_ptr(), _lib.stream_of(qf))
-    return sel.long()
+    return sel
+
+
+@torch.no_grad()
+def descend_beam(levels, F, q, W, top_c, q_pos=None, beta=0.0):
+    """q: (BH, Q, d). Returns (BH, Q, min(top_c, W)) leaf-block indices (-1 = empty), best first;
+    fixed beam width W (ssa/treecode.py:89-137)."""
+    return _descend(levels, F, q, W, top_c, q_pos, beta).long()
 
 
 def tree_router(levels, F, qb, W, top_c, tile=4096):
@@ -151,19 +156,12 @@ def tree_route(q, k, block=BLOCK, top_c=8, local=1, W=16, F=8, top_cap=8, beta=0
     qb = block_summary(q[:, :, :nb * block], block, "qmean").view(B, Hkv, G, nb, d)
     qb = qb.reshape(B * Hkv, G * nb, d)
     pos = (torch.arange(nb, device=q.device, dtype=torch.int64) * block).repeat(G)
-    sel = descend_beam(levels, F, qb, W, top_c, q_pos=pos.expand(B * Hkv, G * nb), beta=beta)
+    sel = _descend(levels, F, qb, W, top_c, q_pos=pos.expand(B * Hkv, G * nb), beta=beta)
+    # rows (b, kv head, g, i) are rows (b, h = kv head * G + g, i)
     tc = sel.shape[-1]
-    sel = sel.view(B, Hkv, G, nb, tc).reshape(B, Hq, nb, tc)
-    i = torch.arange(nb, device=q.device)
-    loc = i[:, None] - torch.arange(local, -1, -1, device=q.device)[None, :]  # (nb, local + 1)
-    cand = torch.cat([sel, loc.expand(B, Hq, nb, local + 1)], dim=-1)
-    big = nb + 1
-    cand = torch.where(cand < 0, torch.full_like(cand, big), cand)
-    cand, _ = torch.sort(cand, dim=-1)
-    dup = torch.zeros_like(cand, dtype=torch.bool)
-    dup[..., 1:] = cand[..., 1:] == cand[..., :-1]
-    cand = torch.where(dup, torch.full_like(cand, big), cand)
-    cand, _ = torch.sort(cand, dim=-1)
-    kv_num = (cand < big).sum(-1).to(torch.int32)
-    kv_idx = torch.where(cand < big, cand, torch.zeros_like(cand)).to(torch.int32)
+    Wp = tc + local + 1
+    kv_num = torch.empty(B, Hq, nb, device=q.device, dtype=torch.int32)
+    kv_idx = torch.empty(B, Hq, nb, Wp, device=q.device, dtype=torch.int32)
+    _lib.call("ssa_tree_pack", sel.data_ptr(), B * Hq * nb, nb, tc, local, kv_num.data_ptr(),
+              kv_idx.data_ptr(), Wp, _lib.stream_of(sel))
     return kv_num, kv_idx

@@ -139,3 +139,31 @@ def test_tree_route_contract_and_attention(cuda):
         for i in qb:
             sl = slice(i * block, (i + 1) * block)
             assert np.abs(o[0, h, sl] - ref[0, h, sl]).max() < 2e-2
+
+
+@pytest.mark.parametrize("tc,local,nb", [(8, 1, 40), (16, 3, 9), (1, 0, 5), (64, 2, 300)])
+def test_tree_pack(cuda, tc, local, nb):
+    """ssa_tree_pack (tree_route's compact lists): each row's leaves (-1 = none, duplicates
+    allowed) OR blocks i - local .. i, distinct and ascending, pad 0."""
+    from ssa_amd import _lib
+    rng = np.random.default_rng(tc * 7 + nb)
+    rows = 3 * nb
+    i = np.arange(rows) % nb
+    sel = rng.integers(-1, nb, size=(rows, tc))
+    sel = np.where(sel > i[:, None], -1, sel).astype(np.int32)   # leaves at or before block i
+    sel[::5, :2] = sel[::5, :1]                                   # a duplicated leaf
+    W = tc + local + 1
+    st = torch.from_numpy(sel).to(cuda)
+    kv_num = torch.full((rows,), -7, device=cuda, dtype=torch.int32)
+    kv_idx = torch.full((rows, W), -7, device=cuda, dtype=torch.int32)
+    _lib.call("ssa_tree_pack", st.data_ptr(), rows, nb, tc, local, kv_num.data_ptr(),
+              kv_idx.data_ptr(), W, _lib.stream_of(st))
+    kn, ki = kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    for r in range(rows):
+        want = sorted({int(x) for x in sel[r] if x >= 0} |
+                      {int(i[r]) - L for L in range(local + 1) if i[r] - L >= 0})
+        assert kn[r] == len(want) and ki[r, :kn[r]].tolist() == want, r
+        assert (ki[r, kn[r]:] == 0).all()
+    with pytest.raises(_lib.SSAError):
+        _lib.call("ssa_tree_pack", st.data_ptr(), rows, nb, tc, local, kv_num.data_ptr(),
+                  kv_idx.data_ptr(), W - 1 if nb > local else tc, _lib.stream_of(st))
