@@ -284,7 +284,11 @@ int ssa_tree_pack(const int32_t* sel, int64_t rows, int64_t nb, int64_t tc, int6
  *   |qr| R_c and no filled search's last score reaches tau - cert_margin (flat: full budget and
  *   tau above -inf or q = 0); an uncertified block with an index is searched again with nprobe *
  *   escalate_factor lists and twice the search_k (at most max_escalations times); rounds = the
- *   last round run. search_k values up to 1024.
+ *   last round run. search_k values up to 1024. ws: with an index, certify and
+ *   max_escalations > 0, an 8-byte aligned workspace of nbq * 8 * skmax bytes, skmax = the
+ *   largest search_k a round uses (min(search_k, committed), doubled per escalation up to
+ *   committed): each round keeps the skmax best committed keys of the lists probed so far there,
+ *   so a later round scans only the lists it adds; otherwise ws may be NULL.
  */
 size_t ssa_ccc_index_size(int64_t n_cap, int64_t nlist, int64_t d);
 
@@ -311,8 +315,8 @@ int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int64_t d, con
                   int64_t top_c, int64_t local, int64_t outlier_cap, int64_t search_k_staged,
                   int64_t search_k, int64_t nprobe, int64_t escalate_factor,
                   int64_t max_escalations, int certify, float cert_margin, int32_t* kv_num,
-                  int32_t* kv_idx, int64_t W, uint8_t* cert, int32_t* rounds,
-                  ssa_stream_t stream);
+                  int32_t* kv_idx, int64_t W, uint8_t* cert, int32_t* rounds, void* ws,
+                  size_t ws_bytes, ssa_stream_t stream);
 
 /*
  * Block-sparse causal attention forward (replaces FlexAttention with

@@ -70,7 +70,7 @@ _SIGNATURES = {
     "ssa_ccc_index_add": (_c_int, [_c_p] + [_c_i64] * 4 + [_c_p, _c_i64, _c_sz, _c_p]),
     "ssa_ccc_route": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
                                _c_i64, _c_i64, _c_p, _c_p] + [_c_i64] * 9 +
-                      [_c_int, _c_f, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p]),
+                      [_c_int, _c_f, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "ssa_masked_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ssa_masked_attn_fwd": (_c_int, [_c_p] * 5 + [_c_int] + [_c_i64] * 6 +
                             [_c_p] * 3 + [_c_i64, _c_f, _c_p, _c_sz, _c_p]),

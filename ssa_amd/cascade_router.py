@@ -312,6 +312,15 @@ class CausalCascade:
         rounds = torch.zeros(nbq, dtype=torch.int32, device=dev)
         ix = self.index
         means = self.means
+        ws = None
+        if ix is not None and certify and self.max_escalations > 0:
+            # escalation carry: per query block the best keys of the lists probed so far, as many
+            # as the last round's search_k
+            sk = sk0
+            for _ in range(self.max_escalations):
+                sk = min(2 * sk, self.committed)
+            skmax = max(min(sk0, self.committed), sk)
+            ws = torch.empty(nbq * skmax, dtype=torch.int64, device=dev)
         _lib.call("ssa_ccc_route", qr.data_ptr(), nbq, qb_start, self.dr,
                   None if means is None else means.data_ptr(), self.committed, self.n_sub,
                   self.spb, None if ix is None else ix.buf.data_ptr(),
@@ -321,7 +330,8 @@ class CausalCascade:
                   self.top_c, self.local, self.outlier_cap, self.search_k, sk0, self.nprobe,
                   self.escalate_factor, self.max_escalations, 1 if certify else 0,
                   float(self.cert_margin), kv_num.data_ptr(), kv_idx.data_ptr(), W,
-                  cert.data_ptr(), rounds.data_ptr(), _lib.stream_of(qr))
+                  cert.data_ptr(), rounds.data_ptr(), None if ws is None else ws.data_ptr(),
+                  0 if ws is None else 8 * ws.numel(), _lib.stream_of(qr))
         stats = {"nbq": nbq, "rounds": rounds,
                  "cert_rate": float(cert.float().mean()) if certify and nbq else None}
         return kv_num, kv_idx, (cert.bool() if certify else None), stats

@@ -100,12 +100,13 @@ __device__ inline float block_max_f32(float x, float* slot) {
 // Streams M candidates through buf (LDS, kIvfCap keys), keeping the K largest (K <= kIvfMaxSearch,
 // keys unique); keyof(m) is candidate m's key, or 0 to skip it. Once K keys are kept, a candidate
 // below the threshold that kept them (K keys above it already) cannot enter the K largest and is
-// dropped on arrival, so later batches fill the buffer slowly. Returns how many are kept (in
-// buf[0..), any order). 256 threads.
+// dropped on arrival, so later batches fill the buffer slowly. buf[0..nk0) may hold up to K keys
+// of earlier candidates (nonzero, visible to the workgroup), ranked with the M new ones. Returns
+// how many are kept (in buf[0..), any order). 256 threads.
 template <typename F>
 __device__ int stream_top(unsigned long long* buf, int64_t M, int K, F keyof, unsigned int* hist,
-                          unsigned int* shv, int* ws) {
-  int nk = 0;
+                          unsigned int* shv, int* ws, int nk0 = 0) {
+  int nk = nk0;
   unsigned long long floor_key = 1ull;  // every real key is at least 1
   for (int64_t m0 = 0; m0 < M;) {
     const int room = kIvfCap - nk;
@@ -405,9 +406,17 @@ struct CccRouteArgs {
   int64_t W;
   unsigned char* cert;
   int32_t* rounds;
+  unsigned long long* carry;  // (nbq, kkeep) keys, or NULL: see ccc_route_kernel
+  int64_t kkeep;
 };
 
 // One workgroup per query block i of the chunk (global block qblk = qb_start + i).
+// Escalation rounds probe nested sets of lists (the nprobe cells of largest <q, c>, nprobe growing).
+// With a carry, each round keeps the kkeep best committed keys of every list probed so far in
+// carry row i (kkeep >= every round's search_k), and a later round streams only the lists it adds
+// through stream_top seeded with them: the top search_k of (the kkeep best of the earlier lists)
+// and (the new lists) is the top search_k of all of them. Each thread reads back only the carry
+// entries it wrote. Without a carry every round scans all of its lists.
 __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
   __shared__ unsigned long long buf[kIvfCap];     // streamed keys, then the merged candidates
   __shared__ unsigned long long stg[kIvfMaxSearch];  // the staged top
@@ -462,6 +471,10 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
   }
 
   int64_t nprobe = a.nprobe0, sk = a.sk0;
+  unsigned long long* carry = a.carry != nullptr ? a.carry + i * a.kkeep : nullptr;
+  int ncarry = 0;
+  int64_t mtot = 0;              // members of every list probed so far
+  unsigned long long Tprev = 0;  // the previous round's Tc
   for (int rnd = 0;; ++rnd) {
     // committed candidates: exhaustive (flat regime) or the probed lists (index)
     const int64_t kc = sk < committed ? sk : committed;
@@ -484,7 +497,8 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
           int running = 0;
           for (int64_t c0 = 0; c0 < nlist; c0 += 256) {
             const int64_t c = c0 + tid;
-            const bool take = c < nlist && buf[c] >= Tc;
+            const bool take = c < nlist && buf[c] >= Tc &&
+                              (carry == nullptr || rnd == 0 || buf[c] < Tprev);
             int tot;
             const int ex = ivf_block_scan(take ? 1 : 0, ws, &tot);
             if (take) lst[running + ex] = (int)c;
@@ -508,8 +522,11 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
         __syncthreads();
         const int64_t M = aux[nprobed];
         const int np = nprobed;
+        mtot += M;
+        for (int e = tid; e < ncarry; e += 256) buf[e] = carry[e];
+        __syncthreads();
         ncm = stream_top(
-            buf, M, (int)kc,
+            buf, M, carry != nullptr ? (int)a.kkeep : (int)kc,
             [&](int64_t m) -> unsigned long long {
               int lo = 0, hi = np - 1;
               while (lo < hi) {
@@ -522,10 +539,19 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
               const int64_t j = a.ids[a.off[p] + k];
               return ivf_key(dot_strided(qs, a.muL + d * (int64_t)a.off[p] + k, L, d), j);
             },
-            hist, shv, ws);
+            hist, shv, ws, ncarry);
+        if (carry != nullptr) {
+          for (int e = tid; e < ncm; e += 256) carry[e] = buf[e];
+          ncarry = ncm;
+          if (ncm > kc) {  // this round's kc best of the kkeep kept
+            const unsigned long long T = block_kth_largest(buf, ncm, (int)kc, hist, shv);
+            ncm = block_compact<unsigned long long>(buf, ncm, buf, ws,
+                                                    [T](unsigned long long k) { return k >= T; });
+          }
+        }
         // a search that filled its kc slots reports its smallest score; a starved one (fewer
         // members than kc) reports -inf: nothing was cut by truncation
-        if (M >= kc) dlast = key_score(block_min_key(buf, ncm, kslot));
+        if (mtot >= kc) dlast = key_score(block_min_key(buf, ncm, kslot));
       }
     }
 
@@ -660,6 +686,7 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
     if (!a.certify || ok || !a.has_index || rnd >= a.max_esc) break;
     nprobe = nprobe * a.esc < nlist ? nprobe * a.esc : nlist;
     sk = sk * 2 < committed ? sk * 2 : committed;
+    Tprev = Tc;
     __syncthreads();  // the next round rewrites buf / lst / aux
   }
 }
@@ -861,7 +888,8 @@ extern "C" int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int
                              int64_t search_k_staged, int64_t search_k, int64_t nprobe,
                              int64_t escalate_factor, int64_t max_escalations, int certify,
                              float cert_margin, int32_t* kv_num, int32_t* kv_idx, int64_t W,
-                             uint8_t* cert, int32_t* rounds, ssa_stream_t stream) {
+                             uint8_t* cert, int32_t* rounds, void* ws, size_t ws_bytes,
+                             ssa_stream_t stream) {
   SSA_REQUIRE(nbq >= 0 && nbq <= 0x7fffffff && qb_start >= 0, SSA_ERR_INVALID,
               "ccc_route: bad nbq / qb_start");
   if (nbq == 0) return SSA_OK;
@@ -951,6 +979,16 @@ extern "C" int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int
   a.W = W;
   a.cert = cert;
   a.rounds = rounds;
+  if (index != nullptr && certify && max_escalations > 0) {
+    // the escalation carry: nbq rows of skmax keys (skmax >= every round's search_k)
+    const size_t need = size_t(nbq) * size_t(skmax) * 8;
+    SSA_REQUIRE(ws != nullptr && (reinterpret_cast<uintptr_t>(ws) & 7u) == 0, SSA_ERR_INVALID,
+                "ccc_route: escalation needs an 8-byte aligned workspace");
+    SSA_REQUIRE(ws_bytes >= need, SSA_ERR_WORKSPACE,
+                "ccc_route: workspace holds %zu bytes, escalation needs %zu", ws_bytes, need);
+    a.carry = static_cast<unsigned long long*>(ws);
+    a.kkeep = skmax;
+  }
   ssa::ccc_route_kernel<<<(unsigned)nbq, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return ssa::launch_status("ccc_route_kernel");
 }

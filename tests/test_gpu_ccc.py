@@ -292,4 +292,28 @@ def test_errors(cuda):
     with pytest.raises(_lib.SSAError):        # routing dim not a multiple of 32
         _lib.call("ssa_ccc_route", x.data_ptr(), 1, 1, 48, None, 0, 0, 4, None, 0, 0, None, None,
                   0, 8, 1, 4, 32, 32, 4, 4, 2, 0, 0.0, kv.data_ptr(), kv.data_ptr(), 8,
-                  kv.data_ptr(), kv.data_ptr(), _lib.stream_of(x))
+                  kv.data_ptr(), kv.data_ptr(), None, 0, _lib.stream_of(x))
+
+
+def test_escalation_needs_workspace(cuda):
+    """With an index, certificates and escalation rounds, ssa_ccc_route keeps each round's best
+    committed keys in the caller's workspace; without one it refuses the call."""
+    d, nlist, per = 32, 8, 4
+    Cm = np.eye(nlist, d, dtype=np.float32)
+    cc = C.CausalCascade(d, block=128, sub=32, top_c=8, local=1, nprobe=1, nlist=nlist,
+                         search_k=16)
+    cc._kmeans = lambda X, iters=6: torch.from_numpy(Cm).to(cuda)
+    cc.means = torch.from_numpy(np.repeat(Cm, per, 0)).to(cuda)
+    cc.n_sub = cc.committed = nlist * per
+    cc._build_index()
+    qr = torch.randn(1, d, device=cuda)
+    out = torch.zeros(16, device=cuda, dtype=torch.int32)
+    ix = cc.index
+    args = [qr.data_ptr(), 1, cc.n_sub // 4, d, cc.means.data_ptr(), cc.committed, cc.n_sub, 4,
+            ix.buf.data_ptr(), ix.n_cap, ix.nlist, None, None, 0, 8, 1, 4, 16, 16, 1, 4, 2, 1,
+            0.0, out.data_ptr(), out.data_ptr(), 16, out.data_ptr(), out.data_ptr()]
+    with pytest.raises(_lib.SSAError):        # no workspace
+        _lib.call("ssa_ccc_route", *args, None, 0, _lib.stream_of(qr))
+    ws = torch.empty(32, device=cuda, dtype=torch.int64)
+    with pytest.raises(_lib.SSAError):        # 1 x 8 x 32 bytes needed (16 doubled twice, cap 32)
+        _lib.call("ssa_ccc_route", *args, ws.data_ptr(), 8 * 31, _lib.stream_of(qr))
