@@ -111,9 +111,12 @@ __device__ int stream_top(unsigned long long* buf, int64_t M, int K, F keyof, un
   for (int64_t m0 = 0; m0 < M;) {
     const int room = kIvfCap - nk;
     const int batch = (int)(M - m0 < room ? M - m0 : room);
-    for (int e = threadIdx.x; e < batch; e += 256) {
-      const unsigned long long k = keyof(m0 + e);
-      buf[nk + e] = k >= floor_key ? k : 0ull;
+    for (int e = threadIdx.x; e < batch; e += 512) {  // two candidates per thread per pass
+      const bool two = e + 256 < batch;
+      const unsigned long long k0 = keyof(m0 + e);
+      const unsigned long long k1 = two ? keyof(m0 + e + 256) : 0ull;
+      buf[nk + e] = k0 >= floor_key ? k0 : 0ull;
+      if (two) buf[nk + e + 256] = k1 >= floor_key ? k1 : 0ull;
     }
     __syncthreads();
     int tot = block_compact<unsigned long long>(buf, nk + batch, buf, ws,
@@ -508,13 +511,20 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
         }
         __syncthreads();  // the probed lists (written by any wave) before their sizes are read
         {
+          // member prefix of the probed lists in aux; lst[p] becomes list p's member offset (only
+          // thread tid reads and rewrites entry p; the scan's barriers order it before other reads)
           int running = 0;
           for (int p0 = 0; p0 < nprobed; p0 += 256) {
             const int p = p0 + tid;
-            const int sz = p < nprobed ? a.count[lst[p]] : 0;
+            const int cell = p < nprobed ? lst[p] : 0;
+            const int sz = p < nprobed ? a.count[cell] : 0;
+            const int of = p < nprobed ? a.off[cell] : 0;
             int tot;
             const int ex = ivf_block_scan(sz, ws, &tot);
-            if (p < nprobed) aux[p] = running + ex;
+            if (p < nprobed) {
+              aux[p] = running + ex;
+              lst[p] = of;
+            }
             running += tot;
           }
           if (tid == 0) aux[nprobed] = running;
@@ -534,10 +544,9 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
                 if (aux[mid] <= m) lo = mid;
                 else hi = mid - 1;
               }
-              const int p = lst[lo];
-              const int64_t k = m - aux[lo], L = a.count[p];
-              const int64_t j = a.ids[a.off[p] + k];
-              return ivf_key(dot_strided(qs, a.muL + d * (int64_t)a.off[p] + k, L, d), j);
+              const int64_t o = lst[lo], k = m - aux[lo], L = aux[lo + 1] - aux[lo];
+              const int64_t j = a.ids[o + k];
+              return ivf_key(dot_strided(qs, a.muL + d * o + k, L, d), j);
             },
             hist, shv, ws, ncarry);
         if (carry != nullptr) {
