@@ -80,8 +80,7 @@ class _Index:
         r = lambda x: (x + 255) // 256 * 256
         o_cent = 0
         o_rc = 2 * r(nlist * d * 4)
-        o_assign = o_rc + r(nlist * 4) + r(nlist * 4) + r((nlist + 1) * 4) + r(n_cap * 4) + \
-            r(n_cap * d * 4)
+        o_assign = o_rc + r(nlist * 4)
         self.centroids = self.buf[o_cent:o_cent + nlist * d * 4].view(torch.float32).view(nlist, d)
         self.Rc = self.buf[o_rc:o_rc + nlist * 4].view(torch.float32)
         self.assign = self.buf[o_assign:o_assign + n_cap * 4].view(torch.int32)

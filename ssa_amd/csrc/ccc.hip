@@ -242,13 +242,24 @@ __global__ __launch_bounds__(256) void ccc_outlier_kernel(
 // ---- index: Lloyd rounds, lists, radii ------------------------------------------------------------
 
 // Byte offsets of the index regions: the centroids (nlist, d), transposed (d, nlist), the radii
-// (nlist), list sizes, list offsets (nlist + 1), list members (ascending), the members' means
-// stored list by list, each list transposed (d, size), the assignment of every committed mean,
-// and the scratch of the list build (ranks, per-tile counts, assignment keys).
+// (nlist), the assignment of every committed mean, list sizes, list capacity offsets (nlist + 1),
+// list members (ascending) and the members' means, and the scratch of the list build (overflow
+// flag, new members per list, ranks, per-tile counts, assignment keys).
+//
+// List p owns member slots off[p] .. off[p + 1] - 1 (a multiple of 64 of them, off[p] a multiple of
+// 64): its capacity, set at its last full layout to roundup64(2 size) + 64, so that incremental
+// adds write only the new members. Member k's id is ids[off[p] + k]; its mean sits in tile
+// (off[p] + k) / 64 of 64 members, each tile stored transposed (d, 64): element t of member k at
+// muL[(off[p] + k - k % 64) d + 64 t + k % 64], 256-byte aligned runs of 64 members per dimension.
 struct CccLayout {
-  size_t cent, centT, rc, count, off, ids, muL, assign, rank, tcount, pbest, total;
+  size_t cent, centT, rc, assign, count, off, ids, muL, flag, cnew, rank, tcount, pbest, total;
   int64_t pcap;  // assignment keys the pbest region holds
+  int64_t mcap;  // member slots: capacities summing to at most 2 n_cap + 128 nlist
 };
+
+__host__ __device__ inline int32_t ccc_list_cap(int32_t size) {
+  return ((2 * size + 63) & ~63) + 64;
+}
 
 CccLayout ccc_layout(int64_t n_cap, int64_t nlist, int64_t d) {
   CccLayout L;
@@ -257,12 +268,15 @@ CccLayout ccc_layout(int64_t n_cap, int64_t nlist, int64_t d) {
   size_t o = 0;
   L.cent = o;   o += r256(size_t(nlist) * d * 4);
   L.centT = o;  o += r256(size_t(nlist) * d * 4);
+  L.mcap = 2 * n_cap + 128 * nlist;
   L.rc = o;     o += r256(size_t(nlist) * 4);
+  L.assign = o; o += r256(size_t(n_cap) * 4);
   L.count = o;  o += r256(size_t(nlist) * 4);
   L.off = o;    o += r256(size_t(nlist + 1) * 4);
-  L.ids = o;    o += r256(size_t(n_cap) * 4);
-  L.muL = o;    o += r256(size_t(n_cap) * d * 4);
-  L.assign = o; o += r256(size_t(n_cap) * 4);
+  L.ids = o;    o += r256(size_t(L.mcap) * 4);
+  L.muL = o;    o += r256(size_t(L.mcap) * d * 4);
+  L.flag = o;   o += 256;
+  L.cnew = o;   o += r256(size_t(nlist) * 4);
   L.rank = o;   o += r256(size_t(n_cap) * 4);
   L.tcount = o; o += r256(size_t(ntiles) * nlist * 4);
   L.pbest = o;  o += r256(size_t(L.pcap) * 8);
@@ -319,11 +333,14 @@ __global__ __launch_bounds__(256) void ccc_assign_kernel(
 
 // One workgroup per tile of 256 means: rank = position among the tile's members of its centroid;
 // the tile's member count of every centroid goes to its tcount row (0 for absent ones).
+// With gate set, nothing runs unless *gate != 0.
 __global__ __launch_bounds__(256) void ccc_rank_kernel(const int32_t* __restrict__ assign,
                                                         int64_t n, int64_t nlist,
                                                         int32_t* __restrict__ rank,
-                                                        int32_t* __restrict__ tcount) {
+                                                        int32_t* __restrict__ tcount,
+                                                        const int32_t* __restrict__ gate) {
   __shared__ int sa[kTile];
+  if (gate != nullptr && *gate == 0) return;
   const int tid = threadIdx.x;
   const int64_t tile = blockIdx.x, j = tile * kTile + tid;
   const bool live = j < n;
@@ -367,20 +384,128 @@ int ccc_assign_rows(const float* x, int64_t m, int64_t base, int64_t d, const fl
   return launch_status("ccc_assign_kernel");
 }
 
-// Lists of the assignment of means x[0..n): sizes, offsets, ascending members and (muL set) the
-// members' means stored list by list, transposed.
+// One workgroup: off[c] = the capacity slots (ccc_list_cap of each size) of the lists before c,
+// off[nlist] = all of them. With gate set, nothing runs unless *gate != 0.
+__global__ __launch_bounds__(256) void ccc_cap_offsets_kernel(const int32_t* __restrict__ count,
+                                                               int64_t nlist,
+                                                               int32_t* __restrict__ off,
+                                                               const int32_t* __restrict__ gate) {
+  __shared__ int ws[4];
+  if (gate != nullptr && *gate == 0) return;
+  int running = 0;
+  for (int64_t c0 = 0; c0 < nlist; c0 += 256) {
+    const int64_t c = c0 + threadIdx.x;
+    const int v = c < nlist ? ccc_list_cap(count[c]) : 0;
+    int tot;
+    const int ex = ivf_block_scan(v, ws, &tot);
+    if (c < nlist) off[c] = running + ex;
+    running += tot;
+  }
+  if (threadIdx.x == 0) off[nlist] = running;
+}
+
+// One thread per mean j < m (id base + j, list a = assign[j]): it is member k = start[a] (0 without
+// start) + tbase[(j / kTile) nlist + a] + rank[j] of list a, stored at slot off[a] + k: its id and,
+// with muL set, its mean in the list's tiled storage. With gate set, runs only if
+// (*gate != 0) == gate_on.
+__global__ __launch_bounds__(256) void ccc_scatter_kernel(
+    const int32_t* __restrict__ assign, const int32_t* __restrict__ rank,
+    const int32_t* __restrict__ tbase, int64_t m, int64_t base, int64_t nlist,
+    const int32_t* __restrict__ start, const int32_t* __restrict__ off, int32_t* __restrict__ ids,
+    const float* __restrict__ x, int64_t d, float* __restrict__ muL,
+    const int32_t* __restrict__ gate, int gate_on) {
+  if (gate != nullptr && ((*gate != 0) != (gate_on != 0))) return;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= m) return;
+  const int a = assign[j];
+  const int64_t k = (start != nullptr ? start[a] : 0) + tbase[(j / kTile) * nlist + a] + rank[j];
+  const int64_t slot = off[a] + k;
+  ids[slot] = (int32_t)(base + j);
+  if (muL != nullptr) {
+    float* dst = muL + (slot - (k & 63)) * d + (k & 63);
+    const float* src = x + j * d;
+    for (int64_t t = 0; t < d; ++t) dst[t * 64] = src[t];
+  }
+}
+
+// One workgroup: *flag = 1 if some list's size plus its new members exceeds its capacity, else 0.
+__global__ __launch_bounds__(256) void ccc_add_check_kernel(const int32_t* __restrict__ count,
+                                                             const int32_t* __restrict__ cnew,
+                                                             const int32_t* __restrict__ off,
+                                                             int64_t nlist,
+                                                             int32_t* __restrict__ flag) {
+  __shared__ int any;
+  if (threadIdx.x == 0) any = 0;
+  __syncthreads();
+  bool over = false;
+  for (int64_t c = threadIdx.x; c < nlist; c += 256)
+    over |= (int64_t)count[c] + cnew[c] > (int64_t)off[c + 1] - off[c];
+  if (over) atomicOr(&any, 1);
+  __syncthreads();
+  if (threadIdx.x == 0) flag[0] = any;
+}
+
+// count[c] += cnew[c], unless *flag is set (the full layout recounts them).
+__global__ __launch_bounds__(256) void ccc_add_count_kernel(int32_t* __restrict__ count,
+                                                             const int32_t* __restrict__ cnew,
+                                                             int64_t nlist,
+                                                             const int32_t* __restrict__ flag) {
+  if (*flag != 0) return;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c < nlist) count[c] += cnew[c];
+}
+
+// Full layout of the lists of the means x[0..n) from their assignment in the index: sizes,
+// capacity offsets, ascending members and (with_means) the members' means. With gate set, runs
+// only if *gate != 0 (every kernel checks it on the device).
 int ccc_lists(const float* x, int64_t n, int64_t d, int64_t nlist, const CccLayout& L, char* base,
-              bool with_means, hipStream_t s) {
+              bool with_means, const int32_t* gate, hipStream_t s) {
   const int64_t ntiles = (n + kTile - 1) / kTile;
   int32_t* assign = reinterpret_cast<int32_t*>(base + L.assign);
   int32_t* rank = reinterpret_cast<int32_t*>(base + L.rank);
   int32_t* tcount = reinterpret_cast<int32_t*>(base + L.tcount);
-  ccc_rank_kernel<<<(unsigned)ntiles, kTile, 0, s>>>(assign, n, nlist, rank, tcount);
+  int32_t* count = reinterpret_cast<int32_t*>(base + L.count);
+  int32_t* off = reinterpret_cast<int32_t*>(base + L.off);
+  ccc_rank_kernel<<<(unsigned)ntiles, kTile, 0, s>>>(assign, n, nlist, rank, tcount, gate);
   SSA_TRY(launch_status("ccc_rank_kernel"));
-  return ivf_lists(assign, rank, tcount, 1, n, nlist, ntiles,
-                   reinterpret_cast<int32_t*>(base + L.count), reinterpret_cast<int32_t*>(base + L.off),
-                   reinterpret_cast<int32_t*>(base + L.ids), x, d,
-                   with_means ? reinterpret_cast<float*>(base + L.muL) : nullptr, s);
+  ivf_tile_prefix_kernel<<<dim3((unsigned)nlist, 1), 256, 0, s>>>(tcount, ntiles, nlist, count,
+                                                                  gate);
+  SSA_TRY(launch_status("ivf_tile_prefix_kernel"));
+  ccc_cap_offsets_kernel<<<1, 256, 0, s>>>(count, nlist, off, gate);
+  SSA_TRY(launch_status("ccc_cap_offsets_kernel"));
+  ccc_scatter_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+      assign, rank, tcount, n, 0, nlist, nullptr, off, reinterpret_cast<int32_t*>(base + L.ids),
+      x, d, with_means ? reinterpret_cast<float*>(base + L.muL) : nullptr, gate, 1);
+  return launch_status("ccc_scatter_kernel");
+}
+
+// Incremental add of the means n_old..n-1 (already assigned) to lists laid out over x[0..n_old):
+// each list's new members (ascending) go to the slots after its current ones, unless some list
+// would exceed its capacity; then (decided on the device) the lists are laid out again in full.
+int ccc_lists_add(const float* x, int64_t n_old, int64_t n, int64_t d, int64_t nlist,
+                  const CccLayout& L, char* base, hipStream_t s) {
+  const int64_t m = n - n_old, ntn = (m + kTile - 1) / kTile;
+  const int32_t* assign = reinterpret_cast<const int32_t*>(base + L.assign) + n_old;
+  int32_t* rank = reinterpret_cast<int32_t*>(base + L.rank);
+  int32_t* tcount = reinterpret_cast<int32_t*>(base + L.tcount);
+  int32_t* count = reinterpret_cast<int32_t*>(base + L.count);
+  int32_t* off = reinterpret_cast<int32_t*>(base + L.off);
+  int32_t* cnew = reinterpret_cast<int32_t*>(base + L.cnew);
+  int32_t* flag = reinterpret_cast<int32_t*>(base + L.flag);
+  ccc_rank_kernel<<<(unsigned)ntn, kTile, 0, s>>>(assign, m, nlist, rank, tcount, nullptr);
+  SSA_TRY(launch_status("ccc_rank_kernel"));
+  ivf_tile_prefix_kernel<<<dim3((unsigned)nlist, 1), 256, 0, s>>>(tcount, ntn, nlist, cnew,
+                                                                  nullptr);
+  SSA_TRY(launch_status("ivf_tile_prefix_kernel"));
+  ccc_add_check_kernel<<<1, 256, 0, s>>>(count, cnew, off, nlist, flag);
+  SSA_TRY(launch_status("ccc_add_check_kernel"));
+  ccc_scatter_kernel<<<(unsigned)((m + 255) / 256), 256, 0, s>>>(
+      assign, rank, tcount, m, n_old, nlist, count, off, reinterpret_cast<int32_t*>(base + L.ids),
+      x + n_old * d, d, reinterpret_cast<float*>(base + L.muL), flag, 0);
+  SSA_TRY(launch_status("ccc_scatter_kernel"));
+  ccc_add_count_kernel<<<(unsigned)((nlist + 255) / 256), 256, 0, s>>>(count, cnew, nlist, flag);
+  SSA_TRY(launch_status("ccc_add_count_kernel"));
+  return ccc_lists(x, n, d, nlist, L, base, true, flag, s);
 }
 
 // ---- route ----------------------------------------------------------------------------------------
@@ -544,9 +669,10 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
                 if (aux[mid] <= m) lo = mid;
                 else hi = mid - 1;
               }
-              const int64_t o = lst[lo], k = m - aux[lo], L = aux[lo + 1] - aux[lo];
+              const int64_t o = lst[lo], k = m - aux[lo];  // o: a multiple of 64
               const int64_t j = a.ids[o + k];
-              return ivf_key(dot_strided(qs, a.muL + d * o + k, L, d), j);
+              return ivf_key(dot_strided(qs, a.muL + (o + (k & ~int64_t(63))) * d + (k & 63), 64, d),
+                             j);
             },
             hist, shv, ws, ncarry);
         if (carry != nullptr) {
@@ -706,11 +832,19 @@ __global__ __launch_bounds__(256) void ccc_route_kernel(CccRouteArgs a) {
 using ssa::CccLayout;
 
 extern "C" size_t ssa_ccc_index_size(int64_t n_cap, int64_t nlist, int64_t d) {
-  if (n_cap <= 0 || nlist <= 0 || d <= 0) return 0;
+  if (n_cap <= 0 || nlist <= 0 || d <= 0 || 2 * n_cap + 128 * nlist >= (int64_t(1) << 31)) return 0;
   return ssa::ccc_layout(n_cap, nlist, d).total;
 }
 
 namespace {
+
+// The index addresses its list slots (2 n_cap + 128 nlist of them) with 32-bit offsets.
+int check_ccc_cap(const char* fn, int64_t n_cap, int64_t nlist) {
+  SSA_REQUIRE(2 * n_cap + 128 * nlist < (int64_t(1) << 31), SSA_ERR_UNSUPPORTED,
+              "%s: n_cap=%lld with nlist=%lld exceeds the 32-bit list slots", fn,
+              (long long)n_cap, (long long)nlist);
+  return SSA_OK;
+}
 
 int check_ccc_rows(const char* fn, const float* x, int64_t n, int64_t d, int64_t nlist) {
   SSA_REQUIRE(x != nullptr && ssa::aligned16(x), SSA_ERR_INVALID,
@@ -801,6 +935,7 @@ extern "C" int ssa_ccc_assign(const float* x, int64_t n, int64_t d, const float*
   SSA_TRY(check_ccc_rows("ccc_assign", x, n, d, nlist));
   SSA_REQUIRE(cent != nullptr && assign != nullptr, SSA_ERR_INVALID,
               "ccc_assign: cent / assign is NULL");
+  SSA_TRY(check_ccc_cap("ccc_assign", n, nlist));
   const CccLayout L = ssa::ccc_layout(n, nlist, d);
   SSA_TRY(check_ccc_buffer("ccc_assign", ws, ws_bytes, L.total));
   char* base = static_cast<char*>(ws);
@@ -815,6 +950,7 @@ extern "C" int ssa_ccc_kmeans(const float* x, int64_t n, int64_t d, int64_t nlis
   SSA_TRY(check_ccc_rows("ccc_kmeans", x, n, d, nlist));
   SSA_REQUIRE(cent != nullptr && iters >= 0, SSA_ERR_INVALID,
               "ccc_kmeans: cent is NULL or iters < 0");
+  SSA_TRY(check_ccc_cap("ccc_kmeans", n, nlist));
   const CccLayout L = ssa::ccc_layout(n, nlist, d);
   SSA_TRY(check_ccc_buffer("ccc_kmeans", ws, ws_bytes, L.total));
   char* base = static_cast<char*>(ws);
@@ -828,7 +964,7 @@ extern "C" int ssa_ccc_kmeans(const float* x, int64_t n, int64_t d, int64_t nlis
     SSA_TRY(ssa::ccc_assign_rows(x, n, 0, d, cent, nlist,
                                  reinterpret_cast<unsigned long long*>(base + L.pbest), L.pcap,
                                  reinterpret_cast<int32_t*>(base + L.assign), nullptr, s));
-    SSA_TRY(ssa::ccc_lists(x, n, d, nlist, L, base, false, s));
+    SSA_TRY(ssa::ccc_lists(x, n, d, nlist, L, base, false, nullptr, s));
     const int32_t* count = reinterpret_cast<const int32_t*>(base + L.count);
     const int32_t* off = reinterpret_cast<const int32_t*>(base + L.off);
     const int32_t* ids = reinterpret_cast<const int32_t*>(base + L.ids);
@@ -849,6 +985,7 @@ extern "C" int ssa_ccc_index_build(const float* x, int64_t n, int64_t d, int64_t
   SSA_TRY(check_ccc_rows("ccc_index_build", x, n, d, nlist));
   SSA_REQUIRE(cent != nullptr && n_cap >= n, SSA_ERR_INVALID,
               "ccc_index_build: cent is NULL or n_cap < n");
+  SSA_TRY(check_ccc_cap("ccc_index_build", n_cap, nlist));
   const CccLayout L = ssa::ccc_layout(n_cap, nlist, d);
   SSA_TRY(check_ccc_buffer("ccc_index_build", index, index_bytes, L.total));
   char* base = static_cast<char*>(index);
@@ -864,7 +1001,7 @@ extern "C" int ssa_ccc_index_build(const float* x, int64_t n, int64_t d, int64_t
   SSA_TRY(ssa::ccc_assign_rows(x, n, 0, d, ic, nlist,
                                reinterpret_cast<unsigned long long*>(base + L.pbest), L.pcap,
                                reinterpret_cast<int32_t*>(base + L.assign), rc, s));
-  SSA_TRY(ssa::ccc_lists(x, n, d, nlist, L, base, true, s));
+  SSA_TRY(ssa::ccc_lists(x, n, d, nlist, L, base, true, nullptr, s));
   ssa::ivf_transpose_cent_kernel<<<dim3((unsigned)nlist, 1), 64, 0, s>>>(
       ic, d, nlist, reinterpret_cast<float*>(base + L.centT));
   return ssa::launch_status("ivf_transpose_cent_kernel");
@@ -876,6 +1013,7 @@ extern "C" int ssa_ccc_index_add(const float* x, int64_t n_old, int64_t n, int64
   SSA_TRY(check_ccc_rows("ccc_index_add", x, n, d, nlist));
   SSA_REQUIRE(n_old >= 0 && n_old <= n && n <= n_cap, SSA_ERR_INVALID,
               "ccc_index_add: need 0 <= n_old <= n <= n_cap");
+  SSA_TRY(check_ccc_cap("ccc_index_add", n_cap, nlist));
   const CccLayout L = ssa::ccc_layout(n_cap, nlist, d);
   SSA_TRY(check_ccc_buffer("ccc_index_add", index, index_bytes, L.total));
   if (n_old == n) return SSA_OK;
@@ -886,7 +1024,7 @@ extern "C" int ssa_ccc_index_add(const float* x, int64_t n_old, int64_t n, int64
                                reinterpret_cast<unsigned long long*>(base + L.pbest), L.pcap,
                                reinterpret_cast<int32_t*>(base + L.assign),
                                reinterpret_cast<float*>(base + L.rc), s));
-  return ssa::ccc_lists(x, n, d, nlist, L, base, true, s);
+  return ssa::ccc_lists_add(x, n_old, n, d, nlist, L, base, s);
 }
 
 extern "C" int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int64_t d,
@@ -951,6 +1089,7 @@ extern "C" int ssa_ccc_route(const float* qr, int64_t nbq, int64_t qb_start, int
                 SSA_ERR_INVALID, "ccc_route: bad index geometry (nlist, n_cap, committed)");
     SSA_REQUIRE((reinterpret_cast<uintptr_t>(index) & 255u) == 0, SSA_ERR_INVALID,
                 "ccc_route: index must be a 256-byte aligned device pointer");
+    SSA_TRY(check_ccc_cap("ccc_route", n_cap, nlist));
     const CccLayout L = ssa::ccc_layout(n_cap, nlist, d);
     const char* base = static_cast<const char*>(index);
     a.has_index = 1;

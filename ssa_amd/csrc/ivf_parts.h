@@ -249,11 +249,13 @@ __global__ __launch_bounds__(256) void ivf_rank_kernel(
 
 // One workgroup per (centroid, head): tcount[t] <- the centroid's members in the tiles before t
 // (an exclusive prefix over the tiles, in place, 256 tiles per pass) and count = its members in
-// all tiles. Work O(tiles x centroids).
+// all tiles. Work O(tiles x centroids). With gate set, nothing runs unless *gate != 0.
 __global__ __launch_bounds__(256) void ivf_tile_prefix_kernel(int32_t* __restrict__ tcount,
                                                                int64_t ntiles, int64_t nlist,
-                                                               int32_t* __restrict__ count) {
+                                                               int32_t* __restrict__ count,
+                                                               const int32_t* __restrict__ gate) {
   __shared__ int ws[4];
+  if (gate != nullptr && *gate == 0) return;
   const int64_t bh = blockIdx.y, c = blockIdx.x;
   int32_t* col = tcount + bh * ntiles * nlist + c;
   int running = 0;
@@ -318,7 +320,7 @@ inline int ivf_lists(const int32_t* assign, const int32_t* rank, int32_t* tcount
                      int64_t nb, int64_t nlist, int64_t ntiles, int32_t* count, int32_t* off,
                      int32_t* ids, const float* mu, int64_t d, float* muL, hipStream_t s) {
   ivf_tile_prefix_kernel<<<dim3((unsigned)nlist, (unsigned)BH), 256, 0, s>>>(tcount, ntiles,
-                                                                             nlist, count);
+                                                                             nlist, count, nullptr);
   SSA_TRY(launch_status("ivf_tile_prefix_kernel"));
   ivf_offsets_kernel<<<(unsigned)BH, 256, 0, s>>>(count, nlist, off);
   SSA_TRY(launch_status("ivf_offsets_kernel"));

@@ -317,3 +317,55 @@ def test_escalation_needs_workspace(cuda):
     ws = torch.empty(32, device=cuda, dtype=torch.int64)
     with pytest.raises(_lib.SSAError):        # 1 x 8 x 32 bytes needed (16 doubled twice, cap 32)
         _lib.call("ssa_ccc_route", *args, ws.data_ptr(), 8 * 31, _lib.stream_of(qr))
+
+
+def test_index_add_in_place_and_overflow(cuda):
+    """Incremental adds write a list's new members after its current ones while they fit the
+    capacity its last layout gave it (roundup64(2 size) + 64 slots), and lay every list out again
+    when one would overflow; either way list c holds its members ascending from slot off[c] (a
+    multiple of 64), their means in 64-member tiles stored transposed (d, 64)."""
+    d, nlist, per = 32, 8, 4
+    Cm = np.eye(nlist, d, dtype=np.float32)
+    rng = np.random.default_rng(1)
+    X = np.concatenate([np.repeat(Cm, per, 0),                      # the build: 4 per list
+                        Cm[rng.integers(0, nlist, 40)],             # fits every capacity (128)
+                        np.repeat(Cm[:1], 300, 0)])                 # overflows list 0
+    X = (X + 0.01 * rng.standard_normal(X.shape)).astype(np.float32)
+    cc = C.CausalCascade(d, block=128, sub=32, nlist=nlist, n_hint=4096 * 32)
+    cc._kmeans = lambda X, iters=6: torch.from_numpy(Cm).to(cuda)
+    cc.means = torch.from_numpy(X).to(cuda)
+    cc.n_sub = cc.committed = nlist * per
+    cc._build_index()
+
+    def layout(n):
+        ix = cc.index
+        buf = ix.buf.cpu().numpy()
+        r = lambda x: (x + 255) // 256 * 256
+        mcap = 2 * ix.n_cap + 128 * nlist
+        o_count = 2 * r(nlist * d * 4) + r(nlist * 4) + r(ix.n_cap * 4)
+        o_off = o_count + r(nlist * 4)
+        o_ids = o_off + r((nlist + 1) * 4)
+        o_mu = o_ids + r(mcap * 4)
+        count = buf[o_count:o_count + 4 * nlist].view(np.int32)
+        off = buf[o_off:o_off + 4 * (nlist + 1)].view(np.int32)
+        ids = buf[o_ids:o_ids + 4 * mcap].view(np.int32)
+        mu = buf[o_mu:o_mu + 4 * mcap * d].view(np.float32)
+        a = O.ccc_assign(X[:n], Cm)
+        np.testing.assert_array_equal(cc.cell_of.cpu().numpy(), a)
+        for c in range(nlist):
+            want = np.flatnonzero(a == c)
+            assert count[c] == len(want) and off[c] % 64 == 0 and off[c + 1] - off[c] >= len(want)
+            np.testing.assert_array_equal(ids[off[c]:off[c] + len(want)], want)
+            for k, j in enumerate(want):
+                t0 = off[c] + k - k % 64
+                np.testing.assert_array_equal(mu[t0 * d + np.arange(d) * 64 + k % 64], X[j])
+        return off[1:] - off[:-1]
+
+    caps = [layout(nlist * per)]
+    for n in (nlist * per + 40, len(X)):
+        cc.n_sub = n
+        cc.committed_at_rebuild = n               # keep the adds from triggering a rebuild
+        cc._commit()
+        caps.append(layout(n))
+    assert (caps[1] == caps[0]).all()             # the first add wrote in place
+    assert caps[2][0] > caps[0][0]                # the second laid the lists out again
