@@ -269,8 +269,12 @@ int ssa_tree_pack(const int32_t* sel, int64_t rows, int64_t nb, int64_t tc, int6
  * ssa_ccc_assign (_assign, :139-147): assign[j] = the centroid of largest <x_j, c>; same ws.
  * ssa_ccc_index_build (_build_index, :163-190): the index over x[0..n) with the centroids cent:
  *   the lists of the assignment (members ascending) and exact radii max ||x - c|| (fp64, rounded).
+ *   Each list gets roundup64(2 size) + 64 member slots; 2 n_cap + 128 nlist must stay below 2^31.
  * ssa_ccc_index_add (_commit with an index + _update_radii, :140-147,:192-194): x[n_old..n)
- *   join their best centroid's list; radii rise to cover them.
+ *   join their best centroid's list; radii rise to cover them. n_old must be the count of the
+ *   index's last build or add. The new members are written after each list's current ones; when
+ *   a list would exceed its slots, every list is laid out again (decided on the device, no host
+ *   synchronisation).
  * ssa_ccc_route (route, :282-331; _search_committed :233-255, _search_staged :257-280,
  *   _select_topc :333-347, _outlier_parents :349-366, _pack :374-383, _certify :385-403): one
  *   workgroup per query block i (global block q = qb_start + i) of qr (nbq, d) fp32: the staged
