@@ -377,7 +377,7 @@ int ccc_assign_rows(const float* x, int64_t m, int64_t base, int64_t d, const fl
   const int64_t per_group = (nlist + g - 1) / g;
   const int64_t groups = (nlist + per_group - 1) / per_group;
   ivf_score_kernel<<<dim3((unsigned)stiles, 1, (unsigned)groups), kScoreTile,
-                     kAssignC * d * sizeof(float), s>>>(x, cent, m, d, nlist, per_group, pbest);
+                     kAssignC * d * sizeof(double), s>>>(x, cent, m, d, nlist, per_group, pbest);
   SSA_TRY(launch_status("ivf_score_kernel"));
   ccc_assign_kernel<<<(unsigned)((m + 255) / 256), 256, 0, s>>>(pbest, groups, m, base, x, cent, d,
                                                                  assign, rc);

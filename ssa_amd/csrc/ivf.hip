@@ -293,7 +293,7 @@ extern "C" int ssa_ivf_build(const float* mu, int64_t BH, int64_t nb, int64_t d,
   SSA_TRY(ssa::launch_status("ivf_init_kernel"));
   for (int64_t it = 0; it <= niter; ++it) {
     const bool last = it == niter;  // the last assignment only fills the lists
-    ssa::ivf_score_kernel<<<gs, ssa::kScoreTile, ssa::kAssignC * d * sizeof(float), s>>>(
+    ssa::ivf_score_kernel<<<gs, ssa::kScoreTile, ssa::kAssignC * d * sizeof(double), s>>>(
         mu, cent, nb, d, nlist, L.per_group, pbest);
     SSA_TRY(ssa::launch_status("ivf_score_kernel"));
     ssa::ivf_rank_kernel<<<gt, ssa::kTile, 0, s>>>(pbest, nb, nlist, L.ntiles, L.groups, assign,

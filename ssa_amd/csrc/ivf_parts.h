@@ -125,12 +125,13 @@ __device__ unsigned long long block_kth_largest(const unsigned long long* keys, 
 // ---- build --------------------------------------------------------------------------------------
 // One wave per (tile of 128 block means, centroid group): the key of the best centroid of the
 // group for each block mean (largest inner product, ties to the lower centroid). Each lane owns
-// block means j and j + 64, so every staged centroid value (fp32 in LDS, 4 per 16-byte read)
-// feeds two fp64 chains: LDS traffic, not the fp64 rate, bounds this loop.
+// block means j and j + 64, so every staged centroid value (widened to fp64 once, when staged in
+// LDS, 2 per 16-byte read) feeds two fp64 chains with no conversion in the loop. Dynamic LDS:
+// kAssignC * d doubles.
 __global__ __launch_bounds__(kScoreTile) void ivf_score_kernel(
     const float* __restrict__ mu, const float* __restrict__ cent, int64_t nb, int64_t d,
     int64_t nlist, int64_t per_group, unsigned long long* __restrict__ pbest) {
-  extern __shared__ float scf[];  // d x kAssignC: element t of centroid c0 + c at t * kAssignC + c
+  extern __shared__ double scd[];  // d x kAssignC: element t of centroid c0 + c at t * kAssignC + c
   const int tid = threadIdx.x;
   const int64_t bh = blockIdx.y, tile = blockIdx.x, g = blockIdx.z;
   int64_t j[2];
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(kScoreTile) void ivf_score_kernel(
     __syncthreads();
     for (int e = tid; e < kAssignC * (int)d; e += kScoreTile) {
       const int c = e / (int)d, t = e - c * (int)d;
-      scf[t * kAssignC + c] = c < cc ? cb[(c0 + c) * d + t] : 0.0f;
+      scd[t * kAssignC + c] = c < cc ? (double)cb[(c0 + c) * d + t] : 0.0;
     }
     __syncthreads();
     double acc[2][kAssignC];
@@ -173,15 +174,13 @@ __global__ __launch_bounds__(kScoreTile) void ivf_score_kernel(
         }
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        const float4* s4 = reinterpret_cast<const float4*>(scf + (t0 + t) * kAssignC);
+        const double2* s2 = reinterpret_cast<const double2*>(scd + (t0 + t) * kAssignC);
         double cv[kAssignC];
 #pragma unroll
-        for (int q = 0; q < kAssignC / 4; ++q) {
-          const float4 x = s4[q];
-          cv[4 * q] = x.x;
-          cv[4 * q + 1] = x.y;
-          cv[4 * q + 2] = x.z;
-          cv[4 * q + 3] = x.w;
+        for (int q = 0; q < kAssignC / 2; ++q) {
+          const double2 x = s2[q];
+          cv[2 * q] = x.x;
+          cv[2 * q + 1] = x.y;
         }
         const double r0 = r[0][t], r1 = r[1][t];
 #pragma unroll
